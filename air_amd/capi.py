@@ -1,0 +1,218 @@
+"""ctypes binding of libair_hip.so (the C ABI declared in include/air_hip.h).
+
+This module is a thin Python view of the C boundary: every call goes through
+the native library, and importing it fails loudly when the library has not
+been built (there is no Python or CPU fallback for any compute entry point).
+Pointers are plain integers; ``ptr()`` accepts ints, torch tensors
+(``data_ptr()``) and numpy arrays (host memory, for matrix upload only).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libair_hip.so")
+
+AIR_HIP_OK = 0
+STATUS_NAMES = {
+    0: "ok",
+    1: "invalid_argument",
+    2: "invalid_state",
+    3: "io_error",
+    4: "cancelled",
+    5: "data_error",
+    6: "unsupported",
+    7: "internal_error",
+}
+
+TYPE_Q4_0 = 2
+TYPE_Q8_0 = 8
+TYPE_Q4_K = 12
+TYPE_NAMES = {TYPE_Q4_0: "q4_0", TYPE_Q8_0: "q8_0", TYPE_Q4_K: "q4_k"}
+
+LINEAR_AUTO = 0
+LINEAR_DECODE = 1
+LINEAR_PREFILL = 2
+MAX_DECODE_ROWS = 64
+
+# Every exported entry point of include/air_hip.h: name -> (restype, argtypes).
+_P = ctypes.c_void_p
+_U64 = ctypes.c_uint64
+_U32 = ctypes.c_uint32
+_I = ctypes.c_int
+
+
+class MatrixDesc(ctypes.Structure):
+    _fields_ = [
+        ("type", ctypes.c_int32),
+        ("device", ctypes.c_int32),
+        ("k", ctypes.c_uint64),
+        ("n", ctypes.c_uint64),
+        ("canonical_bytes", ctypes.c_uint64),
+        ("resident_bytes", ctypes.c_uint64),
+    ]
+
+
+class Stats(ctypes.Structure):
+    _fields_ = [
+        ("resident_matrix_bytes", ctypes.c_uint64),
+        ("workspace_bytes", ctypes.c_uint64),
+        ("host_to_device_bytes", ctypes.c_uint64),
+        ("prepared_matrices", ctypes.c_uint64),
+        ("decode_linear_calls", ctypes.c_uint64),
+        ("prefill_linear_calls", ctypes.c_uint64),
+        ("decode_rows", ctypes.c_uint64),
+        ("prefill_rows", ctypes.c_uint64),
+    ]
+
+
+SIGNATURES = {
+    "air_hip_abi_version": (_I, []),
+    "air_hip_status_string": (ctypes.c_char_p, [_I]),
+    "air_hip_last_error": (ctypes.c_char_p, []),
+    "air_hip_device_count": (_I, [ctypes.POINTER(_I)]),
+    "air_hip_mem_info": (_I, [_I, ctypes.POINTER(_U64), ctypes.POINTER(_U64)]),
+    "air_hip_context_create": (_I, [_I, _P, ctypes.POINTER(_P)]),
+    "air_hip_context_destroy": (_I, [_P]),
+    "air_hip_context_set_stream": (_I, [_P, _P]),
+    "air_hip_context_reserve": (_I, [_P, _U64, _U32]),
+    "air_hip_context_stats": (_I, [_P, ctypes.POINTER(Stats)]),
+    "air_hip_canonical_bytes": (_U64, [_I, _U64, _U64]),
+    "air_hip_matrix_prepare": (_I, [_P, _I, _U64, _U64, _P, _U64, _I, ctypes.POINTER(_P)]),
+    "air_hip_matrix_release": (_I, [_P]),
+    "air_hip_matrix_describe": (_I, [_P, ctypes.POINTER(MatrixDesc)]),
+    "air_hip_matrix_dequantize": (_I, [_P, _P, _P]),
+    "air_hip_dequantize_canonical": (_I, [_P, _I, _P, _U64, _U64, _P]),
+    "air_hip_linear": (_I, [_P, _P, _P, _P, _P, _U32, _I]),
+}
+
+
+class HipError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        self.status = status
+        self.status_name = STATUS_NAMES.get(status, "unknown")
+        super().__init__(f"{self.status_name}: {message}")
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    """Loads the in-tree native library; raises if it was not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                "(there is no fallback path)"
+            )
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = handle
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != AIR_HIP_OK:
+        msg = lib().air_hip_last_error().decode("utf-8", "replace")
+        raise HipError(status, msg)
+
+
+def ptr(obj) -> int:
+    """Address of a device/host buffer: int, torch tensor, or numpy array."""
+    if obj is None:
+        return 0
+    if isinstance(obj, int):
+        return obj
+    if hasattr(obj, "data_ptr"):
+        return int(obj.data_ptr())
+    if hasattr(obj, "ctypes"):
+        return int(obj.ctypes.data)
+    raise TypeError(f"cannot take the address of {type(obj)!r}")
+
+
+def canonical_bytes(type_id: int, k: int, n: int) -> int:
+    return int(lib().air_hip_canonical_bytes(type_id, k, n))
+
+
+def device_count() -> int:
+    n = _I(0)
+    check(lib().air_hip_device_count(ctypes.byref(n)))
+    return n.value
+
+
+def mem_info(device: int = 0):
+    free, total = _U64(0), _U64(0)
+    check(lib().air_hip_mem_info(device, ctypes.byref(free), ctypes.byref(total)))
+    return free.value, total.value
+
+
+class Context:
+    """A device + stream + workspace (air_hip_context)."""
+
+    def __init__(self, device: int = 0, stream: int = 0):
+        handle = _P()
+        check(lib().air_hip_context_create(device, stream or None, ctypes.byref(handle)))
+        self.handle = handle
+        self.device = device
+
+    def set_stream(self, stream: int) -> None:
+        check(lib().air_hip_context_set_stream(self.handle, stream or None))
+
+    def reserve(self, max_k: int, max_m: int) -> None:
+        check(lib().air_hip_context_reserve(self.handle, max_k, max_m))
+
+    def stats(self) -> dict:
+        s = Stats()
+        check(lib().air_hip_context_stats(self.handle, ctypes.byref(s)))
+        return {name: getattr(s, name) for name, _ in Stats._fields_}
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib().air_hip_context_destroy(self.handle))
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def dequantize_canonical(self, type_id: int, canonical, nbytes: int, elements: int, out) -> None:
+        check(lib().air_hip_dequantize_canonical(self.handle, type_id, ptr(canonical), nbytes, elements, ptr(out)))
+
+
+class Matrix:
+    """A resident quantized matrix with GGML dims {k, n} (air_hip_matrix)."""
+
+    def __init__(self, ctx: Context, type_id: int, k: int, n: int, canonical, nbytes: int, on_device: bool):
+        handle = _P()
+        check(
+            lib().air_hip_matrix_prepare(
+                ctx.handle, type_id, k, n, ptr(canonical), nbytes, 1 if on_device else 0, ctypes.byref(handle)
+            )
+        )
+        self.handle = handle
+        self.ctx = ctx
+        self.type_id, self.k, self.n = type_id, k, n
+
+    def describe(self) -> dict:
+        d = MatrixDesc()
+        check(lib().air_hip_matrix_describe(self.handle, ctypes.byref(d)))
+        return {name: getattr(d, name) for name, _ in MatrixDesc._fields_}
+
+    def dequantize(self, out) -> None:
+        check(lib().air_hip_matrix_dequantize(self.ctx.handle, self.handle, ptr(out)))
+
+    def linear(self, x, y, m: int, bias=None, tactic: int = LINEAR_AUTO) -> None:
+        check(lib().air_hip_linear(self.ctx.handle, self.handle, ptr(x), ptr(y), ptr(bias), m, tactic))
+
+    def release(self) -> None:
+        if self.handle:
+            check(lib().air_hip_matrix_release(self.handle))
+            self.handle = None

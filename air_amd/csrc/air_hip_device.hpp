@@ -1,0 +1,88 @@
+// air_hip_device.hpp -- device helpers shared by the HIP kernels.
+#pragma once
+
+#include "air_hip_layout.hpp"
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace air_hip {
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+// Exact IEEE half -> single from the bit pattern, integer-only so NaN
+// payloads and subnormals decode exactly as src/reference/tensor_reader.cpp:11-36.
+__device__ __forceinline__ float f16_bits_to_f32(std::uint32_t h) {
+    const std::uint32_t sign = (h & 0x8000u) << 16;
+    const std::uint32_t exponent = (h >> 10) & 0x1fu;
+    std::uint32_t mantissa = h & 0x03ffu;
+    std::uint32_t bits;
+    if (exponent == 0u) {
+        if (mantissa == 0u) {
+            bits = sign;
+        } else {
+            // value = mantissa * 2^-24: normalise with one count-leading-zeros
+            const std::uint32_t shift = __clz(mantissa) - 21u; // bit 10 reached
+            mantissa = (mantissa << shift) & 0x03ffu;
+            bits = sign | ((113u - shift) << 23) | (mantissa << 13);
+        }
+    } else if (exponent == 0x1fu) {
+        bits = sign | 0x7f800000u | (mantissa << 13);
+    } else {
+        bits = sign | ((exponent + 112u) << 23) | (mantissa << 13);
+    }
+    return __uint_as_float(bits);
+}
+
+__device__ __forceinline__ half2v bits_as_half2(std::uint32_t v) {
+    return __builtin_bit_cast(half2v, v);
+}
+
+// Four biased Q8_0 codes u = q + 128 (one dword) -> four exact f16 values q.
+// v_perm_b32 places each byte under the exponent byte 0x64: f16 0x64uu = 1024+u.
+__device__ __forceinline__ void q8_dword_to_half(std::uint32_t u, half2v& lo, half2v& hi) {
+    const half2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    lo = bits_as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias;
+    hi = bits_as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias;
+}
+
+// One nibble dword (placement kNibblePos) -> eight exact f16 values n - offset.
+template <int Offset>
+__device__ __forceinline__ half8v nibble_dword_to_half8(std::uint32_t w) {
+    const half2v b_hi = {(_Float16)(1024.0f + Offset), (_Float16)(1024.0f + Offset)};
+    const half2v b_lo = {(_Float16)(64.0f + Offset), (_Float16)(64.0f + Offset)};
+    const std::uint32_t w8 = w >> 8;
+    const half2v p0 = bits_as_half2((w & 0x000f000fu) | 0x64006400u) - b_hi;
+    const half2v p1 = bits_as_half2((w & 0x00f000f0u) | 0x54005400u) - b_lo;
+    const half2v p2 = bits_as_half2((w8 & 0x000f000fu) | 0x64006400u) - b_hi;
+    const half2v p3 = bits_as_half2((w8 & 0x00f000f0u) | 0x54005400u) - b_lo;
+    half8v out;
+    out[0] = p0[0]; out[1] = p0[1]; out[2] = p1[0]; out[3] = p1[1];
+    out[4] = p2[0]; out[5] = p2[1]; out[6] = p3[0]; out[7] = p3[1];
+    return out;
+}
+
+// Q4_K 6-bit scale/min of sub-block j from the 12 packed bytes
+// (src/reference/tensor_reader.cpp:153-165).  `s` holds the three dwords of
+// the packed bytes (little-endian).
+__device__ __forceinline__ std::uint32_t byte_of(const std::uint32_t s[3], std::uint32_t i) {
+    return (s[i >> 2] >> ((i & 3u) * 8u)) & 0xffu;
+}
+__device__ __forceinline__ void q4k_scale_min(const std::uint32_t s[3], std::uint32_t j,
+                                              std::uint32_t& sc, std::uint32_t& mn) {
+    if (j < 4u) {
+        sc = byte_of(s, j) & 63u;
+        mn = byte_of(s, j + 4u) & 63u;
+    } else {
+        sc = (byte_of(s, j + 4u) & 0x0fu) | ((byte_of(s, j - 4u) >> 6) << 4);
+        mn = (byte_of(s, j + 4u) >> 4) | ((byte_of(s, j) >> 6) << 4);
+    }
+}
+
+__device__ __forceinline__ float4v mfma16x16x32(const half8v& a, const half8v& b, const float4v& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+} // namespace air_hip

@@ -1,0 +1,381 @@
+// capi.hip -- the C ABI of libair_hip.so (include/air_hip.h).
+//
+// Host-side owner of contexts (device + stream + workspace) and resident
+// matrices; validates every argument, launches the kernels and maps HIP
+// failures onto air_hip_status.  Structure follows CudaExecutor::Impl's
+// residency/dispatch duties (src/cuda/cuda_backend.cu:1435-1478,1773-1869,
+// 1898-2124) without its per-call tensor-name lookup: callers hold matrix
+// handles.
+#include "../../include/air_hip.h"
+
+#include "air_hip_kernels.hpp"
+#include "air_hip_layout.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+#include <new>
+#include <string>
+
+using namespace air_hip;
+
+struct air_hip_context {
+    int device{0};
+    hipStream_t stream{nullptr};
+    void* workspace{nullptr};
+    std::uint64_t workspace_bytes{0};
+    std::atomic<std::uint64_t> resident_matrix_bytes{0};
+    std::atomic<std::uint64_t> host_to_device_bytes{0};
+    std::atomic<std::uint64_t> prepared_matrices{0};
+    std::atomic<std::uint64_t> decode_linear_calls{0};
+    std::atomic<std::uint64_t> prefill_linear_calls{0};
+    std::atomic<std::uint64_t> decode_rows{0};
+    std::atomic<std::uint64_t> prefill_rows{0};
+};
+
+struct air_hip_matrix {
+    air_hip_context* owner{nullptr};
+    TilePlanes planes;
+    std::uint64_t canonical_bytes{0};
+    std::uint64_t resident_bytes{0};
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return status;
+}
+
+int hip_fail(hipError_t err, const char* what) {
+    return fail(AIR_HIP_INTERNAL_ERROR, "%s: %s", what, hipGetErrorString(err));
+}
+
+// Makes ctx->device current for the scope and restores the caller's device.
+class DeviceScope {
+public:
+    explicit DeviceScope(int device) {
+        if (hipGetDevice(&previous_) != hipSuccess) previous_ = -1;
+        status_ = hipSetDevice(device);
+    }
+    ~DeviceScope() {
+        if (previous_ >= 0) (void)hipSetDevice(previous_);
+    }
+    hipError_t status() const { return status_; }
+
+private:
+    int previous_{-1};
+    hipError_t status_{hipSuccess};
+};
+
+std::uint64_t resident_plane_bytes(const TilePlanes& p, std::uint64_t& scale_bytes) {
+    const auto geo = geometry_of(p.type);
+    const std::uint64_t tiles = static_cast<std::uint64_t>(p.nt) * p.kt;
+    scale_bytes = tiles * geo.scale_tile_bytes;
+    return tiles * geo.code_tile_bytes;
+}
+
+int ensure_workspace(air_hip_context* ctx, std::uint64_t bytes) {
+    if (bytes <= ctx->workspace_bytes) return AIR_HIP_OK;
+    if (ctx->workspace) {
+        // The old workspace may still be read by queued kernels.
+        const hipError_t sync = hipStreamSynchronize(ctx->stream);
+        if (sync != hipSuccess) return hip_fail(sync, "hipStreamSynchronize(workspace growth)");
+        (void)hipFree(ctx->workspace);
+        ctx->workspace = nullptr;
+        ctx->workspace_bytes = 0;
+    }
+    void* p = nullptr;
+    const hipError_t err = hipMalloc(&p, bytes);
+    if (err != hipSuccess) return hip_fail(err, "hipMalloc(workspace)");
+    ctx->workspace = p;
+    ctx->workspace_bytes = bytes;
+    return AIR_HIP_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+int air_hip_abi_version(void) { return AIR_HIP_ABI_VERSION; }
+
+const char* air_hip_status_string(int status) {
+    switch (status) {
+    case AIR_HIP_OK: return "ok";
+    case AIR_HIP_INVALID_ARGUMENT: return "invalid_argument";
+    case AIR_HIP_INVALID_STATE: return "invalid_state";
+    case AIR_HIP_IO_ERROR: return "io_error";
+    case AIR_HIP_CANCELLED: return "cancelled";
+    case AIR_HIP_DATA_ERROR: return "data_error";
+    case AIR_HIP_UNSUPPORTED: return "unsupported";
+    case AIR_HIP_INTERNAL_ERROR: return "internal_error";
+    default: return "unknown";
+    }
+}
+
+const char* air_hip_last_error(void) { return g_last_error.c_str(); }
+
+int air_hip_device_count(int* count) {
+    if (!count) return fail(AIR_HIP_INVALID_ARGUMENT, "count must not be null");
+    int n = 0;
+    const hipError_t err = hipGetDeviceCount(&n);
+    if (err == hipErrorNoDevice) { *count = 0; return AIR_HIP_OK; }
+    if (err != hipSuccess) return hip_fail(err, "hipGetDeviceCount");
+    *count = n;
+    return AIR_HIP_OK;
+}
+
+int air_hip_mem_info(int device, uint64_t* free_bytes, uint64_t* total_bytes) {
+    if (!free_bytes || !total_bytes) return fail(AIR_HIP_INVALID_ARGUMENT, "outputs must not be null");
+    DeviceScope scope(device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    std::size_t f = 0, t = 0;
+    const hipError_t err = hipMemGetInfo(&f, &t);
+    if (err != hipSuccess) return hip_fail(err, "hipMemGetInfo");
+    *free_bytes = f;
+    *total_bytes = t;
+    return AIR_HIP_OK;
+}
+
+int air_hip_context_create(int device, void* stream, air_hip_context** out) {
+    if (!out) return fail(AIR_HIP_INVALID_ARGUMENT, "out must not be null");
+    *out = nullptr;
+    int n = 0;
+    hipError_t err = hipGetDeviceCount(&n);
+    if (err != hipSuccess || n == 0) return fail(AIR_HIP_UNSUPPORTED, "no HIP device is available");
+    if (device < 0 || device >= n) return fail(AIR_HIP_INVALID_ARGUMENT, "device %d is out of range", device);
+    hipDeviceProp_t prop{};
+    err = hipGetDeviceProperties(&prop, device);
+    if (err != hipSuccess) return hip_fail(err, "hipGetDeviceProperties");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        return fail(AIR_HIP_UNSUPPORTED, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
+    }
+    auto* ctx = new (std::nothrow) air_hip_context();
+    if (!ctx) return fail(AIR_HIP_INTERNAL_ERROR, "out of host memory");
+    ctx->device = device;
+    ctx->stream = static_cast<hipStream_t>(stream);
+    *out = ctx;
+    return AIR_HIP_OK;
+}
+
+int air_hip_context_destroy(air_hip_context* ctx) {
+    if (!ctx) return AIR_HIP_OK;
+    if (ctx->workspace) {
+        DeviceScope scope(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipFree(ctx->workspace);
+    }
+    delete ctx;
+    return AIR_HIP_OK;
+}
+
+int air_hip_context_set_stream(air_hip_context* ctx, void* stream) {
+    if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
+    ctx->stream = static_cast<hipStream_t>(stream);
+    return AIR_HIP_OK;
+}
+
+int air_hip_context_reserve(air_hip_context* ctx, uint64_t max_k, uint32_t max_m) {
+    if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
+    if (max_k == 0 || max_m == 0) return AIR_HIP_OK;
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const std::uint64_t kp = ceil_div(max_k, 256u) * 256u;
+    return ensure_workspace(ctx, split_workspace_bytes(kp, max_m));
+}
+
+int air_hip_context_stats(const air_hip_context* ctx, air_hip_stats* out) {
+    if (!ctx || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    out->resident_matrix_bytes = ctx->resident_matrix_bytes.load(std::memory_order_relaxed);
+    out->workspace_bytes = ctx->workspace_bytes;
+    out->host_to_device_bytes = ctx->host_to_device_bytes.load(std::memory_order_relaxed);
+    out->prepared_matrices = ctx->prepared_matrices.load(std::memory_order_relaxed);
+    out->decode_linear_calls = ctx->decode_linear_calls.load(std::memory_order_relaxed);
+    out->prefill_linear_calls = ctx->prefill_linear_calls.load(std::memory_order_relaxed);
+    out->decode_rows = ctx->decode_rows.load(std::memory_order_relaxed);
+    out->prefill_rows = ctx->prefill_rows.load(std::memory_order_relaxed);
+    return AIR_HIP_OK;
+}
+
+uint64_t air_hip_canonical_bytes(int type, uint64_t k, uint64_t n) {
+    const auto geo = geometry_of(type);
+    if (geo.block_elements == 0 || k % geo.block_elements != 0) return 0;
+    const std::uint64_t blocks = k / geo.block_elements;
+    if (n != 0 && blocks > std::numeric_limits<std::uint64_t>::max() / geo.block_bytes / n) return 0;
+    return blocks * geo.block_bytes * n;
+}
+
+int air_hip_matrix_prepare(air_hip_context* ctx, int type, uint64_t k, uint64_t n,
+                           const void* canonical, uint64_t canonical_bytes, int bytes_on_device,
+                           air_hip_matrix** out) {
+    if (!out) return fail(AIR_HIP_INVALID_ARGUMENT, "out must not be null");
+    *out = nullptr;
+    if (!ctx || !canonical) return fail(AIR_HIP_INVALID_ARGUMENT, "context and bytes must not be null");
+    const auto geo = geometry_of(type);
+    if (geo.block_elements == 0) return fail(AIR_HIP_UNSUPPORTED, "tensor type %d is not executed by the HIP engine", type);
+    if (k == 0 || n == 0) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix dims must be non-zero");
+    if (k % geo.block_elements != 0) {
+        return fail(AIR_HIP_UNSUPPORTED, "input width %llu is not a multiple of the %u-element block",
+                    static_cast<unsigned long long>(k), geo.block_elements);
+    }
+    const std::uint64_t expected = air_hip_canonical_bytes(type, k, n);
+    if (expected == 0 || canonical_bytes != expected) {
+        return fail(AIR_HIP_DATA_ERROR, "canonical size %llu does not match %llu for {%llu, %llu}",
+                    static_cast<unsigned long long>(canonical_bytes), static_cast<unsigned long long>(expected),
+                    static_cast<unsigned long long>(k), static_cast<unsigned long long>(n));
+    }
+    const std::uint64_t nt64 = ceil_div(n, kTileRows);
+    const std::uint64_t kt64 = ceil_div(k, geo.tile_k);
+    if (nt64 > std::numeric_limits<std::uint32_t>::max() / 4u || kt64 > std::numeric_limits<std::uint32_t>::max()) {
+        return fail(AIR_HIP_UNSUPPORTED, "matrix is too large for the tile grid");
+    }
+
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+
+    auto* m = new (std::nothrow) air_hip_matrix();
+    if (!m) return fail(AIR_HIP_INTERNAL_ERROR, "out of host memory");
+    m->owner = ctx;
+    m->canonical_bytes = canonical_bytes;
+    TilePlanes& p = m->planes;
+    p.type = type;
+    p.k = k;
+    p.n = n;
+    p.nt = static_cast<std::uint32_t>(nt64);
+    p.kt = static_cast<std::uint32_t>(kt64);
+    p.kp = kt64 * geo.tile_k;
+    std::uint64_t scale_bytes = 0;
+    const std::uint64_t code_bytes = resident_plane_bytes(p, scale_bytes);
+
+    hipError_t err = hipMalloc(&p.codes, code_bytes);
+    if (err == hipSuccess) err = hipMalloc(&p.scales, scale_bytes);
+    if (err != hipSuccess) {
+        (void)hipFree(p.codes);
+        delete m;
+        return hip_fail(err, "hipMalloc(resident planes)");
+    }
+
+    const std::uint8_t* src = static_cast<const std::uint8_t*>(canonical);
+    void* staging = nullptr;
+    if (!bytes_on_device) {
+        err = hipMalloc(&staging, canonical_bytes);
+        if (err == hipSuccess) err = hipMemcpyAsync(staging, canonical, canonical_bytes, hipMemcpyHostToDevice, ctx->stream);
+        if (err != hipSuccess) {
+            (void)hipFree(staging);
+            (void)hipFree(p.codes);
+            (void)hipFree(p.scales);
+            delete m;
+            return hip_fail(err, "upload of canonical bytes");
+        }
+        src = static_cast<const std::uint8_t*>(staging);
+        ctx->host_to_device_bytes.fetch_add(canonical_bytes, std::memory_order_relaxed);
+    }
+    err = launch_repack(p, src, ctx->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
+    if (staging) (void)hipFree(staging);
+    if (err != hipSuccess) {
+        (void)hipFree(p.codes);
+        (void)hipFree(p.scales);
+        delete m;
+        return hip_fail(err, "repack");
+    }
+    m->resident_bytes = code_bytes + scale_bytes;
+    ctx->resident_matrix_bytes.fetch_add(m->resident_bytes, std::memory_order_relaxed);
+    ctx->prepared_matrices.fetch_add(1, std::memory_order_relaxed);
+    *out = m;
+    return AIR_HIP_OK;
+}
+
+int air_hip_matrix_release(air_hip_matrix* m) {
+    if (!m) return AIR_HIP_OK;
+    {
+        DeviceScope scope(m->owner->device);
+        (void)hipStreamSynchronize(m->owner->stream);
+        (void)hipFree(m->planes.codes);
+        (void)hipFree(m->planes.scales);
+    }
+    m->owner->resident_matrix_bytes.fetch_sub(m->resident_bytes, std::memory_order_relaxed);
+    delete m;
+    return AIR_HIP_OK;
+}
+
+int air_hip_matrix_describe(const air_hip_matrix* m, air_hip_matrix_desc* out) {
+    if (!m || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    out->type = m->planes.type;
+    out->device = m->owner->device;
+    out->k = m->planes.k;
+    out->n = m->planes.n;
+    out->canonical_bytes = m->canonical_bytes;
+    out->resident_bytes = m->resident_bytes;
+    return AIR_HIP_OK;
+}
+
+int air_hip_matrix_dequantize(air_hip_context* ctx, const air_hip_matrix* m, float* out) {
+    if (!ctx || !m || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const hipError_t err = launch_dequantize_tiles(m->planes, out, ctx->stream);
+    if (err != hipSuccess) return hip_fail(err, "dequantize_tiles_kernel");
+    return AIR_HIP_OK;
+}
+
+int air_hip_dequantize_canonical(air_hip_context* ctx, int type, const void* canonical,
+                                 uint64_t canonical_bytes, uint64_t elements, float* out) {
+    if (!ctx || !canonical || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    const auto geo = geometry_of(type);
+    if (geo.block_elements == 0) return fail(AIR_HIP_UNSUPPORTED, "tensor type %d is not decoded by the HIP engine", type);
+    if (elements % geo.block_elements != 0 || canonical_bytes != (elements / geo.block_elements) * geo.block_bytes) {
+        return fail(AIR_HIP_DATA_ERROR, "canonical storage geometry mismatch");
+    }
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const hipError_t err = launch_dequantize_canonical(type, static_cast<const std::uint8_t*>(canonical),
+                                                       elements, out, ctx->stream);
+    if (err != hipSuccess) return hip_fail(err, "dequantize_canonical_kernel");
+    return AIR_HIP_OK;
+}
+
+int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y,
+                   const float* bias, uint32_t rows, int tactic) {
+    if (!ctx || !m || !x || !y) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix, x and y must not be null");
+    if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
+    if (rows == 0) return fail(AIR_HIP_INVALID_ARGUMENT, "linear batch width must be non-zero");
+    if (tactic != AIR_HIP_LINEAR_AUTO && tactic != AIR_HIP_LINEAR_DECODE && tactic != AIR_HIP_LINEAR_PREFILL) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "unknown linear tactic %d", tactic);
+    }
+    if (tactic == AIR_HIP_LINEAR_PREFILL) {
+        return fail(AIR_HIP_UNSUPPORTED, "the prefill MFMA tactic is not available in this build");
+    }
+    if (rows > 4096u) return fail(AIR_HIP_UNSUPPORTED, "linear batch width %u exceeds 4096", rows);
+    if (static_cast<const void*>(x) == static_cast<const void*>(y)) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "y must not alias x");
+    }
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+
+    const TilePlanes& p = m->planes;
+    int rc = ensure_workspace(ctx, split_workspace_bytes(p.kp, rows));
+    if (rc != AIR_HIP_OK) return rc;
+    const SplitWorkspace ws = carve_split_workspace(ctx->workspace, p.kp, rows);
+    hipError_t err = launch_split_activations(x, rows, p.k, p.kp, ws, ctx->stream);
+    if (err != hipSuccess) return hip_fail(err, "split_activations_kernel");
+    err = launch_decode_linear(p, ws, bias, y, rows, ctx->stream);
+    if (err != hipSuccess) return hip_fail(err, "decode_linear_kernel");
+    ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
+    ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
+    return AIR_HIP_OK;
+}
+
+} // extern "C"

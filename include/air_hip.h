@@ -1,0 +1,178 @@
+/*
+ * air_hip.h -- C ABI of the MI355X quantized linear engine (libair_hip.so).
+ *
+ * The engine executes AIR's quantized linear contract -- a GGUF Q8_0 / Q4_0 /
+ * Q4_K weight matrix with GGML dims {K, N} applied to M f32 activation rows --
+ * on one AMD Instinct MI355X (gfx950) with hand-written HIP kernels.  It is
+ * the device half of a HIP executor that plugs in behind AIR's executor
+ * contract (src/runtime/backend.hpp:97-145) the way CudaExecutor does.
+ *
+ * Conventions
+ *   - Plain C: no C++ or HIP types cross this boundary.  Streams are passed
+ *     as `void*` holding a hipStream_t (NULL = the legacy default stream).
+ *   - Every function returns an air_hip_status; on failure
+ *     air_hip_last_error() holds a message for the calling thread.  Nothing
+ *     throws across the boundary (src/cuda/cuda_backend.cu:1180-1182 checks
+ *     every launch the same way).
+ *   - Activation and output pointers are non-owning device pointers; matrices
+ *     and contexts are owned by the library and released explicitly.
+ *   - Results are deterministic: a fixed launch configuration sums in a fixed
+ *     order.
+ *
+ * Type ids are GGML/GGUF on-disk tensor type ids (the reference's
+ * TensorDescriptor::format_type, src/formats/gguf/gguf_format.cpp:24-63).
+ */
+#ifndef AIR_HIP_H
+#define AIR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AIR_HIP_ABI_VERSION 1
+
+/* Mirrors air::ErrorCode (include/air/status.hpp:8-17). */
+typedef enum air_hip_status {
+    AIR_HIP_OK = 0,
+    AIR_HIP_INVALID_ARGUMENT = 1,
+    AIR_HIP_INVALID_STATE = 2,
+    AIR_HIP_IO_ERROR = 3,
+    AIR_HIP_CANCELLED = 4,
+    AIR_HIP_DATA_ERROR = 5,
+    AIR_HIP_UNSUPPORTED = 6,
+    AIR_HIP_INTERNAL_ERROR = 7
+} air_hip_status;
+
+/* GGML type ids this engine executes. */
+enum {
+    AIR_HIP_TYPE_Q4_0 = 2,
+    AIR_HIP_TYPE_Q8_0 = 8,
+    AIR_HIP_TYPE_Q4_K = 12
+};
+
+/* Linear tactics: the HIP members of AIR's QuantizedLinearExecutionKind
+ * (include/air/execution.hpp:159-165).
+ *   DECODE  exact integer codes as f16 MFMA operands, activations split into
+ *           f16 hi+lo parts with a per-row power-of-two scale, per-block f32
+ *           scale epilogue.  M = 1..64.  Relative L2 error vs the double
+ *           oracle ~1e-6 (gate 1e-4).  Replaces specialized_matvec_kernel /
+ *           specialized_matmul_batch_reuse_kernel (cuda_backend.cu:501-606).
+ *   PREFILL weights dequantised to f16, activations rounded to f16, f16
+ *           MFMA with f32 accumulation for prefill-sized M (gate 1e-2).
+ *           Replaces the dense-f32 dequantise + GEMM tactic
+ *           (cuda_backend.cu:375-382,1971-1992).
+ *   AUTO    DECODE for M <= 64, PREFILL above. */
+enum {
+    AIR_HIP_LINEAR_AUTO = 0,
+    AIR_HIP_LINEAR_DECODE = 1,
+    AIR_HIP_LINEAR_PREFILL = 2
+};
+
+#define AIR_HIP_MAX_DECODE_ROWS 64u
+
+typedef struct air_hip_context air_hip_context;
+typedef struct air_hip_matrix air_hip_matrix;
+
+typedef struct air_hip_matrix_desc {
+    int32_t type;               /* GGML type id */
+    int32_t device;             /* device ordinal holding the planes */
+    uint64_t k;                 /* input width (GGML dim 0) */
+    uint64_t n;                 /* output width (GGML dim 1) */
+    uint64_t canonical_bytes;   /* exact GGUF storage size */
+    uint64_t resident_bytes;    /* device bytes of the repacked planes */
+} air_hip_matrix_desc;
+
+/* Hot-path evidence counters, the HIP analogue of CudaExecutionStats
+ * (include/air/cuda.hpp:19-54).  Cumulative per context; relaxed atomics. */
+typedef struct air_hip_stats {
+    uint64_t resident_matrix_bytes;
+    uint64_t workspace_bytes;
+    uint64_t host_to_device_bytes;
+    uint64_t prepared_matrices;
+    uint64_t decode_linear_calls;
+    uint64_t prefill_linear_calls;
+    uint64_t decode_rows;
+    uint64_t prefill_rows;
+} air_hip_stats;
+
+/* ---- library ---------------------------------------------------------- */
+
+int air_hip_abi_version(void);
+const char* air_hip_status_string(int status);
+/* Message of the calling thread's most recent failure ("" if none). */
+const char* air_hip_last_error(void);
+
+/* Number of visible HIP devices.  cuda_devices() (cuda_backend.cu:2447-2471). */
+int air_hip_device_count(int* count);
+/* Free and total device memory of `device` via hipMemGetInfo; the source of
+ * PreparedModel::free_device_bytes / sequence_capacity_bytes
+ * (src/runtime/backend.cpp:541-560). */
+int air_hip_mem_info(int device, uint64_t* free_bytes, uint64_t* total_bytes);
+
+/* ---- context: one device, one stream, one workspace -------------------- */
+
+/* Binds `device` and `stream` (a hipStream_t or NULL), like
+ * CudaExecutor::create / Impl::initialize (cuda_backend.cu:1773-1776).  The
+ * context owns the activation workspace; calls through one context are
+ * ordered on its stream, so one context must not be used from two threads
+ * at once. */
+int air_hip_context_create(int device, void* stream, air_hip_context** out);
+int air_hip_context_destroy(air_hip_context* ctx);
+int air_hip_context_set_stream(air_hip_context* ctx, void* stream);
+/* Grows the workspace so linears with input width <= max_k and up to max_m
+ * rows never allocate on the hot path (workspace sizing,
+ * cuda_backend.cu:1825-1869).  Without it the first call that needs more
+ * space allocates. */
+int air_hip_context_reserve(air_hip_context* ctx, uint64_t max_k, uint32_t max_m);
+int air_hip_context_stats(const air_hip_context* ctx, air_hip_stats* out);
+
+/* ---- matrices ----------------------------------------------------------- */
+
+/* Exact GGUF storage size of a {k, n} matrix of `type`, 0 if unsupported
+ * (gguf_format.cpp:246-259). */
+uint64_t air_hip_canonical_bytes(int type, uint64_t k, uint64_t n);
+
+/* Makes a {k, n} matrix resident: canonical GGUF bytes (host memory when
+ * bytes_on_device == 0, else device memory of the context's device) are
+ * repacked once into the wavefront tile layout.  This is the residency step
+ * of Impl::initialize (cuda_backend.cu:1790-1822) plus the one-time repack
+ * the reference does only for dp4a (pack_signed32_weights_kernel,
+ * cuda_backend.cu:398-427).  k must be a multiple of the block size
+ * (cuda_backend.cu:1797-1801).  Blocks until the repack has finished. */
+int air_hip_matrix_prepare(air_hip_context* ctx, int type, uint64_t k, uint64_t n,
+                           const void* canonical, uint64_t canonical_bytes,
+                           int bytes_on_device, air_hip_matrix** out);
+int air_hip_matrix_release(air_hip_matrix* matrix);
+int air_hip_matrix_describe(const air_hip_matrix* matrix, air_hip_matrix_desc* out);
+
+/* Decodes the resident matrix to f32 out[n][k] (device pointer), bit-exact
+ * with decode_all (src/reference/tensor_reader.cpp:51-247). */
+int air_hip_matrix_dequantize(air_hip_context* ctx, const air_hip_matrix* matrix, float* out);
+
+/* Decodes `elements` values of canonical GGUF bytes that are already in
+ * device memory into f32 `out` (device), bit-exact; the device analogue of
+ * decode_element / dequantize_to_f32_kernel (cuda_backend.cu:241-344,375-382). */
+int air_hip_dequantize_canonical(air_hip_context* ctx, int type, const void* canonical,
+                                 uint64_t canonical_bytes, uint64_t elements, float* out);
+
+/* ---- the linear --------------------------------------------------------- */
+
+/* y[m][n] = sum_k w[n][k] * x[m][k] (+ bias[n]) for m < M.
+ *   x    device f32 [M][k], row-major
+ *   y    device f32 [M][n], row-major (must not alias x)
+ *   bias device f32 [n] or NULL (fused; add_optional_tensor,
+ *        cuda_backend.cu:2143-2161 / reference_executor.cpp:315-323)
+ * Asynchronous on the context's stream.  Replaces Impl::matvec / matmul /
+ * linear_single (cuda_backend.cu:1898-2124). */
+int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* matrix,
+                   const float* x, float* y, const float* bias,
+                   uint32_t m, int tactic);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AIR_HIP_H */

@@ -1,0 +1,134 @@
+"""GPU parity of the HIP engine against the CPU oracle, through the C ABI.
+
+Dequantisation must be bit-exact (decode_all, tensor_reader.cpp:51-247);
+linear outputs must be within relative L2 1e-4 of the double-accumulating
+matvec (tensor_reader.cpp:369-394) on the decode tactic.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from air_amd import capi
+from tests import helpers
+
+pytestmark = pytest.mark.gpu
+
+DECODE_TOL = 1e-4
+FORMATS = [capi.TYPE_Q8_0, capi.TYPE_Q4_0, capi.TYPE_Q4_K]
+
+
+def _dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+@pytest.mark.parametrize("type_id", FORMATS)
+def test_dequantize_canonical_bit_exact(torch_cuda, hip_ctx, type_id):
+    torch = torch_cuda
+    be, bb = helpers.BLOCK[type_id]
+    for seed, finite in [(1, True), (2, True), (3, False)]:
+        raw = helpers.random_blocks(type_id, 257, seed, finite_scales=finite)
+        elements = 257 * be
+        want = oracle.decode(type_id, raw, elements)
+        src = _dev(torch, raw)
+        out = torch.empty(elements, dtype=torch.float32, device="cuda:0")
+        hip_ctx.dequantize_canonical(type_id, src, raw.nbytes, elements, out)
+        torch.cuda.synchronize()
+        assert helpers.same_bits(out.cpu().numpy(), want), (type_id, seed)
+
+
+@pytest.mark.parametrize("type_id,k,n", [
+    (capi.TYPE_Q8_0, 96, 37), (capi.TYPE_Q8_0, 896, 64), (capi.TYPE_Q8_0, 32, 1),
+    (capi.TYPE_Q4_0, 160, 45), (capi.TYPE_Q4_0, 896, 48),
+    (capi.TYPE_Q4_K, 256, 19), (capi.TYPE_Q4_K, 768, 40),
+])
+def test_resident_tiles_decode_bit_exact(torch_cuda, hip_ctx, type_id, k, n):
+    """The repacked planes decode to exactly the canonical values."""
+    torch = torch_cuda
+    be, bb = helpers.BLOCK[type_id]
+    raw = helpers.random_blocks(type_id, n * (k // be), seed=k * 31 + n)
+    want = oracle.decode(type_id, raw, n * k).reshape(n, k)
+    for on_device in (False, True):
+        src = _dev(torch, raw) if on_device else raw
+        mat = capi.Matrix(hip_ctx, type_id, k, n, src, raw.nbytes, on_device=on_device)
+        out = torch.empty((n, k), dtype=torch.float32, device="cuda:0")
+        mat.dequantize(out)
+        torch.cuda.synchronize()
+        assert helpers.same_bits(out.cpu().numpy(), want)
+        mat.release()
+
+
+CASES = [
+    # config 0 shape (Qwen2-0.5B FFN up-proj, Q8_0 4864 x 896)
+    (capi.TYPE_Q8_0, 896, 4864, [1, 2, 7, 16, 33, 64, 100]),
+    (capi.TYPE_Q8_0, 96, 37, [1, 5, 20]),
+    (capi.TYPE_Q8_0, 32, 1, [1, 3]),
+    (capi.TYPE_Q4_0, 896, 4864, [1, 16, 64]),
+    (capi.TYPE_Q4_0, 160, 45, [1, 3, 17]),
+    (capi.TYPE_Q4_K, 3584, 512, [1, 16, 64]),
+    (capi.TYPE_Q4_K, 256, 19, [1, 4]),
+    (capi.TYPE_Q4_K, 768, 40, [2, 31]),
+]
+
+
+@pytest.mark.parametrize("type_id,k,n,ms", CASES)
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_linear_matches_oracle(torch_cuda, hip_ctx, type_id, k, n, ms, with_bias):
+    torch = torch_cuda
+    canon = helpers.weights(type_id, k, n, seed=k + 7 * n + type_id)
+    mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    bias = (np.random.default_rng(5).standard_normal(n).astype(np.float32) * 0.02) if with_bias else None
+    bias_d = _dev(torch, bias) if with_bias else None
+    for m in ms:
+        x = helpers.activations(m, k, seed=m * 1000 + k)
+        want = oracle.linear(type_id, canon, k, n, x, bias=bias)
+        y = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+        mat.linear(_dev(torch, x), y, m, bias=bias_d, tactic=capi.LINEAR_DECODE)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        assert np.isfinite(got).all(), (type_id, k, n, m)
+        err = helpers.rel_l2(got, want)
+        assert err <= DECODE_TOL, (type_id, k, n, m, err)
+    mat.release()
+
+
+def test_linear_scale_extremes(torch_cuda, hip_ctx):
+    """Activations far from unit scale keep full relative precision
+    (per-row power-of-two scaling of the split activations)."""
+    torch = torch_cuda
+    k, n = 896, 256
+    canon = helpers.weights(capi.TYPE_Q8_0, k, n, seed=11)
+    mat = capi.Matrix(hip_ctx, capi.TYPE_Q8_0, k, n, canon, canon.nbytes, on_device=False)
+    base = helpers.activations(4, k, seed=3)
+    x = base * np.array([[1e-6], [1.0], [3e3], [6e4]], dtype=np.float32)
+    want = oracle.linear(capi.TYPE_Q8_0, canon, k, n, x)
+    y = torch.empty((4, n), dtype=torch.float32, device="cuda:0")
+    mat.linear(_dev(torch, x), y, 4)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    for i in range(4):
+        assert helpers.rel_l2(got[i], want[i]) <= DECODE_TOL, i
+    mat.release()
+
+
+def test_linear_rejects_bad_arguments(torch_cuda, hip_ctx):
+    torch = torch_cuda
+    k, n = 64, 16
+    canon = helpers.weights(capi.TYPE_Q8_0, k, n, seed=1)
+    with pytest.raises(capi.HipError) as e:
+        capi.Matrix(hip_ctx, capi.TYPE_Q8_0, k, n, canon, canon.nbytes - 1, on_device=False)
+    assert e.value.status_name == "data_error"
+    with pytest.raises(capi.HipError) as e:
+        capi.Matrix(hip_ctx, capi.TYPE_Q8_0, 48, n, canon, canon.nbytes, on_device=False)
+    assert e.value.status_name == "unsupported"
+    mat = capi.Matrix(hip_ctx, capi.TYPE_Q8_0, k, n, canon, canon.nbytes, on_device=False)
+    x = torch.zeros((1, k), device="cuda:0")
+    y = torch.zeros((1, n), device="cuda:0")
+    with pytest.raises(capi.HipError) as e:
+        mat.linear(x, y, 0)
+    assert e.value.status_name == "invalid_argument"
+    with pytest.raises(capi.HipError) as e:
+        mat.linear(x, y, 1, tactic=99)
+    assert e.value.status_name == "invalid_argument"
+    mat.release()
