@@ -79,12 +79,15 @@ SIGNATURES = {
     "air_hip_context_set_stream": (_I, [_P, _P]),
     "air_hip_context_reserve": (_I, [_P, _U64, _U32]),
     "air_hip_context_stats": (_I, [_P, ctypes.POINTER(Stats)]),
+    "air_hip_context_set_tuning": (_I, [_P, _U32, _U32, _U32]),
     "air_hip_canonical_bytes": (_U64, [_I, _U64, _U64]),
     "air_hip_matrix_prepare": (_I, [_P, _I, _U64, _U64, _P, _U64, _I, ctypes.POINTER(_P)]),
     "air_hip_matrix_release": (_I, [_P]),
     "air_hip_matrix_describe": (_I, [_P, ctypes.POINTER(MatrixDesc)]),
     "air_hip_matrix_dequantize": (_I, [_P, _P, _P]),
     "air_hip_dequantize_canonical": (_I, [_P, _I, _P, _U64, _U64, _P]),
+    "air_hip_activations_load": (_I, [_P, _P, _U64, _U32]),
+    "air_hip_linear_loaded": (_I, [_P, _P, _P, _P, _I]),
     "air_hip_linear": (_I, [_P, _P, _P, _P, _P, _U32, _I]),
 }
 
@@ -167,6 +170,9 @@ class Context:
     def reserve(self, max_k: int, max_m: int) -> None:
         check(lib().air_hip_context_reserve(self.handle, max_k, max_m))
 
+    def set_tuning(self, rows_per_wave: int = 0, waves_per_group: int = 0, k_splits: int = 0) -> None:
+        check(lib().air_hip_context_set_tuning(self.handle, rows_per_wave, waves_per_group, k_splits))
+
     def stats(self) -> dict:
         s = Stats()
         check(lib().air_hip_context_stats(self.handle, ctypes.byref(s)))
@@ -182,6 +188,10 @@ class Context:
 
     def __exit__(self, *exc):
         self.close()
+
+    def load_activations(self, x, k: int, m: int) -> None:
+        """Stage 1 of a linear: split x [m][k] into this context's workspace."""
+        check(lib().air_hip_activations_load(self.handle, ptr(x), k, m))
 
     def dequantize_canonical(self, type_id: int, canonical, nbytes: int, elements: int, out) -> None:
         check(lib().air_hip_dequantize_canonical(self.handle, type_id, ptr(canonical), nbytes, elements, ptr(out)))
@@ -211,6 +221,10 @@ class Matrix:
 
     def linear(self, x, y, m: int, bias=None, tactic: int = LINEAR_AUTO) -> None:
         check(lib().air_hip_linear(self.ctx.handle, self.handle, ptr(x), ptr(y), ptr(bias), m, tactic))
+
+    def linear_loaded(self, y, bias=None, tactic: int = LINEAR_AUTO) -> None:
+        """Stage 2 of a linear, over the context's loaded activations."""
+        check(lib().air_hip_linear_loaded(self.ctx.handle, self.handle, ptr(y), ptr(bias), tactic))
 
     def release(self) -> None:
         if self.handle:

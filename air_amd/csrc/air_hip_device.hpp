@@ -85,4 +85,37 @@ __device__ __forceinline__ float4v mfma16x16x32(const half8v& a, const half8v& b
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Power-of-two scale of one (row, 32-element block) of activations: with
+// amax = max|x| over the block, amax*s lies in [2^14, 2^15), so the f16 hi
+// part cannot overflow and the lo part keeps the residual.  Zero and
+// non-finite blocks are left unscaled (NaN/inf then propagate as in f32).
+__device__ __forceinline__ void block_scale(float amax, float& s, float& inv) {
+    const std::uint32_t e = (__float_as_uint(amax) >> 23) & 0xffu;
+    if (!(amax > 0.0f) || e == 0xffu) {
+        s = 1.0f;
+        inv = 1.0f;
+        return;
+    }
+    int se = 268 - static_cast<int>(e);  // s = 2^(141 - e)
+    se = se > 253 ? 253 : se;
+    s = __uint_as_float(static_cast<std::uint32_t>(se) << 23);
+    inv = __uint_as_float(static_cast<std::uint32_t>(254 - se) << 23);
+}
+
+// Splits eight scaled activations v*s into f16 hi + lo with hi + lo = v*s to
+// ~21 significant bits (hi truncated, the exact f32 residual rounded).
+__device__ __forceinline__ void split8(const float (&v)[8], float s, half8v& hi, half8v& lo) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float a = v[2 * e] * s;
+        const float b = v[2 * e + 1] * s;
+        const auto h = __builtin_amdgcn_cvt_pkrtz(a, b);
+        const auto l = __builtin_amdgcn_cvt_pkrtz(a - static_cast<float>(h[0]), b - static_cast<float>(h[1]));
+        hi[2 * e] = static_cast<_Float16>(h[0]);
+        hi[2 * e + 1] = static_cast<_Float16>(h[1]);
+        lo[2 * e] = static_cast<_Float16>(l[0]);
+        lo[2 * e + 1] = static_cast<_Float16>(l[1]);
+    }
+}
+
 } // namespace air_hip

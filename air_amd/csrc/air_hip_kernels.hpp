@@ -27,20 +27,56 @@ hipError_t launch_dequantize_canonical(int type, const std::uint8_t* canonical,
 
 // Workspace of the split activations for `m` rows of width kp (padded).
 struct SplitWorkspace {
-    void* xs{nullptr};       // [kp/32][mp/16][2][64][8] f16  (hi, lo)
-    float* block_sums{nullptr}; // [kp/32][mp] f32  (sum of scaled x per 32-block)
-    float* inv_scale{nullptr};  // [mp] f32
+    void* xs{nullptr};          // [kp/32][mp/16][2][64][8] f16  (hi, lo), scaled per (block, row)
+    float* block_sums{nullptr}; // [kp/32][mp] f32  sum of the unscaled x of each 32-block
+    float* inv_scale{nullptr};  // [kp/32][mp] f32  inverse power-of-two scale of each (block, row)
+};
+
+// Launch-shape override of the decode linear (0 = automatic choice).
+struct DecodeTuning {
+    std::uint32_t rows_per_wave{0};   // 16-row tiles per wave: 1, 2 or 4
+    std::uint32_t waves_per_group{0}; // waves splitting K inside a workgroup
+    std::uint32_t k_splits{0};        // workgroups splitting K (fused path)
 };
 std::uint64_t split_workspace_bytes(std::uint64_t kp, std::uint32_t m);
 SplitWorkspace carve_split_workspace(void* base, std::uint64_t kp, std::uint32_t m);
 
-// Activation split: x [m][k] f32 -> per-row power-of-two scaled f16 hi/lo
-// tiles, scaled 32-block sums and inverse scales.  Rows m..mp-1 are zeroed.
+// Activation split: x [m][k] f32 -> f16 hi/lo tiles scaled per (32-block, row)
+// by a power of two, block sums and inverse scales.  Rows m..mp-1 are zeroed.
 hipError_t launch_split_activations(const float* x, std::uint32_t m, std::uint64_t k,
                                     std::uint64_t kp, const SplitWorkspace& ws, hipStream_t stream);
 
 // Decode linear over the split activations: y[m][n] (+ bias[n]).
 hipError_t launch_decode_linear(const TilePlanes& planes, const SplitWorkspace& ws,
-                                const float* bias, float* y, std::uint32_t m, hipStream_t stream);
+                                const float* bias, float* y, std::uint32_t m,
+                                const DecodeTuning& tuning, hipStream_t stream);
+
+// Single-launch decode linear for up to kFusedMaxRows rows: reads x [m][k]
+// f32 directly and splits it in registers (no workspace).
+constexpr std::uint32_t kFusedMaxRows = 16;
+struct FusedShape {
+    std::uint32_t rows_per_wave{1};
+    std::uint32_t waves_per_group{1};
+    std::uint32_t k_splits{1};
+    std::uint32_t groups{0};          // row-tile groups (grid x)
+};
+FusedShape plan_decode_fused(const TilePlanes& planes, std::uint32_t m, const DecodeTuning& tuning);
+// Device bytes of the cross-workgroup partials of a K-split launch (0 if none);
+// the launch also needs `groups` zero-initialised uint32 counters, which it
+// leaves at zero.
+std::uint64_t fused_split_workspace_bytes(const FusedShape& shape);
+hipError_t launch_decode_fused(const TilePlanes& planes, const float* x, const float* bias, float* y,
+                               std::uint32_t m, const FusedShape& shape, void* partials,
+                               std::uint32_t* counters, hipStream_t stream);
+
+// M = 1 decode linear (matrix-vector product) with block-diagonal activation
+// operands and whole-chunk prefetch.
+struct GemvShape {
+    std::uint32_t rows_per_wave{1};
+    std::uint32_t waves_per_group{1};
+};
+GemvShape plan_decode_gemv(const TilePlanes& planes, const DecodeTuning& tuning);
+hipError_t launch_decode_gemv(const TilePlanes& planes, const float* x, const float* bias, float* y,
+                              const GemvShape& shape, hipStream_t stream);
 
 } // namespace air_hip

@@ -35,6 +35,16 @@ struct air_hip_context {
     std::atomic<std::uint64_t> prefill_linear_calls{0};
     std::atomic<std::uint64_t> decode_rows{0};
     std::atomic<std::uint64_t> prefill_rows{0};
+    std::uint64_t loaded_k{0};       // width of the activations in the workspace
+    std::uint32_t loaded_rows{0};    // rows of the activations in the workspace (0 = none)
+    DecodeTuning tuning{};
+    // Cross-workgroup K-split of the fused decode linear: partial sums and one
+    // arrival counter per row group.  Counters are zeroed when allocated and
+    // every launch leaves them at zero.
+    void* split_partials{nullptr};
+    std::uint64_t split_partials_bytes{0};
+    std::uint32_t* split_counters{nullptr};
+    std::uint32_t split_counter_count{0};
 };
 
 struct air_hip_matrix {
@@ -47,6 +57,11 @@ struct air_hip_matrix {
 namespace {
 
 thread_local std::string g_last_error;
+
+// Activations are split over k padded to whole 256-element units, which
+// covers the k tile of every format.
+constexpr std::uint64_t kSplitK = 256;
+constexpr std::uint32_t kMaxRows = 4096;
 
 int fail(int status, const char* fmt, ...) {
     char buf[512];
@@ -101,6 +116,37 @@ int ensure_workspace(air_hip_context* ctx, std::uint64_t bytes) {
     if (err != hipSuccess) return hip_fail(err, "hipMalloc(workspace)");
     ctx->workspace = p;
     ctx->workspace_bytes = bytes;
+    return AIR_HIP_OK;
+}
+
+int ensure_split_buffers(air_hip_context* ctx, std::uint64_t partial_bytes, std::uint32_t counters) {
+    if (partial_bytes > ctx->split_partials_bytes || counters > ctx->split_counter_count) {
+        const hipError_t sync = hipStreamSynchronize(ctx->stream);
+        if (sync != hipSuccess) return hip_fail(sync, "hipStreamSynchronize(split buffer growth)");
+    }
+    if (partial_bytes > ctx->split_partials_bytes) {
+        (void)hipFree(ctx->split_partials);
+        ctx->split_partials = nullptr;
+        ctx->split_partials_bytes = 0;
+        const hipError_t err = hipMalloc(&ctx->split_partials, partial_bytes);
+        if (err != hipSuccess) return hip_fail(err, "hipMalloc(split partials)");
+        ctx->split_partials_bytes = partial_bytes;
+    }
+    if (counters > ctx->split_counter_count) {
+        (void)hipFree(ctx->split_counters);
+        ctx->split_counters = nullptr;
+        ctx->split_counter_count = 0;
+        const std::uint32_t count = counters < 4096u ? 4096u : counters;
+        void* p = nullptr;
+        hipError_t err = hipMalloc(&p, count * sizeof(std::uint32_t));
+        if (err == hipSuccess) err = hipMemset(p, 0, count * sizeof(std::uint32_t));
+        if (err != hipSuccess) {
+            (void)hipFree(p);
+            return hip_fail(err, "hipMalloc(split counters)");
+        }
+        ctx->split_counters = static_cast<std::uint32_t*>(p);
+        ctx->split_counter_count = count;
+    }
     return AIR_HIP_OK;
 }
 
@@ -171,10 +217,12 @@ int air_hip_context_create(int device, void* stream, air_hip_context** out) {
 
 int air_hip_context_destroy(air_hip_context* ctx) {
     if (!ctx) return AIR_HIP_OK;
-    if (ctx->workspace) {
+    {
         DeviceScope scope(ctx->device);
         (void)hipStreamSynchronize(ctx->stream);
-        (void)hipFree(ctx->workspace);
+        if (ctx->workspace) (void)hipFree(ctx->workspace);
+        if (ctx->split_partials) (void)hipFree(ctx->split_partials);
+        if (ctx->split_counters) (void)hipFree(ctx->split_counters);
     }
     delete ctx;
     return AIR_HIP_OK;
@@ -191,8 +239,22 @@ int air_hip_context_reserve(air_hip_context* ctx, uint64_t max_k, uint32_t max_m
     if (max_k == 0 || max_m == 0) return AIR_HIP_OK;
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-    const std::uint64_t kp = ceil_div(max_k, 256u) * 256u;
+    const std::uint64_t kp = ceil_div(max_k, kSplitK) * kSplitK;
     return ensure_workspace(ctx, split_workspace_bytes(kp, max_m));
+}
+
+int air_hip_context_set_tuning(air_hip_context* ctx, uint32_t rows_per_wave, uint32_t waves_per_group,
+                               uint32_t k_splits) {
+    if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
+    if (rows_per_wave != 0 && rows_per_wave != 1 && rows_per_wave != 2 && rows_per_wave != 4) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "rows_per_wave must be 0, 1, 2 or 4");
+    }
+    if (waves_per_group > 16) return fail(AIR_HIP_INVALID_ARGUMENT, "waves_per_group must be at most 16");
+    if (k_splits > 64) return fail(AIR_HIP_INVALID_ARGUMENT, "k_splits must be at most 64");
+    ctx->tuning.rows_per_wave = rows_per_wave;
+    ctx->tuning.waves_per_group = waves_per_group;
+    ctx->tuning.k_splits = k_splits;
+    return AIR_HIP_OK;
 }
 
 int air_hip_context_stats(const air_hip_context* ctx, air_hip_stats* out) {
@@ -347,35 +409,91 @@ int air_hip_dequantize_canonical(air_hip_context* ctx, int type, const void* can
     return AIR_HIP_OK;
 }
 
-int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y,
-                   const float* bias, uint32_t rows, int tactic) {
-    if (!ctx || !m || !x || !y) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix, x and y must not be null");
-    if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
+int air_hip_activations_load(air_hip_context* ctx, const float* x, uint64_t k, uint32_t rows) {
+    if (!ctx || !x) return fail(AIR_HIP_INVALID_ARGUMENT, "context and x must not be null");
     if (rows == 0) return fail(AIR_HIP_INVALID_ARGUMENT, "linear batch width must be non-zero");
+    if (rows > kMaxRows) return fail(AIR_HIP_UNSUPPORTED, "linear batch width %u exceeds %u", rows, kMaxRows);
+    if (k == 0 || k % 32u != 0) return fail(AIR_HIP_UNSUPPORTED, "input width must be a non-zero multiple of 32");
+    if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const std::uint64_t kp = ceil_div(k, kSplitK) * kSplitK;
+    int rc = ensure_workspace(ctx, split_workspace_bytes(kp, rows));
+    if (rc != AIR_HIP_OK) return rc;
+    const SplitWorkspace ws = carve_split_workspace(ctx->workspace, kp, rows);
+    const hipError_t err = launch_split_activations(x, rows, k, kp, ws, ctx->stream);
+    if (err != hipSuccess) return hip_fail(err, "split_activations_kernel");
+    ctx->loaded_k = k;
+    ctx->loaded_rows = rows;
+    return AIR_HIP_OK;
+}
+
+int air_hip_linear_loaded(air_hip_context* ctx, const air_hip_matrix* m, float* y, const float* bias, int tactic) {
+    if (!ctx || !m || !y) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix and y must not be null");
+    if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
     if (tactic != AIR_HIP_LINEAR_AUTO && tactic != AIR_HIP_LINEAR_DECODE && tactic != AIR_HIP_LINEAR_PREFILL) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "unknown linear tactic %d", tactic);
     }
     if (tactic == AIR_HIP_LINEAR_PREFILL) {
         return fail(AIR_HIP_UNSUPPORTED, "the prefill MFMA tactic is not available in this build");
     }
-    if (rows > 4096u) return fail(AIR_HIP_UNSUPPORTED, "linear batch width %u exceeds 4096", rows);
-    if (static_cast<const void*>(x) == static_cast<const void*>(y)) {
-        return fail(AIR_HIP_INVALID_ARGUMENT, "y must not alias x");
+    if (ctx->loaded_rows == 0) return fail(AIR_HIP_INVALID_STATE, "no activations are loaded in this context");
+    if (ctx->loaded_k != m->planes.k) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "loaded activations have width %llu, matrix expects %llu",
+                    static_cast<unsigned long long>(ctx->loaded_k), static_cast<unsigned long long>(m->planes.k));
     }
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-
-    const TilePlanes& p = m->planes;
-    int rc = ensure_workspace(ctx, split_workspace_bytes(p.kp, rows));
-    if (rc != AIR_HIP_OK) return rc;
-    const SplitWorkspace ws = carve_split_workspace(ctx->workspace, p.kp, rows);
-    hipError_t err = launch_split_activations(x, rows, p.k, p.kp, ws, ctx->stream);
-    if (err != hipSuccess) return hip_fail(err, "split_activations_kernel");
-    err = launch_decode_linear(p, ws, bias, y, rows, ctx->stream);
+    const std::uint32_t rows = ctx->loaded_rows;
+    const std::uint64_t kp = ceil_div(ctx->loaded_k, kSplitK) * kSplitK;
+    const SplitWorkspace ws = carve_split_workspace(ctx->workspace, kp, rows);
+    const hipError_t err = launch_decode_linear(m->planes, ws, bias, y, rows, ctx->tuning, ctx->stream);
     if (err != hipSuccess) return hip_fail(err, "decode_linear_kernel");
     ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
     ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
     return AIR_HIP_OK;
+}
+
+int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y,
+                   const float* bias, uint32_t rows, int tactic) {
+    if (!ctx || !m || !x || !y) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix, x and y must not be null");
+    if (static_cast<const void*>(x) == static_cast<const void*>(y)) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "y must not alias x");
+    }
+    if (tactic != AIR_HIP_LINEAR_AUTO && tactic != AIR_HIP_LINEAR_DECODE && tactic != AIR_HIP_LINEAR_PREFILL) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "unknown linear tactic %d", tactic);
+    }
+    if (tactic == AIR_HIP_LINEAR_PREFILL) {
+        return fail(AIR_HIP_UNSUPPORTED, "the prefill MFMA tactic is not available in this build");
+    }
+    if (rows >= 1u && rows <= kFusedMaxRows) {
+        // One launch: the activations are split in registers.
+        if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
+        DeviceScope scope(ctx->device);
+        if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+        if (rows == 1u) {
+            const GemvShape gshape = plan_decode_gemv(m->planes, ctx->tuning);
+            const hipError_t gerr = launch_decode_gemv(m->planes, x, bias, y, gshape, ctx->stream);
+            if (gerr != hipSuccess) return hip_fail(gerr, "decode_gemv_kernel");
+            ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
+            ctx->decode_rows.fetch_add(1, std::memory_order_relaxed);
+            return AIR_HIP_OK;
+        }
+        const FusedShape shape = plan_decode_fused(m->planes, rows, ctx->tuning);
+        if (shape.k_splits > 1u) {
+            const int rc = ensure_split_buffers(ctx, fused_split_workspace_bytes(shape), shape.groups);
+            if (rc != AIR_HIP_OK) return rc;
+        }
+        const hipError_t err = launch_decode_fused(m->planes, x, bias, y, rows, shape, ctx->split_partials,
+                                                   ctx->split_counters, ctx->stream);
+        if (err != hipSuccess) return hip_fail(err, "decode_fused_kernel");
+        ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
+        ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
+        return AIR_HIP_OK;
+    }
+    int rc = air_hip_activations_load(ctx, x, m->planes.k, rows);
+    if (rc != AIR_HIP_OK) return rc;
+    return air_hip_linear_loaded(ctx, m, y, bias, tactic);
 }
 
 } // extern "C"

@@ -9,11 +9,12 @@
 //   * the weight tile is the B operand of v_mfma_f32_16x16x32_f16: integer
 //     codes are exact in f16 (two v_perm_b32 / v_and_or_b32 per four codes);
 //   * the activations are the A operand, split into f16 hi + lo parts after a
-//     per-row power-of-two scale (split_activations_kernel), so x is carried
-//     to ~22 significant bits and products are exact in the f32 accumulator;
-//   * each 32-element block's MFMA partial is scaled by its f16 block scale
-//     in f32 (Q4_K: (d*sc_j)*P - (dmin*m_j)*sum(x_block)), which is the
-//     reference's per-block dequantisation applied after the dot product.
+//     power-of-two scale per (row, 32-element block), so x is carried to ~21
+//     significant bits and every product is exact in the f32 accumulator;
+//   * each 32-element block's MFMA partial is multiplied by its f16 block
+//     scale and the activation block's inverse scale in f32 (Q4_K:
+//     (d*sc_j)*P - (dmin*m_j)*sum(x_block)), i.e. the reference's per-block
+//     dequantisation applied after the dot product.
 //
 // Relative L2 error against the double-accumulating oracle is ~1e-6.
 #include "air_hip_device.hpp"
@@ -30,55 +31,53 @@ __device__ __forceinline__ std::uint64_t xs_index(std::uint64_t block, std::uint
     return ((block * mtiles + tile) * 2u + part) * 64u + lane;
 }
 
-// One workgroup per activation row (rows >= M are written as zeros).
+// One thread per (row m, 32-block b, eighth g); the four threads of a block
+// are adjacent lanes.  Rows M..mp-1 and blocks past K are written as zeros.
 __global__ void __launch_bounds__(256)
-split_activations_kernel(const float* x, std::uint32_t M, std::uint64_t K, std::uint64_t kp,
-                         std::uint32_t mp, uint4* xs, float* block_sums, float* inv_scale) {
-    const std::uint32_t m = blockIdx.x;
-    const std::uint32_t tid = threadIdx.x;
-    __shared__ float wave_max[4];
-    const float* row = x + static_cast<std::uint64_t>(m) * K;
-    const bool live = m < M;
+split_activations_kernel(const float* __restrict__ x, std::uint32_t M, std::uint64_t K, std::uint64_t nb,
+                         std::uint32_t mp, uint4* __restrict__ xs, float* __restrict__ block_sums,
+                         float* __restrict__ inv_scale) {
+    const std::uint64_t idx = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x;
+    const std::uint64_t total = static_cast<std::uint64_t>(mp) * nb * 4u;
+    const bool in_grid = idx < total;
+    const std::uint32_t g = static_cast<std::uint32_t>(idx & 3u);
+    const std::uint64_t rest = idx >> 2;
+    const std::uint64_t b = in_grid ? rest % nb : 0;
+    const std::uint32_t m = in_grid ? static_cast<std::uint32_t>(rest / nb) : 0;
+    const bool live = in_grid && m < M && (b * 32u) < K;
 
-    float mx = 0.0f;
+    float v[8];
     if (live) {
-        for (std::uint64_t k = tid; k < K; k += 256u) mx = fmaxf(mx, fabsf(row[k]));
+        const float4* src = reinterpret_cast<const float4*>(x + static_cast<std::uint64_t>(m) * K + b * 32u + 8u * g);
+        const float4 a = src[0], c = src[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.0f;
     }
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if ((tid & 63u) == 0u) wave_max[tid >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3]));
-
-    // Scale so that max|x|*s lies in [2^14, 2^15): the f16 hi part cannot
-    // overflow and the lo part keeps the residual.  Powers of two are exact.
-    int shift = 0;
-    if (mx > 0.0f && isfinite(mx)) {
-        shift = 14 - ilogbf(mx);
-        shift = shift < -126 ? -126 : (shift > 126 ? 126 : shift);
+    float amax = 0.0f, sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        amax = fmaxf(amax, fabsf(v[e]));
+        sum += v[e];
     }
-    const float s = ldexpf(1.0f, shift);
-    if (tid == 0) inv_scale[m] = ldexpf(1.0f, -shift);
-
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    float s, inv;
+    block_scale(amax, s, inv);
+    half8v hi, lo;
+    split8(v, s, hi, lo);
+    if (!in_grid) return;
     const std::uint32_t mtiles = mp / 16u;
-    const std::uint32_t tile = m >> 4, r = m & 15u;
-    const std::uint64_t blocks = kp / 32u;
-    for (std::uint64_t b = tid; b < blocks; b += 256u) {
-        float sum = 0.0f;
-        for (std::uint32_t g = 0; g < 4; ++g) {
-            half8v hi, lo;
-            for (std::uint32_t e = 0; e < 8; ++e) {
-                const std::uint64_t k = b * 32u + 8u * g + e;
-                const float v = (live && k < K) ? row[k] * s : 0.0f;
-                const _Float16 h = static_cast<_Float16>(v);
-                hi[e] = h;
-                lo[e] = static_cast<_Float16>(v - static_cast<float>(h));
-                sum += v;
-            }
-            const std::uint32_t lane = r + 16u * g;
-            xs[xs_index(b, mtiles, tile, 0, lane)] = __builtin_bit_cast(uint4, hi);
-            xs[xs_index(b, mtiles, tile, 1, lane)] = __builtin_bit_cast(uint4, lo);
-        }
+    const std::uint32_t lane = (m & 15u) + 16u * g;
+    xs[xs_index(b, mtiles, m >> 4, 0, lane)] = __builtin_bit_cast(uint4, hi);
+    xs[xs_index(b, mtiles, m >> 4, 1, lane)] = __builtin_bit_cast(uint4, lo);
+    if (g == 0u) {
         block_sums[b * mp + m] = sum;
+        inv_scale[b * mp + m] = inv;
     }
 }
 
@@ -102,15 +101,36 @@ __device__ __forceinline__ half8v q8_codes_to_half8(std::uint32_t d0, std::uint3
     return out;
 }
 
-// Accumulate the block partial of one 16-row tile against MT m tiles.
+// Split activations of block kb for MT m tiles starting at mt0, with the
+// inverse scales of the lane's four output rows (D-layout rows 4*(lane/16)+i).
 template <int MT>
-__device__ __forceinline__ void block_mfma(const half8v (&xh)[MT], const half8v (&xl)[MT],
-                                           const half8v& w, float scale, float4v (&acc)[MT]) {
+struct BlockActivations {
+    half8v hi[MT], lo[MT];
+    float4v inv[MT];
+};
+
+template <int MT>
+__device__ __forceinline__ void load_block(BlockActivations<MT>& a, const uint4* __restrict__ xs,
+                                           const float* __restrict__ inv_scale, std::uint64_t kb,
+                                           std::uint32_t mtiles_total, std::uint32_t mt0, std::uint32_t lane) {
+    const std::uint32_t mp = mtiles_total * 16u;
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-        float4v p = mfma16x16x32(xh[t], w, float4v{0.0f, 0.0f, 0.0f, 0.0f});
-        p = mfma16x16x32(xl[t], w, p);
-        acc[t] += scale * p;
+        a.hi[t] = load_half8(xs + xs_index(kb, mtiles_total, mt0 + t, 0, lane));
+        a.lo[t] = load_half8(xs + xs_index(kb, mtiles_total, mt0 + t, 1, lane));
+        a.inv[t] = *reinterpret_cast<const float4v*>(inv_scale + kb * mp + (mt0 + t) * 16u + 4u * (lane >> 4));
+    }
+}
+
+// acc[t] += (scale * inv[t]) * (A_t . W) for one 16-row tile and one block.
+template <int MT>
+__device__ __forceinline__ void block_mfma(const BlockActivations<MT>& a, const half8v& w, float scale,
+                                           float4v (&acc)[MT]) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        float4v p = mfma16x16x32(a.hi[t], w, float4v{0.0f, 0.0f, 0.0f, 0.0f});
+        p = mfma16x16x32(a.lo[t], w, p);
+        acc[t] += (scale * a.inv[t]) * p;
     }
 }
 
@@ -161,18 +181,13 @@ decode_linear_kernel(const void* __restrict__ codes_, const void* __restrict__ s
             }
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                const std::uint64_t kb = 2u * static_cast<std::uint64_t>(kt) + b;
-                half8v xh[MT], xl[MT];
-#pragma unroll
-                for (int t = 0; t < MT; ++t) {
-                    xh[t] = load_half8(xs + xs_index(kb, mtiles_total, mt0 + t, 0, lane));
-                    xl[t] = load_half8(xs + xs_index(kb, mtiles_total, mt0 + t, 1, lane));
-                }
+                BlockActivations<MT> a;
+                load_block<MT>(a, xs, inv_scale, 2u * static_cast<std::uint64_t>(kt) + b, mtiles_total, mt0, lane);
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     const half8v w = b == 0 ? q8_codes_to_half8(c[r].x, c[r].y) : q8_codes_to_half8(c[r].z, c[r].w);
                     const float d = half_bits_to_float((sc[r] >> (16 * b)) & 0xffffu);
-                    block_mfma<MT>(xh, xl, w, d, acc[r]);
+                    block_mfma<MT>(a, w, d, acc[r]);
                 }
             }
         } else if constexpr (FMT == kQ4_0) {
@@ -188,20 +203,15 @@ decode_linear_kernel(const void* __restrict__ codes_, const void* __restrict__ s
             }
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-                const std::uint64_t kb = 4u * static_cast<std::uint64_t>(kt) + b;
-                half8v xh[MT], xl[MT];
-#pragma unroll
-                for (int t = 0; t < MT; ++t) {
-                    xh[t] = load_half8(xs + xs_index(kb, mtiles_total, mt0 + t, 0, lane));
-                    xl[t] = load_half8(xs + xs_index(kb, mtiles_total, mt0 + t, 1, lane));
-                }
+                BlockActivations<MT> a;
+                load_block<MT>(a, xs, inv_scale, 4u * static_cast<std::uint64_t>(kt) + b, mtiles_total, mt0, lane);
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     const std::uint32_t cw = b == 0 ? c[r].x : b == 1 ? c[r].y : b == 2 ? c[r].z : c[r].w;
                     const half8v w = nibble_dword_to_half8<8>(cw);
                     const std::uint32_t sw = b < 2 ? sc[r].x : sc[r].y;
                     const float d = half_bits_to_float((sw >> (16 * (b & 1))) & 0xffffu);
-                    block_mfma<MT>(xh, xl, w, d, acc[r]);
+                    block_mfma<MT>(a, w, d, acc[r]);
                 }
             }
         } else { // Q4_K
@@ -226,15 +236,13 @@ decode_linear_kernel(const void* __restrict__ codes_, const void* __restrict__ s
                     const float dj = d * static_cast<float>(s6);
                     const float mj = dmin * static_cast<float>(m6);
                     const half8v w = nibble_dword_to_half8<0>(cw[j]);
+                    BlockActivations<MT> a;
+                    load_block<MT>(a, xs, inv_scale, kb, mtiles_total, mt0, lane);
+                    block_mfma<MT>(a, w, dj, acc[r]);
 #pragma unroll
                     for (int t = 0; t < MT; ++t) {
-                        const half8v xh = load_half8(xs + xs_index(kb, mtiles_total, mt0 + t, 0, lane));
-                        const half8v xl = load_half8(xs + xs_index(kb, mtiles_total, mt0 + t, 1, lane));
-                        float4v p = mfma16x16x32(xh, w, float4v{0.0f, 0.0f, 0.0f, 0.0f});
-                        p = mfma16x16x32(xl, w, p);
                         const float4v sx = *reinterpret_cast<const float4v*>(
                             block_sums + kb * mp + (mt0 + t) * 16u + 4u * (lane >> 4));
-                        acc[r][t] += dj * p;
                         acc[r][t] -= mj * sx;
                     }
                 }
@@ -273,11 +281,10 @@ decode_linear_kernel(const void* __restrict__ codes_, const void* __restrict__ s
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
             const std::uint32_t m0 = (mt0 + t) * 16u + 4u * (lane >> 4);
-            const float4v is = *reinterpret_cast<const float4v*>(inv_scale + m0);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const std::uint32_t m = m0 + i;
-                if (m < M) y[static_cast<std::uint64_t>(m) * N + n] = acc[r][t][i] * is[i] + bn;
+                if (m < M) y[static_cast<std::uint64_t>(m) * N + n] = acc[r][t][i] + bn;
             }
         }
     }
@@ -331,21 +338,21 @@ std::uint64_t split_workspace_bytes(std::uint64_t kp, std::uint32_t m) {
     m_partition(m, mt, groups);
     const std::uint64_t mp = static_cast<std::uint64_t>(mt) * groups * 16u;
     const std::uint64_t xs = kp * mp * 4u;                // hi + lo f16
-    const std::uint64_t sums = (kp / 32u) * mp * 4u;
-    const std::uint64_t inv = mp * 4u;
-    return ceil_div(xs, 256u) * 256u + ceil_div(sums, 256u) * 256u + ceil_div(inv, 256u) * 256u;
+    const std::uint64_t per_block = (kp / 32u) * mp * 4u; // one f32 per (block, row)
+    return ceil_div(xs, 256u) * 256u + 2u * (ceil_div(per_block, 256u) * 256u);
 }
 
 SplitWorkspace carve_split_workspace(void* base, std::uint64_t kp, std::uint32_t m) {
     std::uint32_t mt = 0, groups = 0;
     m_partition(m, mt, groups);
     const std::uint64_t mp = static_cast<std::uint64_t>(mt) * groups * 16u;
+    const std::uint64_t per_block = ceil_div((kp / 32u) * mp * 4u, 256u) * 256u;
     auto* p = static_cast<std::uint8_t*>(base);
     SplitWorkspace ws;
     ws.xs = p;
     p += ceil_div(kp * mp * 4u, 256u) * 256u;
     ws.block_sums = reinterpret_cast<float*>(p);
-    p += ceil_div((kp / 32u) * mp * 4u, 256u) * 256u;
+    p += per_block;
     ws.inv_scale = reinterpret_cast<float*>(p);
     return ws;
 }
@@ -355,23 +362,30 @@ hipError_t launch_split_activations(const float* x, std::uint32_t m, std::uint64
     std::uint32_t mt = 0, groups = 0;
     m_partition(m, mt, groups);
     const std::uint32_t mp = mt * groups * 16u;
-    split_activations_kernel<<<mp, 256, 0, stream>>>(x, m, k, kp, mp, static_cast<uint4*>(ws.xs),
-                                                     ws.block_sums, ws.inv_scale);
+    const std::uint64_t nb = kp / 32u;
+    const std::uint64_t threads = static_cast<std::uint64_t>(mp) * nb * 4u;
+    split_activations_kernel<<<static_cast<unsigned>(ceil_div(threads, 256u)), 256, 0, stream>>>(
+        x, m, k, nb, mp, static_cast<uint4*>(ws.xs), ws.block_sums, ws.inv_scale);
     return hipGetLastError();
 }
 
 hipError_t launch_decode_linear(const TilePlanes& p, const SplitWorkspace& ws, const float* bias, float* y,
-                                std::uint32_t m, hipStream_t stream) {
+                                std::uint32_t m, const DecodeTuning& tuning, hipStream_t stream) {
     std::uint32_t MT = 0, groups = 0;
     m_partition(m, MT, groups);
     // Enough workgroups to cover 256 CUs several times; split K across the
     // waves of a workgroup when the row tiles alone cannot fill the chip.
     std::uint32_t R = 4;
     while (R > 1u && ceil_div(p.nt, R) * groups < 1024u) R >>= 1;
+    if (tuning.rows_per_wave == 1u || tuning.rows_per_wave == 2u || tuning.rows_per_wave == 4u) R = tuning.rows_per_wave;
+    const std::uint32_t w_cap = static_cast<std::uint32_t>(max_waves(static_cast<int>(R), static_cast<int>(MT)));
     std::uint32_t W = 1;
     const std::uint64_t wgs = ceil_div(p.nt, R) * groups;
-    const std::uint32_t w_cap = static_cast<std::uint32_t>(max_waves(static_cast<int>(R), static_cast<int>(MT)));
     while (W < w_cap && wgs * W < 8192u && p.kt >= 4u * W && (2u * W - 1u) * R * MT <= 64u) W <<= 1;
+    if (tuning.waves_per_group != 0u) {
+        W = tuning.waves_per_group;
+        if (W > w_cap || (W - 1u) * R * MT > 63u) return hipErrorInvalidConfiguration;
+    }
     switch (p.type) {
     case kQ8_0: return launch_fmt<kQ8_0>(p, ws, bias, y, m, R, MT, groups, W, stream);
     case kQ4_0: return launch_fmt<kQ4_0>(p, ws, bias, y, m, R, MT, groups, W, stream);

@@ -105,3 +105,84 @@ def synthetic_weights(type_id: int, k: int, n: int, seed: int, sigma: float = 0.
     rng = np.random.default_rng(seed)
     w = rng.standard_normal((n, k), dtype=np.float32) * np.float32(sigma)
     return quantize(type_id, w)
+
+
+# ---- device-side synthesis (torch) for benchmark-sized sweeps -------------
+# The same quantization rules evaluated with torch on the GPU, so that
+# multi-GB synthetic models are produced in seconds.  Used for benchmark
+# inputs only; the parity tests use the host quantizers above.
+
+def _torch_round_half_away(t):
+    import torch
+
+    return torch.sign(t) * torch.floor(torch.abs(t) + 0.5)
+
+
+def synthetic_weights_device(type_id: int, k: int, n: int, seed: int, device, sigma: float = 0.02,
+                             row_chunk: int = 8192):
+    """Canonical bytes (torch uint8 [n, row_bytes] on `device`) of w ~ N(0, sigma)."""
+    import torch
+
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    be, bb = BLOCK[type_id]
+    out = torch.empty((n, (k // be) * bb), dtype=torch.uint8, device=device)
+    for r0 in range(0, n, row_chunk):
+        r1 = min(n, r0 + row_chunk)
+        w = torch.randn((r1 - r0, k), generator=gen, device=device, dtype=torch.float32) * sigma
+        out[r0:r1] = _quantize_torch(type_id, w)
+    return out
+
+
+def _quantize_torch(type_id: int, w):
+    import torch
+
+    n, k = w.shape
+    if type_id == 8:
+        b = w.reshape(n, k // 32, 32)
+        d = b.abs().amax(dim=2) / 127.0
+        inv = torch.where(d > 0, 1.0 / torch.where(d > 0, d, torch.ones_like(d)), torch.zeros_like(d))
+        q = torch.clamp(_torch_round_half_away(b * inv[..., None]), -127, 127).to(torch.int8)
+        blk = torch.empty((n, k // 32, 34), dtype=torch.uint8, device=w.device)
+        blk[..., 0:2] = d.to(torch.float16).view(torch.uint8).reshape(n, k // 32, 2)
+        blk[..., 2:] = q.view(torch.uint8)
+        return blk.reshape(n, -1)
+    if type_id == 2:
+        b = w.reshape(n, k // 32, 32)
+        idx = b.abs().argmax(dim=2, keepdim=True)
+        vmax = torch.gather(b, 2, idx)[..., 0]
+        d = vmax / -8.0
+        inv = torch.where(d != 0, 1.0 / torch.where(d != 0, d, torch.ones_like(d)), torch.zeros_like(d))
+        q = torch.clamp(torch.floor(b * inv[..., None] + 8.5), 0, 15).to(torch.uint8)
+        blk = torch.empty((n, k // 32, 18), dtype=torch.uint8, device=w.device)
+        blk[..., 0:2] = d.to(torch.float16).view(torch.uint8).reshape(n, k // 32, 2)
+        blk[..., 2:] = q[..., :16] | (q[..., 16:] << 4)
+        return blk.reshape(n, -1)
+    if type_id == 12:
+        nb = k // 256
+        b = w.reshape(n, nb, 8, 32)
+        lo = torch.clamp(b.amin(dim=3), max=0.0)
+        hi = b.amax(dim=3)
+        scale = (hi - lo) / 15.0
+        d = (scale.amax(dim=2) / 63.0).to(torch.float16)
+        dmin = ((-lo).amax(dim=2) / 63.0).to(torch.float16)
+        d32 = d.float()[..., None]
+        dm32 = dmin.float()[..., None]
+        one = torch.ones_like(d32)
+        sc = torch.clamp(_torch_round_half_away(torch.where(d32 > 0, scale / torch.where(d32 > 0, d32, one), 0 * d32)), 0, 63)
+        mn = torch.clamp(_torch_round_half_away(torch.where(dm32 > 0, -lo / torch.where(dm32 > 0, dm32, one), 0 * dm32)), 0, 63)
+        step = (d32 * sc)[..., None]
+        offs = (dm32 * mn)[..., None]
+        q = torch.where(step > 0, (b + offs) / torch.where(step > 0, step, torch.ones_like(step)), torch.zeros_like(b))
+        q = torch.clamp(_torch_round_half_away(q), 0, 15).to(torch.uint8)
+        sc8 = sc.to(torch.uint8)
+        mn8 = mn.to(torch.uint8)
+        blk = torch.zeros((n, nb, 144), dtype=torch.uint8, device=w.device)
+        blk[..., 0:2] = d.view(torch.uint8).reshape(n, nb, 2)
+        blk[..., 2:4] = dmin.view(torch.uint8).reshape(n, nb, 2)
+        blk[..., 4:8] = (sc8[..., 0:4] & 63) | ((sc8[..., 4:8] >> 4) << 6)
+        blk[..., 8:12] = (mn8[..., 0:4] & 63) | ((mn8[..., 4:8] >> 4) << 6)
+        blk[..., 12:16] = (sc8[..., 4:8] & 0x0F) | ((mn8[..., 4:8] & 0x0F) << 4)
+        blk[..., 16:] = (q[:, :, 0::2, :] | (q[:, :, 1::2, :] << 4)).reshape(n, nb, 128)
+        return blk.reshape(n, -1)
+    raise ValueError(f"unsupported type {type_id}")

@@ -1,0 +1,268 @@
+#!/usr/bin/env python3
+"""Benchmark: Qwen2-7B-shaped Q8_0 decode linears on one MI355X.
+
+Workload: every linear of a 28-layer Qwen2-7B
+(q 3584x3584 +bias, k/v 512x3584 +bias, o 3584x3584, gate/up 18944x3584,
+down 3584x18944) plus lm_head 152064x3584, random-init weights w ~ N(0, 0.02)
+quantized to GGUF Q8_0, activations ~ N(0, 1), at M decode rows.  One "step"
+is one pass of all 197 linears over one batch of M rows, i.e. the linear
+work of one decode step; weights (7.5 GB) stream from HBM every step, well
+past the 256 MB Infinity Cache.
+
+The engine runs q|k|v and gate|up as one fused matrix each (they share their
+input), so a step is 4 loads + 4 linears per layer + lm_head.  Throughput is
+reported on the algorithmic bytes of the reference's 197 separate linears:
+W_bytes + 4*M*K + 4*M*N (+ 4*N bias).
+
+Output: one JSON line (metric = GB/s at M=1, plus tok/s at each M, the
+roofline of the dominant kernel and the reference CPU baseline).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HIDDEN, KV, FFN, VOCAB, LAYERS = 3584, 512, 18944, 152064, 28
+HBM_PEAK_GBS = 8000.0
+Q8_BLOCK, Q8_BYTES = 32, 34
+
+
+def w_bytes(k: int, n: int) -> int:
+    return n * (k // Q8_BLOCK) * Q8_BYTES
+
+
+def step_algorithmic_bytes(m: int, layers: int) -> int:
+    """BASELINE.md section 2 formula over the reference's separate linears."""
+    per_layer = [(HIDDEN, HIDDEN, True), (HIDDEN, KV, True), (HIDDEN, KV, True), (HIDDEN, HIDDEN, False),
+                 (HIDDEN, FFN, False), (HIDDEN, FFN, False), (FFN, HIDDEN, False)]
+    total = 0
+    for k, n, bias in per_layer:
+        total += w_bytes(k, n) + 4 * m * k + 4 * m * n + (4 * n if bias else 0)
+    total *= layers
+    total += w_bytes(HIDDEN, VOCAB) + 4 * m * HIDDEN + 4 * m * VOCAB
+    return total
+
+
+def gate_up_launch_bytes(m: int) -> int:
+    """Algorithmic bytes of one fused gate|up launch (gate + up linears)."""
+    return 2 * (w_bytes(HIDDEN, FFN) + 4 * m * FFN) + 4 * m * HIDDEN
+
+
+def cpu_baseline(canon_host, k: int, n: int, target_s: float):
+    """Times the reference matvec (oracle/_ref: AIR's own tensor_reader.cpp,
+    single-threaded) on a bounded sample of rows of one 7B gate matrix."""
+    import numpy as np
+
+    import oracle
+
+    kind = "reference" if oracle.ref_available() else "port"
+    run = (lambda data, rows, x: oracle.ref_matvec(8, data, k, rows, x)) if kind == "reference" else \
+          (lambda data, rows, x: oracle.linear(8, data, k, rows, x))
+    row_bytes = w_bytes(k, 1)
+    x = np.random.default_rng(7).standard_normal((1, k), dtype=np.float32)
+    rows = 256
+    t0 = time.perf_counter()
+    run(canon_host[:rows].reshape(-1), rows, x)
+    dt = time.perf_counter() - t0
+    rows = int(min(n, max(256, rows * target_s / max(dt, 1e-6))))
+    sample = np.ascontiguousarray(canon_host[:rows])
+    t0 = time.perf_counter()
+    run(sample.reshape(-1), rows, x)
+    dt = time.perf_counter() - t0
+    algo = rows * row_bytes + 4 * k + 4 * rows
+    return {
+        "value": round(algo / dt / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": kind,
+        "sample": f"M=1 matvec over {rows} rows of a 7B gate matrix (Q8_0 {rows}x{k}), {dt:.1f} s",
+        "seconds": round(dt, 2),
+    }
+
+
+def read_traffic(m: int):
+    path = os.path.join(ROOT, "profiles", "traffic_gate_up_q8_0.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+        return data.get(str(m))
+    except (OSError, ValueError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--m", default="1,8,32", help="decode rows per step, comma separated; the first is the headline")
+    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget (0 = skip)")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the engine is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from air_amd import capi, quant
+
+    ms = [int(v) for v in args.m.split(",") if v]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    ctx = capi.Context(0, stream.cuda_stream)
+
+    t_build = time.perf_counter()
+    layers = []
+    cpu_sample = None
+    seed = 1000
+    for layer in range(args.layers):
+        mats = {}
+        for name, k, n in (("qkv", HIDDEN, HIDDEN + 2 * KV), ("o", HIDDEN, HIDDEN),
+                           ("gate_up", HIDDEN, 2 * FFN), ("down", FFN, HIDDEN)):
+            canon = quant.synthetic_weights_device(capi.TYPE_Q8_0, k, n, seed, dev)
+            seed += 1
+            mats[name] = capi.Matrix(ctx, capi.TYPE_Q8_0, k, n, canon, canon.numel(), on_device=True)
+            if cpu_sample is None and name == "gate_up":
+                cpu_sample = canon[:FFN].cpu().numpy()
+            del canon
+        layers.append(mats)
+    canon = quant.synthetic_weights_device(capi.TYPE_Q8_0, HIDDEN, VOCAB, seed, dev)
+    lm_head = capi.Matrix(ctx, capi.TYPE_Q8_0, HIDDEN, VOCAB, canon, canon.numel(), on_device=True)
+    del canon
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    build_s = time.perf_counter() - t_build
+
+    mmax = max(ms)
+    ctx.reserve(FFN, mmax)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(42)
+    x_h = torch.randn((mmax, HIDDEN), generator=gen, device=dev)
+    x_attn = torch.randn((mmax, HIDDEN), generator=gen, device=dev)
+    x_ffn = torch.randn((mmax, HIDDEN), generator=gen, device=dev)
+    x_act = torch.randn((mmax, FFN), generator=gen, device=dev)
+    bias_qkv = torch.randn((HIDDEN + 2 * KV,), generator=gen, device=dev) * 0.02
+    y_qkv = torch.empty((mmax, HIDDEN + 2 * KV), device=dev)
+    y_o = torch.empty((mmax, HIDDEN), device=dev)
+    y_gu = torch.empty((mmax, 2 * FFN), device=dev)
+    y_down = torch.empty((mmax, HIDDEN), device=dev)
+    logits = torch.empty((mmax, VOCAB), device=dev)
+
+    def run_step(m, gu_events=None):
+        for i, mats in enumerate(layers):
+            mats["qkv"].linear(x_h, y_qkv, m, bias=bias_qkv)
+            mats["o"].linear(x_attn, y_o, m)
+            if gu_events is not None:
+                gu_events[i][0].record(stream)
+            mats["gate_up"].linear(x_ffn, y_gu, m)
+            if gu_events is not None:
+                gu_events[i][1].record(stream)
+            mats["down"].linear(x_act, y_down, m)
+        lm_head.linear(x_h, logits, m)
+
+    results = {}
+    roofline = None
+    for m in ms:
+        for _ in range(args.warmup):
+            run_step(m)
+        torch.cuda.synchronize()
+        ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(args.layers)] for _ in range(args.steps)]
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record(stream)
+        for s in range(args.steps):
+            run_step(m, ev[s])
+        end.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms_step = start.elapsed_time(end) / args.steps
+        algo = step_algorithmic_bytes(m, args.layers)
+        gu_ms = [a.elapsed_time(b) for row in ev for (a, b) in row]
+        gu_avg_ms = sum(gu_ms) / len(gu_ms)
+        gu_gbs = gate_up_launch_bytes(m) / (gu_avg_ms * 1e-3) / 1e9
+        results[m] = {
+            "ms_per_step": round(ms_step, 4),
+            "gbps": round(algo / (ms_step * 1e-3) / 1e9, 1),
+            "pct_of_hbm_peak": round(100.0 * algo / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+            "tok_s": round(m / (ms_step * 1e-3), 1),
+            "algorithmic_bytes_per_step": algo,
+            "gate_up_avg_us": round(gu_avg_ms * 1e3, 2),
+            "gate_up_gbps": round(gu_gbs, 1),
+            "wall_s": round(wall, 3),
+        }
+        if roofline is None:
+            roofline = {
+                "kernel": ("decode_gemv_kernel<Q8_0>" if m == 1 else
+                           "decode_fused_kernel<Q8_0>" if m <= 16 else
+                           "split_activations + decode_linear_kernel<Q8_0>") + " (fused gate|up 37888x3584)",
+                "bound": "hbm",
+                "achieved": round(gu_gbs, 1),
+                "peak": HBM_PEAK_GBS,
+                "unit": "GB/s",
+                "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                "traffic": read_traffic(m),
+                "m": m,
+                "bytes_per_launch": gate_up_launch_bytes(m),
+                "avg_launch_us": round(gu_avg_ms * 1e3, 2),
+            }
+        print(f"# M={m}: {results[m]}", file=sys.stderr, flush=True)
+
+    for mats in layers:
+        for mat in mats.values():
+            mat.release()
+    lm_head.release()
+
+    cpu = None
+    if args.cpu_seconds > 0 and cpu_sample is not None:
+        cpu = cpu_baseline(cpu_sample, HIDDEN, FFN, args.cpu_seconds)
+        print(f"# cpu baseline: {cpu}", file=sys.stderr, flush=True)
+
+    head = ms[0]
+    line = {
+        "metric": "Q8_0 linear HBM GB/s (% of peak) + Qwen2-7B-shape decode tok/s at M=1/32",
+        "value": results[head]["gbps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": results[head]["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q8_0 weights x f32 activations (f16 hi+lo MFMA, f32 accumulate)",
+        "data": "synthetic: w ~ N(0,0.02) quantized to Q8_0 on device, x ~ N(0,1)",
+        "config": {
+            "workload": "configs[2]: Qwen2-7B-shaped Q8_0 decode linears, 28 layers + lm_head",
+            "layers": args.layers,
+            "m_rows": ms,
+            "pct_of_hbm_peak": results[head]["pct_of_hbm_peak"],
+            "tok_s_by_m": {str(m): results[m]["tok_s"] for m in ms},
+            "gbps_by_m": {str(m): results[m]["gbps"] for m in ms},
+            "ms_per_step_by_m": {str(m): results[m]["ms_per_step"] for m in ms},
+            "model_build_s": round(build_s, 1),
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    ctx.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

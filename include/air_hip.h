@@ -128,6 +128,14 @@ int air_hip_context_set_stream(air_hip_context* ctx, void* stream);
  * space allocates. */
 int air_hip_context_reserve(air_hip_context* ctx, uint64_t max_k, uint32_t max_m);
 int air_hip_context_stats(const air_hip_context* ctx, air_hip_stats* out);
+/* Overrides the decode linear's launch shape for this context (autotuning):
+ * rows_per_wave = 16-row tiles per wavefront (1, 2 or 4), waves_per_group =
+ * wavefronts splitting K inside one workgroup (1..16), k_splits =
+ * workgroups splitting K (1..64, single-launch path only).  0 keeps the
+ * automatic choice; wave counts beyond what a compiled variant supports are
+ * clamped to its maximum. */
+int air_hip_context_set_tuning(air_hip_context* ctx, uint32_t rows_per_wave, uint32_t waves_per_group,
+                               uint32_t k_splits);
 
 /* ---- matrices ----------------------------------------------------------- */
 
@@ -160,7 +168,20 @@ int air_hip_dequantize_canonical(air_hip_context* ctx, int type, const void* can
 
 /* ---- the linear --------------------------------------------------------- */
 
-/* y[m][n] = sum_k w[n][k] * x[m][k] (+ bias[n]) for m < M.
+/* Stage 1: loads activations x [m][k] (device f32, row-major) into the
+ * context workspace as the engine's split f16 hi/lo operand tiles with a
+ * per-row power-of-two scale.  One load serves every following
+ * air_hip_linear_loaded call with the same input width k (q/k/v and
+ * gate/up share their input).  Asynchronous on the context's stream. */
+int air_hip_activations_load(air_hip_context* ctx, const float* x, uint64_t k, uint32_t m);
+
+/* Stage 2: y[m][n] = sum_k w[n][k] * x[m][k] (+ bias[n]) over the activations
+ * last loaded into ctx; the matrix input width must equal the loaded k.
+ * Asynchronous on the context's stream. */
+int air_hip_linear_loaded(air_hip_context* ctx, const air_hip_matrix* matrix,
+                          float* y, const float* bias, int tactic);
+
+/* Both stages in one call: y[m][n] = sum_k w[n][k] * x[m][k] (+ bias[n]).
  *   x    device f32 [M][k], row-major
  *   y    device f32 [M][n], row-major (must not alias x)
  *   bias device f32 [n] or NULL (fused; add_optional_tensor,

@@ -132,3 +132,33 @@ def test_linear_rejects_bad_arguments(torch_cuda, hip_ctx):
         mat.linear(x, y, 1, tactic=99)
     assert e.value.status_name == "invalid_argument"
     mat.release()
+
+
+@pytest.mark.parametrize("type_id,k,n", [(capi.TYPE_Q8_0, 18944, 512), (capi.TYPE_Q4_0, 3584, 256),
+                                         (capi.TYPE_Q4_K, 3584, 96)])
+def test_linear_k_split_shapes_agree(torch_cuda, hip_ctx, type_id, k, n):
+    """Every launch shape (row tiles per wave, waves per group, workgroups
+    splitting K) gives the oracle's result, and repeated K-split launches
+    re-arm their arrival counters (same bits on every repeat)."""
+    torch = torch_cuda
+    canon = helpers.weights(type_id, k, n, seed=k + n)
+    mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    try:
+        for m in (1, 3, 16):
+            x = helpers.activations(m, k, seed=m + 17)
+            want = oracle.linear(type_id, canon, k, n, x)
+            xd = _dev(torch, x)
+            widest = (1, 4, 16) if type_id == capi.TYPE_Q4_K else (1, 16, 16)
+            for rows, waves, splits in [(1, 1, 1), (1, 4, 8), (2, 2, 3), (4, 1, 2), widest]:
+                hip_ctx.set_tuning(rows, waves, splits)
+                outs = []
+                for _ in range(3):
+                    y = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+                    mat.linear(xd, y, m)
+                    torch.cuda.synchronize()
+                    outs.append(y.cpu().numpy())
+                assert helpers.rel_l2(outs[0], want) <= DECODE_TOL, (m, rows, waves, splits)
+                assert all(np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)) for o in outs[1:])
+    finally:
+        hip_ctx.set_tuning(0, 0, 0)
+        mat.release()
