@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark: Qwen2-7B-shaped Q8_0 decode linears on one MI355X.
 
-Workload (BASELINE.json configs[2]): every linear of a 28-layer Qwen2-7B
+Workload: every linear of a 28-layer Qwen2-7B
 (q 3584x3584 +bias, k/v 512x3584 +bias, o 3584x3584, gate/up 18944x3584,
 down 3584x18944) plus lm_head 152064x3584, random-init weights w ~ N(0, 0.02)
 quantized to GGUF Q8_0, activations ~ N(0, 1), at M decode rows.  One "step"
@@ -39,7 +39,8 @@ def w_bytes(k: int, n: int) -> int:
 
 
 def step_algorithmic_bytes(m: int, layers: int) -> int:
-    """BASELINE.md section 2 formula over the reference's separate linears."""
+    """Algorithmic bytes of one step: sum over the reference's separate linears of
+    W_bytes + 4*M*K + 4*M*N (+ 4*N for a bias)."""
     per_layer = [(HIDDEN, HIDDEN, True), (HIDDEN, KV, True), (HIDDEN, KV, True), (HIDDEN, HIDDEN, False),
                  (HIDDEN, FFN, False), (HIDDEN, FFN, False), (FFN, HIDDEN, False)]
     total = 0
@@ -56,35 +57,64 @@ def gate_up_launch_bytes(m: int) -> int:
 
 
 def cpu_baseline(canon_host, k: int, n: int, target_s: float):
-    """Times the reference matvec (oracle/_ref: AIR's own tensor_reader.cpp,
-    single-threaded) on a bounded sample of rows of one 7B gate matrix."""
+    """Times the reference matvec on the host, single-threaded like the
+    reference (src/reference/tensor_reader.cpp:369-394): AIR's own code from
+    oracle/_ref when it was built, else the plain-C restatement.  The sample
+    is one fused 7B gate|up matrix (144 MB of Q8_0, larger than any CPU
+    cache) at M=1, repeated for about `target_s` seconds."""
     import numpy as np
 
     import oracle
 
     kind = "reference" if oracle.ref_available() else "port"
-    run = (lambda data, rows, x: oracle.ref_matvec(8, data, k, rows, x)) if kind == "reference" else \
-          (lambda data, rows, x: oracle.linear(8, data, k, rows, x))
-    row_bytes = w_bytes(k, 1)
     x = np.random.default_rng(7).standard_normal((1, k), dtype=np.float32)
-    rows = 256
+    if kind == "reference":
+        mat = oracle.RefMatrix(8, canon_host, k, n)
+        run = lambda: mat.matvec(x)  # noqa: E731
+    else:
+        run = lambda: oracle.linear(8, canon_host, k, n, x)  # noqa: E731
+    reps = 0
     t0 = time.perf_counter()
-    run(canon_host[:rows].reshape(-1), rows, x)
-    dt = time.perf_counter() - t0
-    rows = int(min(n, max(256, rows * target_s / max(dt, 1e-6))))
-    sample = np.ascontiguousarray(canon_host[:rows])
-    t0 = time.perf_counter()
-    run(sample.reshape(-1), rows, x)
-    dt = time.perf_counter() - t0
-    algo = rows * row_bytes + 4 * k + 4 * rows
+    while True:
+        run()
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= target_s:
+            break
+    algo = reps * (w_bytes(k, n) + 4 * k + 4 * n)
     return {
         "value": round(algo / dt / 1e9, 4),
         "unit": "GB/s",
         "cores": 1,
         "kind": kind,
-        "sample": f"M=1 matvec over {rows} rows of a 7B gate matrix (Q8_0 {rows}x{k}), {dt:.1f} s",
-        "seconds": round(dt, 2),
+        "sample": f"{reps} x M=1 matvec over one fused 7B gate|up matrix (Q8_0 {n}x{k}, "
+                  f"{w_bytes(k, n) / 1e6:.0f} MB), {dt:.1f} s",
+        "tok_s_equivalent": round(algo / dt / step_algorithmic_bytes(1, LAYERS), 4),
     }
+
+
+def trace_summary(csv_path: str) -> str:
+    """Markdown table of the engine's kernels in a `rocprofv3 --kernel-trace
+    --output-format csv` trace, one row per (kernel, grid, workgroup) so the
+    launches of each Qwen2 matrix shape are separated."""
+    import csv
+    import statistics
+
+    groups = {}
+    with open(csv_path, newline="") as f:
+        for row in csv.DictReader(f):
+            name = row["Kernel_Name"]
+            if "air_hip::" not in name:
+                continue
+            short = name.replace("air_hip::(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+            wg = int(row["Workgroup_Size_X"])
+            key = (short, int(row["Grid_Size_X"]) // wg, int(row.get("Grid_Size_Y") or 1), wg)
+            groups.setdefault(key, []).append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1000.0)
+    lines = ["| kernel | workgroups | grid y | threads/WG | launches | avg us | min us | max us |",
+             "|---|---|---|---|---|---|---|---|"]
+    for (name, wgs, gy, wg), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| `{name}` | {wgs} | {gy} | {wg} | {len(d)} | {statistics.mean(d):.2f} | {min(d):.2f} | {max(d):.2f} |")
+    return "\n".join(lines)
 
 
 def read_traffic(m: int):
@@ -105,11 +135,18 @@ def main() -> int:
     ap.add_argument("--m", default="1,8,32", help="decode rows per step, comma separated; the first is the headline")
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget (0 = skip)")
+    ap.add_argument("--graph", type=int, default=1, help="replay each step as a captured HIP graph (1) or launch eagerly (0)")
+    ap.add_argument("--trace-summary", default=None, metavar="CSV",
+                    help="summarise a rocprofv3 kernel-trace CSV instead of benchmarking")
     args = ap.parse_args()
+
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary))
+        return 0
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the engine is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(the engine runs on one GPU; its linears shard over output rows)", file=sys.stderr)
         return 2
 
     import numpy as np
@@ -135,7 +172,7 @@ def main() -> int:
             seed += 1
             mats[name] = capi.Matrix(ctx, capi.TYPE_Q8_0, k, n, canon, canon.numel(), on_device=True)
             if cpu_sample is None and name == "gate_up":
-                cpu_sample = canon[:FFN].cpu().numpy()
+                cpu_sample = canon.cpu().numpy()
             del canon
         layers.append(mats)
     canon = quant.synthetic_weights_device(capi.TYPE_Q8_0, HIDDEN, VOCAB, seed, dev)
@@ -160,15 +197,11 @@ def main() -> int:
     y_down = torch.empty((mmax, HIDDEN), device=dev)
     logits = torch.empty((mmax, VOCAB), device=dev)
 
-    def run_step(m, gu_events=None):
-        for i, mats in enumerate(layers):
+    def run_step(m):
+        for mats in layers:
             mats["qkv"].linear(x_h, y_qkv, m, bias=bias_qkv)
             mats["o"].linear(x_attn, y_o, m)
-            if gu_events is not None:
-                gu_events[i][0].record(stream)
             mats["gate_up"].linear(x_ffn, y_gu, m)
-            if gu_events is not None:
-                gu_events[i][1].record(stream)
             mats["down"].linear(x_act, y_down, m)
         lm_head.linear(x_h, logits, m)
 
@@ -178,22 +211,60 @@ def main() -> int:
         for _ in range(args.warmup):
             run_step(m)
         torch.cuda.synchronize()
-        ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(args.layers)] for _ in range(args.steps)]
+        graph = None
+        if args.graph:
+            # One step captured as a HIP graph: 113 kernel launches replayed
+            # with one host call (the context launches on the capture stream).
+            capture_stream = torch.cuda.Stream(dev)
+            ctx.set_stream(capture_stream.cuda_stream)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=capture_stream):
+                run_step(m)
+            ctx.set_stream(stream.cuda_stream)
+            for _ in range(args.warmup):
+                graph.replay()
+            torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         start.record(stream)
         for s in range(args.steps):
-            run_step(m, ev[s])
+            if graph is not None:
+                graph.replay()
+            else:
+                run_step(m)
         end.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         ms_step = start.elapsed_time(end) / args.steps
+        # The dominant kernel (the fused gate|up linear of every layer, 28
+        # distinct matrices streamed from HBM) timed with HIP events on the
+        # stream it runs on: its launches back to back, replayed as a graph
+        # like the step, so the average includes no host launch latency.
+        gate_up_only = lambda: [mats["gate_up"].linear(x_ffn, y_gu, m) for mats in layers]
+        gu_graph = None
+        if args.graph:
+            capture_stream = torch.cuda.Stream(dev)
+            ctx.set_stream(capture_stream.cuda_stream)
+            gu_graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gu_graph, stream=capture_stream):
+                gate_up_only()
+            ctx.set_stream(stream.cuda_stream)
+        g0 = torch.cuda.Event(enable_timing=True)
+        g1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        g0.record(stream)
+        for s in range(args.steps):
+            if gu_graph is not None:
+                gu_graph.replay()
+            else:
+                gate_up_only()
+        g1.record(stream)
+        torch.cuda.synchronize()
+        gu_ms = [g0.elapsed_time(g1) / (args.steps * args.layers)]
         algo = step_algorithmic_bytes(m, args.layers)
-        gu_ms = [a.elapsed_time(b) for row in ev for (a, b) in row]
-        gu_avg_ms = sum(gu_ms) / len(gu_ms)
+        gu_avg_ms = gu_ms[0]
         gu_gbs = gate_up_launch_bytes(m) / (gu_avg_ms * 1e-3) / 1e9
         results[m] = {
             "ms_per_step": round(ms_step, 4),
@@ -204,6 +275,7 @@ def main() -> int:
             "gate_up_avg_us": round(gu_avg_ms * 1e3, 2),
             "gate_up_gbps": round(gu_gbs, 1),
             "wall_s": round(wall, 3),
+            "graph": bool(graph is not None),
         }
         if roofline is None:
             roofline = {
@@ -229,7 +301,7 @@ def main() -> int:
 
     cpu = None
     if args.cpu_seconds > 0 and cpu_sample is not None:
-        cpu = cpu_baseline(cpu_sample, HIDDEN, FFN, args.cpu_seconds)
+        cpu = cpu_baseline(cpu_sample, HIDDEN, 2 * FFN, args.cpu_seconds)
         print(f"# cpu baseline: {cpu}", file=sys.stderr, flush=True)
 
     head = ms[0]

@@ -62,6 +62,12 @@ def _load_ref() -> ctypes.CDLL:
         lib.airref_decode.argtypes = [ctypes.c_int, _P, _U64, _U64, _P]
         lib.airref_matvec.restype = ctypes.c_int
         lib.airref_matvec.argtypes = [ctypes.c_int, _P, _U64, _U64, _U64, ctypes.c_uint32, _P, _P]
+        lib.airref_model_create.restype = ctypes.c_int
+        lib.airref_model_create.argtypes = [ctypes.c_int, _P, _U64, _U64, _U64, ctypes.POINTER(_P)]
+        lib.airref_model_matvec.restype = ctypes.c_int
+        lib.airref_model_matvec.argtypes = [_P, _P, _P]
+        lib.airref_model_destroy.restype = None
+        lib.airref_model_destroy.argtypes = [_P]
         _ref = lib
     return _ref
 
@@ -108,6 +114,39 @@ def ref_decode(type_id: int, data: np.ndarray, elements: int) -> np.ndarray:
     if rc != 0:
         raise ValueError(f"airref_decode failed with status {rc}")
     return out
+
+
+class RefMatrix:
+    """One matrix held by AIR's reference ModelDefinition, for timing loops
+    that should measure only ReferenceTensorReader::matvec."""
+
+    def __init__(self, type_id: int, data: np.ndarray, k: int, n: int):
+        self._data = np.ascontiguousarray(data, dtype=np.uint8).reshape(-1)
+        self.k, self.n = k, n
+        handle = _P()
+        rc = _load_ref().airref_model_create(type_id, _addr(self._data), self._data.nbytes, k, n, ctypes.byref(handle))
+        if rc != 0:
+            raise ValueError(f"airref_model_create failed with status {rc}")
+        self._handle = handle
+
+    def matvec(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(self.k)
+        y = np.empty(self.n, dtype=np.float32)
+        rc = _load_ref().airref_model_matvec(self._handle, _addr(x), _addr(y))
+        if rc != 0:
+            raise ValueError(f"airref_model_matvec failed with status {rc}")
+        return y
+
+    def close(self) -> None:
+        if self._handle:
+            _load_ref().airref_model_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def ref_matvec(type_id: int, data: np.ndarray, k: int, n: int, x: np.ndarray) -> np.ndarray:

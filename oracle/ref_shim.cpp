@@ -120,4 +120,35 @@ int airref_matvec(int ggml_type, const std::uint8_t* bytes, std::uint64_t nbytes
     return 0;
 }
 
+// A persistent one-matrix model, so that timing loops measure only
+// ReferenceTensorReader::matvec and not the model assembly.
+struct airref_model {
+    std::shared_ptr<const air::ModelDefinition> model;
+    std::uint64_t k{0}, n{0};
+};
+
+int airref_model_create(int ggml_type, const std::uint8_t* bytes, std::uint64_t nbytes,
+                        std::uint64_t K, std::uint64_t N, airref_model** out) {
+    air::DataType type{};
+    if (!out) return 1;
+    *out = nullptr;
+    if (!data_type_for(ggml_type, type)) return 6;
+    int rc = 0;
+    auto model = one_tensor_model("w", type, ggml_type, {K, N}, bytes, nbytes, rc);
+    if (!model) return rc;
+    *out = new airref_model{std::move(model), K, N};
+    return 0;
+}
+
+int airref_model_matvec(const airref_model* m, const float* x, float* y) {
+    if (!m) return 1;
+    air::ReferenceTensorReader reader(m->model);
+    auto out = reader.matvec("w", std::span<const float>(x, m->k));
+    if (!out) return code_of(out.status());
+    std::memcpy(y, out.value().data(), m->n * sizeof(float));
+    return 0;
+}
+
+void airref_model_destroy(airref_model* m) { delete m; }
+
 } // extern "C"
