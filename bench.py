@@ -117,12 +117,86 @@ def trace_summary(csv_path: str) -> str:
     return "\n".join(lines)
 
 
+def traffic_probe(ms) -> int:
+    """Launch sequence for the HBM-traffic counter passes: one plain copy of a
+    known size (the calibration kernel), then the fused gate|up linear of four
+    distinct layers at each M.  Run under `rocprofv3 --pmc FETCH_SIZE` and
+    then `--pmc WRITE_SIZE`; `--counter-summary` turns the two CSVs into
+    bytes per launch."""
+    import torch
+
+    from air_amd import capi, quant
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    ctx = capi.Context(0, stream.cuda_stream)
+    src = torch.ones(COPY_PROBE_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    mats = []
+    for seed in range(4):
+        canon = quant.synthetic_weights_device(capi.TYPE_Q8_0, HIDDEN, 2 * FFN, 500 + seed, dev)
+        mats.append(capi.Matrix(ctx, capi.TYPE_Q8_0, HIDDEN, 2 * FFN, canon, canon.numel(), on_device=True))
+        del canon
+    ctx.reserve(HIDDEN, max(ms))
+    x = torch.randn((max(ms), HIDDEN), device=dev)
+    y = torch.empty((max(ms), 2 * FFN), device=dev)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    for m in ms:
+        for mat in mats:
+            mat.linear(x, y, m)
+        torch.cuda.synchronize()
+    for mat in mats:
+        mat.release()
+    ctx.close()
+    return 0
+
+
+COPY_PROBE_BYTES = 256 * 1024 * 1024
+
+
+def counter_summary(fetch_csv: str, write_csv: str, ms) -> dict:
+    """Bytes per launch of the probe's gate|up linears from two rocprofv3
+    counter CSVs, each counter scaled by its reading on the copy kernel
+    (which reads and writes COPY_PROBE_BYTES exactly)."""
+    import csv
+
+    def per_dispatch(path, counter):
+        rows = []
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") != counter:
+                    continue
+                rows.append((int(row["Dispatch_Id"]), row["Kernel_Name"], float(row["Counter_Value"])))
+        rows.sort()
+        return rows
+
+    out = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        rows = per_dispatch(path, counter)
+        copy = [v for _, name, v in rows if "copyBuffer" in name]
+        gemv = [v for _, name, v in rows if "air_hip::" in name and "decode_" in name]
+        factor = COPY_PROBE_BYTES / (copy[-1] * 1024.0)     # counter is in KiB
+        per_m = len(gemv) // len(ms)
+        for i, m in enumerate(ms):
+            vals = gemv[i * per_m:(i + 1) * per_m]
+            out.setdefault(str(m), {})[counter] = sum(vals) / len(vals) * 1024.0 * factor
+        out.setdefault("_factors", {})[counter] = factor
+    for m in ms:
+        d = out[str(m)]
+        d["bytes"] = d["FETCH_SIZE"] + d["WRITE_SIZE"]
+        d["algorithmic"] = gate_up_launch_bytes(m)
+    return out
+
+
 def read_traffic(m: int):
     path = os.path.join(ROOT, "profiles", "traffic_gate_up_q8_0.json")
     try:
         with open(path) as f:
             data = json.load(f)
-        return data.get(str(m))
+        entry = data.get(str(m))
+        return None if entry is None else int(entry["bytes"])
     except (OSError, ValueError):
         return None
 
@@ -138,10 +212,20 @@ def main() -> int:
     ap.add_argument("--graph", type=int, default=1, help="replay each step as a captured HIP graph (1) or launch eagerly (0)")
     ap.add_argument("--trace-summary", default=None, metavar="CSV",
                     help="summarise a rocprofv3 kernel-trace CSV instead of benchmarking")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run the launch sequence for the FETCH_SIZE / WRITE_SIZE counter passes")
+    ap.add_argument("--counter-summary", nargs=2, default=None, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="bytes per launch from the two counter passes of --traffic-probe")
     args = ap.parse_args()
 
     if args.trace_summary:
         print(trace_summary(args.trace_summary))
+        return 0
+    if args.traffic_probe:
+        return traffic_probe([int(v) for v in args.m.split(",") if v])
+    if args.counter_summary:
+        fetch_csv, write_csv = args.counter_summary
+        print(json.dumps(counter_summary(fetch_csv, write_csv, [int(v) for v in args.m.split(",") if v]), indent=1))
         return 0
 
     if args.gpus != 1:
