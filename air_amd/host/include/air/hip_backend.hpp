@@ -1,0 +1,134 @@
+// hip_backend.hpp -- the HIP prepared model: Qwen2 linears resident on one GPU.
+//
+// HipPreparedModel is the MI355X counterpart of CudaPreparedModel
+// (src/runtime/backend.cpp:268-574): it owns the device residency of every
+// quantized projection, advertises the HIP linear tactics per operation scope
+// and answers the capacity queries CapacityScheduler asks.  Weights become
+// resident once, repacked into the wavefront tile layout by
+// air_hip_matrix_prepare; q|k|v and gate|up are concatenated along N (their
+// GGUF rows are contiguous, so the fusion is a byte append) when the parts
+// share a format, and their f32 biases are concatenated the same way.
+//
+// The linear engine is the whole of this backend's device work: sequences
+// (KV pages, attention, sampling) are not part of it, so create_sequence
+// and restore_sequence return `unsupported` after validating the plan.
+#pragma once
+
+#include "air/backend.hpp"
+
+#include <memory>
+
+struct air_hip_context;
+struct air_hip_matrix;
+
+namespace air {
+
+enum class LinearRole {
+    attn_qkv = 0,   // fused q|k|v, N = q_width + 2 kv_width
+    attn_q,
+    attn_k,
+    attn_v,
+    attn_output,
+    ffn_gate_up,    // fused gate|up, N = 2 ffn
+    ffn_gate,
+    ffn_up,
+    ffn_down,
+    output,         // lm_head (output.weight, or token_embd.weight when tied)
+};
+
+[[nodiscard]] const char* to_string(LinearRole role) noexcept;
+
+struct HipLinearInfo {
+    std::uint32_t format_type{0};
+    std::uint64_t k{0};
+    std::uint64_t n{0};
+    bool has_bias{false};
+    std::uint64_t resident_bytes{0};
+};
+
+struct HipPrepareOptions {
+    int device{0};
+    void* stream{nullptr};              // hipStream_t the engine launches on
+    std::uint32_t max_decode_rows{64};  // workspace reserved for decode widths
+    bool fuse{true};                    // concatenate q|k|v and gate|up when formats agree
+};
+
+class HipPreparedModel final : public runtime_detail::PreparedModel {
+public:
+    ~HipPreparedModel() override;
+    HipPreparedModel(const HipPreparedModel&) = delete;
+    HipPreparedModel& operator=(const HipPreparedModel&) = delete;
+
+    [[nodiscard]] static Result<std::unique_ptr<HipPreparedModel>> create(std::shared_ptr<const ModelDefinition> model,
+                                                                          const HipPrepareOptions& options);
+
+    // PreparedModel
+    [[nodiscard]] BackendKind backend() const noexcept override { return BackendKind::hip; }
+    [[nodiscard]] const BackendCapabilities& capabilities() const noexcept override { return capabilities_; }
+    [[nodiscard]] const ModelDefinition& model() const noexcept override { return *model_; }
+    [[nodiscard]] Result<std::unique_ptr<runtime_detail::SequenceState>> create_sequence(
+        const ExecutionPlan& plan) override;
+    [[nodiscard]] Result<std::unique_ptr<runtime_detail::SequenceState>> restore_sequence(
+        const ExecutionPlan& plan, const runtime_detail::SequenceCheckpoint& checkpoint) override;
+    [[nodiscard]] std::uint64_t resident_device_bytes() const noexcept override;
+    [[nodiscard]] std::uint64_t estimate_sequence_device_bytes(const ExecutionPlan& plan,
+                                                               std::uint64_t max_tokens) const noexcept override;
+    [[nodiscard]] std::optional<std::uint64_t> sequence_capacity_bytes() const override;
+    [[nodiscard]] std::optional<std::uint64_t> free_device_bytes() const override;
+    [[nodiscard]] std::uint64_t kv_pool_allocated_bytes() const noexcept override { return 0U; }
+    [[nodiscard]] std::uint64_t kv_pool_free_bytes() const noexcept override { return 0U; }
+
+    // Linear engine.  x: device f32 [rows x K], y: device f32 [rows x N], both
+    // row-major; the role's bias (if any) is fused.  Asynchronous on the
+    // engine's stream.  The tactic must be one this backend advertises for
+    // some scope (hip-decode, hip-prefill).
+    [[nodiscard]] Status linear(std::uint32_t layer, LinearRole role, const float* x, float* y,
+                                std::uint32_t rows, QuantizedLinearExecutionKind tactic) const;
+    [[nodiscard]] Result<HipLinearInfo> linear_info(std::uint32_t layer, LinearRole role) const;
+    [[nodiscard]] bool fused_qkv() const noexcept { return fused_qkv_; }
+    [[nodiscard]] bool fused_gate_up() const noexcept { return fused_gate_up_; }
+    [[nodiscard]] Status set_stream(void* stream);
+    [[nodiscard]] Status synchronize() const;
+    [[nodiscard]] air_hip_context* context() const noexcept { return ctx_; }
+    [[nodiscard]] int device() const noexcept { return device_; }
+
+private:
+    struct Linear {
+        air_hip_matrix* matrix{nullptr};
+        float* bias{nullptr};  // device f32 [N] or null
+        HipLinearInfo info{};
+    };
+    struct Layer {
+        Linear qkv, q, k, v, o, gate_up, gate, up, down;
+    };
+
+    HipPreparedModel(std::shared_ptr<const ModelDefinition> model, int device);
+    [[nodiscard]] const Linear* find(std::uint32_t layer, LinearRole role) const noexcept;
+    [[nodiscard]] Status make_linear(std::span<const TensorDescriptor* const> parts,
+                                     std::span<const TensorDescriptor* const> biases, Linear& out);
+    void release(Linear& linear) noexcept;
+
+    std::shared_ptr<const ModelDefinition> model_;
+    int device_{0};
+    air_hip_context* ctx_{nullptr};
+    BackendCapabilities capabilities_{};
+    std::vector<Layer> layers_;
+    Linear output_{};
+    bool fused_qkv_{false};
+    bool fused_gate_up_{false};
+    std::uint64_t bias_bytes_{0};
+};
+
+// Paged fp32 K and V of every layer for max_tokens plus the two page tables,
+// saturating at UINT64_MAX (backend.cpp:511-538); 0 when either count is 0.
+[[nodiscard]] std::uint64_t estimate_paged_fp32_sequence_bytes(const ModelConfig& config, std::uint32_t page_tokens,
+                                                               std::uint64_t max_tokens) noexcept;
+
+// The AIR factory spelling (backend.hpp:147-150).
+[[nodiscard]] Result<std::unique_ptr<runtime_detail::PreparedModel>> prepare_hip_model(
+    std::shared_ptr<const ModelDefinition> model, int device_ordinal);
+
+// Maps an air_hip_status code and the thread's last ABI message to a Status.
+[[nodiscard]] Status hip_status(int rc);
+
+} // namespace air

@@ -1,0 +1,741 @@
+// host_tests.cpp -- tests of the C++ executor contract and the HIP prepared model.
+//
+//   host_tests cpu   plan vocabulary and validation, capacity and micro-batch
+//                    scheduling (the cases of AIR's tests/scheduler_tests.cpp:77-348
+//                    and tests/core_tests.cpp:389-481, restated), model and
+//                    Qwen2 contract checks, f16 conversion and the quantizers.
+//   host_tests gpu   HipPreparedModel on device 0: every resident projection
+//                    of synthetic Q8_0 / Q4_0 / Q4_K Qwen2 models against the
+//                    CPU oracle (rel-L2 <= 1e-4), fused and unfused residency,
+//                    tied embeddings, capacity answers and plan checks.
+// Exit status 0 when every check passes.
+#include "air/execution.hpp"
+#include "air/hip_backend.hpp"
+#include "air/model.hpp"
+#include "air/scheduler.hpp"
+#include "air/synthetic.hpp"
+
+#include "air_oracle.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstring>
+#include <iostream>
+#include <string>
+#include <vector>
+
+namespace {
+
+int failures = 0;
+int checks = 0;
+
+void check(bool condition, const std::string& message) {
+    ++checks;
+    if (!condition) {
+        ++failures;
+        std::cerr << "FAIL: " << message << '\n';
+    }
+}
+
+using air::runtime_detail::CapacityScheduler;
+using air::runtime_detail::MicrobatchScheduler;
+using air::runtime_detail::SchedulableSequence;
+using air::runtime_detail::WorkPhase;
+
+// A prepared model that answers only the capacity questions.
+class FakePreparedModel final : public air::runtime_detail::PreparedModel {
+public:
+    FakePreparedModel(std::uint64_t bytes_per_token, std::optional<std::uint64_t> capacity,
+                      std::uint64_t preparation_bytes = 0U)
+        : bytes_per_token_(bytes_per_token), capacity_(capacity), preparation_bytes_(preparation_bytes) {
+        caps_.backend = air::BackendKind::hip;
+        caps_.prefill_execution = air::PrefillExecutionKind::native_batch;
+        caps_.kv_storage = air::KvStorageKind::paged;
+        caps_.max_prefill_batch_width = 512U;
+        caps_.max_decode_batch_width = 64U;
+    }
+    air::BackendKind backend() const noexcept override { return air::BackendKind::hip; }
+    const air::BackendCapabilities& capabilities() const noexcept override { return caps_; }
+    const air::ModelDefinition& model() const noexcept override { return model_; }
+    air::Result<std::unique_ptr<air::runtime_detail::SequenceState>> create_sequence(const air::ExecutionPlan&) override {
+        return air::Status::unsupported("fake backend has no sequence");
+    }
+    air::Result<std::unique_ptr<air::runtime_detail::SequenceState>> restore_sequence(
+        const air::ExecutionPlan&, const air::runtime_detail::SequenceCheckpoint&) override {
+        return air::Status::unsupported("fake backend has no sequence");
+    }
+    std::uint64_t estimate_plan_preparation_device_bytes(const air::ExecutionPlan&) const noexcept override {
+        return preparation_bytes_;
+    }
+    std::uint64_t resident_device_bytes() const noexcept override { return 0U; }
+    std::uint64_t estimate_sequence_device_bytes(const air::ExecutionPlan&, std::uint64_t t) const noexcept override {
+        return t * bytes_per_token_;
+    }
+    std::optional<std::uint64_t> sequence_capacity_bytes() const override { return capacity_; }
+    std::optional<std::uint64_t> free_device_bytes() const override { return capacity_; }
+    std::uint64_t kv_pool_allocated_bytes() const noexcept override { return 0U; }
+    std::uint64_t kv_pool_free_bytes() const noexcept override { return 0U; }
+
+private:
+    std::uint64_t bytes_per_token_;
+    std::optional<std::uint64_t> capacity_;
+    std::uint64_t preparation_bytes_;
+    air::BackendCapabilities caps_{};
+    air::ModelDefinition model_{};
+};
+
+air::ExecutionPlan paged_plan() {
+    air::ExecutionPlan plan;
+    plan.backend = air::BackendKind::hip;
+    plan.kv.page_tokens = 16U;
+    return plan;
+}
+
+// ---- scheduler (scheduler_tests.cpp:77-348) -------------------------------
+
+void test_capacity_reservations() {
+    FakePreparedModel backend(100U, 1000U);
+    const auto plan = paged_plan();
+    CapacityScheduler scheduler(4U);
+    auto d = scheduler.evaluate(0U, 0U, backend, plan, 4U);
+    check(d.admit && d.reservation_bytes == 400U, "first request fits with the backend's estimate");
+    d = scheduler.evaluate(1U, 400U, backend, plan, 6U);
+    check(d.admit && d.reservation_bytes == 600U, "a reservation that exactly fills capacity fits");
+    d = scheduler.evaluate(1U, 401U, backend, plan, 6U);
+    check(!d.admit && d.reason == "device-capacity", "future reservations prevent overcommit");
+    d = scheduler.evaluate(0U, 0U, backend, plan, 11U);
+    check(!d.admit && d.reason == "device-capacity" && d.reservation_bytes == 1100U,
+          "a single request above capacity fails before allocation");
+    d = scheduler.evaluate(4U, 0U, backend, plan, 1U);
+    check(!d.admit && d.reason == "max-active-requests", "the active-request ceiling is an independent guard");
+}
+
+void test_plan_preparation_capacity() {
+    FakePreparedModel backend(100U, 1000U);
+    const auto plan = paged_plan();
+    CapacityScheduler scheduler(4U);
+    auto d = scheduler.evaluate(0U, 0U, backend, plan, 4U, 500U);
+    check(d.admit, "artifact plus reservation within capacity admits");
+    d = scheduler.evaluate(0U, 0U, backend, plan, 6U, 500U);
+    check(!d.admit && d.reason == "device-capacity", "prospective artifacts reduce sequence capacity");
+    d = scheduler.evaluate(0U, 0U, backend, plan, 1U, 1100U);
+    check(!d.admit && d.reason == "device-capacity-plan-artifact", "an artifact above free memory is rejected");
+}
+
+void test_transition_capacity() {
+    const auto plan = paged_plan();
+    CapacityScheduler scheduler(4U);
+    FakePreparedModel no_prepare(100U, 1000U);
+    auto d = scheduler.evaluate_transition(no_prepare, plan, 900U);
+    check(d.admit && d.temporary_device_bytes == 900U, "temporary transition state within free memory admits");
+    d = scheduler.evaluate_transition(no_prepare, plan, 1001U);
+    check(!d.admit && d.reason == "device-capacity-transition-temporary", "temporary state beyond free memory");
+    FakePreparedModel with_prepare(100U, 1000U, 300U);
+    d = scheduler.evaluate_transition(with_prepare, plan, 700U);
+    check(d.admit && d.plan_preparation_bytes == 300U && d.temporary_device_bytes == 700U,
+          "artifact plus migration bytes that exactly fit admit");
+    d = scheduler.evaluate_transition(with_prepare, plan, 701U);
+    check(!d.admit && d.reason == "device-capacity-transition-plan-artifact",
+          "transition accounts for artifacts plus migration bytes");
+    d = scheduler.evaluate_transition(with_prepare, plan, std::numeric_limits<std::uint64_t>::max());
+    check(!d.admit && d.reason == "device-capacity-transition-overflow", "transition byte sum overflow is refused");
+}
+
+void test_unbounded_capacity() {
+    FakePreparedModel backend(1000000U, std::nullopt);
+    air::ExecutionPlan plan;
+    CapacityScheduler scheduler(2U);
+    check(scheduler.evaluate(0U, 0U, backend, plan, 1000000U).admit,
+          "a backend without device capacity is bounded by request count only");
+}
+
+void test_decode_first_order() {
+    const std::vector<SchedulableSequence> c{
+        {0U, WorkPhase::prefill}, {1U, WorkPhase::decode}, {2U, WorkPhase::prefill}, {3U, WorkPhase::decode}};
+    MicrobatchScheduler s;
+    const auto o = s.order(c);
+    check(o.size() == 4U, "order preserves candidates");
+    if (o.size() == 4U) {
+        check(o[0].slot == 1U && o[1].slot == 3U, "decode work runs before prefill");
+        check(o[2].slot == 0U && o[3].slot == 2U, "first pass keeps phase-local input order");
+    }
+}
+
+void test_round_robin_order() {
+    const std::vector<SchedulableSequence> c{{0U, WorkPhase::decode}, {1U, WorkPhase::decode}, {2U, WorkPhase::decode}};
+    MicrobatchScheduler s;
+    std::vector<std::size_t> first;
+    for (int i = 0; i < 6; ++i) {
+        const auto o = s.order(c);
+        if (!o.empty()) first.push_back(o.front().slot);
+    }
+    check(first == std::vector<std::size_t>({0U, 1U, 2U, 0U, 1U, 2U}), "decode sequences round-robin");
+}
+
+void test_batch_decode_priority() {
+    const std::vector<SchedulableSequence> c{{0U, WorkPhase::prefill, 4U},
+                                             {1U, WorkPhase::decode, 1U},
+                                             {2U, WorkPhase::prefill, 4U},
+                                             {3U, WorkPhase::decode, 1U}};
+    MicrobatchScheduler s;
+    const auto b = s.schedule(c, 5U);
+    check(b.token_count == 5U, "the batch stays within the token budget");
+    check(b.decode_tokens == 2U && b.prefill_tokens == 3U, "decode consumes budget first, prefill the rest");
+    check(b.slices.size() == 3U && b.slices[0].slot == 1U && b.slices[1].slot == 3U &&
+              b.slices[2].phase == WorkPhase::prefill,
+          "the batch keeps decode-first order");
+}
+
+void test_batch_spans_prefill() {
+    const std::vector<SchedulableSequence> c{
+        {0U, WorkPhase::prefill, 4U}, {1U, WorkPhase::prefill, 4U}, {2U, WorkPhase::prefill, 4U}};
+    MicrobatchScheduler s;
+    const auto b = s.schedule(c, 9U);
+    check(b.prefill_sequences == 3U && b.prefill_tokens == 9U && b.token_count == 9U,
+          "one batch spans prefill slices of several sequences");
+    check(b.slices.size() == 3U && b.slices[0].token_count == 4U && b.slices[1].token_count == 4U &&
+              b.slices[2].token_count == 1U,
+          "per-sequence limits hold while filling the budget");
+}
+
+void test_batch_zero_limit() {
+    const std::vector<SchedulableSequence> c{{0U, WorkPhase::prefill, 0U}, {1U, WorkPhase::prefill, 3U}};
+    MicrobatchScheduler s;
+    const auto b = s.schedule(c, 3U);
+    check(b.slices.size() == 1U && b.slices.front().slot == 1U && b.token_count == 3U,
+          "zero-limit candidates consume no budget");
+}
+
+void test_batch_round_robin() {
+    const std::vector<SchedulableSequence> c{
+        {0U, WorkPhase::prefill, 1U}, {1U, WorkPhase::prefill, 1U}, {2U, WorkPhase::prefill, 1U}};
+    MicrobatchScheduler s;
+    std::vector<std::size_t> first;
+    for (int i = 0; i < 6; ++i) {
+        const auto b = s.schedule(c, 1U);
+        if (!b.slices.empty()) first.push_back(b.slices.front().slot);
+    }
+    check(first == std::vector<std::size_t>({0U, 1U, 2U, 0U, 1U, 2U}), "batches round-robin under tiny budgets");
+    check(s.schedule(c, 0U).slices.empty() && s.schedule({}, 4U).slices.empty(), "empty budget or input: no work");
+}
+
+void test_regime_identity_and_admission() {
+    air::ExecutionPlan a = paged_plan();
+    a.strategy_id = "qualified-a";
+    a.scheduling.prefill_quantum_tokens = 32U;
+    a.linear = {air::QuantizedLinearExecutionKind::hip_prefill, air::QuantizedLinearExecutionKind::hip_decode,
+                air::QuantizedLinearExecutionKind::hip_decode};
+    a.attention.prefill = air::AttentionExecutionKind::online_softmax;
+    auto b = a;
+    b.strategy_id = "same-physical-plan";
+    using air::runtime_detail::execution_regime_key;
+    check(execution_regime_key(a) == execution_regime_key(b), "strategy label does not split a regime");
+    b.linear.decode_block = air::QuantizedLinearExecutionKind::baseline;
+    check(!(execution_regime_key(a) == execution_regime_key(b)), "a tactic change changes the regime");
+
+    using air::runtime_detail::RegimeAdmissionAction;
+    using air::runtime_detail::classify_regime_admission;
+    const auto ka = execution_regime_key(a);
+    const auto kb = execution_regime_key(b);
+    check(classify_regime_admission(ka, ka, false) == RegimeAdmissionAction::compatible, "same regime is compatible");
+    check(classify_regime_admission(ka, kb, false) == RegimeAdmissionAction::converge_to_fallback,
+          "first incompatible arrival converges to fallback");
+    check(classify_regime_admission(kb, ka, true) == RegimeAdmissionAction::use_pinned_fallback,
+          "a pinned fallback stays pinned");
+    check(classify_regime_admission(std::nullopt, ka, false) == RegimeAdmissionAction::converge_to_fallback,
+          "no active regime converges");
+}
+
+void test_homogeneous_shapes() {
+    using air::runtime_detail::RegimeRequestShape;
+    const std::vector<RegimeRequestShape> active(6U, {160U, 32U});
+    using air::runtime_detail::homogeneous_regime_shape_accepts;
+    check(homogeneous_regime_shape_accepts(active, {160U, 32U}), "same shape stays eligible");
+    check(!homogeneous_regime_shape_accepts(active, {54U, 32U}), "different prompt is incompatible");
+    check(!homogeneous_regime_shape_accepts(active, {160U, 64U}), "different horizon is incompatible");
+    auto mixed = active;
+    mixed.back().prompt_tokens = 54U;
+    check(!homogeneous_regime_shape_accepts(mixed, {160U, 32U}), "a heterogeneous group never accepts");
+    check(!homogeneous_regime_shape_accepts({}, {160U, 32U}), "an empty group never accepts");
+    const std::vector<RegimeRequestShape> same(8U, {160U, 32U});
+    const auto p = air::runtime_detail::homogeneous_regime_profile(same);
+    check(p && p->prompt_tokens == 160U && p->max_output_tokens == 32U && p->active_sequences == 8U,
+          "a homogeneous group yields its exact profile");
+    auto het = same;
+    het[0].prompt_tokens = 1042U;
+    check(!air::runtime_detail::homogeneous_regime_profile(het), "heterogeneous shapes yield no profile");
+}
+
+void test_decode_launch_grouping() {
+    using air::runtime_detail::ScheduledSlice;
+    std::vector<ScheduledSlice> slices;
+    for (std::size_t i = 0; i < 70; ++i) slices.push_back({i, WorkPhase::decode, 1U});
+    slices.push_back({70U, WorkPhase::prefill, 8U});
+    auto plan = paged_plan();
+    plan.linear.decode_block = air::QuantizedLinearExecutionKind::hip_decode;
+    const auto g = air::runtime_detail::group_decode_launches(slices, plan, 64U);
+    check(g.size() == 3U && g[0].size() == 64U && g[1].size() == 6U && g[2].size() == 1U && g[2][0] == 70U,
+          "decode rows group up to the width, prefill stays alone");
+    plan.linear.decode_block = air::QuantizedLinearExecutionKind::baseline;
+    check(air::runtime_detail::group_decode_launches(slices, plan, 64U).size() == 71U,
+          "baseline decode tactics run one row per launch");
+    plan.linear.decode_block = air::QuantizedLinearExecutionKind::hip_decode;
+    check(air::runtime_detail::group_decode_launches(slices, plan, 1U).size() == 71U, "width 1 never batches");
+    const std::vector<ScheduledSlice> one{{0U, WorkPhase::decode, 1U}, {1U, WorkPhase::prefill, 4U},
+                                          {2U, WorkPhase::decode, 1U}};
+    check(air::runtime_detail::group_decode_launches(one, plan, 64U).size() == 3U, "runs of one are single launches");
+}
+
+// ---- plans (core_tests.cpp:389-481) ----------------------------------------
+
+void test_tactic_parsing() {
+    using K = air::QuantizedLinearExecutionKind;
+    auto p = [](const char* s) { return air::quantized_linear_execution_kind_from_string(s); };
+    check(p("baseline") && p("baseline").value() == K::baseline, "parser accepts baseline");
+    check(p("reuse4") && p("reuse4").value() == K::batch_reuse4, "parser accepts reuse4 alias");
+    check(p("batch-reuse8") && p("batch-reuse8").value() == K::batch_reuse8, "parser accepts batch-reuse8");
+    check(!p("q5q8-dp4a-hybrid"), "the rejected hybrid tactic is not parseable");
+    check(p("dense-f32-cublas") && p("dense-f32-cublas").value() == K::dense_f32_cublas, "parser accepts dense");
+    check(!p("magic-fast"), "parser rejects unknown tactics");
+    check(p("hip-decode") && p("hip-decode").value() == K::hip_decode, "parser accepts hip-decode");
+    check(p("hip-prefill") && p("hip-prefill").value() == K::hip_prefill, "parser accepts hip-prefill");
+    for (auto k : {K::baseline, K::batch_reuse4, K::batch_reuse8, K::dense_f32_cublas, K::hip_decode, K::hip_prefill}) {
+        const auto back = p(air::to_string(k));
+        check(back && back.value() == k, std::string("to_string round-trips ") + air::to_string(k));
+    }
+    auto a = [](const char* s) { return air::attention_execution_kind_from_string(s); };
+    check(a("baseline") && a("online-softmax") && a("online") && !a("magic-attention"), "attention parsing");
+    check(a("online").value() == air::AttentionExecutionKind::online_softmax, "online alias");
+    auto b = air::backend_kind_from_string("hip");
+    check(b && b.value() == air::BackendKind::hip && !air::backend_kind_from_string("rocm"), "backend parsing");
+}
+
+void test_plan_validation() {
+    air::BackendCapabilities ref;
+    ref.backend = air::BackendKind::reference;
+    ref.kv_storage = air::KvStorageKind::paged;
+    ref.sequence_checkpointing = true;
+    ref.exact_prefix_reuse = true;
+    air::ExecutionPlan rp;
+    rp.backend = air::BackendKind::reference;
+    rp.strategy_id = "reference-test";
+    rp.scheduling.prefill_quantum_tokens = 8;
+    check(!air::validate_execution_plan(rp, ref), "paged backend rejects a plan without page size");
+    rp.kv.page_tokens = 16;
+    check(air::validate_execution_plan(rp, ref).is_ok(), "paged backend accepts explicit page size");
+
+    air::BackendCapabilities hip;
+    hip.backend = air::BackendKind::hip;
+    hip.prefill_execution = air::PrefillExecutionKind::native_batch;
+    hip.kv_storage = air::KvStorageKind::paged;
+    hip.max_prefill_batch_width = 512;
+    hip.max_decode_batch_width = 64;
+    air::ExecutionPlan hp;
+    hp.backend = air::BackendKind::hip;
+    hp.strategy_id = "hip-test";
+    hp.scheduling.prefill_quantum_tokens = 32;
+    check(!air::validate_execution_plan(hp, hip), "paged HIP backend rejects a plan without page size");
+    hp.kv.page_tokens = 16;
+    check(air::validate_execution_plan(hp, hip).is_ok(), "truthful geometry validates");
+    hp.linear.prefill_block = air::QuantizedLinearExecutionKind::hip_prefill;
+    const auto s = air::validate_execution_plan(hp, hip);
+    check(!s && s.code() == air::ErrorCode::unsupported, "an unadvertised tactic is unsupported");
+    hip.prefill_block_quantized_linear.push_back(air::QuantizedLinearExecutionKind::hip_prefill);
+    check(air::validate_execution_plan(hp, hip).is_ok(), "an advertised tactic validates");
+    hp.linear.decode_output = air::QuantizedLinearExecutionKind::hip_prefill;
+    check(!air::validate_execution_plan(hp, hip), "a block-only tactic is refused for the vocabulary projection");
+    hp.linear.decode_output = air::QuantizedLinearExecutionKind::baseline;
+    hp.attention.prefill = air::AttentionExecutionKind::online_softmax;
+    check(!air::validate_execution_plan(hp, hip), "an unadvertised attention tactic is refused");
+    hip.prefill_attention.push_back(air::AttentionExecutionKind::online_softmax);
+    check(air::validate_execution_plan(hp, hip).is_ok(), "an advertised attention tactic validates");
+
+    auto bad = hp;
+    bad.backend = air::BackendKind::cuda;
+    check(air::validate_execution_plan(bad, hip).code() == air::ErrorCode::invalid_argument, "backend mismatch");
+    bad = hp;
+    bad.strategy_id.clear();
+    check(air::validate_execution_plan(bad, hip).code() == air::ErrorCode::invalid_argument, "empty strategy id");
+    bad = hp;
+    bad.scheduling.prefill_quantum_tokens = 0;
+    check(air::validate_execution_plan(bad, hip).code() == air::ErrorCode::invalid_argument, "zero quantum");
+    auto contiguous = hip;
+    contiguous.kv_storage = air::KvStorageKind::contiguous;
+    check(air::validate_execution_plan(hp, contiguous).code() == air::ErrorCode::invalid_argument,
+          "contiguous backend refuses a page size");
+    auto zero = hip;
+    zero.max_decode_batch_width = 0;
+    check(air::validate_execution_plan(hp, zero).code() == air::ErrorCode::invalid_state, "zero widths");
+    auto reuse = hip;
+    reuse.exact_prefix_reuse = true;
+    check(air::validate_execution_plan(hp, reuse).code() == air::ErrorCode::invalid_state,
+          "prefix reuse requires checkpointing");
+}
+
+// ---- model, contract, conversions, quantizers ------------------------------
+
+air::ModelConfig small_config(std::uint32_t embedding = 256, std::uint32_t ffn = 512) {
+    return air::qwen2_config(2, embedding, ffn, 4, 2, 1000, 256);
+}
+
+void test_model_and_contract() {
+    air::SyntheticQwen2Spec spec;
+    spec.config = small_config();
+    auto m = air::make_synthetic_qwen2(spec);
+    check(m.is_ok(), "synthetic Qwen2 builds and validates");
+    if (!m) {
+        std::cerr << m.status().message() << '\n';
+        return;
+    }
+    const auto& model = *m.value();
+    const auto* q = model.find_tensor("blk.1.attn_q.weight");
+    check(q && q->shape.dimensions == std::vector<std::uint64_t>({256, 256}) && q->byte_size == 256 * 8 * 34,
+          "q weight shape and Q8_0 size");
+    const auto* k = model.find_tensor("blk.0.attn_k.weight");
+    check(k && k->shape.dimensions == std::vector<std::uint64_t>({256, 128}), "k width = kv heads x head dim");
+    check(model.find_tensor("blk.0.attn_v.bias") != nullptr, "v bias present");
+    check(model.find_tensor("output.bias") == nullptr, "output bias absent by default");
+
+    auto config = spec.config;
+    config.rope_scaling_type = "yarn";
+    air::ModelDefinition yarn(config, model.tensors(), model.storage());
+    check(air::validate_qwen2_structure(yarn).code() == air::ErrorCode::unsupported, "RoPE scaling is unsupported");
+    config = spec.config;
+    config.attention_sliding_window = 4096;
+    air::ModelDefinition window(config, model.tensors(), model.storage());
+    check(air::validate_qwen2_structure(window).code() == air::ErrorCode::unsupported, "sliding window unsupported");
+    config = spec.config;
+    config.architecture = "llama";
+    air::ModelDefinition llama(config, model.tensors(), model.storage());
+    check(air::validate_qwen2_structure(llama).code() == air::ErrorCode::unsupported, "qwen2 only");
+
+    auto tensors = model.tensors();
+    for (auto& t : tensors) {
+        if (t.name == "blk.1.ffn_down.weight") t.shape.dimensions = {512, 255};
+    }
+    air::ModelDefinition bad_shape(spec.config, tensors, model.storage());
+    const auto s = air::validate_qwen2_structure(bad_shape);
+    check(s.code() == air::ErrorCode::data_error && s.message() == "shape mismatch for tensor: blk.1.ffn_down.weight",
+          "shape mismatch names the tensor");
+    tensors = model.tensors();
+    tensors.erase(tensors.begin() + 5);
+    air::ModelDefinition missing(spec.config, tensors, model.storage());
+    check(air::validate_qwen2_structure(missing).code() == air::ErrorCode::data_error, "missing tensor is data_error");
+    tensors = model.tensors();
+    tensors[3].byte_size -= 34;
+    air::ModelDefinition short_bytes(spec.config, tensors, model.storage());
+    check(short_bytes.validate().code() == air::ErrorCode::data_error, "byte size must match the format");
+    tensors = model.tensors();
+    tensors.back().byte_offset = model.storage()->bytes().size();
+    air::ModelDefinition outside(spec.config, tensors, model.storage());
+    check(outside.validate().code() == air::ErrorCode::data_error, "storage range is checked");
+    tensors = model.tensors();
+    tensors[1].name = tensors[0].name;
+    air::ModelDefinition dup(spec.config, tensors, model.storage());
+    check(dup.validate().code() == air::ErrorCode::invalid_argument, "duplicate names are refused");
+
+    const std::uint64_t dims[] = {896, 4864};
+    auto bytes = air::exact_tensor_bytes(8, dims);
+    check(bytes && bytes.value() == 4630528U, "0.5B up-proj Q8_0 is 4,630,528 bytes");
+    const std::uint64_t q4k_bad[] = {896, 4864};
+    check(!air::exact_tensor_bytes(12, q4k_bad), "Q4_K needs K a multiple of 256");
+    const std::uint64_t q7[] = {3584, 18944};
+    check(air::exact_tensor_bytes(12, q7).value() == 38191104U && air::exact_tensor_bytes(2, q7).value() == 38191104U,
+          "7B gate in Q4_K and Q4_0 is 38,191,104 bytes");
+}
+
+void test_f16_conversion() {
+    bool exact = true;
+    for (std::uint32_t b = 0; b < 65536; ++b) {
+        const auto bits = static_cast<std::uint16_t>(b);
+        const float f = air::f16_bits_to_f32(bits);
+        if (f != oracle_f16_to_f32(bits) && !(std::isnan(f) && std::isnan(oracle_f16_to_f32(bits)))) exact = false;
+        if (!std::isnan(f) && air::f32_to_f16_bits(f) != bits) exact = false;
+    }
+    check(exact, "all 65,536 halves decode like the oracle and re-encode to themselves");
+    // Ties round to even, overflow to inf, underflow to signed zero.
+    check(air::f32_to_f16_bits(1.0f + 0x1.0p-11f) == 0x3C00, "tie to even (down)");
+    check(air::f32_to_f16_bits(1.0f + 3 * 0x1.0p-11f) == 0x3C02, "tie to even (up)");
+    check(air::f32_to_f16_bits(65520.0f) == 0x7C00 && air::f32_to_f16_bits(65519.0f) == 0x7BFF, "overflow edge");
+    check(air::f32_to_f16_bits(0x1.0p-25f) == 0x0000 && air::f32_to_f16_bits(0x1.8p-25f) == 0x0001,
+          "smallest subnormal edge");
+    check(air::f32_to_f16_bits(-0x1.0p-30f) == 0x8000, "signed underflow");
+}
+
+void test_quantizers() {
+    std::vector<float> w(4 * 512);
+    air::normal_fill(w, 123U, 0.02f);
+    std::vector<float> w2(4 * 512);
+    air::normal_fill(w2, 123U, 0.02f);
+    check(w == w2, "normal_fill is deterministic");
+    double mean = 0, var = 0;
+    for (float v : w) mean += v;
+    mean /= w.size();
+    for (float v : w) var += (v - mean) * (v - mean);
+    var /= w.size();
+    check(std::fabs(mean) < 0.002 && std::fabs(std::sqrt(var) - 0.02) < 0.002, "normal_fill has sigma 0.02");
+    for (std::uint32_t type : {8U, 2U, 12U}) {
+        auto q = air::quantize_rows(type, w, 512, 4);
+        check(q.is_ok(), "quantize_rows succeeds");
+        if (!q) continue;
+        std::vector<float> back(w.size());
+        const int rc = oracle_decode(static_cast<int>(type), reinterpret_cast<const std::uint8_t*>(q.value().data()),
+                                     q.value().size(), back.size(), back.data());
+        check(rc == 0, "oracle decodes the quantized bytes");
+        double num = 0, den = 0;
+        for (std::size_t i = 0; i < w.size(); ++i) {
+            num += (back[i] - w[i]) * (back[i] - w[i]);
+            den += w[i] * w[i];
+        }
+        const double rel = std::sqrt(num / den);
+        const double bound = type == 8U ? 0.01 : 0.12;
+        check(rel < bound, std::string("quantization error of ") + air::format_name(type) + " is " +
+                               std::to_string(rel));
+    }
+}
+
+void test_sequence_estimate() {
+    const auto c7 = air::qwen2_config(28, 3584, 18944, 28, 4, 152064, 32768);
+    // 28 layers x 512 KV width x 2 x 4 B = 114,688 B per token.
+    const auto one_page = air::estimate_paged_fp32_sequence_bytes(c7, 16, 1);
+    check(one_page == 16U * 114688U + (32768U / 16U) * 2U * 8U, "one page plus both page tables");
+    const auto seq = air::estimate_paged_fp32_sequence_bytes(c7, 16, 640);
+    check(seq == 40U * 16U * 114688U + 2048U * 16U, "640 tokens = 40 pages");
+    check(air::estimate_paged_fp32_sequence_bytes(c7, 0, 640) == 0U &&
+              air::estimate_paged_fp32_sequence_bytes(c7, 16, 0) == 0U,
+          "no page size or no tokens reserves nothing");
+    check(air::estimate_paged_fp32_sequence_bytes(c7, 16, std::numeric_limits<std::uint64_t>::max() - 16) ==
+              std::numeric_limits<std::uint64_t>::max(),
+          "overflow saturates");
+}
+
+int run_cpu() {
+    test_capacity_reservations();
+    test_plan_preparation_capacity();
+    test_transition_capacity();
+    test_unbounded_capacity();
+    test_decode_first_order();
+    test_round_robin_order();
+    test_batch_decode_priority();
+    test_batch_spans_prefill();
+    test_batch_zero_limit();
+    test_batch_round_robin();
+    test_regime_identity_and_admission();
+    test_homogeneous_shapes();
+    test_decode_launch_grouping();
+    test_tactic_parsing();
+    test_plan_validation();
+    test_model_and_contract();
+    test_f16_conversion();
+    test_quantizers();
+    test_sequence_estimate();
+    return 0;
+}
+
+// ---- GPU: HipPreparedModel against the oracle ------------------------------
+
+struct DeviceBuffer {
+    float* ptr{nullptr};
+    explicit DeviceBuffer(std::size_t n) {
+        if (hipMalloc(reinterpret_cast<void**>(&ptr), std::max<std::size_t>(n, 1) * sizeof(float)) != hipSuccess) {
+            ptr = nullptr;
+        }
+    }
+    ~DeviceBuffer() {
+        if (ptr) (void)hipFree(ptr);
+    }
+};
+
+double rel_l2(const std::vector<float>& got, const std::vector<float>& want) {
+    double num = 0, den = 0;
+    for (std::size_t i = 0; i < want.size(); ++i) {
+        const double d = static_cast<double>(got[i]) - want[i];
+        num += d * d;
+        den += static_cast<double>(want[i]) * want[i];
+    }
+    return den > 0 ? std::sqrt(num / den) : std::sqrt(num);
+}
+
+// y rows of [M x sum(N_i)] from per-part oracle linears (with per-part bias).
+std::vector<float> oracle_parts(const air::ModelDefinition& model, const std::vector<std::string>& parts,
+                                const std::vector<std::string>& biases, const std::vector<float>& x,
+                                std::uint32_t rows) {
+    std::uint64_t total = 0;
+    for (const auto& p : parts) total += model.find_tensor(p)->shape.dimensions[1];
+    std::vector<float> y(static_cast<std::size_t>(rows) * total);
+    std::uint64_t col = 0;
+    for (std::size_t i = 0; i < parts.size(); ++i) {
+        const auto* t = model.find_tensor(parts[i]);
+        const auto k = t->shape.dimensions[0];
+        const auto n = t->shape.dimensions[1];
+        const float* bias = nullptr;
+        if (i < biases.size() && !biases[i].empty()) {
+            if (const auto* b = model.find_tensor(biases[i])) {
+                bias = reinterpret_cast<const float*>(model.tensor_bytes(*b).value().data());
+            }
+        }
+        const auto bytes = model.tensor_bytes(*t).value();
+        std::vector<float> part(static_cast<std::size_t>(rows) * n);
+        const int rc = oracle_linear(static_cast<int>(t->format_type),
+                                     reinterpret_cast<const std::uint8_t*>(bytes.data()), bytes.size(), k, n, rows,
+                                     x.data(), bias, part.data());
+        if (rc != 0) std::cerr << "oracle_linear failed for " << parts[i] << '\n';
+        for (std::uint32_t r = 0; r < rows; ++r) {
+            std::memcpy(y.data() + r * total + col, part.data() + r * n, n * sizeof(float));
+        }
+        col += n;
+    }
+    return y;
+}
+
+void gpu_check_role(const air::HipPreparedModel& prepared, std::uint32_t layer, air::LinearRole role,
+                    const std::vector<std::string>& parts, const std::vector<std::string>& biases,
+                    std::uint32_t rows, const std::string& label) {
+    const auto info = prepared.linear_info(layer, role);
+    check(info.is_ok(), label + ": role resident");
+    if (!info) return;
+    const auto k = info.value().k;
+    const auto n = info.value().n;
+    std::vector<float> x(static_cast<std::size_t>(rows) * k);
+    air::normal_fill(x, air::tensor_seed(rows * 131U + layer, label), 1.0f);
+    DeviceBuffer dx(x.size()), dy(static_cast<std::size_t>(rows) * n);
+    check(dx.ptr && dy.ptr, label + ": device buffers");
+    if (!dx.ptr || !dy.ptr) return;
+    (void)hipMemcpy(dx.ptr, x.data(), x.size() * sizeof(float), hipMemcpyHostToDevice);
+    const auto s = prepared.linear(layer, role, dx.ptr, dy.ptr, rows, air::QuantizedLinearExecutionKind::hip_decode);
+    check(s.is_ok(), label + ": linear launches (" + s.message() + ")");
+    check(prepared.synchronize().is_ok(), label + ": synchronize");
+    std::vector<float> y(static_cast<std::size_t>(rows) * n);
+    (void)hipMemcpy(y.data(), dy.ptr, y.size() * sizeof(float), hipMemcpyDeviceToHost);
+    const auto want = oracle_parts(prepared.model(), parts, biases, x, rows);
+    const double err = rel_l2(y, want);
+    check(err <= 1e-4, label + ": rel-L2 " + std::to_string(err) + " > 1e-4");
+    std::cout << "  " << label << " rows=" << rows << " k=" << k << " n=" << n << " rel_l2=" << err << '\n';
+}
+
+void gpu_model_case(std::uint32_t format, bool fuse, bool tied, bool output_bias) {
+    air::SyntheticQwen2Spec spec;
+    spec.config = small_config();
+    spec.weight_format = format;
+    spec.embedding_format = format;
+    spec.tied_output = tied;
+    spec.output_bias = output_bias;
+    spec.seed = 0xA174D1FFULL + format;
+    auto model = air::make_synthetic_qwen2(spec);
+    check(model.is_ok(), "synthetic model");
+    if (!model) return;
+    air::HipPrepareOptions options;
+    options.fuse = fuse;
+    auto prepared = air::HipPreparedModel::create(model.value(), options);
+    const std::string tag = std::string(air::format_name(format)) + (fuse ? " fused" : " unfused") +
+                            (tied ? " tied" : "") + (output_bias ? " out-bias" : "");
+    check(prepared.is_ok(), tag + ": prepare (" + (prepared ? std::string() : prepared.status().message()) + ")");
+    if (!prepared) return;
+    const auto& p = *prepared.value();
+    check(p.fused_qkv() == fuse && p.fused_gate_up() == fuse, tag + ": fusion as requested");
+    std::cout << tag << '\n';
+    for (std::uint32_t rows : {1U, 5U, 16U, 33U, 64U}) {
+        for (std::uint32_t layer = 0; layer < 2; ++layer) {
+            const auto n = [layer](const char* s) { return air::block_tensor_name(layer, s); };
+            if (fuse) {
+                gpu_check_role(p, layer, air::LinearRole::attn_qkv, {n("attn_q.weight"), n("attn_k.weight"), n("attn_v.weight")},
+                               {n("attn_q.bias"), n("attn_k.bias"), n("attn_v.bias")}, rows, tag + " qkv");
+                gpu_check_role(p, layer, air::LinearRole::ffn_gate_up, {n("ffn_gate.weight"), n("ffn_up.weight")}, {},
+                               rows, tag + " gate_up");
+            } else {
+                gpu_check_role(p, layer, air::LinearRole::attn_q, {n("attn_q.weight")}, {n("attn_q.bias")}, rows, tag + " q");
+                gpu_check_role(p, layer, air::LinearRole::attn_k, {n("attn_k.weight")}, {n("attn_k.bias")}, rows, tag + " k");
+                gpu_check_role(p, layer, air::LinearRole::attn_v, {n("attn_v.weight")}, {n("attn_v.bias")}, rows, tag + " v");
+                gpu_check_role(p, layer, air::LinearRole::ffn_gate, {n("ffn_gate.weight")}, {}, rows, tag + " gate");
+                gpu_check_role(p, layer, air::LinearRole::ffn_up, {n("ffn_up.weight")}, {}, rows, tag + " up");
+            }
+            gpu_check_role(p, layer, air::LinearRole::attn_output, {n("attn_output.weight")}, {}, rows, tag + " o");
+            gpu_check_role(p, layer, air::LinearRole::ffn_down, {n("ffn_down.weight")}, {}, rows, tag + " down");
+        }
+        gpu_check_role(p, 0, air::LinearRole::output, {tied ? "token_embd.weight" : "output.weight"},
+                       {output_bias ? "output.bias" : ""}, rows, tag + " output");
+    }
+    // Roles that are not resident under this residency are refused.
+    DeviceBuffer dummy(16);
+    const auto wrong = p.linear(0, fuse ? air::LinearRole::attn_q : air::LinearRole::attn_qkv, dummy.ptr, dummy.ptr, 1,
+                                air::QuantizedLinearExecutionKind::hip_decode);
+    check(wrong.code() == air::ErrorCode::invalid_argument, tag + ": non-resident role refused");
+    const auto layer_oob = p.linear(2, air::LinearRole::attn_output, dummy.ptr, dummy.ptr, 1,
+                                    air::QuantizedLinearExecutionKind::hip_decode);
+    check(layer_oob.code() == air::ErrorCode::invalid_argument, tag + ": layer out of range refused");
+    const auto tactic = p.linear(0, air::LinearRole::attn_output, dummy.ptr, dummy.ptr, 1,
+                                 air::QuantizedLinearExecutionKind::batch_reuse8);
+    check(tactic.code() == air::ErrorCode::unsupported, tag + ": CUDA tactic refused");
+}
+
+void gpu_prepared_model_contract() {
+    air::SyntheticQwen2Spec spec;
+    spec.config = small_config();
+    auto model = air::make_synthetic_qwen2(spec);
+    if (!model) return;
+    auto prepared = air::prepare_hip_model(model.value(), 0);
+    check(prepared.is_ok(), "prepare_hip_model");
+    if (!prepared) return;
+    auto& p = *prepared.value();
+    check(p.backend() == air::BackendKind::hip && p.capabilities().backend == air::BackendKind::hip, "backend hip");
+    check(p.capabilities().max_decode_batch_width == 64U, "decode width 64 advertised");
+    const auto free = p.free_device_bytes();
+    const auto capacity = p.sequence_capacity_bytes();
+    check(free && *free > (1ULL << 30) && capacity && *capacity >= *free, "capacity from hipMemGetInfo");
+    check(p.resident_device_bytes() > 0U, "resident bytes are counted");
+    auto plan = paged_plan();
+    plan.linear = {air::QuantizedLinearExecutionKind::hip_decode, air::QuantizedLinearExecutionKind::hip_decode,
+                   air::QuantizedLinearExecutionKind::hip_decode};
+    check(air::validate_execution_plan(plan, p.capabilities()).is_ok(), "a hip-decode plan validates");
+    const auto seq = p.create_sequence(plan);
+    check(!seq && seq.status().code() == air::ErrorCode::unsupported, "sequences are not provided");
+    auto baseline = paged_plan();
+    const auto seq2 = p.create_sequence(baseline);
+    check(!seq2 && seq2.status().code() == air::ErrorCode::unsupported &&
+              seq2.status().message().find("tactic") != std::string::npos,
+          "a baseline plan fails validation first");
+    CapacityScheduler scheduler(32U);
+    const auto d = scheduler.evaluate(0U, 0U, p, plan, 640U);
+    check(d.admit && d.reservation_bytes == air::estimate_paged_fp32_sequence_bytes(spec.config, 16U, 640U),
+          "CapacityScheduler admits against the HIP model's capacity");
+    const auto huge = scheduler.evaluate(0U, 0U, p, plan, spec.config.context_length * 100000000ULL);
+    check(!huge.admit && huge.reason == "device-capacity", "a reservation beyond HBM is refused");
+}
+
+int run_gpu() {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0) {
+        std::cerr << "no HIP device\n";
+        return 2;
+    }
+    gpu_prepared_model_contract();
+    gpu_model_case(8U, true, false, false);
+    gpu_model_case(8U, false, true, true);
+    gpu_model_case(2U, true, false, true);
+    gpu_model_case(12U, true, true, false);
+    gpu_model_case(12U, false, false, false);
+    return 0;
+}
+
+} // namespace
+
+int main(int argc, char** argv) {
+    const std::string mode = argc > 1 ? argv[1] : "cpu";
+    int rc = 0;
+    if (mode == "cpu") {
+        rc = run_cpu();
+    } else if (mode == "gpu") {
+        rc = run_gpu();
+    } else {
+        std::cerr << "usage: host_tests cpu|gpu\n";
+        return 2;
+    }
+    if (rc != 0) return rc;
+    if (failures != 0) {
+        std::cerr << failures << " of " << checks << " host checks failed\n";
+        return 1;
+    }
+    std::cout << "host " << mode << " tests passed (" << checks << " checks)\n";
+    return 0;
+}
