@@ -15,6 +15,10 @@ struct TilePlanes {
     std::uint64_t kp{0};   // padded k = kt * tile_k
     void* codes{nullptr};
     void* scales{nullptr};
+    // Power-of-two factors of the prefill GEMM: dequantized weights are
+    // formed in f16 as w * prefill_scale, outputs multiplied by prefill_unscale.
+    float prefill_scale{1.0f};
+    float prefill_unscale{1.0f};
 };
 
 // Canonical GGUF bytes (device) -> tile planes.
@@ -78,5 +82,31 @@ struct GemvShape {
 GemvShape plan_decode_gemv(const TilePlanes& planes, const DecodeTuning& tuning);
 hipError_t launch_decode_gemv(const TilePlanes& planes, const float* x, const float* bias, float* y,
                               const GemvShape& shape, hipStream_t stream);
+
+// Prefill linear on f16 MFMA (M = 1..4096; planned for M >= 65).
+struct PrefillTuning {
+    std::uint32_t tile_m{0};   // 16-row activation tiles per wave: 4 or 8 (0 = automatic)
+    std::uint32_t tile_n{0};   // 16-row weight tiles per wave: 2 or 4
+    std::uint32_t k_splits{0}; // workgroups splitting K (0 = automatic)
+};
+struct PrefillShape {
+    std::uint32_t tile_m{8};
+    std::uint32_t tile_n{4};
+    std::uint32_t m_tiles{0};
+    std::uint32_t groups{0};
+    std::uint32_t steps{0};
+    std::uint32_t steps_per_split{0};
+    std::uint32_t splits{1};
+};
+PrefillShape plan_prefill(const TilePlanes& planes, std::uint32_t m, const PrefillTuning& tuning);
+// Workspace of one prefill linear: f16 activations, row scales and (with a K
+// split) the f32 partials.
+std::uint64_t prefill_workspace_bytes(std::uint64_t k, std::uint32_t m, const PrefillShape& shape, std::uint64_t n);
+hipError_t launch_prefill_linear(const TilePlanes& planes, const float* x, const float* bias, float* y,
+                                 std::uint32_t m, const PrefillShape& shape, void* workspace, hipStream_t stream);
+// Sets planes.prefill_scale / prefill_unscale from the largest dequantized
+// magnitude of the resident matrix (synchronous; `bound_scratch` is one
+// device uint32).
+hipError_t compute_prefill_scale(TilePlanes& planes, std::uint32_t* bound_scratch, hipStream_t stream);
 
 } // namespace air_hip

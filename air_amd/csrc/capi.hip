@@ -45,6 +45,11 @@ struct air_hip_context {
     std::uint64_t split_partials_bytes{0};
     std::uint32_t* split_counters{nullptr};
     std::uint32_t split_counter_count{0};
+    // Prefill GEMM: f16 activations, row scales and K-split partials.
+    void* prefill_workspace{nullptr};
+    std::uint64_t prefill_workspace_bytes{0};
+    PrefillTuning prefill_tuning{};
+    std::uint32_t* bound_scratch{nullptr};  // one uint32 for the weight exponent at residency
 };
 
 struct air_hip_matrix {
@@ -116,6 +121,36 @@ int ensure_workspace(air_hip_context* ctx, std::uint64_t bytes) {
     if (err != hipSuccess) return hip_fail(err, "hipMalloc(workspace)");
     ctx->workspace = p;
     ctx->workspace_bytes = bytes;
+    return AIR_HIP_OK;
+}
+
+int ensure_prefill_workspace(air_hip_context* ctx, std::uint64_t bytes) {
+    if (bytes <= ctx->prefill_workspace_bytes) return AIR_HIP_OK;
+    if (ctx->prefill_workspace) {
+        const hipError_t sync = hipStreamSynchronize(ctx->stream);
+        if (sync != hipSuccess) return hip_fail(sync, "hipStreamSynchronize(prefill workspace growth)");
+        (void)hipFree(ctx->prefill_workspace);
+        ctx->prefill_workspace = nullptr;
+        ctx->prefill_workspace_bytes = 0;
+    }
+    void* p = nullptr;
+    const hipError_t err = hipMalloc(&p, bytes);
+    if (err != hipSuccess) return hip_fail(err, "hipMalloc(prefill workspace)");
+    ctx->prefill_workspace = p;
+    ctx->prefill_workspace_bytes = bytes;
+    return AIR_HIP_OK;
+}
+
+// Prefill linear: x [rows][k] -> y [rows][n] on the f16 MFMA GEMM.
+int run_prefill(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y, const float* bias,
+                std::uint32_t rows) {
+    const PrefillShape shape = plan_prefill(m->planes, rows, ctx->prefill_tuning);
+    int rc = ensure_prefill_workspace(ctx, prefill_workspace_bytes(m->planes.k, rows, shape, m->planes.n));
+    if (rc != AIR_HIP_OK) return rc;
+    const hipError_t err = launch_prefill_linear(m->planes, x, bias, y, rows, shape, ctx->prefill_workspace, ctx->stream);
+    if (err != hipSuccess) return hip_fail(err, "prefill_gemm_kernel");
+    ctx->prefill_linear_calls.fetch_add(1, std::memory_order_relaxed);
+    ctx->prefill_rows.fetch_add(rows, std::memory_order_relaxed);
     return AIR_HIP_OK;
 }
 
@@ -223,6 +258,8 @@ int air_hip_context_destroy(air_hip_context* ctx) {
         if (ctx->workspace) (void)hipFree(ctx->workspace);
         if (ctx->split_partials) (void)hipFree(ctx->split_partials);
         if (ctx->split_counters) (void)hipFree(ctx->split_counters);
+        if (ctx->prefill_workspace) (void)hipFree(ctx->prefill_workspace);
+        if (ctx->bound_scratch) (void)hipFree(ctx->bound_scratch);
     }
     delete ctx;
     return AIR_HIP_OK;
@@ -240,7 +277,21 @@ int air_hip_context_reserve(air_hip_context* ctx, uint64_t max_k, uint32_t max_m
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
     const std::uint64_t kp = ceil_div(max_k, kSplitK) * kSplitK;
-    return ensure_workspace(ctx, split_workspace_bytes(kp, max_m));
+    int rc = ensure_workspace(ctx, split_workspace_bytes(kp, max_m < kMaxRows ? max_m : kMaxRows));
+    if (rc != AIR_HIP_OK || max_m <= kFusedMaxRows) return rc;
+    PrefillShape unsplit{};
+    return ensure_prefill_workspace(ctx, prefill_workspace_bytes(max_k, max_m < kMaxRows ? max_m : kMaxRows, unsplit, 0));
+}
+
+int air_hip_context_set_prefill_tuning(air_hip_context* ctx, uint32_t tile_m, uint32_t tile_n, uint32_t k_splits) {
+    if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
+    if (tile_m != 0 && tile_m != 4 && tile_m != 8) return fail(AIR_HIP_INVALID_ARGUMENT, "tile_m must be 0, 4 or 8");
+    if (tile_n != 0 && tile_n != 2 && tile_n != 4) return fail(AIR_HIP_INVALID_ARGUMENT, "tile_n must be 0, 2 or 4");
+    if (k_splits > 64) return fail(AIR_HIP_INVALID_ARGUMENT, "k_splits must be at most 64");
+    ctx->prefill_tuning.tile_m = tile_m;
+    ctx->prefill_tuning.tile_n = tile_n;
+    ctx->prefill_tuning.k_splits = k_splits;
+    return AIR_HIP_OK;
 }
 
 int air_hip_context_set_tuning(air_hip_context* ctx, uint32_t rows_per_wave, uint32_t waves_per_group,
@@ -346,6 +397,12 @@ int air_hip_matrix_prepare(air_hip_context* ctx, int type, uint64_t k, uint64_t 
     err = launch_repack(p, src, ctx->stream);
     if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
     if (staging) (void)hipFree(staging);
+    if (err == hipSuccess && !ctx->bound_scratch) {
+        void* b = nullptr;
+        err = hipMalloc(&b, 256);
+        ctx->bound_scratch = static_cast<std::uint32_t*>(b);
+    }
+    if (err == hipSuccess) err = compute_prefill_scale(p, ctx->bound_scratch, ctx->stream);
     if (err != hipSuccess) {
         (void)hipFree(p.codes);
         (void)hipFree(p.scales);
@@ -435,7 +492,7 @@ int air_hip_linear_loaded(air_hip_context* ctx, const air_hip_matrix* m, float* 
         return fail(AIR_HIP_INVALID_ARGUMENT, "unknown linear tactic %d", tactic);
     }
     if (tactic == AIR_HIP_LINEAR_PREFILL) {
-        return fail(AIR_HIP_UNSUPPORTED, "the prefill MFMA tactic is not available in this build");
+        return fail(AIR_HIP_UNSUPPORTED, "the prefill tactic runs through air_hip_linear, not loaded activations");
     }
     if (ctx->loaded_rows == 0) return fail(AIR_HIP_INVALID_STATE, "no activations are loaded in this context");
     if (ctx->loaded_k != m->planes.k) {
@@ -463,8 +520,16 @@ int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* m, const float* x
     if (tactic != AIR_HIP_LINEAR_AUTO && tactic != AIR_HIP_LINEAR_DECODE && tactic != AIR_HIP_LINEAR_PREFILL) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "unknown linear tactic %d", tactic);
     }
-    if (tactic == AIR_HIP_LINEAR_PREFILL) {
-        return fail(AIR_HIP_UNSUPPORTED, "the prefill MFMA tactic is not available in this build");
+    if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
+    const bool prefill = tactic == AIR_HIP_LINEAR_PREFILL ||
+                         (tactic == AIR_HIP_LINEAR_AUTO && rows > AIR_HIP_MAX_DECODE_ROWS);
+    if (prefill) {
+        if (rows == 0) return fail(AIR_HIP_INVALID_ARGUMENT, "linear batch width must be non-zero");
+        if (rows > kMaxRows) return fail(AIR_HIP_UNSUPPORTED, "linear batch width %u exceeds %u", rows, kMaxRows);
+        if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
+        DeviceScope scope(ctx->device);
+        if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+        return run_prefill(ctx, m, x, y, bias, rows);
     }
     if (rows >= 1u && rows <= kFusedMaxRows) {
         // One launch: the activations are split in registers.

@@ -1,0 +1,490 @@
+// linear_prefill.hip -- prefill-sized linears (M = 65..4096) on f16 MFMA.
+//
+// The reference runs prefill linears through the same f32 kernels as decode
+// (specialized_matmul / batch_reuse, src/cuda/cuda_backend.cu:501-583), so a
+// 512-token prefill decodes every weight 64 times.  Here a prefill linear is a
+// GEMM on the matrix cores:
+//
+//   1. prefill_activations_kernel: x f32 [M][K] -> xh f16 [Mp][Kx], each row
+//      scaled by a power of two so that its max |x| lies in [2^14, 2^15)
+//      (no f16 overflow, no needless subnormals); row_inv[m] undoes it.
+//   2. prefill_gemm_kernel: each workgroup owns BM = 16*TM activation rows and
+//      4*TN 16-row weight tiles; each of its four waves owns TN weight tiles.
+//      Per 64-k step the activation tile is staged through LDS (it is shared
+//      by all four waves) while every wave streams its own weight codes from
+//      the resident tile layout, dequantizes them to f16 in registers
+//      (w = code * f16(d * 2^-e), exact codes, one rounding) and feeds them as
+//      the A operand of v_mfma_f32_16x16x32_f16; the LDS activation fragments
+//      are the B operand.  The lane layout of the resident records is the MFMA
+//      operand layout, so weights never pass through LDS: no wave reads
+//      another wave's weights.  Accumulation is f32.
+//   3. With a K split, prefill_reduce_kernel sums the split partials in a
+//      fixed order (deterministic) and adds the bias.
+//
+// The weight exponent e is chosen per matrix when it becomes resident
+// (prefill_bound_kernel): max |w| * 2^-e <= 2^15.  Outputs are
+// acc * row_inv[m] * 2^e + bias[n].
+#include "air_hip_device.hpp"
+#include "air_hip_kernels.hpp"
+
+#include <cmath>
+#include <cstring>
+
+namespace air_hip {
+namespace {
+
+constexpr unsigned kThreads = 256;       // four waves
+constexpr unsigned kStepK = 64;          // k per pipeline step: two 32-blocks
+constexpr unsigned kLdsStride = kStepK + 8;  // halfs per staged activation row
+
+// ---- 1. activations ----------------------------------------------------
+
+// One workgroup per padded row.  Row scale as block_scale, over the whole row.
+__global__ __launch_bounds__(kThreads) void prefill_activations_kernel(const float* __restrict__ x, std::uint32_t m,
+                                                                       std::uint64_t k, std::uint64_t ldx,
+                                                                       _Float16* __restrict__ xh,
+                                                                       float* __restrict__ row_inv) {
+    __shared__ float red[kThreads / 64];
+    const std::uint32_t row = blockIdx.x;
+    _Float16* out = xh + static_cast<std::uint64_t>(row) * ldx;
+    if (row >= m) {
+        for (std::uint64_t c = threadIdx.x * 8u; c < ldx; c += kThreads * 8u) {
+            *reinterpret_cast<uint4*>(out + c) = make_uint4(0u, 0u, 0u, 0u);
+        }
+        if (threadIdx.x == 0) row_inv[row] = 1.0f;
+        return;
+    }
+    const float* in = x + static_cast<std::uint64_t>(row) * k;
+    float amax = 0.0f;
+    for (std::uint64_t c = threadIdx.x * 4u; c < k; c += kThreads * 4u) {
+        const float4 v = *reinterpret_cast<const float4*>(in + c);
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float s, inv;
+    block_scale(amax, s, inv);
+    for (std::uint64_t c = threadIdx.x * 8u; c < ldx; c += kThreads * 8u) {
+        half8v h;
+        if (c < k) {  // k is a multiple of 32, so a run of 8 is all in or all out
+            const float4 a = *reinterpret_cast<const float4*>(in + c);
+            const float4 b = *reinterpret_cast<const float4*>(in + c + 4);
+            h[0] = static_cast<_Float16>(a.x * s); h[1] = static_cast<_Float16>(a.y * s);
+            h[2] = static_cast<_Float16>(a.z * s); h[3] = static_cast<_Float16>(a.w * s);
+            h[4] = static_cast<_Float16>(b.x * s); h[5] = static_cast<_Float16>(b.y * s);
+            h[6] = static_cast<_Float16>(b.z * s); h[7] = static_cast<_Float16>(b.w * s);
+        } else {
+            for (int e = 0; e < 8; ++e) h[e] = static_cast<_Float16>(0.0f);
+        }
+        *reinterpret_cast<half8v*>(out + c) = h;
+    }
+    if (threadIdx.x == 0) row_inv[row] = inv;
+}
+
+// ---- weight fragments -----------------------------------------------------
+
+// Raw codes and scales of one 64-k step of one 16-row tile, for one lane.
+template <int FMT>
+struct StepCodes;
+
+template <>
+struct StepCodes<kQ8_0> {
+    uint4 c;               // bytes of blocks 2kt, 2kt+1
+    std::uint32_t d;       // two f16 scales
+};
+template <>
+struct StepCodes<kQ4_0> {
+    uint2 c;               // dwords of blocks 2hs, 2hs+1 of the 128-k tile
+    std::uint32_t d;       // their two f16 scales
+};
+template <>
+struct StepCodes<kQ4_K> {
+    uint2 c;               // dwords of sub-blocks 2sub, 2sub+1
+    uint4 h;               // the 16-byte super-block header of the lane's row
+};
+
+template <int FMT>
+__device__ __forceinline__ void load_step(const void* codes, const void* scales, std::uint32_t rt, std::uint32_t kt_count,
+                                          std::uint32_t s, std::uint32_t lane, bool live, StepCodes<FMT>& out) {
+    if constexpr (FMT == kQ8_0) {
+        if (!live) { out.c = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u); out.d = 0u; return; }
+        const std::uint64_t tile = static_cast<std::uint64_t>(rt) * kt_count + s;
+        out.c = static_cast<const uint4*>(codes)[tile * 64u + lane];
+        out.d = static_cast<const std::uint32_t*>(scales)[tile * 16u + (lane & 15u)];
+    } else if constexpr (FMT == kQ4_0) {
+        if (!live) { out.c = make_uint2(0x88888888u, 0x88888888u); out.d = 0u; return; }
+        const std::uint64_t tile = static_cast<std::uint64_t>(rt) * kt_count + (s >> 1);
+        const uint2* rec = static_cast<const uint2*>(codes) + (tile * 64u + lane) * 2u + (s & 1u);
+        out.c = *rec;
+        out.d = static_cast<const std::uint32_t*>(scales)[(tile * 16u + (lane & 15u)) * 2u + (s & 1u)];
+    } else {
+        if (!live) { out.c = make_uint2(0u, 0u); out.h = make_uint4(0u, 0u, 0u, 0u); return; }
+        const std::uint64_t tile = static_cast<std::uint64_t>(rt) * kt_count + (s >> 2);
+        const std::uint32_t sub = s & 3u;
+        const uint2* rec = static_cast<const uint2*>(codes) + ((tile * 2u + (sub >> 1)) * 64u + lane) * 2u + (sub & 1u);
+        out.c = *rec;
+        out.h = static_cast<const uint4*>(scales)[tile * 16u + (lane & 15u)];
+    }
+}
+
+__device__ __forceinline__ _Float16 scaled_half(std::uint32_t bits, float w_scale) {
+    const float v = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<std::uint16_t>(bits))) * w_scale;
+    return static_cast<_Float16>(v);
+}
+
+// f16 weights of the step's two 32-blocks (A fragments: row l%16, k 8(l/16)+e).
+template <int FMT>
+__device__ __forceinline__ void dequant_step(const StepCodes<FMT>& in, std::uint32_t s, float w_scale, half8v (&w)[2]) {
+    if constexpr (FMT == kQ8_0) {
+        const std::uint32_t cw[4] = {in.c.x, in.c.y, in.c.z, in.c.w};
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            half2v p0, p1, p2, p3;
+            q8_dword_to_half(cw[2 * b], p0, p1);
+            q8_dword_to_half(cw[2 * b + 1], p2, p3);
+            const _Float16 d = scaled_half((in.d >> (16 * b)) & 0xffffu, w_scale);
+            const half2v dd = {d, d};
+            p0 *= dd; p1 *= dd; p2 *= dd; p3 *= dd;
+            w[b][0] = p0[0]; w[b][1] = p0[1]; w[b][2] = p1[0]; w[b][3] = p1[1];
+            w[b][4] = p2[0]; w[b][5] = p2[1]; w[b][6] = p3[0]; w[b][7] = p3[1];
+        }
+    } else if constexpr (FMT == kQ4_0) {
+        const std::uint32_t cw[2] = {in.c.x, in.c.y};
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const _Float16 d = scaled_half((in.d >> (16 * b)) & 0xffffu, w_scale);
+            w[b] = nibble_dword_to_half8<8>(cw[b]) * d;
+        }
+    } else {
+        const std::uint32_t cw[2] = {in.c.x, in.c.y};
+        const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<std::uint16_t>(in.h.x & 0xffffu)));
+        const float dmin = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<std::uint16_t>(in.h.x >> 16)));
+        const std::uint32_t packed[3] = {in.h.y, in.h.z, in.h.w};
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            std::uint32_t sc = 0, mn = 0;
+            q4k_scale_min(packed, 2u * (s & 3u) + static_cast<std::uint32_t>(b), sc, mn);
+            const _Float16 a = static_cast<_Float16>(d * static_cast<float>(sc) * w_scale);
+            const _Float16 o = static_cast<_Float16>(dmin * static_cast<float>(mn) * w_scale);
+            w[b] = nibble_dword_to_half8<0>(cw[b]) * a - o;
+        }
+    }
+}
+
+// ---- 2. GEMM --------------------------------------------------------------
+
+struct GemmArgs {
+    const void* codes;
+    const void* scales;
+    std::uint32_t nt, kt;        // tile grid of the matrix
+    std::uint64_t n;
+    const _Float16* xh;          // [Mp][ldx]
+    std::uint64_t ldx;
+    const float* row_inv;        // [Mp]
+    float w_scale, w_unscale;
+    const float* bias;           // [n] or null (ignored when splits > 1)
+    float* out;                  // y [m][n], or partials [splits][m][n]
+    std::uint32_t m;
+    std::uint32_t m_tiles;       // ceil(m / BM)
+    std::uint32_t groups;        // ceil(nt / (4 * TN))
+    std::uint32_t steps;         // 64-k steps of the padded k
+    std::uint32_t steps_per_split;
+    std::uint32_t partial;       // 1: write split partials (no bias)
+};
+
+template <int FMT, int TM, int TN>
+__global__ __launch_bounds__(kThreads, 2) void prefill_gemm_kernel(GemmArgs a) {
+    constexpr unsigned BM = 16u * TM;
+    constexpr unsigned kChunks = BM * (kStepK / 8u) / kThreads;  // 16-byte activation chunks per thread
+    static_assert(kChunks * kThreads == BM * (kStepK / 8u), "activation tile must split evenly");
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][BM * kLdsStride];
+
+    const std::uint32_t tid = threadIdx.x;
+    const std::uint32_t lane = tid & 63u;
+    const std::uint32_t wave = tid >> 6;
+    std::uint32_t bid = blockIdx.x;
+    const std::uint32_t mt = bid % a.m_tiles;
+    bid /= a.m_tiles;
+    const std::uint32_t group = bid % a.groups;
+    const std::uint32_t split = bid / a.groups;
+    const std::uint32_t m0 = mt * BM;
+    const std::uint32_t rt0 = (group * 4u + wave) * TN;
+    const std::uint32_t s_begin = split * a.steps_per_split;
+    const std::uint32_t s_end = min(a.steps, s_begin + a.steps_per_split);
+
+    float4v acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int t = 0; t < TN; ++t) acc[i][t] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+    uint4 xr[kChunks];
+    const auto load_x = [&](std::uint32_t s) {
+#pragma unroll
+        for (unsigned j = 0; j < kChunks; ++j) {
+            const std::uint32_t c = tid + kThreads * j;
+            const std::uint32_t row = c >> 3, col = (c & 7u) * 8u;
+            xr[j] = *reinterpret_cast<const uint4*>(a.xh + static_cast<std::uint64_t>(m0 + row) * a.ldx +
+                                                    static_cast<std::uint64_t>(s) * kStepK + col);
+        }
+    };
+    const auto store_x = [&](unsigned buf) {
+#pragma unroll
+        for (unsigned j = 0; j < kChunks; ++j) {
+            const std::uint32_t c = tid + kThreads * j;
+            const std::uint32_t row = c >> 3, col = (c & 7u) * 8u;
+            *reinterpret_cast<uint4*>(&xs[buf][row * kLdsStride + col]) = xr[j];
+        }
+    };
+    StepCodes<FMT> wr[TN];
+    const auto load_w = [&](std::uint32_t s) {
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+            const std::uint32_t rt = rt0 + static_cast<std::uint32_t>(t);
+            load_step<FMT>(a.codes, a.scales, rt, a.kt, s, lane, rt < a.nt, wr[t]);
+        }
+    };
+
+    if (s_begin < s_end) {
+        load_x(s_begin);
+        load_w(s_begin);
+        store_x(0);
+    }
+    __syncthreads();
+    for (std::uint32_t s = s_begin; s < s_end; ++s) {
+        const unsigned buf = (s - s_begin) & 1u;
+        half8v w[TN][2];
+#pragma unroll
+        for (int t = 0; t < TN; ++t) dequant_step<FMT>(wr[t], s, a.w_scale, w[t]);
+        const bool more = s + 1u < s_end;
+        if (more) {
+            load_x(s + 1u);
+            load_w(s + 1u);
+        }
+        const _Float16* xb = xs[buf];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            half8v xf[TM];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                xf[i] = *reinterpret_cast<const half8v*>(
+                    xb + (static_cast<unsigned>(i) * 16u + (lane & 15u)) * kLdsStride + 32u * b + 8u * (lane >> 4));
+            }
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int t = 0; t < TN; ++t) acc[i][t] = mfma16x16x32(w[t][b], xf[i], acc[i][t]);
+        }
+        if (more) store_x(buf ^ 1u);
+        __syncthreads();
+    }
+
+    // D[row = weight row][col = activation row]: lane holds rows 4(l/16)+r of column l%16.
+    float* out = a.out + (a.partial ? static_cast<std::uint64_t>(split) * a.m * a.n : 0u);
+    const bool vec = (a.n & 3u) == 0u;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const std::uint32_t m = m0 + static_cast<std::uint32_t>(i) * 16u + (lane & 15u);
+        if (m >= a.m) continue;
+        const float scale = a.row_inv[m] * a.w_unscale;
+        float* yrow = out + static_cast<std::uint64_t>(m) * a.n;
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+            const std::uint64_t n0 = static_cast<std::uint64_t>(rt0 + static_cast<std::uint32_t>(t)) * 16u + 4u * (lane >> 4);
+            if (n0 >= a.n) continue;
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                v[r] = acc[i][t][r] * scale;
+                if (a.bias && n0 + r < a.n) v[r] += a.bias[n0 + r];
+            }
+            if (vec && n0 + 4u <= a.n) {
+                *reinterpret_cast<float4*>(yrow + n0) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+                for (int r = 0; r < 4; ++r)
+                    if (n0 + r < a.n) yrow[n0 + r] = v[r];
+            }
+        }
+    }
+}
+
+// ---- 3. split reduction ------------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void prefill_reduce_kernel(const float* __restrict__ partials,
+                                                                  std::uint32_t splits, std::uint32_t m,
+                                                                  std::uint64_t n, const float* __restrict__ bias,
+                                                                  float* __restrict__ y) {
+    const std::uint64_t total = static_cast<std::uint64_t>(m) * n;
+    for (std::uint64_t i = blockIdx.x * static_cast<std::uint64_t>(kThreads) + threadIdx.x; i < total;
+         i += static_cast<std::uint64_t>(gridDim.x) * kThreads) {
+        float v = 0.0f;
+        for (std::uint32_t s = 0; s < splits; ++s) v += partials[s * total + i];
+        if (bias) v += bias[i % n];
+        y[i] = v;
+    }
+}
+
+// ---- weight exponent ---------------------------------------------------
+
+// Largest |dequantized weight| bound over all blocks, as float bits (>= 0).
+__global__ __launch_bounds__(kThreads) void prefill_bound_kernel(int type, const void* scales, std::uint64_t entries,
+                                                                 std::uint32_t* bound_bits) {
+    float local = 0.0f;
+    for (std::uint64_t i = blockIdx.x * static_cast<std::uint64_t>(kThreads) + threadIdx.x; i < entries;
+         i += static_cast<std::uint64_t>(gridDim.x) * kThreads) {
+        float b;
+        if (type == kQ4_K) {
+            const uint4 h = static_cast<const uint4*>(scales)[i];
+            const float d = fabsf(f16_bits_to_f32(h.x & 0xffffu));
+            const float dmin = fabsf(f16_bits_to_f32(h.x >> 16));
+            b = fmaxf(d * 945.0f, dmin * 63.0f);  // (d*63)*15 and dmin*63
+        } else {
+            const float d = fabsf(f16_bits_to_f32(static_cast<const std::uint16_t*>(scales)[i]));
+            b = d * (type == kQ8_0 ? 128.0f : 8.0f);
+        }
+        local = (b > local || b != b) ? b : local;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float o = __shfl_xor(local, off);
+        local = (o > local || o != o) ? o : local;
+    }
+    if ((threadIdx.x & 63u) == 0) atomicMax(bound_bits, __float_as_uint(local) & 0x7fffffffu);
+}
+
+template <int FMT>
+hipError_t launch_gemm_fmt(const GemmArgs& args, std::uint32_t tm, std::uint32_t tn, std::uint32_t blocks,
+                           hipStream_t stream) {
+    const dim3 grid(blocks), block(kThreads);
+    if (tm == 8 && tn == 4) {
+        hipLaunchKernelGGL((prefill_gemm_kernel<FMT, 8, 4>), grid, block, 0, stream, args);
+    } else if (tm == 8 && tn == 2) {
+        hipLaunchKernelGGL((prefill_gemm_kernel<FMT, 8, 2>), grid, block, 0, stream, args);
+    } else if (tm == 4 && tn == 4) {
+        hipLaunchKernelGGL((prefill_gemm_kernel<FMT, 4, 4>), grid, block, 0, stream, args);
+    } else {
+        hipLaunchKernelGGL((prefill_gemm_kernel<FMT, 4, 2>), grid, block, 0, stream, args);
+    }
+    return hipGetLastError();
+}
+
+} // namespace
+
+PrefillShape plan_prefill(const TilePlanes& p, std::uint32_t m, const PrefillTuning& tuning) {
+    PrefillShape s;
+    // Register tile per wave: TM x TN MFMA tiles (16 x 16 each).
+    if (tuning.tile_m == 4 || tuning.tile_m == 8) s.tile_m = tuning.tile_m;
+    if (tuning.tile_n == 2 || tuning.tile_n == 4) s.tile_n = tuning.tile_n;
+    const std::uint32_t bm = 16u * s.tile_m;
+    s.m_tiles = static_cast<std::uint32_t>(ceil_div(m, bm));
+    s.groups = static_cast<std::uint32_t>(ceil_div(p.nt, 4u * s.tile_n));
+    s.steps = static_cast<std::uint32_t>(p.kp / kStepK);
+    std::uint32_t splits = tuning.k_splits;
+    if (splits == 0u) {
+        // Fill the 256 CUs (two workgroups each) when the tile grid alone
+        // cannot, keeping at least 16 steps per split.
+        const std::uint64_t tiles = static_cast<std::uint64_t>(s.m_tiles) * s.groups;
+        splits = 1u;
+        while (tiles * splits * 2u <= 512u && s.steps / (splits * 2u) >= 16u) splits *= 2u;
+    }
+    splits = splits < 1u ? 1u : (splits > s.steps ? s.steps : splits);
+    s.steps_per_split = static_cast<std::uint32_t>(ceil_div(s.steps, splits));
+    s.splits = static_cast<std::uint32_t>(ceil_div(s.steps, s.steps_per_split));
+    return s;
+}
+
+std::uint64_t prefill_ldx(std::uint64_t k) { return ceil_div(k, 256u) * 256u; }
+std::uint32_t prefill_rows_padded(std::uint32_t m) { return static_cast<std::uint32_t>(ceil_div(m, 256u) * 256u); }
+
+std::uint64_t prefill_workspace_bytes(std::uint64_t k, std::uint32_t m, const PrefillShape& shape, std::uint64_t n) {
+    const std::uint64_t mp = prefill_rows_padded(m);
+    std::uint64_t bytes = ceil_div(mp * prefill_ldx(k) * 2u, 256u) * 256u + ceil_div(mp * 4u, 256u) * 256u;
+    if (shape.splits > 1u) bytes += static_cast<std::uint64_t>(shape.splits) * m * n * 4u;
+    return bytes;
+}
+
+hipError_t launch_prefill_linear(const TilePlanes& p, const float* x, const float* bias, float* y, std::uint32_t m,
+                                 const PrefillShape& shape, void* workspace, hipStream_t stream) {
+    const std::uint64_t mp = prefill_rows_padded(m);
+    const std::uint64_t ldx = prefill_ldx(p.k);
+    auto* base = static_cast<std::uint8_t*>(workspace);
+    auto* xh = reinterpret_cast<_Float16*>(base);
+    base += ceil_div(mp * ldx * 2u, 256u) * 256u;
+    auto* row_inv = reinterpret_cast<float*>(base);
+    base += ceil_div(mp * 4u, 256u) * 256u;
+    auto* partials = reinterpret_cast<float*>(base);
+
+    hipLaunchKernelGGL(prefill_activations_kernel, dim3(static_cast<unsigned>(mp)), dim3(kThreads), 0, stream, x, m,
+                       p.k, ldx, xh, row_inv);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+
+    GemmArgs a{};
+    a.codes = p.codes;
+    a.scales = p.scales;
+    a.nt = p.nt;
+    a.kt = p.kt;
+    a.n = p.n;
+    a.xh = xh;
+    a.ldx = ldx;
+    a.row_inv = row_inv;
+    a.w_scale = p.prefill_scale;
+    a.w_unscale = p.prefill_unscale;
+    a.m = m;
+    a.m_tiles = shape.m_tiles;
+    a.groups = shape.groups;
+    a.steps = shape.steps;
+    a.steps_per_split = shape.steps_per_split;
+    const bool split = shape.splits > 1u;
+    a.partial = split ? 1u : 0u;
+    a.bias = split ? nullptr : bias;
+    a.out = split ? partials : y;
+    const std::uint32_t blocks = shape.m_tiles * shape.groups * shape.splits;
+    switch (p.type) {
+    case kQ8_0: err = launch_gemm_fmt<kQ8_0>(a, shape.tile_m, shape.tile_n, blocks, stream); break;
+    case kQ4_0: err = launch_gemm_fmt<kQ4_0>(a, shape.tile_m, shape.tile_n, blocks, stream); break;
+    case kQ4_K: err = launch_gemm_fmt<kQ4_K>(a, shape.tile_m, shape.tile_n, blocks, stream); break;
+    default: return hipErrorInvalidValue;
+    }
+    if (err != hipSuccess || !split) return err;
+    const std::uint64_t total = static_cast<std::uint64_t>(m) * p.n;
+    const std::uint64_t grid = ceil_div(total, kThreads);
+    hipLaunchKernelGGL(prefill_reduce_kernel, dim3(static_cast<unsigned>(grid < 8192u ? grid : 8192u)), dim3(kThreads),
+                       0, stream, partials, shape.splits, m, p.n, bias, y);
+    return hipGetLastError();
+}
+
+hipError_t compute_prefill_scale(TilePlanes& p, std::uint32_t* bound_scratch, hipStream_t stream) {
+    const auto geo = geometry_of(p.type);
+    const std::uint64_t tiles = static_cast<std::uint64_t>(p.nt) * p.kt;
+    // Scale entries: f16 per block (Q8_0, Q4_0), one 16-byte header per super-block (Q4_K).
+    const std::uint64_t entries = p.type == kQ4_K ? tiles * 16u : tiles * (geo.scale_tile_bytes / 2u);
+    hipError_t err = hipMemsetAsync(bound_scratch, 0, sizeof(std::uint32_t), stream);
+    if (err != hipSuccess) return err;
+    const std::uint64_t grid = ceil_div(entries, kThreads);
+    hipLaunchKernelGGL(prefill_bound_kernel, dim3(static_cast<unsigned>(grid < 4096u ? grid : 4096u)), dim3(kThreads),
+                       0, stream, p.type, p.scales, entries, bound_scratch);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    std::uint32_t bits = 0;
+    err = hipMemcpyAsync(&bits, bound_scratch, sizeof(bits), hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(stream);
+    if (err != hipSuccess) return err;
+    float bound;
+    std::memcpy(&bound, &bits, sizeof(bound));
+    p.prefill_scale = 1.0f;
+    p.prefill_unscale = 1.0f;
+    if (bound > 0.0f && bound < 3.0e38f) {
+        // e = smallest integer with bound * 2^-e <= 2^15
+        int e = 0;
+        (void)std::frexp(bound, &e);          // bound = f * 2^e, f in [0.5, 1)
+        e -= 15;                              // bound * 2^-e < 2^15
+        e = e < -100 ? -100 : (e > 100 ? 100 : e);
+        p.prefill_scale = std::ldexp(1.0f, -e);
+        p.prefill_unscale = std::ldexp(1.0f, e);
+    }
+    return hipSuccess;
+}
+
+} // namespace air_hip

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define AIR_HIP_ABI_VERSION 1
+#define AIR_HIP_ABI_VERSION 2
 
 /* Mirrors air::ErrorCode (include/air/status.hpp:8-17). */
 typedef enum air_hip_status {
@@ -60,8 +60,10 @@ enum {
  *           scale epilogue.  M = 1..64.  Relative L2 error vs the double
  *           oracle ~1e-6 (gate 1e-4).  Replaces specialized_matvec_kernel /
  *           specialized_matmul_batch_reuse_kernel (cuda_backend.cu:501-606).
- *   PREFILL weights dequantised to f16, activations rounded to f16, f16
- *           MFMA with f32 accumulation for prefill-sized M (gate 1e-2).
+ *   PREFILL weights dequantised to f16 in registers (exact codes times an
+ *           f16 block scale), activations rounded to f16 after a per-row
+ *           power-of-two scale, f16 MFMA with f32 accumulation, for
+ *           prefill-sized M (any M >= 1; gate 1e-2, measured ~3e-4).
  *           Replaces the dense-f32 dequantise + GEMM tactic
  *           (cuda_backend.cu:375-382,1971-1992).
  *   AUTO    DECODE for M <= 64, PREFILL above. */
@@ -122,10 +124,11 @@ int air_hip_mem_info(int device, uint64_t* free_bytes, uint64_t* total_bytes);
 int air_hip_context_create(int device, void* stream, air_hip_context** out);
 int air_hip_context_destroy(air_hip_context* ctx);
 int air_hip_context_set_stream(air_hip_context* ctx, void* stream);
-/* Grows the workspace so linears with input width <= max_k and up to max_m
+/* Grows the workspaces so linears with input width <= max_k and up to max_m
  * rows never allocate on the hot path (workspace sizing,
- * cuda_backend.cu:1825-1869).  Without it the first call that needs more
- * space allocates. */
+ * cuda_backend.cu:1825-1869); the f32 partials of a K-split prefill GEMM,
+ * which depend on the output width, are sized by the first call that needs
+ * them.  Without it the first call that needs more space allocates. */
 int air_hip_context_reserve(air_hip_context* ctx, uint64_t max_k, uint32_t max_m);
 int air_hip_context_stats(const air_hip_context* ctx, air_hip_stats* out);
 /* Overrides the decode linear's launch shape for this context (autotuning):
@@ -136,6 +139,14 @@ int air_hip_context_stats(const air_hip_context* ctx, air_hip_stats* out);
  * clamped to its maximum. */
 int air_hip_context_set_tuning(air_hip_context* ctx, uint32_t rows_per_wave, uint32_t waves_per_group,
                                uint32_t k_splits);
+/* Overrides the prefill GEMM's launch shape for this context: tile_m =
+ * 16-row activation tiles per wavefront (4 or 8), tile_n = 16-row weight
+ * tiles per wavefront (2 or 4), k_splits = workgroups splitting K (1..64; a
+ * split sums its partials in a second, deterministic pass).  0 keeps the
+ * automatic choice.  No counterpart in the reference (its tactics have fixed
+ * shapes); it exists for autotuning sweeps. */
+int air_hip_context_set_prefill_tuning(air_hip_context* ctx, uint32_t tile_m, uint32_t tile_n,
+                                       uint32_t k_splits);
 
 /* ---- matrices ----------------------------------------------------------- */
 
@@ -177,7 +188,8 @@ int air_hip_activations_load(air_hip_context* ctx, const float* x, uint64_t k, u
 
 /* Stage 2: y[m][n] = sum_k w[n][k] * x[m][k] (+ bias[n]) over the activations
  * last loaded into ctx; the matrix input width must equal the loaded k.
- * Asynchronous on the context's stream. */
+ * Decode tactic only (PREFILL returns unsupported: it loads its own f16
+ * operand inside air_hip_linear).  Asynchronous on the context's stream. */
 int air_hip_linear_loaded(air_hip_context* ctx, const air_hip_matrix* matrix,
                           float* y, const float* bias, int tactic);
 

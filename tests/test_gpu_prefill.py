@@ -1,0 +1,158 @@
+"""GPU parity of the prefill tactic (f16 MFMA GEMM) against the CPU oracle.
+
+The prefill tactic rounds activations and dequantized weights to f16 and
+accumulates in f32, so it is held to relative L2 1e-2 of the double
+accumulating matvec (tensor_reader.cpp:369-394) plus the f32 bias add
+(reference_executor.cpp:315-323); the observed error is about 3e-4, and the
+tests also check that it stays below 2e-3 so a lost term cannot hide in the
+tolerance.  Shapes cover ragged N (not whole 16-row tiles), K that is not a
+whole 64/128/256-k tile, M that is not a whole activation tile, every
+compiled launch shape and K splits.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from air_amd import capi, quant
+from tests import helpers
+
+pytestmark = pytest.mark.gpu
+
+PREFILL_TOL = 1e-2      # gate for the MFMA path
+PREFILL_EXPECT = 2e-3   # what f16 rounding of both operands leaves (~3e-4)
+
+
+def _dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+def _run(torch, mat, x, n, m, bias=None, tactic=capi.LINEAR_PREFILL):
+    y = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+    mat.linear(_dev(torch, x), y, m, bias=None if bias is None else _dev(torch, bias), tactic=tactic)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+CASES = [
+    (capi.TYPE_Q8_0, 896, 4864, 65),     # config-0 shape
+    (capi.TYPE_Q8_0, 96, 37, 100),       # ragged N, K = 1.5 tiles
+    (capi.TYPE_Q8_0, 3584, 512, 257),    # M one past a 256-row multiple
+    (capi.TYPE_Q4_0, 160, 45, 70),       # K = 1.25 tiles
+    (capi.TYPE_Q4_0, 896, 640, 128),
+    (capi.TYPE_Q4_K, 256, 19, 66),
+    (capi.TYPE_Q4_K, 768, 200, 129),
+]
+
+
+@pytest.mark.parametrize("type_id,k,n,m", CASES)
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_prefill_matches_oracle(torch_cuda, hip_ctx, type_id, k, n, m, with_bias):
+    torch = torch_cuda
+    canon = helpers.weights(type_id, k, n, seed=3 * k + n + type_id)
+    mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    x = helpers.activations(m, k, seed=k + m)
+    bias = np.random.default_rng(n).standard_normal(n).astype(np.float32) * 0.02 if with_bias else None
+    want = oracle.linear(type_id, canon, k, n, x, bias=bias)
+    got = _run(torch, mat, x, n, m, bias)
+    assert np.isfinite(got).all()
+    err = helpers.rel_l2(got, want)
+    print(f"prefill type={type_id} k={k} n={n} m={m} bias={with_bias} rel_l2={err:.3e}")
+    assert err <= PREFILL_TOL
+    assert err <= PREFILL_EXPECT
+    # every row on its own, so a dropped row cannot hide in the total
+    for r in range(m):
+        assert helpers.rel_l2(got[r], want[r]) <= PREFILL_TOL, r
+    mat.release()
+
+
+@pytest.mark.parametrize("type_id,k,n", [
+    (capi.TYPE_Q8_0, 1024, 400), (capi.TYPE_Q4_0, 1024, 333), (capi.TYPE_Q4_K, 1280, 272)])
+def test_prefill_launch_shapes_agree(torch_cuda, hip_ctx, type_id, k, n):
+    """Every compiled tile shape and K split gives the oracle's answer; a
+    fixed shape is bit-reproducible."""
+    torch = torch_cuda
+    m = 150
+    canon = helpers.weights(type_id, k, n, seed=k * 5 + n)
+    mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    x = helpers.activations(m, k, seed=77)
+    bias = np.linspace(-1, 1, n, dtype=np.float32)
+    want = oracle.linear(type_id, canon, k, n, x, bias=bias)
+    try:
+        for tm in (4, 8):
+            for tn in (2, 4):
+                for splits in (1, 2, 3, 5):
+                    hip_ctx.set_prefill_tuning(tm, tn, splits)
+                    got = _run(torch, mat, x, n, m, bias)
+                    err = helpers.rel_l2(got, want)
+                    assert err <= PREFILL_EXPECT, (tm, tn, splits, err)
+                    again = _run(torch, mat, x, n, m, bias)
+                    assert helpers.same_bits(got, again), (tm, tn, splits)
+    finally:
+        hip_ctx.set_prefill_tuning(0, 0, 0)
+    mat.release()
+
+
+def test_prefill_scale_extremes(torch_cuda, hip_ctx):
+    """Per-row activation scaling and the per-matrix weight exponent keep f16
+    in range: huge and tiny activations, huge and tiny weights."""
+    torch = torch_cuda
+    k, n, m = 512, 96, 72
+    x = helpers.activations(m, k, seed=5)
+    x *= np.logspace(-8, 8, m, dtype=np.float32)[:, None]     # 1e-8 .. 1e8 per row
+    for wscale in (1e-3, 1.0, 4e3):
+        w = np.random.default_rng(9).standard_normal((n, k)).astype(np.float32) * 0.02 * wscale
+        for type_id in (capi.TYPE_Q8_0, capi.TYPE_Q4_0, capi.TYPE_Q4_K):
+            canon = quant.quantize(type_id, w).reshape(-1)
+            mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+            want = oracle.linear(type_id, canon, k, n, x)
+            got = _run(torch, mat, x, n, m)
+            assert np.isfinite(got).all(), (type_id, wscale)
+            for r in range(m):
+                assert helpers.rel_l2(got[r], want[r]) <= PREFILL_EXPECT, (type_id, wscale, r)
+            mat.release()
+
+
+def test_auto_routes_by_width(torch_cuda, hip_ctx):
+    """AUTO takes the decode tactic up to 64 rows and the prefill GEMM above."""
+    torch = torch_cuda
+    k, n = 512, 128
+    canon = helpers.weights(capi.TYPE_Q8_0, k, n, seed=2)
+    mat = capi.Matrix(hip_ctx, capi.TYPE_Q8_0, k, n, canon, canon.nbytes, on_device=False)
+    before = hip_ctx.stats()
+    _run(torch, mat, helpers.activations(64, k, 1), n, 64, tactic=capi.LINEAR_AUTO)
+    mid = hip_ctx.stats()
+    _run(torch, mat, helpers.activations(65, k, 1), n, 65, tactic=capi.LINEAR_AUTO)
+    after = hip_ctx.stats()
+    assert mid["decode_linear_calls"] == before["decode_linear_calls"] + 1
+    assert mid["prefill_linear_calls"] == before["prefill_linear_calls"]
+    assert after["prefill_linear_calls"] == mid["prefill_linear_calls"] + 1
+    assert after["prefill_rows"] == mid["prefill_rows"] + 65
+    # prefill on a decode-sized width is allowed and correct
+    x = helpers.activations(3, k, 4)
+    got = _run(torch, mat, x, n, 3)
+    assert helpers.rel_l2(got, oracle.linear(capi.TYPE_Q8_0, canon, k, n, x)) <= PREFILL_EXPECT
+    mat.release()
+
+
+def test_prefill_rejects_bad_arguments(torch_cuda, hip_ctx):
+    torch = torch_cuda
+    k, n = 64, 16
+    canon = helpers.weights(capi.TYPE_Q8_0, k, n, seed=1)
+    mat = capi.Matrix(hip_ctx, capi.TYPE_Q8_0, k, n, canon, canon.nbytes, on_device=False)
+    x = torch.zeros((5000, k), dtype=torch.float32, device="cuda:0")
+    y = torch.zeros((5000, n), dtype=torch.float32, device="cuda:0")
+    with pytest.raises(capi.HipError) as e:
+        mat.linear(x, y, 5000, tactic=capi.LINEAR_PREFILL)
+    assert e.value.status_name == "unsupported"
+    with pytest.raises(capi.HipError) as e:
+        mat.linear(x, y, 0, tactic=capi.LINEAR_PREFILL)
+    assert e.value.status_name == "invalid_argument"
+    with pytest.raises(capi.HipError) as e:
+        mat.linear_loaded(y, tactic=capi.LINEAR_PREFILL)
+    assert e.value.status_name == "unsupported"
+    with pytest.raises(capi.HipError) as e:
+        hip_ctx.set_prefill_tuning(3, 0, 0)
+    assert e.value.status_name == "invalid_argument"
+    mat.release()

@@ -68,7 +68,7 @@ def test_library_exports_every_declared_entry_point():
 
 def test_library_basics_without_device_work():
     lib = capi.lib()
-    assert lib.air_hip_abi_version() == 1
+    assert lib.air_hip_abi_version() == 2
     assert lib.air_hip_status_string(0) == b"ok"
     assert lib.air_hip_status_string(6) == b"unsupported"
     assert lib.air_hip_status_string(99) == b"unknown"
