@@ -88,10 +88,12 @@ struct PrefillTuning {
     std::uint32_t tile_m{0};   // 16-row activation tiles per wave: 4 or 8 (0 = automatic)
     std::uint32_t tile_n{0};   // 16-row weight tiles per wave: 2 or 4
     std::uint32_t k_splits{0}; // workgroups splitting K (0 = automatic)
+    std::uint32_t prefetch{0}; // weight prefetch distance in steps: 1 or 2 (8x4 tile only)
 };
 struct PrefillShape {
     std::uint32_t tile_m{8};
     std::uint32_t tile_n{4};
+    std::uint32_t prefetch{1};
     std::uint32_t m_tiles{0};
     std::uint32_t groups{0};
     std::uint32_t steps{0};

@@ -283,11 +283,14 @@ int air_hip_context_reserve(air_hip_context* ctx, uint64_t max_k, uint32_t max_m
     return ensure_prefill_workspace(ctx, prefill_workspace_bytes(max_k, max_m < kMaxRows ? max_m : kMaxRows, unsplit, 0));
 }
 
-int air_hip_context_set_prefill_tuning(air_hip_context* ctx, uint32_t tile_m, uint32_t tile_n, uint32_t k_splits) {
+int air_hip_context_set_prefill_tuning(air_hip_context* ctx, uint32_t tile_m, uint32_t tile_n, uint32_t k_splits,
+                                       uint32_t prefetch) {
     if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
     if (tile_m != 0 && tile_m != 4 && tile_m != 8) return fail(AIR_HIP_INVALID_ARGUMENT, "tile_m must be 0, 4 or 8");
     if (tile_n != 0 && tile_n != 2 && tile_n != 4) return fail(AIR_HIP_INVALID_ARGUMENT, "tile_n must be 0, 2 or 4");
     if (k_splits > 64) return fail(AIR_HIP_INVALID_ARGUMENT, "k_splits must be at most 64");
+    if (prefetch > 2) return fail(AIR_HIP_INVALID_ARGUMENT, "prefetch must be 0, 1 or 2");
+    ctx->prefill_tuning.prefetch = prefetch;
     ctx->prefill_tuning.tile_m = tile_m;
     ctx->prefill_tuning.tile_n = tile_n;
     ctx->prefill_tuning.k_splits = k_splits;

@@ -134,43 +134,35 @@ __device__ __forceinline__ _Float16 scaled_half(std::uint32_t bits, float w_scal
     return static_cast<_Float16>(v);
 }
 
-// f16 weights of the step's two 32-blocks (A fragments: row l%16, k 8(l/16)+e).
+// f16 weights of block b (0, 1) of the step (A fragment: row l%16, k 8(l/16)+e).
 template <int FMT>
-__device__ __forceinline__ void dequant_step(const StepCodes<FMT>& in, std::uint32_t s, float w_scale, half8v (&w)[2]) {
+__device__ __forceinline__ half8v dequant_block(const StepCodes<FMT>& in, std::uint32_t s, int b, float w_scale) {
+    half8v w;
     if constexpr (FMT == kQ8_0) {
-        const std::uint32_t cw[4] = {in.c.x, in.c.y, in.c.z, in.c.w};
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            half2v p0, p1, p2, p3;
-            q8_dword_to_half(cw[2 * b], p0, p1);
-            q8_dword_to_half(cw[2 * b + 1], p2, p3);
-            const _Float16 d = scaled_half((in.d >> (16 * b)) & 0xffffu, w_scale);
-            const half2v dd = {d, d};
-            p0 *= dd; p1 *= dd; p2 *= dd; p3 *= dd;
-            w[b][0] = p0[0]; w[b][1] = p0[1]; w[b][2] = p1[0]; w[b][3] = p1[1];
-            w[b][4] = p2[0]; w[b][5] = p2[1]; w[b][6] = p3[0]; w[b][7] = p3[1];
-        }
+        const std::uint32_t lo = b == 0 ? in.c.x : in.c.z;
+        const std::uint32_t hi = b == 0 ? in.c.y : in.c.w;
+        half2v p0, p1, p2, p3;
+        q8_dword_to_half(lo, p0, p1);
+        q8_dword_to_half(hi, p2, p3);
+        const _Float16 d = scaled_half((in.d >> (16 * b)) & 0xffffu, w_scale);
+        const half2v dd = {d, d};
+        p0 *= dd; p1 *= dd; p2 *= dd; p3 *= dd;
+        w[0] = p0[0]; w[1] = p0[1]; w[2] = p1[0]; w[3] = p1[1];
+        w[4] = p2[0]; w[5] = p2[1]; w[6] = p3[0]; w[7] = p3[1];
     } else if constexpr (FMT == kQ4_0) {
-        const std::uint32_t cw[2] = {in.c.x, in.c.y};
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            const _Float16 d = scaled_half((in.d >> (16 * b)) & 0xffffu, w_scale);
-            w[b] = nibble_dword_to_half8<8>(cw[b]) * d;
-        }
+        const _Float16 d = scaled_half((in.d >> (16 * b)) & 0xffffu, w_scale);
+        w = nibble_dword_to_half8<8>(b == 0 ? in.c.x : in.c.y) * d;
     } else {
-        const std::uint32_t cw[2] = {in.c.x, in.c.y};
         const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<std::uint16_t>(in.h.x & 0xffffu)));
         const float dmin = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<std::uint16_t>(in.h.x >> 16)));
         const std::uint32_t packed[3] = {in.h.y, in.h.z, in.h.w};
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            std::uint32_t sc = 0, mn = 0;
-            q4k_scale_min(packed, 2u * (s & 3u) + static_cast<std::uint32_t>(b), sc, mn);
-            const _Float16 a = static_cast<_Float16>(d * static_cast<float>(sc) * w_scale);
-            const _Float16 o = static_cast<_Float16>(dmin * static_cast<float>(mn) * w_scale);
-            w[b] = nibble_dword_to_half8<0>(cw[b]) * a - o;
-        }
+        std::uint32_t sc = 0, mn = 0;
+        q4k_scale_min(packed, 2u * (s & 3u) + static_cast<std::uint32_t>(b), sc, mn);
+        const _Float16 a = static_cast<_Float16>(d * static_cast<float>(sc) * w_scale);
+        const _Float16 o = static_cast<_Float16>(dmin * static_cast<float>(mn) * w_scale);
+        w = nibble_dword_to_half8<0>(b == 0 ? in.c.x : in.c.y) * a - o;
     }
+    return w;
 }
 
 // ---- 2. GEMM --------------------------------------------------------------
@@ -192,10 +184,14 @@ struct GemmArgs {
     std::uint32_t steps;         // 64-k steps of the padded k
     std::uint32_t steps_per_split;
     std::uint32_t partial;       // 1: write split partials (no bias)
+    std::uint32_t blocks;        // logical workgroups: m_tiles * groups * splits
 };
 
-template <int FMT, int TM, int TN>
-__global__ __launch_bounds__(kThreads, 2) void prefill_gemm_kernel(GemmArgs a) {
+// PF = how many steps ahead the weight codes are fetched (1 or 2).  The
+// largest register tile with PF = 2 runs at one wave per SIMD so that its
+// accumulators fit (VGPR + AGPR).
+template <int FMT, int TM, int TN, int PF>
+__global__ __launch_bounds__(kThreads, (TM * TN >= 32 && PF == 2) ? 1 : 2) void prefill_gemm_kernel(GemmArgs a) {
     constexpr unsigned BM = 16u * TM;
     constexpr unsigned kChunks = BM * (kStepK / 8u) / kThreads;  // 16-byte activation chunks per thread
     static_assert(kChunks * kThreads == BM * (kStepK / 8u), "activation tile must split evenly");
@@ -204,7 +200,12 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_gemm_kernel(GemmArgs a) {
     const std::uint32_t tid = threadIdx.x;
     const std::uint32_t lane = tid & 63u;
     const std::uint32_t wave = tid >> 6;
-    std::uint32_t bid = blockIdx.x;
+    // XCD-aware order: hardware hands workgroup i to XCD i % 8, so logical
+    // tiles are dealt in contiguous runs per XCD; the m-tiles of one weight
+    // group (the fastest logical index) then share that XCD's L2.
+    const std::uint32_t per_xcd = (a.blocks + 7u) / 8u;
+    std::uint32_t bid = (blockIdx.x & 7u) * per_xcd + (blockIdx.x >> 3);
+    if (bid >= a.blocks) return;
     const std::uint32_t mt = bid % a.m_tiles;
     bid /= a.m_tiles;
     const std::uint32_t group = bid % a.groups;
@@ -238,34 +239,29 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_gemm_kernel(GemmArgs a) {
             *reinterpret_cast<uint4*>(&xs[buf][row * kLdsStride + col]) = xr[j];
         }
     };
-    StepCodes<FMT> wr[TN];
-    const auto load_w = [&](std::uint32_t s) {
+    // Weight codes run PF steps ahead of the MFMAs: with PF = 2, while step
+    // s computes, the codes of s+1 are resident and those of s+2 in flight.
+    StepCodes<FMT> wa[TN], wb[TN];
+    const auto load_w = [&](StepCodes<FMT>(&dst)[TN], std::uint32_t s) {
 #pragma unroll
         for (int t = 0; t < TN; ++t) {
             const std::uint32_t rt = rt0 + static_cast<std::uint32_t>(t);
-            load_step<FMT>(a.codes, a.scales, rt, a.kt, s, lane, rt < a.nt, wr[t]);
+            load_step<FMT>(a.codes, a.scales, rt, a.kt, s, lane, rt < a.nt, dst[t]);
         }
     };
-
-    if (s_begin < s_end) {
-        load_x(s_begin);
-        load_w(s_begin);
-        store_x(0);
-    }
-    __syncthreads();
-    for (std::uint32_t s = s_begin; s < s_end; ++s) {
+    // One pipeline step over codes `cur`; refills `cur` with step s+PF once
+    // its last block is dequantized.
+    const auto step = [&](std::uint32_t s, StepCodes<FMT>(&cur)[TN]) {
         const unsigned buf = (s - s_begin) & 1u;
-        half8v w[TN][2];
-#pragma unroll
-        for (int t = 0; t < TN; ++t) dequant_step<FMT>(wr[t], s, a.w_scale, w[t]);
         const bool more = s + 1u < s_end;
-        if (more) {
-            load_x(s + 1u);
-            load_w(s + 1u);
-        }
+        if (more) load_x(s + 1u);
         const _Float16* xb = xs[buf];
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
+            half8v w[TN];
+#pragma unroll
+            for (int t = 0; t < TN; ++t) w[t] = dequant_block<FMT>(cur[t], s, b, a.w_scale);
+            if (b == 1 && s + PF < s_end) load_w(cur, s + PF);
             half8v xf[TM];
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
@@ -275,10 +271,28 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int t = 0; t < TN; ++t) acc[i][t] = mfma16x16x32(w[t][b], xf[i], acc[i][t]);
+                for (int t = 0; t < TN; ++t) acc[i][t] = mfma16x16x32(w[t], xf[i], acc[i][t]);
         }
         if (more) store_x(buf ^ 1u);
         __syncthreads();
+    };
+
+    if (s_begin < s_end) {
+        load_x(s_begin);
+        load_w(wa, s_begin);
+        if (PF == 2 && s_begin + 1u < s_end) load_w(wb, s_begin + 1u);
+        store_x(0);
+    }
+    __syncthreads();
+    if constexpr (PF == 2) {
+        std::uint32_t s = s_begin;
+        for (; s + 1u < s_end; s += 2u) {
+            step(s, wa);
+            step(s + 1u, wb);
+        }
+        if (s < s_end) step(s, wa);
+    } else {
+        for (std::uint32_t s = s_begin; s < s_end; ++s) step(s, wa);
     }
 
     // D[row = weight row][col = activation row]: lane holds rows 4(l/16)+r of column l%16.
@@ -354,17 +368,18 @@ __global__ __launch_bounds__(kThreads) void prefill_bound_kernel(int type, const
 }
 
 template <int FMT>
-hipError_t launch_gemm_fmt(const GemmArgs& args, std::uint32_t tm, std::uint32_t tn, std::uint32_t blocks,
-                           hipStream_t stream) {
+hipError_t launch_gemm_fmt(const GemmArgs& args, const PrefillShape& shape, std::uint32_t blocks, hipStream_t stream) {
     const dim3 grid(blocks), block(kThreads);
+    const std::uint32_t tm = shape.tile_m, tn = shape.tile_n, pf = shape.prefetch;
     if (tm == 8 && tn == 4) {
-        hipLaunchKernelGGL((prefill_gemm_kernel<FMT, 8, 4>), grid, block, 0, stream, args);
+        if (pf == 2) hipLaunchKernelGGL((prefill_gemm_kernel<FMT, 8, 4, 2>), grid, block, 0, stream, args);
+        else hipLaunchKernelGGL((prefill_gemm_kernel<FMT, 8, 4, 1>), grid, block, 0, stream, args);
     } else if (tm == 8 && tn == 2) {
-        hipLaunchKernelGGL((prefill_gemm_kernel<FMT, 8, 2>), grid, block, 0, stream, args);
+        hipLaunchKernelGGL((prefill_gemm_kernel<FMT, 8, 2, 2>), grid, block, 0, stream, args);
     } else if (tm == 4 && tn == 4) {
-        hipLaunchKernelGGL((prefill_gemm_kernel<FMT, 4, 4>), grid, block, 0, stream, args);
+        hipLaunchKernelGGL((prefill_gemm_kernel<FMT, 4, 4, 2>), grid, block, 0, stream, args);
     } else {
-        hipLaunchKernelGGL((prefill_gemm_kernel<FMT, 4, 2>), grid, block, 0, stream, args);
+        hipLaunchKernelGGL((prefill_gemm_kernel<FMT, 4, 2, 2>), grid, block, 0, stream, args);
     }
     return hipGetLastError();
 }
@@ -373,9 +388,18 @@ hipError_t launch_gemm_fmt(const GemmArgs& args, std::uint32_t tm, std::uint32_t
 
 PrefillShape plan_prefill(const TilePlanes& p, std::uint32_t m, const PrefillTuning& tuning) {
     PrefillShape s;
-    // Register tile per wave: TM x TN MFMA tiles (16 x 16 each).
+    // Register tile per wave: TM x TN MFMA tiles (16 x 16 each).  Measured on
+    // the Qwen2-7B shapes at M = 512: long K (down, K = 18944) runs best on
+    // the 8x4 tile with one step of prefetch and a K split; the rest on the
+    // 4x4 tile with two steps of prefetch.
+    const bool long_k = p.k >= 8192u;
+    s.tile_m = long_k ? 8u : 4u;
+    s.tile_n = 4u;
+    s.prefetch = long_k ? 1u : 2u;
     if (tuning.tile_m == 4 || tuning.tile_m == 8) s.tile_m = tuning.tile_m;
     if (tuning.tile_n == 2 || tuning.tile_n == 4) s.tile_n = tuning.tile_n;
+    if (tuning.prefetch == 1 || tuning.prefetch == 2) s.prefetch = tuning.prefetch;
+    if (s.tile_m != 8 || s.tile_n != 4) s.prefetch = 2;
     const std::uint32_t bm = 16u * s.tile_m;
     s.m_tiles = static_cast<std::uint32_t>(ceil_div(m, bm));
     s.groups = static_cast<std::uint32_t>(ceil_div(p.nt, 4u * s.tile_n));
@@ -440,11 +464,12 @@ hipError_t launch_prefill_linear(const TilePlanes& p, const float* x, const floa
     a.partial = split ? 1u : 0u;
     a.bias = split ? nullptr : bias;
     a.out = split ? partials : y;
-    const std::uint32_t blocks = shape.m_tiles * shape.groups * shape.splits;
+    a.blocks = shape.m_tiles * shape.groups * shape.splits;
+    const std::uint32_t blocks = (a.blocks + 7u) / 8u * 8u;  // whole rounds of the eight XCDs
     switch (p.type) {
-    case kQ8_0: err = launch_gemm_fmt<kQ8_0>(a, shape.tile_m, shape.tile_n, blocks, stream); break;
-    case kQ4_0: err = launch_gemm_fmt<kQ4_0>(a, shape.tile_m, shape.tile_n, blocks, stream); break;
-    case kQ4_K: err = launch_gemm_fmt<kQ4_K>(a, shape.tile_m, shape.tile_n, blocks, stream); break;
+    case kQ8_0: err = launch_gemm_fmt<kQ8_0>(a, shape, blocks, stream); break;
+    case kQ4_0: err = launch_gemm_fmt<kQ4_0>(a, shape, blocks, stream); break;
+    case kQ4_K: err = launch_gemm_fmt<kQ4_K>(a, shape, blocks, stream); break;
     default: return hipErrorInvalidValue;
     }
     if (err != hipSuccess || !split) return err;

@@ -80,8 +80,8 @@ public:
 
     // Linear engine.  x: device f32 [rows x K], y: device f32 [rows x N], both
     // row-major; the role's bias (if any) is fused.  Asynchronous on the
-    // engine's stream.  The tactic must be one this backend advertises for
-    // some scope (hip-decode, hip-prefill).
+    // engine's stream.  Tactics: hip-decode (exact codes, M <= 64 in
+    // practice), hip-prefill (f16 MFMA GEMM, M up to 4096).
     [[nodiscard]] Status linear(std::uint32_t layer, LinearRole role, const float* x, float* y,
                                 std::uint32_t rows, QuantizedLinearExecutionKind tactic) const;
     [[nodiscard]] Result<HipLinearInfo> linear_info(std::uint32_t layer, LinearRole role) const;

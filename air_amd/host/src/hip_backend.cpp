@@ -73,10 +73,10 @@ HipPreparedModel::HipPreparedModel(std::shared_ptr<const ModelDefinition> model,
     capabilities_.sequence_checkpointing = false;
     capabilities_.exact_prefix_reuse = false;
     capabilities_.device_greedy_selection = false;
-    // One tactic per scope, each naming real device work: the exact-code
-    // decode linear serves every width; hip-prefill is advertised only when
-    // the library provides it.
-    capabilities_.prefill_block_quantized_linear = {QuantizedLinearExecutionKind::hip_decode};
+    // Tactics per scope, each naming real device work: the exact-code decode
+    // linear serves every width; the f16 MFMA GEMM serves prefill blocks.
+    capabilities_.prefill_block_quantized_linear = {QuantizedLinearExecutionKind::hip_decode,
+                                                    QuantizedLinearExecutionKind::hip_prefill};
     capabilities_.decode_block_quantized_linear = {QuantizedLinearExecutionKind::hip_decode};
     capabilities_.decode_output_quantized_linear = {QuantizedLinearExecutionKind::hip_decode};
 }

@@ -142,11 +142,12 @@ int air_hip_context_set_tuning(air_hip_context* ctx, uint32_t rows_per_wave, uin
 /* Overrides the prefill GEMM's launch shape for this context: tile_m =
  * 16-row activation tiles per wavefront (4 or 8), tile_n = 16-row weight
  * tiles per wavefront (2 or 4), k_splits = workgroups splitting K (1..64; a
- * split sums its partials in a second, deterministic pass).  0 keeps the
- * automatic choice.  No counterpart in the reference (its tactics have fixed
- * shapes); it exists for autotuning sweeps. */
+ * split sums its partials in a second, deterministic pass), prefetch = steps
+ * of weight codes in flight (1 or 2; only the 8x4 tile has both).  0 keeps
+ * the automatic choice.  No counterpart in the reference (its tactics have
+ * fixed shapes); it exists for autotuning sweeps. */
 int air_hip_context_set_prefill_tuning(air_hip_context* ctx, uint32_t tile_m, uint32_t tile_n,
-                                       uint32_t k_splits);
+                                       uint32_t k_splits, uint32_t prefetch);
 
 /* ---- matrices ----------------------------------------------------------- */
 

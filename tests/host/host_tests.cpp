@@ -591,7 +591,11 @@ std::vector<float> oracle_parts(const air::ModelDefinition& model, const std::ve
 
 void gpu_check_role(const air::HipPreparedModel& prepared, std::uint32_t layer, air::LinearRole role,
                     const std::vector<std::string>& parts, const std::vector<std::string>& biases,
-                    std::uint32_t rows, const std::string& label) {
+                    std::uint32_t rows, const std::string& label,
+                    air::QuantizedLinearExecutionKind tactic = air::QuantizedLinearExecutionKind::hip_decode) {
+    // Decode: exact codes, rel-L2 1e-4.  Prefill: f16 operands, gate 1e-2
+    // (observed ~3e-4, held to 2e-3).
+    const double tol = tactic == air::QuantizedLinearExecutionKind::hip_prefill ? 2e-3 : 1e-4;
     const auto info = prepared.linear_info(layer, role);
     check(info.is_ok(), label + ": role resident");
     if (!info) return;
@@ -603,14 +607,14 @@ void gpu_check_role(const air::HipPreparedModel& prepared, std::uint32_t layer, 
     check(dx.ptr && dy.ptr, label + ": device buffers");
     if (!dx.ptr || !dy.ptr) return;
     (void)hipMemcpy(dx.ptr, x.data(), x.size() * sizeof(float), hipMemcpyHostToDevice);
-    const auto s = prepared.linear(layer, role, dx.ptr, dy.ptr, rows, air::QuantizedLinearExecutionKind::hip_decode);
+    const auto s = prepared.linear(layer, role, dx.ptr, dy.ptr, rows, tactic);
     check(s.is_ok(), label + ": linear launches (" + s.message() + ")");
     check(prepared.synchronize().is_ok(), label + ": synchronize");
     std::vector<float> y(static_cast<std::size_t>(rows) * n);
     (void)hipMemcpy(y.data(), dy.ptr, y.size() * sizeof(float), hipMemcpyDeviceToHost);
     const auto want = oracle_parts(prepared.model(), parts, biases, x, rows);
     const double err = rel_l2(y, want);
-    check(err <= 1e-4, label + ": rel-L2 " + std::to_string(err) + " > 1e-4");
+    check(err <= tol, label + ": rel-L2 " + std::to_string(err) + " > " + std::to_string(tol));
     std::cout << "  " << label << " rows=" << rows << " k=" << k << " n=" << n << " rel_l2=" << err << '\n';
 }
 
@@ -656,6 +660,21 @@ void gpu_model_case(std::uint32_t format, bool fuse, bool tied, bool output_bias
         gpu_check_role(p, 0, air::LinearRole::output, {tied ? "token_embd.weight" : "output.weight"},
                        {output_bias ? "output.bias" : ""}, rows, tag + " output");
     }
+    // Prefill widths on the MFMA GEMM.
+    for (std::uint32_t rows : {65U, 200U}) {
+        const auto n = [](const char* s) { return air::block_tensor_name(1, s); };
+        const auto prefill = air::QuantizedLinearExecutionKind::hip_prefill;
+        if (fuse) {
+            gpu_check_role(p, 1, air::LinearRole::attn_qkv, {n("attn_q.weight"), n("attn_k.weight"), n("attn_v.weight")},
+                           {n("attn_q.bias"), n("attn_k.bias"), n("attn_v.bias")}, rows, tag + " prefill qkv", prefill);
+            gpu_check_role(p, 1, air::LinearRole::ffn_gate_up, {n("ffn_gate.weight"), n("ffn_up.weight")}, {}, rows,
+                           tag + " prefill gate_up", prefill);
+        } else {
+            gpu_check_role(p, 1, air::LinearRole::attn_v, {n("attn_v.weight")}, {n("attn_v.bias")}, rows,
+                           tag + " prefill v", prefill);
+        }
+        gpu_check_role(p, 1, air::LinearRole::ffn_down, {n("ffn_down.weight")}, {}, rows, tag + " prefill down", prefill);
+    }
     // Roles that are not resident under this residency are refused.
     DeviceBuffer dummy(16);
     const auto wrong = p.linear(0, fuse ? air::LinearRole::attn_q : air::LinearRole::attn_qkv, dummy.ptr, dummy.ptr, 1,
@@ -680,6 +699,14 @@ void gpu_prepared_model_contract() {
     auto& p = *prepared.value();
     check(p.backend() == air::BackendKind::hip && p.capabilities().backend == air::BackendKind::hip, "backend hip");
     check(p.capabilities().max_decode_batch_width == 64U, "decode width 64 advertised");
+    {
+        auto prefill_plan = paged_plan();
+        prefill_plan.linear = {air::QuantizedLinearExecutionKind::hip_prefill, air::QuantizedLinearExecutionKind::hip_decode,
+                               air::QuantizedLinearExecutionKind::hip_decode};
+        check(air::validate_execution_plan(prefill_plan, p.capabilities()).is_ok(), "hip-prefill blocks validate");
+        prefill_plan.linear.decode_output = air::QuantizedLinearExecutionKind::hip_prefill;
+        check(!air::validate_execution_plan(prefill_plan, p.capabilities()), "hip-prefill is not a vocabulary tactic");
+    }
     const auto free = p.free_device_bytes();
     const auto capacity = p.sequence_capacity_bytes();
     check(free && *free > (1ULL << 30) && capacity && *capacity >= *free, "capacity from hipMemGetInfo");

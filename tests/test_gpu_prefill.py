@@ -80,17 +80,16 @@ def test_prefill_launch_shapes_agree(torch_cuda, hip_ctx, type_id, k, n):
     bias = np.linspace(-1, 1, n, dtype=np.float32)
     want = oracle.linear(type_id, canon, k, n, x, bias=bias)
     try:
-        for tm in (4, 8):
-            for tn in (2, 4):
+        for tm, tn, pf in ((4, 2, 2), (4, 4, 2), (8, 2, 2), (8, 4, 1), (8, 4, 2)):
                 for splits in (1, 2, 3, 5):
-                    hip_ctx.set_prefill_tuning(tm, tn, splits)
+                    hip_ctx.set_prefill_tuning(tm, tn, splits, pf)
                     got = _run(torch, mat, x, n, m, bias)
                     err = helpers.rel_l2(got, want)
-                    assert err <= PREFILL_EXPECT, (tm, tn, splits, err)
+                    assert err <= PREFILL_EXPECT, (tm, tn, pf, splits, err)
                     again = _run(torch, mat, x, n, m, bias)
-                    assert helpers.same_bits(got, again), (tm, tn, splits)
+                    assert helpers.same_bits(got, again), (tm, tn, pf, splits)
     finally:
-        hip_ctx.set_prefill_tuning(0, 0, 0)
+        hip_ctx.set_prefill_tuning(0, 0, 0, 0)
     mat.release()
 
 
@@ -153,6 +152,6 @@ def test_prefill_rejects_bad_arguments(torch_cuda, hip_ctx):
         mat.linear_loaded(y, tactic=capi.LINEAR_PREFILL)
     assert e.value.status_name == "unsupported"
     with pytest.raises(capi.HipError) as e:
-        hip_ctx.set_prefill_tuning(3, 0, 0)
+        hip_ctx.set_prefill_tuning(3, 0, 0, 0)
     assert e.value.status_name == "invalid_argument"
     mat.release()
