@@ -81,6 +81,7 @@ SIGNATURES = {
     "air_hip_context_stats": (_I, [_P, ctypes.POINTER(Stats)]),
     "air_hip_context_set_tuning": (_I, [_P, _U32, _U32, _U32]),
     "air_hip_context_set_prefill_tuning": (_I, [_P, _U32, _U32, _U32, _U32]),
+    "air_hip_context_set_decode_path": (_I, [_P, _U32, _U32, _U32]),
     "air_hip_canonical_bytes": (_U64, [_I, _U64, _U64]),
     "air_hip_matrix_prepare": (_I, [_P, _I, _U64, _U64, _P, _U64, _I, ctypes.POINTER(_P)]),
     "air_hip_matrix_release": (_I, [_P]),
@@ -173,6 +174,9 @@ class Context:
 
     def set_tuning(self, rows_per_wave: int = 0, waves_per_group: int = 0, k_splits: int = 0) -> None:
         check(lib().air_hip_context_set_tuning(self.handle, rows_per_wave, waves_per_group, k_splits))
+
+    def set_decode_path(self, path: int = 0, tile_n: int = 0, k_splits: int = 0) -> None:
+        check(lib().air_hip_context_set_decode_path(self.handle, path, tile_n, k_splits))
 
     def set_prefill_tuning(self, tile_m: int = 0, tile_n: int = 0, k_splits: int = 0, prefetch: int = 0) -> None:
         check(lib().air_hip_context_set_prefill_tuning(self.handle, tile_m, tile_n, k_splits, prefetch))

@@ -11,6 +11,11 @@ namespace air_hip {
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+// Native 128/64-bit integer vectors for staging registers: HIP's uint4 is a
+// struct whose copies become memcpys, which can pin an array of them in
+// scratch memory; these stay in VGPRs.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
 // Exact IEEE half -> single from the bit pattern, integer-only so NaN
 // payloads and subnormals decode exactly as src/reference/tensor_reader.cpp:11-36.

@@ -106,6 +106,32 @@ PrefillShape plan_prefill(const TilePlanes& planes, std::uint32_t m, const Prefi
 std::uint64_t prefill_workspace_bytes(std::uint64_t k, std::uint32_t m, const PrefillShape& shape, std::uint64_t n);
 hipError_t launch_prefill_linear(const TilePlanes& planes, const float* x, const float* bias, float* y,
                                  std::uint32_t m, const PrefillShape& shape, void* workspace, hipStream_t stream);
+// y[m][n] = sum over splits of partials[s][m][n] (in split order) + bias[n].
+hipError_t launch_split_reduce(const float* partials, std::uint32_t splits, std::uint32_t m, std::uint64_t n,
+                               const float* bias, float* y, hipStream_t stream);
+
+// Activation split for the skinny kernel: the same hi/lo tile layout, but one
+// power-of-two scale per row (inv_scale[m], m < mp) and block sums of the
+// scaled values (block_sums[b][m]).
+hipError_t launch_split_activations_rows(const float* x, std::uint32_t m, std::uint64_t k, std::uint64_t kp,
+                                         const SplitWorkspace& ws, hipStream_t stream);
+
+// Skinny decode linear (M = 1..64) over split activations: activations staged
+// once per workgroup in LDS, exact weight codes streamed per wave, optional K
+// split with a deterministic reduction.
+struct SkinnyShape {
+    std::uint32_t mt{1};       // 16-row activation tiles (all M rows)
+    std::uint32_t tile_n{1};   // 16-row weight tiles per wave (1 or 2)
+    std::uint32_t groups{0};
+    std::uint32_t steps{0};
+    std::uint32_t steps_per_split{0};
+    std::uint32_t splits{1};
+};
+SkinnyShape plan_skinny(const TilePlanes& planes, std::uint32_t m, std::uint32_t tile_n, std::uint32_t k_splits);
+std::uint64_t skinny_partials_bytes(const SkinnyShape& shape, std::uint32_t m, std::uint64_t n);
+hipError_t launch_skinny_linear(const TilePlanes& planes, const SplitWorkspace& ws, const float* bias, float* y,
+                                std::uint32_t m, const SkinnyShape& shape, float* partials, hipStream_t stream);
+
 // Sets planes.prefill_scale / prefill_unscale from the largest dequantized
 // magnitude of the resident matrix (synchronous; `bound_scratch` is one
 // device uint32).

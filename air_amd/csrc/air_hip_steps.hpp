@@ -1,0 +1,99 @@
+// air_hip_steps.hpp -- per-lane weight codes of one 64-k step (internal).
+//
+// The GEMM-shaped kernels (prefill, skinny decode) walk K in steps of 64
+// (two 32-element blocks) whatever the format's resident tile width: a Q8_0
+// tile is one step, a Q4_0 tile two, a Q4_K super-block four.  A lane's
+// share of one step of one 16-row tile is its code words plus the scales of
+// its row; padded row tiles (rt >= nt) read as codes that decode to zero.
+#pragma once
+
+#include "air_hip_device.hpp"
+
+namespace air_hip {
+
+constexpr unsigned kStepK = 64;
+
+template <int FMT>
+struct StepCodes;
+
+template <>
+struct StepCodes<kQ8_0> {
+    u32x4 c;               // bytes of blocks 2kt, 2kt+1
+    std::uint32_t d;       // two f16 scales
+};
+template <>
+struct StepCodes<kQ4_0> {
+    u32x2 c;               // dwords of blocks 2hs, 2hs+1 of the 128-k tile
+    std::uint32_t d;       // their two f16 scales
+};
+template <>
+struct StepCodes<kQ4_K> {
+    u32x2 c;               // dwords of sub-blocks 2sub, 2sub+1
+    u32x4 h;               // the 16-byte super-block header of the lane's row
+};
+
+template <int FMT>
+__device__ __forceinline__ void load_step(const void* codes, const void* scales, std::uint32_t rt, std::uint32_t kt_count,
+                                          std::uint32_t s, std::uint32_t lane, bool live, StepCodes<FMT>& out) {
+    if constexpr (FMT == kQ8_0) {
+        if (!live) { out.c = u32x4{0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u}; out.d = 0u; return; }
+        const std::uint64_t tile = static_cast<std::uint64_t>(rt) * kt_count + s;
+        out.c = static_cast<const u32x4*>(codes)[tile * 64u + lane];
+        out.d = static_cast<const std::uint32_t*>(scales)[tile * 16u + (lane & 15u)];
+    } else if constexpr (FMT == kQ4_0) {
+        if (!live) { out.c = u32x2{0x88888888u, 0x88888888u}; out.d = 0u; return; }
+        const std::uint64_t tile = static_cast<std::uint64_t>(rt) * kt_count + (s >> 1);
+        const u32x2* rec = static_cast<const u32x2*>(codes) + (tile * 64u + lane) * 2u + (s & 1u);
+        out.c = *rec;
+        out.d = static_cast<const std::uint32_t*>(scales)[(tile * 16u + (lane & 15u)) * 2u + (s & 1u)];
+    } else {
+        if (!live) { out.c = u32x2{0u, 0u}; out.h = u32x4{0u, 0u, 0u, 0u}; return; }
+        const std::uint64_t tile = static_cast<std::uint64_t>(rt) * kt_count + (s >> 2);
+        const std::uint32_t sub = s & 3u;
+        const u32x2* rec = static_cast<const u32x2*>(codes) + ((tile * 2u + (sub >> 1)) * 64u + lane) * 2u + (sub & 1u);
+        out.c = *rec;
+        out.h = static_cast<const u32x4*>(scales)[tile * 16u + (lane & 15u)];
+    }
+}
+
+// Exact codes of block b (0, 1) of the step as f16 operand fragments
+// (lane: row l%16, k 8(l/16)+e): Q8_0 q, Q4_0 n-8, Q4_K n.
+template <int FMT>
+__device__ __forceinline__ half8v step_codes(const StepCodes<FMT>& in, int b) {
+    if constexpr (FMT == kQ8_0) {
+        half2v p0, p1, p2, p3;
+        q8_dword_to_half(b == 0 ? in.c.x : in.c.z, p0, p1);
+        q8_dword_to_half(b == 0 ? in.c.y : in.c.w, p2, p3);
+        half8v w;
+        w[0] = p0[0]; w[1] = p0[1]; w[2] = p1[0]; w[3] = p1[1];
+        w[4] = p2[0]; w[5] = p2[1]; w[6] = p3[0]; w[7] = p3[1];
+        return w;
+    } else if constexpr (FMT == kQ4_0) {
+        return nibble_dword_to_half8<8>(b == 0 ? in.c.x : in.c.y);
+    } else {
+        return nibble_dword_to_half8<0>(b == 0 ? in.c.x : in.c.y);
+    }
+}
+
+__device__ __forceinline__ float f16_bits_value(std::uint32_t bits16) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<std::uint16_t>(bits16)));
+}
+
+// f32 factors of block b of step s for the lane's row: w = scale * code - offset
+// (offset is zero except for Q4_K, where scale = d*sc_j and offset = dmin*m_j).
+template <int FMT>
+__device__ __forceinline__ void step_scale(const StepCodes<FMT>& in, std::uint32_t s, int b, float& scale,
+                                           float& offset) {
+    if constexpr (FMT == kQ4_K) {
+        const std::uint32_t packed[3] = {in.h.y, in.h.z, in.h.w};
+        std::uint32_t sc = 0, mn = 0;
+        q4k_scale_min(packed, 2u * (s & 3u) + static_cast<std::uint32_t>(b), sc, mn);
+        scale = f16_bits_value(in.h.x & 0xffffu) * static_cast<float>(sc);
+        offset = f16_bits_value(in.h.x >> 16) * static_cast<float>(mn);
+    } else {
+        scale = f16_bits_value((in.d >> (16 * b)) & 0xffffu);
+        offset = 0.0f;
+    }
+}
+
+} // namespace air_hip

@@ -37,6 +37,7 @@ struct air_hip_context {
     std::atomic<std::uint64_t> prefill_rows{0};
     std::uint64_t loaded_k{0};       // width of the activations in the workspace
     std::uint32_t loaded_rows{0};    // rows of the activations in the workspace (0 = none)
+    bool loaded_row_scaled{false};   // split with one scale per row (skinny kernel layout)
     DecodeTuning tuning{};
     // Cross-workgroup K-split of the fused decode linear: partial sums and one
     // arrival counter per row group.  Counters are zeroed when allocated and
@@ -49,6 +50,11 @@ struct air_hip_context {
     void* prefill_workspace{nullptr};
     std::uint64_t prefill_workspace_bytes{0};
     PrefillTuning prefill_tuning{};
+    // Decode widths 2..64: 0 = automatic (skinny kernel), 1 = the earlier
+    // kernels (fused for M <= 16, decode_linear above), 2 = skinny.
+    std::uint32_t decode_path{0};
+    std::uint32_t skinny_tile_n{0};
+    std::uint32_t skinny_splits{0};
     std::uint32_t* bound_scratch{nullptr};  // one uint32 for the weight exponent at residency
 };
 
@@ -283,6 +289,17 @@ int air_hip_context_reserve(air_hip_context* ctx, uint64_t max_k, uint32_t max_m
     return ensure_prefill_workspace(ctx, prefill_workspace_bytes(max_k, max_m < kMaxRows ? max_m : kMaxRows, unsplit, 0));
 }
 
+int air_hip_context_set_decode_path(air_hip_context* ctx, uint32_t path, uint32_t tile_n, uint32_t k_splits) {
+    if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
+    if (path > 2u) return fail(AIR_HIP_INVALID_ARGUMENT, "path must be 0, 1 or 2");
+    if (tile_n > 2u) return fail(AIR_HIP_INVALID_ARGUMENT, "tile_n must be 0, 1 or 2");
+    if (k_splits > 64u) return fail(AIR_HIP_INVALID_ARGUMENT, "k_splits must be at most 64");
+    ctx->decode_path = path;
+    ctx->skinny_tile_n = tile_n;
+    ctx->skinny_splits = k_splits;
+    return AIR_HIP_OK;
+}
+
 int air_hip_context_set_prefill_tuning(air_hip_context* ctx, uint32_t tile_m, uint32_t tile_n, uint32_t k_splits,
                                        uint32_t prefetch) {
     if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
@@ -481,10 +498,15 @@ int air_hip_activations_load(air_hip_context* ctx, const float* x, uint64_t k, u
     int rc = ensure_workspace(ctx, split_workspace_bytes(kp, rows));
     if (rc != AIR_HIP_OK) return rc;
     const SplitWorkspace ws = carve_split_workspace(ctx->workspace, kp, rows);
-    const hipError_t err = launch_split_activations(x, rows, k, kp, ws, ctx->stream);
+    // The skinny kernel (M <= 64) takes one scale per row, the K-split
+    // kernel one per (row, block).
+    const bool row_scaled = rows <= AIR_HIP_MAX_DECODE_ROWS && ctx->decode_path != 1u;
+    const hipError_t err = row_scaled ? launch_split_activations_rows(x, rows, k, kp, ws, ctx->stream)
+                                      : launch_split_activations(x, rows, k, kp, ws, ctx->stream);
     if (err != hipSuccess) return hip_fail(err, "split_activations_kernel");
     ctx->loaded_k = k;
     ctx->loaded_rows = rows;
+    ctx->loaded_row_scaled = row_scaled;
     return AIR_HIP_OK;
 }
 
@@ -507,6 +529,24 @@ int air_hip_linear_loaded(air_hip_context* ctx, const air_hip_matrix* m, float* 
     const std::uint32_t rows = ctx->loaded_rows;
     const std::uint64_t kp = ceil_div(ctx->loaded_k, kSplitK) * kSplitK;
     const SplitWorkspace ws = carve_split_workspace(ctx->workspace, kp, rows);
+    const bool skinny = rows <= AIR_HIP_MAX_DECODE_ROWS && ctx->decode_path != 1u;
+    if (skinny != ctx->loaded_row_scaled) {
+        return fail(AIR_HIP_INVALID_STATE, "activations were loaded for another decode path; load them again");
+    }
+    if (skinny) {
+        const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits);
+        const std::uint64_t partial_bytes = skinny_partials_bytes(shape, rows, m->planes.n);
+        if (partial_bytes > 0u) {
+            const int rc = ensure_split_buffers(ctx, partial_bytes, 0u);
+            if (rc != AIR_HIP_OK) return rc;
+        }
+        const hipError_t err = launch_skinny_linear(m->planes, ws, bias, y, rows, shape,
+                                                    static_cast<float*>(ctx->split_partials), ctx->stream);
+        if (err != hipSuccess) return hip_fail(err, "skinny_kernel");
+        ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
+        ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
+        return AIR_HIP_OK;
+    }
     const hipError_t err = launch_decode_linear(m->planes, ws, bias, y, rows, ctx->tuning, ctx->stream);
     if (err != hipSuccess) return hip_fail(err, "decode_linear_kernel");
     ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
@@ -546,6 +586,18 @@ int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* m, const float* x
             ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
             ctx->decode_rows.fetch_add(1, std::memory_order_relaxed);
             return AIR_HIP_OK;
+        }
+        // Measured on the Qwen2-7B shapes (M = 2..16): the single-launch fused
+        // kernel wins for narrow matrices (N <= 4096, where the skinny
+        // kernel's three launches dominate) and for very large ones at M <= 4.
+        const std::uint64_t weight_bytes = static_cast<std::uint64_t>(m->planes.nt) * m->planes.kt *
+                                           geometry_of(m->planes.type).code_tile_bytes;
+        const bool prefer_fused = m->planes.n <= 4096u || (rows <= 4u && weight_bytes >= (256ull << 20));
+        if (ctx->decode_path == 2u || (ctx->decode_path == 0u && !prefer_fused)) {
+            // Split the activations once, then the skinny kernel.
+            int rc = air_hip_activations_load(ctx, x, m->planes.k, rows);
+            if (rc != AIR_HIP_OK) return rc;
+            return air_hip_linear_loaded(ctx, m, y, bias, AIR_HIP_LINEAR_DECODE);
         }
         const FusedShape shape = plan_decode_fused(m->planes, rows, ctx->tuning);
         if (shape.k_splits > 1u) {

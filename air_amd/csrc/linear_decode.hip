@@ -383,8 +383,9 @@ hipError_t launch_decode_linear(const TilePlanes& p, const SplitWorkspace& ws, c
     const std::uint64_t wgs = ceil_div(p.nt, R) * groups;
     while (W < w_cap && wgs * W < 8192u && p.kt >= 4u * W && (2u * W - 1u) * R * MT <= 64u) W <<= 1;
     if (tuning.waves_per_group != 0u) {
-        W = tuning.waves_per_group;
-        if (W > w_cap || (W - 1u) * R * MT > 63u) return hipErrorInvalidConfiguration;
+        // Clamped to what the variant is compiled for and to the LDS partials.
+        W = tuning.waves_per_group < w_cap ? tuning.waves_per_group : w_cap;
+        while (W > 1u && (W - 1u) * R * MT > 63u) --W;
     }
     switch (p.type) {
     case kQ8_0: return launch_fmt<kQ8_0>(p, ws, bias, y, m, R, MT, groups, W, stream);

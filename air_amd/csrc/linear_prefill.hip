@@ -26,6 +26,7 @@
 // acc * row_inv[m] * 2^e + bias[n].
 #include "air_hip_device.hpp"
 #include "air_hip_kernels.hpp"
+#include "air_hip_steps.hpp"
 
 #include <cmath>
 #include <cstring>
@@ -34,7 +35,6 @@ namespace air_hip {
 namespace {
 
 constexpr unsigned kThreads = 256;       // four waves
-constexpr unsigned kStepK = 64;          // k per pipeline step: two 32-blocks
 constexpr unsigned kLdsStride = kStepK + 8;  // halfs per staged activation row
 
 // ---- 1. activations ----------------------------------------------------
@@ -84,50 +84,6 @@ __global__ __launch_bounds__(kThreads) void prefill_activations_kernel(const flo
 }
 
 // ---- weight fragments -----------------------------------------------------
-
-// Raw codes and scales of one 64-k step of one 16-row tile, for one lane.
-template <int FMT>
-struct StepCodes;
-
-template <>
-struct StepCodes<kQ8_0> {
-    uint4 c;               // bytes of blocks 2kt, 2kt+1
-    std::uint32_t d;       // two f16 scales
-};
-template <>
-struct StepCodes<kQ4_0> {
-    uint2 c;               // dwords of blocks 2hs, 2hs+1 of the 128-k tile
-    std::uint32_t d;       // their two f16 scales
-};
-template <>
-struct StepCodes<kQ4_K> {
-    uint2 c;               // dwords of sub-blocks 2sub, 2sub+1
-    uint4 h;               // the 16-byte super-block header of the lane's row
-};
-
-template <int FMT>
-__device__ __forceinline__ void load_step(const void* codes, const void* scales, std::uint32_t rt, std::uint32_t kt_count,
-                                          std::uint32_t s, std::uint32_t lane, bool live, StepCodes<FMT>& out) {
-    if constexpr (FMT == kQ8_0) {
-        if (!live) { out.c = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u); out.d = 0u; return; }
-        const std::uint64_t tile = static_cast<std::uint64_t>(rt) * kt_count + s;
-        out.c = static_cast<const uint4*>(codes)[tile * 64u + lane];
-        out.d = static_cast<const std::uint32_t*>(scales)[tile * 16u + (lane & 15u)];
-    } else if constexpr (FMT == kQ4_0) {
-        if (!live) { out.c = make_uint2(0x88888888u, 0x88888888u); out.d = 0u; return; }
-        const std::uint64_t tile = static_cast<std::uint64_t>(rt) * kt_count + (s >> 1);
-        const uint2* rec = static_cast<const uint2*>(codes) + (tile * 64u + lane) * 2u + (s & 1u);
-        out.c = *rec;
-        out.d = static_cast<const std::uint32_t*>(scales)[(tile * 16u + (lane & 15u)) * 2u + (s & 1u)];
-    } else {
-        if (!live) { out.c = make_uint2(0u, 0u); out.h = make_uint4(0u, 0u, 0u, 0u); return; }
-        const std::uint64_t tile = static_cast<std::uint64_t>(rt) * kt_count + (s >> 2);
-        const std::uint32_t sub = s & 3u;
-        const uint2* rec = static_cast<const uint2*>(codes) + ((tile * 2u + (sub >> 1)) * 64u + lane) * 2u + (sub & 1u);
-        out.c = *rec;
-        out.h = static_cast<const uint4*>(scales)[tile * 16u + (lane & 15u)];
-    }
-}
 
 __device__ __forceinline__ _Float16 scaled_half(std::uint32_t bits, float w_scale) {
     const float v = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<std::uint16_t>(bits))) * w_scale;
@@ -221,28 +177,28 @@ __global__ __launch_bounds__(kThreads, (TM * TN >= 32 && PF == 2) ? 1 : 2) void 
 #pragma unroll
         for (int t = 0; t < TN; ++t) acc[i][t] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
-    uint4 xr[kChunks];
-    const auto load_x = [&](std::uint32_t s) {
+    u32x4 xr[kChunks];
+    const auto load_x = [&](std::uint32_t s) __attribute__((always_inline)) {
 #pragma unroll
         for (unsigned j = 0; j < kChunks; ++j) {
             const std::uint32_t c = tid + kThreads * j;
             const std::uint32_t row = c >> 3, col = (c & 7u) * 8u;
-            xr[j] = *reinterpret_cast<const uint4*>(a.xh + static_cast<std::uint64_t>(m0 + row) * a.ldx +
+            xr[j] = *reinterpret_cast<const u32x4*>(a.xh + static_cast<std::uint64_t>(m0 + row) * a.ldx +
                                                     static_cast<std::uint64_t>(s) * kStepK + col);
         }
     };
-    const auto store_x = [&](unsigned buf) {
+    const auto store_x = [&](unsigned buf) __attribute__((always_inline)) {
 #pragma unroll
         for (unsigned j = 0; j < kChunks; ++j) {
             const std::uint32_t c = tid + kThreads * j;
             const std::uint32_t row = c >> 3, col = (c & 7u) * 8u;
-            *reinterpret_cast<uint4*>(&xs[buf][row * kLdsStride + col]) = xr[j];
+            *reinterpret_cast<u32x4*>(&xs[buf][row * kLdsStride + col]) = xr[j];
         }
     };
     // Weight codes run PF steps ahead of the MFMAs: with PF = 2, while step
     // s computes, the codes of s+1 are resident and those of s+2 in flight.
     StepCodes<FMT> wa[TN], wb[TN];
-    const auto load_w = [&](StepCodes<FMT>(&dst)[TN], std::uint32_t s) {
+    const auto load_w = [&](StepCodes<FMT>(&dst)[TN], std::uint32_t s) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < TN; ++t) {
             const std::uint32_t rt = rt0 + static_cast<std::uint32_t>(t);
@@ -251,7 +207,7 @@ __global__ __launch_bounds__(kThreads, (TM * TN >= 32 && PF == 2) ? 1 : 2) void 
     };
     // One pipeline step over codes `cur`; refills `cur` with step s+PF once
     // its last block is dequantized.
-    const auto step = [&](std::uint32_t s, StepCodes<FMT>(&cur)[TN]) {
+    const auto step = [&](std::uint32_t s, StepCodes<FMT>(&cur)[TN]) __attribute__((always_inline)) {
         const unsigned buf = (s - s_begin) & 1u;
         const bool more = s + 1u < s_end;
         if (more) load_x(s + 1u);
@@ -473,10 +429,15 @@ hipError_t launch_prefill_linear(const TilePlanes& p, const float* x, const floa
     default: return hipErrorInvalidValue;
     }
     if (err != hipSuccess || !split) return err;
-    const std::uint64_t total = static_cast<std::uint64_t>(m) * p.n;
+    return launch_split_reduce(partials, shape.splits, m, p.n, bias, y, stream);
+}
+
+hipError_t launch_split_reduce(const float* partials, std::uint32_t splits, std::uint32_t m, std::uint64_t n,
+                               const float* bias, float* y, hipStream_t stream) {
+    const std::uint64_t total = static_cast<std::uint64_t>(m) * n;
     const std::uint64_t grid = ceil_div(total, kThreads);
     hipLaunchKernelGGL(prefill_reduce_kernel, dim3(static_cast<unsigned>(grid < 8192u ? grid : 8192u)), dim3(kThreads),
-                       0, stream, partials, shape.splits, m, p.n, bias, y);
+                       0, stream, partials, splits, m, n, bias, y);
     return hipGetLastError();
 }
 

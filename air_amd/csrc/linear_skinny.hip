@@ -1,0 +1,322 @@
+// linear_skinny.hip -- the decode linear for M = 2..64 rows on exact codes.
+//
+// Exact integer codes as f16 MFMA operands, activations split into f16 hi +
+// lo after one power-of-two scale per row (so the row's largest |x| lands in
+// [2^14, 2^15); every value above 2^-17 of it keeps ~22 significant bits),
+// per-block f32 weight-scale epilogue, the row scale undone once at the end;
+// relative L2 error ~1e-6.  Arranged so that the weights stream once:
+//
+//   * a workgroup is four waves that own 4 * TN distinct 16-row weight tiles
+//     and ALL activation rows (M <= 64: up to four 16-row tiles), so every
+//     weight byte is read exactly once per launch;
+//   * per 64-k step the split activations of the step (hi, lo, inverse
+//     scales, Q4_K block sums) are copied once into LDS by the whole
+//     workgroup and read by each wave once per 32-block, then reused for all
+//     of that wave's weight tiles;
+//   * each wave streams its own weight codes two steps ahead of the MFMAs;
+//   * when the weight tiles alone cannot occupy the 256 CUs, K is split over
+//     workgroups and the partials are summed by a second, fixed-order pass.
+//
+// Replaces specialized_matmul_kernel / specialized_matmul_batch_reuse_kernel
+// (src/cuda/cuda_backend.cu:501-583), which decode every weight M/4 or M/8
+// times.
+#include "air_hip_device.hpp"
+#include "air_hip_kernels.hpp"
+#include "air_hip_steps.hpp"
+
+namespace air_hip {
+namespace {
+
+constexpr unsigned kThreads = 256;
+constexpr unsigned kSplitThreads = 1024;  // one workgroup per activation row
+
+struct SkinnyArgs {
+    const void* codes;
+    const void* scales;
+    std::uint32_t nt, kt;
+    std::uint64_t n;
+    const uint4* xs;             // split activations [block][MT][2][64] x 16 B
+    const float* inv_scale;      // [mp] inverse power-of-two scale of each row
+    const float* block_sums;     // [block][mp] sums of the scaled values (Q4_K)
+    const float* bias;           // fused when not split
+    float* out;                  // y, or partials [splits][m][n]
+    std::uint32_t m;
+    std::uint32_t groups;
+    std::uint32_t steps;
+    std::uint32_t steps_per_split;
+    std::uint32_t partial;
+};
+
+template <int FMT, int MT, int TN>
+__global__ __launch_bounds__(kThreads, 2) void skinny_kernel(SkinnyArgs a) {
+    constexpr unsigned kMp = 16u * MT;
+    constexpr unsigned kChunks = 2u * MT * 2u * 64u / kThreads;  // uint4 of activations per thread per step
+    constexpr bool kSums = FMT == kQ4_K;
+    __shared__ u32x4 xa[2][2 * MT * 2 * 64];     // [buf][block][tile][part][lane]
+    __shared__ float4v sm[2][kSums ? 2 * kMp / 4 : 1];  // [buf][block][row] sums of scaled x (Q4_K)
+
+    const std::uint32_t tid = threadIdx.x;
+    const std::uint32_t lane = tid & 63u;
+    const std::uint32_t wave = tid >> 6;
+    const std::uint32_t group = blockIdx.x % a.groups;
+    const std::uint32_t split = blockIdx.x / a.groups;
+    const std::uint32_t rt0 = (group * 4u + wave) * TN;
+    const std::uint32_t s_begin = split * a.steps_per_split;
+    const std::uint32_t s_end = min(a.steps, s_begin + a.steps_per_split);
+
+    float4v acc[TN][MT];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[j][t] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Activation staging: step s covers blocks 2s, 2s+1, contiguous in the workspace.
+    u32x4 xr[kChunks];
+    float4v mr = {0.f, 0.f, 0.f, 0.f};
+    const auto load_x = [&](std::uint32_t s) __attribute__((always_inline)) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(a.xs) + static_cast<std::uint64_t>(s) * (2u * MT * 2u * 64u);
+#pragma unroll
+        for (unsigned j = 0; j < kChunks; ++j) xr[j] = src[tid + kThreads * j];
+        if constexpr (kSums) {
+            if (tid < 2u * kMp / 4u) mr = reinterpret_cast<const float4v*>(a.block_sums + static_cast<std::uint64_t>(s) * 2u * kMp)[tid];
+        }
+    };
+    const auto store_x = [&](unsigned buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (unsigned j = 0; j < kChunks; ++j) xa[buf][tid + kThreads * j] = xr[j];
+        if constexpr (kSums) {
+            if (tid < 2u * kMp / 4u) sm[buf][tid] = mr;
+        }
+    };
+    StepCodes<FMT> wa[TN], wb[TN];
+    const auto load_w = [&](StepCodes<FMT>(&dst)[TN], std::uint32_t s) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const std::uint32_t rt = rt0 + static_cast<std::uint32_t>(j);
+            load_step<FMT>(a.codes, a.scales, rt, a.kt, s, lane, rt < a.nt, dst[j]);
+        }
+    };
+    const auto step = [&](std::uint32_t s, StepCodes<FMT>(&cur)[TN]) __attribute__((always_inline)) {
+        const unsigned buf = (s - s_begin) & 1u;
+        const bool more = s + 1u < s_end;
+        if (more) load_x(s + 1u);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            half8v w[TN];
+            float ws[TN], wo[TN];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                w[j] = step_codes<FMT>(cur[j], b);
+                step_scale<FMT>(cur[j], s, b, ws[j], wo[j]);
+            }
+            if (b == 1 && s + 2u < s_end) load_w(cur, s + 2u);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const unsigned base = ((static_cast<unsigned>(b) * MT + t) * 2u) * 64u + lane;
+                const half8v hi = __builtin_bit_cast(half8v, xa[buf][base]);
+                const half8v lo = __builtin_bit_cast(half8v, xa[buf][base + 64u]);
+                float4v sum4 = {0.f, 0.f, 0.f, 0.f};
+                if constexpr (kSums) sum4 = sm[buf][(static_cast<unsigned>(b) * kMp + t * 16u) / 4u + (lane >> 4)];
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    float4v p = mfma16x16x32(hi, w[j], float4v{0.f, 0.f, 0.f, 0.f});
+                    p = mfma16x16x32(lo, w[j], p);
+                    acc[j][t] += ws[j] * p;
+                    if constexpr (kSums) acc[j][t] -= wo[j] * sum4;
+                }
+            }
+        }
+        if (more) store_x(buf ^ 1u);
+        __syncthreads();
+    };
+
+    if (s_begin < s_end) {
+        load_x(s_begin);
+        load_w(wa, s_begin);
+        if (s_begin + 1u < s_end) load_w(wb, s_begin + 1u);
+        store_x(0);
+    }
+    __syncthreads();
+    std::uint32_t s = s_begin;
+    for (; s + 1u < s_end; s += 2u) {
+        step(s, wa);
+        step(s + 1u, wb);
+    }
+    if (s < s_end) step(s, wa);
+
+    // D[row = activation row][col = weight row]: lane holds rows 4(l/16)+i of
+    // column l%16; the rows' power-of-two activation scales are undone here.
+    float4v inv[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) inv[t] = reinterpret_cast<const float4v*>(a.inv_scale)[t * 4 + (lane >> 4)];
+    float* out = a.out + (a.partial ? static_cast<std::uint64_t>(split) * a.m * a.n : 0u);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const std::uint64_t n = static_cast<std::uint64_t>(rt0 + static_cast<std::uint32_t>(j)) * 16u + (lane & 15u);
+        if (n >= a.n) continue;
+        const float bn = a.bias ? a.bias[n] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const std::uint32_t m = static_cast<std::uint32_t>(t) * 16u + 4u * (lane >> 4) + static_cast<std::uint32_t>(i);
+                if (m < a.m) out[static_cast<std::uint64_t>(m) * a.n + n] = acc[j][t][i] * inv[t][i] + bn;
+            }
+        }
+    }
+}
+
+// Row-scaled activation split: one workgroup per padded row.  Pass 1 finds
+// the row's max |x|; pass 2 writes the hi/lo fragments of every (block,
+// eighth) run and the block sums of the scaled values.
+__global__ __launch_bounds__(kSplitThreads) void split_rows_kernel(const float* __restrict__ x, std::uint32_t M,
+                                                              std::uint64_t K, std::uint64_t nb, std::uint32_t mp,
+                                                              uint4* __restrict__ xs, float* __restrict__ block_sums,
+                                                              float* __restrict__ inv_scale) {
+    __shared__ float red[kSplitThreads / 64];
+    const std::uint32_t m = blockIdx.x;
+    const bool row_live = m < M;
+    const float* in = x + static_cast<std::uint64_t>(m) * K;
+    float amax = 0.0f;
+    if (row_live) {
+        for (std::uint64_t c = threadIdx.x * 4u; c < K; c += kSplitThreads * 4u) {
+            const float4 v = *reinterpret_cast<const float4*>(in + c);
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = red[0];
+#pragma unroll
+    for (unsigned w = 1; w < kSplitThreads / 64; ++w) amax = fmaxf(amax, red[w]);
+    float s, inv;
+    block_scale(amax, s, inv);
+    const std::uint32_t mtiles = mp / 16u;
+    // Runs of 8: run r = 4 * block + g; the four runs of a block are adjacent lanes.
+    for (std::uint64_t r = threadIdx.x; r < nb * 4u; r += kSplitThreads) {
+        const std::uint64_t b = r >> 2;
+        const std::uint32_t g = static_cast<std::uint32_t>(r & 3u);
+        float v[8];
+        if (row_live && b * 32u < K) {
+            const float4* src = reinterpret_cast<const float4*>(in + b * 32u + 8u * g);
+            const float4 p = src[0], q = src[1];
+            v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w;
+            v[4] = q.x; v[5] = q.y; v[6] = q.z; v[7] = q.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+        }
+        half8v hi, lo;
+        split8(v, s, hi, lo);
+        float sum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += v[e] * s;
+        sum += __shfl_xor(sum, 1);
+        sum += __shfl_xor(sum, 2);
+        const std::uint32_t lane = (m & 15u) + 16u * g;
+        xs[((b * mtiles + (m >> 4)) * 2u + 0u) * 64u + lane] = __builtin_bit_cast(uint4, hi);
+        xs[((b * mtiles + (m >> 4)) * 2u + 1u) * 64u + lane] = __builtin_bit_cast(uint4, lo);
+        if (g == 0u) block_sums[b * mp + m] = sum;
+    }
+    if (threadIdx.x == 0) inv_scale[m] = inv;
+}
+
+template <int FMT, int MT>
+hipError_t launch_mt(const SkinnyArgs& a, std::uint32_t tn, std::uint32_t blocks, hipStream_t stream) {
+    if (tn == 2u) {
+        hipLaunchKernelGGL((skinny_kernel<FMT, MT, 2>), dim3(blocks), dim3(kThreads), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((skinny_kernel<FMT, MT, 1>), dim3(blocks), dim3(kThreads), 0, stream, a);
+    }
+    return hipGetLastError();
+}
+
+template <int FMT>
+hipError_t launch_fmt(const SkinnyArgs& a, const SkinnyShape& shape, std::uint32_t blocks, hipStream_t stream) {
+    switch (shape.mt) {
+    case 1: return launch_mt<FMT, 1>(a, shape.tile_n, blocks, stream);
+    case 2: return launch_mt<FMT, 2>(a, shape.tile_n, blocks, stream);
+    case 3: return launch_mt<FMT, 3>(a, shape.tile_n, blocks, stream);
+    default: return launch_mt<FMT, 4>(a, shape.tile_n, blocks, stream);
+    }
+}
+
+} // namespace
+
+hipError_t launch_split_activations_rows(const float* x, std::uint32_t m, std::uint64_t k, std::uint64_t kp,
+                                         const SplitWorkspace& ws, hipStream_t stream) {
+    if (m == 0u || m > 64u) return hipErrorInvalidValue;
+    const std::uint32_t mp = static_cast<std::uint32_t>(ceil_div(m, 16u) * 16u);
+    hipLaunchKernelGGL(split_rows_kernel, dim3(mp), dim3(kSplitThreads), 0, stream, x, m, k, kp / 32u, mp,
+                       static_cast<uint4*>(ws.xs), ws.block_sums, ws.inv_scale);
+    return hipGetLastError();
+}
+
+SkinnyShape plan_skinny(const TilePlanes& p, std::uint32_t m, std::uint32_t tile_n, std::uint32_t k_splits) {
+    SkinnyShape s;
+    s.mt = static_cast<std::uint32_t>(ceil_div(m, 16u));
+    // Two weight tiles per wave halve the LDS activation reads per weight
+    // byte; Q4_K with three or more activation tiles would spill registers.
+    // Automatic choice, measured on the Qwen2-7B shapes: two tiles only pay
+    // for matrices of 2000..4096 row tiles (gate|up) at M <= 32.
+    const std::uint32_t tn2_max_mt = p.type == kQ4_K ? 2u : 4u;
+    const std::uint32_t want = tile_n != 0u ? tile_n : ((s.mt <= 2u && p.nt >= 2000u && p.nt <= 4096u) ? 2u : 1u);
+    s.tile_n = (want == 2u && s.mt <= tn2_max_mt) ? 2u : 1u;
+    s.groups = static_cast<std::uint32_t>(ceil_div(p.nt, 4u * s.tile_n));
+    s.steps = static_cast<std::uint32_t>(p.kp / kStepK);
+    std::uint32_t splits = k_splits;
+    if (splits == 0u) {
+        // Up to about four workgroups per CU, keeping at least 4 steps per
+        // split and the partials' round trip below the weight bytes.
+        const std::uint64_t weight_bytes = static_cast<std::uint64_t>(p.nt) * p.kt * geometry_of(p.type).code_tile_bytes;
+        const std::uint64_t partial_trip = 2u * static_cast<std::uint64_t>(m) * p.n * 4u;
+        splits = 1u;
+        while (static_cast<std::uint64_t>(s.groups) * splits * 2u <= 1024u && s.steps / (splits * 2u) >= 4u &&
+               partial_trip * splits * 2u <= weight_bytes) {
+            splits *= 2u;
+        }
+    }
+    splits = splits < 1u ? 1u : (splits > s.steps ? s.steps : splits);
+    s.steps_per_split = static_cast<std::uint32_t>(ceil_div(s.steps, splits));
+    s.splits = static_cast<std::uint32_t>(ceil_div(s.steps, s.steps_per_split));
+    return s;
+}
+
+std::uint64_t skinny_partials_bytes(const SkinnyShape& shape, std::uint32_t m, std::uint64_t n) {
+    return shape.splits > 1u ? static_cast<std::uint64_t>(shape.splits) * m * n * 4u : 0u;
+}
+
+hipError_t launch_skinny_linear(const TilePlanes& p, const SplitWorkspace& ws, const float* bias, float* y,
+                                std::uint32_t m, const SkinnyShape& shape, float* partials, hipStream_t stream) {
+    if (m == 0u || m > 64u || shape.mt != ceil_div(m, 16u)) return hipErrorInvalidValue;
+    SkinnyArgs a{};
+    a.codes = p.codes;
+    a.scales = p.scales;
+    a.nt = p.nt;
+    a.kt = p.kt;
+    a.n = p.n;
+    a.xs = static_cast<const uint4*>(ws.xs);
+    a.inv_scale = ws.inv_scale;
+    a.block_sums = ws.block_sums;
+    a.m = m;
+    a.groups = shape.groups;
+    a.steps = shape.steps;
+    a.steps_per_split = shape.steps_per_split;
+    const bool split = shape.splits > 1u;
+    a.partial = split ? 1u : 0u;
+    a.bias = split ? nullptr : bias;
+    a.out = split ? partials : y;
+    const std::uint32_t blocks = shape.groups * shape.splits;
+    hipError_t err;
+    switch (p.type) {
+    case kQ8_0: err = launch_fmt<kQ8_0>(a, shape, blocks, stream); break;
+    case kQ4_0: err = launch_fmt<kQ4_0>(a, shape, blocks, stream); break;
+    case kQ4_K: err = launch_fmt<kQ4_K>(a, shape, blocks, stream); break;
+    default: return hipErrorInvalidValue;
+    }
+    if (err != hipSuccess || !split) return err;
+    return launch_split_reduce(partials, shape.splits, m, p.n, bias, y, stream);
+}
+
+} // namespace air_hip

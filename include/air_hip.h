@@ -139,6 +139,15 @@ int air_hip_context_stats(const air_hip_context* ctx, air_hip_stats* out);
  * clamped to its maximum. */
 int air_hip_context_set_tuning(air_hip_context* ctx, uint32_t rows_per_wave, uint32_t waves_per_group,
                                uint32_t k_splits);
+/* Chooses the decode kernel for 2..64 rows (autotuning): path 0 = automatic
+ * (the skinny kernel: activations split once into the workspace and staged
+ * through LDS, every weight read once, K split over workgroups when the
+ * weight tiles cannot fill the GPU), 1 = the single-launch fused kernel for
+ * M <= 16 and the per-wave K-split kernel above, 2 = skinny.  tile_n = 16-row
+ * weight tiles per wavefront of the skinny kernel (1 or 2), k_splits its K
+ * split (1..64); 0 keeps the automatic choice.  No counterpart in the
+ * reference. */
+int air_hip_context_set_decode_path(air_hip_context* ctx, uint32_t path, uint32_t tile_n, uint32_t k_splits);
 /* Overrides the prefill GEMM's launch shape for this context: tile_m =
  * 16-row activation tiles per wavefront (4 or 8), tile_n = 16-row weight
  * tiles per wavefront (2 or 4), k_splits = workgroups splitting K (1..64; a

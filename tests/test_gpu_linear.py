@@ -143,8 +143,9 @@ def test_linear_k_split_shapes_agree(torch_cuda, hip_ctx, type_id, k, n):
     torch = torch_cuda
     canon = helpers.weights(type_id, k, n, seed=k + n)
     mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    hip_ctx.set_decode_path(1)  # the fused / per-wave K-split kernels
     try:
-        for m in (1, 3, 16):
+        for m in (1, 3, 16, 40):
             x = helpers.activations(m, k, seed=m + 17)
             want = oracle.linear(type_id, canon, k, n, x)
             xd = _dev(torch, x)
@@ -161,4 +162,37 @@ def test_linear_k_split_shapes_agree(torch_cuda, hip_ctx, type_id, k, n):
                 assert all(np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)) for o in outs[1:])
     finally:
         hip_ctx.set_tuning(0, 0, 0)
+        hip_ctx.set_decode_path(0)
+        mat.release()
+
+
+@pytest.mark.parametrize("type_id,k,n", [(capi.TYPE_Q8_0, 3584, 200), (capi.TYPE_Q4_0, 1152, 333),
+                                         (capi.TYPE_Q4_K, 2304, 96), (capi.TYPE_Q8_0, 18944, 64)])
+def test_skinny_shapes_agree(torch_cuda, hip_ctx, type_id, k, n):
+    """The skinny decode kernel (M = 2..64): every activation-tile count,
+    one and two weight tiles per wave, K splits of 1..5 workgroups; each
+    matches the oracle to 1e-4 and repeats bit-identically."""
+    torch = torch_cuda
+    canon = helpers.weights(type_id, k, n, seed=k * 3 + n)
+    mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    try:
+        for m in (2, 16, 17, 33, 48, 64):
+            x = helpers.activations(m, k, seed=m + 5)
+            want = oracle.linear(type_id, canon, k, n, x)
+            xd = _dev(torch, x)
+            for tile_n, splits in [(1, 1), (2, 1), (1, 3), (2, 2), (1, 5), (0, 0)]:
+                hip_ctx.set_decode_path(2, tile_n, splits)
+                outs = []
+                for _ in range(2):
+                    y = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+                    mat.linear(xd, y, m)
+                    torch.cuda.synchronize()
+                    outs.append(y.cpu().numpy())
+                err = helpers.rel_l2(outs[0], want)
+                assert err <= DECODE_TOL, (m, tile_n, splits, err)
+                for r in range(m):
+                    assert helpers.rel_l2(outs[0][r], want[r]) <= DECODE_TOL, (m, tile_n, splits, r)
+                assert np.array_equal(outs[1].view(np.uint32), outs[0].view(np.uint32)), (m, tile_n, splits)
+    finally:
+        hip_ctx.set_decode_path(0)
         mat.release()
