@@ -177,8 +177,31 @@ __global__ __launch_bounds__(kSplitThreads) void split_rows_kernel(const float* 
     const std::uint32_t m = blockIdx.x;
     const bool row_live = m < M;
     const float* in = x + static_cast<std::uint64_t>(m) * K;
+    // Rows of up to kHeldRuns * 1024 runs (K <= 32768) are read once and held
+    // in registers for the split; longer rows are read twice.
+    constexpr unsigned kHeldRuns = 4;
+    const bool held = nb * 4u <= kHeldRuns * kSplitThreads;
+    float4v part[kHeldRuns][2];
     float amax = 0.0f;
-    if (row_live) {
+    if (held) {
+#pragma unroll
+        for (unsigned i = 0; i < kHeldRuns; ++i) {
+            const std::uint64_t r = threadIdx.x + kSplitThreads * i;
+            const std::uint64_t b = r >> 2;
+            if (row_live && r < nb * 4u && b * 32u < K) {
+                const float4v* src = reinterpret_cast<const float4v*>(in + b * 32u + 8u * (r & 3u));
+                part[i][0] = src[0];
+                part[i][1] = src[1];
+            } else {
+                part[i][0] = float4v{0.f, 0.f, 0.f, 0.f};
+                part[i][1] = float4v{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(part[i][h][e]));
+        }
+    } else if (row_live) {
         for (std::uint64_t c = threadIdx.x * 4u; c < K; c += kSplitThreads * 4u) {
             const float4 v = *reinterpret_cast<const float4*>(in + c);
             amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
@@ -193,6 +216,33 @@ __global__ __launch_bounds__(kSplitThreads) void split_rows_kernel(const float* 
     float s, inv;
     block_scale(amax, s, inv);
     const std::uint32_t mtiles = mp / 16u;
+    const auto emit = [&](std::uint64_t r, const float (&v)[8]) __attribute__((always_inline)) {
+        const std::uint64_t b = r >> 2;
+        const std::uint32_t g = static_cast<std::uint32_t>(r & 3u);
+        half8v hi, lo;
+        split8(v, s, hi, lo);
+        float sum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += v[e] * s;
+        sum += __shfl_xor(sum, 1);
+        sum += __shfl_xor(sum, 2);
+        const std::uint32_t lane = (m & 15u) + 16u * g;
+        xs[((b * mtiles + (m >> 4)) * 2u + 0u) * 64u + lane] = __builtin_bit_cast(uint4, hi);
+        xs[((b * mtiles + (m >> 4)) * 2u + 1u) * 64u + lane] = __builtin_bit_cast(uint4, lo);
+        if (g == 0u) block_sums[b * mp + m] = sum;
+    };
+    if (held) {
+#pragma unroll
+        for (unsigned i = 0; i < kHeldRuns; ++i) {
+            const std::uint64_t r = threadIdx.x + kSplitThreads * i;
+            if (r >= nb * 4u) break;  // uniform per aligned group of four lanes
+            const float v[8] = {part[i][0][0], part[i][0][1], part[i][0][2], part[i][0][3],
+                                part[i][1][0], part[i][1][1], part[i][1][2], part[i][1][3]};
+            emit(r, v);
+        }
+        if (threadIdx.x == 0) inv_scale[m] = inv;
+        return;
+    }
     // Runs of 8: run r = 4 * block + g; the four runs of a block are adjacent lanes.
     for (std::uint64_t r = threadIdx.x; r < nb * 4u; r += kSplitThreads) {
         const std::uint64_t b = r >> 2;
@@ -207,17 +257,8 @@ __global__ __launch_bounds__(kSplitThreads) void split_rows_kernel(const float* 
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[e] = 0.0f;
         }
-        half8v hi, lo;
-        split8(v, s, hi, lo);
-        float sum = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sum += v[e] * s;
-        sum += __shfl_xor(sum, 1);
-        sum += __shfl_xor(sum, 2);
-        const std::uint32_t lane = (m & 15u) + 16u * g;
-        xs[((b * mtiles + (m >> 4)) * 2u + 0u) * 64u + lane] = __builtin_bit_cast(uint4, hi);
-        xs[((b * mtiles + (m >> 4)) * 2u + 1u) * 64u + lane] = __builtin_bit_cast(uint4, lo);
-        if (g == 0u) block_sums[b * mp + m] = sum;
+        (void)g;
+        emit(r, v);
     }
     if (threadIdx.x == 0) inv_scale[m] = inv;
 }

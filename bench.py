@@ -31,6 +31,7 @@ if ROOT not in sys.path:
 
 HIDDEN, KV, FFN, VOCAB, LAYERS = 3584, 512, 18944, 152064, 28
 HBM_PEAK_GBS = 8000.0
+F16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense f16 MFMA
 Q8_BLOCK, Q8_BYTES = 32, 34
 
 
@@ -201,6 +202,43 @@ def read_traffic(m: int):
         return None
 
 
+def measure_prefill(torch, ctx, capi, layers, m, steps, dev, stream):
+    """One prefill pass over the layers' linears at M rows on the prefill
+    tactic (the f16 MFMA GEMM), timed with HIP events on the context's
+    stream; the roofline is the dense f16 MFMA peak."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    xs = {name: torch.randn((m, k), generator=gen, device=dev)
+          for name, k in (("qkv", HIDDEN), ("o", HIDDEN), ("gate_up", HIDDEN), ("down", FFN))}
+    ys = {name: torch.empty((m, n), device=dev)
+          for name, n in (("qkv", HIDDEN + 2 * KV), ("o", HIDDEN), ("gate_up", 2 * FFN), ("down", HIDDEN))}
+    flops = 0
+    for name, k, n in (("qkv", HIDDEN, HIDDEN + 2 * KV), ("o", HIDDEN, HIDDEN),
+                       ("gate_up", HIDDEN, 2 * FFN), ("down", FFN, HIDDEN)):
+        flops += 2 * m * n * k * len(layers)
+
+    def one_pass():
+        for mats in layers:
+            for name in ("qkv", "o", "gate_up", "down"):
+                mats[name].linear(xs[name], ys[name], m, tactic=capi.LINEAR_PREFILL)
+
+    one_pass()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        one_pass()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    tflops = flops / (ms * 1e-3) / 1e12
+    del xs, ys
+    return {"m": m, "layers": len(layers), "ms_per_pass": round(ms, 3), "tflops": round(tflops, 1),
+            "tok_s": round(m / (ms * 1e-3), 1), "mfma_peak_tflops": F16_MFMA_PEAK_TFLOPS,
+            "mfma_frac": round(tflops / F16_MFMA_PEAK_TFLOPS, 4), "dtype": "f16 operands, f32 accumulate"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -210,6 +248,8 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget (0 = skip)")
     ap.add_argument("--graph", type=int, default=1, help="replay each step as a captured HIP graph (1) or launch eagerly (0)")
+    ap.add_argument("--prefill-m", type=int, default=512,
+                    help="also time the prefill tactic (f16 MFMA GEMM) over the 28 layers' linears at this M (0 = skip)")
     ap.add_argument("--trace-summary", default=None, metavar="CSV",
                     help="summarise a rocprofv3 kernel-trace CSV instead of benchmarking")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -288,6 +328,11 @@ def main() -> int:
             mats["gate_up"].linear(x_ffn, y_gu, m)
             mats["down"].linear(x_act, y_down, m)
         lm_head.linear(x_h, logits, m)
+
+    prefill = None
+    if args.prefill_m > 0:
+        prefill = measure_prefill(torch, ctx, capi, layers, args.prefill_m, max(3, args.steps // 5), dev, stream)
+        print(f"# prefill M={args.prefill_m}: {prefill}", file=sys.stderr, flush=True)
 
     results = {}
     roofline = None
@@ -414,6 +459,7 @@ def main() -> int:
         },
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "prefill": prefill,
     }
     print(json.dumps(line), flush=True)
     ctx.close()
