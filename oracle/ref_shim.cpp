@@ -151,4 +151,100 @@ int airref_model_matvec(const airref_model* m, const float* x, float* y) {
 
 void airref_model_destroy(airref_model* m) { delete m; }
 
+// ---- a whole Qwen2 model through ReferenceExecutor -----------------------
+
+struct airref_qwen2_config {
+    std::uint32_t layers, embedding, ffn, heads, kv_heads, rope_dims;
+    std::uint64_t context, vocab;
+    double rope_base, eps;
+};
+
+struct airref_qwen2 {
+    std::unique_ptr<air::ReferenceExecutor> executor;
+    std::unique_ptr<air::ReferenceKvCache> cache;
+    airref_qwen2_config config{};
+};
+
+// Tensors are `count` entries of one blob (offsets/sizes in bytes, dims
+// [count][2] in GGML order, rank 1 or 2).  The blob goes to a temporary
+// mapped file, as the reference's tests assemble models.
+int airref_qwen2_create(const airref_qwen2_config* cfg, std::uint32_t count, const char* const* names,
+                        const int* types, const std::uint32_t* ranks, const std::uint64_t* dims,
+                        const std::uint64_t* offsets, const std::uint64_t* sizes, const std::uint8_t* blob,
+                        std::uint64_t blob_bytes, airref_qwen2** out) {
+    if (!cfg || !out) return 1;
+    *out = nullptr;
+    char path[] = "/tmp/airref-qwen2-XXXXXX";
+    const int fd = mkstemp(path);
+    if (fd < 0) return 3;
+    std::uint64_t written = 0;
+    while (written < blob_bytes) {
+        const auto n = ::write(fd, blob + written, blob_bytes - written);
+        if (n <= 0) { ::close(fd); std::filesystem::remove(path); return 3; }
+        written += static_cast<std::uint64_t>(n);
+    }
+    ::close(fd);
+    auto storage = air::ModelStorage::map_read_only(path);
+    std::filesystem::remove(path);
+    if (!storage) return code_of(storage.status());
+
+    std::vector<air::TensorDescriptor> tensors;
+    for (std::uint32_t i = 0; i < count; ++i) {
+        air::TensorDescriptor t;
+        t.name = names[i];
+        if (!data_type_for(types[i], t.type)) return 6;
+        t.format_type = static_cast<std::uint32_t>(types[i]);
+        t.shape.dimensions.assign(dims + 2u * i, dims + 2u * i + ranks[i]);
+        t.byte_offset = offsets[i];
+        t.byte_size = sizes[i];
+        t.byte_size_exact = true;
+        tensors.push_back(std::move(t));
+    }
+    air::ModelConfig config;
+    config.architecture = "qwen2";
+    config.layer_count = cfg->layers;
+    config.embedding_size = cfg->embedding;
+    config.feed_forward_size = cfg->ffn;
+    config.attention_head_count = cfg->heads;
+    config.kv_head_count = cfg->kv_heads;
+    config.rope_dimension_count = cfg->rope_dims;
+    config.context_length = cfg->context;
+    config.vocabulary_size = cfg->vocab;
+    config.rope_frequency_base = cfg->rope_base;
+    config.rms_norm_epsilon = cfg->eps;
+    air::TokenizerDefinition tokenizer;
+    for (std::uint64_t i = 0; i < cfg->vocab; ++i) tokenizer.vocabulary.push_back("t" + std::to_string(i));
+    auto model = std::make_shared<air::ModelDefinition>(
+        air::ModelFingerprint{"test", "qwen2", "oracle"}, std::move(config), std::move(tokenizer),
+        std::move(tensors), std::move(storage).value());
+    auto executor = air::ReferenceExecutor::create(model);
+    if (!executor) return code_of(executor.status());
+    auto* q = new airref_qwen2();
+    q->executor = std::move(executor).value();
+    q->config = *cfg;
+    q->cache = std::make_unique<air::ReferenceKvCache>(cfg->layers, cfg->kv_heads, cfg->embedding / cfg->heads,
+                                                       cfg->context);
+    *out = q;
+    return 0;
+}
+
+// ReferenceExecutor::step: appends `token` and writes the vocabulary logits.
+int airref_qwen2_step(airref_qwen2* q, std::int32_t token, float* logits) {
+    if (!q) return 1;
+    auto out = q->executor->step(token, *q->cache);
+    if (!out) return code_of(out.status());
+    std::memcpy(logits, out.value().data(), out.value().size() * sizeof(float));
+    return 0;
+}
+
+// Drops the sequence (a fresh cache).
+int airref_qwen2_reset(airref_qwen2* q) {
+    if (!q) return 1;
+    const auto& c = q->config;
+    q->cache = std::make_unique<air::ReferenceKvCache>(c.layers, c.kv_heads, c.embedding / c.heads, c.context);
+    return 0;
+}
+
+void airref_qwen2_destroy(airref_qwen2* q) { delete q; }
+
 } // extern "C"

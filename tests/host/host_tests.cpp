@@ -16,8 +16,11 @@
 #include "air/synthetic.hpp"
 
 #include "air_oracle.h"
+#include "air_oracle_qwen2.h"
+#include "qwen2_fixture.hpp"
 
 #include <hip/hip_runtime_api.h>
+#include <unistd.h>
 
 #include <cmath>
 #include <cstring>
@@ -510,7 +513,68 @@ void test_sequence_estimate() {
           "overflow saturates");
 }
 
+// tests/golden/... relative to this binary (tests/host/host_tests).
+std::string repo_file(const std::string& rel) {
+    char buf[4096];
+    const ssize_t n = readlink("/proc/self/exe", buf, sizeof(buf) - 1);
+    std::string exe = n > 0 ? std::string(buf, static_cast<std::size_t>(n)) : std::string("tests/host/host_tests");
+    const auto dir = exe.substr(0, exe.find_last_of('/'));
+    return dir + "/../../" + rel;
+}
+
+// The C oracle's Qwen2 step against AIR's ReferenceExecutor: every logit of
+// every step of the golden sequences, bit for bit, and the greedy tokens.
+void test_qwen2_oracle_matches_reference() {
+    const auto cases = fixture::load(repo_file("tests/golden/qwen2_tiny.txt"));
+    check(cases.size() == 3U, "three golden Qwen2 cases");
+    for (const auto& c : cases) {
+        auto built = air::make_synthetic_qwen2(c.spec);
+        check(built.is_ok(), c.name + ": model rebuilds");
+        if (!built) continue;
+        const auto view = fixture::oracle_view(*built.value());
+        const auto vocab = c.spec.config.vocabulary_size;
+        std::vector<float> logits(vocab);
+        for (const auto& seq : c.sequences) {
+            oracle_qwen2_cache cache{};
+            check(oracle_qwen2_cache_init(&view->model, &cache, c.spec.config.context_length) == 0, "cache");
+            std::vector<std::int32_t> feed = seq.prompt;
+            feed.insert(feed.end(), seq.generated.begin(), seq.generated.end() - 1);
+            std::size_t mismatched = 0;
+            std::vector<std::int32_t> greedy;
+            for (std::size_t s = 0; s < feed.size(); ++s) {
+                if (oracle_qwen2_step(&view->model, &cache, feed[s], logits.data()) != 0) {
+                    check(false, c.name + ": oracle step failed");
+                    break;
+                }
+                for (std::uint64_t i = 0; i < vocab; ++i) {
+                    if (std::memcmp(&logits[i], &seq.logits[s][i], sizeof(float)) != 0) ++mismatched;
+                }
+                if (s + 1 >= seq.prompt.size()) greedy.push_back(static_cast<std::int32_t>(oracle_greedy(logits.data(), vocab)));
+            }
+            check(mismatched == 0, c.name + ": oracle logits differ from the reference in " + std::to_string(mismatched) +
+                                       " places");
+            check(greedy == seq.generated, c.name + ": oracle greedy tokens match the reference");
+            oracle_qwen2_cache_free(&cache);
+        }
+    }
+    // A planted mistake in the oracle's inputs is seen: feeding one wrong
+    // prompt token changes the logits.
+    if (!cases.empty()) {
+        const auto& c = cases.front();
+        auto built = air::make_synthetic_qwen2(c.spec);
+        const auto view = fixture::oracle_view(*built.value());
+        std::vector<float> logits(c.spec.config.vocabulary_size);
+        oracle_qwen2_cache cache{};
+        oracle_qwen2_cache_init(&view->model, &cache, c.spec.config.context_length);
+        oracle_qwen2_step(&view->model, &cache, c.sequences.front().prompt.front() + 1, logits.data());
+        check(std::memcmp(logits.data(), c.sequences.front().logits.front().data(), logits.size() * 4) != 0,
+              "a different token gives different logits");
+        oracle_qwen2_cache_free(&cache);
+    }
+}
+
 int run_cpu() {
+    test_qwen2_oracle_matches_reference();
     test_capacity_reservations();
     test_plan_preparation_capacity();
     test_transition_capacity();
