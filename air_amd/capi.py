@@ -82,6 +82,14 @@ SIGNATURES = {
     "air_hip_context_set_tuning": (_I, [_P, _U32, _U32, _U32]),
     "air_hip_context_set_prefill_tuning": (_I, [_P, _U32, _U32, _U32, _U32]),
     "air_hip_context_set_decode_path": (_I, [_P, _U32, _U32, _U32]),
+    "air_hip_matrix_rows": (_I, [_P, _P, _P, _U32, _P]),
+    "air_hip_rms_norm": (_I, [_P, _P, _P, _P, _U32, _U64, ctypes.c_double]),
+    "air_hip_rope": (_I, [_P, _P, _U64, _U32, _P, _U32, _U32, _U32, _U32, _P, _U64]),
+    "air_hip_kv_append": (_I, [_P, _P, _P, _U64, _U64, _U32, _P, _P, _U32]),
+    "air_hip_attention": (_I, [_P, _P, _P, _U64, _U32, _P, _P, _U32, _U32, _U32, _U32, _U64, _P]),
+    "air_hip_silu_mul": (_I, [_P, _P, _P, _U32, _U64]),
+    "air_hip_add": (_I, [_P, _P, _P, _U64]),
+    "air_hip_argmax": (_I, [_P, _P, _U32, _U64, _P]),
     "air_hip_canonical_bytes": (_U64, [_I, _U64, _U64]),
     "air_hip_matrix_prepare": (_I, [_P, _I, _U64, _U64, _P, _U64, _I, ctypes.POINTER(_P)]),
     "air_hip_matrix_release": (_I, [_P]),

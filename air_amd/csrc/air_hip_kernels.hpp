@@ -132,6 +132,35 @@ std::uint64_t skinny_partials_bytes(const SkinnyShape& shape, std::uint32_t m, s
 hipError_t launch_skinny_linear(const TilePlanes& planes, const SplitWorkspace& ws, const float* bias, float* y,
                                 std::uint32_t m, const SkinnyShape& shape, float* partials, hipStream_t stream);
 
+// ---- the Qwen2 step around the linears ----------------------------------
+
+// Paged fp32 KV pool: page p holds [layer][2 (K, V)][page_tokens][kv_width].
+struct KvLayout {
+    float* pool{nullptr};
+    std::uint32_t page_tokens{0};
+    std::uint32_t kv_width{0};
+    std::uint32_t layers{0};
+    std::uint32_t max_pages{0};    // page-table row length (int32 entries)
+    std::uint32_t pool_pages{0};
+};
+hipError_t launch_matrix_rows(const TilePlanes& planes, const std::int32_t* rows, std::uint32_t m, float* out,
+                              hipStream_t stream);
+hipError_t launch_rms_norm(const float* x, const float* w, float* out, std::uint32_t m, std::uint64_t n, double eps,
+                           hipStream_t stream);
+hipError_t launch_rope(float* qkv, std::uint64_t stride, std::uint32_t m, const std::int32_t* positions,
+                       std::uint32_t q_heads, std::uint32_t kv_heads, std::uint32_t head_dim, std::uint32_t rope_dims,
+                       const void* table, std::uint64_t table_positions, hipStream_t stream);
+hipError_t launch_kv_append(const KvLayout& kv, const float* qkv, std::uint64_t stride, std::uint64_t q_width,
+                            std::uint32_t m, const std::int32_t* positions, const std::int32_t* tables,
+                            std::uint32_t layer, hipStream_t stream);
+hipError_t launch_attention(const KvLayout& kv, const float* qkv, std::uint64_t stride, std::uint32_t m,
+                            const std::int32_t* positions, const std::int32_t* tables, std::uint32_t layer,
+                            std::uint32_t q_heads, std::uint32_t kv_heads, std::uint32_t head_dim, double* scratch,
+                            std::uint64_t score_stride, float* out, hipStream_t stream);
+hipError_t launch_silu_mul(const float* gate_up, float* out, std::uint32_t m, std::uint64_t ffn, hipStream_t stream);
+hipError_t launch_add(float* x, const float* y, std::uint64_t count, hipStream_t stream);
+hipError_t launch_argmax(const float* logits, std::uint32_t m, std::uint64_t n, std::int32_t* out, hipStream_t stream);
+
 // Sets planes.prefill_scale / prefill_unscale from the largest dequantized
 // magnitude of the resident matrix (synchronous; `bound_scratch` is one
 // device uint32).

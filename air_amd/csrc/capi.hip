@@ -56,6 +56,8 @@ struct air_hip_context {
     std::uint32_t skinny_tile_n{0};
     std::uint32_t skinny_splits{0};
     std::uint32_t* bound_scratch{nullptr};  // one uint32 for the weight exponent at residency
+    void* attention_scratch{nullptr};       // attention scores, grown on demand
+    std::uint64_t attention_scratch_bytes{0};
 };
 
 struct air_hip_matrix {
@@ -266,6 +268,7 @@ int air_hip_context_destroy(air_hip_context* ctx) {
         if (ctx->split_counters) (void)hipFree(ctx->split_counters);
         if (ctx->prefill_workspace) (void)hipFree(ctx->prefill_workspace);
         if (ctx->bound_scratch) (void)hipFree(ctx->bound_scratch);
+        if (ctx->attention_scratch) (void)hipFree(ctx->attention_scratch);
     }
     delete ctx;
     return AIR_HIP_OK;
@@ -614,6 +617,145 @@ int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* m, const float* x
     int rc = air_hip_activations_load(ctx, x, m->planes.k, rows);
     if (rc != AIR_HIP_OK) return rc;
     return air_hip_linear_loaded(ctx, m, y, bias, tactic);
+}
+
+// ---- the Qwen2 step around the linears ------------------------------------
+
+int air_hip_matrix_rows(air_hip_context* ctx, const air_hip_matrix* m, const int32_t* rows, uint32_t count,
+                        float* out) {
+    if (!ctx || !m || !rows || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
+    if (count == 0) return AIR_HIP_OK;
+    if (count > 65535u) return fail(AIR_HIP_UNSUPPORTED, "at most 65535 rows per call");
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const hipError_t err = launch_matrix_rows(m->planes, rows, count, out, ctx->stream);
+    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "matrix_rows_kernel");
+}
+
+int air_hip_rms_norm(air_hip_context* ctx, const float* x, const float* weight, float* out, uint32_t m, uint64_t n,
+                     double eps) {
+    if (!ctx || !x || !weight || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    if (n == 0 || !(eps >= 0.0)) return fail(AIR_HIP_INVALID_ARGUMENT, "width must be non-zero and eps non-negative");
+    if (m == 0) return AIR_HIP_OK;
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const hipError_t err = launch_rms_norm(x, weight, out, m, n, eps, ctx->stream);
+    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "rms_norm_kernel");
+}
+
+int air_hip_rope(air_hip_context* ctx, float* qkv, uint64_t row_stride, uint32_t m, const int32_t* positions,
+                 uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim, uint32_t rope_dims, const float* table,
+                 uint64_t table_positions) {
+    if (!ctx || !qkv || !positions || !table) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    if (rope_dims == 0 || rope_dims % 2u != 0 || rope_dims > head_dim || table_positions == 0) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "RoPE needs an even rope_dims <= head_dim and a table");
+    }
+    if (row_stride < static_cast<uint64_t>(q_heads + kv_heads) * head_dim) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "row stride is shorter than the q and k heads");
+    }
+    if (m == 0) return AIR_HIP_OK;
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const hipError_t err = launch_rope(qkv, row_stride, m, positions, q_heads, kv_heads, head_dim, rope_dims, table,
+                                       table_positions, ctx->stream);
+    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "rope_kernel");
+}
+
+namespace {
+int check_kv(const air_hip_kv_layout* kv) {
+    if (!kv || !kv->pool) return fail(AIR_HIP_INVALID_ARGUMENT, "KV layout and pool must not be null");
+    if (kv->page_tokens == 0 || kv->kv_width == 0 || kv->layers == 0 || kv->max_pages == 0 || kv->pool_pages == 0) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "KV layout has a zero dimension");
+    }
+    return AIR_HIP_OK;
+}
+KvLayout kv_layout_of(const air_hip_kv_layout* kv) {
+    return KvLayout{kv->pool, kv->page_tokens, kv->kv_width, kv->layers, kv->max_pages, kv->pool_pages};
+}
+} // namespace
+
+int air_hip_kv_append(air_hip_context* ctx, const air_hip_kv_layout* kv, const float* qkv, uint64_t row_stride,
+                      uint64_t q_width, uint32_t m, const int32_t* positions, const int32_t* page_tables,
+                      uint32_t layer) {
+    if (!ctx || !qkv || !positions || !page_tables) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    if (int rc = check_kv(kv); rc != AIR_HIP_OK) return rc;
+    if (layer >= kv->layers) return fail(AIR_HIP_INVALID_ARGUMENT, "layer %u is out of range", layer);
+    if (row_stride < q_width + 2u * static_cast<uint64_t>(kv->kv_width)) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "row stride is shorter than q|k|v");
+    }
+    if (m == 0) return AIR_HIP_OK;
+    if (m > 65535u) return fail(AIR_HIP_UNSUPPORTED, "at most 65535 rows per call");
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const hipError_t err = launch_kv_append(kv_layout_of(kv), qkv, row_stride, q_width, m, positions, page_tables,
+                                            layer, ctx->stream);
+    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "kv_append_kernel");
+}
+
+int air_hip_attention(air_hip_context* ctx, const air_hip_kv_layout* kv, const float* qkv, uint64_t row_stride,
+                      uint32_t m, const int32_t* positions, const int32_t* page_tables, uint32_t layer,
+                      uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim, uint64_t max_tokens, float* out) {
+    if (!ctx || !qkv || !positions || !page_tables || !out) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    }
+    if (int rc = check_kv(kv); rc != AIR_HIP_OK) return rc;
+    if (layer >= kv->layers) return fail(AIR_HIP_INVALID_ARGUMENT, "layer %u is out of range", layer);
+    if (q_heads == 0 || kv_heads == 0 || q_heads % kv_heads != 0 || head_dim == 0 || head_dim > 512u ||
+        static_cast<uint64_t>(kv_heads) * head_dim != kv->kv_width) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "head geometry does not match the KV layout");
+    }
+    if (max_tokens == 0 || max_tokens > static_cast<uint64_t>(kv->max_pages) * kv->page_tokens) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "max_tokens must be in [1, max_pages * page_tokens]");
+    }
+    if (m == 0) return AIR_HIP_OK;
+    const uint64_t blocks = static_cast<uint64_t>(m) * q_heads;
+    if (blocks > 0x7fffffffu) return fail(AIR_HIP_UNSUPPORTED, "too many (row, head) pairs");
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const uint64_t scratch_bytes = blocks * max_tokens * sizeof(double);
+    if (scratch_bytes > ctx->attention_scratch_bytes) {
+        const hipError_t sync = hipStreamSynchronize(ctx->stream);
+        if (sync != hipSuccess) return hip_fail(sync, "hipStreamSynchronize(attention scratch growth)");
+        (void)hipFree(ctx->attention_scratch);
+        ctx->attention_scratch = nullptr;
+        ctx->attention_scratch_bytes = 0;
+        const hipError_t err = hipMalloc(&ctx->attention_scratch, scratch_bytes);
+        if (err != hipSuccess) return hip_fail(err, "hipMalloc(attention scratch)");
+        ctx->attention_scratch_bytes = scratch_bytes;
+    }
+    const hipError_t err = launch_attention(kv_layout_of(kv), qkv, row_stride, m, positions, page_tables, layer,
+                                            q_heads, kv_heads, head_dim, static_cast<double*>(ctx->attention_scratch),
+                                            max_tokens, out, ctx->stream);
+    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "attention_kernel");
+}
+
+int air_hip_silu_mul(air_hip_context* ctx, const float* gate_up, float* out, uint32_t m, uint64_t ffn) {
+    if (!ctx || !gate_up || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    if (m == 0 || ffn == 0) return AIR_HIP_OK;
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const hipError_t err = launch_silu_mul(gate_up, out, m, ffn, ctx->stream);
+    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "silu_mul_kernel");
+}
+
+int air_hip_add(air_hip_context* ctx, float* x, const float* y, uint64_t count) {
+    if (!ctx || !x || !y) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    if (count == 0) return AIR_HIP_OK;
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const hipError_t err = launch_add(x, y, count, ctx->stream);
+    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "add_kernel");
+}
+
+int air_hip_argmax(air_hip_context* ctx, const float* logits, uint32_t m, uint64_t n, int32_t* out) {
+    if (!ctx || !logits || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    if (n == 0 || n > 0x7fffffffu) return fail(AIR_HIP_INVALID_ARGUMENT, "row width must be in [1, 2^31)");
+    if (m == 0) return AIR_HIP_OK;
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const hipError_t err = launch_argmax(logits, m, n, out, ctx->stream);
+    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "argmax_kernel");
 }
 
 } // extern "C"

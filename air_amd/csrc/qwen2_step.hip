@@ -1,0 +1,380 @@
+// qwen2_step.hip -- the Qwen2 step around the linears: embedding rows,
+// RMSNorm, RoPE, paged KV append, attention, SiLU * up, residual add, greedy
+// argmax.
+//
+// Each kernel follows the reference executor's arithmetic (src/reference/
+// reference_executor.cpp:17-138, 325-428) operation by operation where that
+// is cheap on the GPU, so a HIP step differs from the reference only through
+// the linears (relative error ~1e-6):
+//   * RMSNorm: double sum of squares, scale = float(1 / sqrt(mean + eps)),
+//     out = (x * scale) * w in float;
+//   * RoPE: cos / sin come from a host table built with the reference's
+//     double formulas; the rotation is two float products and one float
+//     add / subtract, never fused;
+//   * attention: double scores (sequential dot over the head dimension),
+//     double softmax with the denominator summed in token order, float
+//     probabilities, float accumulation of p * v in token order, never fused;
+//   * greedy: the first maximum (std::max_element, src/runtime/sampling.cpp:13-16).
+//
+// The KV cache is paged: a page holds `page_tokens` tokens of every layer's K
+// and V ([layer][2][page_tokens][kv_width] f32); a row's sequence is named by
+// its page table (int32 page indices).
+#include "air_hip_device.hpp"
+#include "air_hip_kernels.hpp"
+
+namespace air_hip {
+namespace {
+
+constexpr unsigned kThreads = 256;
+
+// ---- embedding rows --------------------------------------------------------
+
+// out[i][k] = W[rows[i]][k] decoded bit-exactly from the resident tiles.
+__global__ __launch_bounds__(kThreads) void matrix_rows_kernel(int type, const void* codes_, const void* scales_,
+                                                               std::uint64_t K, std::uint64_t N, std::uint32_t KT,
+                                                               const std::int32_t* __restrict__ rows,
+                                                               std::uint32_t m, float* __restrict__ out) {
+#pragma clang fp contract(off)
+    const std::uint32_t i = blockIdx.y;
+    if (i >= m) return;
+    const std::int32_t row = rows[i];
+    if (row < 0 || static_cast<std::uint64_t>(row) >= N) return;
+    const std::uint32_t rt = static_cast<std::uint32_t>(row) >> 4, r = static_cast<std::uint32_t>(row) & 15u;
+    float* dst = out + static_cast<std::uint64_t>(i) * K;
+    for (std::uint64_t k = blockIdx.x * static_cast<std::uint64_t>(kThreads) + threadIdx.x; k < K;
+         k += static_cast<std::uint64_t>(gridDim.x) * kThreads) {
+        float value = 0.0f;
+        if (type == kQ8_0) {
+            const std::uint32_t kt = static_cast<std::uint32_t>(k / 64u), kk = static_cast<std::uint32_t>(k % 64u);
+            const std::uint32_t hb = kk / 32u, within = kk % 32u, g = within / 8u, e = within % 8u;
+            const std::uint64_t tile = static_cast<std::uint64_t>(rt) * KT + kt;
+            const std::uint8_t* rec = static_cast<const std::uint8_t*>(codes_) + (tile * 64u + 16u * g + r) * 16u;
+            const int q = static_cast<int>(rec[8u * hb + e]) - 128;
+            const std::uint32_t sc = static_cast<const std::uint32_t*>(scales_)[tile * 16u + r];
+            value = f16_bits_to_f32((sc >> (16u * hb)) & 0xffffu) * static_cast<float>(q);
+        } else if (type == kQ4_0) {
+            const std::uint32_t kt = static_cast<std::uint32_t>(k / 128u), kk = static_cast<std::uint32_t>(k % 128u);
+            const std::uint32_t j = kk / 32u, within = kk % 32u, g = within / 8u, e = within % 8u;
+            const std::uint64_t tile = static_cast<std::uint64_t>(rt) * KT + kt;
+            const std::uint32_t w = static_cast<const std::uint32_t*>(codes_)[(tile * 64u + 16u * g + r) * 4u + j];
+            const int q = static_cast<int>((w >> kNibblePos[e]) & 0x0fu) - 8;
+            const std::uint32_t sw = static_cast<const std::uint32_t*>(scales_)[(tile * 16u + r) * 2u + j / 2u];
+            value = f16_bits_to_f32((sw >> (16u * (j & 1u))) & 0xffffu) * static_cast<float>(q);
+        } else {
+            const std::uint32_t kt = static_cast<std::uint32_t>(k / 256u), kk = static_cast<std::uint32_t>(k % 256u);
+            const std::uint32_t j = kk / 32u, within = kk % 32u, g = within / 8u, e = within % 8u;
+            const std::uint64_t tile = static_cast<std::uint64_t>(rt) * KT + kt;
+            const std::uint32_t w = static_cast<const std::uint32_t*>(
+                codes_)[(((tile * 2u + j / 4u) * 64u) + 16u * g + r) * 4u + (j & 3u)];
+            const std::uint32_t n = (w >> kNibblePos[e]) & 0x0fu;
+            const std::uint32_t* hd = static_cast<const std::uint32_t*>(scales_) + (tile * 16u + r) * 4u;
+            const std::uint32_t packed[3] = {hd[1], hd[2], hd[3]};
+            std::uint32_t s6 = 0, m6 = 0;
+            q4k_scale_min(packed, j, s6, m6);
+            const float d = f16_bits_to_f32(hd[0] & 0xffffu);
+            const float dmin = f16_bits_to_f32(hd[0] >> 16);
+            value = (d * static_cast<float>(s6)) * static_cast<float>(n) - dmin * static_cast<float>(m6);
+        }
+        dst[k] = value;
+    }
+}
+
+// ---- RMSNorm ---------------------------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void rms_norm_kernel(const float* x, const float* __restrict__ w,
+                                                            float* out, std::uint64_t n, double eps) {
+#pragma clang fp contract(off)
+    __shared__ double red[kThreads / 64];
+    const float* row = x + static_cast<std::uint64_t>(blockIdx.x) * n;
+    float* dst = out + static_cast<std::uint64_t>(blockIdx.x) * n;
+    double sum = 0.0;
+    for (std::uint64_t i = threadIdx.x; i < n; i += kThreads) sum += static_cast<double>(row[i]) * row[i];
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = sum;
+    __syncthreads();
+    const double total = (red[0] + red[1]) + (red[2] + red[3]);
+    const double mean = total / static_cast<double>(n);
+    const float scale = static_cast<float>(1.0 / sqrt(mean + eps));
+    for (std::uint64_t i = threadIdx.x; i < n; i += kThreads) dst[i] = row[i] * scale * w[i];
+}
+
+// ---- RoPE ------------------------------------------------------------------
+
+// One thread per (row, head, pair); q heads then k heads of each fused row.
+__global__ __launch_bounds__(kThreads) void rope_kernel(float* __restrict__ qkv, std::uint64_t stride, std::uint32_t m,
+                                                        const std::int32_t* __restrict__ positions,
+                                                        std::uint32_t q_heads, std::uint32_t kv_heads,
+                                                        std::uint32_t head_dim, std::uint32_t rope_dims,
+                                                        const float2* __restrict__ table,
+                                                        std::uint64_t table_positions) {
+#pragma clang fp contract(off)
+    const std::uint32_t half = rope_dims / 2u;
+    const std::uint32_t heads = q_heads + kv_heads;
+    const std::uint64_t total = static_cast<std::uint64_t>(m) * heads * half;
+    for (std::uint64_t idx = blockIdx.x * static_cast<std::uint64_t>(kThreads) + threadIdx.x; idx < total;
+         idx += static_cast<std::uint64_t>(gridDim.x) * kThreads) {
+        const std::uint32_t i = static_cast<std::uint32_t>(idx % half);
+        const std::uint32_t h = static_cast<std::uint32_t>((idx / half) % heads);
+        const std::uint32_t r = static_cast<std::uint32_t>(idx / (static_cast<std::uint64_t>(half) * heads));
+        const std::int32_t pos = positions[r];
+        if (pos < 0 || static_cast<std::uint64_t>(pos) >= table_positions) continue;
+        float* base = qkv + static_cast<std::uint64_t>(r) * stride + static_cast<std::uint64_t>(h) * head_dim;
+        const float2 cs = table[static_cast<std::uint64_t>(pos) * half + i];
+        const float first = base[i];
+        const float second = base[i + half];
+        const float a = first * cs.x;
+        const float b = second * cs.y;
+        const float c = first * cs.y;
+        const float d = second * cs.x;
+        base[i] = a - b;
+        base[i + half] = c + d;
+    }
+}
+
+// ---- paged KV ----------------------------------------------------------------
+
+struct KvGeometry {
+    float* pool;
+    std::uint32_t page_tokens;
+    std::uint32_t kv_width;       // kv_heads * head_dim
+    std::uint32_t layers;
+    std::uint32_t max_pages;      // page-table row length
+    std::uint32_t pool_pages;     // pages in the pool
+};
+
+__device__ __forceinline__ std::uint64_t page_floats(const KvGeometry& g) {
+    return static_cast<std::uint64_t>(g.layers) * 2u * g.page_tokens * g.kv_width;
+}
+
+// K and V of (layer, token) of a row's sequence; null when the page table
+// does not name a page of the pool (the caller skips the token).
+__device__ __forceinline__ float* kv_slot(const KvGeometry& g, const std::int32_t* table, std::uint32_t layer,
+                                          std::uint64_t token, bool value) {
+    const std::uint64_t slot = token / g.page_tokens;
+    if (slot >= g.max_pages) return nullptr;
+    const std::int32_t page = table[slot];
+    if (page < 0 || static_cast<std::uint32_t>(page) >= g.pool_pages) return nullptr;
+    return g.pool + static_cast<std::uint64_t>(page) * page_floats(g) +
+           ((static_cast<std::uint64_t>(layer) * 2u + (value ? 1u : 0u)) * g.page_tokens + token % g.page_tokens) *
+               g.kv_width;
+}
+
+// Copies each row's k and v (after RoPE) from its fused q|k|v output into its page slot.
+__global__ __launch_bounds__(kThreads) void kv_append_kernel(KvGeometry g, const float* __restrict__ qkv,
+                                                             std::uint64_t stride, std::uint64_t q_width,
+                                                             std::uint32_t m, const std::int32_t* __restrict__ positions,
+                                                             const std::int32_t* __restrict__ tables,
+                                                             std::uint32_t layer) {
+    const std::uint32_t r = blockIdx.y;
+    if (r >= m) return;
+    const std::int32_t* table = tables + static_cast<std::uint64_t>(r) * g.max_pages;
+    const std::uint64_t pos = static_cast<std::uint64_t>(positions[r]);
+    float* k = kv_slot(g, table, layer, pos, false);
+    float* v = kv_slot(g, table, layer, pos, true);
+    if (!k || !v) return;
+    const float* src = qkv + static_cast<std::uint64_t>(r) * stride + q_width;
+    for (std::uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < g.kv_width; i += gridDim.x * kThreads) {
+        k[i] = src[i];
+        v[i] = src[g.kv_width + i];
+    }
+}
+
+// One workgroup per (row, q head): attention over tokens 0..positions[row] of
+// the row's sequence, in the reference's arithmetic (see file comment).
+// scratch: [m * q_heads][score_stride] doubles.
+__global__ __launch_bounds__(kThreads) void attention_kernel(KvGeometry g, const float* __restrict__ qkv,
+                                                             std::uint64_t stride, std::uint32_t m,
+                                                             const std::int32_t* __restrict__ positions,
+                                                             const std::int32_t* __restrict__ tables,
+                                                             std::uint32_t layer, std::uint32_t q_heads,
+                                                             std::uint32_t kv_heads, std::uint32_t head_dim,
+                                                             double* __restrict__ scratch, std::uint64_t score_stride,
+                                                             float* __restrict__ out) {
+#pragma clang fp contract(off)
+    __shared__ float qs[512];
+    __shared__ double red[kThreads / 64];
+    __shared__ double denom_shared;
+    const std::uint32_t r = blockIdx.x / q_heads;
+    const std::uint32_t qh = blockIdx.x % q_heads;
+    if (r >= m) return;
+    const std::uint32_t kvh = static_cast<std::uint32_t>((static_cast<std::uint64_t>(qh) * kv_heads) / q_heads);
+    const std::int32_t* table = tables + static_cast<std::uint64_t>(r) * g.max_pages;
+    std::uint64_t total = static_cast<std::uint64_t>(positions[r] < 0 ? 0 : positions[r]) + 1u;
+    if (total > score_stride) total = score_stride;
+    const float* q = qkv + static_cast<std::uint64_t>(r) * stride + static_cast<std::uint64_t>(qh) * head_dim;
+    for (std::uint32_t d = threadIdx.x; d < head_dim; d += kThreads) qs[d] = q[d];
+    __syncthreads();
+    double* scores = scratch + static_cast<std::uint64_t>(blockIdx.x) * score_stride;
+    const double scale = 1.0 / sqrt(static_cast<double>(head_dim));
+    double local_max = -__builtin_huge_val();
+    for (std::uint64_t t = threadIdx.x; t < total; t += kThreads) {
+        const float* slot = kv_slot(g, table, layer, t, false);
+        double s = 0.0;
+        if (slot) {
+            const float* key = slot + static_cast<std::uint64_t>(kvh) * head_dim;
+            for (std::uint32_t d = 0; d < head_dim; ++d) s += static_cast<double>(qs[d]) * static_cast<double>(key[d]);
+        }
+        s *= scale;
+        scores[t] = s;
+        local_max = s > local_max ? s : local_max;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const double o = __shfl_xor(local_max, off);
+        local_max = o > local_max ? o : local_max;
+    }
+    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = local_max;
+    __syncthreads();
+    double maximum = red[0];
+    for (unsigned w = 1; w < kThreads / 64; ++w) maximum = red[w] > maximum ? red[w] : maximum;
+    for (std::uint64_t t = threadIdx.x; t < total; t += kThreads) scores[t] = exp(scores[t] - maximum);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double denominator = 0.0;
+        for (std::uint64_t t = 0; t < total; ++t) denominator += scores[t];
+        denom_shared = denominator;
+    }
+    __syncthreads();
+    const double denominator = denom_shared;
+    float* dst = out + static_cast<std::uint64_t>(r) * q_heads * head_dim + static_cast<std::uint64_t>(qh) * head_dim;
+    for (std::uint32_t d = threadIdx.x; d < head_dim; d += kThreads) {
+        float acc = 0.0f;
+        for (std::uint64_t t = 0; t < total; ++t) {
+            const float p = static_cast<float>(scores[t] / denominator);
+            const float* slot = kv_slot(g, table, layer, t, true);
+            const float pv = slot ? p * slot[static_cast<std::uint64_t>(kvh) * head_dim + d] : 0.0f;
+            acc = acc + pv;
+        }
+        dst[d] = acc;
+    }
+}
+
+// ---- elementwise -------------------------------------------------------------
+
+// out[r][i] = silu(gate[r][i]) * up[r][i] over fused gate|up rows.
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float* __restrict__ gate_up, float* __restrict__ out,
+                                                            std::uint32_t m, std::uint64_t ffn) {
+#pragma clang fp contract(off)
+    const std::uint64_t total = static_cast<std::uint64_t>(m) * ffn;
+    for (std::uint64_t idx = blockIdx.x * static_cast<std::uint64_t>(kThreads) + threadIdx.x; idx < total;
+         idx += static_cast<std::uint64_t>(gridDim.x) * kThreads) {
+        const std::uint64_t r = idx / ffn, i = idx % ffn;
+        const float g = gate_up[r * 2u * ffn + i];
+        const float u = gate_up[r * 2u * ffn + ffn + i];
+        const float s = g / (1.0f + expf(-g));
+        out[idx] = s * u;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void add_kernel(float* __restrict__ x, const float* __restrict__ y,
+                                                       std::uint64_t count) {
+    for (std::uint64_t i = blockIdx.x * static_cast<std::uint64_t>(kThreads) + threadIdx.x; i < count;
+         i += static_cast<std::uint64_t>(gridDim.x) * kThreads) {
+        x[i] = x[i] + y[i];
+    }
+}
+
+// First maximum of each row (std::max_element with operator<).
+__global__ __launch_bounds__(kThreads) void argmax_kernel(const float* __restrict__ logits, std::uint64_t n,
+                                                          std::int32_t* __restrict__ out) {
+    __shared__ float best_v[kThreads];
+    __shared__ std::uint32_t best_i[kThreads];
+    const float* row = logits + static_cast<std::uint64_t>(blockIdx.x) * n;
+    // Each thread scans a contiguous chunk, keeping its first maximum.
+    const std::uint64_t chunk = (n + kThreads - 1u) / kThreads;
+    const std::uint64_t begin = threadIdx.x * chunk;
+    const std::uint64_t end = begin + chunk < n ? begin + chunk : n;
+    std::uint32_t bi = static_cast<std::uint32_t>(begin < n ? begin : 0u);
+    float bv = begin < n ? row[begin] : 0.0f;
+    bool valid = begin < n;
+    for (std::uint64_t i = begin + 1u; i < end; ++i) {
+        if (bv < row[i]) {
+            bv = row[i];
+            bi = static_cast<std::uint32_t>(i);
+        }
+    }
+    best_v[threadIdx.x] = bv;
+    best_i[threadIdx.x] = valid ? bi : 0xffffffffu;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        // Chunks in index order: a later chunk wins only if strictly greater.
+        float v = best_v[0];
+        std::uint32_t idx = best_i[0];
+        for (unsigned t = 1; t < kThreads; ++t) {
+            if (best_i[t] == 0xffffffffu) break;
+            if (v < best_v[t]) {
+                v = best_v[t];
+                idx = best_i[t];
+            }
+        }
+        out[blockIdx.x] = static_cast<std::int32_t>(idx);
+    }
+}
+
+unsigned grid_for(std::uint64_t work) {
+    const std::uint64_t g = ceil_div(work, kThreads);
+    return static_cast<unsigned>(g < 16384u ? (g ? g : 1u) : 16384u);
+}
+
+} // namespace
+
+hipError_t launch_matrix_rows(const TilePlanes& p, const std::int32_t* rows, std::uint32_t m, float* out,
+                              hipStream_t stream) {
+    const unsigned gx = static_cast<unsigned>(ceil_div(p.k, kThreads) < 64u ? ceil_div(p.k, kThreads) : 64u);
+    hipLaunchKernelGGL(matrix_rows_kernel, dim3(gx, m), dim3(kThreads), 0, stream, p.type, p.codes, p.scales, p.k,
+                       p.n, p.kt, rows, m, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm(const float* x, const float* w, float* out, std::uint32_t m, std::uint64_t n, double eps,
+                           hipStream_t stream) {
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(m), dim3(kThreads), 0, stream, x, w, out, n, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(float* qkv, std::uint64_t stride, std::uint32_t m, const std::int32_t* positions,
+                       std::uint32_t q_heads, std::uint32_t kv_heads, std::uint32_t head_dim, std::uint32_t rope_dims,
+                       const void* table, std::uint64_t table_positions, hipStream_t stream) {
+    const std::uint64_t work = static_cast<std::uint64_t>(m) * (q_heads + kv_heads) * (rope_dims / 2u);
+    hipLaunchKernelGGL(rope_kernel, dim3(grid_for(work)), dim3(kThreads), 0, stream, qkv, stride, m, positions,
+                       q_heads, kv_heads, head_dim, rope_dims, static_cast<const float2*>(table), table_positions);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_append(const KvLayout& kv, const float* qkv, std::uint64_t stride, std::uint64_t q_width,
+                            std::uint32_t m, const std::int32_t* positions, const std::int32_t* tables,
+                            std::uint32_t layer, hipStream_t stream) {
+    const KvGeometry g{kv.pool, kv.page_tokens, kv.kv_width, kv.layers, kv.max_pages, kv.pool_pages};
+    const unsigned gx = static_cast<unsigned>(ceil_div(kv.kv_width, kThreads));
+    hipLaunchKernelGGL(kv_append_kernel, dim3(gx, m), dim3(kThreads), 0, stream, g, qkv, stride, q_width, m,
+                       positions, tables, layer);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention(const KvLayout& kv, const float* qkv, std::uint64_t stride, std::uint32_t m,
+                            const std::int32_t* positions, const std::int32_t* tables, std::uint32_t layer,
+                            std::uint32_t q_heads, std::uint32_t kv_heads, std::uint32_t head_dim, double* scratch,
+                            std::uint64_t score_stride, float* out, hipStream_t stream) {
+    if (head_dim > 512u) return hipErrorInvalidValue;
+    const KvGeometry g{kv.pool, kv.page_tokens, kv.kv_width, kv.layers, kv.max_pages, kv.pool_pages};
+    hipLaunchKernelGGL(attention_kernel, dim3(m * q_heads), dim3(kThreads), 0, stream, g, qkv, stride, m, positions,
+                       tables, layer, q_heads, kv_heads, head_dim, scratch, score_stride, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(const float* gate_up, float* out, std::uint32_t m, std::uint64_t ffn, hipStream_t stream) {
+    hipLaunchKernelGGL(silu_mul_kernel, dim3(grid_for(static_cast<std::uint64_t>(m) * ffn)), dim3(kThreads), 0, stream,
+                       gate_up, out, m, ffn);
+    return hipGetLastError();
+}
+
+hipError_t launch_add(float* x, const float* y, std::uint64_t count, hipStream_t stream) {
+    hipLaunchKernelGGL(add_kernel, dim3(grid_for(count)), dim3(kThreads), 0, stream, x, y, count);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float* logits, std::uint32_t m, std::uint64_t n, std::int32_t* out, hipStream_t stream) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(m), dim3(kThreads), 0, stream, logits, n, out);
+    return hipGetLastError();
+}
+
+} // namespace air_hip

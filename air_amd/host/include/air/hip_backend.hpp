@@ -9,9 +9,9 @@
 // GGUF rows are contiguous, so the fusion is a byte append) when the parts
 // share a format, and their f32 biases are concatenated the same way.
 //
-// The linear engine is the whole of this backend's device work: sequences
-// (KV pages, attention, sampling) are not part of it, so create_sequence
-// and restore_sequence return `unsupported` after validating the plan.
+// Sequences (paged KV, attention, device greedy selection) run on the
+// HipStepEngine of hip_step.hpp, created with the first sequence from the
+// plan's KV page size.  Checkpoints are not provided.
 #pragma once
 
 #include "air/backend.hpp"
@@ -51,7 +51,11 @@ struct HipPrepareOptions {
     void* stream{nullptr};              // hipStream_t the engine launches on
     std::uint32_t max_decode_rows{64};  // workspace reserved for decode widths
     bool fuse{true};                    // concatenate q|k|v and gate|up when formats agree
+    std::uint32_t kv_pool_pages{1024};  // KV pages allocated with the first sequence
+    std::uint32_t max_step_rows{512};   // rows per device step (prefill chunk)
 };
+
+class HipStepEngine;
 
 class HipPreparedModel final : public runtime_detail::PreparedModel {
 public:
@@ -75,8 +79,18 @@ public:
                                                                std::uint64_t max_tokens) const noexcept override;
     [[nodiscard]] std::optional<std::uint64_t> sequence_capacity_bytes() const override;
     [[nodiscard]] std::optional<std::uint64_t> free_device_bytes() const override;
-    [[nodiscard]] std::uint64_t kv_pool_allocated_bytes() const noexcept override { return 0U; }
-    [[nodiscard]] std::uint64_t kv_pool_free_bytes() const noexcept override { return 0U; }
+    [[nodiscard]] std::uint64_t kv_pool_allocated_bytes() const noexcept override;
+    [[nodiscard]] std::uint64_t kv_pool_free_bytes() const noexcept override;
+    [[nodiscard]] Result<runtime_detail::PrefillBatchExecution> prefill_batch(
+        std::span<const runtime_detail::PrefillBatchItem> items) override;
+    [[nodiscard]] Result<std::vector<TokenId>> decode_greedy_batch(
+        std::span<const runtime_detail::GreedyDecodeBatchItem> items) override;
+
+    // The lm_head matrix and whether it is token_embd (tied embeddings).
+    [[nodiscard]] air_hip_matrix* output_matrix() const noexcept { return output_.matrix; }
+    [[nodiscard]] const float* output_bias() const noexcept { return output_.bias; }
+    [[nodiscard]] bool output_is_embedding() const noexcept { return output_is_embedding_; }
+    [[nodiscard]] const HipPrepareOptions& options() const noexcept { return options_; }
 
     // Linear engine.  x: device f32 [rows x K], y: device f32 [rows x N], both
     // row-major; the role's bias (if any) is fused.  Asynchronous on the
@@ -116,7 +130,11 @@ private:
     Linear output_{};
     bool fused_qkv_{false};
     bool fused_gate_up_{false};
+    bool output_is_embedding_{false};
     std::uint64_t bias_bytes_{0};
+    HipPrepareOptions options_{};
+    std::unique_ptr<HipStepEngine> engine_;
+    [[nodiscard]] Result<HipStepEngine*> engine_for(const ExecutionPlan& plan);
 };
 
 // Paged fp32 K and V of every layer for max_tokens plus the two page tables,

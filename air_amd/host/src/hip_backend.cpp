@@ -6,6 +6,7 @@
 // (src/runtime/backend.cpp:268-306, 511-560), with device memory read from
 // hipMemGetInfo through air_hip_mem_info.
 #include "air/hip_backend.hpp"
+#include "air/hip_step.hpp"
 
 #include "air_hip.h"
 
@@ -72,7 +73,7 @@ HipPreparedModel::HipPreparedModel(std::shared_ptr<const ModelDefinition> model,
     capabilities_.max_decode_batch_width = AIR_HIP_MAX_DECODE_ROWS;
     capabilities_.sequence_checkpointing = false;
     capabilities_.exact_prefix_reuse = false;
-    capabilities_.device_greedy_selection = false;
+    capabilities_.device_greedy_selection = true;
     // Tactics per scope, each naming real device work: the exact-code decode
     // linear serves every width; the f16 MFMA GEMM serves prefill blocks.
     capabilities_.prefill_block_quantized_linear = {QuantizedLinearExecutionKind::hip_decode,
@@ -82,6 +83,7 @@ HipPreparedModel::HipPreparedModel(std::shared_ptr<const ModelDefinition> model,
 }
 
 HipPreparedModel::~HipPreparedModel() {
+    engine_.reset();  // its buffers and embedding live on this model's context
     for (auto& layer : layers_) {
         for (Linear* l : {&layer.qkv, &layer.q, &layer.k, &layer.v, &layer.o, &layer.gate_up, &layer.gate, &layer.up,
                           &layer.down}) {
@@ -179,6 +181,7 @@ Result<std::unique_ptr<HipPreparedModel>> HipPreparedModel::create(std::shared_p
     }
 
     std::unique_ptr<HipPreparedModel> prepared(new HipPreparedModel(model, options.device));
+    prepared->options_ = options;
     if (const int rc = air_hip_context_create(options.device, options.stream, &prepared->ctx_); rc != AIR_HIP_OK) {
         return hip_status(rc);
     }
@@ -237,7 +240,10 @@ Result<std::unique_ptr<HipPreparedModel>> HipPreparedModel::create(std::shared_p
         if (!(s = prepared->make_linear(down, {none, 1}, layer.down))) return s;
     }
     const TensorDescriptor* out[] = {model->find_tensor("output.weight")};
-    if (!out[0]) out[0] = model->find_tensor("token_embd.weight");  // tied embeddings
+    if (!out[0]) {
+        out[0] = model->find_tensor("token_embd.weight");  // tied embeddings
+        prepared->output_is_embedding_ = true;
+    }
     const TensorDescriptor* out_bias[] = {model->find_tensor("output.bias")};
     if (Status s = prepared->make_linear(out, out_bias, prepared->output_); !s) return s;
     if (Status s = prepared->synchronize(); !s) return s;
@@ -290,16 +296,136 @@ Status HipPreparedModel::linear(std::uint32_t layer, LinearRole role, const floa
     return hip_status(air_hip_linear(ctx_, l->matrix, x, y, l->bias, rows, t));
 }
 
-Status HipPreparedModel::set_stream(void* stream) { return hip_status(air_hip_context_set_stream(ctx_, stream)); }
+Status HipPreparedModel::set_stream(void* stream) {
+    if (Status s = hip_status(air_hip_context_set_stream(ctx_, stream)); !s) return s;
+    options_.stream = stream;
+    return Status::ok();
+}
 
 Status HipPreparedModel::synchronize() const {
     if (Status s = runtime_status(hipSetDevice(device_), "hipSetDevice"); !s) return s;
     return runtime_status(hipDeviceSynchronize(), "hipDeviceSynchronize");
 }
 
+Result<HipStepEngine*> HipPreparedModel::engine_for(const ExecutionPlan& plan) {
+    const std::uint32_t page_tokens = plan.kv.page_tokens.value_or(0U);
+    if (page_tokens == 0U) return Status::invalid_argument("HIP sequences need a KV page size");
+    if (engine_) {
+        if (engine_->page_tokens() != page_tokens) {
+            return Status::invalid_argument("HIP KV pool already uses " + std::to_string(engine_->page_tokens()) +
+                                            "-token pages");
+        }
+        return engine_.get();
+    }
+    auto engine = HipStepEngine::create(*this, page_tokens, options_.kv_pool_pages, options_.max_step_rows);
+    if (!engine) return engine.status();
+    engine_ = std::move(engine).value();
+    return engine_.get();
+}
+
 Result<std::unique_ptr<runtime_detail::SequenceState>> HipPreparedModel::create_sequence(const ExecutionPlan& plan) {
     if (Status s = validate_execution_plan(plan, capabilities_); !s) return s;
-    return Status::unsupported("the HIP backend provides the linear engine only; sequence execution is not built");
+    auto engine = engine_for(plan);
+    if (!engine) return engine.status();
+    return std::unique_ptr<runtime_detail::SequenceState>(std::make_unique<HipSequence>(
+        *engine.value(), plan.linear.prefill_block, plan.linear.decode_block, plan.linear.decode_output));
+}
+
+std::uint64_t HipPreparedModel::kv_pool_allocated_bytes() const noexcept {
+    return engine_ ? engine_->pool_bytes() : 0U;
+}
+
+std::uint64_t HipPreparedModel::kv_pool_free_bytes() const noexcept {
+    return engine_ ? engine_->free_pool_bytes() : 0U;
+}
+
+// Rows of every item packed into device steps of up to max_step_rows rows (a
+// sequence's prompt may span steps; its rows stay in order).  A step runs one
+// tactic pair, so a change of tactics between items starts a new step.
+Result<runtime_detail::PrefillBatchExecution> HipPreparedModel::prefill_batch(
+    std::span<const runtime_detail::PrefillBatchItem> items) {
+    runtime_detail::PrefillBatchExecution execution;
+    execution.items.resize(items.size());
+    if (items.empty()) return execution;
+    if (!engine_) return Status::invalid_state("no HIP sequence has been created");
+    for (const auto& item : items) {
+        if (!dynamic_cast<HipSequence*>(item.sequence)) return Status::invalid_argument("prefill item is not a HIP sequence");
+        if (item.tokens.empty()) return Status::invalid_argument("prefill requires at least one token");
+    }
+    HipStepEngine* engine = engine_.get();
+    std::vector<StepRow> rows;
+    std::vector<std::size_t> owner;  // item of each row with an output
+    QuantizedLinearExecutionKind block = QuantizedLinearExecutionKind::hip_decode;
+    QuantizedLinearExecutionKind output = QuantizedLinearExecutionKind::hip_decode;
+    const auto flush = [&]() -> Status {
+        if (rows.empty()) return Status::ok();
+        auto result = engine->run(rows, block, output);
+        if (!result) return result.status();
+        std::size_t g = 0, l = 0, o = 0;
+        for (const auto& row : rows) {
+            if (row.output == RowOutput::none) continue;
+            auto& item = execution.items[owner[o++]];
+            if (row.output == RowOutput::greedy) item.greedy_token = result.value().greedy[g++];
+            if (row.output == RowOutput::logits) item.logits = std::move(result.value().logits[l++]);
+        }
+        ++execution.physical_batches;
+        execution.physical_tokens += rows.size();
+        rows.clear();
+        owner.clear();
+        return Status::ok();
+    };
+    std::uint32_t sequences = 0;
+    for (std::size_t i = 0; i < items.size(); ++i) {
+        auto* seq = static_cast<HipSequence*>(items[i].sequence);
+        if (!rows.empty() && (seq->prefill_block_tactic() != block || seq->decode_output_tactic() != output)) {
+            if (Status s = flush(); !s) return s;
+        }
+        block = seq->prefill_block_tactic();
+        output = seq->decode_output_tactic();
+        ++sequences;
+        for (std::size_t t = 0; t < items[i].tokens.size(); ++t) {
+            StepRow row{seq, items[i].tokens[t], RowOutput::none};
+            if (t + 1 == items[i].tokens.size()) {
+                row.output = items[i].output == runtime_detail::PrefillBatchOutput::greedy   ? RowOutput::greedy
+                             : items[i].output == runtime_detail::PrefillBatchOutput::logits ? RowOutput::logits
+                                                                                             : RowOutput::none;
+                if (row.output != RowOutput::none) owner.push_back(i);
+            }
+            rows.push_back(row);
+            if (rows.size() == engine->max_rows()) {
+                if (Status s = flush(); !s) return s;
+            }
+        }
+        ++execution.physical_sequence_participations;
+    }
+    if (Status s = flush(); !s) return s;
+    execution.max_sequences = sequences;
+    return execution;
+}
+
+Result<std::vector<TokenId>> HipPreparedModel::decode_greedy_batch(
+    std::span<const runtime_detail::GreedyDecodeBatchItem> items) {
+    if (items.empty()) return std::vector<TokenId>{};
+    if (!engine_) return Status::invalid_state("no HIP sequence has been created");
+    if (items.size() > capabilities_.max_decode_batch_width) {
+        return Status::invalid_argument("decode batch exceeds the advertised width");
+    }
+    std::vector<StepRow> rows;
+    QuantizedLinearExecutionKind block = QuantizedLinearExecutionKind::hip_decode;
+    QuantizedLinearExecutionKind output = QuantizedLinearExecutionKind::hip_decode;
+    for (const auto& item : items) {
+        auto* seq = dynamic_cast<HipSequence*>(item.sequence);
+        if (!seq) return Status::invalid_argument("decode item is not a HIP sequence");
+        for (const auto& row : rows) {
+            if (row.sequence == seq) return Status::invalid_argument("a sequence appears twice in a decode batch");
+        }
+        block = seq->decode_block_tactic();
+        output = seq->decode_output_tactic();
+        rows.push_back({seq, item.token, RowOutput::greedy});
+    }
+    auto result = engine_->run(rows, block, output);
+    if (!result) return result.status();
+    return std::move(result.value().greedy);
 }
 
 Result<std::unique_ptr<runtime_detail::SequenceState>> HipPreparedModel::restore_sequence(
@@ -308,13 +434,14 @@ Result<std::unique_ptr<runtime_detail::SequenceState>> HipPreparedModel::restore
     if (checkpoint.backend() != BackendKind::hip) {
         return Status::invalid_argument("HIP backend cannot restore a checkpoint from another backend");
     }
-    return Status::unsupported("the HIP backend provides the linear engine only; sequence execution is not built");
+    return Status::unsupported("HIP sequences do not provide checkpoints");
 }
 
 std::uint64_t HipPreparedModel::resident_device_bytes() const noexcept {
     air_hip_stats stats{};
     if (air_hip_context_stats(ctx_, &stats) != AIR_HIP_OK) return bias_bytes_;
-    return stats.resident_matrix_bytes + stats.workspace_bytes + bias_bytes_;
+    return stats.resident_matrix_bytes + stats.workspace_bytes + bias_bytes_ +
+           (engine_ ? engine_->resident_bytes() : 0U);
 }
 
 std::uint64_t HipPreparedModel::estimate_sequence_device_bytes(const ExecutionPlan& plan,

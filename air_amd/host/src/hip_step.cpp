@@ -1,0 +1,575 @@
+// hip_step.cpp -- HipStepEngine and HipSequence: the Qwen2 step on one GPU.
+//
+// Per step the host validates the rows, reserves KV pages, uploads tokens,
+// positions and page tables through one pinned staging copy, issues the
+// layer loop through the air_hip C ABI on the model's stream and reads back
+// only what the rows asked for (greedy ids, or logits rows).  The step
+// follows ReferenceExecutor::step_impl (src/reference/reference_executor.cpp:
+// 325-428) operation by operation; its validation messages are the
+// reference's (reference_executor.cpp:328-335).
+#include "air/hip_step.hpp"
+
+#include "air/synthetic.hpp"
+#include "air_hip.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+namespace air {
+
+namespace {
+
+Status runtime_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return Status::ok();
+    return Status::internal_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// f32 (or f16) norm vector of `width` values, as ReferenceTensorReader::vector
+// decodes it (tensor_reader.cpp:325-345).
+Result<std::vector<float>> norm_vector(const ModelDefinition& model, const std::string& name, std::uint64_t width) {
+    const auto* t = model.find_tensor(name);
+    if (!t) return Status::data_error("missing tensor: " + name);
+    if (t->shape.element_count() != width) return Status::data_error("norm width mismatch: " + name);
+    auto bytes = model.tensor_bytes(*t);
+    if (!bytes) return bytes.status();
+    std::vector<float> out(width);
+    if (t->format_type == static_cast<std::uint32_t>(GgmlType::f32) && bytes.value().size() == width * 4U) {
+        std::memcpy(out.data(), bytes.value().data(), width * 4U);
+    } else if (t->format_type == static_cast<std::uint32_t>(GgmlType::f16) && bytes.value().size() == width * 2U) {
+        for (std::uint64_t i = 0; i < width; ++i) {
+            std::uint16_t h = 0;
+            std::memcpy(&h, bytes.value().data() + 2U * i, 2U);
+            out[i] = f16_bits_to_f32(h);
+        }
+    } else {
+        return Status::unsupported("norm weights must be f32 or f16: " + name);
+    }
+    return out;
+}
+
+} // namespace
+
+// ---- HipSequence ------------------------------------------------------------
+
+HipSequence::HipSequence(HipStepEngine& engine, QuantizedLinearExecutionKind prefill_block,
+                         QuantizedLinearExecutionKind decode_block, QuantizedLinearExecutionKind decode_output)
+    : engine_(engine), prefill_block_(prefill_block), decode_block_(decode_block), decode_output_(decode_output) {}
+
+HipSequence::~HipSequence() { engine_.release_pages(pages_); }
+
+namespace {
+
+std::vector<StepRow> prompt_rows(HipSequence* seq, std::span<const TokenId> tokens, RowOutput last) {
+    std::vector<StepRow> rows(tokens.size());
+    for (std::size_t i = 0; i < tokens.size(); ++i) rows[i] = StepRow{seq, tokens[i], RowOutput::none};
+    if (!rows.empty()) rows.back().output = last;
+    return rows;
+}
+
+} // namespace
+
+// A prompt longer than the engine's step width runs as consecutive steps.
+Result<std::vector<float>> HipSequence::prefill(std::span<const TokenId> tokens) {
+    if (tokens.empty()) return Status::invalid_argument("prefill requires at least one token");
+    std::vector<float> logits;
+    const std::size_t width = engine_.max_rows();
+    for (std::size_t begin = 0; begin < tokens.size(); begin += width) {
+        const std::size_t count = std::min(width, tokens.size() - begin);
+        const bool last = begin + count == tokens.size();
+        auto rows = prompt_rows(this, tokens.subspan(begin, count), last ? RowOutput::logits : RowOutput::none);
+        auto result = engine_.run(rows, prefill_block_, decode_output_);
+        if (!result) return result.status();
+        if (last) logits = std::move(result.value().logits.front());
+    }
+    return logits;
+}
+
+Status HipSequence::prefill_discard(std::span<const TokenId> tokens) {
+    if (tokens.empty()) return Status::invalid_argument("prefill requires at least one token");
+    const std::size_t width = engine_.max_rows();
+    for (std::size_t begin = 0; begin < tokens.size(); begin += width) {
+        const std::size_t count = std::min(width, tokens.size() - begin);
+        auto rows = prompt_rows(this, tokens.subspan(begin, count), RowOutput::none);
+        auto result = engine_.run(rows, prefill_block_, decode_output_);
+        if (!result) return result.status();
+    }
+    return Status::ok();
+}
+
+Result<TokenId> HipSequence::prefill_greedy(std::span<const TokenId> tokens) {
+    if (tokens.empty()) return Status::invalid_argument("prefill requires at least one token");
+    TokenId token = 0;
+    const std::size_t width = engine_.max_rows();
+    for (std::size_t begin = 0; begin < tokens.size(); begin += width) {
+        const std::size_t count = std::min(width, tokens.size() - begin);
+        const bool last = begin + count == tokens.size();
+        auto rows = prompt_rows(this, tokens.subspan(begin, count), last ? RowOutput::greedy : RowOutput::none);
+        auto result = engine_.run(rows, prefill_block_, decode_output_);
+        if (!result) return result.status();
+        if (last) token = result.value().greedy.front();
+    }
+    return token;
+}
+
+Result<std::vector<float>> HipSequence::decode(TokenId token) {
+    const StepRow row{this, token, RowOutput::logits};
+    auto result = engine_.run({&row, 1}, decode_block_, decode_output_);
+    if (!result) return result.status();
+    return std::move(result.value().logits.front());
+}
+
+Result<TokenId> HipSequence::decode_greedy(TokenId token) {
+    const StepRow row{this, token, RowOutput::greedy};
+    auto result = engine_.run({&row, 1}, decode_block_, decode_output_);
+    if (!result) return result.status();
+    return result.value().greedy.front();
+}
+
+runtime_detail::SequenceResources HipSequence::resources() const noexcept {
+    const std::uint64_t kv = static_cast<std::uint64_t>(pages_.size()) * engine_.page_bytes();
+    return {tokens_, kv, kv};
+}
+
+Result<std::unique_ptr<runtime_detail::SequenceCheckpoint>> HipSequence::checkpoint() const {
+    return Status::unsupported("HIP sequences do not provide checkpoints");
+}
+
+// ---- HipStepEngine ---------------------------------------------------------
+
+Status HipStepEngine::allocate(void** ptr, std::uint64_t bytes, const char* what) {
+    *ptr = nullptr;
+    if (bytes == 0U) return Status::ok();
+    if (Status s = runtime_status(hipMalloc(ptr, bytes), what); !s) return s;
+    allocations_.push_back(*ptr);
+    resident_bytes_ += bytes;
+    return Status::ok();
+}
+
+HipStepEngine::~HipStepEngine() {
+    (void)hipSetDevice(prepared_.device());
+    (void)hipStreamSynchronize(static_cast<hipStream_t>(stream()));
+    for (void* p : allocations_) (void)hipFree(p);
+    if (staging_) (void)hipHostFree(staging_);
+    if (owns_embedding_ && embedding_) air_hip_matrix_release(embedding_);
+}
+
+Result<std::unique_ptr<HipStepEngine>> HipStepEngine::create(const HipPreparedModel& prepared,
+                                                             std::uint32_t page_tokens, std::uint32_t pool_pages,
+                                                             std::uint32_t max_rows) {
+    const auto& model = prepared.model();
+    const auto& c = model.config();
+    if (page_tokens == 0U) return Status::invalid_argument("KV page size must be non-zero");
+    if (pool_pages == 0U) return Status::invalid_argument("KV pool must hold at least one page");
+    if (pool_pages > static_cast<std::uint32_t>(INT32_MAX)) return Status::invalid_argument("KV pool is too large");
+    if (max_rows == 0U || max_rows > 4096U) return Status::invalid_argument("step width must be in [1, 4096]");
+    if (c.attention_head_count == 0U || c.embedding_size % c.attention_head_count != 0U) {
+        return Status::data_error("embedding width must divide into the attention heads");
+    }
+    const std::uint32_t head_dim = c.embedding_size / c.attention_head_count;
+    if (c.kv_head_count == 0U || c.attention_head_count % c.kv_head_count != 0U) {
+        return Status::data_error("attention heads must be a multiple of the KV heads");
+    }
+    if (c.rope_dimension_count == 0U || c.rope_dimension_count > head_dim || c.rope_dimension_count % 2U != 0U) {
+        return Status::invalid_state("Qwen2 reference executor requires an even RoPE dimension within each head");
+    }
+    if (!(c.rope_frequency_base > 0.0)) {
+        return Status::invalid_state("Qwen2 reference executor requires a positive RoPE base");
+    }
+    if (head_dim > 512U) return Status::unsupported("HIP attention supports head widths up to 512");
+    if (c.context_length == 0U || c.context_length > static_cast<std::uint64_t>(INT32_MAX)) {
+        return Status::unsupported("context length must be in [1, 2^31)");
+    }
+
+    std::unique_ptr<HipStepEngine> e(new HipStepEngine(prepared));
+    e->page_tokens_ = page_tokens;
+    e->pool_pages_ = pool_pages;
+    e->max_rows_ = max_rows;
+    e->max_pages_ = static_cast<std::uint32_t>((c.context_length + page_tokens - 1U) / page_tokens);
+    e->output_rows_ = std::min<std::uint32_t>(max_rows, AIR_HIP_MAX_DECODE_ROWS);
+    e->embed_ = c.embedding_size;
+    e->head_dim_ = head_dim;
+    e->q_width_ = c.attention_head_count * head_dim;
+    e->kv_width_ = c.kv_head_count * head_dim;
+    e->qkv_width_ = e->q_width_ + 2U * e->kv_width_;
+    e->ffn_ = c.feed_forward_size;
+    e->vocab_ = c.vocabulary_size;
+    e->page_bytes_ = static_cast<std::uint64_t>(c.layer_count) * 2U * page_tokens * e->kv_width_ * sizeof(float);
+
+    if (Status s = runtime_status(hipSetDevice(prepared.device()), "hipSetDevice"); !s) return s;
+    const auto upload = [&](float** dst, const std::vector<float>& host, const char* what) -> Status {
+        if (Status s = e->allocate(reinterpret_cast<void**>(dst), host.size() * sizeof(float), what); !s) return s;
+        return runtime_status(hipMemcpy(*dst, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice), what);
+    };
+
+    // Norm weights.
+    e->attn_norm_.assign(c.layer_count, nullptr);
+    e->ffn_norm_.assign(c.layer_count, nullptr);
+    for (std::uint32_t l = 0; l < c.layer_count; ++l) {
+        auto attn = norm_vector(model, block_tensor_name(l, "attn_norm.weight"), c.embedding_size);
+        if (!attn) return attn.status();
+        if (Status s = upload(&e->attn_norm_[l], attn.value(), "hipMalloc(attn_norm)"); !s) return s;
+        auto ffn = norm_vector(model, block_tensor_name(l, "ffn_norm.weight"), c.embedding_size);
+        if (!ffn) return ffn.status();
+        if (Status s = upload(&e->ffn_norm_[l], ffn.value(), "hipMalloc(ffn_norm)"); !s) return s;
+    }
+    auto out_norm = norm_vector(model, "output_norm.weight", c.embedding_size);
+    if (!out_norm) return out_norm.status();
+    if (Status s = upload(&e->output_norm_, out_norm.value(), "hipMalloc(output_norm)"); !s) return s;
+
+    // RoPE table: the reference's double angle per (position, pair), rounded
+    // to float cos / sin (reference_executor.cpp:53-60).  1 / pow(base, 2i/d)
+    // depends on i only, so it is computed once per pair with the same
+    // expression.
+    {
+        const std::uint32_t half = c.rope_dimension_count / 2U;
+        std::vector<double> inverse(half);
+        for (std::uint32_t i = 0; i < half; ++i) {
+            const double exponent = (2.0 * static_cast<double>(i)) / static_cast<double>(c.rope_dimension_count);
+            inverse[i] = 1.0 / std::pow(c.rope_frequency_base, exponent);
+        }
+        std::vector<float> table(static_cast<std::size_t>(c.context_length) * half * 2U);
+        for (std::uint64_t p = 0; p < c.context_length; ++p) {
+            for (std::uint32_t i = 0; i < half; ++i) {
+                const double angle = static_cast<double>(p) * inverse[i];
+                table[(p * half + i) * 2U] = static_cast<float>(std::cos(angle));
+                table[(p * half + i) * 2U + 1U] = static_cast<float>(std::sin(angle));
+            }
+        }
+        if (Status s = upload(&e->rope_table_, table, "hipMalloc(rope)"); !s) return s;
+    }
+
+    // Embedding rows come from the resident token_embd matrix (the output
+    // matrix itself when the model ties them).
+    if (prepared.output_is_embedding()) {
+        e->embedding_ = prepared.output_matrix();
+    } else {
+        const auto* t = model.find_tensor("token_embd.weight");
+        if (!t) return Status::data_error("missing tensor: token_embd.weight");
+        if (t->shape.dimensions.size() != 2U || t->shape.dimensions[0] != c.embedding_size ||
+            t->shape.dimensions[1] != c.vocabulary_size) {
+            return Status::data_error("token_embd.weight must be {embedding, vocabulary}");
+        }
+        auto bytes = model.tensor_bytes(*t);
+        if (!bytes) return bytes.status();
+        air_hip_matrix* m = nullptr;
+        const int rc = air_hip_matrix_prepare(prepared.context(), static_cast<int>(t->format_type),
+                                              t->shape.dimensions[0], t->shape.dimensions[1],
+                                              bytes.value().data(), bytes.value().size(), 0, &m);
+        if (rc != AIR_HIP_OK) return hip_status(rc);
+        e->embedding_ = m;
+        e->owns_embedding_ = true;
+        air_hip_matrix_desc desc{};
+        if (air_hip_matrix_describe(m, &desc) == AIR_HIP_OK) e->resident_bytes_ += desc.resident_bytes;
+    }
+
+    // KV pool, zeroed once.
+    if (Status s = e->allocate(reinterpret_cast<void**>(&e->pool_), e->page_bytes_ * pool_pages, "hipMalloc(kv pool)");
+        !s) {
+        return s;
+    }
+    if (Status s = runtime_status(hipMemset(e->pool_, 0, e->page_bytes_ * pool_pages), "hipMemset(kv pool)"); !s) {
+        return s;
+    }
+    e->free_pages_.resize(pool_pages);
+    for (std::uint32_t i = 0; i < pool_pages; ++i) e->free_pages_[i] = static_cast<std::int32_t>(pool_pages - 1U - i);
+
+    // Step buffers.
+    const std::uint64_t rows = max_rows;
+    const auto buffer = [&](float** dst, std::uint64_t floats, const char* what) {
+        return e->allocate(reinterpret_cast<void**>(dst), floats * sizeof(float), what);
+    };
+    Status s;
+    if (!(s = buffer(&e->hidden_, rows * e->embed_, "hipMalloc(hidden)"))) return s;
+    if (!(s = buffer(&e->normed_, rows * e->embed_, "hipMalloc(normed)"))) return s;
+    if (!(s = buffer(&e->qkv_, rows * e->qkv_width_, "hipMalloc(qkv)"))) return s;
+    if (!(s = buffer(&e->att_, rows * e->q_width_, "hipMalloc(attention)"))) return s;
+    if (!(s = buffer(&e->proj_, rows * e->embed_, "hipMalloc(projection)"))) return s;
+    if (!(s = buffer(&e->gate_up_, rows * 2U * e->ffn_, "hipMalloc(gate_up)"))) return s;
+    if (!(s = buffer(&e->act_, rows * e->ffn_, "hipMalloc(activation)"))) return s;
+    if (!prepared.fused_qkv() || !prepared.fused_gate_up()) {
+        const std::uint64_t widest = std::max<std::uint64_t>({e->q_width_, e->kv_width_, e->ffn_});
+        if (!(s = buffer(&e->part_, rows * widest, "hipMalloc(parts)"))) return s;
+    }
+    if (!(s = buffer(&e->final_, static_cast<std::uint64_t>(e->output_rows_) * e->embed_, "hipMalloc(final)"))) {
+        return s;
+    }
+    if (!(s = buffer(&e->logits_, static_cast<std::uint64_t>(e->output_rows_) * e->vocab_, "hipMalloc(logits)"))) {
+        return s;
+    }
+    const std::uint64_t ints = rows * (2U + e->max_pages_);
+    if (!(s = e->allocate(reinterpret_cast<void**>(&e->tokens_dev_), ints * sizeof(std::int32_t), "hipMalloc(rows)"))) {
+        return s;
+    }
+    e->positions_dev_ = e->tokens_dev_ + rows;
+    e->tables_dev_ = e->positions_dev_ + rows;
+    if (!(s = e->allocate(reinterpret_cast<void**>(&e->argmax_dev_), e->output_rows_ * sizeof(std::int32_t),
+                          "hipMalloc(argmax)"))) {
+        return s;
+    }
+    void* pinned = nullptr;
+    if (!(s = runtime_status(hipHostMalloc(&pinned, (ints + e->output_rows_) * sizeof(std::int32_t)),
+                             "hipHostMalloc(staging)"))) {
+        return s;
+    }
+    e->staging_ = static_cast<std::int32_t*>(pinned);
+    return e;
+}
+
+std::uint64_t HipStepEngine::free_pool_bytes() const noexcept {
+    std::lock_guard<std::mutex> lock(pool_mutex_);
+    return static_cast<std::uint64_t>(free_pages_.size()) * page_bytes_;
+}
+
+void HipStepEngine::release_pages(std::vector<std::int32_t>& pages) {
+    std::lock_guard<std::mutex> lock(pool_mutex_);
+    free_pages_.insert(free_pages_.end(), pages.rbegin(), pages.rend());
+    pages.clear();
+}
+
+// q|k|v (or gate|up) of `m` rows into y with row stride sum(widths): the
+// fused matrix in one linear, otherwise each part into `part_` and a strided
+// copy into its columns.
+Status HipStepEngine::project(std::uint32_t layer, LinearRole fused, LinearRole first, LinearRole second,
+                              LinearRole third, const float* x, float* y, std::uint32_t m,
+                              QuantizedLinearExecutionKind tactic) {
+    const bool is_fused = fused == LinearRole::attn_qkv ? prepared_.fused_qkv() : prepared_.fused_gate_up();
+    if (is_fused) return prepared_.linear(layer, fused, x, y, m, tactic);
+    const LinearRole parts[] = {first, second, third};
+    const std::size_t count = fused == LinearRole::attn_qkv ? 3U : 2U;
+    std::uint64_t widths[3] = {0, 0, 0}, total = 0;
+    for (std::size_t i = 0; i < count; ++i) {
+        auto info = prepared_.linear_info(layer, parts[i]);
+        if (!info) return info.status();
+        widths[i] = info.value().n;
+        total += widths[i];
+    }
+    std::uint64_t offset = 0;
+    for (std::size_t i = 0; i < count; ++i) {
+        if (Status s = prepared_.linear(layer, parts[i], x, part_, m, tactic); !s) return s;
+        const hipError_t err = hipMemcpy2DAsync(y + offset, total * sizeof(float), part_, widths[i] * sizeof(float),
+                                                widths[i] * sizeof(float), m, hipMemcpyDeviceToDevice,
+                                                static_cast<hipStream_t>(stream()));
+        if (Status s = runtime_status(err, "hipMemcpy2DAsync(parts)"); !s) return s;
+        offset += widths[i];
+    }
+    return Status::ok();
+}
+
+// Embedding through the last layer's residual for `m` uploaded rows.
+Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uint32_t table_pages,
+                             QuantizedLinearExecutionKind tactic) {
+    const auto& c = prepared_.model().config();
+    air_hip_context* ctx = prepared_.context();
+    const air_hip_kv_layout kv{pool_, page_tokens_, kv_width_, c.layer_count, table_pages, pool_pages_};
+    const std::uint64_t hidden_floats = static_cast<std::uint64_t>(m) * embed_;
+    int rc = air_hip_matrix_rows(ctx, embedding_, tokens_dev_, m, hidden_);
+    if (rc != AIR_HIP_OK) return hip_status(rc);
+    for (std::uint32_t l = 0; l < c.layer_count; ++l) {
+        if ((rc = air_hip_rms_norm(ctx, hidden_, attn_norm_[l], normed_, m, embed_, c.rms_norm_epsilon)) != AIR_HIP_OK) {
+            return hip_status(rc);
+        }
+        if (Status s = project(l, LinearRole::attn_qkv, LinearRole::attn_q, LinearRole::attn_k, LinearRole::attn_v,
+                               normed_, qkv_, m, tactic);
+            !s) {
+            return s;
+        }
+        if ((rc = air_hip_rope(ctx, qkv_, qkv_width_, m, positions_dev_, c.attention_head_count, c.kv_head_count,
+                               head_dim_, c.rope_dimension_count, rope_table_, c.context_length)) != AIR_HIP_OK) {
+            return hip_status(rc);
+        }
+        if ((rc = air_hip_kv_append(ctx, &kv, qkv_, qkv_width_, q_width_, m, positions_dev_, tables_dev_, l)) !=
+            AIR_HIP_OK) {
+            return hip_status(rc);
+        }
+        if ((rc = air_hip_attention(ctx, &kv, qkv_, qkv_width_, m, positions_dev_, tables_dev_, l,
+                                    c.attention_head_count, c.kv_head_count, head_dim_, max_tokens, att_)) !=
+            AIR_HIP_OK) {
+            return hip_status(rc);
+        }
+        if (Status s = prepared_.linear(l, LinearRole::attn_output, att_, proj_, m, tactic); !s) return s;
+        if ((rc = air_hip_add(ctx, hidden_, proj_, hidden_floats)) != AIR_HIP_OK) return hip_status(rc);
+        if ((rc = air_hip_rms_norm(ctx, hidden_, ffn_norm_[l], normed_, m, embed_, c.rms_norm_epsilon)) != AIR_HIP_OK) {
+            return hip_status(rc);
+        }
+        if (Status s = project(l, LinearRole::ffn_gate_up, LinearRole::ffn_gate, LinearRole::ffn_up,
+                               LinearRole::ffn_up, normed_, gate_up_, m, tactic);
+            !s) {
+            return s;
+        }
+        if ((rc = air_hip_silu_mul(ctx, gate_up_, act_, m, ffn_)) != AIR_HIP_OK) return hip_status(rc);
+        if (Status s = prepared_.linear(l, LinearRole::ffn_down, act_, proj_, m, tactic); !s) return s;
+        if ((rc = air_hip_add(ctx, hidden_, proj_, hidden_floats)) != AIR_HIP_OK) return hip_status(rc);
+    }
+    return Status::ok();
+}
+
+Result<StepResult> HipStepEngine::run(std::span<const StepRow> rows, QuantizedLinearExecutionKind block_tactic,
+                                      QuantizedLinearExecutionKind output_tactic) {
+    const auto& c = prepared_.model().config();
+    if (rows.empty()) return Status::invalid_argument("a step needs at least one row");
+    if (rows.size() > max_rows_) {
+        return Status::invalid_argument("step of " + std::to_string(rows.size()) + " rows exceeds the engine width " +
+                                        std::to_string(max_rows_));
+    }
+    const auto m = static_cast<std::uint32_t>(rows.size());
+
+    // Positions: each sequence's next tokens in row order.
+    struct Claim {
+        HipSequence* sequence;
+        std::uint64_t rows;
+        std::size_t pages_before;
+    };
+    std::vector<Claim> claims;
+    std::vector<std::uint64_t> positions(m);
+    std::vector<std::size_t> claim_of(m);
+    for (std::uint32_t r = 0; r < m; ++r) {
+        HipSequence* seq = rows[r].sequence;
+        if (!seq || &seq->engine_ != this) return Status::invalid_argument("row belongs to another engine");
+        const TokenId token = rows[r].token;
+        if (token < 0 || static_cast<std::uint64_t>(token) >= c.vocabulary_size) {
+            return Status::invalid_argument("input token is outside model vocabulary");
+        }
+        auto it = std::find_if(claims.begin(), claims.end(), [&](const Claim& x) { return x.sequence == seq; });
+        if (it == claims.end()) {
+            claims.push_back({seq, 0U, seq->pages_.size()});
+            it = claims.end() - 1;
+        }
+        positions[r] = seq->tokens_ + it->rows;
+        if (positions[r] >= c.context_length) return Status::invalid_state("model context length exceeded");
+        ++it->rows;
+        claim_of[r] = static_cast<std::size_t>(it - claims.begin());
+    }
+
+    // Pages for the new tokens; returned on any failure below.
+    const auto rollback = [&]() {
+        std::lock_guard<std::mutex> lock(pool_mutex_);
+        for (auto& claim : claims) {
+            auto& pages = claim.sequence->pages_;
+            while (pages.size() > claim.pages_before) {
+                free_pages_.push_back(pages.back());
+                pages.pop_back();
+            }
+        }
+    };
+    std::uint32_t table_pages = 1U;
+    {
+        std::lock_guard<std::mutex> lock(pool_mutex_);
+        std::uint64_t needed = 0;
+        for (const auto& claim : claims) {
+            const std::uint64_t pages = (claim.sequence->tokens_ + claim.rows + page_tokens_ - 1U) / page_tokens_;
+            needed += pages - std::min<std::uint64_t>(pages, claim.sequence->pages_.size());
+            table_pages = std::max<std::uint32_t>(table_pages, static_cast<std::uint32_t>(pages));
+        }
+        if (needed > free_pages_.size()) {
+            return Status::invalid_state("HIP KV page pool exhausted: " + std::to_string(needed) + " pages needed, " +
+                                         std::to_string(free_pages_.size()) + " free");
+        }
+        for (auto& claim : claims) {
+            const std::uint64_t pages = (claim.sequence->tokens_ + claim.rows + page_tokens_ - 1U) / page_tokens_;
+            while (claim.sequence->pages_.size() < pages) {
+                claim.sequence->pages_.push_back(free_pages_.back());
+                free_pages_.pop_back();
+            }
+        }
+    }
+
+    // Upload: tokens | positions | page tables [m][table_pages], one copy.
+    std::int32_t* host = staging_;
+    std::uint64_t max_tokens = 1U;
+    for (std::uint32_t r = 0; r < m; ++r) {
+        host[r] = rows[r].token;
+        host[m + r] = static_cast<std::int32_t>(positions[r]);
+        max_tokens = std::max<std::uint64_t>(max_tokens, positions[r] + 1U);
+        const auto& pages = claims[claim_of[r]].sequence->pages_;
+        std::int32_t* table = host + 2U * m + static_cast<std::uint64_t>(r) * table_pages;
+        for (std::uint32_t p = 0; p < table_pages; ++p) table[p] = p < pages.size() ? pages[p] : -1;
+    }
+    // Device arrays are packed the same way as the host staging.
+    const std::uint64_t upload_ints = 2U * m + static_cast<std::uint64_t>(m) * table_pages;
+    auto* hs = static_cast<hipStream_t>(stream());
+    if (Status s = runtime_status(hipSetDevice(prepared_.device()), "hipSetDevice"); !s) {
+        rollback();
+        return s;
+    }
+    std::int32_t* positions_dev = tokens_dev_ + m;
+    std::int32_t* tables_dev = tokens_dev_ + 2U * m;
+    if (Status s = runtime_status(hipMemcpyAsync(tokens_dev_, host, upload_ints * sizeof(std::int32_t),
+                                                 hipMemcpyHostToDevice, hs),
+                                  "hipMemcpyAsync(rows)");
+        !s) {
+        rollback();
+        return s;
+    }
+    positions_dev_ = positions_dev;
+    tables_dev_ = tables_dev;
+
+    Status status = layers(m, max_tokens, table_pages, block_tactic);
+
+    // Output rows: final RMSNorm, lm_head (+bias), argmax, in chunks of the
+    // logits buffer.
+    StepResult result;
+    std::vector<std::uint32_t> outputs;
+    for (std::uint32_t r = 0; r < m; ++r) {
+        if (rows[r].output != RowOutput::none) outputs.push_back(r);
+    }
+    air_hip_context* ctx = prepared_.context();
+    std::int32_t* argmax_host = staging_ + upload_ints;
+    for (std::size_t begin = 0; status && begin < outputs.size(); begin += output_rows_) {
+        const auto k = static_cast<std::uint32_t>(std::min<std::size_t>(output_rows_, outputs.size() - begin));
+        // Gather the hidden rows (runs of consecutive rows in one copy).
+        for (std::uint32_t j = 0; j < k && status;) {
+            std::uint32_t run = 1;
+            while (j + run < k && outputs[begin + j + run] == outputs[begin + j] + run) ++run;
+            status = runtime_status(
+                hipMemcpyAsync(final_ + static_cast<std::uint64_t>(j) * embed_,
+                               hidden_ + static_cast<std::uint64_t>(outputs[begin + j]) * embed_,
+                               static_cast<std::uint64_t>(run) * embed_ * sizeof(float), hipMemcpyDeviceToDevice, hs),
+                "hipMemcpyAsync(gather)");
+            j += run;
+        }
+        if (!status) break;
+        int rc = air_hip_rms_norm(ctx, final_, output_norm_, final_, k, embed_, c.rms_norm_epsilon);
+        if (rc != AIR_HIP_OK) {
+            status = hip_status(rc);
+            break;
+        }
+        if (!(status = prepared_.linear(0, LinearRole::output, final_, logits_, k, output_tactic))) break;
+        if ((rc = air_hip_argmax(ctx, logits_, k, vocab_, argmax_dev_)) != AIR_HIP_OK) {
+            status = hip_status(rc);
+            break;
+        }
+        if (!(status = runtime_status(hipMemcpyAsync(argmax_host, argmax_dev_, k * sizeof(std::int32_t),
+                                                     hipMemcpyDeviceToHost, hs),
+                                      "hipMemcpyAsync(argmax)"))) {
+            break;
+        }
+        std::vector<std::vector<float>> logits;
+        for (std::uint32_t j = 0; j < k && status; ++j) {
+            if (rows[outputs[begin + j]].output != RowOutput::logits) continue;
+            logits.emplace_back(vocab_);
+            status = runtime_status(hipMemcpyAsync(logits.back().data(), logits_ + static_cast<std::uint64_t>(j) * vocab_,
+                                                   vocab_ * sizeof(float), hipMemcpyDeviceToHost, hs),
+                                    "hipMemcpyAsync(logits)");
+        }
+        if (!status) break;
+        if (!(status = runtime_status(hipStreamSynchronize(hs), "hipStreamSynchronize"))) break;
+        for (std::uint32_t j = 0; j < k; ++j) {
+            if (rows[outputs[begin + j]].output == RowOutput::greedy) result.greedy.push_back(argmax_host[j]);
+        }
+        for (auto& row : logits) result.logits.push_back(std::move(row));
+    }
+    // Always drain the stream: the staging buffer is reused by the next step.
+    const Status drained = runtime_status(hipStreamSynchronize(hs), "hipStreamSynchronize");
+    if (status) status = drained;
+    if (!status) {
+        rollback();
+        return status;
+    }
+    for (const auto& claim : claims) claim.sequence->tokens_ += claim.rows;
+    return result;
+}
+
+} // namespace air

@@ -214,6 +214,72 @@ int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* matrix,
                    const float* x, float* y, const float* bias,
                    uint32_t m, int tactic);
 
+/* ---- the Qwen2 step around the linears ---------------------------------- */
+/* Device primitives of one Qwen2 step over M rows, each row a (sequence,
+ * position, token).  Arithmetic follows the reference executor operation by
+ * operation (src/reference/reference_executor.cpp:17-138): double RMSNorm
+ * sums, host-built double RoPE tables, double attention scores and softmax
+ * with float probabilities, unfused float products.  All pointers are device
+ * pointers; every call is asynchronous on the context's stream. */
+
+/* out[i][k] = W[rows[i]][k], decoded bit-exactly from a resident matrix: the
+ * embedding lookup (ReferenceTensorReader::row, tensor_reader.cpp:347-367).
+ * rows: int32 [m]; rows outside [0, n) leave their output row untouched. */
+int air_hip_matrix_rows(air_hip_context* ctx, const air_hip_matrix* matrix, const int32_t* rows,
+                        uint32_t m, float* out);
+
+/* out[r] = x[r] * float(1 / sqrt(mean(x[r]^2) + eps)) * weight, rows of n
+ * (rms_norm, reference_executor.cpp:17-27).  out may alias x. */
+int air_hip_rms_norm(air_hip_context* ctx, const float* x, const float* weight, float* out, uint32_t m,
+                     uint64_t n, double eps);
+
+/* In-place rotary embedding of the q and k heads of fused q|k|v rows
+ * (apply_rope, reference_executor.cpp:37-72): row r (stride floats apart)
+ * rotates by position positions[r] with table[position][i] = {cos, sin} of
+ * the reference's double angle for pair i < rope_dims / 2 (table_positions
+ * positions; positions beyond it are the caller's error). */
+int air_hip_rope(air_hip_context* ctx, float* qkv, uint64_t row_stride, uint32_t m, const int32_t* positions,
+                 uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim, uint32_t rope_dims,
+                 const float* table, uint64_t table_positions);
+
+/* Paged fp32 KV cache.  Page p of `pool` holds [layer][K, V][page_tokens]
+ * [kv_width] floats for `layers` layers; a sequence is the list of its pages
+ * (int32), max_pages entries per page-table row.  Entries outside
+ * [0, pool_pages) are skipped by the kernels. */
+typedef struct air_hip_kv_layout {
+    float* pool;
+    uint32_t page_tokens;
+    uint32_t kv_width;       /* kv_heads * head_dim */
+    uint32_t layers;
+    uint32_t max_pages;
+    uint32_t pool_pages;
+} air_hip_kv_layout;
+
+/* Writes each row's k and v (the q|k|v row after RoPE) into the slot of
+ * positions[r] of its sequence: page_tables is int32 [m][max_pages]. */
+int air_hip_kv_append(air_hip_context* ctx, const air_hip_kv_layout* kv, const float* qkv, uint64_t row_stride,
+                      uint64_t q_width, uint32_t m, const int32_t* positions, const int32_t* page_tables,
+                      uint32_t layer);
+
+/* Attention of every row's q heads over tokens 0..positions[r] of its
+ * sequence for one layer (attention, reference_executor.cpp:74-138):
+ * out[r][q_heads * head_dim].  max_tokens bounds positions[r] + 1 and sizes
+ * the context's score scratch (m * q_heads * max_tokens doubles). */
+int air_hip_attention(air_hip_context* ctx, const air_hip_kv_layout* kv, const float* qkv, uint64_t row_stride,
+                      uint32_t m, const int32_t* positions, const int32_t* page_tables, uint32_t layer,
+                      uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim, uint64_t max_tokens, float* out);
+
+/* out[r][i] = silu(gate_up[r][i]) * gate_up[r][ffn + i] over fused gate|up
+ * rows (reference_executor.cpp:33-35, 400). */
+int air_hip_silu_mul(air_hip_context* ctx, const float* gate_up, float* out, uint32_t m, uint64_t ffn);
+
+/* x[i] += y[i] (the residual adds, add_in_place, reference_executor.cpp:29-31). */
+int air_hip_add(air_hip_context* ctx, float* x, const float* y, uint64_t count);
+
+/* out[r] = index of the first maximum of logits[r][0..n) (greedy selection,
+ * src/runtime/sampling.cpp:13-16). */
+int air_hip_argmax(air_hip_context* ctx, const float* logits, uint32_t m, uint64_t n, int32_t* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,6 +11,7 @@
 // Exit status 0 when every check passes.
 #include "air/execution.hpp"
 #include "air/hip_backend.hpp"
+#include "air/hip_step.hpp"
 #include "air/model.hpp"
 #include "air/scheduler.hpp"
 #include "air/synthetic.hpp"
@@ -612,6 +613,7 @@ struct DeviceBuffer {
 };
 
 double rel_l2(const std::vector<float>& got, const std::vector<float>& want) {
+    if (got.size() != want.size() || want.empty()) return 1e30;
     double num = 0, den = 0;
     for (std::size_t i = 0; i < want.size(); ++i) {
         const double d = static_cast<double>(got[i]) - want[i];
@@ -779,19 +781,309 @@ void gpu_prepared_model_contract() {
     plan.linear = {air::QuantizedLinearExecutionKind::hip_decode, air::QuantizedLinearExecutionKind::hip_decode,
                    air::QuantizedLinearExecutionKind::hip_decode};
     check(air::validate_execution_plan(plan, p.capabilities()).is_ok(), "a hip-decode plan validates");
+    check(p.kv_pool_allocated_bytes() == 0U, "no KV pool before the first sequence");
     const auto seq = p.create_sequence(plan);
-    check(!seq && seq.status().code() == air::ErrorCode::unsupported, "sequences are not provided");
+    check(seq.is_ok() && seq.value()->backend() == air::BackendKind::hip, "a hip-decode plan creates a sequence");
+    check(p.kv_pool_allocated_bytes() > 0U && p.kv_pool_free_bytes() == p.kv_pool_allocated_bytes(),
+          "the first sequence allocates the KV pool, all pages free");
+    check(p.capabilities().device_greedy_selection, "device greedy selection advertised");
+    auto other_pages = plan;
+    other_pages.kv.page_tokens = 32U;
+    check(!p.create_sequence(other_pages), "one KV page size per prepared model");
     auto baseline = paged_plan();
     const auto seq2 = p.create_sequence(baseline);
     check(!seq2 && seq2.status().code() == air::ErrorCode::unsupported &&
               seq2.status().message().find("tactic") != std::string::npos,
           "a baseline plan fails validation first");
+    if (seq) {
+        const auto ck = seq.value()->checkpoint();
+        check(!ck && ck.status().code() == air::ErrorCode::unsupported, "checkpoints are not provided");
+    }
     CapacityScheduler scheduler(32U);
     const auto d = scheduler.evaluate(0U, 0U, p, plan, 640U);
     check(d.admit && d.reservation_bytes == air::estimate_paged_fp32_sequence_bytes(spec.config, 16U, 640U),
           "CapacityScheduler admits against the HIP model's capacity");
     const auto huge = scheduler.evaluate(0U, 0U, p, plan, spec.config.context_length * 100000000ULL);
     check(!huge.admit && huge.reason == "device-capacity", "a reservation beyond HBM is refused");
+}
+
+// ---- GPU: Qwen2 sequences on the HIP step engine ---------------------------
+
+std::int32_t first_max(const std::vector<float>& v) {
+    std::size_t best = 0;
+    for (std::size_t i = 1; i < v.size(); ++i) {
+        if (v[best] < v[i]) best = i;
+    }
+    return static_cast<std::int32_t>(best);
+}
+
+air::ExecutionPlan hip_plan(air::QuantizedLinearExecutionKind prefill_block, std::uint32_t page_tokens) {
+    auto plan = paged_plan();
+    plan.kv.page_tokens = page_tokens;
+    plan.linear = {prefill_block, air::QuantizedLinearExecutionKind::hip_decode,
+                   air::QuantizedLinearExecutionKind::hip_decode};
+    return plan;
+}
+
+// Logit tolerances: the exact-code decode linear keeps the step within 1e-4
+// (relative L2) of the reference; the f16 MFMA prefill GEMM within 1e-2.
+constexpr double kDecodeTolerance = 1e-4;
+constexpr double kPrefillTolerance = 1e-2;
+
+// Every golden sequence of AIR's ReferenceExecutor (tests/golden/qwen2_tiny.txt):
+// prompt logits and every decode step's logits within tolerance, identical
+// greedy tokens, through single sequences, the prefill tactic and batches.
+void gpu_golden_sequences(bool fuse, std::uint32_t page_tokens, std::uint32_t step_rows) {
+    const auto cases = fixture::load(repo_file("tests/golden/qwen2_tiny.txt"));
+    check(cases.size() == 3U, "three golden Qwen2 cases");
+    for (const auto& c : cases) {
+        const std::string tag = "golden " + c.name + (fuse ? " fused" : " unfused") + " page " +
+                                std::to_string(page_tokens) + " step " + std::to_string(step_rows);
+        std::cout << tag << std::endl;
+        auto model = air::make_synthetic_qwen2(c.spec);
+        if (!model) {
+            check(false, tag + ": model");
+            continue;
+        }
+        air::HipPrepareOptions options;
+        options.fuse = fuse;
+        options.kv_pool_pages = 64U;
+        options.max_step_rows = step_rows;
+        auto prepared = air::HipPreparedModel::create(model.value(), options);
+        check(prepared.is_ok(), tag + ": prepare");
+        if (!prepared) continue;
+        auto& p = *prepared.value();
+        const auto plan = hip_plan(air::QuantizedLinearExecutionKind::hip_decode, page_tokens);
+
+        // One sequence at a time: prefill logits, then decode logits.
+        for (std::size_t si = 0; si < c.sequences.size(); ++si) {
+            const auto& g = c.sequences[si];
+            auto seq = p.create_sequence(plan);
+            check(seq.is_ok(), tag + ": create_sequence");
+            if (!seq) continue;
+            auto& s = *seq.value();
+            auto logits = s.prefill(g.prompt);
+            check(logits.is_ok(), tag + ": prefill");
+            if (!logits) continue;
+            double worst = rel_l2(logits.value(), g.logits[g.prompt.size() - 1U]);
+            std::vector<std::int32_t> tokens{first_max(logits.value())};
+            for (std::size_t i = 0; i + 1U < g.generated.size(); ++i) {
+                auto step = s.decode(g.generated[i]);
+                check(step.is_ok(), tag + ": decode");
+                if (!step) break;
+                worst = std::max(worst, rel_l2(step.value(), g.logits[g.prompt.size() + i]));
+                tokens.push_back(first_max(step.value()));
+            }
+            check(worst <= kDecodeTolerance, tag + ": logits rel-L2 " + std::to_string(worst));
+            check(tokens == g.generated, tag + ": greedy tokens equal the reference's");
+            const auto res = s.resources();
+            const std::uint64_t committed = g.prompt.size() + g.generated.size() - 1U;
+            check(res.committed_tokens == committed, tag + ": committed tokens");
+            const auto& cfg = c.spec.config;
+            const std::uint64_t kv_width =
+                static_cast<std::uint64_t>(cfg.kv_head_count) * (cfg.embedding_size / cfg.attention_head_count);
+            const std::uint64_t page_bytes = cfg.layer_count * 2ULL * page_tokens * kv_width * sizeof(float);
+            check(res.committed_kv_bytes == (committed + page_tokens - 1U) / page_tokens * page_bytes,
+                  tag + ": committed KV bytes are whole pages");
+            // The same sequence through device greedy selection.
+            auto seq2 = p.create_sequence(plan);
+            if (!seq2) continue;
+            auto first = seq2.value()->prefill_greedy(g.prompt);
+            std::vector<std::int32_t> greedy;
+            if (first) greedy.push_back(first.value());
+            for (std::size_t i = 0; first && i + 1U < g.generated.size(); ++i) {
+                auto t = seq2.value()->decode_greedy(greedy.back());
+                if (!t) break;
+                greedy.push_back(t.value());
+            }
+            check(greedy == g.generated, tag + ": device greedy generation equals the reference's");
+        }
+        check(p.kv_pool_free_bytes() == p.kv_pool_allocated_bytes(), tag + ": released sequences return their pages");
+
+        // Prompt through the f16 MFMA prefill GEMM.
+        const auto prefill_plan = hip_plan(air::QuantizedLinearExecutionKind::hip_prefill, page_tokens);
+        for (const auto& g : c.sequences) {
+            auto seq = p.create_sequence(prefill_plan);
+            if (!seq) {
+                check(false, tag + ": prefill-tactic sequence");
+                continue;
+            }
+            auto logits = seq.value()->prefill(g.prompt);
+            check(logits && rel_l2(logits.value(), g.logits[g.prompt.size() - 1U]) <= kPrefillTolerance,
+                  tag + ": hip-prefill prompt logits within 1e-2");
+            check(logits && first_max(logits.value()) == g.generated.front(), tag + ": hip-prefill first token");
+        }
+
+        // All sequences of the case as one prefill batch, then batched decode.
+        std::vector<std::unique_ptr<air::runtime_detail::SequenceState>> seqs;
+        std::vector<air::runtime_detail::PrefillBatchItem> items;
+        for (const auto& g : c.sequences) {
+            auto seq = p.create_sequence(plan);
+            if (!seq) break;
+            seqs.push_back(std::move(seq).value());
+            items.push_back({seqs.back().get(), g.prompt, air::runtime_detail::PrefillBatchOutput::greedy});
+        }
+        auto batch = p.prefill_batch(items);
+        check(batch.is_ok() && batch.value().items.size() == c.sequences.size(), tag + ": prefill batch");
+        if (!batch) continue;
+        bool batch_ok = true;
+        for (std::size_t i = 0; i < c.sequences.size(); ++i) {
+            batch_ok = batch_ok && batch.value().items[i].greedy_token == c.sequences[i].generated.front();
+        }
+        for (std::size_t step = 0; batch_ok && step + 1U < c.spec.config.context_length; ++step) {
+            std::vector<air::runtime_detail::GreedyDecodeBatchItem> decode;
+            std::vector<std::size_t> owners;
+            for (std::size_t i = 0; i < c.sequences.size(); ++i) {
+                if (step + 1U < c.sequences[i].generated.size()) {
+                    decode.push_back({seqs[i].get(), c.sequences[i].generated[step]});
+                    owners.push_back(i);
+                }
+            }
+            if (decode.empty()) break;
+            auto out = p.decode_greedy_batch(decode);
+            if (!out || out.value().size() != decode.size()) {
+                batch_ok = false;
+                break;
+            }
+            for (std::size_t j = 0; j < owners.size(); ++j) {
+                batch_ok = batch_ok && out.value()[j] == c.sequences[owners[j]].generated[step + 1U];
+            }
+        }
+        check(batch_ok, tag + ": batched prefill and decode give the reference's tokens");
+    }
+}
+
+// A longer sequence across many pages against the C oracle (bit-exact with
+// the reference), interleaved with a second sequence in batched decode.
+void gpu_long_sequences_vs_oracle(std::uint32_t format) {
+    air::SyntheticQwen2Spec spec;
+    spec.config = air::qwen2_config(2, 256, 512, 4, 2, 512, 96);
+    spec.weight_format = format;
+    spec.seed = 0xA17C0DE5ULL + format;
+    const std::string tag = "long sequences format " + std::to_string(format);
+    std::cout << tag << std::endl;
+    auto model = air::make_synthetic_qwen2(spec);
+    if (!model) {
+        check(false, tag + ": model");
+        return;
+    }
+    const auto view = fixture::oracle_view(*model.value());
+    air::HipPrepareOptions options;
+    options.kv_pool_pages = 64U;
+    auto prepared = air::HipPreparedModel::create(model.value(), options);
+    check(prepared.is_ok(), tag + ": prepare");
+    if (!prepared) return;
+    auto& p = *prepared.value();
+    const auto plan = hip_plan(air::QuantizedLinearExecutionKind::hip_decode, 4U);
+    const std::uint64_t vocab = spec.config.vocabulary_size;
+
+    std::uint64_t lcg = 0x9E3779B97F4A7C15ULL + format;
+    const auto next = [&]() {
+        lcg = lcg * 6364136223846793005ULL + 1442695040888963407ULL;
+        return static_cast<std::int32_t>((lcg >> 33) % vocab);
+    };
+    std::vector<std::int32_t> prompts[2];
+    for (int i = 0; i < 37; ++i) prompts[0].push_back(next());
+    for (int i = 0; i < 9; ++i) prompts[1].push_back(next());
+
+    // Oracle: prompt then 30 greedy tokens, logits of every generated step.
+    std::vector<std::int32_t> expect[2];
+    std::vector<std::vector<float>> expect_logits[2];
+    for (int s = 0; s < 2; ++s) {
+        oracle_qwen2_cache cache{};
+        oracle_qwen2_cache_init(&view->model, &cache, spec.config.context_length);
+        std::vector<float> logits(vocab);
+        for (auto t : prompts[s]) oracle_qwen2_step(&view->model, &cache, t, logits.data());
+        expect_logits[s].push_back(logits);
+        expect[s].push_back(static_cast<std::int32_t>(oracle_greedy(logits.data(), vocab)));
+        for (int i = 0; i < 30; ++i) {
+            oracle_qwen2_step(&view->model, &cache, expect[s].back(), logits.data());
+            expect_logits[s].push_back(logits);
+            expect[s].push_back(static_cast<std::int32_t>(oracle_greedy(logits.data(), vocab)));
+        }
+        oracle_qwen2_cache_free(&cache);
+    }
+
+    std::unique_ptr<air::runtime_detail::SequenceState> seqs[2];
+    for (auto& s : seqs) {
+        auto created = p.create_sequence(plan);
+        if (!created) {
+            check(false, tag + ": create_sequence");
+            return;
+        }
+        s = std::move(created).value();
+    }
+    double worst = 0.0;
+    std::vector<std::int32_t> got[2];
+    for (int s = 0; s < 2; ++s) {
+        auto logits = seqs[s]->prefill(prompts[s]);
+        if (!logits) {
+            check(false, tag + ": prefill");
+            return;
+        }
+        worst = std::max(worst, rel_l2(logits.value(), expect_logits[s][0]));
+        got[s].push_back(first_max(logits.value()));
+    }
+    for (int i = 0; i < 30; ++i) {
+        const air::runtime_detail::GreedyDecodeBatchItem items[] = {{seqs[0].get(), got[0].back()},
+                                                                    {seqs[1].get(), got[1].back()}};
+        auto out = p.decode_greedy_batch(items);
+        if (!out) {
+            check(false, tag + ": decode batch: " + out.status().message());
+            return;
+        }
+        got[0].push_back(out.value()[0]);
+        got[1].push_back(out.value()[1]);
+    }
+    // Logits of one more step of sequence 1 at its position against the oracle.
+    check(worst <= kDecodeTolerance, tag + ": prompt logits rel-L2 " + std::to_string(worst));
+    check(got[0] == expect[0] && got[1] == expect[1], tag + ": batched greedy tokens equal the oracle's");
+    check(seqs[0]->resources().committed_tokens == 37U + 30U && seqs[1]->resources().committed_tokens == 9U + 30U,
+          tag + ": committed tokens");
+    // Context limit: sequence 0 holds 67 of 96 tokens; a 30-token prompt tail
+    // overflows and is refused without committing anything.
+    std::vector<std::int32_t> tail(30, 1);
+    const auto before = p.kv_pool_free_bytes();
+    const auto refused = seqs[0]->prefill(tail);
+    check(!refused && refused.status().code() == air::ErrorCode::invalid_state &&
+              refused.status().message() == "model context length exceeded",
+          tag + ": context overflow is refused");
+    check(seqs[0]->resources().committed_tokens == 67U && p.kv_pool_free_bytes() == before,
+          tag + ": a refused step commits nothing");
+    const std::int32_t bad_token = static_cast<std::int32_t>(vocab);
+    const auto bad = seqs[1]->decode_greedy(bad_token);
+    check(!bad && bad.status().code() == air::ErrorCode::invalid_argument, tag + ": out-of-vocabulary token refused");
+}
+
+// KV pool exhaustion: a step that needs more pages than are free fails, its
+// sequence keeps its committed state and the pages stay in the pool.
+void gpu_pool_exhaustion() {
+    air::SyntheticQwen2Spec spec;
+    spec.config = air::qwen2_config(2, 256, 512, 4, 2, 512, 64);
+    auto model = air::make_synthetic_qwen2(spec);
+    if (!model) return;
+    air::HipPrepareOptions options;
+    options.kv_pool_pages = 3U;
+    auto prepared = air::HipPreparedModel::create(model.value(), options);
+    check(prepared.is_ok(), "pool: prepare");
+    if (!prepared) return;
+    auto& p = *prepared.value();
+    const auto plan = hip_plan(air::QuantizedLinearExecutionKind::hip_decode, 4U);
+    auto a = p.create_sequence(plan);
+    auto b = p.create_sequence(plan);
+    if (!a || !b) {
+        check(false, "pool: sequences");
+        return;
+    }
+    const std::vector<std::int32_t> eight(8, 3), five(5, 4);
+    check(a.value()->prefill_discard(eight).is_ok(), "pool: 8 tokens take 2 of 3 pages");
+    const auto refused = b.value()->prefill_discard(five);
+    check(!refused && refused.code() == air::ErrorCode::invalid_state, "pool: 5 more tokens need 2 pages, 1 free");
+    check(b.value()->resources().committed_tokens == 0U && p.kv_pool_free_bytes() == p.kv_pool_allocated_bytes() / 3U,
+          "pool: the refused step returned its page");
+    a.value().reset();
+    check(p.kv_pool_free_bytes() == p.kv_pool_allocated_bytes(), "pool: a destroyed sequence frees its pages");
+    check(b.value()->prefill_discard(five).is_ok(), "pool: freed pages are reused");
 }
 
 int run_gpu() {
@@ -801,6 +1093,12 @@ int run_gpu() {
         return 2;
     }
     gpu_prepared_model_contract();
+    gpu_golden_sequences(true, 16U, 512U);
+    gpu_golden_sequences(false, 4U, 3U);
+    gpu_long_sequences_vs_oracle(8U);
+    gpu_long_sequences_vs_oracle(2U);
+    gpu_long_sequences_vs_oracle(12U);
+    gpu_pool_exhaustion();
     gpu_model_case(8U, true, false, false);
     gpu_model_case(8U, false, true, true);
     gpu_model_case(2U, true, false, true);
