@@ -68,6 +68,35 @@ class Stats(ctypes.Structure):
     ]
 
 
+class KvLayout(ctypes.Structure):
+    """air_hip_kv_layout: the paged fp32 KV pool."""
+    _fields_ = [
+        ("pool", ctypes.c_void_p),
+        ("page_tokens", ctypes.c_uint32),
+        ("kv_width", ctypes.c_uint32),
+        ("layers", ctypes.c_uint32),
+        ("max_pages", ctypes.c_uint32),
+        ("pool_pages", ctypes.c_uint32),
+    ]
+
+
+class AttentionTile(ctypes.Structure):
+    """air_hip_attention_tile."""
+    _fields_ = [("row", ctypes.c_uint32), ("rows", ctypes.c_uint32), ("head", ctypes.c_uint32),
+                ("heads", ctypes.c_uint32)]
+
+
+def attention_tiles(run_rows, q_heads: int, kv_heads: int):
+    """Host tiles of the online attention for rows in runs of one sequence each."""
+    runs = (ctypes.c_uint32 * max(len(run_rows), 1))(*run_rows)
+    count = ctypes.c_uint32()
+    check(lib().air_hip_attention_make_tiles(runs, len(run_rows), q_heads, kv_heads, None, 0, ctypes.byref(count)))
+    tiles = (AttentionTile * max(count.value, 1))()
+    check(lib().air_hip_attention_make_tiles(runs, len(run_rows), q_heads, kv_heads, tiles, count.value,
+                                             ctypes.byref(count)))
+    return [(t.row, t.rows, t.head, t.heads) for t in tiles[:count.value]]
+
+
 SIGNATURES = {
     "air_hip_abi_version": (_I, []),
     "air_hip_status_string": (ctypes.c_char_p, [_I]),
@@ -87,6 +116,8 @@ SIGNATURES = {
     "air_hip_rope": (_I, [_P, _P, _U64, _U32, _P, _U32, _U32, _U32, _U32, _P, _U64]),
     "air_hip_kv_append": (_I, [_P, _P, _P, _U64, _U64, _U32, _P, _P, _U32]),
     "air_hip_attention": (_I, [_P, _P, _P, _U64, _U32, _P, _P, _U32, _U32, _U32, _U32, _U64, _P]),
+    "air_hip_attention_make_tiles": (_I, [_P, _U32, _U32, _U32, _P, _U32, _P]),
+    "air_hip_attention_online": (_I, [_P, _P, _P, _U64, _U32, _P, _P, _U32, _U32, _U32, _U32, _P, _U32, _U64, _P]),
     "air_hip_silu_mul": (_I, [_P, _P, _P, _U32, _U64]),
     "air_hip_add": (_I, [_P, _P, _P, _U64]),
     "air_hip_argmax": (_I, [_P, _P, _U32, _U64, _P]),

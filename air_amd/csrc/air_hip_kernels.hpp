@@ -157,6 +157,29 @@ hipError_t launch_attention(const KvLayout& kv, const float* qkv, std::uint64_t 
                             const std::int32_t* positions, const std::int32_t* tables, std::uint32_t layer,
                             std::uint32_t q_heads, std::uint32_t kv_heads, std::uint32_t head_dim, double* scratch,
                             std::uint64_t score_stride, float* out, hipStream_t stream);
+// Tiled online-softmax attention (attention.hip).  A tile is up to 16 query
+// vectors of one sequence and one KV head: rows [row, row + rows) x q heads
+// [head, head + heads), rows * heads <= 16.
+struct AttentionTile {
+    std::uint32_t row, rows, head, heads;
+};
+// Tiles of a step whose rows form `runs` consecutive runs of one sequence
+// each (run_rows[i] rows): a one-row run gives one tile per KV head (its
+// grouped q heads), a longer run tiles of 16 rows per q head.  Writes up to
+// `capacity` tiles (tiles may be null) and returns the count.
+std::uint32_t make_attention_tiles(const std::uint32_t* run_rows, std::uint32_t runs, std::uint32_t q_heads,
+                                   std::uint32_t kv_heads, AttentionTile* tiles, std::uint32_t capacity);
+// Workgroups splitting the keys of each tile (1 = no merge pass).
+std::uint32_t attention_splits(std::uint32_t tiles, std::uint64_t max_tokens);
+std::uint64_t attention_partials_bytes(std::uint32_t tiles, std::uint32_t splits, std::uint32_t head_dim);
+// head_dim 64 or 128.  tiles: device array; partials: attention_partials_bytes.
+// A tile outside the m rows or q heads, or with more than 16 vectors or heads
+// of two KV heads, is skipped by the kernel.
+hipError_t launch_attention_tiles(const KvLayout& kv, const float* qkv, std::uint64_t stride, std::uint32_t m,
+                                  const std::int32_t* positions, const std::int32_t* tables, std::uint32_t layer,
+                                  std::uint32_t q_heads, std::uint32_t kv_heads, std::uint32_t head_dim,
+                                  const AttentionTile* tiles, std::uint32_t tile_count, std::uint32_t splits,
+                                  float* partials, float* out, hipStream_t stream);
 hipError_t launch_silu_mul(const float* gate_up, float* out, std::uint32_t m, std::uint64_t ffn, hipStream_t stream);
 hipError_t launch_add(float* x, const float* y, std::uint64_t count, hipStream_t stream);
 hipError_t launch_argmax(const float* logits, std::uint32_t m, std::uint64_t n, std::int32_t* out, hipStream_t stream);

@@ -1,0 +1,39 @@
+// air_hip_kv.hpp -- device view of the paged fp32 KV pool (internal).
+//
+// Page p of the pool holds [layer][K, V][page_tokens][kv_width] floats; a
+// sequence is named by its page table (int32 page indices, max_pages per
+// row).  Slots whose table entry is outside [0, pool_pages) read as absent.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace air_hip {
+
+struct KvGeometry {
+    float* pool;
+    std::uint32_t page_tokens;
+    std::uint32_t kv_width;       // kv_heads * head_dim
+    std::uint32_t layers;
+    std::uint32_t max_pages;      // page-table row length
+    std::uint32_t pool_pages;     // pages in the pool
+};
+
+__device__ __forceinline__ std::uint64_t page_floats(const KvGeometry& g) {
+    return static_cast<std::uint64_t>(g.layers) * 2u * g.page_tokens * g.kv_width;
+}
+
+// K and V of (layer, token) of a row's sequence; null when the page table
+// does not name a page of the pool (the caller skips the token).
+__device__ __forceinline__ float* kv_slot(const KvGeometry& g, const std::int32_t* table, std::uint32_t layer,
+                                          std::uint64_t token, bool value) {
+    const std::uint64_t slot = token / g.page_tokens;
+    if (slot >= g.max_pages) return nullptr;
+    const std::int32_t page = table[slot];
+    if (page < 0 || static_cast<std::uint32_t>(page) >= g.pool_pages) return nullptr;
+    return g.pool + static_cast<std::uint64_t>(page) * page_floats(g) +
+           ((static_cast<std::uint64_t>(layer) * 2u + (value ? 1u : 0u)) * g.page_tokens + token % g.page_tokens) *
+               g.kv_width;
+}
+
+} // namespace air_hip

@@ -673,6 +673,34 @@ int check_kv(const air_hip_kv_layout* kv) {
 KvLayout kv_layout_of(const air_hip_kv_layout* kv) {
     return KvLayout{kv->pool, kv->page_tokens, kv->kv_width, kv->layers, kv->max_pages, kv->pool_pages};
 }
+int check_heads(const air_hip_kv_layout* kv, uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim,
+                uint64_t max_tokens) {
+    if (q_heads == 0 || kv_heads == 0 || q_heads % kv_heads != 0 || head_dim == 0 || head_dim > 512u ||
+        static_cast<uint64_t>(kv_heads) * head_dim != kv->kv_width) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "head geometry does not match the KV layout");
+    }
+    if (max_tokens == 0 || max_tokens > static_cast<uint64_t>(kv->max_pages) * kv->page_tokens) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "max_tokens must be in [1, max_pages * page_tokens]");
+    }
+    return AIR_HIP_OK;
+}
+// Grows the attention scratch to at least `bytes` (geometrically, so a decode
+// loop whose key count grows by one per step reallocates rarely).  Waits for
+// the stream first: queued kernels may still read the old buffer.
+int ensure_attention_scratch(air_hip_context* ctx, uint64_t bytes) {
+    if (bytes <= ctx->attention_scratch_bytes) return AIR_HIP_OK;
+    const uint64_t grown = std::max<uint64_t>(bytes, ctx->attention_scratch_bytes + ctx->attention_scratch_bytes / 2);
+    const hipError_t sync = hipStreamSynchronize(ctx->stream);
+    if (sync != hipSuccess) return hip_fail(sync, "hipStreamSynchronize(attention scratch growth)");
+    (void)hipFree(ctx->attention_scratch);
+    ctx->attention_scratch = nullptr;
+    ctx->attention_scratch_bytes = 0;
+    const hipError_t err = hipMalloc(&ctx->attention_scratch, grown);
+    if (err != hipSuccess) return hip_fail(err, "hipMalloc(attention scratch)");
+    ctx->attention_scratch_bytes = grown;
+    return AIR_HIP_OK;
+}
+static_assert(sizeof(AttentionTile) == sizeof(air_hip_attention_tile), "tile layouts agree");
 } // namespace
 
 int air_hip_kv_append(air_hip_context* ctx, const air_hip_kv_layout* kv, const float* qkv, uint64_t row_stride,
@@ -701,33 +729,67 @@ int air_hip_attention(air_hip_context* ctx, const air_hip_kv_layout* kv, const f
     }
     if (int rc = check_kv(kv); rc != AIR_HIP_OK) return rc;
     if (layer >= kv->layers) return fail(AIR_HIP_INVALID_ARGUMENT, "layer %u is out of range", layer);
-    if (q_heads == 0 || kv_heads == 0 || q_heads % kv_heads != 0 || head_dim == 0 || head_dim > 512u ||
-        static_cast<uint64_t>(kv_heads) * head_dim != kv->kv_width) {
-        return fail(AIR_HIP_INVALID_ARGUMENT, "head geometry does not match the KV layout");
-    }
-    if (max_tokens == 0 || max_tokens > static_cast<uint64_t>(kv->max_pages) * kv->page_tokens) {
-        return fail(AIR_HIP_INVALID_ARGUMENT, "max_tokens must be in [1, max_pages * page_tokens]");
-    }
+    if (int rc = check_heads(kv, q_heads, kv_heads, head_dim, max_tokens); rc != AIR_HIP_OK) return rc;
     if (m == 0) return AIR_HIP_OK;
     const uint64_t blocks = static_cast<uint64_t>(m) * q_heads;
     if (blocks > 0x7fffffffu) return fail(AIR_HIP_UNSUPPORTED, "too many (row, head) pairs");
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-    const uint64_t scratch_bytes = blocks * max_tokens * sizeof(double);
-    if (scratch_bytes > ctx->attention_scratch_bytes) {
-        const hipError_t sync = hipStreamSynchronize(ctx->stream);
-        if (sync != hipSuccess) return hip_fail(sync, "hipStreamSynchronize(attention scratch growth)");
-        (void)hipFree(ctx->attention_scratch);
-        ctx->attention_scratch = nullptr;
-        ctx->attention_scratch_bytes = 0;
-        const hipError_t err = hipMalloc(&ctx->attention_scratch, scratch_bytes);
-        if (err != hipSuccess) return hip_fail(err, "hipMalloc(attention scratch)");
-        ctx->attention_scratch_bytes = scratch_bytes;
-    }
+    if (int rc = ensure_attention_scratch(ctx, blocks * max_tokens * sizeof(double)); rc != AIR_HIP_OK) return rc;
     const hipError_t err = launch_attention(kv_layout_of(kv), qkv, row_stride, m, positions, page_tables, layer,
                                             q_heads, kv_heads, head_dim, static_cast<double*>(ctx->attention_scratch),
                                             max_tokens, out, ctx->stream);
     return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "attention_kernel");
+}
+
+int air_hip_attention_make_tiles(const uint32_t* run_rows, uint32_t runs, uint32_t q_heads, uint32_t kv_heads,
+                                 air_hip_attention_tile* tiles, uint32_t capacity, uint32_t* count) {
+    if (!run_rows || !count) return fail(AIR_HIP_INVALID_ARGUMENT, "run_rows and count must not be null");
+    if (q_heads == 0 || kv_heads == 0 || q_heads % kv_heads != 0) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "q heads must be a non-zero multiple of the KV heads");
+    }
+    for (uint32_t i = 0; i < runs; ++i) {
+        if (run_rows[i] == 0) return fail(AIR_HIP_INVALID_ARGUMENT, "run %u has no rows", i);
+    }
+    *count = make_attention_tiles(run_rows, runs, q_heads, kv_heads, reinterpret_cast<AttentionTile*>(tiles),
+                                  tiles ? capacity : 0u);
+    if (tiles && *count > capacity) return fail(AIR_HIP_INVALID_ARGUMENT, "%u tiles exceed capacity %u", *count, capacity);
+    return AIR_HIP_OK;
+}
+
+int air_hip_attention_online(air_hip_context* ctx, const air_hip_kv_layout* kv, const float* qkv, uint64_t row_stride,
+                             uint32_t m, const int32_t* positions, const int32_t* page_tables, uint32_t layer,
+                             uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim,
+                             const air_hip_attention_tile* tiles, uint32_t tile_count, uint64_t max_tokens,
+                             float* out) {
+    if (!ctx || !qkv || !positions || !page_tables || !tiles || !out) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    }
+    if (int rc = check_kv(kv); rc != AIR_HIP_OK) return rc;
+    if (layer >= kv->layers) return fail(AIR_HIP_INVALID_ARGUMENT, "layer %u is out of range", layer);
+    if (int rc = check_heads(kv, q_heads, kv_heads, head_dim, max_tokens); rc != AIR_HIP_OK) return rc;
+    if (head_dim != 64u && head_dim != 128u) {
+        return fail(AIR_HIP_UNSUPPORTED, "online attention supports head widths 64 and 128, not %u", head_dim);
+    }
+    const uint64_t qkv_width = static_cast<uint64_t>(q_heads) * head_dim + 2u * static_cast<uint64_t>(kv->kv_width);
+    if (row_stride < qkv_width || row_stride % 4u != 0 || reinterpret_cast<std::uintptr_t>(qkv) % 16u != 0 ||
+        reinterpret_cast<std::uintptr_t>(out) % 16u != 0 || reinterpret_cast<std::uintptr_t>(kv->pool) % 16u != 0) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "q|k|v rows, output and pool must be 16-byte aligned, stride >= q|k|v");
+    }
+    if (m == 0 || tile_count == 0) return AIR_HIP_OK;
+    if (tile_count > 0x7fffffffu) return fail(AIR_HIP_UNSUPPORTED, "too many tiles");
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const uint32_t splits = attention_splits(tile_count, max_tokens);
+    if (int rc = ensure_attention_scratch(ctx, attention_partials_bytes(tile_count, splits, head_dim));
+        rc != AIR_HIP_OK) {
+        return rc;
+    }
+    const hipError_t err = launch_attention_tiles(kv_layout_of(kv), qkv, row_stride, m, positions, page_tables, layer,
+                                                  q_heads, kv_heads, head_dim,
+                                                  reinterpret_cast<const AttentionTile*>(tiles), tile_count, splits,
+                                                  static_cast<float*>(ctx->attention_scratch), out, ctx->stream);
+    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "attention_tile_kernel");
 }
 
 int air_hip_silu_mul(air_hip_context* ctx, const float* gate_up, float* out, uint32_t m, uint64_t ffn) {

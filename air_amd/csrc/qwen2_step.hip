@@ -21,6 +21,7 @@
 // its page table (int32 page indices).
 #include "air_hip_device.hpp"
 #include "air_hip_kernels.hpp"
+#include "air_hip_kv.hpp"
 
 namespace air_hip {
 namespace {
@@ -132,32 +133,6 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(float* __restrict__ qkv,
 }
 
 // ---- paged KV ----------------------------------------------------------------
-
-struct KvGeometry {
-    float* pool;
-    std::uint32_t page_tokens;
-    std::uint32_t kv_width;       // kv_heads * head_dim
-    std::uint32_t layers;
-    std::uint32_t max_pages;      // page-table row length
-    std::uint32_t pool_pages;     // pages in the pool
-};
-
-__device__ __forceinline__ std::uint64_t page_floats(const KvGeometry& g) {
-    return static_cast<std::uint64_t>(g.layers) * 2u * g.page_tokens * g.kv_width;
-}
-
-// K and V of (layer, token) of a row's sequence; null when the page table
-// does not name a page of the pool (the caller skips the token).
-__device__ __forceinline__ float* kv_slot(const KvGeometry& g, const std::int32_t* table, std::uint32_t layer,
-                                          std::uint64_t token, bool value) {
-    const std::uint64_t slot = token / g.page_tokens;
-    if (slot >= g.max_pages) return nullptr;
-    const std::int32_t page = table[slot];
-    if (page < 0 || static_cast<std::uint32_t>(page) >= g.pool_pages) return nullptr;
-    return g.pool + static_cast<std::uint64_t>(page) * page_floats(g) +
-           ((static_cast<std::uint64_t>(layer) * 2u + (value ? 1u : 0u)) * g.page_tokens + token % g.page_tokens) *
-               g.kv_width;
-}
 
 // Copies each row's k and v (after RoPE) from its fused q|k|v output into its page slot.
 __global__ __launch_bounds__(kThreads) void kv_append_kernel(KvGeometry g, const float* __restrict__ qkv,

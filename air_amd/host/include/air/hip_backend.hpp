@@ -51,7 +51,10 @@ struct HipPrepareOptions {
     void* stream{nullptr};              // hipStream_t the engine launches on
     std::uint32_t max_decode_rows{64};  // workspace reserved for decode widths
     bool fuse{true};                    // concatenate q|k|v and gate|up when formats agree
-    std::uint32_t kv_pool_pages{1024};  // KV pages allocated with the first sequence
+    // KV pages allocated with the first sequence; 0 sizes the pool for
+    // max_decode_rows sequences of min(context, 4096) tokens, capped at 40%
+    // of free device memory.
+    std::uint32_t kv_pool_pages{0};
     std::uint32_t max_step_rows{512};   // rows per device step (prefill chunk)
 };
 

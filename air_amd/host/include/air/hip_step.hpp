@@ -31,8 +31,7 @@ class HipStepEngine;
 
 class HipSequence final : public runtime_detail::SequenceState {
 public:
-    HipSequence(HipStepEngine& engine, QuantizedLinearExecutionKind prefill_block,
-                QuantizedLinearExecutionKind decode_block, QuantizedLinearExecutionKind decode_output);
+    HipSequence(HipStepEngine& engine, const LinearPolicy& linear, const AttentionPolicy& attention);
     ~HipSequence() override;
 
     [[nodiscard]] BackendKind backend() const noexcept override { return BackendKind::hip; }
@@ -48,12 +47,15 @@ public:
     [[nodiscard]] QuantizedLinearExecutionKind prefill_block_tactic() const noexcept { return prefill_block_; }
     [[nodiscard]] QuantizedLinearExecutionKind decode_block_tactic() const noexcept { return decode_block_; }
     [[nodiscard]] QuantizedLinearExecutionKind decode_output_tactic() const noexcept { return decode_output_; }
+    [[nodiscard]] AttentionExecutionKind prefill_attention() const noexcept { return prefill_attention_; }
+    [[nodiscard]] AttentionExecutionKind decode_attention() const noexcept { return decode_attention_; }
     [[nodiscard]] const HipStepEngine& engine() const noexcept { return engine_; }
 
 private:
     friend class HipStepEngine;
     HipStepEngine& engine_;
     QuantizedLinearExecutionKind prefill_block_, decode_block_, decode_output_;
+    AttentionExecutionKind prefill_attention_, decode_attention_;
     std::vector<std::int32_t> pages_;
     std::uint64_t tokens_{0};
 };
@@ -86,7 +88,8 @@ public:
     // Rows of several sequences; the positions are each sequence's next
     // tokens in row order.  The batch commits to every sequence on success.
     [[nodiscard]] Result<StepResult> run(std::span<const StepRow> rows, QuantizedLinearExecutionKind block_tactic,
-                                         QuantizedLinearExecutionKind output_tactic);
+                                         QuantizedLinearExecutionKind output_tactic,
+                                         AttentionExecutionKind attention);
 
     [[nodiscard]] std::uint32_t page_tokens() const noexcept { return page_tokens_; }
     [[nodiscard]] std::uint64_t page_bytes() const noexcept { return page_bytes_; }
@@ -101,7 +104,7 @@ private:
     explicit HipStepEngine(const HipPreparedModel& prepared) : prepared_(prepared) {}
     [[nodiscard]] Status allocate(void** ptr, std::uint64_t bytes, const char* what);
     [[nodiscard]] Status layers(std::uint32_t m, std::uint64_t max_tokens, std::uint32_t table_pages,
-                                QuantizedLinearExecutionKind tactic);
+                                QuantizedLinearExecutionKind tactic, std::uint32_t tiles);
     [[nodiscard]] Status project(std::uint32_t layer, LinearRole fused, LinearRole first, LinearRole second,
                                  LinearRole third, const float* x, float* y, std::uint32_t m,
                                  QuantizedLinearExecutionKind tactic);
@@ -126,7 +129,9 @@ private:
     float *hidden_{nullptr}, *normed_{nullptr}, *qkv_{nullptr}, *att_{nullptr}, *proj_{nullptr};
     float *gate_up_{nullptr}, *act_{nullptr}, *part_{nullptr}, *final_{nullptr}, *logits_{nullptr};
     std::int32_t *tokens_dev_{nullptr}, *positions_dev_{nullptr}, *tables_dev_{nullptr}, *argmax_dev_{nullptr};
-    std::int32_t* staging_{nullptr};  // pinned host: tokens | positions | page tables | argmax
+    std::int32_t* tiles_dev_{nullptr};  // attention tiles of the online tactic (4 x uint32 each)
+    std::uint32_t tile_capacity_{0};
+    std::int32_t* staging_{nullptr};    // pinned host: tokens | positions | page tables | tiles | argmax
 };
 
 } // namespace air

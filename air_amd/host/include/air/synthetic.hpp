@@ -28,8 +28,10 @@ namespace air {
 [[nodiscard]] Result<std::vector<std::byte>> quantize_rows(std::uint32_t format_type, std::span<const float> w,
                                                            std::uint64_t k, std::uint64_t n);
 
-// Deterministic N(0, sigma) values from a 64-bit seed.
-void normal_fill(std::span<float> out, std::uint64_t seed, float sigma);
+// Deterministic N(0, sigma) values from a 64-bit seed: out[j] is value
+// first + j of the seed's stream (first must be even), so chunks filled
+// independently equal one sequential fill.
+void normal_fill(std::span<float> out, std::uint64_t seed, float sigma, std::uint64_t first = 0);
 [[nodiscard]] std::uint64_t tensor_seed(std::uint64_t seed, const std::string& name) noexcept;
 
 struct SyntheticQwen2Spec {

@@ -80,6 +80,10 @@ HipPreparedModel::HipPreparedModel(std::shared_ptr<const ModelDefinition> model,
                                                     QuantizedLinearExecutionKind::hip_prefill};
     capabilities_.decode_block_quantized_linear = {QuantizedLinearExecutionKind::hip_decode};
     capabilities_.decode_output_quantized_linear = {QuantizedLinearExecutionKind::hip_decode};
+    // baseline: the reference executor's double-precision softmax; online:
+    // the tiled f32 online-softmax kernel.
+    capabilities_.prefill_attention = {AttentionExecutionKind::baseline, AttentionExecutionKind::online_softmax};
+    capabilities_.decode_attention = {AttentionExecutionKind::baseline, AttentionExecutionKind::online_softmax};
 }
 
 HipPreparedModel::~HipPreparedModel() {
@@ -327,8 +331,8 @@ Result<std::unique_ptr<runtime_detail::SequenceState>> HipPreparedModel::create_
     if (Status s = validate_execution_plan(plan, capabilities_); !s) return s;
     auto engine = engine_for(plan);
     if (!engine) return engine.status();
-    return std::unique_ptr<runtime_detail::SequenceState>(std::make_unique<HipSequence>(
-        *engine.value(), plan.linear.prefill_block, plan.linear.decode_block, plan.linear.decode_output));
+    return std::unique_ptr<runtime_detail::SequenceState>(
+        std::make_unique<HipSequence>(*engine.value(), plan.linear, plan.attention));
 }
 
 std::uint64_t HipPreparedModel::kv_pool_allocated_bytes() const noexcept {
@@ -357,9 +361,10 @@ Result<runtime_detail::PrefillBatchExecution> HipPreparedModel::prefill_batch(
     std::vector<std::size_t> owner;  // item of each row with an output
     QuantizedLinearExecutionKind block = QuantizedLinearExecutionKind::hip_decode;
     QuantizedLinearExecutionKind output = QuantizedLinearExecutionKind::hip_decode;
+    AttentionExecutionKind attention = AttentionExecutionKind::baseline;
     const auto flush = [&]() -> Status {
         if (rows.empty()) return Status::ok();
-        auto result = engine->run(rows, block, output);
+        auto result = engine->run(rows, block, output, attention);
         if (!result) return result.status();
         std::size_t g = 0, l = 0, o = 0;
         for (const auto& row : rows) {
@@ -377,11 +382,13 @@ Result<runtime_detail::PrefillBatchExecution> HipPreparedModel::prefill_batch(
     std::uint32_t sequences = 0;
     for (std::size_t i = 0; i < items.size(); ++i) {
         auto* seq = static_cast<HipSequence*>(items[i].sequence);
-        if (!rows.empty() && (seq->prefill_block_tactic() != block || seq->decode_output_tactic() != output)) {
+        if (!rows.empty() && (seq->prefill_block_tactic() != block || seq->decode_output_tactic() != output ||
+                              seq->prefill_attention() != attention)) {
             if (Status s = flush(); !s) return s;
         }
         block = seq->prefill_block_tactic();
         output = seq->decode_output_tactic();
+        attention = seq->prefill_attention();
         ++sequences;
         for (std::size_t t = 0; t < items[i].tokens.size(); ++t) {
             StepRow row{seq, items[i].tokens[t], RowOutput::none};
@@ -410,20 +417,26 @@ Result<std::vector<TokenId>> HipPreparedModel::decode_greedy_batch(
     if (items.size() > capabilities_.max_decode_batch_width) {
         return Status::invalid_argument("decode batch exceeds the advertised width");
     }
+    // One launch runs one tactic set: the first item's; items whose plan
+    // differs are refused (the service batches only matching plans).
     std::vector<StepRow> rows;
-    QuantizedLinearExecutionKind block = QuantizedLinearExecutionKind::hip_decode;
-    QuantizedLinearExecutionKind output = QuantizedLinearExecutionKind::hip_decode;
+    const HipSequence* first = nullptr;
     for (const auto& item : items) {
         auto* seq = dynamic_cast<HipSequence*>(item.sequence);
         if (!seq) return Status::invalid_argument("decode item is not a HIP sequence");
         for (const auto& row : rows) {
             if (row.sequence == seq) return Status::invalid_argument("a sequence appears twice in a decode batch");
         }
-        block = seq->decode_block_tactic();
-        output = seq->decode_output_tactic();
+        if (!first) first = seq;
+        if (seq->decode_block_tactic() != first->decode_block_tactic() ||
+            seq->decode_output_tactic() != first->decode_output_tactic() ||
+            seq->decode_attention() != first->decode_attention()) {
+            return Status::invalid_argument("decode batch mixes execution plans");
+        }
         rows.push_back({seq, item.token, RowOutput::greedy});
     }
-    auto result = engine_->run(rows, block, output);
+    auto result = engine_->run(rows, first->decode_block_tactic(), first->decode_output_tactic(),
+                               first->decode_attention());
     if (!result) return result.status();
     return std::move(result.value().greedy);
 }
@@ -474,12 +487,11 @@ std::optional<std::uint64_t> HipPreparedModel::free_device_bytes() const {
     return free;
 }
 
+// Before the first sequence, the free device memory its pool can take; after,
+// the fixed KV pool every sequence lives in.
 std::optional<std::uint64_t> HipPreparedModel::sequence_capacity_bytes() const {
-    const auto free = free_device_bytes();
-    if (!free) return std::nullopt;
-    const auto pool = kv_pool_allocated_bytes();
-    if (*free > std::numeric_limits<std::uint64_t>::max() - pool) return std::numeric_limits<std::uint64_t>::max();
-    return *free + pool;
+    if (engine_) return engine_->pool_bytes();
+    return free_device_bytes();
 }
 
 Result<std::unique_ptr<runtime_detail::PreparedModel>> prepare_hip_model(std::shared_ptr<const ModelDefinition> model,

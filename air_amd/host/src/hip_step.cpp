@@ -54,9 +54,13 @@ Result<std::vector<float>> norm_vector(const ModelDefinition& model, const std::
 
 // ---- HipSequence ------------------------------------------------------------
 
-HipSequence::HipSequence(HipStepEngine& engine, QuantizedLinearExecutionKind prefill_block,
-                         QuantizedLinearExecutionKind decode_block, QuantizedLinearExecutionKind decode_output)
-    : engine_(engine), prefill_block_(prefill_block), decode_block_(decode_block), decode_output_(decode_output) {}
+HipSequence::HipSequence(HipStepEngine& engine, const LinearPolicy& linear, const AttentionPolicy& attention)
+    : engine_(engine),
+      prefill_block_(linear.prefill_block),
+      decode_block_(linear.decode_block),
+      decode_output_(linear.decode_output),
+      prefill_attention_(attention.prefill),
+      decode_attention_(attention.decode) {}
 
 HipSequence::~HipSequence() { engine_.release_pages(pages_); }
 
@@ -80,7 +84,7 @@ Result<std::vector<float>> HipSequence::prefill(std::span<const TokenId> tokens)
         const std::size_t count = std::min(width, tokens.size() - begin);
         const bool last = begin + count == tokens.size();
         auto rows = prompt_rows(this, tokens.subspan(begin, count), last ? RowOutput::logits : RowOutput::none);
-        auto result = engine_.run(rows, prefill_block_, decode_output_);
+        auto result = engine_.run(rows, prefill_block_, decode_output_, prefill_attention_);
         if (!result) return result.status();
         if (last) logits = std::move(result.value().logits.front());
     }
@@ -93,7 +97,7 @@ Status HipSequence::prefill_discard(std::span<const TokenId> tokens) {
     for (std::size_t begin = 0; begin < tokens.size(); begin += width) {
         const std::size_t count = std::min(width, tokens.size() - begin);
         auto rows = prompt_rows(this, tokens.subspan(begin, count), RowOutput::none);
-        auto result = engine_.run(rows, prefill_block_, decode_output_);
+        auto result = engine_.run(rows, prefill_block_, decode_output_, prefill_attention_);
         if (!result) return result.status();
     }
     return Status::ok();
@@ -107,7 +111,7 @@ Result<TokenId> HipSequence::prefill_greedy(std::span<const TokenId> tokens) {
         const std::size_t count = std::min(width, tokens.size() - begin);
         const bool last = begin + count == tokens.size();
         auto rows = prompt_rows(this, tokens.subspan(begin, count), last ? RowOutput::greedy : RowOutput::none);
-        auto result = engine_.run(rows, prefill_block_, decode_output_);
+        auto result = engine_.run(rows, prefill_block_, decode_output_, prefill_attention_);
         if (!result) return result.status();
         if (last) token = result.value().greedy.front();
     }
@@ -116,14 +120,14 @@ Result<TokenId> HipSequence::prefill_greedy(std::span<const TokenId> tokens) {
 
 Result<std::vector<float>> HipSequence::decode(TokenId token) {
     const StepRow row{this, token, RowOutput::logits};
-    auto result = engine_.run({&row, 1}, decode_block_, decode_output_);
+    auto result = engine_.run({&row, 1}, decode_block_, decode_output_, decode_attention_);
     if (!result) return result.status();
     return std::move(result.value().logits.front());
 }
 
 Result<TokenId> HipSequence::decode_greedy(TokenId token) {
     const StepRow row{this, token, RowOutput::greedy};
-    auto result = engine_.run({&row, 1}, decode_block_, decode_output_);
+    auto result = engine_.run({&row, 1}, decode_block_, decode_output_, decode_attention_);
     if (!result) return result.status();
     return result.value().greedy.front();
 }
@@ -162,8 +166,6 @@ Result<std::unique_ptr<HipStepEngine>> HipStepEngine::create(const HipPreparedMo
     const auto& model = prepared.model();
     const auto& c = model.config();
     if (page_tokens == 0U) return Status::invalid_argument("KV page size must be non-zero");
-    if (pool_pages == 0U) return Status::invalid_argument("KV pool must hold at least one page");
-    if (pool_pages > static_cast<std::uint32_t>(INT32_MAX)) return Status::invalid_argument("KV pool is too large");
     if (max_rows == 0U || max_rows > 4096U) return Status::invalid_argument("step width must be in [1, 4096]");
     if (c.attention_head_count == 0U || c.embedding_size % c.attention_head_count != 0U) {
         return Status::data_error("embedding width must divide into the attention heads");
@@ -197,6 +199,18 @@ Result<std::unique_ptr<HipStepEngine>> HipStepEngine::create(const HipPreparedMo
     e->ffn_ = c.feed_forward_size;
     e->vocab_ = c.vocabulary_size;
     e->page_bytes_ = static_cast<std::uint64_t>(c.layer_count) * 2U * page_tokens * e->kv_width_ * sizeof(float);
+    if (pool_pages == 0U) {
+        const std::uint64_t tokens = std::min<std::uint64_t>(c.context_length, 4096U);
+        std::uint64_t pages = static_cast<std::uint64_t>(prepared.options().max_decode_rows) *
+                              ((tokens + page_tokens - 1U) / page_tokens);
+        if (const auto free = prepared.free_device_bytes()) {
+            pages = std::min<std::uint64_t>(pages, *free / 10U * 4U / e->page_bytes_);
+        }
+        pool_pages = static_cast<std::uint32_t>(std::min<std::uint64_t>(pages, INT32_MAX));
+        e->pool_pages_ = pool_pages;
+    }
+    if (pool_pages == 0U) return Status::invalid_state("no device memory for one KV page");
+    if (pool_pages > static_cast<std::uint32_t>(INT32_MAX)) return Status::invalid_argument("KV pool is too large");
 
     if (Status s = runtime_status(hipSetDevice(prepared.device()), "hipSetDevice"); !s) return s;
     const auto upload = [&](float** dst, const std::vector<float>& host, const char* what) -> Status {
@@ -299,7 +313,9 @@ Result<std::unique_ptr<HipStepEngine>> HipStepEngine::create(const HipPreparedMo
     if (!(s = buffer(&e->logits_, static_cast<std::uint64_t>(e->output_rows_) * e->vocab_, "hipMalloc(logits)"))) {
         return s;
     }
-    const std::uint64_t ints = rows * (2U + e->max_pages_);
+    // tokens | positions | page tables | attention tiles; a tile is 4 int32.
+    e->tile_capacity_ = max_rows * c.attention_head_count;
+    const std::uint64_t ints = rows * (2U + e->max_pages_) + 4ULL * e->tile_capacity_;
     if (!(s = e->allocate(reinterpret_cast<void**>(&e->tokens_dev_), ints * sizeof(std::int32_t), "hipMalloc(rows)"))) {
         return s;
     }
@@ -359,8 +375,10 @@ Status HipStepEngine::project(std::uint32_t layer, LinearRole fused, LinearRole 
 }
 
 // Embedding through the last layer's residual for `m` uploaded rows.
+// tiles > 0: the online_softmax attention over the uploaded tiles; 0: the
+// baseline (reference arithmetic) attention.
 Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uint32_t table_pages,
-                             QuantizedLinearExecutionKind tactic) {
+                             QuantizedLinearExecutionKind tactic, std::uint32_t tiles) {
     const auto& c = prepared_.model().config();
     air_hip_context* ctx = prepared_.context();
     const air_hip_kv_layout kv{pool_, page_tokens_, kv_width_, c.layer_count, table_pages, pool_pages_};
@@ -384,11 +402,13 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
             AIR_HIP_OK) {
             return hip_status(rc);
         }
-        if ((rc = air_hip_attention(ctx, &kv, qkv_, qkv_width_, m, positions_dev_, tables_dev_, l,
-                                    c.attention_head_count, c.kv_head_count, head_dim_, max_tokens, att_)) !=
-            AIR_HIP_OK) {
-            return hip_status(rc);
-        }
+        rc = tiles ? air_hip_attention_online(ctx, &kv, qkv_, qkv_width_, m, positions_dev_, tables_dev_, l,
+                                              c.attention_head_count, c.kv_head_count, head_dim_,
+                                              reinterpret_cast<const air_hip_attention_tile*>(tiles_dev_), tiles,
+                                              max_tokens, att_)
+                   : air_hip_attention(ctx, &kv, qkv_, qkv_width_, m, positions_dev_, tables_dev_, l,
+                                       c.attention_head_count, c.kv_head_count, head_dim_, max_tokens, att_);
+        if (rc != AIR_HIP_OK) return hip_status(rc);
         if (Status s = prepared_.linear(l, LinearRole::attn_output, att_, proj_, m, tactic); !s) return s;
         if ((rc = air_hip_add(ctx, hidden_, proj_, hidden_floats)) != AIR_HIP_OK) return hip_status(rc);
         if ((rc = air_hip_rms_norm(ctx, hidden_, ffn_norm_[l], normed_, m, embed_, c.rms_norm_epsilon)) != AIR_HIP_OK) {
@@ -407,7 +427,7 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
 }
 
 Result<StepResult> HipStepEngine::run(std::span<const StepRow> rows, QuantizedLinearExecutionKind block_tactic,
-                                      QuantizedLinearExecutionKind output_tactic) {
+                                      QuantizedLinearExecutionKind output_tactic, AttentionExecutionKind attention) {
     const auto& c = prepared_.model().config();
     if (rows.empty()) return Status::invalid_argument("a step needs at least one row");
     if (rows.size() > max_rows_) {
@@ -487,8 +507,30 @@ Result<StepResult> HipStepEngine::run(std::span<const StepRow> rows, QuantizedLi
         std::int32_t* table = host + 2U * m + static_cast<std::uint64_t>(r) * table_pages;
         for (std::uint32_t p = 0; p < table_pages; ++p) table[p] = p < pages.size() ? pages[p] : -1;
     }
+    // Online attention: tiles from the runs of consecutive rows of one sequence.
+    std::uint32_t tiles = 0;
+    std::uint64_t upload_ints = 2U * m + static_cast<std::uint64_t>(m) * table_pages;
+    if (attention == AttentionExecutionKind::online_softmax) {
+        std::vector<std::uint32_t> runs;
+        for (std::uint32_t r = 0; r < m; ++r) {
+            if (r > 0 && rows[r].sequence == rows[r - 1].sequence) {
+                ++runs.back();
+            } else {
+                runs.push_back(1U);
+            }
+        }
+        auto* tile_host = reinterpret_cast<air_hip_attention_tile*>(host + upload_ints);
+        const int rc = air_hip_attention_make_tiles(runs.data(), static_cast<std::uint32_t>(runs.size()),
+                                                    c.attention_head_count, c.kv_head_count, tile_host,
+                                                    tile_capacity_, &tiles);
+        if (rc != AIR_HIP_OK) {
+            rollback();
+            return hip_status(rc);
+        }
+        tiles_dev_ = tokens_dev_ + upload_ints;
+        upload_ints += 4ULL * tiles;
+    }
     // Device arrays are packed the same way as the host staging.
-    const std::uint64_t upload_ints = 2U * m + static_cast<std::uint64_t>(m) * table_pages;
     auto* hs = static_cast<hipStream_t>(stream());
     if (Status s = runtime_status(hipSetDevice(prepared_.device()), "hipSetDevice"); !s) {
         rollback();
@@ -506,7 +548,7 @@ Result<StepResult> HipStepEngine::run(std::span<const StepRow> rows, QuantizedLi
     positions_dev_ = positions_dev;
     tables_dev_ = tables_dev;
 
-    Status status = layers(m, max_tokens, table_pages, block_tactic);
+    Status status = layers(m, max_tokens, table_pages, block_tactic, tiles);
 
     // Output rows: final RMSNorm, lm_head (+bias), argmax, in chunks of the
     // logits buffer.

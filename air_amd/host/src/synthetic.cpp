@@ -8,8 +8,10 @@
 #include "air/synthetic.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstring>
+#include <thread>
 
 namespace air {
 
@@ -151,6 +153,22 @@ void quantize_q4_k_block(const float* b, std::byte* out) noexcept {
     }
 }
 
+// `blocks` consecutive blocks of `format_type` from w into out.
+void quantize_blocks(std::uint32_t format_type, const float* w, std::uint64_t blocks, std::byte* out) noexcept {
+    const auto g = format_geometry(format_type);
+    for (std::uint64_t i = 0; i < blocks; ++i) {
+        const float* src = w + i * g.block_elements;
+        std::byte* dst = out + i * g.block_bytes;
+        switch (static_cast<GgmlType>(format_type)) {
+        case GgmlType::f32: std::memcpy(dst, src, 4); break;
+        case GgmlType::f16: put_f16(dst, *src); break;
+        case GgmlType::q8_0: quantize_q8_0_block(src, dst); break;
+        case GgmlType::q4_0: quantize_q4_0_block(src, dst); break;
+        case GgmlType::q4_k: quantize_q4_k_block(src, dst); break;
+        }
+    }
+}
+
 } // namespace
 
 Result<std::vector<std::byte>> quantize_rows(std::uint32_t format_type, std::span<const float> w, std::uint64_t k,
@@ -160,24 +178,15 @@ Result<std::vector<std::byte>> quantize_rows(std::uint32_t format_type, std::spa
     if (!bytes) return bytes.status();
     if (w.size() != k * n) return Status::invalid_argument("quantize_rows: value count does not match k x n");
     std::vector<std::byte> out(bytes.value());
-    const auto g = format_geometry(format_type);
-    const std::uint64_t blocks = k * n / g.block_elements;
-    for (std::uint64_t i = 0; i < blocks; ++i) {
-        const float* src = w.data() + i * g.block_elements;
-        std::byte* dst = out.data() + i * g.block_bytes;
-        switch (static_cast<GgmlType>(format_type)) {
-        case GgmlType::f32: std::memcpy(dst, src, 4); break;
-        case GgmlType::f16: put_f16(dst, *src); break;
-        case GgmlType::q8_0: quantize_q8_0_block(src, dst); break;
-        case GgmlType::q4_0: quantize_q4_0_block(src, dst); break;
-        case GgmlType::q4_k: quantize_q4_k_block(src, dst); break;
-        }
-    }
+    quantize_blocks(format_type, w.data(), k * n / format_geometry(format_type).block_elements, out.data());
     return out;
 }
 
-void normal_fill(std::span<float> out, std::uint64_t seed, float sigma) {
-    std::uint64_t state = seed;
+// Value i of the stream is the (i mod 2) half of Box-Muller pair i / 2, made
+// from splitmix64 draws i and i + 1; a chunk starting at an even `first`
+// therefore starts from state seed + first * gamma.
+void normal_fill(std::span<float> out, std::uint64_t seed, float sigma, std::uint64_t first) {
+    std::uint64_t state = seed + first * 0x9E3779B97F4A7C15ULL;
     constexpr double kTwoPi = 6.283185307179586476925286766559;
     for (std::size_t i = 0; i < out.size(); i += 2) {
         // Box-Muller over two 53-bit uniforms, u1 in (0, 1].
@@ -271,16 +280,42 @@ Result<std::shared_ptr<const ModelDefinition>> make_synthetic_qwen2(const Synthe
         tensors.push_back(std::move(t));
     }
 
+    // Chunks of 2^20 values (whole blocks, even offsets) filled and quantized
+    // on up to 16 threads; the bytes equal a sequential fill.
     std::vector<std::byte> storage(offset);
-    std::vector<float> values;
+    struct Job {
+        std::size_t tensor;
+        std::uint64_t first, count;
+    };
+    constexpr std::uint64_t kChunk = 1ULL << 20;
+    std::vector<Job> jobs;
     for (std::size_t i = 0; i < pending.size(); ++i) {
-        const auto& p = pending[i];
-        values.assign(p.k * p.n, 1.0f);
-        if (p.fill == Pending::normal) normal_fill(values, tensor_seed(spec.seed, p.name), spec.sigma);
-        auto bytes = quantize_rows(p.format, values, p.k, p.n);
-        if (!bytes) return bytes.status();
-        std::memcpy(storage.data() + tensors[i].byte_offset, bytes.value().data(), bytes.value().size());
+        const std::uint64_t total = pending[i].k * pending[i].n;
+        for (std::uint64_t first = 0; first < total; first += kChunk) {
+            jobs.push_back({i, first, std::min(kChunk, total - first)});
+        }
     }
+    std::atomic<std::size_t> next{0};
+    const auto worker = [&]() {
+        std::vector<float> values;
+        for (std::size_t j = next.fetch_add(1); j < jobs.size(); j = next.fetch_add(1)) {
+            const auto& job = jobs[j];
+            const auto& p = pending[job.tensor];
+            values.assign(job.count, 1.0f);
+            if (p.fill == Pending::normal) {
+                normal_fill(values, tensor_seed(spec.seed, p.name), spec.sigma, job.first);
+            }
+            const auto g = format_geometry(p.format);
+            quantize_blocks(p.format, values.data(), job.count / g.block_elements,
+                            storage.data() + tensors[job.tensor].byte_offset +
+                                job.first / g.block_elements * g.block_bytes);
+        }
+    };
+    const unsigned threads = std::clamp(std::thread::hardware_concurrency(), 1U, 16U);
+    std::vector<std::thread> pool;
+    for (unsigned t = 1; t < threads && jobs.size() > 1U; ++t) pool.emplace_back(worker);
+    worker();
+    for (auto& t : pool) t.join();
     auto model = std::make_shared<const ModelDefinition>(
         c, std::move(tensors), std::make_shared<const BufferStorage>(std::move(storage)));
     if (Status s = model->validate(); !s) return s;

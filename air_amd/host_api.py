@@ -1,0 +1,171 @@
+"""ctypes binding of libair_host.so (the C ABI declared in include/air_host.h).
+
+The host library is the C++ executor: model definitions, the HIP prepared
+model with its Qwen2 step engine and paged KV, and TokenService, the token-id
+caller slice of AIR's InferenceService (src/runtime/serving.cpp:2401-2481).
+Importing this module fails loudly when the library has not been built; no
+part of it falls back to Python or CPU compute.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import List, Optional, Sequence
+
+from . import capi
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libair_host.so")
+
+_P = ctypes.c_void_p
+_PP = ctypes.POINTER(ctypes.c_void_p)
+_U32 = ctypes.c_uint32
+_U64 = ctypes.c_uint64
+_I32 = ctypes.c_int32
+_I = ctypes.c_int
+
+
+class Qwen2Spec(ctypes.Structure):
+    _fields_ = [
+        ("layers", _U32), ("embedding", _U32), ("ffn", _U32), ("heads", _U32), ("kv_heads", _U32),
+        ("vocab", _U64), ("context", _U64), ("weight_format", _U32), ("embedding_format", _U32),
+        ("seed", _U64), ("sigma", ctypes.c_float), ("qkv_bias", _I32), ("output_bias", _I32),
+        ("tied_output", _I32),
+    ]
+
+
+class EngineConfig(ctypes.Structure):
+    _fields_ = [
+        ("device", _I32), ("page_tokens", _U32), ("kv_pool_pages", _U32), ("max_step_rows", _U32),
+        ("prefill_tactic", _I32), ("prefill_quantum_tokens", _U32), ("token_budget_per_cycle", _U32),
+        ("max_active_requests", _U32), ("attention_tactic", _I32),
+    ]
+
+
+class CohortStats(ctypes.Structure):
+    _fields_ = [
+        ("wall_ms", ctypes.c_double), ("prefill_ms", ctypes.c_double), ("decode_ms", ctypes.c_double),
+        ("cycles", _U64), ("prefill_calls", _U64), ("prefill_tokens", _U64), ("decode_calls", _U64),
+        ("decode_rows", _U64), ("max_decode_width", _U32), ("max_prefill_sequences", _U32),
+        ("generated_tokens", _U64), ("mean_ttft_ms", ctypes.c_double),
+    ]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+# Every exported entry point of include/air_host.h: name -> (restype, argtypes).
+SIGNATURES = {
+    "air_host_abi_version": (_I, []),
+    "air_host_last_error": (ctypes.c_char_p, []),
+    "air_host_synthetic_qwen2": (_I, [ctypes.POINTER(Qwen2Spec), _PP]),
+    "air_host_model_describe": (_I, [_P, ctypes.POINTER(_U64), ctypes.POINTER(_U64)]),
+    "air_host_model_release": (_I, [_P]),
+    "air_host_engine_create": (_I, [_P, ctypes.POINTER(EngineConfig), _PP]),
+    "air_host_engine_release": (_I, [_P]),
+    "air_host_generate_cohort": (_I, [_P, ctypes.POINTER(_I32), ctypes.POINTER(_U32), _U32, _U32, _I32,
+                                      ctypes.POINTER(_I32), ctypes.POINTER(_U32), ctypes.POINTER(CohortStats)]),
+}
+
+ATTENTION_BASELINE = 0   # the reference executor's double-precision softmax
+ATTENTION_ONLINE = 1     # tiled f32 online softmax
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded host library (libair_hip.so is loaded first, as its dependency)."""
+    global _lib
+    if _lib is None:
+        capi.lib()
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = handle
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != capi.AIR_HIP_OK:
+        message = lib().air_host_last_error().decode(errors="replace")
+        raise capi.HipError(status, message)
+
+
+class Model:
+    """A model definition held by the host library."""
+
+    def __init__(self, handle: int):
+        self.handle = handle
+
+    @classmethod
+    def synthetic_qwen2(cls, layers: int, embedding: int, ffn: int, heads: int, kv_heads: int, vocab: int,
+                        context: int = 4096, weight_format: int = capi.TYPE_Q8_0,
+                        embedding_format: int = capi.TYPE_Q8_0, seed: int = 0xA17C0DE, sigma: float = 0.02,
+                        qkv_bias: bool = True, output_bias: bool = False, tied_output: bool = False) -> "Model":
+        spec = Qwen2Spec(layers, embedding, ffn, heads, kv_heads, vocab, context, weight_format,
+                         embedding_format, seed, sigma, int(qkv_bias), int(output_bias), int(tied_output))
+        out = ctypes.c_void_p()
+        check(lib().air_host_synthetic_qwen2(ctypes.byref(spec), ctypes.byref(out)))
+        return cls(out.value)
+
+    def describe(self):
+        storage, tensors = _U64(), _U64()
+        check(lib().air_host_model_describe(self.handle, ctypes.byref(storage), ctypes.byref(tensors)))
+        return storage.value, tensors.value
+
+    def close(self) -> None:
+        if self.handle:
+            lib().air_host_model_release(self.handle)
+            self.handle = None
+
+    def __del__(self):  # pragma: no cover - interpreter shutdown order
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Engine:
+    """A prepared model on one device plus its token service."""
+
+    def __init__(self, model: Model, device: int = 0, page_tokens: int = 16, kv_pool_pages: int = 0,
+                 max_step_rows: int = 512, prefill_tactic: int = capi.LINEAR_PREFILL,
+                 prefill_quantum_tokens: int = 512, token_budget_per_cycle: int = 512,
+                 max_active_requests: int = 64, attention: int = ATTENTION_ONLINE):
+        config = EngineConfig(device, page_tokens, kv_pool_pages, max_step_rows, prefill_tactic,
+                              prefill_quantum_tokens, token_budget_per_cycle, max_active_requests, attention)
+        out = ctypes.c_void_p()
+        check(lib().air_host_engine_create(model.handle, ctypes.byref(config), ctypes.byref(out)))
+        self.handle = out.value
+
+    def generate_cohort(self, prompts: Sequence[Sequence[int]], max_new_tokens: int,
+                        stop_token: int = -1):
+        """Greedy tokens of every prompt (list of lists) and the cohort's CohortStats."""
+        n = len(prompts)
+        flat = [int(t) for p in prompts for t in p]
+        tokens = (_I32 * max(len(flat), 1))(*flat)
+        lengths = (_U32 * max(n, 1))(*[len(p) for p in prompts])
+        out = (_I32 * max(n * max_new_tokens, 1))()
+        counts = (_U32 * max(n, 1))()
+        stats = CohortStats()
+        check(lib().air_host_generate_cohort(self.handle, tokens, lengths, n, max_new_tokens, stop_token, out,
+                                             counts, ctypes.byref(stats)))
+        result: List[List[int]] = []
+        for i in range(n):
+            result.append([out[i * max_new_tokens + t] for t in range(counts[i])])
+        return result, stats
+
+    def close(self) -> None:
+        if self.handle:
+            lib().air_host_engine_release(self.handle)
+            self.handle = None
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass

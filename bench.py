@@ -239,6 +239,58 @@ def measure_prefill(torch, ctx, capi, layers, m, steps, dev, stream):
             "mfma_frac": round(tflops / F16_MFMA_PEAK_TFLOPS, 4), "dtype": "f16 operands, f32 accumulate"}
 
 
+def measure_e2e(sequences: int, prompt_tokens: int, new_tokens: int, layers: int) -> dict:
+    """a random-init Qwen2-7B-shaped Q8_0 model through TokenService
+    (admission, MicrobatchScheduler cycles, prefill_batch at up to 512 rows on
+    the f16 MFMA tactic, decode_greedy_batch at one row per sequence), fp32
+    paged KV of 16-token pages, device greedy selection.  The cohort is
+    `sequences` prompts of `prompt_tokens` uniform token ids generating
+    `new_tokens` greedy tokens each; then one request alone (decode at M=1)."""
+    import numpy as np
+
+    from air_amd import capi, host_api
+
+    t0 = time.perf_counter()
+    model = host_api.Model.synthetic_qwen2(layers, HIDDEN, FFN, 28, 4, VOCAB, context=4096,
+                                           weight_format=capi.TYPE_Q8_0, embedding_format=capi.TYPE_Q8_0,
+                                           seed=0xA17C0DE)
+    gen_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    pages = sequences * ((prompt_tokens + new_tokens + 15) // 16) + 64
+    engine = host_api.Engine(model, page_tokens=16, kv_pool_pages=pages, max_step_rows=512,
+                             prefill_tactic=capi.LINEAR_PREFILL, prefill_quantum_tokens=512,
+                             token_budget_per_cycle=512, max_active_requests=64,
+                             attention=host_api.ATTENTION_ONLINE)
+    prepare_s = time.perf_counter() - t0
+    rng = np.random.default_rng(4)
+    prompts = rng.integers(0, VOCAB, size=(sequences, prompt_tokens)).tolist()
+    engine.generate_cohort([p[:64] for p in prompts[:4]], 4)          # warm-up: workspaces, KV pool
+    tokens, st = engine.generate_cohort(prompts, new_tokens)
+    generated = sum(len(t) for t in tokens)
+    _, st1 = engine.generate_cohort([prompts[0]], new_tokens)
+    engine.close()
+    model.close()
+    return {
+        "workload": f"configs[4]: {sequences} sequences x {prompt_tokens}-token prompts, {new_tokens} greedy tokens "
+                    f"each, Qwen2-7B shape ({layers} layers), Q8_0, TokenService on one GPU",
+        "generated_tok_s": round(generated / (st.wall_ms * 1e-3), 1),
+        "wall_s": round(st.wall_ms * 1e-3, 3),
+        "prefill_tok_s": round(st.prefill_tokens / (st.prefill_ms * 1e-3), 1),
+        "decode_tok_s": round(st.decode_rows / (st.decode_ms * 1e-3), 1),
+        "decode_max_width": st.max_decode_width,
+        "mean_ttft_ms": round(st.mean_ttft_ms, 1),
+        "prefill_calls": st.prefill_calls,
+        "decode_calls": st.decode_calls,
+        "cycles": st.cycles,
+        "m1_decode_tok_s": round(st1.decode_rows / (st1.decode_ms * 1e-3), 1),
+        "m1_ms_per_token": round(st1.decode_ms / max(st1.decode_rows, 1), 3),
+        "m1_prefill_ms": round(st1.prefill_ms, 2),
+        "attention": "online_softmax",
+        "model_generate_s": round(gen_s, 1),
+        "prepare_s": round(prepare_s, 1),
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -250,6 +302,9 @@ def main() -> int:
     ap.add_argument("--graph", type=int, default=1, help="replay each step as a captured HIP graph (1) or launch eagerly (0)")
     ap.add_argument("--prefill-m", type=int, default=512,
                     help="also time the prefill tactic (f16 MFMA GEMM) over the 28 layers' linears at this M (0 = skip)")
+    ap.add_argument("--e2e", default="32,512,128",
+                    help="configs[4] end to end: sequences,prompt,new tokens through TokenService ('' = skip)")
+    ap.add_argument("--e2e-only", action="store_true", help="run only the end-to-end leg and print its JSON")
     ap.add_argument("--trace-summary", default=None, metavar="CSV",
                     help="summarise a rocprofv3 kernel-trace CSV instead of benchmarking")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -272,6 +327,11 @@ def main() -> int:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(the engine runs on one GPU; its linears shard over output rows)", file=sys.stderr)
         return 2
+
+    if args.e2e_only:
+        seqs, prompt, new = (int(v) for v in args.e2e.split(","))
+        print(json.dumps(measure_e2e(seqs, prompt, new, args.layers)), flush=True)
+        return 0
 
     import numpy as np
     import torch
@@ -433,6 +493,14 @@ def main() -> int:
         cpu = cpu_baseline(cpu_sample, HIDDEN, 2 * FFN, args.cpu_seconds)
         print(f"# cpu baseline: {cpu}", file=sys.stderr, flush=True)
 
+    e2e = None
+    if args.e2e:
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        seqs, prompt, new = (int(v) for v in args.e2e.split(","))
+        e2e = measure_e2e(seqs, prompt, new, args.layers)
+        print(f"# e2e: {e2e}", file=sys.stderr, flush=True)
+
     head = ms[0]
     line = {
         "metric": "Q8_0 linear HBM GB/s (% of peak) + Qwen2-7B-shape decode tok/s at M=1/32",
@@ -460,6 +528,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "e2e": e2e,
     }
     print(json.dumps(line), flush=True)
     ctx.close()

@@ -269,6 +269,39 @@ int air_hip_attention(air_hip_context* ctx, const air_hip_kv_layout* kv, const f
                       uint32_t m, const int32_t* positions, const int32_t* page_tables, uint32_t layer,
                       uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim, uint64_t max_tokens, float* out);
 
+/* The online_softmax attention tactic (AttentionExecutionKind::online_softmax,
+ * include/air/execution.hpp:47-50; the reference's
+ * attention_batch_paged_online_kernel, cuda_backend.cu:1089-1154): the same
+ * output as air_hip_attention, computed in f32 with a running maximum over
+ * key chunks staged through LDS, ~1e-6 relative from the double softmax.
+ * Work is cut into tiles of up to 16 query vectors that share a sequence and
+ * a KV head. */
+typedef struct air_hip_attention_tile {
+    uint32_t row;    /* first row */
+    uint32_t rows;   /* rows of one sequence, consecutive in the step */
+    uint32_t head;   /* first q head */
+    uint32_t heads;  /* q heads of one KV head; rows * heads <= 16 */
+} air_hip_attention_tile;
+
+/* Host helper: the tiles of a step whose rows form `runs` consecutive runs,
+ * run i holding run_rows[i] rows of one sequence at consecutive positions.
+ * A one-row run (decode) gives a tile per KV head of its grouped q heads; a
+ * longer run (prefill) tiles of 16 rows per q head.  tiles may be NULL (the
+ * count is still returned). */
+int air_hip_attention_make_tiles(const uint32_t* run_rows, uint32_t runs, uint32_t q_heads, uint32_t kv_heads,
+                                 air_hip_attention_tile* tiles, uint32_t capacity, uint32_t* count);
+
+/* Attention through tiles made by air_hip_attention_make_tiles for these m
+ * rows (device array, uploaded by the caller; the kernel skips a tile that
+ * names rows or heads outside the call).  head_dim 64 or 128; q|k|v rows,
+ * out and the pool 16-byte aligned.  Tiles with long key ranges are split
+ * over workgroups and merged in a second pass (context scratch). */
+int air_hip_attention_online(air_hip_context* ctx, const air_hip_kv_layout* kv, const float* qkv, uint64_t row_stride,
+                             uint32_t m, const int32_t* positions, const int32_t* page_tables, uint32_t layer,
+                             uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim,
+                             const air_hip_attention_tile* tiles, uint32_t tile_count, uint64_t max_tokens,
+                             float* out);
+
 /* out[r][i] = silu(gate_up[r][i]) * gate_up[r][ffn + i] over fused gate|up
  * rows (reference_executor.cpp:33-35, 400). */
 int air_hip_silu_mul(air_hip_context* ctx, const float* gate_up, float* out, uint32_t m, uint64_t ffn);

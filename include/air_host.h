@@ -1,0 +1,102 @@
+/*
+ * air_host.h -- C ABI of the host executor library (libair_host.so).
+ *
+ * libair_host.so is the C++20 executor around the kernel library of
+ * air_hip.h: model definitions, HipPreparedModel (resident weights, the
+ * Qwen2 step engine, paged KV), CapacityScheduler / MicrobatchScheduler and
+ * TokenService, the token-id caller slice of InferenceService
+ * (src/runtime/serving.cpp:2401-2481).  This header exposes that caller
+ * slice to non-C++ callers (Python ctypes in this repository): build or load
+ * a model, prepare it on a device, run a cohort of greedy token requests.
+ *
+ * Conventions follow air_hip.h: plain C types, air_hip_status return codes,
+ * air_host_last_error() for the calling thread's message, explicit release.
+ */
+#ifndef AIR_HOST_H
+#define AIR_HOST_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AIR_HOST_ABI_VERSION 1
+
+typedef struct air_host_model air_host_model;
+typedef struct air_host_engine air_host_engine;
+
+int air_host_abi_version(void);
+const char* air_host_last_error(void);
+
+/* Random-init Qwen2 model (weights N(0, sigma) quantized to weight_format,
+ * norms 1, RoPE theta 1e6, RMSNorm eps 1e-6), generated on the host; the
+ * same bytes for the same spec on every machine. */
+typedef struct air_host_qwen2_spec {
+    uint32_t layers;
+    uint32_t embedding;
+    uint32_t ffn;
+    uint32_t heads;
+    uint32_t kv_heads;
+    uint64_t vocab;
+    uint64_t context;
+    uint32_t weight_format;     /* GGML type id: 8 Q8_0, 2 Q4_0, 12 Q4_K */
+    uint32_t embedding_format;
+    uint64_t seed;
+    float sigma;
+    int32_t qkv_bias;
+    int32_t output_bias;
+    int32_t tied_output;
+} air_host_qwen2_spec;
+
+int air_host_synthetic_qwen2(const air_host_qwen2_spec* spec, air_host_model** out);
+/* Model bytes and tensor count, for callers that size host memory. */
+int air_host_model_describe(const air_host_model* model, uint64_t* storage_bytes, uint64_t* tensors);
+int air_host_model_release(air_host_model* model);
+
+typedef struct air_host_engine_config {
+    int32_t device;
+    uint32_t page_tokens;          /* KV page size in tokens (16 in the reference's CUDA plans) */
+    uint32_t kv_pool_pages;        /* KV pages allocated with the first sequence */
+    uint32_t max_step_rows;        /* rows per device step (prefill width) */
+    int32_t prefill_tactic;        /* AIR_HIP_LINEAR_DECODE or AIR_HIP_LINEAR_PREFILL for prompt blocks */
+    uint32_t prefill_quantum_tokens;
+    uint32_t token_budget_per_cycle;
+    uint32_t max_active_requests;
+    int32_t attention_tactic;      /* 0 baseline (the reference's double softmax), 1 online softmax (tiled f32) */
+} air_host_engine_config;
+
+/* Prepares the model on `device` (weights resident, repacked) and creates
+ * the token service.  The engine keeps the model alive. */
+int air_host_engine_create(const air_host_model* model, const air_host_engine_config* config, air_host_engine** out);
+int air_host_engine_release(air_host_engine* engine);
+
+typedef struct air_host_cohort_stats {
+    double wall_ms;                /* whole cohort, submission to last token */
+    double prefill_ms;             /* inside prefill_batch calls */
+    double decode_ms;              /* inside decode_greedy_batch calls */
+    uint64_t cycles;
+    uint64_t prefill_calls;
+    uint64_t prefill_tokens;
+    uint64_t decode_calls;
+    uint64_t decode_rows;
+    uint32_t max_decode_width;
+    uint32_t max_prefill_sequences;
+    uint64_t generated_tokens;
+    double mean_ttft_ms;
+} air_host_cohort_stats;
+
+/* Runs `requests` greedy requests to completion.  Prompts are concatenated
+ * in prompt_tokens with prompt_lengths[i] tokens each; out_tokens holds
+ * requests x max_new_tokens ids (row i = request i), out_counts[i] the
+ * number generated (fewer when stop_token >= 0 was produced).  stats may be
+ * NULL; its counters cover this call only. */
+int air_host_generate_cohort(air_host_engine* engine, const int32_t* prompt_tokens, const uint32_t* prompt_lengths,
+                             uint32_t requests, uint32_t max_new_tokens, int32_t stop_token, int32_t* out_tokens,
+                             uint32_t* out_counts, air_host_cohort_stats* stats);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AIR_HOST_H */

@@ -574,7 +574,34 @@ void test_qwen2_oracle_matches_reference() {
     }
 }
 
+// Chunked generation equals one sequential fill: the value stream at an even
+// offset, and a model tensor larger than one 2^20-value chunk.
+void test_parallel_synthetic() {
+    constexpr std::size_t n = (1U << 21) + 4096U + 6U;
+    std::vector<float> whole(n), parts(n);
+    air::normal_fill(whole, 0x1234ULL, 0.02f);
+    const std::size_t cuts[] = {0U, 1000U, 1U << 20, (1U << 21) + 2U, n};
+    for (std::size_t i = 0; i + 1 < std::size(cuts); ++i) {
+        air::normal_fill(std::span<float>(parts).subspan(cuts[i], cuts[i + 1] - cuts[i]), 0x1234ULL, 0.02f, cuts[i]);
+    }
+    check(std::memcmp(whole.data(), parts.data(), n * sizeof(float)) == 0, "chunked normal_fill equals sequential");
+    air::SyntheticQwen2Spec spec;
+    spec.config = air::qwen2_config(1, 256, 512, 4, 2, 9000, 64);
+    auto model = air::make_synthetic_qwen2(spec);
+    check(model.is_ok(), "synthetic model with multi-chunk tensors");
+    if (!model) return;
+    const auto* t = model.value()->find_tensor("token_embd.weight");
+    std::vector<float> values(256U * 9000U);
+    air::normal_fill(values, air::tensor_seed(spec.seed, "token_embd.weight"), spec.sigma);
+    const auto expect = air::quantize_rows(spec.embedding_format, values, 256U, 9000U);
+    const auto got = model.value()->tensor_bytes(*t);
+    check(expect && got && got.value().size() == expect.value().size() &&
+              std::memcmp(got.value().data(), expect.value().data(), expect.value().size()) == 0,
+          "a 2.3M-value tensor generated in parallel equals the sequential bytes");
+}
+
 int run_cpu() {
+    test_parallel_synthetic();
     test_qwen2_oracle_matches_reference();
     test_capacity_reservations();
     test_plan_preparation_capacity();
@@ -817,11 +844,19 @@ std::int32_t first_max(const std::vector<float>& v) {
     return static_cast<std::int32_t>(best);
 }
 
+// The attention tactic of the GPU sequence tests; each suite runs once per tactic.
+air::AttentionExecutionKind g_attention = air::AttentionExecutionKind::baseline;
+
+const char* attention_name() {
+    return g_attention == air::AttentionExecutionKind::online_softmax ? " online" : " baseline";
+}
+
 air::ExecutionPlan hip_plan(air::QuantizedLinearExecutionKind prefill_block, std::uint32_t page_tokens) {
     auto plan = paged_plan();
     plan.kv.page_tokens = page_tokens;
     plan.linear = {prefill_block, air::QuantizedLinearExecutionKind::hip_decode,
                    air::QuantizedLinearExecutionKind::hip_decode};
+    plan.attention = {g_attention, g_attention};
     return plan;
 }
 
@@ -838,7 +873,8 @@ void gpu_golden_sequences(bool fuse, std::uint32_t page_tokens, std::uint32_t st
     check(cases.size() == 3U, "three golden Qwen2 cases");
     for (const auto& c : cases) {
         const std::string tag = "golden " + c.name + (fuse ? " fused" : " unfused") + " page " +
-                                std::to_string(page_tokens) + " step " + std::to_string(step_rows);
+                                std::to_string(page_tokens) + " step " + std::to_string(step_rows) +
+                                attention_name();
         std::cout << tag << std::endl;
         auto model = air::make_synthetic_qwen2(c.spec);
         if (!model) {
@@ -960,7 +996,7 @@ void gpu_long_sequences_vs_oracle(std::uint32_t format) {
     spec.config = air::qwen2_config(2, 256, 512, 4, 2, 512, 96);
     spec.weight_format = format;
     spec.seed = 0xA17C0DE5ULL + format;
-    const std::string tag = "long sequences format " + std::to_string(format);
+    const std::string tag = "long sequences format " + std::to_string(format) + attention_name();
     std::cout << tag << std::endl;
     auto model = air::make_synthetic_qwen2(spec);
     if (!model) {
@@ -1093,11 +1129,15 @@ int run_gpu() {
         return 2;
     }
     gpu_prepared_model_contract();
-    gpu_golden_sequences(true, 16U, 512U);
-    gpu_golden_sequences(false, 4U, 3U);
-    gpu_long_sequences_vs_oracle(8U);
-    gpu_long_sequences_vs_oracle(2U);
-    gpu_long_sequences_vs_oracle(12U);
+    for (const auto attention : {air::AttentionExecutionKind::baseline, air::AttentionExecutionKind::online_softmax}) {
+        g_attention = attention;
+        gpu_golden_sequences(true, 16U, 512U);
+        gpu_golden_sequences(false, 4U, 3U);
+        gpu_long_sequences_vs_oracle(8U);
+        gpu_long_sequences_vs_oracle(2U);
+        gpu_long_sequences_vs_oracle(12U);
+    }
+    g_attention = air::AttentionExecutionKind::baseline;
     gpu_pool_exhaustion();
     gpu_model_case(8U, true, false, false);
     gpu_model_case(8U, false, true, true);

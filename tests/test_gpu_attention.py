@@ -1,0 +1,133 @@
+"""The two attention tactics over the paged fp32 KV pool.
+
+cpu: tile construction of the online tactic (air_hip_attention_make_tiles).
+gpu: at Qwen2-7B head geometry (28 q heads, 4 KV heads of 128) and at the
+     0.5B-like geometry of the tiny models (head 64), one step mixing decode
+     rows of many lengths with a 100-row prompt run: the online tactic equals
+     the baseline (the reference executor's double softmax) within 1e-5
+     relative, and both equal a float64 CPU attention computed from the same
+     pool.  Split tiles (few rows, long keys) go through the merge pass.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from air_amd import capi
+
+
+def test_tiles_for_decode_and_prefill_runs():
+    # Two decode rows at 7B geometry: one tile per KV head with its 7 q heads.
+    tiles = capi.attention_tiles([1, 1], 28, 4)
+    assert tiles == [(r, 1, 7 * h, 7) for r in range(2) for h in range(4)]
+    # A 37-row prompt run: 16-row tiles of one q head.
+    tiles = capi.attention_tiles([37], 4, 2)
+    assert tiles == [(r, min(16, 37 - r), h, 1) for h in range(4) for r in (0, 16, 32)]
+    # Mixed: rows continue across runs.
+    tiles = capi.attention_tiles([1, 20], 2, 2)
+    assert tiles[:2] == [(0, 1, 0, 1), (0, 1, 1, 1)]
+    assert tiles[2:] == [(1, 16, 0, 1), (17, 4, 0, 1), (1, 16, 1, 1), (17, 4, 1, 1)]
+    with pytest.raises(capi.HipError):
+        capi.attention_tiles([1], 6, 4)           # q heads not a multiple of KV heads
+    with pytest.raises(capi.HipError):
+        capi.attention_tiles([0], 4, 2)           # empty run
+
+
+def _reference(pool, tables, positions, qkv, layer, q_heads, kv_heads, head, page_tokens, layers):
+    """float64 attention of every row from the pool (CPU)."""
+    kv_width = kv_heads * head
+    m = len(positions)
+    out = np.zeros((m, q_heads * head))
+    pages = pool.reshape(-1, layers, 2, page_tokens, kv_width)
+    for r in range(m):
+        n = positions[r] + 1
+        slots = [tables[r][t // page_tokens] for t in range(n)]
+        k = np.stack([pages[slots[t], layer, 0, t % page_tokens] for t in range(n)]).astype(np.float64)
+        v = np.stack([pages[slots[t], layer, 1, t % page_tokens] for t in range(n)]).astype(np.float64)
+        for h in range(q_heads):
+            g = h * kv_heads // q_heads
+            q = qkv[r, h * head:(h + 1) * head].astype(np.float64)
+            s = k[:, g * head:(g + 1) * head] @ q / np.sqrt(head)
+            p = np.exp(s - s.max())
+            out[r, h * head:(h + 1) * head] = (p / p.sum()) @ v[:, g * head:(g + 1) * head]
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("q_heads,kv_heads,head,decode_lengths,prompt", [
+    (28, 4, 128, [1, 17, 64, 65, 300, 700], (50, 100)),   # split tiles, merge pass
+    (28, 4, 128, [3], (0, 60)),                           # one key chunk: no split
+    (4, 2, 64, [1, 2, 63, 129], (0, 37)),
+])
+def test_online_matches_baseline(torch_cuda, hip_ctx, q_heads, kv_heads, head, decode_lengths, prompt):
+    torch = torch_cuda
+    dev = torch.device("cuda:0")
+    page_tokens, layers, layer = 16, 2, 1
+    kv_width = kv_heads * head
+    rng = np.random.default_rng(q_heads * 1000 + head)
+    start, run = prompt
+    lengths = decode_lengths + [start + run]
+    max_tokens = max(lengths)
+    max_pages = (max_tokens + page_tokens - 1) // page_tokens
+    pool_pages = sum((n + page_tokens - 1) // page_tokens for n in lengths) + 3
+    perm = rng.permutation(pool_pages)
+    seq_tables, used = [], 0
+    for n in lengths:
+        need = (n + page_tokens - 1) // page_tokens
+        seq_tables.append(list(perm[used:used + need]) + [-1] * (max_pages - need))
+        used += need
+    # Rows: one per decode sequence (its last token), then the prompt run.
+    positions = [n - 1 for n in decode_lengths] + list(range(start, start + run))
+    tables = seq_tables[:len(decode_lengths)] + [seq_tables[-1]] * run
+    m = len(positions)
+    print(f"attention q={q_heads} kv={kv_heads} head={head} rows={m} max_tokens={max_tokens}", flush=True)
+
+    pool_h = rng.standard_normal(pool_pages * layers * 2 * page_tokens * kv_width).astype(np.float32)
+    qkv_h = rng.standard_normal((m, q_heads * head + 2 * kv_width)).astype(np.float32)
+    pool = torch.from_numpy(pool_h).to(dev)
+    qkv = torch.from_numpy(qkv_h).to(dev)
+    pos_d = torch.tensor(positions, dtype=torch.int32, device=dev)
+    tab_d = torch.tensor(np.array(tables, dtype=np.int32), device=dev)
+    kv = capi.KvLayout(pool.data_ptr(), page_tokens, kv_width, layers, max_pages, pool_pages)
+    runs = [1] * len(decode_lengths) + [run]
+    tiles_h = capi.attention_tiles(runs, q_heads, kv_heads)
+    tiles_d = torch.tensor(np.array(tiles_h, dtype=np.uint32).view(np.int32), device=dev)
+    out_base = torch.empty((m, q_heads * head), device=dev)
+    out_online = torch.full((m, q_heads * head), float("nan"), device=dev)
+    lib = capi.lib()
+    stride = q_heads * head + 2 * kv_width
+    capi.check(lib.air_hip_attention(hip_ctx.handle, ctypes.byref(kv), qkv.data_ptr(), stride, m, pos_d.data_ptr(),
+                                     tab_d.data_ptr(), layer, q_heads, kv_heads, head, max_tokens,
+                                     out_base.data_ptr()))
+    capi.check(lib.air_hip_attention_online(hip_ctx.handle, ctypes.byref(kv), qkv.data_ptr(), stride, m,
+                                            pos_d.data_ptr(), tab_d.data_ptr(), layer, q_heads, kv_heads, head,
+                                            tiles_d.data_ptr(), len(tiles_h), max_tokens, out_online.data_ptr()))
+    torch.cuda.synchronize()
+    base = out_base.cpu().numpy().astype(np.float64)
+    online = out_online.cpu().numpy().astype(np.float64)
+    assert np.isfinite(online).all()
+    ref = _reference(pool_h, tables, positions, qkv_h, layer, q_heads, kv_heads, head, page_tokens, layers)
+    scale = np.abs(ref).max()
+    assert np.abs(base - ref).max() <= 1e-6 * scale
+    err = np.abs(online - ref).max() / scale
+    assert err <= 1e-5, err
+    # Per row relative L2 (each row's own softmax).
+    rel = np.linalg.norm(online - base, axis=1) / np.linalg.norm(base, axis=1)
+    assert rel.max() <= 1e-5, rel.max()
+
+
+@pytest.mark.gpu
+def test_online_rejects_bad_geometry(torch_cuda, hip_ctx):
+    torch = torch_cuda
+    dev = torch.device("cuda:0")
+    pool = torch.zeros(4 * 2 * 2 * 16 * 96, device=dev)
+    kv = capi.KvLayout(pool.data_ptr(), 16, 96, 2, 4, 4)
+    qkv = torch.zeros((2, 3 * 96 + 2 * 96), device=dev)
+    ints = torch.zeros(64, dtype=torch.int32, device=dev)
+    out = torch.zeros((2, 3 * 96), device=dev)
+    lib = capi.lib()
+    status = lib.air_hip_attention_online(hip_ctx.handle, ctypes.byref(kv), qkv.data_ptr(), 5 * 96, 2,
+                                          ints.data_ptr(), ints.data_ptr(), 0, 3, 1, 96, ints.data_ptr(), 1, 16,
+                                          out.data_ptr())
+    assert status == 6  # head width 96 is not compiled: unsupported
+    assert b"64 and 128" in lib.air_hip_last_error()
