@@ -65,6 +65,7 @@ class Stats(ctypes.Structure):
         ("prefill_linear_calls", ctypes.c_uint64),
         ("decode_rows", ctypes.c_uint64),
         ("prefill_rows", ctypes.c_uint64),
+        ("workspace_generation", ctypes.c_uint64),
     ]
 
 
@@ -116,6 +117,7 @@ SIGNATURES = {
     "air_hip_rope": (_I, [_P, _P, _U64, _U32, _P, _U32, _U32, _U32, _U32, _P, _U64]),
     "air_hip_kv_append": (_I, [_P, _P, _P, _U64, _U64, _U32, _P, _P, _U32]),
     "air_hip_attention": (_I, [_P, _P, _P, _U64, _U32, _P, _P, _U32, _U32, _U32, _U32, _U64, _P]),
+    "air_hip_add_rms_norm": (_I, [_P, _P, _P, _P, _P, _U32, _U64, ctypes.c_double]),
     "air_hip_attention_make_tiles": (_I, [_P, _U32, _U32, _U32, _P, _U32, _P]),
     "air_hip_attention_online": (_I, [_P, _P, _P, _U64, _U32, _P, _P, _U32, _U32, _U32, _U32, _P, _U32, _U64, _P]),
     "air_hip_silu_mul": (_I, [_P, _P, _P, _U32, _U64]),

@@ -147,6 +147,9 @@ hipError_t launch_matrix_rows(const TilePlanes& planes, const std::int32_t* rows
                               hipStream_t stream);
 hipError_t launch_rms_norm(const float* x, const float* w, float* out, std::uint32_t m, std::uint64_t n, double eps,
                            hipStream_t stream);
+// x += y (m x n), then out = rms_norm(x) * w; out must not alias x.
+hipError_t launch_add_rms_norm(float* x, const float* y, const float* w, float* out, std::uint32_t m, std::uint64_t n,
+                               double eps, hipStream_t stream);
 hipError_t launch_rope(float* qkv, std::uint64_t stride, std::uint32_t m, const std::int32_t* positions,
                        std::uint32_t q_heads, std::uint32_t kv_heads, std::uint32_t head_dim, std::uint32_t rope_dims,
                        const void* table, std::uint64_t table_positions, hipStream_t stream);

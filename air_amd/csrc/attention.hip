@@ -29,6 +29,7 @@ namespace {
 constexpr unsigned kAttnThreads = 256;
 constexpr unsigned kChunk = 64;      // key tokens per LDS stage
 constexpr unsigned kTileVectors = 16;
+constexpr unsigned kMaxSplits = 64;  // one wave reduces a vector's splits in the merge
 
 __device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
@@ -59,6 +60,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
     __shared__ float ks[kChunk][LD];
     __shared__ float vs[kChunk][LD];
     __shared__ float ps[kTileVectors][kChunk + 1];
+    __shared__ std::int64_t slot_off[kChunk];   // pool offset of each chunk token's K slot, -1 if absent
 
     const AttentionTile tile = tiles[blockIdx.x];
     if (!tile_ok(tile, m, q_heads, kv_heads)) return;
@@ -103,22 +105,44 @@ __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
 #pragma unroll
     for (unsigned i = 0; i < ACC; ++i) acc[i] = 0.0f;
 
+    // V of a token sits page_tokens * kv_width floats after its K in the page.
+    const std::uint64_t v_after_k = static_cast<std::uint64_t>(g.page_tokens) * g.kv_width;
+    constexpr unsigned kIters = kChunk * D4 / kAttnThreads;   // float4 of K (and of V) per thread per chunk
     for (std::uint32_t c = c_begin; c < c_end; ++c) {
         const std::int64_t c0 = static_cast<std::int64_t>(c) * kChunk;
-        __syncthreads();  // previous chunk's K, V and P are consumed
-        for (unsigned idx = tid; idx < kChunk * D4; idx += kAttnThreads) {
-            const unsigned t = idx / D4, d4 = idx % D4;
-            const std::int64_t token = c0 + t;
-            float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
+        __syncthreads();  // previous chunk's K, V, P and slot offsets are consumed
+        // Slot of each token of the chunk, resolved once (page table lookup).
+        if (tid < kChunk) {
+            const std::int64_t token = c0 + tid;
+            std::int64_t off = -1;
             if (token < tmax) {
                 const float* kp = kv_slot(g, table, layer, static_cast<std::uint64_t>(token), false);
-                const float* vp = kv_slot(g, table, layer, static_cast<std::uint64_t>(token), true);
-                const std::uint64_t off = static_cast<std::uint64_t>(kvh) * D + 4u * d4;
-                if (kp) k4 = load4(kp + off);
-                if (vp) v4 = load4(vp + off);
+                if (kp) off = kp - g.pool;
             }
-            *reinterpret_cast<float4*>(&ks[t][4u * d4]) = k4;
-            *reinterpret_cast<float4*>(&vs[t][4u * d4]) = v4;
+            slot_off[tid] = off;
+        }
+        __syncthreads();
+        // All of this thread's K and V loads in flight before the LDS stores.
+        float4 kr[kIters], vr[kIters];
+#pragma unroll
+        for (unsigned it = 0; it < kIters; ++it) {
+            const unsigned idx = tid + it * kAttnThreads;
+            const unsigned t = idx / D4, d4 = idx % D4;
+            const std::int64_t off = slot_off[t];
+            kr[it] = make_float4(0.f, 0.f, 0.f, 0.f);
+            vr[it] = kr[it];
+            if (off >= 0) {
+                const float* kp = g.pool + off + static_cast<std::uint64_t>(kvh) * D + 4u * d4;
+                kr[it] = load4(kp);
+                vr[it] = load4(kp + v_after_k);
+            }
+        }
+#pragma unroll
+        for (unsigned it = 0; it < kIters; ++it) {
+            const unsigned idx = tid + it * kAttnThreads;
+            const unsigned t = idx / D4, d4 = idx % D4;
+            *reinterpret_cast<float4*>(&ks[t][4u * d4]) = kr[it];
+            *reinterpret_cast<float4*>(&vs[t][4u * d4]) = vr[it];
         }
         __syncthreads();
 
@@ -215,25 +239,47 @@ __global__ __launch_bounds__(kAttnThreads) void attention_merge_kernel(const Att
                                                                        std::uint32_t q_heads, std::uint32_t kv_heads,
                                                                        const float* __restrict__ partials,
                                                                        float* __restrict__ out) {
+    __shared__ float weight[kTileVectors][kMaxSplits];   // e^(m_s - M) / L
     const AttentionTile tile = tiles[blockIdx.x];
-    if (!tile_ok(tile, m, q_heads, kv_heads)) return;
+    if (!tile_ok(tile, m, q_heads, kv_heads) || splits > kMaxSplits) return;
     const unsigned nq = tile.rows * tile.heads;
-    for (unsigned idx = threadIdx.x; idx < nq * D; idx += kAttnThreads) {
-        const unsigned v = idx / D, d = idx % D;
-        const float* base = partials + (static_cast<std::uint64_t>(blockIdx.x) * splits * kTileVectors + v) * (D + 4u);
-        const std::uint64_t step = static_cast<std::uint64_t>(kTileVectors) * (D + 4u);
-        float mx = -__builtin_huge_valf();
-        for (std::uint32_t s = 0; s < splits; ++s) mx = base[s * step] > mx ? base[s * step] : mx;
-        float num = 0.0f, den = 0.0f;
+    const std::uint64_t step = static_cast<std::uint64_t>(kTileVectors) * (D + 4u);   // floats between splits
+    const float* tile_base = partials + static_cast<std::uint64_t>(blockIdx.x) * splits * step;
+    // One thread per (vector, split) reads its (m, l); a wave reduces each vector.
+    for (unsigned idx = threadIdx.x; idx < nq * kMaxSplits; idx += kAttnThreads) {
+        const unsigned v = idx / kMaxSplits, s = idx % kMaxSplits;
+        float ms = -__builtin_huge_valf(), ls = 0.0f;
+        if (s < splits) {
+            ms = tile_base[s * step + static_cast<std::uint64_t>(v) * (D + 4u)];
+            ls = tile_base[s * step + static_cast<std::uint64_t>(v) * (D + 4u) + 1u];
+        }
+        float mx = ms;
+        for (int off = 32; off > 0; off >>= 1) {
+            const float o = __shfl_xor(mx, off);
+            mx = o > mx ? o : mx;
+        }
+        const float w = ms == -__builtin_huge_valf() ? 0.0f : __expf(ms - mx);
+        float den = ls * w;
+        for (int off = 32; off > 0; off >>= 1) den += __shfl_xor(den, off);
+        weight[v][s] = w / den;
+    }
+    __syncthreads();
+    constexpr unsigned D4 = D / 4;
+    for (unsigned idx = threadIdx.x; idx < nq * D4; idx += kAttnThreads) {
+        const unsigned v = idx / D4, d4 = idx % D4;
+        const float* base = tile_base + static_cast<std::uint64_t>(v) * (D + 4u) + 4u + 4u * d4;
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
         for (std::uint32_t s = 0; s < splits; ++s) {
-            const float ms = base[s * step];
-            if (ms == -__builtin_huge_valf()) continue;
-            const float w = __expf(ms - mx);
-            den += base[s * step + 1] * w;
-            num += base[s * step + 4 + d] * w;
+            const float w = weight[v][s];
+            const float4 a = load4(base + s * step);
+            o.x += a.x * w;
+            o.y += a.y * w;
+            o.z += a.z * w;
+            o.w += a.w * w;
         }
         const unsigned row = tile.row + v / tile.heads, head = tile.head + v % tile.heads;
-        out[static_cast<std::uint64_t>(row) * q_heads * D + static_cast<std::uint64_t>(head) * D + d] = num / den;
+        *reinterpret_cast<float4*>(out + static_cast<std::uint64_t>(row) * q_heads * D +
+                                   static_cast<std::uint64_t>(head) * D + 4u * d4) = o;
     }
 }
 

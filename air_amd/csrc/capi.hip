@@ -58,6 +58,9 @@ struct air_hip_context {
     std::uint32_t* bound_scratch{nullptr};  // one uint32 for the weight exponent at residency
     void* attention_scratch{nullptr};       // attention scores, grown on demand
     std::uint64_t attention_scratch_bytes{0};
+    // Bumped whenever a context-owned buffer is (re)allocated: launches
+    // recorded into a graph stay valid while it is unchanged.
+    std::uint64_t generation{0};
 };
 
 struct air_hip_matrix {
@@ -129,6 +132,7 @@ int ensure_workspace(air_hip_context* ctx, std::uint64_t bytes) {
     if (err != hipSuccess) return hip_fail(err, "hipMalloc(workspace)");
     ctx->workspace = p;
     ctx->workspace_bytes = bytes;
+    ++ctx->generation;
     return AIR_HIP_OK;
 }
 
@@ -146,6 +150,7 @@ int ensure_prefill_workspace(air_hip_context* ctx, std::uint64_t bytes) {
     if (err != hipSuccess) return hip_fail(err, "hipMalloc(prefill workspace)");
     ctx->prefill_workspace = p;
     ctx->prefill_workspace_bytes = bytes;
+    ++ctx->generation;
     return AIR_HIP_OK;
 }
 
@@ -174,6 +179,7 @@ int ensure_split_buffers(air_hip_context* ctx, std::uint64_t partial_bytes, std:
         const hipError_t err = hipMalloc(&ctx->split_partials, partial_bytes);
         if (err != hipSuccess) return hip_fail(err, "hipMalloc(split partials)");
         ctx->split_partials_bytes = partial_bytes;
+        ++ctx->generation;
     }
     if (counters > ctx->split_counter_count) {
         (void)hipFree(ctx->split_counters);
@@ -189,6 +195,7 @@ int ensure_split_buffers(air_hip_context* ctx, std::uint64_t partial_bytes, std:
         }
         ctx->split_counters = static_cast<std::uint32_t*>(p);
         ctx->split_counter_count = count;
+        ++ctx->generation;
     }
     return AIR_HIP_OK;
 }
@@ -341,6 +348,7 @@ int air_hip_context_stats(const air_hip_context* ctx, air_hip_stats* out) {
     out->prefill_linear_calls = ctx->prefill_linear_calls.load(std::memory_order_relaxed);
     out->decode_rows = ctx->decode_rows.load(std::memory_order_relaxed);
     out->prefill_rows = ctx->prefill_rows.load(std::memory_order_relaxed);
+    out->workspace_generation = ctx->generation;
     return AIR_HIP_OK;
 }
 
@@ -644,6 +652,18 @@ int air_hip_rms_norm(air_hip_context* ctx, const float* x, const float* weight, 
     return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "rms_norm_kernel");
 }
 
+int air_hip_add_rms_norm(air_hip_context* ctx, float* x, const float* y, const float* weight, float* out, uint32_t m,
+                         uint64_t n, double eps) {
+    if (!ctx || !x || !y || !weight || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    if (n == 0 || !(eps >= 0.0)) return fail(AIR_HIP_INVALID_ARGUMENT, "width must be non-zero and eps non-negative");
+    if (out == x || out == y) return fail(AIR_HIP_INVALID_ARGUMENT, "out must not alias x or y");
+    if (m == 0) return AIR_HIP_OK;
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const hipError_t err = launch_add_rms_norm(x, y, weight, out, m, n, eps, ctx->stream);
+    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "rms_norm_vec_kernel");
+}
+
 int air_hip_rope(air_hip_context* ctx, float* qkv, uint64_t row_stride, uint32_t m, const int32_t* positions,
                  uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim, uint32_t rope_dims, const float* table,
                  uint64_t table_positions) {
@@ -698,6 +718,7 @@ int ensure_attention_scratch(air_hip_context* ctx, uint64_t bytes) {
     const hipError_t err = hipMalloc(&ctx->attention_scratch, grown);
     if (err != hipSuccess) return hip_fail(err, "hipMalloc(attention scratch)");
     ctx->attention_scratch_bytes = grown;
+    ++ctx->generation;
     return AIR_HIP_OK;
 }
 static_assert(sizeof(AttentionTile) == sizeof(air_hip_attention_tile), "tile layouts agree");

@@ -248,41 +248,136 @@ __global__ __launch_bounds__(kThreads) void add_kernel(float* __restrict__ x, co
     }
 }
 
-// First maximum of each row (std::max_element with operator<).
-__global__ __launch_bounds__(kThreads) void argmax_kernel(const float* __restrict__ logits, std::uint64_t n,
-                                                          std::int32_t* __restrict__ out) {
-    __shared__ float best_v[kThreads];
-    __shared__ std::uint32_t best_i[kThreads];
-    const float* row = logits + static_cast<std::uint64_t>(blockIdx.x) * n;
-    // Each thread scans a contiguous chunk, keeping its first maximum.
-    const std::uint64_t chunk = (n + kThreads - 1u) / kThreads;
-    const std::uint64_t begin = threadIdx.x * chunk;
-    const std::uint64_t end = begin + chunk < n ? begin + chunk : n;
-    std::uint32_t bi = static_cast<std::uint32_t>(begin < n ? begin : 0u);
-    float bv = begin < n ? row[begin] : 0.0f;
-    bool valid = begin < n;
-    for (std::uint64_t i = begin + 1u; i < end; ++i) {
-        if (bv < row[i]) {
-            bv = row[i];
-            bi = static_cast<std::uint32_t>(i);
-        }
+// First maximum of each row (std::max_element with operator<): the largest
+// value, the lowest index among equal values.  A NaN never wins (the
+// reference CUDA executor refuses non-finite logits); a row of NaNs gives 0.
+constexpr unsigned kArgmaxThreads = 1024;
+
+__device__ __forceinline__ void argmax_take(float v, std::uint32_t i, float& bv, std::uint32_t& bi) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
     }
-    best_v[threadIdx.x] = bv;
-    best_i[threadIdx.x] = valid ? bi : 0xffffffffu;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        // Chunks in index order: a later chunk wins only if strictly greater.
-        float v = best_v[0];
-        std::uint32_t idx = best_i[0];
-        for (unsigned t = 1; t < kThreads; ++t) {
-            if (best_i[t] == 0xffffffffu) break;
-            if (v < best_v[t]) {
-                v = best_v[t];
-                idx = best_i[t];
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ logits, std::uint64_t n,
+                                                                std::int32_t* __restrict__ out) {
+    __shared__ float wave_v[kArgmaxThreads / 64];
+    __shared__ std::uint32_t wave_i[kArgmaxThreads / 64];
+    const float* row = logits + static_cast<std::uint64_t>(blockIdx.x) * n;
+    float bv = -__builtin_huge_valf();
+    std::uint32_t bi = 0xffffffffu;
+    const bool vec = (n % 4u == 0) && (reinterpret_cast<std::uintptr_t>(row) % 16u == 0);
+    if (vec) {
+        // Coalesced float4 loads, four in flight per thread (the selection
+        // rule does not depend on the visiting order).
+        const std::uint64_t n4 = n / 4u;
+        for (std::uint64_t first = threadIdx.x; first < n4; first += 4u * kArgmaxThreads) {
+            float4 v[4];
+#pragma unroll
+            for (unsigned j = 0; j < 4; ++j) {
+                const std::uint64_t i = first + j * kArgmaxThreads;
+                v[j] = i < n4 ? *reinterpret_cast<const float4*>(row + 4u * i)
+                              : make_float4(-__builtin_huge_valf(), -__builtin_huge_valf(), -__builtin_huge_valf(),
+                                            -__builtin_huge_valf());
+            }
+#pragma unroll
+            for (unsigned j = 0; j < 4; ++j) {
+                const std::uint64_t i = first + j * kArgmaxThreads;
+                if (i >= n4) continue;
+                const std::uint32_t base = static_cast<std::uint32_t>(4u * i);
+                argmax_take(v[j].x, base, bv, bi);
+                argmax_take(v[j].y, base + 1u, bv, bi);
+                argmax_take(v[j].z, base + 2u, bv, bi);
+                argmax_take(v[j].w, base + 3u, bv, bi);
             }
         }
-        out[blockIdx.x] = static_cast<std::int32_t>(idx);
+    } else {
+#pragma unroll 8
+        for (std::uint64_t i = threadIdx.x; i < n; i += kArgmaxThreads) {
+            argmax_take(row[i], static_cast<std::uint32_t>(i), bv, bi);
+        }
     }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const std::uint32_t oi = __shfl_xor(bi, off);
+        argmax_take(ov, oi, bv, bi);
+    }
+    if ((threadIdx.x & 63u) == 0) {
+        wave_v[threadIdx.x >> 6] = bv;
+        wave_i[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        bv = wave_v[0];
+        bi = wave_i[0];
+        for (unsigned w = 1; w < kArgmaxThreads / 64; ++w) argmax_take(wave_v[w], wave_i[w], bv, bi);
+        out[blockIdx.x] = static_cast<std::int32_t>(bi == 0xffffffffu ? 0u : bi);
+    }
+}
+
+// RMSNorm of rows of n <= kNormMaxVec * 4 * kThreads floats held in
+// registers (one coalesced read of the row), with the residual add of the
+// reference's add_in_place fused in front when `y` is given: x += y, then
+// out = x * float(1 / sqrt(mean(x^2) + eps)) * w.  Without y, x and out may
+// alias; with y they must not (x receives the sum).
+constexpr unsigned kNormMaxVec = 8;
+
+__global__ __launch_bounds__(kThreads) void rms_norm_vec_kernel(float* x, const float* __restrict__ y,
+                                                                const float* __restrict__ w, float* out,
+                                                                std::uint64_t n, double eps) {
+#pragma clang fp contract(off)
+    __shared__ double red[kThreads / 64];
+    const std::uint64_t n4 = n / 4u;
+    float* row = x + static_cast<std::uint64_t>(blockIdx.x) * n;
+    float* dst = out + static_cast<std::uint64_t>(blockIdx.x) * n;
+    const float* yrow = y ? y + static_cast<std::uint64_t>(blockIdx.x) * n : nullptr;
+    float4 v[kNormMaxVec];
+#pragma unroll
+    for (unsigned j = 0; j < kNormMaxVec; ++j) {
+        const std::uint64_t i = threadIdx.x + static_cast<std::uint64_t>(j) * kThreads;
+        v[j] = i < n4 ? *reinterpret_cast<const float4*>(row + 4u * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (yrow) {
+#pragma unroll
+        for (unsigned j = 0; j < kNormMaxVec; ++j) {
+            const std::uint64_t i = threadIdx.x + static_cast<std::uint64_t>(j) * kThreads;
+            if (i < n4) {
+                const float4 b = *reinterpret_cast<const float4*>(yrow + 4u * i);
+                v[j] = make_float4(v[j].x + b.x, v[j].y + b.y, v[j].z + b.z, v[j].w + b.w);
+                *reinterpret_cast<float4*>(row + 4u * i) = v[j];
+            }
+        }
+    }
+    double sum = 0.0;
+#pragma unroll
+    for (unsigned j = 0; j < kNormMaxVec; ++j) {
+        sum += static_cast<double>(v[j].x) * v[j].x;
+        sum += static_cast<double>(v[j].y) * v[j].y;
+        sum += static_cast<double>(v[j].z) * v[j].z;
+        sum += static_cast<double>(v[j].w) * v[j].w;
+    }
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = sum;
+    __syncthreads();
+    const double total = (red[0] + red[1]) + (red[2] + red[3]);
+    const float scale = static_cast<float>(1.0 / sqrt(total / static_cast<double>(n) + eps));
+#pragma unroll
+    for (unsigned j = 0; j < kNormMaxVec; ++j) {
+        const std::uint64_t i = threadIdx.x + static_cast<std::uint64_t>(j) * kThreads;
+        if (i < n4) {
+            const float4 g = *reinterpret_cast<const float4*>(w + 4u * i);
+            const float4 o = make_float4(v[j].x * scale * g.x, v[j].y * scale * g.y, v[j].z * scale * g.z,
+                                         v[j].w * scale * g.w);
+            *reinterpret_cast<float4*>(dst + 4u * i) = o;
+        }
+    }
+}
+
+bool norm_vectorizable(const float* x, const float* y, const float* w, const float* out, std::uint64_t n) {
+    const auto aligned = [](const void* p) { return reinterpret_cast<std::uintptr_t>(p) % 16u == 0; };
+    return n % 4u == 0 && n <= static_cast<std::uint64_t>(kNormMaxVec) * 4u * kThreads && aligned(x) &&
+           (!y || aligned(y)) && aligned(w) && aligned(out);
 }
 
 unsigned grid_for(std::uint64_t work) {
@@ -302,6 +397,23 @@ hipError_t launch_matrix_rows(const TilePlanes& p, const std::int32_t* rows, std
 
 hipError_t launch_rms_norm(const float* x, const float* w, float* out, std::uint32_t m, std::uint64_t n, double eps,
                            hipStream_t stream) {
+    if (norm_vectorizable(x, nullptr, w, out, n)) {
+        hipLaunchKernelGGL(rms_norm_vec_kernel, dim3(m), dim3(kThreads), 0, stream, const_cast<float*>(x),
+                           static_cast<const float*>(nullptr), w, out, n, eps);
+    } else {
+        hipLaunchKernelGGL(rms_norm_kernel, dim3(m), dim3(kThreads), 0, stream, x, w, out, n, eps);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_add_rms_norm(float* x, const float* y, const float* w, float* out, std::uint32_t m, std::uint64_t n,
+                               double eps, hipStream_t stream) {
+    if (norm_vectorizable(x, y, w, out, n)) {
+        hipLaunchKernelGGL(rms_norm_vec_kernel, dim3(m), dim3(kThreads), 0, stream, x, y, w, out, n, eps);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(add_kernel, dim3(grid_for(static_cast<std::uint64_t>(m) * n)), dim3(kThreads), 0, stream, x, y,
+                       static_cast<std::uint64_t>(m) * n);
     hipLaunchKernelGGL(rms_norm_kernel, dim3(m), dim3(kThreads), 0, stream, x, w, out, n, eps);
     return hipGetLastError();
 }
@@ -348,7 +460,7 @@ hipError_t launch_add(float* x, const float* y, std::uint64_t count, hipStream_t
 }
 
 hipError_t launch_argmax(const float* logits, std::uint32_t m, std::uint64_t n, std::int32_t* out, hipStream_t stream) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(m), dim3(kThreads), 0, stream, logits, n, out);
+    hipLaunchKernelGGL(argmax_kernel, dim3(m), dim3(kArgmaxThreads), 0, stream, logits, n, out);
     return hipGetLastError();
 }
 

@@ -48,7 +48,7 @@ struct HipLinearInfo {
 
 struct HipPrepareOptions {
     int device{0};
-    void* stream{nullptr};              // hipStream_t the engine launches on
+    void* stream{nullptr};              // hipStream_t the engine launches on (null: a stream of its own)
     std::uint32_t max_decode_rows{64};  // workspace reserved for decode widths
     bool fuse{true};                    // concatenate q|k|v and gate|up when formats agree
     // KV pages allocated with the first sequence; 0 sizes the pool for
@@ -56,6 +56,9 @@ struct HipPrepareOptions {
     // of free device memory.
     std::uint32_t kv_pool_pages{0};
     std::uint32_t max_step_rows{512};   // rows per device step (prefill chunk)
+    // Decode steps (one row per sequence, greedy outputs) replay one captured
+    // HIP graph per batch width instead of launching ~13 kernels per layer.
+    bool decode_graphs{true};
 };
 
 class HipStepEngine;
@@ -128,6 +131,7 @@ private:
     std::shared_ptr<const ModelDefinition> model_;
     int device_{0};
     air_hip_context* ctx_{nullptr};
+    void* owned_stream_{nullptr};  // hipStream_t created when the options name none
     BackendCapabilities capabilities_{};
     std::vector<Layer> layers_;
     Linear output_{};

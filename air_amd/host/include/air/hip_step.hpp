@@ -21,6 +21,7 @@
 #include "air/hip_backend.hpp"
 
 #include <cstdint>
+#include <map>
 #include <memory>
 #include <mutex>
 #include <vector>
@@ -108,7 +109,25 @@ private:
     [[nodiscard]] Status project(std::uint32_t layer, LinearRole fused, LinearRole first, LinearRole second,
                                  LinearRole third, const float* x, float* y, std::uint32_t m,
                                  QuantizedLinearExecutionKind tactic);
+    // Device work of a decode-shaped step over rows 0..m-1: the layers, the
+    // lm_head over every row and the argmax into argmax_dev_.
+    [[nodiscard]] Status decode_device(std::uint32_t m, std::uint64_t max_tokens, std::uint32_t table_pages,
+                                       QuantizedLinearExecutionKind block, QuantizedLinearExecutionKind output,
+                                       std::uint32_t tiles);
+    // decode_device through a graph captured per (width, tactics): replayed
+    // when one exists for the context's current buffers, else run eagerly and
+    // captured for the next step.
+    [[nodiscard]] Status decode_graph(std::uint32_t m, std::uint64_t max_tokens, std::uint32_t table_pages,
+                                      QuantizedLinearExecutionKind block, QuantizedLinearExecutionKind output,
+                                      std::uint32_t tiles);
+    [[nodiscard]] std::uint64_t context_generation() const noexcept;
     [[nodiscard]] void* stream() const noexcept { return prepared_.options().stream; }
+
+    struct DecodeGraph {
+        void* exec{nullptr};          // hipGraphExec_t; null when capture failed (eager from then on)
+        std::uint64_t generation{0};  // context buffers the launches point into
+    };
+    std::map<std::uint64_t, DecodeGraph> graphs_;
 
     const HipPreparedModel& prepared_;
     std::uint32_t page_tokens_{0}, pool_pages_{0}, max_rows_{0}, max_pages_{0}, output_rows_{0};

@@ -96,6 +96,10 @@ HipPreparedModel::~HipPreparedModel() {
     }
     release(output_);
     if (ctx_) air_hip_context_destroy(ctx_);
+    if (owned_stream_) {
+        (void)hipSetDevice(device_);
+        (void)hipStreamDestroy(static_cast<hipStream_t>(owned_stream_));
+    }
 }
 
 void HipPreparedModel::release(Linear& linear) noexcept {
@@ -186,7 +190,19 @@ Result<std::unique_ptr<HipPreparedModel>> HipPreparedModel::create(std::shared_p
 
     std::unique_ptr<HipPreparedModel> prepared(new HipPreparedModel(model, options.device));
     prepared->options_ = options;
-    if (const int rc = air_hip_context_create(options.device, options.stream, &prepared->ctx_); rc != AIR_HIP_OK) {
+    if (!options.stream) {
+        // A stream of the model's own (default priority): the legacy stream
+        // cannot be captured into graphs.
+        if (Status s = runtime_status(hipSetDevice(options.device), "hipSetDevice"); !s) return s;
+        hipStream_t stream = nullptr;
+        if (Status s = runtime_status(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate"); !s) {
+            return s;
+        }
+        prepared->owned_stream_ = stream;
+        prepared->options_.stream = stream;
+    }
+    if (const int rc = air_hip_context_create(options.device, prepared->options_.stream, &prepared->ctx_);
+        rc != AIR_HIP_OK) {
         return hip_status(rc);
     }
     const auto& c = model->config();

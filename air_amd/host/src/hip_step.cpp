@@ -155,6 +155,9 @@ Status HipStepEngine::allocate(void** ptr, std::uint64_t bytes, const char* what
 HipStepEngine::~HipStepEngine() {
     (void)hipSetDevice(prepared_.device());
     (void)hipStreamSynchronize(static_cast<hipStream_t>(stream()));
+    for (auto& [key, graph] : graphs_) {
+        if (graph.exec) (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph.exec));
+    }
     for (void* p : allocations_) (void)hipFree(p);
     if (staging_) (void)hipHostFree(staging_);
     if (owns_embedding_ && embedding_) air_hip_matrix_release(embedding_);
@@ -382,13 +385,15 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
     const auto& c = prepared_.model().config();
     air_hip_context* ctx = prepared_.context();
     const air_hip_kv_layout kv{pool_, page_tokens_, kv_width_, c.layer_count, table_pages, pool_pages_};
-    const std::uint64_t hidden_floats = static_cast<std::uint64_t>(m) * embed_;
     int rc = air_hip_matrix_rows(ctx, embedding_, tokens_dev_, m, hidden_);
     if (rc != AIR_HIP_OK) return hip_status(rc);
+    // Each residual add runs fused with the RMSNorm after it (the next
+    // layer's attention norm, or the final norm): normed_ always holds the
+    // input of the next projection.
+    if ((rc = air_hip_rms_norm(ctx, hidden_, attn_norm_[0], normed_, m, embed_, c.rms_norm_epsilon)) != AIR_HIP_OK) {
+        return hip_status(rc);
+    }
     for (std::uint32_t l = 0; l < c.layer_count; ++l) {
-        if ((rc = air_hip_rms_norm(ctx, hidden_, attn_norm_[l], normed_, m, embed_, c.rms_norm_epsilon)) != AIR_HIP_OK) {
-            return hip_status(rc);
-        }
         if (Status s = project(l, LinearRole::attn_qkv, LinearRole::attn_q, LinearRole::attn_k, LinearRole::attn_v,
                                normed_, qkv_, m, tactic);
             !s) {
@@ -410,8 +415,8 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
                                        c.attention_head_count, c.kv_head_count, head_dim_, max_tokens, att_);
         if (rc != AIR_HIP_OK) return hip_status(rc);
         if (Status s = prepared_.linear(l, LinearRole::attn_output, att_, proj_, m, tactic); !s) return s;
-        if ((rc = air_hip_add(ctx, hidden_, proj_, hidden_floats)) != AIR_HIP_OK) return hip_status(rc);
-        if ((rc = air_hip_rms_norm(ctx, hidden_, ffn_norm_[l], normed_, m, embed_, c.rms_norm_epsilon)) != AIR_HIP_OK) {
+        if ((rc = air_hip_add_rms_norm(ctx, hidden_, proj_, ffn_norm_[l], normed_, m, embed_, c.rms_norm_epsilon)) !=
+            AIR_HIP_OK) {
             return hip_status(rc);
         }
         if (Status s = project(l, LinearRole::ffn_gate_up, LinearRole::ffn_gate, LinearRole::ffn_up,
@@ -421,8 +426,65 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
         }
         if ((rc = air_hip_silu_mul(ctx, gate_up_, act_, m, ffn_)) != AIR_HIP_OK) return hip_status(rc);
         if (Status s = prepared_.linear(l, LinearRole::ffn_down, act_, proj_, m, tactic); !s) return s;
-        if ((rc = air_hip_add(ctx, hidden_, proj_, hidden_floats)) != AIR_HIP_OK) return hip_status(rc);
+        const float* next_norm = l + 1U < c.layer_count ? attn_norm_[l + 1U] : output_norm_;
+        if ((rc = air_hip_add_rms_norm(ctx, hidden_, proj_, next_norm, normed_, m, embed_, c.rms_norm_epsilon)) !=
+            AIR_HIP_OK) {
+            return hip_status(rc);
+        }
     }
+    return Status::ok();
+}
+
+std::uint64_t HipStepEngine::context_generation() const noexcept {
+    air_hip_stats stats{};
+    return air_hip_context_stats(prepared_.context(), &stats) == AIR_HIP_OK ? stats.workspace_generation : ~0ULL;
+}
+
+Status HipStepEngine::decode_device(std::uint32_t m, std::uint64_t max_tokens, std::uint32_t table_pages,
+                                    QuantizedLinearExecutionKind block, QuantizedLinearExecutionKind output,
+                                    std::uint32_t tiles) {
+    if (Status s = layers(m, max_tokens, table_pages, block, tiles); !s) return s;
+    if (Status s = prepared_.linear(0, LinearRole::output, normed_, logits_, m, output); !s) return s;
+    return hip_status(air_hip_argmax(prepared_.context(), logits_, m, vocab_, argmax_dev_));
+}
+
+Status HipStepEngine::decode_graph(std::uint32_t m, std::uint64_t max_tokens, std::uint32_t table_pages,
+                                   QuantizedLinearExecutionKind block, QuantizedLinearExecutionKind output,
+                                   std::uint32_t tiles) {
+    auto* hs = static_cast<hipStream_t>(stream());
+    const std::uint64_t key = (static_cast<std::uint64_t>(m) << 32) | (static_cast<std::uint64_t>(block) << 16) |
+                              (static_cast<std::uint64_t>(output) << 8) | (tiles ? 1U : 0U);
+    auto it = graphs_.find(key);
+    if (it != graphs_.end()) {
+        if (!it->second.exec) return decode_device(m, max_tokens, table_pages, block, output, tiles);
+        if (it->second.generation == context_generation()) {
+            return runtime_status(hipGraphLaunch(static_cast<hipGraphExec_t>(it->second.exec), hs), "hipGraphLaunch");
+        }
+        (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(it->second.exec));
+        graphs_.erase(it);
+    }
+    // This step runs eagerly (growing any buffer it needs); its launches are
+    // then recorded, unexecuted, for the next steps of this width.
+    if (Status s = decode_device(m, max_tokens, table_pages, block, output, tiles); !s) return s;
+    const std::uint64_t generation = context_generation();
+    DecodeGraph entry;
+    if (hipStreamBeginCapture(hs, hipStreamCaptureModeThreadLocal) == hipSuccess) {
+        const Status recorded = decode_device(m, max_tokens, table_pages, block, output, tiles);
+        hipGraph_t graph = nullptr;
+        const hipError_t ended = hipStreamEndCapture(hs, &graph);
+        hipGraphExec_t exec = nullptr;
+        if (recorded && ended == hipSuccess && graph &&
+            hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess &&
+            context_generation() == generation) {
+            entry.exec = exec;
+            entry.generation = generation;
+        } else if (exec) {
+            (void)hipGraphExecDestroy(exec);
+        }
+        if (graph) (void)hipGraphDestroy(graph);
+    }
+    (void)hipGetLastError();  // a refused capture leaves no error behind for the next launch check
+    graphs_[key] = entry;
     return Status::ok();
 }
 
@@ -496,9 +558,17 @@ Result<StepResult> HipStepEngine::run(std::span<const StepRow> rows, QuantizedLi
         }
     }
 
+    // Decode-shaped steps (one row per sequence, every row a greedy output)
+    // go through a graph captured per width: their page tables span the whole
+    // context and the attention is sized for it, so one graph serves every
+    // step of that width.
+    bool decode_shape = prepared_.options().decode_graphs && claims.size() == m && m <= output_rows_;
+    for (std::uint32_t r = 0; r < m && decode_shape; ++r) decode_shape = rows[r].output == RowOutput::greedy;
+    if (decode_shape) table_pages = max_pages_;
+
     // Upload: tokens | positions | page tables [m][table_pages], one copy.
     std::int32_t* host = staging_;
-    std::uint64_t max_tokens = 1U;
+    std::uint64_t max_tokens = decode_shape ? c.context_length : 1U;
     for (std::uint32_t r = 0; r < m; ++r) {
         host[r] = rows[r].token;
         host[m + r] = static_cast<std::int32_t>(positions[r]);
@@ -548,10 +618,11 @@ Result<StepResult> HipStepEngine::run(std::span<const StepRow> rows, QuantizedLi
     positions_dev_ = positions_dev;
     tables_dev_ = tables_dev;
 
-    Status status = layers(m, max_tokens, table_pages, block_tactic, tiles);
+    Status status = decode_shape ? decode_graph(m, max_tokens, table_pages, block_tactic, output_tactic, tiles)
+                                 : layers(m, max_tokens, table_pages, block_tactic, tiles);
 
-    // Output rows: final RMSNorm, lm_head (+bias), argmax, in chunks of the
-    // logits buffer.
+    // Output rows: lm_head (+bias) over their final-normed rows, argmax, in
+    // chunks of the logits buffer.
     StepResult result;
     std::vector<std::uint32_t> outputs;
     for (std::uint32_t r = 0; r < m; ++r) {
@@ -561,27 +632,29 @@ Result<StepResult> HipStepEngine::run(std::span<const StepRow> rows, QuantizedLi
     std::int32_t* argmax_host = staging_ + upload_ints;
     for (std::size_t begin = 0; status && begin < outputs.size(); begin += output_rows_) {
         const auto k = static_cast<std::uint32_t>(std::min<std::size_t>(output_rows_, outputs.size() - begin));
-        // Gather the hidden rows (runs of consecutive rows in one copy).
-        for (std::uint32_t j = 0; j < k && status;) {
-            std::uint32_t run = 1;
-            while (j + run < k && outputs[begin + j + run] == outputs[begin + j] + run) ++run;
-            status = runtime_status(
-                hipMemcpyAsync(final_ + static_cast<std::uint64_t>(j) * embed_,
-                               hidden_ + static_cast<std::uint64_t>(outputs[begin + j]) * embed_,
-                               static_cast<std::uint64_t>(run) * embed_ * sizeof(float), hipMemcpyDeviceToDevice, hs),
-                "hipMemcpyAsync(gather)");
-            j += run;
+        // The chunk's rows as one block: in place when they are consecutive,
+        // else gathered into final_ (runs of consecutive rows in one copy).
+        const float* x = normed_ + static_cast<std::uint64_t>(outputs[begin]) * embed_;
+        if (outputs[begin + k - 1] - outputs[begin] != k - 1 || reinterpret_cast<std::uintptr_t>(x) % 16U != 0) {
+            for (std::uint32_t j = 0; j < k && status;) {
+                std::uint32_t run = 1;
+                while (j + run < k && outputs[begin + j + run] == outputs[begin + j] + run) ++run;
+                status = runtime_status(hipMemcpyAsync(final_ + static_cast<std::uint64_t>(j) * embed_,
+                                                       normed_ + static_cast<std::uint64_t>(outputs[begin + j]) * embed_,
+                                                       static_cast<std::uint64_t>(run) * embed_ * sizeof(float),
+                                                       hipMemcpyDeviceToDevice, hs),
+                                        "hipMemcpyAsync(gather)");
+                j += run;
+            }
+            x = final_;
         }
         if (!status) break;
-        int rc = air_hip_rms_norm(ctx, final_, output_norm_, final_, k, embed_, c.rms_norm_epsilon);
-        if (rc != AIR_HIP_OK) {
-            status = hip_status(rc);
-            break;
-        }
-        if (!(status = prepared_.linear(0, LinearRole::output, final_, logits_, k, output_tactic))) break;
-        if ((rc = air_hip_argmax(ctx, logits_, k, vocab_, argmax_dev_)) != AIR_HIP_OK) {
-            status = hip_status(rc);
-            break;
+        if (!decode_shape) {  // a decode-shaped step has its logits and argmax already
+            if (!(status = prepared_.linear(0, LinearRole::output, x, logits_, k, output_tactic))) break;
+            if (const int rc = air_hip_argmax(ctx, logits_, k, vocab_, argmax_dev_); rc != AIR_HIP_OK) {
+                status = hip_status(rc);
+                break;
+            }
         }
         if (!(status = runtime_status(hipMemcpyAsync(argmax_host, argmax_dev_, k * sizeof(std::int32_t),
                                                      hipMemcpyDeviceToHost, hs),

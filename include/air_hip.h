@@ -98,6 +98,10 @@ typedef struct air_hip_stats {
     uint64_t prefill_linear_calls;
     uint64_t decode_rows;
     uint64_t prefill_rows;
+    /* Bumped whenever the context (re)allocates a workspace or scratch
+     * buffer: launches captured into a HIP graph stay valid while it is
+     * unchanged.  No counterpart in the reference. */
+    uint64_t workspace_generation;
 } air_hip_stats;
 
 /* ---- library ---------------------------------------------------------- */
@@ -232,6 +236,13 @@ int air_hip_matrix_rows(air_hip_context* ctx, const air_hip_matrix* matrix, cons
  * (rms_norm, reference_executor.cpp:17-27).  out may alias x. */
 int air_hip_rms_norm(air_hip_context* ctx, const float* x, const float* weight, float* out, uint32_t m,
                      uint64_t n, double eps);
+
+/* The residual add and the RMSNorm that follows it in one pass over each row
+ * (add_in_place then rms_norm, reference_executor.cpp:29-31, 17-27):
+ * x[r] += y[r], then out[r] = rms_norm(x[r]) * weight.  out must not alias
+ * x or y. */
+int air_hip_add_rms_norm(air_hip_context* ctx, float* x, const float* y, const float* weight, float* out, uint32_t m,
+                         uint64_t n, double eps);
 
 /* In-place rotary embedding of the q and k heads of fused q|k|v rows
  * (apply_rope, reference_executor.cpp:37-72): row r (stride floats apart)
