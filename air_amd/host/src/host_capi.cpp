@@ -108,6 +108,7 @@ int air_host_engine_create(const air_host_model* model, const air_host_engine_co
         options.device = config->device;
         if (config->kv_pool_pages) options.kv_pool_pages = config->kv_pool_pages;
         if (config->max_step_rows) options.max_step_rows = config->max_step_rows;
+        options.decode_graphs = config->eager_decode == 0;
         auto prepared = air::HipPreparedModel::create(model->model, options);
         if (!prepared) return fail(prepared.status());
         std::shared_ptr<air::HipPreparedModel> shared(std::move(prepared).value());

@@ -239,7 +239,7 @@ def measure_prefill(torch, ctx, capi, layers, m, steps, dev, stream):
             "mfma_frac": round(tflops / F16_MFMA_PEAK_TFLOPS, 4), "dtype": "f16 operands, f32 accumulate"}
 
 
-def measure_e2e(sequences: int, prompt_tokens: int, new_tokens: int, layers: int) -> dict:
+def measure_e2e(sequences: int, prompt_tokens: int, new_tokens: int, layers: int, eager: bool = False) -> dict:
     """a random-init Qwen2-7B-shaped Q8_0 model through TokenService
     (admission, MicrobatchScheduler cycles, prefill_batch at up to 512 rows on
     the f16 MFMA tactic, decode_greedy_batch at one row per sequence), fp32
@@ -260,7 +260,7 @@ def measure_e2e(sequences: int, prompt_tokens: int, new_tokens: int, layers: int
     engine = host_api.Engine(model, page_tokens=16, kv_pool_pages=pages, max_step_rows=512,
                              prefill_tactic=capi.LINEAR_PREFILL, prefill_quantum_tokens=512,
                              token_budget_per_cycle=512, max_active_requests=64,
-                             attention=host_api.ATTENTION_ONLINE)
+                             attention=host_api.ATTENTION_ONLINE, eager_decode=eager)
     prepare_s = time.perf_counter() - t0
     rng = np.random.default_rng(4)
     prompts = rng.integers(0, VOCAB, size=(sequences, prompt_tokens)).tolist()
@@ -286,6 +286,7 @@ def measure_e2e(sequences: int, prompt_tokens: int, new_tokens: int, layers: int
         "m1_ms_per_token": round(st1.decode_ms / max(st1.decode_rows, 1), 3),
         "m1_prefill_ms": round(st1.prefill_ms, 2),
         "attention": "online_softmax",
+        "decode_graphs": not eager,
         "model_generate_s": round(gen_s, 1),
         "prepare_s": round(prepare_s, 1),
     }
@@ -305,6 +306,8 @@ def main() -> int:
     ap.add_argument("--e2e", default="32,512,128",
                     help="configs[4] end to end: sequences,prompt,new tokens through TokenService ('' = skip)")
     ap.add_argument("--e2e-only", action="store_true", help="run only the end-to-end leg and print its JSON")
+    ap.add_argument("--e2e-eager", action="store_true",
+                    help="decode steps launch kernel by kernel instead of replaying graphs (for kernel traces)")
     ap.add_argument("--trace-summary", default=None, metavar="CSV",
                     help="summarise a rocprofv3 kernel-trace CSV instead of benchmarking")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -330,7 +333,7 @@ def main() -> int:
 
     if args.e2e_only:
         seqs, prompt, new = (int(v) for v in args.e2e.split(","))
-        print(json.dumps(measure_e2e(seqs, prompt, new, args.layers)), flush=True)
+        print(json.dumps(measure_e2e(seqs, prompt, new, args.layers, args.e2e_eager)), flush=True)
         return 0
 
     import numpy as np

@@ -64,6 +64,8 @@ typedef struct air_host_engine_config {
     uint32_t token_budget_per_cycle;
     uint32_t max_active_requests;
     int32_t attention_tactic;      /* 0 baseline (the reference's double softmax), 1 online softmax (tiled f32) */
+    int32_t eager_decode;          /* 1: launch decode steps kernel by kernel instead of replaying a captured
+                                      graph per batch width (for kernel-level profiling) */
 } air_host_engine_config;
 
 /* Prepares the model on `device` (weights resident, repacked) and creates
