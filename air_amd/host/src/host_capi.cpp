@@ -1,6 +1,7 @@
 // host_capi.cpp -- the C ABI of include/air_host.h over the C++ executor.
 #include "air_host.h"
 
+#include "air/gguf.hpp"
 #include "air/hip_backend.hpp"
 #include "air/synthetic.hpp"
 #include "air/token_service.hpp"
@@ -8,10 +9,12 @@
 
 #include <chrono>
 #include <exception>
+#include <optional>
 #include <string>
 
 struct air_host_model {
     std::shared_ptr<const air::ModelDefinition> model;
+    std::optional<air::TokenId> eos;
 };
 
 struct air_host_engine {
@@ -77,7 +80,7 @@ int air_host_synthetic_qwen2(const air_host_qwen2_spec* spec, air_host_model** o
         s.tied_output = spec->tied_output != 0;
         auto model = air::make_synthetic_qwen2(s);
         if (!model) return fail(model.status());
-        *out = new air_host_model{std::move(model).value()};
+        *out = new air_host_model{std::move(model).value(), std::nullopt};
         return static_cast<int>(AIR_HIP_OK);
     });
 }
@@ -91,6 +94,55 @@ int air_host_model_describe(const air_host_model* model, uint64_t* storage_bytes
 
 int air_host_model_release(air_host_model* model) {
     delete model;
+    return AIR_HIP_OK;
+}
+
+int air_host_load_gguf(const char* path, air_host_model** out) {
+    if (!path || !out) return fail_argument("path and out must not be null");
+    *out = nullptr;
+    return guarded([&] {
+        air::gguf::ModelInfo info;
+        auto model = air::gguf::load_model(path, &info);
+        if (!model) return fail(model.status());
+        *out = new air_host_model{std::move(model).value(), info.eos};
+        return static_cast<int>(AIR_HIP_OK);
+    });
+}
+
+int air_host_write_gguf(const air_host_model* model, const char* path, int32_t eos) {
+    if (!model || !model->model || !path) return fail_argument("model and path must not be null");
+    return guarded([&] {
+        air::gguf::WriteOptions options;
+        if (eos >= 0) options.eos = eos;
+        if (air::Status s = air::gguf::write_model(path, *model->model, options); !s) return fail(s);
+        return static_cast<int>(AIR_HIP_OK);
+    });
+}
+
+int air_host_model_get_config(const air_host_model* model, air_host_model_config* out) {
+    if (!model || !model->model || !out) return fail_argument("model and out must not be null");
+    const auto& c = model->model->config();
+    *out = air_host_model_config{c.layer_count, c.embedding_size, c.feed_forward_size, c.attention_head_count,
+                                 c.kv_head_count, c.rope_dimension_count, c.vocabulary_size, c.context_length,
+                                 c.attention_sliding_window, c.rope_frequency_base, c.rms_norm_epsilon,
+                                 model->eos ? *model->eos : -1,
+                                 static_cast<uint32_t>(model->model->tensors().size())};
+    return AIR_HIP_OK;
+}
+
+int air_host_model_tensor(const air_host_model* model, uint32_t index, air_host_tensor_info* out) {
+    if (!model || !model->model || !out) return fail_argument("model and out must not be null");
+    const auto& tensors = model->model->tensors();
+    if (index >= tensors.size()) return fail_argument("tensor index is out of range");
+    const auto& t = tensors[index];
+    if (t.shape.dimensions.size() > 8U) return fail(air::Status::unsupported("tensor rank above 8"));
+    *out = air_host_tensor_info{};
+    out->name = t.name.c_str();
+    out->type = t.format_type;
+    out->rank = static_cast<uint32_t>(t.shape.dimensions.size());
+    for (std::size_t d = 0; d < t.shape.dimensions.size(); ++d) out->dims[d] = t.shape.dimensions[d];
+    out->offset = t.byte_offset;
+    out->size = t.byte_size;
     return AIR_HIP_OK;
 }
 

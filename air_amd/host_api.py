@@ -34,6 +34,24 @@ class Qwen2Spec(ctypes.Structure):
     ]
 
 
+class ModelConfig(ctypes.Structure):
+    _fields_ = [
+        ("layers", _U32), ("embedding", _U32), ("ffn", _U32), ("heads", _U32), ("kv_heads", _U32),
+        ("rope_dims", _U32), ("vocab", _U64), ("context", _U64), ("sliding_window", _U64),
+        ("rope_base", ctypes.c_double), ("rms_eps", ctypes.c_double), ("eos", _I32), ("tensors", _U32),
+    ]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+class TensorInfo(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char_p), ("type", _U32), ("rank", _U32), ("dims", _U64 * 8),
+        ("offset", _U64), ("size", _U64),
+    ]
+
+
 class EngineConfig(ctypes.Structure):
     _fields_ = [
         ("device", _I32), ("page_tokens", _U32), ("kv_pool_pages", _U32), ("max_step_rows", _U32),
@@ -61,6 +79,10 @@ SIGNATURES = {
     "air_host_synthetic_qwen2": (_I, [ctypes.POINTER(Qwen2Spec), _PP]),
     "air_host_model_describe": (_I, [_P, ctypes.POINTER(_U64), ctypes.POINTER(_U64)]),
     "air_host_model_release": (_I, [_P]),
+    "air_host_load_gguf": (_I, [ctypes.c_char_p, _PP]),
+    "air_host_write_gguf": (_I, [_P, ctypes.c_char_p, _I32]),
+    "air_host_model_get_config": (_I, [_P, ctypes.POINTER(ModelConfig)]),
+    "air_host_model_tensor": (_I, [_P, _U32, ctypes.POINTER(TensorInfo)]),
     "air_host_engine_create": (_I, [_P, ctypes.POINTER(EngineConfig), _PP]),
     "air_host_engine_release": (_I, [_P]),
     "air_host_generate_cohort": (_I, [_P, ctypes.POINTER(_I32), ctypes.POINTER(_U32), _U32, _U32, _I32,
@@ -111,6 +133,30 @@ class Model:
         out = ctypes.c_void_p()
         check(lib().air_host_synthetic_qwen2(ctypes.byref(spec), ctypes.byref(out)))
         return cls(out.value)
+
+    @classmethod
+    def load_gguf(cls, path: str) -> "Model":
+        """A GGUF v3 file, memory-mapped (AIR's GgufFormat::load rules)."""
+        out = ctypes.c_void_p()
+        check(lib().air_host_load_gguf(os.fsencode(path), ctypes.byref(out)))
+        return cls(out.value)
+
+    def write_gguf(self, path: str, eos: int = -1) -> None:
+        check(lib().air_host_write_gguf(self.handle, os.fsencode(path), eos))
+
+    def config(self) -> dict:
+        out = ModelConfig()
+        check(lib().air_host_model_get_config(self.handle, ctypes.byref(out)))
+        return out.as_dict()
+
+    def tensors(self) -> list:
+        """[(name, ggml type, dims, byte offset, byte size)] in table order."""
+        out = []
+        for i in range(self.config()["tensors"]):
+            t = TensorInfo()
+            check(lib().air_host_model_tensor(self.handle, i, ctypes.byref(t)))
+            out.append((t.name.decode(), t.type, [t.dims[d] for d in range(t.rank)], t.offset, t.size))
+        return out
 
     def describe(self):
         storage, tensors = _U64(), _U64()

@@ -54,6 +54,45 @@ int air_host_synthetic_qwen2(const air_host_qwen2_spec* spec, air_host_model** o
 int air_host_model_describe(const air_host_model* model, uint64_t* storage_bytes, uint64_t* tensors);
 int air_host_model_release(air_host_model* model);
 
+/* A GGUF v3 file (memory-mapped, read-only), loaded with the rules of AIR's
+ * GgufFormat::load (src/formats/gguf/gguf_format.cpp:278-311, gguf_reader.cpp:
+ * 346-472): the same limits, required keys, defaults and error classes
+ * (io_error: unreadable; invalid_argument: not GGUF; unsupported: not V3 or
+ * split; data_error: malformed). */
+int air_host_load_gguf(const char* path, air_host_model** out);
+/* Writes the model as a GGUF v3 file: Qwen2 metadata from its config, a
+ * placeholder vocabulary of vocab tokens, eos_token_id when eos >= 0, and
+ * every tensor at 32-byte aligned offsets. */
+int air_host_write_gguf(const air_host_model* model, const char* path, int32_t eos);
+
+typedef struct air_host_model_config {
+    uint32_t layers;
+    uint32_t embedding;
+    uint32_t ffn;
+    uint32_t heads;
+    uint32_t kv_heads;
+    uint32_t rope_dims;
+    uint64_t vocab;
+    uint64_t context;
+    uint64_t sliding_window;
+    double rope_base;
+    double rms_eps;
+    int32_t eos;                /* -1 when the file names none (or for synthetic models) */
+    uint32_t tensors;
+} air_host_model_config;
+int air_host_model_get_config(const air_host_model* model, air_host_model_config* out);
+
+/* Tensor `index` of the model's table (file order for GGUF). */
+typedef struct air_host_tensor_info {
+    const char* name;           /* valid while the model is alive */
+    uint32_t type;              /* GGML type id */
+    uint32_t rank;
+    uint64_t dims[8];           /* GGML order: dims[0] is the contiguous direction */
+    uint64_t offset;            /* byte offset in the model's storage (the file) */
+    uint64_t size;              /* bytes */
+} air_host_tensor_info;
+int air_host_model_tensor(const air_host_model* model, uint32_t index, air_host_tensor_info* out);
+
 typedef struct air_host_engine_config {
     int32_t device;
     uint32_t page_tokens;          /* KV page size in tokens (16 in the reference's CUDA plans) */

@@ -157,3 +157,31 @@ def ref_matvec(type_id: int, data: np.ndarray, k: int, n: int, x: np.ndarray) ->
     if rc != 0:
         raise ValueError(f"airref_matvec failed with status {rc}")
     return y
+
+
+class RefGgufConfig(ctypes.Structure):
+    _fields_ = [
+        ("layers", ctypes.c_uint32), ("embedding", ctypes.c_uint32), ("ffn", ctypes.c_uint32),
+        ("heads", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32), ("rope_dims", ctypes.c_uint32),
+        ("vocab", _U64), ("context", _U64), ("sliding_window", _U64),
+        ("rope_base", ctypes.c_double), ("rms_eps", ctypes.c_double), ("eos", ctypes.c_int32),
+        ("tensors", ctypes.c_uint32),
+    ]
+
+
+def ref_gguf_load(path: str, capacity: int = 4096):
+    """AIR's own GgufFormat::load on a file: (status, config dict, [(offset, size, type)])."""
+    lib = _load_ref()
+    fn = lib.airref_gguf_load
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_char_p, ctypes.POINTER(RefGgufConfig), _P, _P, _P, ctypes.c_uint32]
+    cfg = RefGgufConfig()
+    offsets = np.zeros(capacity, dtype=np.uint64)
+    sizes = np.zeros(capacity, dtype=np.uint64)
+    types = np.zeros(capacity, dtype=np.uint32)
+    rc = fn(os.fsencode(path), ctypes.byref(cfg), _addr(offsets), _addr(sizes), _addr(types), capacity)
+    if rc != 0:
+        return rc, None, None
+    n = min(cfg.tensors, capacity)
+    table = [(int(offsets[i]), int(sizes[i]), int(types[i])) for i in range(n)]
+    return 0, {name: getattr(cfg, name) for name, _ in RefGgufConfig._fields_}, table

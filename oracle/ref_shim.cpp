@@ -12,6 +12,7 @@
 // ModelStorage::map_read_only maps it, and ModelDefinition wraps the
 // descriptors.
 
+#include "air/format.hpp"
 #include "air/model.hpp"
 #include "air/reference.hpp"
 #include "air/storage.hpp"
@@ -246,5 +247,37 @@ int airref_qwen2_reset(airref_qwen2* q) {
 }
 
 void airref_qwen2_destroy(airref_qwen2* q) { delete q; }
+
+// GgufFormat::load of AIR itself on a file: the status code, and on success
+// the config and tensor table.  Lets the tests check that this repository's
+// GGUF reader and writer agree with AIR's reader on the same files.
+struct airref_gguf_config {
+    std::uint32_t layers, embedding, ffn, heads, kv_heads, rope_dims;
+    std::uint64_t vocab, context, sliding_window;
+    double rope_base, rms_eps;
+    std::int32_t eos;
+    std::uint32_t tensors;
+};
+
+int airref_gguf_load(const char* path, airref_gguf_config* out, std::uint64_t* offsets, std::uint64_t* sizes,
+                     std::uint32_t* types, std::uint32_t capacity) {
+    air::GgufFormat format;
+    auto model = format.load(path);
+    if (!model) return code_of(model.status());
+    const auto& c = model.value().config();
+    const auto& tok = model.value().tokenizer();
+    *out = airref_gguf_config{c.layer_count, c.embedding_size, c.feed_forward_size, c.attention_head_count,
+                              c.kv_head_count, c.rope_dimension_count, c.vocabulary_size, c.context_length,
+                              c.attention_sliding_window, c.rope_frequency_base, c.rms_norm_epsilon,
+                              tok.special_ids.eos ? *tok.special_ids.eos : -1,
+                              static_cast<std::uint32_t>(model.value().tensors().size())};
+    const auto& tensors = model.value().tensors();
+    for (std::uint32_t i = 0; i < capacity && i < tensors.size(); ++i) {
+        offsets[i] = tensors[i].byte_offset;
+        sizes[i] = tensors[i].byte_size;
+        types[i] = tensors[i].format_type;
+    }
+    return 0;
+}
 
 } // extern "C"

@@ -30,7 +30,7 @@ def _declared():
 def test_host_library_exports_every_declared_entry_point():
     lib = host_api.lib()
     declared = _declared()
-    assert len(declared) == 8
+    assert len(declared) == 12
     for name in declared:
         assert hasattr(lib, name), name
     assert set(host_api.SIGNATURES) == set(declared)
