@@ -4,8 +4,9 @@ import sys
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-if ROOT not in sys.path:
-    sys.path.insert(0, ROOT)
+for path in (ROOT, os.path.join(ROOT, "tests")):   # the package, and test modules sharing helpers
+    if path not in sys.path:
+        sys.path.insert(0, path)
 
 
 def pytest_configure(config):
