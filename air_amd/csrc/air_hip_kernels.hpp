@@ -131,6 +131,11 @@ SkinnyShape plan_skinny(const TilePlanes& planes, std::uint32_t m, std::uint32_t
 std::uint64_t skinny_partials_bytes(const SkinnyShape& shape, std::uint32_t m, std::uint64_t n);
 hipError_t launch_skinny_linear(const TilePlanes& planes, const SplitWorkspace& ws, const float* bias, float* y,
                                 std::uint32_t m, const SkinnyShape& shape, float* partials, hipStream_t stream);
+// The same linear straight from f32 activations x [m][k]: each workgroup
+// splits the activations it stages (one power-of-two scale per (row,
+// 32-block)), so no split launch and no activation workspace.
+hipError_t launch_skinny_linear_x(const TilePlanes& planes, const float* x, const float* bias, float* y,
+                                  std::uint32_t m, const SkinnyShape& shape, float* partials, hipStream_t stream);
 
 // ---- the Qwen2 step around the linears ----------------------------------
 

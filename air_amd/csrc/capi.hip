@@ -167,6 +167,37 @@ int run_prefill(air_hip_context* ctx, const air_hip_matrix* m, const float* x, f
     return AIR_HIP_OK;
 }
 
+int ensure_split_buffers(air_hip_context* ctx, std::uint64_t partial_bytes, std::uint32_t counters);
+
+// Skinny decode linear straight from the f32 rows (M = 2..64): one launch
+// (two with a K split), no activation workspace.
+int run_skinny_x(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y, const float* bias,
+                 std::uint32_t rows) {
+    const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits);
+    // The in-workgroup split repeats the activation split in every
+    // workgroup: it pays on narrow matrices, where the separate split launch
+    // dominates (Qwen2-7B q|k|v, o, down at M <= 32: 10-25 % faster), and
+    // loses on wide ones (gate|up, lm_head: up to 2x slower) and at M = 64.
+    // Q4_K with four activation tiles would also spill in it.
+    const bool narrow = m->planes.nt <= 512u && (rows <= 32u || m->planes.k <= 4096u);
+    if (!narrow || (m->planes.type == kQ4_K && shape.mt == 4u)) {
+        int rc = air_hip_activations_load(ctx, x, m->planes.k, rows);
+        if (rc != AIR_HIP_OK) return rc;
+        return air_hip_linear_loaded(ctx, m, y, bias, AIR_HIP_LINEAR_DECODE);
+    }
+    const std::uint64_t partial_bytes = skinny_partials_bytes(shape, rows, m->planes.n);
+    if (partial_bytes > 0u) {
+        const int rc = ensure_split_buffers(ctx, partial_bytes, 0u);
+        if (rc != AIR_HIP_OK) return rc;
+    }
+    const hipError_t err = launch_skinny_linear_x(m->planes, x, bias, y, rows, shape,
+                                                  static_cast<float*>(ctx->split_partials), ctx->stream);
+    if (err != hipSuccess) return hip_fail(err, "skinny_kernel");
+    ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
+    ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
+    return AIR_HIP_OK;
+}
+
 int ensure_split_buffers(air_hip_context* ctx, std::uint64_t partial_bytes, std::uint32_t counters) {
     if (partial_bytes > ctx->split_partials_bytes || counters > ctx->split_counter_count) {
         const hipError_t sync = hipStreamSynchronize(ctx->stream);
@@ -599,16 +630,15 @@ int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* m, const float* x
             return AIR_HIP_OK;
         }
         // Measured on the Qwen2-7B shapes (M = 2..16): the single-launch fused
-        // kernel wins for narrow matrices (N <= 4096, where the skinny
-        // kernel's three launches dominate) and for very large ones at M <= 4.
+        // kernel wins for small square matrices (o: N, K <= 4096) and for very
+        // large ones at M <= 4; the skinny kernel everywhere else (down, with
+        // its long K, by 10-30 %).
         const std::uint64_t weight_bytes = static_cast<std::uint64_t>(m->planes.nt) * m->planes.kt *
                                            geometry_of(m->planes.type).code_tile_bytes;
-        const bool prefer_fused = m->planes.n <= 4096u || (rows <= 4u && weight_bytes >= (256ull << 20));
+        const bool prefer_fused = (m->planes.n <= 4096u && m->planes.k <= 4096u) ||
+                                  (rows <= 4u && weight_bytes >= (256ull << 20));
         if (ctx->decode_path == 2u || (ctx->decode_path == 0u && !prefer_fused)) {
-            // Split the activations once, then the skinny kernel.
-            int rc = air_hip_activations_load(ctx, x, m->planes.k, rows);
-            if (rc != AIR_HIP_OK) return rc;
-            return air_hip_linear_loaded(ctx, m, y, bias, AIR_HIP_LINEAR_DECODE);
+            return run_skinny_x(ctx, m, x, y, bias, rows);
         }
         const FusedShape shape = plan_decode_fused(m->planes, rows, ctx->tuning);
         if (shape.k_splits > 1u) {
@@ -621,6 +651,13 @@ int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* m, const float* x
         ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
         ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
         return AIR_HIP_OK;
+    }
+    if (rows == 0) return fail(AIR_HIP_INVALID_ARGUMENT, "linear batch width must be non-zero");
+    if (rows <= AIR_HIP_MAX_DECODE_ROWS && ctx->decode_path != 1u) {
+        if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
+        DeviceScope scope(ctx->device);
+        if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+        return run_skinny_x(ctx, m, x, y, bias, rows);
     }
     int rc = air_hip_activations_load(ctx, x, m->planes.k, rows);
     if (rc != AIR_HIP_OK) return rc;

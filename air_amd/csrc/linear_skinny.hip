@@ -17,6 +17,13 @@
 //   * when the weight tiles alone cannot occupy the 256 CUs, K is split over
 //     workgroups and the partials are summed by a second, fixed-order pass.
 //
+// Two activation sources: the row-scaled split written once by
+// split_rows_kernel (air_hip_activations_load, shared by several linears),
+// or the f32 rows themselves (XF): the workgroup then splits each step's
+// activations while staging them, with one power-of-two scale per (row,
+// 32-block) applied in the epilogue, so a linear is one launch (plus the
+// split reduction) and writes no activation workspace.
+//
 // Replaces specialized_matmul_kernel / specialized_matmul_batch_reuse_kernel
 // (src/cuda/cuda_backend.cu:501-583), which decode every weight M/4 or M/8
 // times.
@@ -31,6 +38,8 @@ constexpr unsigned kThreads = 256;
 constexpr unsigned kSplitThreads = 1024;  // one workgroup per activation row
 
 struct SkinnyArgs {
+    const float* x;              // XF: activations [m][k] f32
+    std::uint64_t k;             // XF: input width
     const void* codes;
     const void* scales;
     std::uint32_t nt, kt;
@@ -47,13 +56,17 @@ struct SkinnyArgs {
     std::uint32_t partial;
 };
 
-template <int FMT, int MT, int TN>
+template <int FMT, int MT, int TN, bool XF>
 __global__ __launch_bounds__(kThreads, 2) void skinny_kernel(SkinnyArgs a) {
     constexpr unsigned kMp = 16u * MT;
     constexpr unsigned kChunks = 2u * MT * 2u * 64u / kThreads;  // uint4 of activations per thread per step
     constexpr bool kSums = FMT == kQ4_K;
+    constexpr unsigned kFrags = 2u * MT;                          // XF: (block, tile) fragments per step
+    constexpr unsigned kFragsPerWave = (kFrags + 3u) / 4u;
     __shared__ u32x4 xa[2][2 * MT * 2 * 64];     // [buf][block][tile][part][lane]
-    __shared__ float4v sm[2][kSums ? 2 * kMp / 4 : 1];  // [buf][block][row] sums of scaled x (Q4_K)
+    // [buf][block][row] sums of x (Q4_K): scaled per row, or unscaled (XF).
+    __shared__ float4v sm[2][kSums ? 2 * kMp / 4 : 1];
+    __shared__ float4v sinv[2][XF ? 2 * kMp / 4 : 1];  // XF: [buf][block][row] inverse scales
 
     const std::uint32_t tid = threadIdx.x;
     const std::uint32_t lane = tid & 63u;
@@ -71,21 +84,69 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_kernel(SkinnyArgs a) {
         for (int t = 0; t < MT; ++t) acc[j][t] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
     // Activation staging: step s covers blocks 2s, 2s+1, contiguous in the workspace.
-    u32x4 xr[kChunks];
+    u32x4 xr[XF ? 1 : kChunks];
     float4v mr = {0.f, 0.f, 0.f, 0.f};
+    // XF: wave w splits fragments w, w + 4, ...: fragment c is block c / MT,
+    // activation tile c % MT; lane l holds row l % 16, elements 8 (l / 16)..+7.
+    float4 xf[XF ? kFragsPerWave : 1][2];
     const auto load_x = [&](std::uint32_t s) __attribute__((always_inline)) {
-        const u32x4* src = reinterpret_cast<const u32x4*>(a.xs) + static_cast<std::uint64_t>(s) * (2u * MT * 2u * 64u);
+        if constexpr (XF) {
 #pragma unroll
-        for (unsigned j = 0; j < kChunks; ++j) xr[j] = src[tid + kThreads * j];
-        if constexpr (kSums) {
-            if (tid < 2u * kMp / 4u) mr = reinterpret_cast<const float4v*>(a.block_sums + static_cast<std::uint64_t>(s) * 2u * kMp)[tid];
+            for (unsigned r = 0; r < kFragsPerWave; ++r) {
+                const unsigned c = wave + 4u * r;
+                const unsigned row = (c % MT) * 16u + (lane & 15u);
+                const std::uint64_t col = (2u * static_cast<std::uint64_t>(s) + c / MT) * 32u + 8u * (lane >> 4);
+                xf[r][0] = make_float4(0.f, 0.f, 0.f, 0.f);
+                xf[r][1] = xf[r][0];
+                if (c < kFrags && row < a.m && col < a.k) {
+                    const float4* src = reinterpret_cast<const float4*>(a.x + static_cast<std::uint64_t>(row) * a.k + col);
+                    xf[r][0] = src[0];
+                    xf[r][1] = src[1];
+                }
+            }
+        } else {
+            const u32x4* src = reinterpret_cast<const u32x4*>(a.xs) + static_cast<std::uint64_t>(s) * (2u * MT * 2u * 64u);
+#pragma unroll
+            for (unsigned j = 0; j < kChunks; ++j) xr[j] = src[tid + kThreads * j];
+            if constexpr (kSums) {
+                if (tid < 2u * kMp / 4u) mr = reinterpret_cast<const float4v*>(a.block_sums + static_cast<std::uint64_t>(s) * 2u * kMp)[tid];
+            }
         }
     };
     const auto store_x = [&](unsigned buf) __attribute__((always_inline)) {
+        if constexpr (XF) {
 #pragma unroll
-        for (unsigned j = 0; j < kChunks; ++j) xa[buf][tid + kThreads * j] = xr[j];
-        if constexpr (kSums) {
-            if (tid < 2u * kMp / 4u) sm[buf][tid] = mr;
+            for (unsigned r = 0; r < kFragsPerWave; ++r) {
+                const unsigned c = wave + 4u * r;
+                if (c >= kFrags) continue;  // uniform per wave
+                const float v[8] = {xf[r][0].x, xf[r][0].y, xf[r][0].z, xf[r][0].w,
+                                    xf[r][1].x, xf[r][1].y, xf[r][1].z, xf[r][1].w};
+                float amax = fmaxf(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))),
+                                   fmaxf(fmaxf(fabsf(v[4]), fabsf(v[5])), fmaxf(fabsf(v[6]), fabsf(v[7]))));
+                amax = fmaxf(amax, __shfl_xor(amax, 16));
+                amax = fmaxf(amax, __shfl_xor(amax, 32));
+                float sc, inv;
+                block_scale(amax, sc, inv);
+                half8v hi, lo;
+                split8(v, sc, hi, lo);
+                const unsigned base = (c * 2u) * 64u + lane;   // c = block * MT + tile
+                xa[buf][base] = __builtin_bit_cast(u32x4, hi);
+                xa[buf][base + 64u] = __builtin_bit_cast(u32x4, lo);
+                const unsigned slot = (c / MT) * kMp + (c % MT) * 16u + lane;   // [block][row]
+                if (lane < 16u) reinterpret_cast<float*>(&sinv[buf][0])[slot] = inv;
+                if constexpr (kSums) {
+                    float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+                    sum += __shfl_xor(sum, 16);
+                    sum += __shfl_xor(sum, 32);
+                    if (lane < 16u) reinterpret_cast<float*>(&sm[buf][0])[slot] = sum;
+                }
+            }
+        } else {
+#pragma unroll
+            for (unsigned j = 0; j < kChunks; ++j) xa[buf][tid + kThreads * j] = xr[j];
+            if constexpr (kSums) {
+                if (tid < 2u * kMp / 4u) sm[buf][tid] = mr;
+            }
         }
     };
     StepCodes<FMT> wa[TN], wb[TN];
@@ -117,11 +178,17 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_kernel(SkinnyArgs a) {
                 const half8v lo = __builtin_bit_cast(half8v, xa[buf][base + 64u]);
                 float4v sum4 = {0.f, 0.f, 0.f, 0.f};
                 if constexpr (kSums) sum4 = sm[buf][(static_cast<unsigned>(b) * kMp + t * 16u) / 4u + (lane >> 4)];
+                float4v inv4 = {1.f, 1.f, 1.f, 1.f};
+                if constexpr (XF) inv4 = sinv[buf][(static_cast<unsigned>(b) * kMp + t * 16u) / 4u + (lane >> 4)];
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
                     float4v p = mfma16x16x32(hi, w[j], float4v{0.f, 0.f, 0.f, 0.f});
                     p = mfma16x16x32(lo, w[j], p);
-                    acc[j][t] += ws[j] * p;
+                    if constexpr (XF) {
+                        acc[j][t] += (ws[j] * inv4) * p;
+                    } else {
+                        acc[j][t] += ws[j] * p;
+                    }
                     if constexpr (kSums) acc[j][t] -= wo[j] * sum4;
                 }
             }
@@ -148,7 +215,9 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_kernel(SkinnyArgs a) {
     // column l%16; the rows' power-of-two activation scales are undone here.
     float4v inv[MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) inv[t] = reinterpret_cast<const float4v*>(a.inv_scale)[t * 4 + (lane >> 4)];
+    for (int t = 0; t < MT; ++t) {
+        inv[t] = XF ? float4v{1.f, 1.f, 1.f, 1.f} : reinterpret_cast<const float4v*>(a.inv_scale)[t * 4 + (lane >> 4)];
+    }
     float* out = a.out + (a.partial ? static_cast<std::uint64_t>(split) * a.m * a.n : 0u);
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
@@ -263,23 +332,34 @@ __global__ __launch_bounds__(kSplitThreads) void split_rows_kernel(const float* 
     if (threadIdx.x == 0) inv_scale[m] = inv;
 }
 
-template <int FMT, int MT>
+template <int FMT, int MT, bool XF>
 hipError_t launch_mt(const SkinnyArgs& a, std::uint32_t tn, std::uint32_t blocks, hipStream_t stream) {
     if (tn == 2u) {
-        hipLaunchKernelGGL((skinny_kernel<FMT, MT, 2>), dim3(blocks), dim3(kThreads), 0, stream, a);
+        hipLaunchKernelGGL((skinny_kernel<FMT, MT, 2, XF>), dim3(blocks), dim3(kThreads), 0, stream, a);
     } else {
-        hipLaunchKernelGGL((skinny_kernel<FMT, MT, 1>), dim3(blocks), dim3(kThreads), 0, stream, a);
+        hipLaunchKernelGGL((skinny_kernel<FMT, MT, 1, XF>), dim3(blocks), dim3(kThreads), 0, stream, a);
     }
     return hipGetLastError();
 }
 
-template <int FMT>
+template <int FMT, bool XF>
 hipError_t launch_fmt(const SkinnyArgs& a, const SkinnyShape& shape, std::uint32_t blocks, hipStream_t stream) {
     switch (shape.mt) {
-    case 1: return launch_mt<FMT, 1>(a, shape.tile_n, blocks, stream);
-    case 2: return launch_mt<FMT, 2>(a, shape.tile_n, blocks, stream);
-    case 3: return launch_mt<FMT, 3>(a, shape.tile_n, blocks, stream);
-    default: return launch_mt<FMT, 4>(a, shape.tile_n, blocks, stream);
+    case 1: return launch_mt<FMT, 1, XF>(a, shape.tile_n, blocks, stream);
+    case 2: return launch_mt<FMT, 2, XF>(a, shape.tile_n, blocks, stream);
+    case 3: return launch_mt<FMT, 3, XF>(a, shape.tile_n, blocks, stream);
+    default: return launch_mt<FMT, 4, XF>(a, shape.tile_n, blocks, stream);
+    }
+}
+
+template <bool XF>
+hipError_t launch_any(const TilePlanes& p, const SkinnyArgs& a, const SkinnyShape& shape, std::uint32_t blocks,
+                      hipStream_t stream) {
+    switch (p.type) {
+    case kQ8_0: return launch_fmt<kQ8_0, XF>(a, shape, blocks, stream);
+    case kQ4_0: return launch_fmt<kQ4_0, XF>(a, shape, blocks, stream);
+    case kQ4_K: return launch_fmt<kQ4_K, XF>(a, shape, blocks, stream);
+    default: return hipErrorInvalidValue;
     }
 }
 
@@ -298,10 +378,11 @@ SkinnyShape plan_skinny(const TilePlanes& p, std::uint32_t m, std::uint32_t tile
     SkinnyShape s;
     s.mt = static_cast<std::uint32_t>(ceil_div(m, 16u));
     // Two weight tiles per wave halve the LDS activation reads per weight
-    // byte; Q4_K with three or more activation tiles would spill registers.
+    // byte; with three or more activation tiles they would spill registers
+    // (the in-workgroup split of the f32 variant holds more live values).
     // Automatic choice, measured on the Qwen2-7B shapes: two tiles only pay
     // for matrices of 2000..4096 row tiles (gate|up) at M <= 32.
-    const std::uint32_t tn2_max_mt = p.type == kQ4_K ? 2u : 4u;
+    const std::uint32_t tn2_max_mt = 2u;
     const std::uint32_t want = tile_n != 0u ? tile_n : ((s.mt <= 2u && p.nt >= 2000u && p.nt <= 4096u) ? 2u : 1u);
     s.tile_n = (want == 2u && s.mt <= tn2_max_mt) ? 2u : 1u;
     s.groups = static_cast<std::uint32_t>(ceil_div(p.nt, 4u * s.tile_n));
@@ -349,13 +430,32 @@ hipError_t launch_skinny_linear(const TilePlanes& p, const SplitWorkspace& ws, c
     a.bias = split ? nullptr : bias;
     a.out = split ? partials : y;
     const std::uint32_t blocks = shape.groups * shape.splits;
-    hipError_t err;
-    switch (p.type) {
-    case kQ8_0: err = launch_fmt<kQ8_0>(a, shape, blocks, stream); break;
-    case kQ4_0: err = launch_fmt<kQ4_0>(a, shape, blocks, stream); break;
-    case kQ4_K: err = launch_fmt<kQ4_K>(a, shape, blocks, stream); break;
-    default: return hipErrorInvalidValue;
-    }
+    const hipError_t err = launch_any<false>(p, a, shape, blocks, stream);
+    if (err != hipSuccess || !split) return err;
+    return launch_split_reduce(partials, shape.splits, m, p.n, bias, y, stream);
+}
+
+hipError_t launch_skinny_linear_x(const TilePlanes& p, const float* x, const float* bias, float* y, std::uint32_t m,
+                                  const SkinnyShape& shape, float* partials, hipStream_t stream) {
+    if (m == 0u || m > 64u || shape.mt != ceil_div(m, 16u) || p.k % 32u != 0u) return hipErrorInvalidValue;
+    SkinnyArgs a{};
+    a.x = x;
+    a.k = p.k;
+    a.codes = p.codes;
+    a.scales = p.scales;
+    a.nt = p.nt;
+    a.kt = p.kt;
+    a.n = p.n;
+    a.m = m;
+    a.groups = shape.groups;
+    a.steps = shape.steps;
+    a.steps_per_split = shape.steps_per_split;
+    const bool split = shape.splits > 1u;
+    a.partial = split ? 1u : 0u;
+    a.bias = split ? nullptr : bias;
+    a.out = split ? partials : y;
+    const std::uint32_t blocks = shape.groups * shape.splits;
+    const hipError_t err = launch_any<true>(p, a, shape, blocks, stream);
     if (err != hipSuccess || !split) return err;
     return launch_split_reduce(partials, shape.splits, m, p.n, bias, y, stream);
 }
