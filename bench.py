@@ -239,6 +239,92 @@ def measure_prefill(torch, ctx, capi, layers, m, steps, dev, stream):
             "mfma_frac": round(tflops / F16_MFMA_PEAK_TFLOPS, 4), "dtype": "f16 operands, f32 accumulate"}
 
 
+FORMAT_BLOCKS = {8: (32, 34), 2: (32, 18), 12: (256, 144)}   # GGML id: (block elements, block bytes)
+
+
+def format_step_bytes(type_id: int, m: int, layers: int) -> int:
+    """step_algorithmic_bytes for any of the three formats."""
+    be, bb = FORMAT_BLOCKS[type_id]
+    per_layer = [(HIDDEN, HIDDEN, True), (HIDDEN, KV, True), (HIDDEN, KV, True), (HIDDEN, HIDDEN, False),
+                 (HIDDEN, FFN, False), (HIDDEN, FFN, False), (FFN, HIDDEN, False)]
+    total = sum(n * (k // be) * bb + 4 * m * k + 4 * m * n + (4 * n if bias else 0) for k, n, bias in per_layer)
+    total *= layers
+    return total + VOCAB * (HIDDEN // be) * bb + 4 * m * HIDDEN + 4 * m * VOCAB
+
+
+def measure_formats(torch, capi, quant, dev, stream, types, ms, layers, steps, warmup) -> dict:
+    """the same 7B linear set in Q4_0 / Q4_K at each M, one step
+    replayed as a HIP graph, GB/s on the format's algorithmic bytes."""
+    out = {}
+    ctx = capi.Context(0, stream.cuda_stream)
+    for type_id in types:
+        mats, seed = [], 5000 + type_id * 100
+        for _ in range(layers):
+            layer = {}
+            for name, k, n in (("qkv", HIDDEN, HIDDEN + 2 * KV), ("o", HIDDEN, HIDDEN),
+                               ("gate_up", HIDDEN, 2 * FFN), ("down", FFN, HIDDEN)):
+                canon = quant.synthetic_weights_device(type_id, k, n, seed, dev)
+                seed += 1
+                layer[name] = capi.Matrix(ctx, type_id, k, n, canon, canon.numel(), on_device=True)
+                del canon
+            mats.append(layer)
+        canon = quant.synthetic_weights_device(type_id, HIDDEN, VOCAB, seed, dev)
+        head = capi.Matrix(ctx, type_id, HIDDEN, VOCAB, canon, canon.numel(), on_device=True)
+        del canon
+        torch.cuda.synchronize()
+        mmax = max(ms)
+        ctx.reserve(FFN, mmax)
+        x_h = torch.randn((mmax, HIDDEN), device=dev)
+        x_f = torch.randn((mmax, FFN), device=dev)
+        bias = torch.randn((HIDDEN + 2 * KV,), device=dev) * 0.02
+        y_qkv = torch.empty((mmax, HIDDEN + 2 * KV), device=dev)
+        y_h = torch.empty((mmax, HIDDEN), device=dev)
+        y_gu = torch.empty((mmax, 2 * FFN), device=dev)
+        logits = torch.empty((mmax, VOCAB), device=dev)
+        res = {}
+        for m in ms:
+            def step():
+                for layer in mats:
+                    layer["qkv"].linear(x_h, y_qkv, m, bias=bias)
+                    layer["o"].linear(x_h, y_h, m)
+                    layer["gate_up"].linear(x_h, y_gu, m)
+                    layer["down"].linear(x_f, y_h, m)
+                head.linear(x_h, logits, m)
+            for _ in range(warmup):
+                step()
+            torch.cuda.synchronize()
+            capture = torch.cuda.Stream(dev)
+            ctx.set_stream(capture.cuda_stream)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=capture):
+                step()
+            ctx.set_stream(stream.cuda_stream)
+            for _ in range(warmup):
+                graph.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(steps):
+                graph.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms_step = e0.elapsed_time(e1) / steps
+            algo = format_step_bytes(type_id, m, layers)
+            res[str(m)] = {"ms_per_step": round(ms_step, 4), "gbps": round(algo / (ms_step * 1e-3) / 1e9, 1),
+                           "tok_s": round(m / (ms_step * 1e-3), 1)}
+            del graph
+        out[capi.TYPE_NAMES[type_id]] = res
+        for layer in mats:
+            for mat in layer.values():
+                mat.release()
+        head.release()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        print(f"# {capi.TYPE_NAMES[type_id]}: {res}", file=sys.stderr, flush=True)
+    ctx.close()
+    return out
+
+
 def measure_e2e(sequences: int, prompt_tokens: int, new_tokens: int, layers: int, eager: bool = False) -> dict:
     """a random-init Qwen2-7B-shaped Q8_0 model through TokenService
     (admission, MicrobatchScheduler cycles, prefill_batch at up to 512 rows on
@@ -303,6 +389,9 @@ def main() -> int:
     ap.add_argument("--graph", type=int, default=1, help="replay each step as a captured HIP graph (1) or launch eagerly (0)")
     ap.add_argument("--prefill-m", type=int, default=512,
                     help="also time the prefill tactic (f16 MFMA GEMM) over the 28 layers' linears at this M (0 = skip)")
+    ap.add_argument("--formats", default="2,12",
+                    help="configs[3]: also time the linear set in these GGML formats (2 Q4_0, 12 Q4_K; '' = skip)")
+    ap.add_argument("--formats-m", default="1,16,64", help="decode rows of the configs[3] leg")
     ap.add_argument("--e2e", default="32,512,128",
                     help="configs[4] end to end: sequences,prompt,new tokens through TokenService ('' = skip)")
     ap.add_argument("--e2e-only", action="store_true", help="run only the end-to-end leg and print its JSON")
@@ -496,6 +585,14 @@ def main() -> int:
         cpu = cpu_baseline(cpu_sample, HIDDEN, 2 * FFN, args.cpu_seconds)
         print(f"# cpu baseline: {cpu}", file=sys.stderr, flush=True)
 
+    formats = None
+    if args.formats:
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        formats = measure_formats(torch, capi, quant, dev, stream, [int(v) for v in args.formats.split(",")],
+                                  [int(v) for v in args.formats_m.split(",")], args.layers, max(5, args.steps // 3),
+                                  args.warmup)
+
     e2e = None
     if args.e2e:
         torch.cuda.synchronize()
@@ -531,6 +628,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "formats": formats,
         "e2e": e2e,
     }
     print(json.dumps(line), flush=True)
