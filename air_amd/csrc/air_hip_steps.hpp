@@ -32,13 +32,27 @@ struct StepCodes<kQ4_K> {
     u32x4 h;               // the 16-byte super-block header of the lane's row
 };
 
-template <int FMT>
+// Streaming (read-once) code loads use non-temporal hints so they do not
+// displace reused data in the caches; NT = false for kernels whose
+// workgroups share weight tiles through L2.  Only Q8_0 takes the hint: a
+// Q4_0 / Q4_K step reads half of each lane's 16-byte record and the next
+// step the other half, which a streaming hint would evict in between.
+template <typename T, bool NT>
+__device__ __forceinline__ T load_code(const T* p) {
+    if constexpr (NT) {
+        return __builtin_nontemporal_load(p);
+    } else {
+        return *p;
+    }
+}
+
+template <int FMT, bool NT = false>
 __device__ __forceinline__ void load_step(const void* codes, const void* scales, std::uint32_t rt, std::uint32_t kt_count,
                                           std::uint32_t s, std::uint32_t lane, bool live, StepCodes<FMT>& out) {
     if constexpr (FMT == kQ8_0) {
         if (!live) { out.c = u32x4{0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u}; out.d = 0u; return; }
         const std::uint64_t tile = static_cast<std::uint64_t>(rt) * kt_count + s;
-        out.c = static_cast<const u32x4*>(codes)[tile * 64u + lane];
+        out.c = load_code<u32x4, NT>(static_cast<const u32x4*>(codes) + tile * 64u + lane);
         out.d = static_cast<const std::uint32_t*>(scales)[tile * 16u + (lane & 15u)];
     } else if constexpr (FMT == kQ4_0) {
         if (!live) { out.c = u32x2{0x88888888u, 0x88888888u}; out.d = 0u; return; }

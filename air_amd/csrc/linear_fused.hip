@@ -123,7 +123,9 @@ __device__ __forceinline__ void load_block_tile(BlockTile<FMT, R>& t, const void
     for (int r = 0; r < R; ++r) {
         const std::uint64_t tile = static_cast<std::uint64_t>(rt0 + r) * KT + kt;
         if (row_live[r]) {
-            t.c[r] = codes[tile * 64u + lane];
+            // Weight codes are read once per launch: non-temporal loads.
+            const u32x4 word = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(codes) + tile * 64u + lane);
+            t.c[r] = make_uint4(word.x, word.y, word.z, word.w);
             t.sc[r] = scales[tile * 16u + (lane & 15u)];
         } else {
             t.c[r] = make_uint4(zero_code, zero_code, zero_code, zero_code);
@@ -234,8 +236,14 @@ decode_fused_kernel(const void* __restrict__ codes_, const void* __restrict__ sc
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const std::uint64_t tile = static_cast<std::uint64_t>(rt0 + r) * KT + kt;
-                c0[r] = row_live[r] ? codes[(tile * 2u) * 64u + lane] : make_uint4(0u, 0u, 0u, 0u);
-                c1[r] = row_live[r] ? codes[(tile * 2u) * 64u + 64u + lane] : make_uint4(0u, 0u, 0u, 0u);
+                u32x4 w0 = {0u, 0u, 0u, 0u}, w1 = {0u, 0u, 0u, 0u};
+                if (row_live[r]) {
+                    const u32x4* rec = reinterpret_cast<const u32x4*>(codes) + (tile * 2u) * 64u + lane;
+                    w0 = __builtin_nontemporal_load(rec);
+                    w1 = __builtin_nontemporal_load(rec + 64u);
+                }
+                c0[r] = make_uint4(w0.x, w0.y, w0.z, w0.w);
+                c1[r] = make_uint4(w1.x, w1.y, w1.z, w1.w);
                 sc[r] = row_live[r] ? scales[tile * 16u + mrow] : make_uint4(0u, 0u, 0u, 0u);
             }
 #pragma unroll

@@ -74,7 +74,14 @@ __device__ __forceinline__ void load_chunk(Chunk<FMT, R>& ch, const void* __rest
             const std::uint64_t tile = static_cast<std::uint64_t>(rt0 + r) * KT + kt;
 #pragma unroll
             for (int v = 0; v < F::kCodeVecs; ++v) {
-                ch.c[j][r][v] = live ? codes[(tile * F::kCodeVecs + v) * 64u + lane] : make_uint4(0u, 0u, 0u, 0u);
+                // Weight codes are read once per pass: non-temporal loads keep
+                // them from displacing the activations and scales in the caches.
+                u32x4 word = {0u, 0u, 0u, 0u};
+                if (live) {
+                    word = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(codes) +
+                                                      (tile * F::kCodeVecs + v) * 64u + lane);
+                }
+                ch.c[j][r][v] = make_uint4(word.x, word.y, word.z, word.w);
             }
             ch.sc[j][r] = live ? scales[tile * 16u + (lane & 15u)] : typename F::Scale{};
         }

@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_kernel(SkinnyArgs a) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             const std::uint32_t rt = rt0 + static_cast<std::uint32_t>(j);
-            load_step<FMT>(a.codes, a.scales, rt, a.kt, s, lane, rt < a.nt, dst[j]);
+            load_step<FMT, true>(a.codes, a.scales, rt, a.kt, s, lane, rt < a.nt, dst[j]);
         }
     };
     const auto step = [&](std::uint32_t s, StepCodes<FMT>(&cur)[TN]) __attribute__((always_inline)) {
