@@ -149,7 +149,7 @@ decode_linear_kernel(const void* __restrict__ codes_, const void* __restrict__ s
                      std::uint32_t NT, std::uint32_t KT, std::uint32_t mtiles_total) {
     extern __shared__ float4v partials[];
     const std::uint32_t lane = threadIdx.x & 63u;
-    const std::uint32_t wave = threadIdx.x >> 6;
+    const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const std::uint32_t W = blockDim.x >> 6;
     const std::uint32_t rt0 = blockIdx.x * R;
     const std::uint32_t mt0 = blockIdx.y * MT;

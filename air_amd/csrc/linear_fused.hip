@@ -192,7 +192,7 @@ decode_fused_kernel(const void* __restrict__ codes_, const void* __restrict__ sc
                     float4v* __restrict__ split_partials, std::uint32_t* __restrict__ split_counters) {
     extern __shared__ float4v partials[];
     const std::uint32_t lane = threadIdx.x & 63u;
-    const std::uint32_t wave = threadIdx.x >> 6;
+    const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const std::uint32_t W = blockDim.x >> 6;
     const std::uint32_t rt0 = blockIdx.x * R;
     // k tiles of this workgroup's slice, then of this wave within it

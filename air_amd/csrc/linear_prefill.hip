@@ -155,7 +155,7 @@ __global__ __launch_bounds__(kThreads, (TM * TN >= 32 && PF == 2) ? 1 : 2) void 
 
     const std::uint32_t tid = threadIdx.x;
     const std::uint32_t lane = tid & 63u;
-    const std::uint32_t wave = tid >> 6;
+    const std::uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     // XCD-aware order: hardware hands workgroup i to XCD i % 8, so logical
     // tiles are dealt in contiguous runs per XCD; the m-tiles of one weight
     // group (the fastest logical index) then share that XCD's L2.

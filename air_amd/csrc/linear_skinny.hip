@@ -70,7 +70,7 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_kernel(SkinnyArgs a) {
 
     const std::uint32_t tid = threadIdx.x;
     const std::uint32_t lane = tid & 63u;
-    const std::uint32_t wave = tid >> 6;
+    const std::uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const std::uint32_t group = blockIdx.x % a.groups;
     const std::uint32_t split = blockIdx.x / a.groups;
     const std::uint32_t rt0 = (group * 4u + wave) * TN;
