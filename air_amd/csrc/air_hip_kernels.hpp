@@ -79,6 +79,7 @@ struct GemvShape {
     std::uint32_t rows_per_wave{1};
     std::uint32_t waves_per_group{1};
     std::uint32_t depth{2};           // chunk buffers per wave (1 or 2)
+    std::uint32_t units_per_chunk{1}; // work units per 16-block chunk (1, or 2 for one-tile waves)
 };
 GemvShape plan_decode_gemv(const TilePlanes& planes, const DecodeTuning& tuning);
 hipError_t launch_decode_gemv(const TilePlanes& planes, const float* x, const float* bias, float* y,

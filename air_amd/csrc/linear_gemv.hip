@@ -47,34 +47,39 @@ template <> struct GemvFormat<kQ4_K> {
     using Scale = uint4;
 };
 
-// One chunk (16 blocks) of R row tiles plus the lane's activations.
-template <int FMT, int R>
+// One work unit of R row tiles plus the lane's activations: a chunk (16
+// blocks) split into U units of 16/U blocks each.  The activation operand
+// always spans the whole chunk (A row r = block r of the chunk); a unit's
+// tiles use rows [row0, row0 + 16/U).
+template <int FMT, int R, int U>
 struct Chunk {
-    static constexpr int kTiles = kChunkBlocks / GemvFormat<FMT>::kBlocksPerTile;
+    static constexpr int kTiles = kChunkBlocks / GemvFormat<FMT>::kBlocksPerTile / U;
     uint4 c[kTiles][R][GemvFormat<FMT>::kCodeVecs];
     typename GemvFormat<FMT>::Scale sc[kTiles][R];
     float4 x[2];
 };
 
-template <int FMT, int R>
-__device__ __forceinline__ void load_chunk(Chunk<FMT, R>& ch, const void* __restrict__ codes_,
+template <int FMT, int R, int U>
+__device__ __forceinline__ void load_chunk(Chunk<FMT, R, U>& ch, const void* __restrict__ codes_,
                                            const void* __restrict__ scales_, std::uint32_t rt0, std::uint32_t NT,
-                                           std::uint32_t KT, std::uint32_t chunk, std::uint32_t lane,
+                                           std::uint32_t KT, std::uint32_t unit, std::uint32_t lane,
                                            const float* __restrict__ x, std::uint64_t nblocks) {
     using F = GemvFormat<FMT>;
     using Scale = typename F::Scale;
-    constexpr int T = Chunk<FMT, R>::kTiles;
+    constexpr int T = Chunk<FMT, R, U>::kTiles;
+    const std::uint32_t chunk = unit / U;
+    const std::uint32_t kt0 = unit * T;   // first k tile of the unit
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        // Tile (rt0 + r, chunk * T) as a wave-uniform base; lanes add their
-        // own 16-byte (codes) or scale-record offset.
-        const std::uint64_t tile0 = static_cast<std::uint64_t>(rt0 + r) * KT + static_cast<std::uint64_t>(chunk) * T;
+        // Tile (rt0 + r, kt0) as a wave-uniform base; lanes add their own
+        // 16-byte (codes) or scale-record offset.
+        const std::uint64_t tile0 = static_cast<std::uint64_t>(rt0 + r) * KT + kt0;
         const u32x4* cbase = static_cast<const u32x4*>(codes_) + tile0 * F::kCodeVecs * 64u;
         const Scale* sbase = static_cast<const Scale*>(scales_) + tile0 * 16u;
         const bool row_live = (rt0 + r) < NT;
 #pragma unroll
         for (int j = 0; j < T; ++j) {
-            const bool live = row_live && chunk * T + j < KT;
+            const bool live = row_live && kt0 + j < KT;
 #pragma unroll
             for (int v = 0; v < F::kCodeVecs; ++v) {
                 // Weight codes are read once per pass: non-temporal loads keep
@@ -86,9 +91,13 @@ __device__ __forceinline__ void load_chunk(Chunk<FMT, R>& ch, const void* __rest
             ch.sc[j][r] = live ? sbase[j * 16u + (lane & 15u)] : Scale{};
         }
     }
-    // A row r = lane % 16 holds block chunk*16 + r, elements 8*(lane/16)..+7.
+    // A row r = lane % 16 holds block chunk*16 + r, elements 8*(lane/16)..+7;
+    // only the unit's own rows are read.
+    constexpr std::uint32_t kUnitBlocks = kChunkBlocks / U;
+    const std::uint32_t row0 = (unit % U) * kUnitBlocks;
     const std::uint64_t kb = static_cast<std::uint64_t>(chunk) * kChunkBlocks + (lane & 15u);
-    if (kb < nblocks) {
+    const bool row_used = U == 1 || ((lane & 15u) - row0) < kUnitBlocks;
+    if (kb < nblocks && row_used) {
         const float4* src = reinterpret_cast<const float4*>(x + kb * 32u + 8u * (lane >> 4));
         ch.x[0] = src[0];
         ch.x[1] = src[1];
@@ -99,8 +108,8 @@ __device__ __forceinline__ void load_chunk(Chunk<FMT, R>& ch, const void* __rest
 }
 
 // Weight block j of a tile as the f16 B operand (exact integers).
-template <int FMT, int R>
-__device__ __forceinline__ half8v tile_block_codes(const Chunk<FMT, R>& ch, int t, int r, int j) {
+template <int FMT, int R, int U>
+__device__ __forceinline__ half8v tile_block_codes(const Chunk<FMT, R, U>& ch, int t, int r, int j) {
     if constexpr (FMT == kQ8_0) {
         const uint4 c = ch.c[t][r][0];
         half2v p0, p1, p2, p3;
@@ -120,10 +129,14 @@ __device__ __forceinline__ half8v tile_block_codes(const Chunk<FMT, R>& ch, int 
     }
 }
 
-template <int FMT, int R>
-__device__ __forceinline__ void compute_chunk(const Chunk<FMT, R>& ch, std::uint32_t lane, float4v (&acc)[R]) {
+template <int FMT, int R, int U>
+__device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U>& ch, std::uint32_t unit, std::uint32_t lane,
+                                              float4v (&acc)[R]) {
     using F = GemvFormat<FMT>;
-    constexpr int T = Chunk<FMT, R>::kTiles;
+    constexpr int T = Chunk<FMT, R, U>::kTiles;
+    // First A / D row of the unit: a multiple of 16 / U >= 4, so the D slot
+    // (row % 4) of each block is a compile-time constant.
+    const std::uint32_t row0 = (unit % U) * (kChunkBlocks / U);
     const float v[8] = {ch.x[0].x, ch.x[0].y, ch.x[0].z, ch.x[0].w, ch.x[1].x, ch.x[1].y, ch.x[1].z, ch.x[1].w};
     float amax = fmaxf(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))),
                        fmaxf(fmaxf(fabsf(v[4]), fabsf(v[5])), fmaxf(fabsf(v[6]), fabsf(v[7]))));
@@ -158,15 +171,16 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R>& ch, std::uint
         }
 #pragma unroll
         for (int j = 0; j < F::kBlocksPerTile; ++j) {
-            const int row = t * F::kBlocksPerTile + j;   // A / D row of this block
-            const int i = row & 3;
-            const bool mine = group == static_cast<std::uint32_t>(row >> 2);
-            const float inv_r = lane_value(inv, row);
+            const int rel = t * F::kBlocksPerTile + j;             // row within the unit
+            const std::uint32_t row = row0 + rel;                   // A / D row of this block
+            const int i = rel & 3;
+            const bool mine = group == (row >> 2);
+            const float inv_r = lane_value(inv, static_cast<int>(row));
             float sum_r = 0.0f;
-            if constexpr (FMT == kQ4_K) sum_r = lane_value(xsum, row);
+            if constexpr (FMT == kQ4_K) sum_r = lane_value(xsum, static_cast<int>(row));
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const half8v w = tile_block_codes<FMT, R>(ch, t, r, j);
+                const half8v w = tile_block_codes<FMT, R, U>(ch, t, r, j);
                 float4v p = mfma16x16x32(hi, w, float4v{0.0f, 0.0f, 0.0f, 0.0f});
                 p = mfma16x16x32(lo, w, p);
                 float updated;
@@ -190,29 +204,32 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R>& ch, std::uint
     }
 }
 
-constexpr int gemv_max_waves(int FMT, int R) { return FMT >= 0 && R >= 4 ? 4 : 8; }
+// Waves per workgroup: single-buffered one-tile waves fit 16 per CU.
+constexpr int gemv_max_waves(int R, int P) { return R >= 4 ? 4 : (R == 1 && P == 1 ? 16 : 8); }
 
 // Workgroup = W waves on the same R row tiles; the chunks of K are split
 // across the waves.  P = 2: each wave double-buffers whole chunks.  P = 1:
 // one chunk buffer, loaded and consumed in turn -- the lower register count
 // lets twice as many waves share a CU, which hides the load latency by
 // occupancy instead.
-template <int FMT, int R, int P>
-__global__ void __launch_bounds__(64 * gemv_max_waves(FMT, R))
+template <int FMT, int R, int P, int U>
+__global__ void __launch_bounds__(64 * gemv_max_waves(R, P))
 decode_gemv_kernel(const void* __restrict__ codes_, const void* __restrict__ scales_,
                    const float* __restrict__ x, const float* __restrict__ bias, float* __restrict__ y,
                    std::uint64_t K, std::uint64_t N, std::uint32_t NT, std::uint32_t KT) {
     extern __shared__ float wave_sums[];
-    using Ch = Chunk<FMT, R>;
+    using Ch = Chunk<FMT, R, U>;
     const std::uint32_t lane = threadIdx.x & 63u;
     // Wave-uniform: chunk indices, tile addresses and liveness stay scalar.
     const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const std::uint32_t W = blockDim.x >> 6;
     const std::uint32_t rt0 = blockIdx.x * R;
     const std::uint64_t nblocks = K / 32u;
-    const std::uint32_t chunks = static_cast<std::uint32_t>(ceil_div(KT, static_cast<std::uint64_t>(Ch::kTiles)));
-    const std::uint32_t c_begin = static_cast<std::uint32_t>((static_cast<std::uint64_t>(chunks) * wave) / W);
-    const std::uint32_t c_end = static_cast<std::uint32_t>((static_cast<std::uint64_t>(chunks) * (wave + 1u)) / W);
+    // Work units of Ch::kTiles k tiles (U per 16-block chunk), split over the waves.
+    const std::uint32_t chunks = static_cast<std::uint32_t>(ceil_div(KT, static_cast<std::uint64_t>(Ch::kTiles) * U));
+    const std::uint64_t units = static_cast<std::uint64_t>(chunks) * U;
+    const std::uint32_t c_begin = static_cast<std::uint32_t>((units * wave) / W);
+    const std::uint32_t c_end = static_cast<std::uint32_t>((units * (wave + 1u)) / W);
 
     float4v acc[R];
 #pragma unroll
@@ -221,18 +238,18 @@ decode_gemv_kernel(const void* __restrict__ codes_, const void* __restrict__ sca
     if constexpr (P == 1) {
         for (std::uint32_t c = c_begin; c < c_end; ++c) {
             Ch a;
-            load_chunk<FMT, R>(a, codes_, scales_, rt0, NT, KT, c, lane, x, nblocks);
-            compute_chunk<FMT, R>(a, lane, acc);
+            load_chunk<FMT, R, U>(a, codes_, scales_, rt0, NT, KT, c, lane, x, nblocks);
+            compute_chunk<FMT, R, U>(a, c, lane, acc);
         }
     } else {
         Ch a, b;
-        if (c_begin < c_end) load_chunk<FMT, R>(a, codes_, scales_, rt0, NT, KT, c_begin, lane, x, nblocks);
+        if (c_begin < c_end) load_chunk<FMT, R, U>(a, codes_, scales_, rt0, NT, KT, c_begin, lane, x, nblocks);
         for (std::uint32_t c = c_begin; c < c_end; c += 2u) {
-            if (c + 1u < c_end) load_chunk<FMT, R>(b, codes_, scales_, rt0, NT, KT, c + 1u, lane, x, nblocks);
-            compute_chunk<FMT, R>(a, lane, acc);
+            if (c + 1u < c_end) load_chunk<FMT, R, U>(b, codes_, scales_, rt0, NT, KT, c + 1u, lane, x, nblocks);
+            compute_chunk<FMT, R, U>(a, c, lane, acc);
             if (c + 1u >= c_end) break;
-            if (c + 2u < c_end) load_chunk<FMT, R>(a, codes_, scales_, rt0, NT, KT, c + 2u, lane, x, nblocks);
-            compute_chunk<FMT, R>(b, lane, acc);
+            if (c + 2u < c_end) load_chunk<FMT, R, U>(a, codes_, scales_, rt0, NT, KT, c + 2u, lane, x, nblocks);
+            compute_chunk<FMT, R, U>(b, c + 1u, lane, acc);
         }
     }
 
@@ -266,30 +283,35 @@ decode_gemv_kernel(const void* __restrict__ codes_, const void* __restrict__ sca
     }
 }
 
-template <int FMT, int R, int P>
+template <int FMT, int R, int P, int U>
 hipError_t launch_gemv_variant(const TilePlanes& p, const float* x, const float* bias, float* y,
                                std::uint32_t W, hipStream_t stream) {
-    if (W == 0u || W > static_cast<std::uint32_t>(gemv_max_waves(FMT, R))) return hipErrorInvalidConfiguration;
+    if (W == 0u || W > static_cast<std::uint32_t>(gemv_max_waves(R, P))) return hipErrorInvalidConfiguration;
     const dim3 grid(static_cast<unsigned>(ceil_div(p.nt, R)), 1, 1);
     const std::size_t lds = static_cast<std::size_t>(W - 1u) * R * 16u * sizeof(float);
-    decode_gemv_kernel<FMT, R, P><<<grid, 64u * W, lds, stream>>>(p.codes, p.scales, x, bias, y, p.k, p.n, p.nt,
-                                                                   p.kt);
+    decode_gemv_kernel<FMT, R, P, U><<<grid, 64u * W, lds, stream>>>(p.codes, p.scales, x, bias, y, p.k, p.n,
+                                                                      p.nt, p.kt);
     return hipGetLastError();
 }
 
 template <int FMT>
-hipError_t launch_gemv_fmt(const TilePlanes& p, const float* x, const float* bias, float* y, std::uint32_t R,
-                           std::uint32_t W, std::uint32_t P, hipStream_t s) {
+hipError_t launch_gemv_fmt(const TilePlanes& p, const float* x, const float* bias, float* y, const GemvShape& g,
+                           hipStream_t s) {
+    const std::uint32_t R = g.rows_per_wave, W = g.waves_per_group, P = g.depth;
     if (R == 1u) {
-        return P == 1u ? launch_gemv_variant<FMT, 1, 1>(p, x, bias, y, W, s)
-                       : launch_gemv_variant<FMT, 1, 2>(p, x, bias, y, W, s);
+        if (g.units_per_chunk == 2u) {
+            return P == 1u ? launch_gemv_variant<FMT, 1, 1, 2>(p, x, bias, y, W, s)
+                           : launch_gemv_variant<FMT, 1, 2, 2>(p, x, bias, y, W, s);
+        }
+        return P == 1u ? launch_gemv_variant<FMT, 1, 1, 1>(p, x, bias, y, W, s)
+                       : launch_gemv_variant<FMT, 1, 2, 1>(p, x, bias, y, W, s);
     }
     if (R == 2u) {
-        return P == 1u ? launch_gemv_variant<FMT, 2, 1>(p, x, bias, y, W, s)
-                       : launch_gemv_variant<FMT, 2, 2>(p, x, bias, y, W, s);
+        return P == 1u ? launch_gemv_variant<FMT, 2, 1, 1>(p, x, bias, y, W, s)
+                       : launch_gemv_variant<FMT, 2, 2, 1>(p, x, bias, y, W, s);
     }
-    return P == 1u ? launch_gemv_variant<FMT, 4, 1>(p, x, bias, y, W, s)
-                   : launch_gemv_variant<FMT, 4, 2>(p, x, bias, y, W, s);
+    return P == 1u ? launch_gemv_variant<FMT, 4, 1, 1>(p, x, bias, y, W, s)
+                   : launch_gemv_variant<FMT, 4, 2, 1>(p, x, bias, y, W, s);
 }
 
 } // namespace
@@ -298,37 +320,64 @@ GemvShape plan_decode_gemv(const TilePlanes& p, const DecodeTuning& tuning) {
     GemvShape g{};
     const std::uint32_t tiles_per_chunk = kChunkBlocks / (geometry_of(p.type).tile_k / 32u);
     const std::uint32_t chunks = static_cast<std::uint32_t>(ceil_div(p.kt, tiles_per_chunk));
-    // One row tile per wave (measured best for every Qwen2 shape).  Few row
-    // groups (< 2048, e.g. q|k|v, o, down): split the chunks of K over the
-    // waves of a workgroup until the grid holds about 8192 waves, each wave
-    // double-buffering its chunks.  Many row groups (gate|up, lm_head): four
-    // single-buffered waves per workgroup -- the register count halves and
-    // twice as many waves per CU keep the loads in flight (measured 2-5 %
-    // faster than double buffering on those shapes).
+    // One row tile per wave (measured best for every Qwen2 shape), then by
+    // grid width and K (Qwen2-7B Q8_0, HIP-graph replay):
+    //  * very wide grids (>= 4096 row groups, lm_head): four single-buffered
+    //    waves per workgroup -- half the registers of double buffering, so
+    //    twice the waves per CU keep the loads in flight;
+    //  * Q8_0 with short K (<= 8 chunks: q|k|v, o, gate|up): each chunk is
+    //    split into two units of half its tiles, so more, shorter waves share
+    //    a row tile (one unit per wave up to 16 waves, 8 single-buffered waves
+    //    on wide grids) -- 4-7 % faster on those shapes.  The 4-bit formats
+    //    are bound by instruction issue, and a unit split doubles the
+    //    activation-split work per weight byte (measured 4-5 % slower);
+    //  * otherwise (down; the 4-bit formats): the chunks split over up to 8
+    //    waves until the grid holds about 8192 waves, double-buffered when a
+    //    wave owns several.
     g.rows_per_wave = 1u;
     if (tuning.rows_per_wave == 1u || tuning.rows_per_wave == 2u || tuning.rows_per_wave == 4u) {
         g.rows_per_wave = tuning.rows_per_wave;
     }
-    const std::uint32_t cap = static_cast<std::uint32_t>(g.rows_per_wave >= 4u ? 4 : 8);
     const std::uint64_t groups = ceil_div(p.nt, g.rows_per_wave);
+    const bool huge = groups >= 4096u;
     const bool wide = groups >= 2048u;
-    std::uint64_t w = wide ? 4u : ceil_div(8192u, groups);
-    if (w > cap) w = cap;
-    if (w > chunks) w = chunks;
-    g.waves_per_group = w == 0u ? 1u : static_cast<std::uint32_t>(w);
-    if (tuning.waves_per_group != 0u) g.waves_per_group = tuning.waves_per_group < cap ? tuning.waves_per_group : cap;
-    // Chunks in flight per wave: one for wide grids and when no wave owns
-    // more than one chunk, else two.
-    g.depth = (wide || ceil_div(chunks, g.waves_per_group) <= 1u) ? 1u : 2u;
+    const bool short_k = chunks <= 8u;
+    g.units_per_chunk = (p.type == kQ8_0 && g.rows_per_wave == 1u && short_k && !huge) ? 2u : 1u;
+    const std::uint64_t units = static_cast<std::uint64_t>(chunks) * g.units_per_chunk;
+    std::uint64_t w;
+    if (huge) {
+        w = 4u;
+    } else if (g.units_per_chunk == 2u) {
+        w = wide ? 8u : units;
+    } else {
+        w = ceil_div(8192u, groups);
+    }
+    if (tuning.waves_per_group != 0u) w = tuning.waves_per_group;
+    if (w > units) w = units;
+    if (w == 0u) w = 1u;
+    // Units in flight per wave: one for wide grids and when no wave owns
+    // more than one unit, else two; the buffer count bounds the waves.
+    const auto depth_for = [&](std::uint64_t waves) -> std::uint32_t {
+        return (wide || ceil_div(units, waves) <= 1u) ? 1u : 2u;
+    };
+    std::uint32_t depth = depth_for(w);
+    for (int pass = 0; pass < 2; ++pass) {
+        const std::uint64_t cap = static_cast<std::uint64_t>(gemv_max_waves(static_cast<int>(g.rows_per_wave),
+                                                                            static_cast<int>(depth)));
+        if (w > cap) w = cap;
+        depth = depth_for(w);
+    }
+    g.waves_per_group = static_cast<std::uint32_t>(w);
+    g.depth = depth;
     return g;
 }
 
 hipError_t launch_decode_gemv(const TilePlanes& p, const float* x, const float* bias, float* y,
                               const GemvShape& g, hipStream_t stream) {
     switch (p.type) {
-    case kQ8_0: return launch_gemv_fmt<kQ8_0>(p, x, bias, y, g.rows_per_wave, g.waves_per_group, g.depth, stream);
-    case kQ4_0: return launch_gemv_fmt<kQ4_0>(p, x, bias, y, g.rows_per_wave, g.waves_per_group, g.depth, stream);
-    case kQ4_K: return launch_gemv_fmt<kQ4_K>(p, x, bias, y, g.rows_per_wave, g.waves_per_group, g.depth, stream);
+    case kQ8_0: return launch_gemv_fmt<kQ8_0>(p, x, bias, y, g, stream);
+    case kQ4_0: return launch_gemv_fmt<kQ4_0>(p, x, bias, y, g, stream);
+    case kQ4_K: return launch_gemv_fmt<kQ4_K>(p, x, bias, y, g, stream);
     default: return hipErrorInvalidValue;
     }
 }
