@@ -30,6 +30,21 @@ __device__ __forceinline__ float lane_value(float v, int src) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
 }
 
+template <int kCtrl>
+__device__ __forceinline__ float dpp_float(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, false));
+}
+
+// Maximum over the 64 lanes: within each 16-lane row by DPP (quad swaps,
+// half-row and row mirrors), then across the four rows by readlane.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_float<0xb1>(v));    // quad_perm [1, 0, 3, 2]
+    v = fmaxf(v, dpp_float<0x4e>(v));    // quad_perm [2, 3, 0, 1]
+    v = fmaxf(v, dpp_float<0x141>(v));   // row_half_mirror
+    v = fmaxf(v, dpp_float<0x140>(v));   // row_mirror
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+
 template <int FMT> struct GemvFormat;
 template <> struct GemvFormat<kQ8_0> {
     static constexpr int kBlocksPerTile = 2;
@@ -69,6 +84,24 @@ __device__ __forceinline__ void load_chunk(Chunk<FMT, R, U>& ch, const void* __r
     constexpr int T = Chunk<FMT, R, U>::kTiles;
     const std::uint32_t chunk = unit / U;
     const std::uint32_t kt0 = unit * T;   // first k tile of the unit
+    if (rt0 + R <= NT && kt0 + T <= KT) {
+        // Every tile live (all but the last unit of a ragged K): no fill.
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const std::uint64_t tile0 = static_cast<std::uint64_t>(rt0 + r) * KT + kt0;
+            const u32x4* cbase = static_cast<const u32x4*>(codes_) + tile0 * F::kCodeVecs * 64u;
+            const Scale* sbase = static_cast<const Scale*>(scales_) + tile0 * 16u;
+#pragma unroll
+            for (int j = 0; j < T; ++j) {
+#pragma unroll
+                for (int v = 0; v < F::kCodeVecs; ++v) {
+                    const u32x4 word = __builtin_nontemporal_load(cbase + (j * F::kCodeVecs + v) * 64u + lane);
+                    ch.c[j][r][v] = make_uint4(word.x, word.y, word.z, word.w);
+                }
+                ch.sc[j][r] = sbase[j * 16u + (lane & 15u)];
+            }
+        }
+    } else {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         // Tile (rt0 + r, kt0) as a wave-uniform base; lanes add their own
@@ -90,6 +123,7 @@ __device__ __forceinline__ void load_chunk(Chunk<FMT, R, U>& ch, const void* __r
             }
             ch.sc[j][r] = live ? sbase[j * 16u + (lane & 15u)] : Scale{};
         }
+    }
     }
     // A row r = lane % 16 holds block chunk*16 + r, elements 8*(lane/16)..+7;
     // only the unit's own rows are read.
@@ -138,10 +172,12 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U>& ch, std::u
     // (row % 4) of each block is a compile-time constant.
     const std::uint32_t row0 = (unit % U) * (kChunkBlocks / U);
     const float v[8] = {ch.x[0].x, ch.x[0].y, ch.x[0].z, ch.x[0].w, ch.x[1].x, ch.x[1].y, ch.x[1].z, ch.x[1].w};
+    // One power-of-two scale for the whole unit (all 64 lanes).  The f16
+    // hi + lo split keeps ~21 significant bits of every element, however far
+    // below the unit's maximum it lies, so the scale only guards the range.
     float amax = fmaxf(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))),
                        fmaxf(fmaxf(fabsf(v[4]), fabsf(v[5])), fmaxf(fabsf(v[6]), fabsf(v[7]))));
-    amax = fmaxf(amax, __shfl_xor(amax, 16));
-    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    amax = wave_max(amax);
     float s, inv;
     block_scale(amax, s, inv);
     half8v hi, lo;
@@ -154,16 +190,30 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U>& ch, std::u
     }
     const std::uint32_t group = lane >> 4;
 
+    // Sums in the scaled domain, multiplied by inv once at the end.  The
+    // blocks of one tile (Q4_K: of one half tile) own one lane group of D, so
+    // the tile's scale record is masked once per tile: lanes of other groups
+    // add 0 x (a finite product).
+    float4v cacc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) cacc[r] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-        // Q4_K: the tile is one super-block; its 8 sub-block scales per row.
-        float q4k_d[R], q4k_m[R];
+        const std::uint32_t first_row = row0 + static_cast<std::uint32_t>(t * F::kBlocksPerTile);
+        const bool own = group == (first_row >> 2);
+        typename F::Scale sc[R];
         std::uint32_t q4k_packed[R][3];
-        if constexpr (FMT == kQ4_K) {
+        std::uint32_t q4k_dm[R][2];   // Q4_K: f16 pair (d, dmin), for blocks 0-3 and 4-7
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                q4k_d[r] = half_bits_to_float(ch.sc[t][r].x & 0xffffu);
-                q4k_m[r] = half_bits_to_float(ch.sc[t][r].x >> 16);
+        for (int r = 0; r < R; ++r) {
+            if constexpr (FMT == kQ8_0) {
+                sc[r] = own ? ch.sc[t][r] : 0u;
+            } else if constexpr (FMT == kQ4_0) {
+                sc[r] = own ? ch.sc[t][r] : make_uint2(0u, 0u);
+            } else {
+                const bool own_hi = group == ((first_row >> 2) + 1u);
+                q4k_dm[r][0] = own ? ch.sc[t][r].x : 0u;
+                q4k_dm[r][1] = own_hi ? ch.sc[t][r].x : 0u;
                 q4k_packed[r][0] = ch.sc[t][r].y;
                 q4k_packed[r][1] = ch.sc[t][r].z;
                 q4k_packed[r][2] = ch.sc[t][r].w;
@@ -172,35 +222,37 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U>& ch, std::u
 #pragma unroll
         for (int j = 0; j < F::kBlocksPerTile; ++j) {
             const int rel = t * F::kBlocksPerTile + j;             // row within the unit
-            const std::uint32_t row = row0 + rel;                   // A / D row of this block
-            const int i = rel & 3;
-            const bool mine = group == (row >> 2);
-            const float inv_r = lane_value(inv, static_cast<int>(row));
+            const int i = rel & 3;                                  // D slot of this block
             float sum_r = 0.0f;
-            if constexpr (FMT == kQ4_K) sum_r = lane_value(xsum, static_cast<int>(row));
+            if constexpr (FMT == kQ4_K) sum_r = lane_value(xsum, static_cast<int>(row0) + rel);
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const half8v w = tile_block_codes<FMT, R, U>(ch, t, r, j);
                 float4v p = mfma16x16x32(hi, w, float4v{0.0f, 0.0f, 0.0f, 0.0f});
                 p = mfma16x16x32(lo, w, p);
-                float updated;
                 if constexpr (FMT == kQ8_0) {
-                    const float d = half_bits_to_float((ch.sc[t][r] >> (16 * j)) & 0xffffu);
-                    updated = fmaf(d * inv_r, p[i], acc[r][i]);
+                    const float d = half_bits_to_float((sc[r] >> (16 * j)) & 0xffffu);
+                    cacc[r][i] = fmaf(d, p[i], cacc[r][i]);
                 } else if constexpr (FMT == kQ4_0) {
-                    const std::uint32_t sw = j < 2 ? ch.sc[t][r].x : ch.sc[t][r].y;
+                    const std::uint32_t sw = j < 2 ? sc[r].x : sc[r].y;
                     const float d = half_bits_to_float((sw >> (16 * (j & 1))) & 0xffffu);
-                    updated = fmaf(d * inv_r, p[i], acc[r][i]);
+                    cacc[r][i] = fmaf(d, p[i], cacc[r][i]);
                 } else {
                     std::uint32_t s6 = 0, m6 = 0;
                     q4k_scale_min(q4k_packed[r], static_cast<std::uint32_t>(j), s6, m6);
-                    const float dj = q4k_d[r] * static_cast<float>(s6);
-                    const float mj = q4k_m[r] * static_cast<float>(m6);
-                    updated = fmaf(-mj, sum_r, fmaf(dj * inv_r, p[i], acc[r][i]));
+                    const std::uint32_t dm = q4k_dm[r][j >> 2];
+                    const float dj = half_bits_to_float(dm & 0xffffu) * static_cast<float>(s6);
+                    const float mj = half_bits_to_float(dm >> 16) * static_cast<float>(m6);
+                    cacc[r][i] = fmaf(dj, p[i], cacc[r][i]);
+                    acc[r][i] = fmaf(-mj, sum_r, acc[r][i]);
                 }
-                acc[r][i] = mine ? updated : acc[r][i];
             }
         }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[r][i] = fmaf(inv, cacc[r][i], acc[r][i]);
     }
 }
 
