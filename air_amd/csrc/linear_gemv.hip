@@ -182,11 +182,16 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U>& ch, std::u
     block_scale(amax, s, inv);
     half8v hi, lo;
     split8(v, s, hi, lo);
-    float xsum = 0.0f;
+    // Q4_K: scaled block sums for the dmin term from one MFMA pair against an
+    // all-ones B: D row r = sum of block r, in every column -- the very lanes
+    // and slot where block r's products land.
+    float4v xs{0.0f, 0.0f, 0.0f, 0.0f};
     if constexpr (FMT == kQ4_K) {
-        xsum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-        xsum += __shfl_xor(xsum, 16);
-        xsum += __shfl_xor(xsum, 32);
+        half8v ones;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ones[e] = static_cast<_Float16>(1.0f);
+        xs = mfma16x16x32(hi, ones, xs);
+        xs = mfma16x16x32(lo, ones, xs);
     }
     const std::uint32_t group = lane >> 4;
 
@@ -223,8 +228,6 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U>& ch, std::u
         for (int j = 0; j < F::kBlocksPerTile; ++j) {
             const int rel = t * F::kBlocksPerTile + j;             // row within the unit
             const int i = rel & 3;                                  // D slot of this block
-            float sum_r = 0.0f;
-            if constexpr (FMT == kQ4_K) sum_r = lane_value(xsum, static_cast<int>(row0) + rel);
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const half8v w = tile_block_codes<FMT, R, U>(ch, t, r, j);
@@ -243,8 +246,7 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U>& ch, std::u
                     const std::uint32_t dm = q4k_dm[r][j >> 2];
                     const float dj = half_bits_to_float(dm & 0xffffu) * static_cast<float>(s6);
                     const float mj = half_bits_to_float(dm >> 16) * static_cast<float>(m6);
-                    cacc[r][i] = fmaf(dj, p[i], cacc[r][i]);
-                    acc[r][i] = fmaf(-mj, sum_r, acc[r][i]);
+                    cacc[r][i] = fmaf(-mj, xs[i], fmaf(dj, p[i], cacc[r][i]));
                 }
             }
         }
