@@ -83,13 +83,21 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_kernel(SkinnyArgs a) {
 #pragma unroll
         for (int t = 0; t < MT; ++t) acc[j][t] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Activation staging: step s covers blocks 2s, 2s+1, contiguous in the workspace.
-    u32x4 xr[XF ? 1 : kChunks];
-    float4v mr = {0.f, 0.f, 0.f, 0.f};
+    // Activation staging: step s covers blocks 2s, 2s+1, contiguous in the
+    // workspace.  Two register slots: the activations of step s + 2 are
+    // loaded while step s computes, so their latency spans two steps.  One
+    // slot (load one step ahead) for the Q8_0 f32 variant with two or more
+    // activation tiles, where the second slot would cost a wave per SIMD.
+    constexpr int kXSlots = (XF && FMT == kQ8_0 && MT >= 2) ? 1 : 2;
+    u32x4 xr[kXSlots][XF ? 1 : kChunks];
+    float4v mr[kXSlots];
+#pragma unroll
+    for (int i = 0; i < kXSlots; ++i) mr[i] = float4v{0.f, 0.f, 0.f, 0.f};
     // XF: wave w splits fragments w, w + 4, ...: fragment c is block c / MT,
     // activation tile c % MT; lane l holds row l % 16, elements 8 (l / 16)..+7.
-    float4 xf[XF ? kFragsPerWave : 1][2];
-    const auto load_x = [&](std::uint32_t s) __attribute__((always_inline)) {
+    float4 xfs[kXSlots][XF ? kFragsPerWave : 1][2];
+    const auto load_x = [&](std::uint32_t s, int slot) __attribute__((always_inline)) {
+        auto& xf = xfs[slot];
         if constexpr (XF) {
 #pragma unroll
             for (unsigned r = 0; r < kFragsPerWave; ++r) {
@@ -107,13 +115,14 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_kernel(SkinnyArgs a) {
         } else {
             const u32x4* src = reinterpret_cast<const u32x4*>(a.xs) + static_cast<std::uint64_t>(s) * (2u * MT * 2u * 64u);
 #pragma unroll
-            for (unsigned j = 0; j < kChunks; ++j) xr[j] = src[tid + kThreads * j];
+            for (unsigned j = 0; j < kChunks; ++j) xr[slot][j] = src[tid + kThreads * j];
             if constexpr (kSums) {
-                if (tid < 2u * kMp / 4u) mr = reinterpret_cast<const float4v*>(a.block_sums + static_cast<std::uint64_t>(s) * 2u * kMp)[tid];
+                if (tid < 2u * kMp / 4u) mr[slot] = reinterpret_cast<const float4v*>(a.block_sums + static_cast<std::uint64_t>(s) * 2u * kMp)[tid];
             }
         }
     };
-    const auto store_x = [&](unsigned buf) __attribute__((always_inline)) {
+    const auto store_x = [&](unsigned buf, int slot) __attribute__((always_inline)) {
+        auto& xf = xfs[slot];
         if constexpr (XF) {
 #pragma unroll
             for (unsigned r = 0; r < kFragsPerWave; ++r) {
@@ -143,9 +152,9 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_kernel(SkinnyArgs a) {
             }
         } else {
 #pragma unroll
-            for (unsigned j = 0; j < kChunks; ++j) xa[buf][tid + kThreads * j] = xr[j];
+            for (unsigned j = 0; j < kChunks; ++j) xa[buf][tid + kThreads * j] = xr[slot][j];
             if constexpr (kSums) {
-                if (tid < 2u * kMp / 4u) sm[buf][tid] = mr;
+                if (tid < 2u * kMp / 4u) sm[buf][tid] = mr[slot];
             }
         }
     };
@@ -157,10 +166,16 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_kernel(SkinnyArgs a) {
             load_step<FMT, true>(a.codes, a.scales, rt, a.kt, s, lane, rt < a.nt, dst[j]);
         }
     };
-    const auto step = [&](std::uint32_t s, StepCodes<FMT>(&cur)[TN]) __attribute__((always_inline)) {
+    // slot: the register slot of step s's activations ((s - s_begin) % 2 with
+    // two slots).
+    const auto step = [&](std::uint32_t s, StepCodes<FMT>(&cur)[TN], int slot) __attribute__((always_inline)) {
         const unsigned buf = (s - s_begin) & 1u;
         const bool more = s + 1u < s_end;
-        if (more) load_x(s + 1u);
+        if constexpr (kXSlots == 2) {
+            if (s + 2u < s_end) load_x(s + 2u, slot);   // step s's slot is free: staged already
+        } else {
+            if (more) load_x(s + 1u, 0);
+        }
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             half8v w[TN];
@@ -193,23 +208,26 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_kernel(SkinnyArgs a) {
                 }
             }
         }
-        if (more) store_x(buf ^ 1u);
+        if (more) store_x(buf ^ 1u, kXSlots == 2 ? slot ^ 1 : 0);
         __syncthreads();
     };
 
     if (s_begin < s_end) {
-        load_x(s_begin);
+        load_x(s_begin, 0);
         load_w(wa, s_begin);
-        if (s_begin + 1u < s_end) load_w(wb, s_begin + 1u);
-        store_x(0);
+        if (s_begin + 1u < s_end) {
+            if constexpr (kXSlots == 2) load_x(s_begin + 1u, 1);
+            load_w(wb, s_begin + 1u);
+        }
+        store_x(0, 0);
     }
     __syncthreads();
     std::uint32_t s = s_begin;
     for (; s + 1u < s_end; s += 2u) {
-        step(s, wa);
-        step(s + 1u, wb);
+        step(s, wa, 0);
+        step(s + 1u, wb, 1);
     }
-    if (s < s_end) step(s, wa);
+    if (s < s_end) step(s, wa, 0);
 
     // D[row = activation row][col = weight row]: lane holds rows 4(l/16)+i of
     // column l%16; the rows' power-of-two activation scales are undone here.
