@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <vector>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -59,8 +60,12 @@ struct air_hip_context {
     void* attention_scratch{nullptr};       // attention scores, grown on demand
     std::uint64_t attention_scratch_bytes{0};
     // Bumped whenever a context-owned buffer is (re)allocated: launches
-    // recorded into a graph stay valid while it is unchanged.
+    // recorded into a graph use the current buffers while it is unchanged.
     std::uint64_t generation{0};
+    // Buffers replaced by a larger one.  They are freed only with the
+    // context: a graph captured before the growth still holds their address.
+    // Growth is geometric, so they total less than twice the live size.
+    std::vector<void*> retired;
 };
 
 struct air_hip_matrix {
@@ -117,41 +122,35 @@ std::uint64_t resident_plane_bytes(const TilePlanes& p, std::uint64_t& scale_byt
     return tiles * geo.code_tile_bytes;
 }
 
-int ensure_workspace(air_hip_context* ctx, std::uint64_t bytes) {
-    if (bytes <= ctx->workspace_bytes) return AIR_HIP_OK;
-    if (ctx->workspace) {
-        // The old workspace may still be read by queued kernels.
-        const hipError_t sync = hipStreamSynchronize(ctx->stream);
-        if (sync != hipSuccess) return hip_fail(sync, "hipStreamSynchronize(workspace growth)");
-        (void)hipFree(ctx->workspace);
-        ctx->workspace = nullptr;
-        ctx->workspace_bytes = 0;
-    }
+// Replaces the context buffer *buf (of *size bytes) by one of at least
+// `bytes`, grown geometrically.  The old buffer is retired, not freed: queued
+// kernels and graphs captured earlier may still use it.  keep: the old
+// contents are copied over (stream-ordered), e.g. loaded activations.
+int grow_buffer(air_hip_context* ctx, void** buf, std::uint64_t* size, std::uint64_t bytes, const char* what,
+                bool keep = false) {
+    if (bytes <= *size) return AIR_HIP_OK;
+    const std::uint64_t grown = std::max<std::uint64_t>(bytes, *size + *size / 2);
     void* p = nullptr;
-    const hipError_t err = hipMalloc(&p, bytes);
-    if (err != hipSuccess) return hip_fail(err, "hipMalloc(workspace)");
-    ctx->workspace = p;
-    ctx->workspace_bytes = bytes;
+    hipError_t err = hipMalloc(&p, grown);
+    if (err == hipSuccess && keep && *buf) err = hipMemcpyAsync(p, *buf, *size, hipMemcpyDeviceToDevice, ctx->stream);
+    if (err != hipSuccess) {
+        (void)hipFree(p);
+        return fail(AIR_HIP_INTERNAL_ERROR, "hipMalloc(%s): %s", what, hipGetErrorString(err));
+    }
+    if (*buf) ctx->retired.push_back(*buf);
+    *buf = p;
+    *size = grown;
     ++ctx->generation;
     return AIR_HIP_OK;
 }
 
+int ensure_workspace(air_hip_context* ctx, std::uint64_t bytes) {
+    // Keeps activations loaded before a later reserve.
+    return grow_buffer(ctx, &ctx->workspace, &ctx->workspace_bytes, bytes, "workspace", ctx->loaded_rows != 0);
+}
+
 int ensure_prefill_workspace(air_hip_context* ctx, std::uint64_t bytes) {
-    if (bytes <= ctx->prefill_workspace_bytes) return AIR_HIP_OK;
-    if (ctx->prefill_workspace) {
-        const hipError_t sync = hipStreamSynchronize(ctx->stream);
-        if (sync != hipSuccess) return hip_fail(sync, "hipStreamSynchronize(prefill workspace growth)");
-        (void)hipFree(ctx->prefill_workspace);
-        ctx->prefill_workspace = nullptr;
-        ctx->prefill_workspace_bytes = 0;
-    }
-    void* p = nullptr;
-    const hipError_t err = hipMalloc(&p, bytes);
-    if (err != hipSuccess) return hip_fail(err, "hipMalloc(prefill workspace)");
-    ctx->prefill_workspace = p;
-    ctx->prefill_workspace_bytes = bytes;
-    ++ctx->generation;
-    return AIR_HIP_OK;
+    return grow_buffer(ctx, &ctx->prefill_workspace, &ctx->prefill_workspace_bytes, bytes, "prefill workspace");
 }
 
 // Prefill linear: x [rows][k] -> y [rows][n] on the f16 MFMA GEMM.
@@ -199,24 +198,12 @@ int run_skinny_x(air_hip_context* ctx, const air_hip_matrix* m, const float* x, 
 }
 
 int ensure_split_buffers(air_hip_context* ctx, std::uint64_t partial_bytes, std::uint32_t counters) {
-    if (partial_bytes > ctx->split_partials_bytes || counters > ctx->split_counter_count) {
-        const hipError_t sync = hipStreamSynchronize(ctx->stream);
-        if (sync != hipSuccess) return hip_fail(sync, "hipStreamSynchronize(split buffer growth)");
-    }
-    if (partial_bytes > ctx->split_partials_bytes) {
-        (void)hipFree(ctx->split_partials);
-        ctx->split_partials = nullptr;
-        ctx->split_partials_bytes = 0;
-        const hipError_t err = hipMalloc(&ctx->split_partials, partial_bytes);
-        if (err != hipSuccess) return hip_fail(err, "hipMalloc(split partials)");
-        ctx->split_partials_bytes = partial_bytes;
-        ++ctx->generation;
-    }
+    int rc = grow_buffer(ctx, &ctx->split_partials, &ctx->split_partials_bytes, partial_bytes, "split partials");
+    if (rc != AIR_HIP_OK) return rc;
     if (counters > ctx->split_counter_count) {
-        (void)hipFree(ctx->split_counters);
-        ctx->split_counters = nullptr;
-        ctx->split_counter_count = 0;
-        const std::uint32_t count = counters < 4096u ? 4096u : counters;
+        // Counters start at zero and every launch leaves them at zero.
+        const std::uint32_t count = std::max<std::uint32_t>(counters < 4096u ? 4096u : counters,
+                                                            ctx->split_counter_count + ctx->split_counter_count / 2);
         void* p = nullptr;
         hipError_t err = hipMalloc(&p, count * sizeof(std::uint32_t));
         if (err == hipSuccess) err = hipMemset(p, 0, count * sizeof(std::uint32_t));
@@ -224,6 +211,7 @@ int ensure_split_buffers(air_hip_context* ctx, std::uint64_t partial_bytes, std:
             (void)hipFree(p);
             return hip_fail(err, "hipMalloc(split counters)");
         }
+        if (ctx->split_counters) ctx->retired.push_back(ctx->split_counters);
         ctx->split_counters = static_cast<std::uint32_t*>(p);
         ctx->split_counter_count = count;
         ++ctx->generation;
@@ -307,6 +295,7 @@ int air_hip_context_destroy(air_hip_context* ctx) {
         if (ctx->prefill_workspace) (void)hipFree(ctx->prefill_workspace);
         if (ctx->bound_scratch) (void)hipFree(ctx->bound_scratch);
         if (ctx->attention_scratch) (void)hipFree(ctx->attention_scratch);
+        for (void* p : ctx->retired) (void)hipFree(p);
     }
     delete ctx;
     return AIR_HIP_OK;
@@ -742,21 +731,9 @@ int check_heads(const air_hip_kv_layout* kv, uint32_t q_heads, uint32_t kv_heads
     return AIR_HIP_OK;
 }
 // Grows the attention scratch to at least `bytes` (geometrically, so a decode
-// loop whose key count grows by one per step reallocates rarely).  Waits for
-// the stream first: queued kernels may still read the old buffer.
+// loop whose key count grows by one per step reallocates rarely).
 int ensure_attention_scratch(air_hip_context* ctx, uint64_t bytes) {
-    if (bytes <= ctx->attention_scratch_bytes) return AIR_HIP_OK;
-    const uint64_t grown = std::max<uint64_t>(bytes, ctx->attention_scratch_bytes + ctx->attention_scratch_bytes / 2);
-    const hipError_t sync = hipStreamSynchronize(ctx->stream);
-    if (sync != hipSuccess) return hip_fail(sync, "hipStreamSynchronize(attention scratch growth)");
-    (void)hipFree(ctx->attention_scratch);
-    ctx->attention_scratch = nullptr;
-    ctx->attention_scratch_bytes = 0;
-    const hipError_t err = hipMalloc(&ctx->attention_scratch, grown);
-    if (err != hipSuccess) return hip_fail(err, "hipMalloc(attention scratch)");
-    ctx->attention_scratch_bytes = grown;
-    ++ctx->generation;
-    return AIR_HIP_OK;
+    return grow_buffer(ctx, &ctx->attention_scratch, &ctx->attention_scratch_bytes, bytes, "attention scratch");
 }
 static_assert(sizeof(AttentionTile) == sizeof(air_hip_attention_tile), "tile layouts agree");
 } // namespace

@@ -98,9 +98,13 @@ typedef struct air_hip_stats {
     uint64_t prefill_linear_calls;
     uint64_t decode_rows;
     uint64_t prefill_rows;
-    /* Bumped whenever the context (re)allocates a workspace or scratch
-     * buffer: launches captured into a HIP graph stay valid while it is
-     * unchanged.  No counterpart in the reference. */
+    /* Bumped whenever the context grows a workspace or scratch buffer:
+     * launches captured into a HIP graph use the current buffers while it is
+     * unchanged.  A buffer replaced by a larger one is kept (not freed) until
+     * the context is destroyed, so a graph captured before the growth still
+     * replays on valid memory -- but shares it with no later launch.  Growth
+     * is geometric (at least 1.5x), so kept buffers total less than twice the
+     * live ones.  No counterpart in the reference. */
     uint64_t workspace_generation;
 } air_hip_stats;
 

@@ -196,3 +196,53 @@ def test_skinny_shapes_agree(torch_cuda, hip_ctx, type_id, k, n):
     finally:
         hip_ctx.set_decode_path(0)
         mat.release()
+
+
+def test_graph_replay_after_workspace_growth(torch_cuda):
+    """A HIP graph captured before the context grows its K-split partials
+    replays on the buffer it captured (kept, not freed, until the context is
+    destroyed) and still produces the oracle's result; the workspace
+    generation records the growth.  A context of its own, so the partials
+    start at the captured size."""
+    torch = torch_cuda
+    dev = torch.device("cuda:0")
+    main = torch.cuda.current_stream(dev)
+    type_id, k, n, m = capi.TYPE_Q8_0, 1024, 512, 8
+    canon = helpers.weights(type_id, k, n, seed=77)
+    x = helpers.activations(m, k, seed=78)
+    want = oracle.linear(type_id, canon, k, n, x)
+    ctx = capi.Context(0, main.cuda_stream)
+    mat = capi.Matrix(ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    graph = None
+    try:
+        xd = _dev(torch, x)
+        y = torch.zeros((m, n), dtype=torch.float32, device=dev)
+        ctx.set_decode_path(2, 1, 2)              # skinny, K split over 2 workgroups
+        mat.linear(xd, y, m)
+        torch.cuda.synchronize()
+        gen = ctx.stats()["workspace_generation"]
+        capture = torch.cuda.Stream(dev)
+        ctx.set_stream(capture.cuda_stream)
+        graph = torch.cuda.CUDAGraph()
+        try:
+            with torch.cuda.graph(graph, stream=capture):
+                mat.linear(xd, y, m)
+        finally:
+            ctx.set_stream(main.cuda_stream)
+        assert ctx.stats()["workspace_generation"] == gen
+        ctx.set_decode_path(2, 1, 8)              # four times the partials: the buffer grows
+        y2 = torch.zeros((m, n), dtype=torch.float32, device=dev)
+        mat.linear(xd, y2, m)
+        torch.cuda.synchronize()
+        assert ctx.stats()["workspace_generation"] > gen
+        assert helpers.rel_l2(y2.cpu().numpy(), want) <= DECODE_TOL
+        for _ in range(3):
+            y.fill_(float("nan"))
+            graph.replay()
+            torch.cuda.synchronize()
+            assert helpers.rel_l2(y.cpu().numpy(), want) <= DECODE_TOL
+    finally:
+        torch.cuda.synchronize()
+        graph = None                              # before the context frees its kept buffers
+        mat.release()
+        ctx.close()
