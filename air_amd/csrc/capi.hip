@@ -621,11 +621,12 @@ int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* m, const float* x
         // Measured on the Qwen2-7B shapes (M = 2..16): the single-launch fused
         // kernel wins for small square matrices (o: N, K <= 4096) and for very
         // large ones at M <= 4; the skinny kernel everywhere else (down, with
-        // its long K, by 10-30 %).
+        // its long K, by 10-30 %) and for Q4_K (o at M = 16: 25 %).
         const std::uint64_t weight_bytes = static_cast<std::uint64_t>(m->planes.nt) * m->planes.kt *
                                            geometry_of(m->planes.type).code_tile_bytes;
-        const bool prefer_fused = (m->planes.n <= 4096u && m->planes.k <= 4096u) ||
-                                  (rows <= 4u && weight_bytes >= (256ull << 20));
+        const bool prefer_fused = m->planes.type != kQ4_K &&
+                                  ((m->planes.n <= 4096u && m->planes.k <= 4096u) ||
+                                   (rows <= 4u && weight_bytes >= (256ull << 20)));
         if (ctx->decode_path == 2u || (ctx->decode_path == 0u && !prefer_fused)) {
             return run_skinny_x(ctx, m, x, y, bias, rows);
         }

@@ -407,13 +407,17 @@ SkinnyShape plan_skinny(const TilePlanes& p, std::uint32_t m, std::uint32_t tile
     s.steps = static_cast<std::uint32_t>(p.kp / kStepK);
     std::uint32_t splits = k_splits;
     if (splits == 0u) {
-        // Up to about four workgroups per CU, keeping at least 4 steps per
-        // split and the partials' round trip below the weight bytes.
+        // Up to about four workgroups per CU (two with three or four
+        // activation tiles, whose registers and LDS halve the resident
+        // workgroups), keeping at least 4 steps per split and the partials'
+        // round trip (mostly cache-resident) within twice the weight bytes.
+        // Measured on the Qwen2-7B shapes at M = 16..64 in all three formats.
         const std::uint64_t weight_bytes = static_cast<std::uint64_t>(p.nt) * p.kt * geometry_of(p.type).code_tile_bytes;
         const std::uint64_t partial_trip = 2u * static_cast<std::uint64_t>(m) * p.n * 4u;
+        const std::uint64_t max_groups = s.mt <= 2u ? 1024u : 512u;
         splits = 1u;
-        while (static_cast<std::uint64_t>(s.groups) * splits * 2u <= 1024u && s.steps / (splits * 2u) >= 4u &&
-               partial_trip * splits * 2u <= weight_bytes) {
+        while (static_cast<std::uint64_t>(s.groups) * splits * 2u <= max_groups && s.steps / (splits * 2u) >= 4u &&
+               partial_trip * splits * 2u <= 2u * weight_bytes) {
             splits *= 2u;
         }
     }
