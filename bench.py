@@ -145,6 +145,7 @@ def traffic_probe(ms) -> int:
     dst.copy_(src)
     torch.cuda.synchronize()
     for m in ms:
+        dst[:64].copy_(src[:64])        # separator: a tiny copy before each M's launches
         for mat in mats:
             mat.linear(x, y, m)
         torch.cuda.synchronize()
@@ -158,9 +159,9 @@ COPY_PROBE_BYTES = 256 * 1024 * 1024
 
 
 def counter_summary(fetch_csv: str, write_csv: str, ms) -> dict:
-    """Bytes per launch of the probe's gate|up linears from two rocprofv3
-    counter CSVs, each counter scaled by its reading on the copy kernel
-    (which reads and writes COPY_PROBE_BYTES exactly)."""
+    """Bytes per gate|up linear call (all of its kernels) of the probe from
+    two rocprofv3 counter CSVs, each counter scaled by its reading on the
+    calibration copy (which reads and writes COPY_PROBE_BYTES exactly)."""
     import csv
 
     def per_dispatch(path, counter):
@@ -174,15 +175,22 @@ def counter_summary(fetch_csv: str, write_csv: str, ms) -> dict:
         return rows
 
     out = {}
+    calls_per_m = 4
     for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
         rows = per_dispatch(path, counter)
-        copy = [v for _, name, v in rows if "copyBuffer" in name]
-        gemv = [v for _, name, v in rows if "air_hip::" in name and "decode_" in name]
-        factor = COPY_PROBE_BYTES / (copy[-1] * 1024.0)     # counter is in KiB
-        per_m = len(gemv) // len(ms)
-        for i, m in enumerate(ms):
-            vals = gemv[i * per_m:(i + 1) * per_m]
-            out.setdefault(str(m), {})[counter] = sum(vals) / len(vals) * 1024.0 * factor
+        copies = [i for i, (_, name, _) in enumerate(rows) if "copyBuffer" in name]
+        calib = max(copies, key=lambda i: rows[i][2])          # the 256 MiB copy
+        factor = COPY_PROBE_BYTES / (rows[calib][2] * 1024.0)  # counter is in KiB
+        # Each M's linears (every kernel of the library: split, GEMV or
+        # skinny, reduction) follow one small separator copy.
+        separators = [i for i in copies if i > calib]
+        if len(separators) != len(ms):
+            raise SystemExit(f"expected {len(ms)} separator copies, found {len(separators)}")
+        bounds = separators + [len(rows)]
+        for j, m in enumerate(ms):
+            vals = [v for _, name, v in rows[bounds[j] + 1:bounds[j + 1]] if "air_hip::" in name]
+            out.setdefault(str(m), {})[counter] = sum(vals) / calls_per_m * 1024.0 * factor
+            out[str(m)].setdefault("kernels_per_call", len(vals) / calls_per_m)
         out.setdefault("_factors", {})[counter] = factor
     for m in ms:
         d = out[str(m)]
