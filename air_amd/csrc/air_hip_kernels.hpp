@@ -163,6 +163,12 @@ hipError_t launch_rope(float* qkv, std::uint64_t stride, std::uint32_t m, const 
 hipError_t launch_kv_append(const KvLayout& kv, const float* qkv, std::uint64_t stride, std::uint64_t q_width,
                             std::uint32_t m, const std::int32_t* positions, const std::int32_t* tables,
                             std::uint32_t layer, hipStream_t stream);
+// launch_rope then launch_kv_append in one launch (same results).
+hipError_t launch_rope_kv_append(const KvLayout& kv, float* qkv, std::uint64_t stride, std::uint64_t q_width,
+                                 std::uint32_t m, const std::int32_t* positions, const std::int32_t* tables,
+                                 std::uint32_t layer, std::uint32_t q_heads, std::uint32_t kv_heads,
+                                 std::uint32_t head_dim, std::uint32_t rope_dims, const void* table,
+                                 std::uint64_t table_positions, hipStream_t stream);
 hipError_t launch_attention(const KvLayout& kv, const float* qkv, std::uint64_t stride, std::uint32_t m,
                             const std::int32_t* positions, const std::int32_t* tables, std::uint32_t layer,
                             std::uint32_t q_heads, std::uint32_t kv_heads, std::uint32_t head_dim, double* scratch,

@@ -154,6 +154,78 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(KvGeometry g, const
     }
 }
 
+// RoPE of the q and k heads and the KV append in one pass (one workgroup
+// column per row): the same arithmetic as rope_kernel followed by
+// kv_append_kernel.  A row whose position lies outside the table is not
+// rotated; a row without a valid page slot is rotated but not stored.
+__global__ __launch_bounds__(kThreads) void rope_kv_append_kernel(
+    KvGeometry g, float* __restrict__ qkv, std::uint64_t stride, std::uint64_t q_width, std::uint32_t m,
+    const std::int32_t* __restrict__ positions, const std::int32_t* __restrict__ tables, std::uint32_t layer,
+    std::uint32_t q_heads, std::uint32_t kv_heads, std::uint32_t head_dim, std::uint32_t rope_dims,
+    const float2* __restrict__ table, std::uint64_t table_positions) {
+#pragma clang fp contract(off)
+    const std::uint32_t r = blockIdx.y;
+    if (r >= m) return;
+    const std::int32_t pos = positions[r];
+    const bool rotate = pos >= 0 && static_cast<std::uint64_t>(pos) < table_positions;
+    const std::int32_t* ptable = tables + static_cast<std::uint64_t>(r) * g.max_pages;
+    float* kd = kv_slot(g, ptable, layer, static_cast<std::uint64_t>(pos), false);
+    float* vd = kv_slot(g, ptable, layer, static_cast<std::uint64_t>(pos), true);
+    if (!vd) kd = nullptr;  // both or neither, as the separate append
+    float* row = qkv + static_cast<std::uint64_t>(r) * stride;
+    float* krow = row + q_width;
+    const std::uint32_t half = rope_dims / 2u;
+    const std::uint32_t tail = head_dim - rope_dims;             // k dims past the rotary part
+    const std::uint64_t q_items = static_cast<std::uint64_t>(q_heads) * half;
+    const std::uint64_t k_items = static_cast<std::uint64_t>(kv_heads) * (half + tail);
+    const std::uint64_t total = q_items + k_items + g.kv_width;  // + the v row
+    for (std::uint64_t idx = blockIdx.x * static_cast<std::uint64_t>(kThreads) + threadIdx.x; idx < total;
+         idx += static_cast<std::uint64_t>(gridDim.x) * kThreads) {
+        if (idx < q_items + k_items) {
+            float* base;
+            std::uint32_t i;
+            float* dst = nullptr;                                  // the k head in the pool
+            if (idx < q_items) {
+                base = row + (idx / half) * head_dim;
+                i = static_cast<std::uint32_t>(idx % half);
+            } else {
+                const std::uint64_t e = idx - q_items;
+                const std::uint32_t h = static_cast<std::uint32_t>(e / (half + tail));
+                const std::uint32_t j = static_cast<std::uint32_t>(e % (half + tail));
+                base = krow + static_cast<std::uint64_t>(h) * head_dim;
+                if (kd) dst = kd + static_cast<std::uint64_t>(h) * head_dim;
+                if (j >= half) {                                  // unrotated tail dim
+                    const std::uint32_t t = rope_dims + (j - half);
+                    if (dst) dst[t] = base[t];
+                    continue;
+                }
+                i = j;
+            }
+            const float first = base[i];
+            const float second = base[i + half];
+            float lo = first, hi = second;
+            if (rotate) {
+                const float2 cs = table[static_cast<std::uint64_t>(pos) * half + i];
+                const float a = first * cs.x;
+                const float b = second * cs.y;
+                const float c = first * cs.y;
+                const float d = second * cs.x;
+                lo = a - b;
+                hi = c + d;
+                base[i] = lo;
+                base[i + half] = hi;
+            }
+            if (dst) {
+                dst[i] = lo;
+                dst[i + half] = hi;
+            }
+        } else if (vd) {
+            const std::uint64_t i = idx - q_items - k_items;
+            vd[i] = krow[g.kv_width + i];
+        }
+    }
+}
+
 // One workgroup per (row, q head): attention over tokens 0..positions[row] of
 // the row's sequence, in the reference's arithmetic (see file comment).
 // scratch: [m * q_heads][score_stride] doubles.
@@ -445,6 +517,23 @@ hipError_t launch_attention(const KvLayout& kv, const float* qkv, std::uint64_t 
     const KvGeometry g{kv.pool, kv.page_tokens, kv.kv_width, kv.layers, kv.max_pages, kv.pool_pages};
     hipLaunchKernelGGL(attention_kernel, dim3(m * q_heads), dim3(kThreads), 0, stream, g, qkv, stride, m, positions,
                        tables, layer, q_heads, kv_heads, head_dim, scratch, score_stride, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_kv_append(const KvLayout& kv, float* qkv, std::uint64_t stride, std::uint64_t q_width,
+                                 std::uint32_t m, const std::int32_t* positions, const std::int32_t* tables,
+                                 std::uint32_t layer, std::uint32_t q_heads, std::uint32_t kv_heads,
+                                 std::uint32_t head_dim, std::uint32_t rope_dims, const void* table,
+                                 std::uint64_t table_positions, hipStream_t stream) {
+    const KvGeometry g{kv.pool, kv.page_tokens, kv.kv_width, kv.layers, kv.max_pages, kv.pool_pages};
+    const std::uint64_t per_row = static_cast<std::uint64_t>(q_heads) * (rope_dims / 2u) +
+                                  static_cast<std::uint64_t>(kv_heads) * (rope_dims / 2u + head_dim - rope_dims) +
+                                  kv.kv_width;
+    const std::uint64_t blocks = ceil_div(per_row, static_cast<std::uint64_t>(kThreads));
+    const unsigned gx = static_cast<unsigned>(blocks < 64u ? blocks : 64u);
+    hipLaunchKernelGGL(rope_kv_append_kernel, dim3(gx, m), dim3(kThreads), 0, stream, g, qkv, stride, q_width, m,
+                       positions, tables, layer, q_heads, kv_heads, head_dim, rope_dims,
+                       static_cast<const float2*>(table), table_positions);
     return hipGetLastError();
 }
 

@@ -399,12 +399,9 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
             !s) {
             return s;
         }
-        if ((rc = air_hip_rope(ctx, qkv_, qkv_width_, m, positions_dev_, c.attention_head_count, c.kv_head_count,
-                               head_dim_, c.rope_dimension_count, rope_table_, c.context_length)) != AIR_HIP_OK) {
-            return hip_status(rc);
-        }
-        if ((rc = air_hip_kv_append(ctx, &kv, qkv_, qkv_width_, q_width_, m, positions_dev_, tables_dev_, l)) !=
-            AIR_HIP_OK) {
+        if ((rc = air_hip_rope_kv_append(ctx, &kv, qkv_, qkv_width_, m, positions_dev_, tables_dev_, l,
+                                         c.attention_head_count, c.kv_head_count, head_dim_, c.rope_dimension_count,
+                                         rope_table_, c.context_length)) != AIR_HIP_OK) {
             return hip_status(rc);
         }
         rc = tiles ? air_hip_attention_online(ctx, &kv, qkv_, qkv_width_, m, positions_dev_, tables_dev_, l,

@@ -276,6 +276,17 @@ int air_hip_kv_append(air_hip_context* ctx, const air_hip_kv_layout* kv, const f
                       uint64_t q_width, uint32_t m, const int32_t* positions, const int32_t* page_tables,
                       uint32_t layer);
 
+/* air_hip_rope then air_hip_kv_append in one launch, with the same results
+ * (rope_batch_kernel then append_kv_batch_kernel, cuda_backend.cu:883-906,
+ * 1156-1173): the q and k heads of each row are rotated in place and k
+ * (kv_heads * head_dim = kv->kv_width floats after the q heads) and v are
+ * stored in the row's slot.  A position outside the table is not rotated; a
+ * row without a valid page slot is rotated but not stored. */
+int air_hip_rope_kv_append(air_hip_context* ctx, const air_hip_kv_layout* kv, float* qkv, uint64_t row_stride,
+                           uint32_t m, const int32_t* positions, const int32_t* page_tables, uint32_t layer,
+                           uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim, uint32_t rope_dims,
+                           const float* table, uint64_t table_positions);
+
 /* Attention of every row's q heads over tokens 0..positions[r] of its
  * sequence for one layer (attention, reference_executor.cpp:74-138):
  * out[r][q_heads * head_dim].  max_tokens bounds positions[r] + 1 and sizes

@@ -131,3 +131,59 @@ def test_online_rejects_bad_geometry(torch_cuda, hip_ctx):
                                           out.data_ptr())
     assert status == 6  # head width 96 is not compiled: unsupported
     assert b"64 and 128" in lib.air_hip_last_error()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("q_heads,kv_heads,head,rope_dims", [(28, 4, 128, 128), (4, 2, 64, 32)])
+def test_rope_kv_append_matches_separate_calls(torch_cuda, hip_ctx, q_heads, kv_heads, head, rope_dims):
+    """air_hip_rope_kv_append leaves q|k|v and the pool bit-identical to
+    air_hip_rope then air_hip_kv_append: rotary and unrotated k dims, a row
+    whose position lies past the RoPE table (stored unrotated), a row whose
+    page-table entry is absent and a negative position (rotated / skipped
+    alike)."""
+    torch = torch_cuda
+    dev = torch.device("cuda:0")
+    page_tokens, layers, layer, max_pages = 16, 3, 2, 4
+    kv_width = kv_heads * head
+    stride = q_heads * head + 2 * kv_width + 8          # padded rows
+    pool_pages = 12
+    rng = np.random.default_rng(head + rope_dims)
+    table_positions = 40
+    positions = [0, 5, 17, 39, 45, 63, 3, -1]
+    tables = [list(rng.permutation(pool_pages)[:max_pages]) for _ in positions]
+    tables[6][0] = -1                                    # position 3: no page for it
+    m = len(positions)
+    half = rope_dims // 2
+    ang = rng.uniform(0.0, 6.28, (table_positions, half))
+    rope = np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)
+    qkv_h = rng.standard_normal((m, stride)).astype(np.float32)
+    pool_h = rng.standard_normal(pool_pages * layers * 2 * page_tokens * kv_width).astype(np.float32)
+    rope_d = torch.from_numpy(rope).to(dev)
+    pos_d = torch.tensor(positions, dtype=torch.int32, device=dev)
+    tab_d = torch.tensor(np.array(tables, dtype=np.int32), device=dev)
+    lib = capi.lib()
+    outs = []
+    for fused in (False, True):
+        qkv = torch.from_numpy(qkv_h).to(dev)
+        pool = torch.from_numpy(pool_h).to(dev)
+        kv = capi.KvLayout(pool.data_ptr(), page_tokens, kv_width, layers, max_pages, pool_pages)
+        if fused:
+            capi.check(lib.air_hip_rope_kv_append(hip_ctx.handle, ctypes.byref(kv), qkv.data_ptr(), stride, m,
+                                                  pos_d.data_ptr(), tab_d.data_ptr(), layer, q_heads, kv_heads,
+                                                  head, rope_dims, rope_d.data_ptr(), table_positions))
+        else:
+            capi.check(lib.air_hip_rope(hip_ctx.handle, qkv.data_ptr(), stride, m, pos_d.data_ptr(), q_heads,
+                                        kv_heads, head, rope_dims, rope_d.data_ptr(), table_positions))
+            capi.check(lib.air_hip_kv_append(hip_ctx.handle, ctypes.byref(kv), qkv.data_ptr(), stride,
+                                             q_heads * head, m, pos_d.data_ptr(), tab_d.data_ptr(), layer))
+        torch.cuda.synchronize()
+        outs.append((qkv.cpu().numpy(), pool.cpu().numpy()))
+    (q0, p0), (q1, p1) = outs
+    assert not np.array_equal(q0, qkv_h)                 # something rotated
+    assert not np.array_equal(p0, pool_h)                # something stored
+    assert np.array_equal(q1.view(np.uint32), q0.view(np.uint32))
+    assert np.array_equal(p1.view(np.uint32), p0.view(np.uint32))
+    bad = lib.air_hip_rope_kv_append(hip_ctx.handle, ctypes.byref(kv), qkv.data_ptr(), stride, m, pos_d.data_ptr(),
+                                     tab_d.data_ptr(), layer, q_heads, kv_heads + 1, head, rope_dims,
+                                     rope_d.data_ptr(), table_positions)
+    assert bad == 1 and b"KV width" in lib.air_hip_last_error()
