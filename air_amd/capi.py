@@ -32,6 +32,10 @@ TYPE_Q8_0 = 8
 TYPE_Q4_K = 12
 TYPE_NAMES = {TYPE_Q4_0: "q4_0", TYPE_Q8_0: "q8_0", TYPE_Q4_K: "q4_k"}
 
+EPILOGUE_STORE = 0
+EPILOGUE_RESIDUAL = 1
+EPILOGUE_SWIGLU = 2
+
 LINEAR_AUTO = 0
 LINEAR_DECODE = 1
 LINEAR_PREFILL = 2
@@ -116,6 +120,7 @@ SIGNATURES = {
     "air_hip_rms_norm": (_I, [_P, _P, _P, _P, _U32, _U64, ctypes.c_double]),
     "air_hip_rope": (_I, [_P, _P, _U64, _U32, _P, _U32, _U32, _U32, _U32, _P, _U64]),
     "air_hip_kv_append": (_I, [_P, _P, _P, _U64, _U64, _U32, _P, _P, _U32]),
+    "air_hip_decode_linear_fused": (_I, [_P, _P, _P, _P, _P, _P, ctypes.c_double, ctypes.c_int]),
     "air_hip_rope_kv_append": (_I, [_P, _P, _P, _U64, _U32, _P, _P, _U32, _U32, _U32, _U32, _U32, _P, _U64]),
     "air_hip_attention": (_I, [_P, _P, _P, _U64, _U32, _P, _P, _U32, _U32, _U32, _U32, _U64, _P]),
     "air_hip_add_rms_norm": (_I, [_P, _P, _P, _P, _P, _U32, _U64, ctypes.c_double]),

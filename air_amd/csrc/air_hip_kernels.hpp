@@ -84,6 +84,18 @@ struct GemvShape {
 GemvShape plan_decode_gemv(const TilePlanes& planes, const DecodeTuning& tuning);
 hipError_t launch_decode_gemv(const TilePlanes& planes, const float* x, const float* bias, float* y,
                               const GemvShape& shape, hipStream_t stream);
+// The M = 1 linear with the step's element-wise neighbours fused in:
+// norm_weight != null RMS-normalises x first (eps); epilogue 0 stores
+// y = W x + b, 1 adds it to y (residual), 2 writes silu(g) * u of a fused
+// gate|up matrix (y has N / 2 entries).
+struct GemvFusion {
+    const float* norm_weight{nullptr};
+    double eps{0.0};
+    int epilogue{0};
+};
+GemvShape plan_decode_gemv_fused(const TilePlanes& planes, const DecodeTuning& tuning, int epilogue);
+hipError_t launch_decode_gemv_fused(const TilePlanes& planes, const float* x, const float* bias, float* y,
+                                    const GemvShape& shape, const GemvFusion& fusion, hipStream_t stream);
 
 // Prefill linear on f16 MFMA (M = 1..4096; planned for M >= 65).
 struct PrefillTuning {

@@ -517,6 +517,40 @@ int air_hip_dequantize_canonical(air_hip_context* ctx, int type, const void* can
     return AIR_HIP_OK;
 }
 
+int air_hip_decode_linear_fused(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y,
+                                const float* bias, const float* norm_weight, double eps, int epilogue) {
+    if (!ctx || !m || !x || !y) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix, x and y must not be null");
+    if (static_cast<const void*>(x) == static_cast<const void*>(y)) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "y must not alias x");
+    }
+    if (epilogue != AIR_HIP_EPILOGUE_STORE && epilogue != AIR_HIP_EPILOGUE_RESIDUAL &&
+        epilogue != AIR_HIP_EPILOGUE_SWIGLU) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "unknown epilogue %d", epilogue);
+    }
+    const bool norm = norm_weight != nullptr;
+    if ((norm && epilogue == AIR_HIP_EPILOGUE_RESIDUAL) || (!norm && epilogue == AIR_HIP_EPILOGUE_SWIGLU)) {
+        return fail(AIR_HIP_UNSUPPORTED, "this norm / epilogue combination is not provided");
+    }
+    if (norm && !(eps >= 0.0)) return fail(AIR_HIP_INVALID_ARGUMENT, "eps must be non-negative");
+    if (epilogue == AIR_HIP_EPILOGUE_SWIGLU && m->planes.n % 32u != 0u) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "a fused gate|up matrix needs n = 2F with F a multiple of 16");
+    }
+    if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
+    if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0 ||
+        (norm && reinterpret_cast<std::uintptr_t>(norm_weight) % 16u != 0)) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "x and the norm weight must be 16-byte aligned");
+    }
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const GemvShape shape = plan_decode_gemv_fused(m->planes, ctx->tuning, epilogue);
+    const hipError_t err = launch_decode_gemv_fused(m->planes, x, bias, y, shape,
+                                                    GemvFusion{norm_weight, eps, epilogue}, ctx->stream);
+    if (err != hipSuccess) return hip_fail(err, "decode_gemv_kernel (fused)");
+    ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
+    ctx->decode_rows.fetch_add(1, std::memory_order_relaxed);
+    return AIR_HIP_OK;
+}
+
 int air_hip_activations_load(air_hip_context* ctx, const float* x, uint64_t k, uint32_t rows) {
     if (!ctx || !x) return fail(AIR_HIP_INVALID_ARGUMENT, "context and x must not be null");
     if (rows == 0) return fail(AIR_HIP_INVALID_ARGUMENT, "linear batch width must be non-zero");

@@ -65,23 +65,26 @@ template <> struct GemvFormat<kQ4_K> {
 // One work unit of R row tiles plus the lane's activations: a chunk (16
 // blocks) split into U units of 16/U blocks each.  The activation operand
 // always spans the whole chunk (A row r = block r of the chunk); a unit's
-// tiles use rows [row0, row0 + 16/U).
-template <int FMT, int R, int U>
+// tiles use rows [row0, row0 + 16/U).  NORM: the activations are RMS-
+// normalised in the kernel, and nw holds the norm weights of the lane's x.
+template <int FMT, int R, int U, bool NORM>
 struct Chunk {
     static constexpr int kTiles = kChunkBlocks / GemvFormat<FMT>::kBlocksPerTile / U;
     uint4 c[kTiles][R][GemvFormat<FMT>::kCodeVecs];
     typename GemvFormat<FMT>::Scale sc[kTiles][R];
     float4 x[2];
+    float4v nw[NORM ? 2 : 1];    // native vectors: struct copies would go to scratch
 };
 
-template <int FMT, int R, int U>
-__device__ __forceinline__ void load_chunk(Chunk<FMT, R, U>& ch, const void* __restrict__ codes_,
+template <int FMT, int R, int U, bool NORM>
+__device__ __forceinline__ void load_chunk(Chunk<FMT, R, U, NORM>& ch, const void* __restrict__ codes_,
                                            const void* __restrict__ scales_, std::uint32_t rt0, std::uint32_t NT,
                                            std::uint32_t KT, std::uint32_t unit, std::uint32_t lane,
-                                           const float* __restrict__ x, std::uint64_t nblocks) {
+                                           const float* __restrict__ x, const float* __restrict__ norm_w,
+                                           std::uint64_t nblocks) {
     using F = GemvFormat<FMT>;
     using Scale = typename F::Scale;
-    constexpr int T = Chunk<FMT, R, U>::kTiles;
+    constexpr int T = Chunk<FMT, R, U, NORM>::kTiles;
     const std::uint32_t chunk = unit / U;
     const std::uint32_t kt0 = unit * T;   // first k tile of the unit
     if (rt0 + R <= NT && kt0 + T <= KT) {
@@ -135,15 +138,24 @@ __device__ __forceinline__ void load_chunk(Chunk<FMT, R, U>& ch, const void* __r
         const float4* src = reinterpret_cast<const float4*>(x + kb * 32u + 8u * (lane >> 4));
         ch.x[0] = src[0];
         ch.x[1] = src[1];
+        if constexpr (NORM) {
+            const float4v* wsrc = reinterpret_cast<const float4v*>(norm_w + kb * 32u + 8u * (lane >> 4));
+            ch.nw[0] = wsrc[0];
+            ch.nw[1] = wsrc[1];
+        }
     } else {
         ch.x[0] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         ch.x[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if constexpr (NORM) {
+            ch.nw[0] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+            ch.nw[1] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+        }
     }
 }
 
 // Weight block j of a tile as the f16 B operand (exact integers).
-template <int FMT, int R, int U>
-__device__ __forceinline__ half8v tile_block_codes(const Chunk<FMT, R, U>& ch, int t, int r, int j) {
+template <int FMT, int R, int U, bool NORM>
+__device__ __forceinline__ half8v tile_block_codes(const Chunk<FMT, R, U, NORM>& ch, int t, int r, int j) {
     if constexpr (FMT == kQ8_0) {
         const uint4 c = ch.c[t][r][0];
         half2v p0, p1, p2, p3;
@@ -163,15 +175,29 @@ __device__ __forceinline__ half8v tile_block_codes(const Chunk<FMT, R, U>& ch, i
     }
 }
 
-template <int FMT, int R, int U>
-__device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U>& ch, std::uint32_t unit, std::uint32_t lane,
-                                              float4v (&acc)[R]) {
+// The RMS norm's per-element step, (x * scale) * w, without contraction (the
+// norm kernel's arithmetic).
+__device__ __forceinline__ float norm_apply(float x, float scale, float w) {
+#pragma clang fp contract(off)
+    const float xs = x * scale;
+    return xs * w;
+}
+
+template <int FMT, int R, int U, bool NORM>
+__device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U, NORM>& ch, std::uint32_t unit,
+                                              std::uint32_t lane, float norm_scale, float4v (&acc)[R]) {
     using F = GemvFormat<FMT>;
-    constexpr int T = Chunk<FMT, R, U>::kTiles;
+    constexpr int T = Chunk<FMT, R, U, NORM>::kTiles;
     // First A / D row of the unit: a multiple of 16 / U >= 4, so the D slot
     // (row % 4) of each block is a compile-time constant.
     const std::uint32_t row0 = (unit % U) * (kChunkBlocks / U);
-    const float v[8] = {ch.x[0].x, ch.x[0].y, ch.x[0].z, ch.x[0].w, ch.x[1].x, ch.x[1].y, ch.x[1].z, ch.x[1].w};
+    float v[8] = {ch.x[0].x, ch.x[0].y, ch.x[0].z, ch.x[0].w, ch.x[1].x, ch.x[1].y, ch.x[1].z, ch.x[1].w};
+    if constexpr (NORM) {
+        const float w[8] = {ch.nw[0][0], ch.nw[0][1], ch.nw[0][2], ch.nw[0][3],
+                            ch.nw[1][0], ch.nw[1][1], ch.nw[1][2], ch.nw[1][3]};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = norm_apply(v[e], norm_scale, w[e]);
+    }
     // One power-of-two scale for the whole unit (all 64 lanes).  The f16
     // hi + lo split keeps ~21 significant bits of every element, however far
     // below the unit's maximum it lies, so the scale only guards the range.
@@ -230,7 +256,7 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U>& ch, std::u
             const int i = rel & 3;                                  // D slot of this block
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const half8v w = tile_block_codes<FMT, R, U>(ch, t, r, j);
+                const half8v w = tile_block_codes<FMT, R, U, NORM>(ch, t, r, j);
                 float4v p = mfma16x16x32(hi, w, float4v{0.0f, 0.0f, 0.0f, 0.0f});
                 p = mfma16x16x32(lo, w, p);
                 if constexpr (FMT == kQ8_0) {
@@ -261,49 +287,100 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U>& ch, std::u
 // Waves per workgroup: single-buffered one-tile waves fit 16 per CU.
 constexpr int gemv_max_waves(int R, int P) { return R >= 4 ? 4 : (R == 1 && P == 1 ? 16 : 8); }
 
+// The SwiGLU of the step, silu(g) * u with silu(g) = g / (1 + e^-g), without
+// contraction (the separate silu_mul kernel's arithmetic).
+__device__ __forceinline__ float swiglu(float g, float u) {
+#pragma clang fp contract(off)
+    const float s = g / (1.0f + expf(-g));
+    return s * u;
+}
+
+__device__ __forceinline__ double square_sum4(double acc, float4 v) {
+#pragma clang fp contract(off)
+    acc += static_cast<double>(v.x) * v.x;
+    acc += static_cast<double>(v.y) * v.y;
+    acc += static_cast<double>(v.z) * v.z;
+    acc += static_cast<double>(v.w) * v.w;
+    return acc;
+}
+
 // Workgroup = W waves on the same R row tiles; the chunks of K are split
 // across the waves.  P = 2: each wave double-buffers whole chunks.  P = 1:
 // one chunk buffer, loaded and consumed in turn -- the lower register count
 // lets twice as many waves share a CU, which hides the load latency by
 // occupancy instead.
-template <int FMT, int R, int P, int U>
+//
+// Fused step work around the linear (R = 1 only):
+//   NORM     x is RMS-normalised first: scale = 1 / sqrt(mean(x^2) + eps)
+//            from a double sum of squares over the whole row (every
+//            workgroup reduces it, each wave a slice), then x * scale * w;
+//   EPI = 0  y = W x + b;  1  y += W x + b (the residual stream);
+//   EPI = 2  SwiGLU over a fused gate|up matrix (N = 2F): the workgroup
+//            owns gate tile t (waves [0, W/2)) and up tile t + NT/2 (waves
+//            [W/2, W)) and writes y[n] = silu(g[n] + b[n]) * (u[n] + b[F + n]).
+template <int FMT, int R, int P, int U, bool NORM, int EPI>
 __global__ void __launch_bounds__(64 * gemv_max_waves(R, P))
 decode_gemv_kernel(const void* __restrict__ codes_, const void* __restrict__ scales_,
                    const float* __restrict__ x, const float* __restrict__ bias, float* __restrict__ y,
-                   std::uint64_t K, std::uint64_t N, std::uint32_t NT, std::uint32_t KT) {
+                   std::uint64_t K, std::uint64_t N, std::uint32_t NT, std::uint32_t KT,
+                   const float* __restrict__ norm_w, double eps) {
     extern __shared__ float wave_sums[];
-    using Ch = Chunk<FMT, R, U>;
+    using Ch = Chunk<FMT, R, U, NORM>;
     const std::uint32_t lane = threadIdx.x & 63u;
     // Wave-uniform: chunk indices, tile addresses and liveness stay scalar.
     const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const std::uint32_t W = blockDim.x >> 6;
-    const std::uint32_t rt0 = blockIdx.x * R;
+    const std::uint32_t group_waves = EPI == 2 ? W / 2u : W;       // waves per row tile
+    const bool up_half = EPI == 2 && wave >= group_waves;
+    const std::uint32_t gw = up_half ? wave - group_waves : wave;
+    const std::uint32_t rt0 = EPI == 2 ? blockIdx.x + (up_half ? NT / 2u : 0u) : blockIdx.x * R;
     const std::uint64_t nblocks = K / 32u;
     // Work units of Ch::kTiles k tiles (U per 16-block chunk), split over the waves.
     const std::uint32_t chunks = static_cast<std::uint32_t>(ceil_div(KT, static_cast<std::uint64_t>(Ch::kTiles) * U));
     const std::uint64_t units = static_cast<std::uint64_t>(chunks) * U;
-    const std::uint32_t c_begin = static_cast<std::uint32_t>((units * wave) / W);
-    const std::uint32_t c_end = static_cast<std::uint32_t>((units * (wave + 1u)) / W);
+    const std::uint32_t c_begin = static_cast<std::uint32_t>((units * gw) / group_waves);
+    const std::uint32_t c_end = static_cast<std::uint32_t>((units * (gw + 1u)) / group_waves);
 
     float4v acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
+    Ch a, b;
+
+    float norm_scale = 1.0f;
+    if constexpr (NORM) {
+        __shared__ double norm_red[16];
+        double ss = 0.0;
+        for (std::uint64_t i = threadIdx.x; i < K / 4u; i += blockDim.x) {
+            ss = square_sum4(ss, reinterpret_cast<const float4*>(x)[i]);
+        }
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+        if (lane == 0u) norm_red[wave] = ss;
+        __syncthreads();
+        double total = 0.0;
+        for (std::uint32_t w = 0; w < W; ++w) total += norm_red[w];
+        norm_scale = static_cast<float>(1.0 / sqrt(total / static_cast<double>(K) + eps));
+    }
+
     if constexpr (P == 1) {
         for (std::uint32_t c = c_begin; c < c_end; ++c) {
-            Ch a;
-            load_chunk<FMT, R, U>(a, codes_, scales_, rt0, NT, KT, c, lane, x, nblocks);
-            compute_chunk<FMT, R, U>(a, c, lane, acc);
+            load_chunk<FMT, R, U, NORM>(a, codes_, scales_, rt0, NT, KT, c, lane, x, norm_w, nblocks);
+            compute_chunk<FMT, R, U, NORM>(a, c, lane, norm_scale, acc);
         }
     } else {
-        Ch a, b;
-        if (c_begin < c_end) load_chunk<FMT, R, U>(a, codes_, scales_, rt0, NT, KT, c_begin, lane, x, nblocks);
+        if (c_begin < c_end) {
+            load_chunk<FMT, R, U, NORM>(a, codes_, scales_, rt0, NT, KT, c_begin, lane, x, norm_w, nblocks);
+        }
         for (std::uint32_t c = c_begin; c < c_end; c += 2u) {
-            if (c + 1u < c_end) load_chunk<FMT, R, U>(b, codes_, scales_, rt0, NT, KT, c + 1u, lane, x, nblocks);
-            compute_chunk<FMT, R, U>(a, c, lane, acc);
+            if (c + 1u < c_end) {
+                load_chunk<FMT, R, U, NORM>(b, codes_, scales_, rt0, NT, KT, c + 1u, lane, x, norm_w, nblocks);
+            }
+            compute_chunk<FMT, R, U, NORM>(a, c, lane, norm_scale, acc);
             if (c + 1u >= c_end) break;
-            if (c + 2u < c_end) load_chunk<FMT, R, U>(a, codes_, scales_, rt0, NT, KT, c + 2u, lane, x, nblocks);
-            compute_chunk<FMT, R, U>(b, c + 1u, lane, acc);
+            if (c + 2u < c_end) {
+                load_chunk<FMT, R, U, NORM>(a, codes_, scales_, rt0, NT, KT, c + 2u, lane, x, norm_w, nblocks);
+            }
+            compute_chunk<FMT, R, U, NORM>(b, c + 1u, lane, norm_scale, acc);
         }
     }
 
@@ -316,6 +393,7 @@ decode_gemv_kernel(const void* __restrict__ codes_, const void* __restrict__ sca
         t += __shfl_xor(t, 32);
         total[r] = t;
     }
+    float up_total = 0.0f;   // EPI 2: the up tile's sum
     if (W > 1u) {
         if (wave > 0u && lane < 16u) {
 #pragma unroll
@@ -323,49 +401,86 @@ decode_gemv_kernel(const void* __restrict__ codes_, const void* __restrict__ sca
         }
         __syncthreads();
         if (wave == 0u && lane < 16u) {
-            for (std::uint32_t w = 1; w < W; ++w) {
+            if constexpr (EPI == 2) {
+                for (std::uint32_t w = 1; w < group_waves; ++w) total[0] += wave_sums[(w - 1u) * 16u + lane];
+                up_total = wave_sums[(group_waves - 1u) * 16u + lane];
+                for (std::uint32_t w = group_waves + 1u; w < W; ++w) up_total += wave_sums[(w - 1u) * 16u + lane];
+            } else {
+                for (std::uint32_t w = 1; w < W; ++w) {
 #pragma unroll
-                for (int r = 0; r < R; ++r) total[r] += wave_sums[((w - 1u) * R + r) * 16u + lane];
+                    for (int r = 0; r < R; ++r) total[r] += wave_sums[((w - 1u) * R + r) * 16u + lane];
+                }
             }
         }
     }
     if (wave != 0u || lane >= 16u) return;
+    if constexpr (EPI == 2) {
+        const std::uint64_t F = N / 2u;
+        const std::uint64_t n = static_cast<std::uint64_t>(blockIdx.x) * 16u + lane;
+        if (n < F) {
+            const float g = total[0] + (bias ? bias[n] : 0.0f);
+            const float u = up_total + (bias ? bias[F + n] : 0.0f);
+            y[n] = swiglu(g, u);
+        }
+    } else {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const std::uint64_t n = static_cast<std::uint64_t>(rt0 + r) * 16u + lane;
-        if ((rt0 + r) < NT && n < N) y[n] = total[r] + (bias ? bias[n] : 0.0f);
+        for (int r = 0; r < R; ++r) {
+            const std::uint64_t n = static_cast<std::uint64_t>(rt0 + r) * 16u + lane;
+            if ((rt0 + r) >= NT || n >= N) continue;
+            const float out = total[r] + (bias ? bias[n] : 0.0f);
+            if constexpr (EPI == 1) {
+                y[n] = y[n] + out;
+            } else {
+                y[n] = out;
+            }
+        }
     }
 }
 
-template <int FMT, int R, int P, int U>
+template <int FMT, int R, int P, int U, bool NORM, int EPI>
 hipError_t launch_gemv_variant(const TilePlanes& p, const float* x, const float* bias, float* y,
-                               std::uint32_t W, hipStream_t stream) {
+                               std::uint32_t W, const GemvFusion& f, hipStream_t stream) {
     if (W == 0u || W > static_cast<std::uint32_t>(gemv_max_waves(R, P))) return hipErrorInvalidConfiguration;
-    const dim3 grid(static_cast<unsigned>(ceil_div(p.nt, R)), 1, 1);
+    if (EPI == 2 && (W % 2u != 0u || p.nt % 2u != 0u)) return hipErrorInvalidConfiguration;
+    const unsigned groups = EPI == 2 ? p.nt / 2u : static_cast<unsigned>(ceil_div(p.nt, R));
     const std::size_t lds = static_cast<std::size_t>(W - 1u) * R * 16u * sizeof(float);
-    decode_gemv_kernel<FMT, R, P, U><<<grid, 64u * W, lds, stream>>>(p.codes, p.scales, x, bias, y, p.k, p.n,
-                                                                      p.nt, p.kt);
+    decode_gemv_kernel<FMT, R, P, U, NORM, EPI><<<dim3(groups), 64u * W, lds, stream>>>(
+        p.codes, p.scales, x, bias, y, p.k, p.n, p.nt, p.kt, f.norm_weight, f.eps);
     return hipGetLastError();
+}
+
+// One row tile per wave (the fused step variants).
+template <int FMT, bool NORM, int EPI>
+hipError_t launch_gemv_r1(const TilePlanes& p, const float* x, const float* bias, float* y, const GemvShape& g,
+                          const GemvFusion& f, hipStream_t s) {
+    const std::uint32_t W = g.waves_per_group, P = g.depth;
+    if (g.units_per_chunk == 2u) {
+        return P == 1u ? launch_gemv_variant<FMT, 1, 1, 2, NORM, EPI>(p, x, bias, y, W, f, s)
+                       : launch_gemv_variant<FMT, 1, 2, 2, NORM, EPI>(p, x, bias, y, W, f, s);
+    }
+    return P == 1u ? launch_gemv_variant<FMT, 1, 1, 1, NORM, EPI>(p, x, bias, y, W, f, s)
+                   : launch_gemv_variant<FMT, 1, 2, 1, NORM, EPI>(p, x, bias, y, W, f, s);
 }
 
 template <int FMT>
 hipError_t launch_gemv_fmt(const TilePlanes& p, const float* x, const float* bias, float* y, const GemvShape& g,
-                           hipStream_t s) {
+                           const GemvFusion& f, hipStream_t s) {
+    const bool norm = f.norm_weight != nullptr;
+    if (norm || f.epilogue != 0) {
+        if (g.rows_per_wave != 1u) return hipErrorInvalidConfiguration;
+        if (!norm && f.epilogue == 1) return launch_gemv_r1<FMT, false, 1>(p, x, bias, y, g, f, s);
+        if (norm && f.epilogue == 0) return launch_gemv_r1<FMT, true, 0>(p, x, bias, y, g, f, s);
+        if (norm && f.epilogue == 2) return launch_gemv_r1<FMT, true, 2>(p, x, bias, y, g, f, s);
+        return hipErrorInvalidValue;
+    }
     const std::uint32_t R = g.rows_per_wave, W = g.waves_per_group, P = g.depth;
-    if (R == 1u) {
-        if (g.units_per_chunk == 2u) {
-            return P == 1u ? launch_gemv_variant<FMT, 1, 1, 2>(p, x, bias, y, W, s)
-                           : launch_gemv_variant<FMT, 1, 2, 2>(p, x, bias, y, W, s);
-        }
-        return P == 1u ? launch_gemv_variant<FMT, 1, 1, 1>(p, x, bias, y, W, s)
-                       : launch_gemv_variant<FMT, 1, 2, 1>(p, x, bias, y, W, s);
-    }
+    if (R == 1u) return launch_gemv_r1<FMT, false, 0>(p, x, bias, y, g, f, s);
     if (R == 2u) {
-        return P == 1u ? launch_gemv_variant<FMT, 2, 1, 1>(p, x, bias, y, W, s)
-                       : launch_gemv_variant<FMT, 2, 2, 1>(p, x, bias, y, W, s);
+        return P == 1u ? launch_gemv_variant<FMT, 2, 1, 1, false, 0>(p, x, bias, y, W, f, s)
+                       : launch_gemv_variant<FMT, 2, 2, 1, false, 0>(p, x, bias, y, W, f, s);
     }
-    return P == 1u ? launch_gemv_variant<FMT, 4, 1, 1>(p, x, bias, y, W, s)
-                   : launch_gemv_variant<FMT, 4, 2, 1>(p, x, bias, y, W, s);
+    return P == 1u ? launch_gemv_variant<FMT, 4, 1, 1, false, 0>(p, x, bias, y, W, f, s)
+                   : launch_gemv_variant<FMT, 4, 2, 1, false, 0>(p, x, bias, y, W, f, s);
 }
 
 } // namespace
@@ -426,12 +541,32 @@ GemvShape plan_decode_gemv(const TilePlanes& p, const DecodeTuning& tuning) {
     return g;
 }
 
+GemvShape plan_decode_gemv_fused(const TilePlanes& p, const DecodeTuning& tuning, int epilogue) {
+    GemvShape g = plan_decode_gemv(p, tuning);
+    g.rows_per_wave = 1u;
+    if (g.units_per_chunk == 2u && p.type != kQ8_0) g.units_per_chunk = 1u;
+    if (epilogue == 2) {
+        // A gate tile and its up tile per workgroup: twice the waves of the
+        // plain plan, single-buffered past eight.
+        std::uint32_t w = 2u * g.waves_per_group;
+        if (w > 16u) w = 16u;
+        if (w > 8u) g.depth = 1u;
+        g.waves_per_group = w < 2u ? 2u : w;
+    }
+    return g;
+}
+
 hipError_t launch_decode_gemv(const TilePlanes& p, const float* x, const float* bias, float* y,
                               const GemvShape& g, hipStream_t stream) {
+    return launch_decode_gemv_fused(p, x, bias, y, g, GemvFusion{}, stream);
+}
+
+hipError_t launch_decode_gemv_fused(const TilePlanes& p, const float* x, const float* bias, float* y,
+                                    const GemvShape& g, const GemvFusion& f, hipStream_t stream) {
     switch (p.type) {
-    case kQ8_0: return launch_gemv_fmt<kQ8_0>(p, x, bias, y, g, stream);
-    case kQ4_0: return launch_gemv_fmt<kQ4_0>(p, x, bias, y, g, stream);
-    case kQ4_K: return launch_gemv_fmt<kQ4_K>(p, x, bias, y, g, stream);
+    case kQ8_0: return launch_gemv_fmt<kQ8_0>(p, x, bias, y, g, f, stream);
+    case kQ4_0: return launch_gemv_fmt<kQ4_0>(p, x, bias, y, g, f, stream);
+    case kQ4_K: return launch_gemv_fmt<kQ4_K>(p, x, bias, y, g, f, stream);
     default: return hipErrorInvalidValue;
     }
 }

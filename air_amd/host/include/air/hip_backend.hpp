@@ -104,6 +104,10 @@ public:
     // practice), hip-prefill (f16 MFMA GEMM, M up to 4096).
     [[nodiscard]] Status linear(std::uint32_t layer, LinearRole role, const float* x, float* y,
                                 std::uint32_t rows, QuantizedLinearExecutionKind tactic) const;
+    // One-row decode linear with the step's RMSNorm before it (norm_weight
+    // non-null) and a residual add or SwiGLU after it (air_hip_decode_linear_fused).
+    [[nodiscard]] Status decode_linear_fused(std::uint32_t layer, LinearRole role, const float* x, float* y,
+                                             const float* norm_weight, double eps, int epilogue) const;
     [[nodiscard]] Result<HipLinearInfo> linear_info(std::uint32_t layer, LinearRole role) const;
     [[nodiscard]] bool fused_qkv() const noexcept { return fused_qkv_; }
     [[nodiscard]] bool fused_gate_up() const noexcept { return fused_gate_up_; }

@@ -316,6 +316,16 @@ Status HipPreparedModel::linear(std::uint32_t layer, LinearRole role, const floa
     return hip_status(air_hip_linear(ctx_, l->matrix, x, y, l->bias, rows, t));
 }
 
+Status HipPreparedModel::decode_linear_fused(std::uint32_t layer, LinearRole role, const float* x, float* y,
+                                             const float* norm_weight, double eps, int epilogue) const {
+    const auto* l = find(layer, role);
+    if (!l) {
+        return Status::invalid_argument(std::string("no resident linear for role ") + to_string(role) + " at layer " +
+                                        std::to_string(layer));
+    }
+    return hip_status(air_hip_decode_linear_fused(ctx_, l->matrix, x, y, l->bias, norm_weight, eps, epilogue));
+}
+
 Status HipPreparedModel::set_stream(void* stream) {
     if (Status s = hip_status(air_hip_context_set_stream(ctx_, stream)); !s) return s;
     options_.stream = stream;

@@ -377,6 +377,26 @@ Status HipStepEngine::project(std::uint32_t layer, LinearRole fused, LinearRole 
     return Status::ok();
 }
 
+// RoPE and the KV append of layer l, then attention of the step's rows over
+// their sequences' keys (q|k|v in qkv_, output in att_).
+Status HipStepEngine::attention(std::uint32_t l, std::uint32_t m, std::uint64_t max_tokens, std::uint32_t table_pages,
+                                std::uint32_t tiles) {
+    const auto& c = prepared_.model().config();
+    air_hip_context* ctx = prepared_.context();
+    const air_hip_kv_layout kv{pool_, page_tokens_, kv_width_, c.layer_count, table_pages, pool_pages_};
+    int rc = air_hip_rope_kv_append(ctx, &kv, qkv_, qkv_width_, m, positions_dev_, tables_dev_, l,
+                                    c.attention_head_count, c.kv_head_count, head_dim_, c.rope_dimension_count,
+                                    rope_table_, c.context_length);
+    if (rc != AIR_HIP_OK) return hip_status(rc);
+    rc = tiles ? air_hip_attention_online(ctx, &kv, qkv_, qkv_width_, m, positions_dev_, tables_dev_, l,
+                                          c.attention_head_count, c.kv_head_count, head_dim_,
+                                          reinterpret_cast<const air_hip_attention_tile*>(tiles_dev_), tiles,
+                                          max_tokens, att_)
+               : air_hip_attention(ctx, &kv, qkv_, qkv_width_, m, positions_dev_, tables_dev_, l,
+                                   c.attention_head_count, c.kv_head_count, head_dim_, max_tokens, att_);
+    return rc == AIR_HIP_OK ? Status::ok() : hip_status(rc);
+}
+
 // Embedding through the last layer's residual for `m` uploaded rows.
 // tiles > 0: the online_softmax attention over the uploaded tiles; 0: the
 // baseline (reference arithmetic) attention.
@@ -384,9 +404,46 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
                              QuantizedLinearExecutionKind tactic, std::uint32_t tiles) {
     const auto& c = prepared_.model().config();
     air_hip_context* ctx = prepared_.context();
-    const air_hip_kv_layout kv{pool_, page_tokens_, kv_width_, c.layer_count, table_pages, pool_pages_};
     int rc = air_hip_matrix_rows(ctx, embedding_, tokens_dev_, m, hidden_);
     if (rc != AIR_HIP_OK) return hip_status(rc);
+    // One row on the decode tactic (single-sequence decode): the attention
+    // norm runs inside the q|k|v linear and both residual adds inside the o
+    // and down linears, the hidden state updated in place.  The FFN norm and
+    // SiLU stay kernels of their own: measured at M = 1 on the 7B shapes, a
+    // norm prologue in each of gate|up's 1184 workgroups costs more than the
+    // norm launch it saves (q|k|v 9.3 us fused vs 10.3 us; o + add 6.2 vs
+    // 9.8; down + add 16.4 vs 20.0; gate|up with norm and SwiGLU 34.4 vs
+    // 31.6 for norm, linear and SiLU).
+    const bool fuse = m == 1U && tactic == QuantizedLinearExecutionKind::hip_decode && prepared_.fused_qkv() &&
+                      prepared_.fused_gate_up();
+    const double eps = c.rms_norm_epsilon;
+    if (fuse) {
+        for (std::uint32_t l = 0; l < c.layer_count; ++l) {
+            if (Status s = prepared_.decode_linear_fused(l, LinearRole::attn_qkv, hidden_, qkv_, attn_norm_[l], eps,
+                                                         AIR_HIP_EPILOGUE_STORE);
+                !s) {
+                return s;
+            }
+            if (Status s = attention(l, m, max_tokens, table_pages, tiles); !s) return s;
+            if (Status s = prepared_.decode_linear_fused(l, LinearRole::attn_output, att_, hidden_, nullptr, 0.0,
+                                                         AIR_HIP_EPILOGUE_RESIDUAL);
+                !s) {
+                return s;
+            }
+            if ((rc = air_hip_rms_norm(ctx, hidden_, ffn_norm_[l], normed_, m, embed_, eps)) != AIR_HIP_OK) {
+                return hip_status(rc);
+            }
+            if (Status s = prepared_.linear(l, LinearRole::ffn_gate_up, normed_, gate_up_, m, tactic); !s) return s;
+            if ((rc = air_hip_silu_mul(ctx, gate_up_, act_, m, ffn_)) != AIR_HIP_OK) return hip_status(rc);
+            if (Status s = prepared_.decode_linear_fused(l, LinearRole::ffn_down, act_, hidden_, nullptr, 0.0,
+                                                         AIR_HIP_EPILOGUE_RESIDUAL);
+                !s) {
+                return s;
+            }
+        }
+        rc = air_hip_rms_norm(ctx, hidden_, output_norm_, normed_, m, embed_, eps);
+        return rc == AIR_HIP_OK ? Status::ok() : hip_status(rc);
+    }
     // Each residual add runs fused with the RMSNorm after it (the next
     // layer's attention norm, or the final norm): normed_ always holds the
     // input of the next projection.
@@ -399,18 +456,7 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
             !s) {
             return s;
         }
-        if ((rc = air_hip_rope_kv_append(ctx, &kv, qkv_, qkv_width_, m, positions_dev_, tables_dev_, l,
-                                         c.attention_head_count, c.kv_head_count, head_dim_, c.rope_dimension_count,
-                                         rope_table_, c.context_length)) != AIR_HIP_OK) {
-            return hip_status(rc);
-        }
-        rc = tiles ? air_hip_attention_online(ctx, &kv, qkv_, qkv_width_, m, positions_dev_, tables_dev_, l,
-                                              c.attention_head_count, c.kv_head_count, head_dim_,
-                                              reinterpret_cast<const air_hip_attention_tile*>(tiles_dev_), tiles,
-                                              max_tokens, att_)
-                   : air_hip_attention(ctx, &kv, qkv_, qkv_width_, m, positions_dev_, tables_dev_, l,
-                                       c.attention_head_count, c.kv_head_count, head_dim_, max_tokens, att_);
-        if (rc != AIR_HIP_OK) return hip_status(rc);
+        if (Status s = attention(l, m, max_tokens, table_pages, tiles); !s) return s;
         if (Status s = prepared_.linear(l, LinearRole::attn_output, att_, proj_, m, tactic); !s) return s;
         if ((rc = air_hip_add_rms_norm(ctx, hidden_, proj_, ffn_norm_[l], normed_, m, embed_, c.rms_norm_epsilon)) !=
             AIR_HIP_OK) {

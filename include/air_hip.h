@@ -222,6 +222,31 @@ int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* matrix,
                    const float* x, float* y, const float* bias,
                    uint32_t m, int tactic);
 
+/* The M = 1 decode linear with its element-wise neighbours in the step
+ * fused into the one launch, for a single-sequence decode loop: the
+ * reference runs them as separate kernels around the projection
+ * (rms_norm_kernel, add_vector_kernel, silu_mul_kernel, cuda_backend.cu:789,
+ * 849-860), in the arithmetic of reference_executor.cpp:17-35.
+ *   norm_weight  NULL, or the RMSNorm weight (k floats): x is first
+ *                normalised, x_i * float(1 / sqrt(mean(x^2) + eps)) * w_i,
+ *                the sum of squares in double (as air_hip_rms_norm; the
+ *                summation order differs);
+ *   epilogue     STORE     y = W x + b (n floats);
+ *                RESIDUAL  y += W x + b (y: the residual stream, n floats);
+ *                SWIGLU    the matrix is a fused gate|up of n = 2F rows
+ *                          (F a multiple of 16): y[i] = silu(g_i) * u_i for
+ *                          the F outputs, silu(g) = g / (1 + e^-g).
+ * Every combination but (norm, RESIDUAL) and (no norm, SWIGLU).  x is one
+ * 16-byte aligned row of k floats and must not alias y.  Same tolerance as
+ * the DECODE tactic.  No counterpart in the reference's linear API. */
+enum {
+    AIR_HIP_EPILOGUE_STORE = 0,
+    AIR_HIP_EPILOGUE_RESIDUAL = 1,
+    AIR_HIP_EPILOGUE_SWIGLU = 2
+};
+int air_hip_decode_linear_fused(air_hip_context* ctx, const air_hip_matrix* matrix, const float* x, float* y,
+                                const float* bias, const float* norm_weight, double eps, int epilogue);
+
 /* ---- the Qwen2 step around the linears ---------------------------------- */
 /* Device primitives of one Qwen2 step over M rows, each row a (sequence,
  * position, token).  Arithmetic follows the reference executor operation by

@@ -246,3 +246,60 @@ def test_graph_replay_after_workspace_growth(torch_cuda):
         graph = None                              # before the context frees its kept buffers
         mat.release()
         ctx.close()
+
+
+@pytest.mark.parametrize("type_id,k,f", [(capi.TYPE_Q8_0, 1056, 512), (capi.TYPE_Q8_0, 3584, 1184),
+                                         (capi.TYPE_Q4_0, 1024, 256), (capi.TYPE_Q4_K, 2304, 512)])
+def test_decode_linear_fused_matches_separate_kernels(torch_cuda, hip_ctx, type_id, k, f):
+    """air_hip_decode_linear_fused against the separate kernels it replaces:
+    RMSNorm then the linear (1e-6: the norm's sum runs in another order),
+    the linear then a residual add (bit-exact: same launch plan), and
+    RMSNorm, the gate|up linear and SwiGLU (1e-6)."""
+    torch = torch_cuda
+    lib = capi.lib()
+    n = 2 * f
+    canon = helpers.weights(type_id, k, n, seed=k + f)
+    mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    try:
+        x = _dev(torch, helpers.activations(1, k, seed=k + 1) * 3.0)
+        w = _dev(torch, helpers.activations(1, k, seed=k + 2)[0])
+        bias = _dev(torch, helpers.activations(1, n, seed=k + 3)[0] * 0.1)
+        eps = 1e-6
+        normed = torch.empty_like(x)
+        ref = torch.empty((1, n), dtype=torch.float32, device="cuda:0")
+        capi.check(lib.air_hip_rms_norm(hip_ctx.handle, x.data_ptr(), w.data_ptr(), normed.data_ptr(), 1, k, eps))
+        mat.linear(normed, ref, 1, bias=bias)
+        # RMSNorm + store
+        got = torch.full((1, n), float("nan"), dtype=torch.float32, device="cuda:0")
+        capi.check(lib.air_hip_decode_linear_fused(hip_ctx.handle, mat.handle, x.data_ptr(), got.data_ptr(),
+                                                   bias.data_ptr(), w.data_ptr(), eps, capi.EPILOGUE_STORE))
+        torch.cuda.synchronize()
+        assert helpers.rel_l2(got.cpu().numpy(), ref.cpu().numpy()) <= 1e-6
+        # residual add, bit-exact against linear + add
+        resid = _dev(torch, helpers.activations(1, n, seed=k + 4))
+        lin = torch.empty((1, n), dtype=torch.float32, device="cuda:0")
+        mat.linear(x, lin, 1, bias=bias)
+        want = (resid + lin).cpu().numpy()
+        capi.check(lib.air_hip_decode_linear_fused(hip_ctx.handle, mat.handle, x.data_ptr(), resid.data_ptr(),
+                                                   bias.data_ptr(), None, 0.0, capi.EPILOGUE_RESIDUAL))
+        torch.cuda.synchronize()
+        assert np.array_equal(resid.cpu().numpy().view(np.uint32), want.view(np.uint32))
+        # RMSNorm + SwiGLU over the fused gate|up
+        act_ref = torch.empty((1, f), dtype=torch.float32, device="cuda:0")
+        capi.check(lib.air_hip_silu_mul(hip_ctx.handle, ref.data_ptr(), act_ref.data_ptr(), 1, f))
+        act = torch.full((1, f), float("nan"), dtype=torch.float32, device="cuda:0")
+        capi.check(lib.air_hip_decode_linear_fused(hip_ctx.handle, mat.handle, x.data_ptr(), act.data_ptr(),
+                                                   bias.data_ptr(), w.data_ptr(), eps, capi.EPILOGUE_SWIGLU))
+        torch.cuda.synchronize()
+        assert helpers.rel_l2(act.cpu().numpy(), act_ref.cpu().numpy()) <= 1e-6
+        # combinations that are not provided, and a bad epilogue
+        assert lib.air_hip_decode_linear_fused(hip_ctx.handle, mat.handle, x.data_ptr(), act.data_ptr(), None,
+                                               None, 0.0, capi.EPILOGUE_SWIGLU) == 6
+        assert lib.air_hip_decode_linear_fused(hip_ctx.handle, mat.handle, x.data_ptr(), resid.data_ptr(), None,
+                                               w.data_ptr(), eps, capi.EPILOGUE_RESIDUAL) == 6
+        assert lib.air_hip_decode_linear_fused(hip_ctx.handle, mat.handle, x.data_ptr(), resid.data_ptr(), None,
+                                               None, 0.0, 7) == 1
+        assert lib.air_hip_decode_linear_fused(hip_ctx.handle, mat.handle, x.data_ptr(), x.data_ptr(), None,
+                                               None, 0.0, capi.EPILOGUE_STORE) == 1
+    finally:
+        mat.release()
