@@ -296,6 +296,20 @@ __global__ __launch_bounds__(kThreads) void prefill_reduce_kernel(const float* _
     }
 }
 
+// The same sum four columns at a time (n % 4 == 0, 16-byte aligned rows),
+// in 32-bit index arithmetic: total4 = m * n / 4 < 2^32.
+__global__ __launch_bounds__(kThreads) void split_reduce4_kernel(const float4v* __restrict__ partials,
+                                                                 std::uint32_t splits, std::uint32_t total4,
+                                                                 std::uint32_t n4, const float4v* __restrict__ bias,
+                                                                 float4v* __restrict__ y) {
+    for (std::uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < total4; i += gridDim.x * kThreads) {
+        float4v v = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (std::uint32_t s = 0; s < splits; ++s) v += partials[static_cast<std::uint64_t>(s) * total4 + i];
+        if (bias) v += bias[i % n4];
+        y[i] = v;
+    }
+}
+
 // ---- weight exponent ---------------------------------------------------
 
 // Largest |dequantized weight| bound over all blocks, as float bits (>= 0).
@@ -435,6 +449,16 @@ hipError_t launch_prefill_linear(const TilePlanes& p, const float* x, const floa
 hipError_t launch_split_reduce(const float* partials, std::uint32_t splits, std::uint32_t m, std::uint64_t n,
                                const float* bias, float* y, hipStream_t stream) {
     const std::uint64_t total = static_cast<std::uint64_t>(m) * n;
+    const auto aligned = [](const void* p) { return reinterpret_cast<std::uintptr_t>(p) % 16u == 0u; };
+    if (n % 4u == 0u && total / 4u < (1ull << 32) && aligned(partials) && aligned(y) && (!bias || aligned(bias))) {
+        const std::uint64_t total4 = total / 4u;
+        const std::uint64_t grid = ceil_div(total4, kThreads);
+        hipLaunchKernelGGL(split_reduce4_kernel, dim3(static_cast<unsigned>(grid < 1024u ? grid : 1024u)),
+                           dim3(kThreads), 0, stream, reinterpret_cast<const float4v*>(partials), splits,
+                           static_cast<std::uint32_t>(total4), static_cast<std::uint32_t>(n / 4u),
+                           reinterpret_cast<const float4v*>(bias), reinterpret_cast<float4v*>(y));
+        return hipGetLastError();
+    }
     const std::uint64_t grid = ceil_div(total, kThreads);
     hipLaunchKernelGGL(prefill_reduce_kernel, dim3(static_cast<unsigned>(grid < 8192u ? grid : 8192u)), dim3(kThreads),
                        0, stream, partials, splits, m, n, bias, y);
