@@ -60,7 +60,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
     __shared__ float ks[kChunk][LD];
     __shared__ float vs[kChunk][LD];
     __shared__ float ps[kTileVectors][kChunk + 1];
-    __shared__ std::int64_t slot_off[kChunk];   // pool offset of each chunk token's K slot, -1 if absent
+    __shared__ std::int64_t slot_off[2][kChunk];   // pool offset of each chunk token's K slot, -1 if absent
 
     const AttentionTile tile = tiles[blockIdx.x];
     if (!tile_ok(tile, m, q_heads, kv_heads)) return;
@@ -108,27 +108,26 @@ __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
     // V of a token sits page_tokens * kv_width floats after its K in the page.
     const std::uint64_t v_after_k = static_cast<std::uint64_t>(g.page_tokens) * g.kv_width;
     constexpr unsigned kIters = kChunk * D4 / kAttnThreads;   // float4 of K (and of V) per thread per chunk
-    for (std::uint32_t c = c_begin; c < c_end; ++c) {
-        const std::int64_t c0 = static_cast<std::int64_t>(c) * kChunk;
-        __syncthreads();  // previous chunk's K, V, P and slot offsets are consumed
-        // Slot of each token of the chunk, resolved once (page table lookup).
-        if (tid < kChunk) {
-            const std::int64_t token = c0 + tid;
+    // Two-stage pipeline: chunk c+1's page slots are resolved and its K and V
+    // loads issued into registers before chunk c is computed from LDS.
+    const auto resolve = [&](std::uint32_t c, unsigned buf) __attribute__((always_inline)) {
+        if (tid < kChunk) {   // page table lookup, once per token
+            const std::int64_t token = static_cast<std::int64_t>(c) * kChunk + tid;
             std::int64_t off = -1;
             if (token < tmax) {
                 const float* kp = kv_slot(g, table, layer, static_cast<std::uint64_t>(token), false);
                 if (kp) off = kp - g.pool;
             }
-            slot_off[tid] = off;
+            slot_off[buf][tid] = off;
         }
-        __syncthreads();
-        // All of this thread's K and V loads in flight before the LDS stores.
-        float4 kr[kIters], vr[kIters];
+    };
+    float4 kr[kIters], vr[kIters];
+    const auto fetch = [&](unsigned buf) __attribute__((always_inline)) {
 #pragma unroll
         for (unsigned it = 0; it < kIters; ++it) {
             const unsigned idx = tid + it * kAttnThreads;
             const unsigned t = idx / D4, d4 = idx % D4;
-            const std::int64_t off = slot_off[t];
+            const std::int64_t off = slot_off[buf][t];
             kr[it] = make_float4(0.f, 0.f, 0.f, 0.f);
             vr[it] = kr[it];
             if (off >= 0) {
@@ -137,6 +136,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
                 vr[it] = load4(kp + v_after_k);
             }
         }
+    };
+    if (c_begin < c_end) resolve(c_begin, 0u);
+    __syncthreads();
+    if (c_begin < c_end) fetch(0u);
+    for (std::uint32_t c = c_begin; c < c_end; ++c) {
+        const std::int64_t c0 = static_cast<std::int64_t>(c) * kChunk;
+        const unsigned buf = (c - c_begin) & 1u;
+        __syncthreads();  // previous chunk's K, V and P are consumed
 #pragma unroll
         for (unsigned it = 0; it < kIters; ++it) {
             const unsigned idx = tid + it * kAttnThreads;
@@ -144,19 +151,25 @@ __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
             *reinterpret_cast<float4*>(&ks[t][4u * d4]) = kr[it];
             *reinterpret_cast<float4*>(&vs[t][4u * d4]) = vr[it];
         }
+        if (c + 1u < c_end) resolve(c + 1u, buf ^ 1u);
         __syncthreads();
+        if (c + 1u < c_end) fetch(buf ^ 1u);   // in flight while chunk c computes
 
-        // Scores of tokens lane16 + 16 j.
+        // Scores of tokens lane16 + 16 j.  Idle vector slots (a decode tile
+        // of 7 grouped heads leaves 9 of 16) skip the LDS reads: whole waves
+        // of them branch around the loop.
         float s[4];
 #pragma unroll
         for (unsigned j = 0; j < 4; ++j) s[j] = 0.0f;
+        if (active) {
 #pragma unroll 4
-        for (unsigned d4 = 0; d4 < D4; ++d4) {
-            const float4 q4 = *reinterpret_cast<const float4*>(&qs[qi][4u * d4]);
+            for (unsigned d4 = 0; d4 < D4; ++d4) {
+                const float4 q4 = *reinterpret_cast<const float4*>(&qs[qi][4u * d4]);
 #pragma unroll
-            for (unsigned j = 0; j < 4; ++j) {
-                const float4 k4 = *reinterpret_cast<const float4*>(&ks[lane16 + 16u * j][4u * d4]);
-                s[j] += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
+                for (unsigned j = 0; j < 4; ++j) {
+                    const float4 k4 = *reinterpret_cast<const float4*>(&ks[lane16 + 16u * j][4u * d4]);
+                    s[j] += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
+                }
             }
         }
         float row_max = -__builtin_huge_valf();
