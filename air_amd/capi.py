@@ -121,6 +121,7 @@ SIGNATURES = {
     "air_hip_rope": (_I, [_P, _P, _U64, _U32, _P, _U32, _U32, _U32, _U32, _P, _U64]),
     "air_hip_kv_append": (_I, [_P, _P, _P, _U64, _U64, _U32, _P, _P, _U32]),
     "air_hip_decode_linear_fused": (_I, [_P, _P, _P, _P, _P, _P, ctypes.c_double, ctypes.c_int]),
+    "air_hip_linear_epilogue": (_I, [_P, _P, _P, _U32, _P, _P, ctypes.c_int, _P, _P, ctypes.c_double, ctypes.c_int]),
     "air_hip_rope_kv_append": (_I, [_P, _P, _P, _U64, _U32, _P, _P, _U32, _U32, _U32, _U32, _U32, _P, _U64]),
     "air_hip_attention": (_I, [_P, _P, _P, _U64, _U32, _P, _P, _U32, _U32, _U32, _U32, _U64, _P]),
     "air_hip_add_rms_norm": (_I, [_P, _P, _P, _P, _P, _U32, _U64, ctypes.c_double]),

@@ -133,6 +133,7 @@ hipError_t launch_split_activations_rows(const float* x, std::uint32_t m, std::u
 // Skinny decode linear (M = 1..64) over split activations: activations staged
 // once per workgroup in LDS, exact weight codes streamed per wave, optional K
 // split with a deterministic reduction.
+struct SplitEpilogue;  // below, with the step kernels
 struct SkinnyShape {
     std::uint32_t mt{1};       // 16-row activation tiles (all M rows)
     std::uint32_t tile_n{1};   // 16-row weight tiles per wave (1 or 2)
@@ -143,13 +144,17 @@ struct SkinnyShape {
 };
 SkinnyShape plan_skinny(const TilePlanes& planes, std::uint32_t m, std::uint32_t tile_n, std::uint32_t k_splits);
 std::uint64_t skinny_partials_bytes(const SkinnyShape& shape, std::uint32_t m, std::uint64_t n);
+// With `epilogue` (only when shape.splits > 1 and split_epilogue_fits), the
+// split reduction applies it and y is not written.
 hipError_t launch_skinny_linear(const TilePlanes& planes, const SplitWorkspace& ws, const float* bias, float* y,
-                                std::uint32_t m, const SkinnyShape& shape, float* partials, hipStream_t stream);
+                                std::uint32_t m, const SkinnyShape& shape, float* partials, hipStream_t stream,
+                                const SplitEpilogue* epilogue = nullptr);
 // The same linear straight from f32 activations x [m][k]: each workgroup
 // splits the activations it stages (one power-of-two scale per (row,
 // 32-block)), so no split launch and no activation workspace.
 hipError_t launch_skinny_linear_x(const TilePlanes& planes, const float* x, const float* bias, float* y,
-                                  std::uint32_t m, const SkinnyShape& shape, float* partials, hipStream_t stream);
+                                  std::uint32_t m, const SkinnyShape& shape, float* partials, hipStream_t stream,
+                                  const SplitEpilogue* epilogue = nullptr);
 
 // ---- the Qwen2 step around the linears ----------------------------------
 
@@ -209,6 +214,30 @@ hipError_t launch_attention_tiles(const KvLayout& kv, const float* qkv, std::uin
                                   const AttentionTile* tiles, std::uint32_t tile_count, std::uint32_t splits,
                                   float* partials, float* out, hipStream_t stream);
 hipError_t launch_silu_mul(const float* gate_up, float* out, std::uint32_t m, std::uint64_t ffn, hipStream_t stream);
+
+// The step's element-wise work after a K-split linear, run by the launch
+// that sums the split partials (partials[s][m][n]) instead of a plain
+// reduction into y -- bit-identical to the reduction followed by the
+// separate kernel:
+//   kEpilogueSwiglu: out [m][n/2] = silu(g) * u, g and u the reduced
+//     columns i and n/2 + i (launch_silu_mul);
+//   kEpilogueResidual: out [m][n] += the reduced rows, then with
+//     norm_weight, norm_out = rms_norm(out) * norm_weight (launch_add_rms_norm;
+//     norm_out must not alias out).
+constexpr int kEpilogueResidual = 1;
+constexpr int kEpilogueSwiglu = 2;
+struct SplitEpilogue {
+    int kind{0};
+    float* out{nullptr};
+    const float* norm_weight{nullptr};
+    float* norm_out{nullptr};
+    double eps{0.0};
+};
+// Whether the reduction can carry `e` for this shape (alignment, widths).
+bool split_epilogue_fits(const SplitEpilogue& e, const float* partials, const float* bias, std::uint32_t m,
+                         std::uint64_t n);
+hipError_t launch_split_epilogue(const float* partials, std::uint32_t splits, std::uint32_t m, std::uint64_t n,
+                                 const float* bias, const SplitEpilogue& e, hipStream_t stream);
 hipError_t launch_add(float* x, const float* y, std::uint64_t count, hipStream_t stream);
 hipError_t launch_argmax(const float* logits, std::uint32_t m, std::uint64_t n, std::int32_t* out, hipStream_t stream);
 

@@ -59,6 +59,8 @@ struct air_hip_context {
     std::uint32_t* bound_scratch{nullptr};  // one uint32 for the weight exponent at residency
     void* attention_scratch{nullptr};       // attention scores, grown on demand
     std::uint64_t attention_scratch_bytes{0};
+    void* epilogue_rows{nullptr};           // linear output of air_hip_linear_epilogue's unfused route
+    std::uint64_t epilogue_rows_bytes{0};
     // Bumped whenever a context-owned buffer is (re)allocated: launches
     // recorded into a graph use the current buffers while it is unchanged.
     std::uint64_t generation{0};
@@ -167,11 +169,26 @@ int run_prefill(air_hip_context* ctx, const air_hip_matrix* m, const float* x, f
 }
 
 int ensure_split_buffers(air_hip_context* ctx, std::uint64_t partial_bytes, std::uint32_t counters);
+int linear_loaded(air_hip_context* ctx, const air_hip_matrix* m, float* y, const float* bias, int tactic,
+                  const SplitEpilogue* epilogue, bool* applied);
+
+// The epilogue when the skinny launch's split reduction can carry it, else
+// null (the linear then writes y).
+const SplitEpilogue* reduction_epilogue(air_hip_context* ctx, const air_hip_matrix* m, const SkinnyShape& shape,
+                                        const float* bias, std::uint32_t rows, const SplitEpilogue* epilogue,
+                                        bool* applied) {
+    if (!epilogue || shape.splits < 2u ||
+        !split_epilogue_fits(*epilogue, static_cast<const float*>(ctx->split_partials), bias, rows, m->planes.n)) {
+        return nullptr;
+    }
+    *applied = true;
+    return epilogue;
+}
 
 // Skinny decode linear straight from the f32 rows (M = 2..64): one launch
 // (two with a K split), no activation workspace.
 int run_skinny_x(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y, const float* bias,
-                 std::uint32_t rows) {
+                 std::uint32_t rows, const SplitEpilogue* epilogue = nullptr, bool* applied = nullptr) {
     const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits);
     // The in-workgroup split repeats the activation split in every
     // workgroup: it pays on narrow matrices, where the separate split launch
@@ -182,15 +199,16 @@ int run_skinny_x(air_hip_context* ctx, const air_hip_matrix* m, const float* x, 
     if (!narrow || (m->planes.type == kQ4_K && shape.mt == 4u)) {
         int rc = air_hip_activations_load(ctx, x, m->planes.k, rows);
         if (rc != AIR_HIP_OK) return rc;
-        return air_hip_linear_loaded(ctx, m, y, bias, AIR_HIP_LINEAR_DECODE);
+        return linear_loaded(ctx, m, y, bias, AIR_HIP_LINEAR_DECODE, epilogue, applied);
     }
     const std::uint64_t partial_bytes = skinny_partials_bytes(shape, rows, m->planes.n);
     if (partial_bytes > 0u) {
         const int rc = ensure_split_buffers(ctx, partial_bytes, 0u);
         if (rc != AIR_HIP_OK) return rc;
     }
+    const SplitEpilogue* epi = reduction_epilogue(ctx, m, shape, bias, rows, epilogue, applied);
     const hipError_t err = launch_skinny_linear_x(m->planes, x, bias, y, rows, shape,
-                                                  static_cast<float*>(ctx->split_partials), ctx->stream);
+                                                  static_cast<float*>(ctx->split_partials), ctx->stream, epi);
     if (err != hipSuccess) return hip_fail(err, "skinny_kernel");
     ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
     ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
@@ -295,6 +313,7 @@ int air_hip_context_destroy(air_hip_context* ctx) {
         if (ctx->prefill_workspace) (void)hipFree(ctx->prefill_workspace);
         if (ctx->bound_scratch) (void)hipFree(ctx->bound_scratch);
         if (ctx->attention_scratch) (void)hipFree(ctx->attention_scratch);
+        if (ctx->epilogue_rows) (void)hipFree(ctx->epilogue_rows);
         for (void* p : ctx->retired) (void)hipFree(p);
     }
     delete ctx;
@@ -576,6 +595,15 @@ int air_hip_activations_load(air_hip_context* ctx, const float* x, uint64_t k, u
 }
 
 int air_hip_linear_loaded(air_hip_context* ctx, const air_hip_matrix* m, float* y, const float* bias, int tactic) {
+    return linear_loaded(ctx, m, y, bias, tactic, nullptr, nullptr);
+}
+
+} // extern "C"
+
+namespace {
+
+int linear_loaded(air_hip_context* ctx, const air_hip_matrix* m, float* y, const float* bias, int tactic,
+                  const SplitEpilogue* epilogue, bool* applied) {
     if (!ctx || !m || !y) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix and y must not be null");
     if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
     if (tactic != AIR_HIP_LINEAR_AUTO && tactic != AIR_HIP_LINEAR_DECODE && tactic != AIR_HIP_LINEAR_PREFILL) {
@@ -605,8 +633,9 @@ int air_hip_linear_loaded(air_hip_context* ctx, const air_hip_matrix* m, float* 
             const int rc = ensure_split_buffers(ctx, partial_bytes, 0u);
             if (rc != AIR_HIP_OK) return rc;
         }
+        const SplitEpilogue* epi = reduction_epilogue(ctx, m, shape, bias, rows, epilogue, applied);
         const hipError_t err = launch_skinny_linear(m->planes, ws, bias, y, rows, shape,
-                                                    static_cast<float*>(ctx->split_partials), ctx->stream);
+                                                    static_cast<float*>(ctx->split_partials), ctx->stream, epi);
         if (err != hipSuccess) return hip_fail(err, "skinny_kernel");
         ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
         ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
@@ -619,8 +648,10 @@ int air_hip_linear_loaded(air_hip_context* ctx, const air_hip_matrix* m, float* 
     return AIR_HIP_OK;
 }
 
-int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y,
-                   const float* bias, uint32_t rows, int tactic) {
+// air_hip_linear; with `epilogue`, a skinny launch with a K split applies it
+// in its reduction (*applied set, y not written).
+int linear_rows(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y, const float* bias,
+                uint32_t rows, int tactic, const SplitEpilogue* epilogue, bool* applied) {
     if (!ctx || !m || !x || !y) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix, x and y must not be null");
     if (static_cast<const void*>(x) == static_cast<const void*>(y)) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "y must not alias x");
@@ -662,7 +693,7 @@ int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* m, const float* x
                                   ((m->planes.n <= 4096u && m->planes.k <= 4096u) ||
                                    (rows <= 4u && weight_bytes >= (256ull << 20)));
         if (ctx->decode_path == 2u || (ctx->decode_path == 0u && !prefer_fused)) {
-            return run_skinny_x(ctx, m, x, y, bias, rows);
+            return run_skinny_x(ctx, m, x, y, bias, rows, epilogue, applied);
         }
         const FusedShape shape = plan_decode_fused(m->planes, rows, ctx->tuning);
         if (shape.k_splits > 1u) {
@@ -681,12 +712,65 @@ int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* m, const float* x
         if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
         DeviceScope scope(ctx->device);
         if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-        return run_skinny_x(ctx, m, x, y, bias, rows);
+        return run_skinny_x(ctx, m, x, y, bias, rows, epilogue, applied);
     }
     int rc = air_hip_activations_load(ctx, x, m->planes.k, rows);
     if (rc != AIR_HIP_OK) return rc;
-    return air_hip_linear_loaded(ctx, m, y, bias, tactic);
+    return linear_loaded(ctx, m, y, bias, tactic, epilogue, applied);
 }
+
+} // namespace
+
+extern "C" {
+
+int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y,
+                   const float* bias, uint32_t rows, int tactic) {
+    return linear_rows(ctx, m, x, y, bias, rows, tactic, nullptr, nullptr);
+}
+
+int air_hip_linear_epilogue(air_hip_context* ctx, const air_hip_matrix* m, const float* x, uint32_t rows, float* out,
+                            const float* bias, int epilogue, const float* norm_weight, float* norm_out, double eps,
+                            int tactic) {
+    if (!ctx || !m || !x || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix, x and out must not be null");
+    if (epilogue != AIR_HIP_EPILOGUE_RESIDUAL && epilogue != AIR_HIP_EPILOGUE_SWIGLU) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "epilogue must be RESIDUAL or SWIGLU, not %d", epilogue);
+    }
+    if (static_cast<const void*>(x) == static_cast<const void*>(out)) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "out must not alias x");
+    }
+    if (epilogue == AIR_HIP_EPILOGUE_SWIGLU && (norm_weight || m->planes.n % 2u != 0u)) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "SWIGLU takes a fused gate|up matrix (even n) and no norm");
+    }
+    if (norm_weight && (!norm_out || norm_out == out || !(eps >= 0.0))) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "a norm needs its own output and a non-negative eps");
+    }
+    if (rows == 0) return fail(AIR_HIP_INVALID_ARGUMENT, "linear batch width must be non-zero");
+    if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    // The linear's own output, for the routes whose reduction cannot carry
+    // the epilogue; allocated up front so a captured step never allocates.
+    const std::uint64_t n = m->planes.n;
+    int rc = grow_buffer(ctx, &ctx->epilogue_rows, &ctx->epilogue_rows_bytes,
+                         static_cast<std::uint64_t>(rows) * n * sizeof(float), "epilogue rows");
+    if (rc != AIR_HIP_OK) return rc;
+    float* y = static_cast<float*>(ctx->epilogue_rows);
+    const SplitEpilogue e{epilogue == AIR_HIP_EPILOGUE_SWIGLU ? kEpilogueSwiglu : kEpilogueResidual, out, norm_weight,
+                          norm_out, eps};
+    bool applied = false;
+    rc = linear_rows(ctx, m, x, y, bias, rows, tactic, &e, &applied);
+    if (rc != AIR_HIP_OK || applied) return rc;
+    hipError_t err;
+    if (epilogue == AIR_HIP_EPILOGUE_SWIGLU) {
+        err = launch_silu_mul(y, out, rows, n / 2u, ctx->stream);
+    } else if (norm_weight) {
+        err = launch_add_rms_norm(out, y, norm_weight, norm_out, rows, n, eps, ctx->stream);
+    } else {
+        err = launch_add(out, y, static_cast<std::uint64_t>(rows) * n, ctx->stream);
+    }
+    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "linear epilogue");
+}
+
 
 // ---- the Qwen2 step around the linears ------------------------------------
 
@@ -743,6 +827,8 @@ int air_hip_rope(air_hip_context* ctx, float* qkv, uint64_t row_stride, uint32_t
     return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "rope_kernel");
 }
 
+} // extern "C"
+
 namespace {
 int check_kv(const air_hip_kv_layout* kv) {
     if (!kv || !kv->pool) return fail(AIR_HIP_INVALID_ARGUMENT, "KV layout and pool must not be null");
@@ -772,6 +858,8 @@ int ensure_attention_scratch(air_hip_context* ctx, uint64_t bytes) {
 }
 static_assert(sizeof(AttentionTile) == sizeof(air_hip_attention_tile), "tile layouts agree");
 } // namespace
+
+extern "C" {
 
 int air_hip_kv_append(air_hip_context* ctx, const air_hip_kv_layout* kv, const float* qkv, uint64_t row_stride,
                       uint64_t q_width, uint32_t m, const int32_t* positions, const int32_t* page_tables,

@@ -432,7 +432,8 @@ std::uint64_t skinny_partials_bytes(const SkinnyShape& shape, std::uint32_t m, s
 }
 
 hipError_t launch_skinny_linear(const TilePlanes& p, const SplitWorkspace& ws, const float* bias, float* y,
-                                std::uint32_t m, const SkinnyShape& shape, float* partials, hipStream_t stream) {
+                                std::uint32_t m, const SkinnyShape& shape, float* partials, hipStream_t stream,
+                                const SplitEpilogue* epilogue) {
     if (m == 0u || m > 64u || shape.mt != ceil_div(m, 16u)) return hipErrorInvalidValue;
     SkinnyArgs a{};
     a.codes = p.codes;
@@ -454,11 +455,13 @@ hipError_t launch_skinny_linear(const TilePlanes& p, const SplitWorkspace& ws, c
     const std::uint32_t blocks = shape.groups * shape.splits;
     const hipError_t err = launch_any<false>(p, a, shape, blocks, stream);
     if (err != hipSuccess || !split) return err;
+    if (epilogue) return launch_split_epilogue(partials, shape.splits, m, p.n, bias, *epilogue, stream);
     return launch_split_reduce(partials, shape.splits, m, p.n, bias, y, stream);
 }
 
 hipError_t launch_skinny_linear_x(const TilePlanes& p, const float* x, const float* bias, float* y, std::uint32_t m,
-                                  const SkinnyShape& shape, float* partials, hipStream_t stream) {
+                                  const SkinnyShape& shape, float* partials, hipStream_t stream,
+                                  const SplitEpilogue* epilogue) {
     if (m == 0u || m > 64u || shape.mt != ceil_div(m, 16u) || p.k % 32u != 0u) return hipErrorInvalidValue;
     SkinnyArgs a{};
     a.x = x;
@@ -479,6 +482,7 @@ hipError_t launch_skinny_linear_x(const TilePlanes& p, const float* x, const flo
     const std::uint32_t blocks = shape.groups * shape.splits;
     const hipError_t err = launch_any<true>(p, a, shape, blocks, stream);
     if (err != hipSuccess || !split) return err;
+    if (epilogue) return launch_split_epilogue(partials, shape.splits, m, p.n, bias, *epilogue, stream);
     return launch_split_reduce(partials, shape.splits, m, p.n, bias, y, stream);
 }
 

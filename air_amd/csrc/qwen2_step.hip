@@ -388,67 +388,143 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
     }
 }
 
-// RMSNorm of rows of n <= kNormMaxVec * 4 * kThreads floats held in
-// registers (one coalesced read of the row), with the residual add of the
-// reference's add_in_place fused in front when `y` is given: x += y, then
-// out = x * float(1 / sqrt(mean(x^2) + eps)) * w.  Without y, x and out may
-// alias; with y they must not (x receives the sum).
-constexpr unsigned kNormMaxVec = 8;
+// RMSNorm of rows of n <= kNormMaxVec * 4 * kNormThreads floats held in
+// registers (one coalesced read of the row by 1024 threads), with the
+// residual add of the reference's add_in_place fused in front when `y` is
+// given: x += y, then out = x * float(1 / sqrt(mean(x^2) + eps)) * w.
+// Without y, x and out may alias; with y they must not (x receives the sum).
+//
+// SPLIT: y holds `splits` partial outputs of a K-split linear
+// (y[s][row][n], split_stride = m * n floats apart) and the value added is
+// their sum from zero in split order plus bias -- the split reduction's
+// arithmetic, so the result is bit-identical to reducing first.  The
+// partials are loaded eight splits at a time so their latencies overlap.
+// w == null stops after the add (no norm, out unused).
+constexpr unsigned kNormThreads = 1024;
+constexpr unsigned kNormMaxVec = 2;
 
-__global__ __launch_bounds__(kThreads) void rms_norm_vec_kernel(float* x, const float* __restrict__ y,
-                                                                const float* __restrict__ w, float* out,
-                                                                std::uint64_t n, double eps) {
+__device__ __forceinline__ float4v split_sum4(const float* __restrict__ p, std::uint32_t splits,
+                                             std::uint64_t stride) {
+    float4v t = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (std::uint32_t s = 0; s < splits; s += 8u) {
+        float4v q[8];
+#pragma unroll
+        for (std::uint32_t e = 0; e < 8u; ++e) {
+            const std::uint32_t src = s + e < splits ? s + e : splits - 1u;  // in bounds; unused past the end
+            q[e] = *reinterpret_cast<const float4v*>(p + src * stride);
+        }
+#pragma unroll
+        for (std::uint32_t e = 0; e < 8u; ++e) {
+            if (s + e < splits) t += q[e];
+        }
+    }
+    return t;
+}
+
+template <bool SPLIT>
+__global__ __launch_bounds__(kNormThreads) void rms_norm_vec_kernel(float* x, const float* __restrict__ y,
+                                                                    const float* __restrict__ w, float* out,
+                                                                    std::uint64_t n, double eps, std::uint32_t splits,
+                                                                    std::uint64_t split_stride,
+                                                                    const float* __restrict__ bias) {
 #pragma clang fp contract(off)
-    __shared__ double red[kThreads / 64];
+    __shared__ double red[kNormThreads / 64];
     const std::uint64_t n4 = n / 4u;
     float* row = x + static_cast<std::uint64_t>(blockIdx.x) * n;
     float* dst = out + static_cast<std::uint64_t>(blockIdx.x) * n;
     const float* yrow = y ? y + static_cast<std::uint64_t>(blockIdx.x) * n : nullptr;
-    float4 v[kNormMaxVec];
+    float4v v[kNormMaxVec], g[kNormMaxVec];
 #pragma unroll
     for (unsigned j = 0; j < kNormMaxVec; ++j) {
-        const std::uint64_t i = threadIdx.x + static_cast<std::uint64_t>(j) * kThreads;
-        v[j] = i < n4 ? *reinterpret_cast<const float4*>(row + 4u * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const std::uint64_t i = threadIdx.x + static_cast<std::uint64_t>(j) * kNormThreads;
+        v[j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+        g[j] = v[j];
+        if (i < n4) {
+            v[j] = *reinterpret_cast<const float4v*>(row + 4u * i);
+            if (w) g[j] = *reinterpret_cast<const float4v*>(w + 4u * i);
+        }
     }
     if (yrow) {
 #pragma unroll
         for (unsigned j = 0; j < kNormMaxVec; ++j) {
-            const std::uint64_t i = threadIdx.x + static_cast<std::uint64_t>(j) * kThreads;
+            const std::uint64_t i = threadIdx.x + static_cast<std::uint64_t>(j) * kNormThreads;
             if (i < n4) {
-                const float4 b = *reinterpret_cast<const float4*>(yrow + 4u * i);
-                v[j] = make_float4(v[j].x + b.x, v[j].y + b.y, v[j].z + b.z, v[j].w + b.w);
-                *reinterpret_cast<float4*>(row + 4u * i) = v[j];
+                float4v b;
+                if constexpr (SPLIT) {
+                    b = split_sum4(yrow + 4u * i, splits, split_stride);
+                    if (bias) b += *reinterpret_cast<const float4v*>(bias + 4u * i);
+                } else {
+                    b = *reinterpret_cast<const float4v*>(yrow + 4u * i);
+                }
+                v[j] += b;
+                *reinterpret_cast<float4v*>(row + 4u * i) = v[j];
             }
         }
     }
+    if (!w) return;
     double sum = 0.0;
 #pragma unroll
     for (unsigned j = 0; j < kNormMaxVec; ++j) {
-        sum += static_cast<double>(v[j].x) * v[j].x;
-        sum += static_cast<double>(v[j].y) * v[j].y;
-        sum += static_cast<double>(v[j].z) * v[j].z;
-        sum += static_cast<double>(v[j].w) * v[j].w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum += static_cast<double>(v[j][e]) * v[j][e];
     }
     for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
     if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = sum;
     __syncthreads();
-    const double total = (red[0] + red[1]) + (red[2] + red[3]);
+    double total = 0.0;
+#pragma unroll
+    for (unsigned k = 0; k < kNormThreads / 64; ++k) total += red[k];
     const float scale = static_cast<float>(1.0 / sqrt(total / static_cast<double>(n) + eps));
 #pragma unroll
     for (unsigned j = 0; j < kNormMaxVec; ++j) {
-        const std::uint64_t i = threadIdx.x + static_cast<std::uint64_t>(j) * kThreads;
+        const std::uint64_t i = threadIdx.x + static_cast<std::uint64_t>(j) * kNormThreads;
         if (i < n4) {
-            const float4 g = *reinterpret_cast<const float4*>(w + 4u * i);
-            const float4 o = make_float4(v[j].x * scale * g.x, v[j].y * scale * g.y, v[j].z * scale * g.z,
-                                         v[j].w * scale * g.w);
-            *reinterpret_cast<float4*>(dst + 4u * i) = o;
+            float4v o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float xs = v[j][e] * scale;
+                o[e] = xs * g[j][e];
+            }
+            *reinterpret_cast<float4v*>(dst + 4u * i) = o;
         }
+    }
+}
+
+// out[r][i] = silu(g) * u with g, u the sums of a K-split fused gate|up
+// linear's columns i and f + i (partials[s][r][2f], summed from zero in split
+// order, then + bias): the split reduction and silu_mul_kernel's arithmetic
+// in one pass, four columns per thread (f % 4 == 0).
+__global__ __launch_bounds__(kThreads) void split_swiglu_kernel(const float4v* __restrict__ partials,
+                                                                std::uint32_t splits, std::uint32_t stride4,
+                                                                std::uint32_t total4, std::uint32_t f4,
+                                                                const float4v* __restrict__ bias,
+                                                                float4v* __restrict__ out) {
+#pragma clang fp contract(off)
+    for (std::uint32_t idx = blockIdx.x * kThreads + threadIdx.x; idx < total4; idx += gridDim.x * kThreads) {
+        const std::uint32_t r = idx / f4, c = idx % f4;
+        const std::uint32_t gi = r * 2u * f4 + c;
+        float4v g = {0.0f, 0.0f, 0.0f, 0.0f}, u = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (std::uint32_t s = 0; s < splits; ++s) {
+            g += partials[static_cast<std::uint64_t>(s) * stride4 + gi];
+            u += partials[static_cast<std::uint64_t>(s) * stride4 + gi + f4];
+        }
+        if (bias) {
+            g += bias[c];
+            u += bias[f4 + c];
+        }
+        float4v o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float sg = g[e] / (1.0f + expf(-g[e]));
+            o[e] = sg * u[e];
+        }
+        out[idx] = o;
     }
 }
 
 bool norm_vectorizable(const float* x, const float* y, const float* w, const float* out, std::uint64_t n) {
     const auto aligned = [](const void* p) { return reinterpret_cast<std::uintptr_t>(p) % 16u == 0; };
-    return n % 4u == 0 && n <= static_cast<std::uint64_t>(kNormMaxVec) * 4u * kThreads && aligned(x) &&
+    return n % 4u == 0 && n <= static_cast<std::uint64_t>(kNormMaxVec) * 4u * kNormThreads && aligned(x) &&
            (!y || aligned(y)) && aligned(w) && aligned(out);
 }
 
@@ -470,8 +546,9 @@ hipError_t launch_matrix_rows(const TilePlanes& p, const std::int32_t* rows, std
 hipError_t launch_rms_norm(const float* x, const float* w, float* out, std::uint32_t m, std::uint64_t n, double eps,
                            hipStream_t stream) {
     if (norm_vectorizable(x, nullptr, w, out, n)) {
-        hipLaunchKernelGGL(rms_norm_vec_kernel, dim3(m), dim3(kThreads), 0, stream, const_cast<float*>(x),
-                           static_cast<const float*>(nullptr), w, out, n, eps);
+        hipLaunchKernelGGL(rms_norm_vec_kernel<false>, dim3(m), dim3(kNormThreads), 0, stream, const_cast<float*>(x),
+                           static_cast<const float*>(nullptr), w, out, n, eps, 0u, std::uint64_t{0},
+                           static_cast<const float*>(nullptr));
     } else {
         hipLaunchKernelGGL(rms_norm_kernel, dim3(m), dim3(kThreads), 0, stream, x, w, out, n, eps);
     }
@@ -481,7 +558,8 @@ hipError_t launch_rms_norm(const float* x, const float* w, float* out, std::uint
 hipError_t launch_add_rms_norm(float* x, const float* y, const float* w, float* out, std::uint32_t m, std::uint64_t n,
                                double eps, hipStream_t stream) {
     if (norm_vectorizable(x, y, w, out, n)) {
-        hipLaunchKernelGGL(rms_norm_vec_kernel, dim3(m), dim3(kThreads), 0, stream, x, y, w, out, n, eps);
+        hipLaunchKernelGGL(rms_norm_vec_kernel<false>, dim3(m), dim3(kNormThreads), 0, stream, x, y, w, out, n, eps, 0u,
+                           std::uint64_t{0}, static_cast<const float*>(nullptr));
         return hipGetLastError();
     }
     hipLaunchKernelGGL(add_kernel, dim3(grid_for(static_cast<std::uint64_t>(m) * n)), dim3(kThreads), 0, stream, x, y,
@@ -545,6 +623,38 @@ hipError_t launch_silu_mul(const float* gate_up, float* out, std::uint32_t m, st
 
 hipError_t launch_add(float* x, const float* y, std::uint64_t count, hipStream_t stream) {
     hipLaunchKernelGGL(add_kernel, dim3(grid_for(count)), dim3(kThreads), 0, stream, x, y, count);
+    return hipGetLastError();
+}
+
+bool split_epilogue_fits(const SplitEpilogue& e, const float* partials, const float* bias, std::uint32_t m,
+                        std::uint64_t n) {
+    const auto aligned = [](const void* p) { return reinterpret_cast<std::uintptr_t>(p) % 16u == 0; };
+    if (!aligned(partials) || (bias && !aligned(bias)) || !aligned(e.out)) return false;
+    if (e.kind == kEpilogueSwiglu) {
+        return n % 8u == 0 && static_cast<std::uint64_t>(m) * n / 4u < (1ull << 32);
+    }
+    if (e.kind == kEpilogueResidual) {
+        return n % 4u == 0 && n <= static_cast<std::uint64_t>(kNormMaxVec) * 4u * kNormThreads &&
+               (!e.norm_weight || (aligned(e.norm_weight) && aligned(e.norm_out)));
+    }
+    return false;
+}
+
+hipError_t launch_split_epilogue(const float* partials, std::uint32_t splits, std::uint32_t m, std::uint64_t n,
+                                 const float* bias, const SplitEpilogue& e, hipStream_t stream) {
+    if (!split_epilogue_fits(e, partials, bias, m, n)) return hipErrorInvalidValue;
+    if (e.kind == kEpilogueSwiglu) {
+        const std::uint32_t f4 = static_cast<std::uint32_t>(n / 8u);
+        const std::uint32_t total4 = m * f4;
+        const std::uint64_t grid = ceil_div(static_cast<std::uint64_t>(total4), kThreads);
+        hipLaunchKernelGGL(split_swiglu_kernel, dim3(static_cast<unsigned>(grid < 2048u ? grid : 2048u)),
+                           dim3(kThreads), 0, stream, reinterpret_cast<const float4v*>(partials), splits,
+                           static_cast<std::uint32_t>(static_cast<std::uint64_t>(m) * n / 4u), total4, f4,
+                           reinterpret_cast<const float4v*>(bias), reinterpret_cast<float4v*>(e.out));
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(rms_norm_vec_kernel<true>, dim3(m), dim3(kNormThreads), 0, stream, e.out, partials, e.norm_weight,
+                       e.norm_out, n, e.eps, splits, static_cast<std::uint64_t>(m) * n, bias);
     return hipGetLastError();
 }
 

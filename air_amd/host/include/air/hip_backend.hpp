@@ -108,6 +108,12 @@ public:
     // non-null) and a residual add or SwiGLU after it (air_hip_decode_linear_fused).
     [[nodiscard]] Status decode_linear_fused(std::uint32_t layer, LinearRole role, const float* x, float* y,
                                              const float* norm_weight, double eps, int epilogue) const;
+    // A linear and the element-wise step work on its output: residual add
+    // (then, with norm_weight, the next RMSNorm into norm_out) or SwiGLU
+    // (air_hip_linear_epilogue; carried by the split reduction at M 2..64).
+    [[nodiscard]] Status linear_epilogue(std::uint32_t layer, LinearRole role, const float* x, std::uint32_t rows,
+                                         float* out, int epilogue, const float* norm_weight, float* norm_out,
+                                         double eps, QuantizedLinearExecutionKind tactic) const;
     [[nodiscard]] Result<HipLinearInfo> linear_info(std::uint32_t layer, LinearRole role) const;
     [[nodiscard]] bool fused_qkv() const noexcept { return fused_qkv_; }
     [[nodiscard]] bool fused_gate_up() const noexcept { return fused_gate_up_; }

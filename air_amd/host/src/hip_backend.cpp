@@ -316,6 +316,25 @@ Status HipPreparedModel::linear(std::uint32_t layer, LinearRole role, const floa
     return hip_status(air_hip_linear(ctx_, l->matrix, x, y, l->bias, rows, t));
 }
 
+Status HipPreparedModel::linear_epilogue(std::uint32_t layer, LinearRole role, const float* x, std::uint32_t rows,
+                                         float* out, int epilogue, const float* norm_weight, float* norm_out,
+                                         double eps, QuantizedLinearExecutionKind tactic) const {
+    const auto* l = find(layer, role);
+    if (!l) {
+        return Status::invalid_argument(std::string("no resident linear for role ") + to_string(role) + " at layer " +
+                                        std::to_string(layer));
+    }
+    int t = AIR_HIP_LINEAR_AUTO;
+    switch (tactic) {
+    case QuantizedLinearExecutionKind::hip_decode: t = AIR_HIP_LINEAR_DECODE; break;
+    case QuantizedLinearExecutionKind::hip_prefill: t = AIR_HIP_LINEAR_PREFILL; break;
+    default:
+        return Status::unsupported(std::string("HIP backend does not provide linear tactic ") + to_string(tactic));
+    }
+    return hip_status(
+        air_hip_linear_epilogue(ctx_, l->matrix, x, rows, out, l->bias, epilogue, norm_weight, norm_out, eps, t));
+}
+
 Status HipPreparedModel::decode_linear_fused(std::uint32_t layer, LinearRole role, const float* x, float* y,
                                              const float* norm_weight, double eps, int epilogue) const {
     const auto* l = find(layer, role);

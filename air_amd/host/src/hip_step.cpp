@@ -446,8 +446,14 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
     }
     // Each residual add runs fused with the RMSNorm after it (the next
     // layer's attention norm, or the final norm): normed_ always holds the
-    // input of the next projection.
-    if ((rc = air_hip_rms_norm(ctx, hidden_, attn_norm_[0], normed_, m, embed_, c.rms_norm_epsilon)) != AIR_HIP_OK) {
+    // input of the next projection.  Decode widths up to 64 hand the add +
+    // norm and the SwiGLU to the linear itself (air_hip_linear_epilogue),
+    // whose split reduction carries them: measured on the 7B shapes at
+    // M = 30 that saves three launches of 4-5 us per layer.  Prefill widths
+    // keep the separate kernels (the epilogue route would add a context
+    // buffer as large as the step's gate|up rows).
+    const bool epilogues = tactic == QuantizedLinearExecutionKind::hip_decode && m <= AIR_HIP_MAX_DECODE_ROWS;
+    if ((rc = air_hip_rms_norm(ctx, hidden_, attn_norm_[0], normed_, m, embed_, eps)) != AIR_HIP_OK) {
         return hip_status(rc);
     }
     for (std::uint32_t l = 0; l < c.layer_count; ++l) {
@@ -457,22 +463,44 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
             return s;
         }
         if (Status s = attention(l, m, max_tokens, table_pages, tiles); !s) return s;
-        if (Status s = prepared_.linear(l, LinearRole::attn_output, att_, proj_, m, tactic); !s) return s;
-        if ((rc = air_hip_add_rms_norm(ctx, hidden_, proj_, ffn_norm_[l], normed_, m, embed_, c.rms_norm_epsilon)) !=
-            AIR_HIP_OK) {
-            return hip_status(rc);
+        if (epilogues) {
+            if (Status s = prepared_.linear_epilogue(l, LinearRole::attn_output, att_, m, hidden_,
+                                                     AIR_HIP_EPILOGUE_RESIDUAL, ffn_norm_[l], normed_, eps, tactic);
+                !s) {
+                return s;
+            }
+        } else {
+            if (Status s = prepared_.linear(l, LinearRole::attn_output, att_, proj_, m, tactic); !s) return s;
+            if ((rc = air_hip_add_rms_norm(ctx, hidden_, proj_, ffn_norm_[l], normed_, m, embed_, eps)) != AIR_HIP_OK) {
+                return hip_status(rc);
+            }
         }
-        if (Status s = project(l, LinearRole::ffn_gate_up, LinearRole::ffn_gate, LinearRole::ffn_up,
-                               LinearRole::ffn_up, normed_, gate_up_, m, tactic);
-            !s) {
-            return s;
+        if (epilogues && prepared_.fused_gate_up()) {
+            if (Status s = prepared_.linear_epilogue(l, LinearRole::ffn_gate_up, normed_, m, act_,
+                                                     AIR_HIP_EPILOGUE_SWIGLU, nullptr, nullptr, 0.0, tactic);
+                !s) {
+                return s;
+            }
+        } else {
+            if (Status s = project(l, LinearRole::ffn_gate_up, LinearRole::ffn_gate, LinearRole::ffn_up,
+                                   LinearRole::ffn_up, normed_, gate_up_, m, tactic);
+                !s) {
+                return s;
+            }
+            if ((rc = air_hip_silu_mul(ctx, gate_up_, act_, m, ffn_)) != AIR_HIP_OK) return hip_status(rc);
         }
-        if ((rc = air_hip_silu_mul(ctx, gate_up_, act_, m, ffn_)) != AIR_HIP_OK) return hip_status(rc);
-        if (Status s = prepared_.linear(l, LinearRole::ffn_down, act_, proj_, m, tactic); !s) return s;
         const float* next_norm = l + 1U < c.layer_count ? attn_norm_[l + 1U] : output_norm_;
-        if ((rc = air_hip_add_rms_norm(ctx, hidden_, proj_, next_norm, normed_, m, embed_, c.rms_norm_epsilon)) !=
-            AIR_HIP_OK) {
-            return hip_status(rc);
+        if (epilogues) {
+            if (Status s = prepared_.linear_epilogue(l, LinearRole::ffn_down, act_, m, hidden_,
+                                                     AIR_HIP_EPILOGUE_RESIDUAL, next_norm, normed_, eps, tactic);
+                !s) {
+                return s;
+            }
+        } else {
+            if (Status s = prepared_.linear(l, LinearRole::ffn_down, act_, proj_, m, tactic); !s) return s;
+            if ((rc = air_hip_add_rms_norm(ctx, hidden_, proj_, next_norm, normed_, m, embed_, eps)) != AIR_HIP_OK) {
+                return hip_status(rc);
+            }
         }
     }
     return Status::ok();

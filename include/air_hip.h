@@ -247,6 +247,26 @@ enum {
 int air_hip_decode_linear_fused(air_hip_context* ctx, const air_hip_matrix* matrix, const float* x, float* y,
                                 const float* bias, const float* norm_weight, double eps, int epilogue);
 
+/* A linear over `rows` rows followed by the step's element-wise work on its
+ * output, the two Qwen2 steps after a projection (reference_executor.cpp:
+ * 29-31 add_in_place, 17-27 rms_norm, 325-428 the SiLU * up of the FFN):
+ *   AIR_HIP_EPILOGUE_SWIGLU: out [rows][n/2] = silu(g) * u, g and u the
+ *     linear's columns i and n/2 + i of a fused gate|up matrix
+ *     (air_hip_silu_mul); norm_weight must be null;
+ *   AIR_HIP_EPILOGUE_RESIDUAL: out [rows][n] += x W^T + bias, then, with
+ *     norm_weight, norm_out[r] = rms_norm(out[r]) * norm_weight
+ *     (air_hip_add_rms_norm; norm_out must not alias out).
+ * Bit-identical to air_hip_linear (same tactic) followed by that call.  Where
+ * the linear runs as a skinny launch with a K split (decode widths 2..64),
+ * its split reduction applies the epilogue, so the epilogue costs no launch
+ * of its own; other routes run the linear into a context buffer and the
+ * separate kernel.  out must not alias x.  No counterpart in the reference's
+ * linear API: it replaces the executor's linear then add / SiLU sequence
+ * (cuda_backend.cu:789, 849-860). */
+int air_hip_linear_epilogue(air_hip_context* ctx, const air_hip_matrix* matrix, const float* x, uint32_t rows,
+                            float* out, const float* bias, int epilogue, const float* norm_weight, float* norm_out,
+                            double eps, int tactic);
+
 /* ---- the Qwen2 step around the linears ---------------------------------- */
 /* Device primitives of one Qwen2 step over M rows, each row a (sequence,
  * position, token).  Arithmetic follows the reference executor operation by

@@ -303,3 +303,80 @@ def test_decode_linear_fused_matches_separate_kernels(torch_cuda, hip_ctx, type_
                                                None, 0.0, capi.EPILOGUE_STORE) == 1
     finally:
         mat.release()
+
+
+@pytest.mark.parametrize("type_id,k,n", [(capi.TYPE_Q8_0, 1024, 1024), (capi.TYPE_Q4_0, 2048, 512),
+                                         (capi.TYPE_Q4_K, 2304, 384), (capi.TYPE_Q8_0, 512, 666)])
+def test_linear_epilogue_matches_separate_kernels(torch_cuda, hip_ctx, type_id, k, n):
+    """air_hip_linear_epilogue against air_hip_linear followed by the kernel
+    it replaces, bit-exact: SwiGLU (silu_mul), residual add + RMSNorm
+    (add_rms_norm) and the add alone, at one row, widths served by the
+    single-launch kernel and by the skinny kernel with and without a K split
+    (the split reduction then carries the epilogue), and a width (n = 666)
+    whose rows are too ragged for the reduction to carry it."""
+    torch = torch_cuda
+    lib = capi.lib()
+    f = n // 2
+    canon = helpers.weights(type_id, k, n, seed=k + n + 11)
+    mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    dec = capi.LINEAR_DECODE
+    h = hip_ctx.handle
+
+    def bits(t):
+        return t.cpu().numpy().view(np.uint32)
+
+    try:
+        bias = _dev(torch, helpers.activations(1, n, seed=k + 3)[0] * 0.1)
+        w = _dev(torch, helpers.activations(1, n, seed=k + 2)[0])
+        eps = 1e-6
+        for m in (1, 8, 30, 64):
+            x = _dev(torch, helpers.activations(m, k, seed=m + k) * 2.0)
+            resid0 = _dev(torch, helpers.activations(m, n, seed=m + 7))
+            for path in [(0, 0, 0), (2, 1, 1), (2, 1, 3), (2, 2, 2)]:
+                hip_ctx.set_decode_path(*path)
+                case = (m, path)
+                lin = torch.empty((m, n), dtype=torch.float32, device="cuda:0")
+                capi.check(lib.air_hip_linear(h, mat.handle, x.data_ptr(), lin.data_ptr(), bias.data_ptr(), m, dec))
+                # SwiGLU
+                act_ref = torch.empty((m, f), dtype=torch.float32, device="cuda:0")
+                capi.check(lib.air_hip_silu_mul(h, lin.data_ptr(), act_ref.data_ptr(), m, f))
+                act = torch.full((m, f), float("nan"), dtype=torch.float32, device="cuda:0")
+                capi.check(lib.air_hip_linear_epilogue(h, mat.handle, x.data_ptr(), m, act.data_ptr(),
+                                                       bias.data_ptr(), capi.EPILOGUE_SWIGLU, None, None, 0.0, dec))
+                # residual add + RMSNorm
+                resid_ref = resid0.clone()
+                normed_ref = torch.empty((m, n), dtype=torch.float32, device="cuda:0")
+                capi.check(lib.air_hip_add_rms_norm(h, resid_ref.data_ptr(), lin.data_ptr(), w.data_ptr(),
+                                                    normed_ref.data_ptr(), m, n, eps))
+                resid = resid0.clone()
+                normed = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+                capi.check(lib.air_hip_linear_epilogue(h, mat.handle, x.data_ptr(), m, resid.data_ptr(),
+                                                       bias.data_ptr(), capi.EPILOGUE_RESIDUAL, w.data_ptr(),
+                                                       normed.data_ptr(), eps, dec))
+                # the add alone
+                plain_ref = resid0.clone()
+                capi.check(lib.air_hip_add(h, plain_ref.data_ptr(), lin.data_ptr(), m * n))
+                plain = resid0.clone()
+                capi.check(lib.air_hip_linear_epilogue(h, mat.handle, x.data_ptr(), m, plain.data_ptr(),
+                                                       bias.data_ptr(), capi.EPILOGUE_RESIDUAL, None, None, 0.0,
+                                                       dec))
+                torch.cuda.synchronize()
+                assert np.array_equal(bits(act), bits(act_ref)), case
+                assert np.array_equal(bits(resid), bits(resid_ref)), case
+                assert np.array_equal(bits(normed), bits(normed_ref)), case
+                assert np.array_equal(bits(plain), bits(plain_ref)), case
+        x = _dev(torch, helpers.activations(8, k, seed=1))
+        out = torch.empty((8, n), dtype=torch.float32, device="cuda:0")
+        assert lib.air_hip_linear_epilogue(h, mat.handle, x.data_ptr(), 8, out.data_ptr(), None,
+                                           capi.EPILOGUE_STORE, None, None, 0.0, dec) == 1
+        assert lib.air_hip_linear_epilogue(h, mat.handle, x.data_ptr(), 8, x.data_ptr(), None,
+                                           capi.EPILOGUE_RESIDUAL, None, None, 0.0, dec) == 1
+        assert lib.air_hip_linear_epilogue(h, mat.handle, x.data_ptr(), 8, out.data_ptr(), None,
+                                           capi.EPILOGUE_SWIGLU, w.data_ptr(), out.data_ptr(), eps, dec) == 1
+        assert lib.air_hip_linear_epilogue(h, mat.handle, x.data_ptr(), 8, out.data_ptr(), None,
+                                           capi.EPILOGUE_RESIDUAL, w.data_ptr(), None, eps, dec) == 1
+        assert lib.air_hip_linear_epilogue(h, mat.handle, x.data_ptr(), 0, out.data_ptr(), None,
+                                           capi.EPILOGUE_RESIDUAL, None, None, 0.0, dec) == 1
+    finally:
+        hip_ctx.set_decode_path(0)
+        mat.release()
