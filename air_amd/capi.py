@@ -123,6 +123,8 @@ SIGNATURES = {
     "air_hip_decode_linear_fused": (_I, [_P, _P, _P, _P, _P, _P, ctypes.c_double, ctypes.c_int]),
     "air_hip_linear_epilogue": (_I, [_P, _P, _P, _U32, _P, _P, ctypes.c_int, _P, _P, ctypes.c_double, ctypes.c_int]),
     "air_hip_rope_kv_append": (_I, [_P, _P, _P, _U64, _U32, _P, _P, _U32, _U32, _U32, _U32, _U32, _P, _U64]),
+    "air_hip_linear_rope_kv": (_I, [_P, _P, _P, _U32, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P, _U64,
+                                     ctypes.c_int]),
     "air_hip_attention": (_I, [_P, _P, _P, _U64, _U32, _P, _P, _U32, _U32, _U32, _U32, _U64, _P]),
     "air_hip_add_rms_norm": (_I, [_P, _P, _P, _P, _P, _U32, _U64, ctypes.c_double]),
     "air_hip_attention_make_tiles": (_I, [_P, _U32, _U32, _U32, _P, _U32, _P]),

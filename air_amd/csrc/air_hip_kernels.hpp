@@ -223,15 +223,32 @@ hipError_t launch_silu_mul(const float* gate_up, float* out, std::uint32_t m, st
 //     columns i and n/2 + i (launch_silu_mul);
 //   kEpilogueResidual: out [m][n] += the reduced rows, then with
 //     norm_weight, norm_out = rms_norm(out) * norm_weight (launch_add_rms_norm;
-//     norm_out must not alias out).
+//     norm_out must not alias out);
+//   kEpilogueRopeKv: out [m][n] = the reduced q|k|v rows with RoPE applied
+//     and k, v appended to the KV pool (launch_rope_kv_append over rows of
+//     stride n).
 constexpr int kEpilogueResidual = 1;
 constexpr int kEpilogueSwiglu = 2;
+constexpr int kEpilogueRopeKv = 3;
+struct RopeKvArgs {
+    KvLayout kv;
+    const std::int32_t* positions{nullptr};
+    const std::int32_t* tables{nullptr};
+    std::uint32_t layer{0};
+    std::uint32_t q_heads{0};
+    std::uint32_t kv_heads{0};
+    std::uint32_t head_dim{0};
+    std::uint32_t rope_dims{0};
+    const void* table{nullptr};
+    std::uint64_t table_positions{0};
+};
 struct SplitEpilogue {
     int kind{0};
     float* out{nullptr};
     const float* norm_weight{nullptr};
     float* norm_out{nullptr};
     double eps{0.0};
+    const RopeKvArgs* rope{nullptr};
 };
 // Whether the reduction can carry `e` for this shape (alignment, widths).
 bool split_epilogue_fits(const SplitEpilogue& e, const float* partials, const float* bias, std::uint32_t m,

@@ -908,6 +908,46 @@ int air_hip_rope_kv_append(air_hip_context* ctx, const air_hip_kv_layout* kv, fl
     return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "rope_kv_append_kernel");
 }
 
+int air_hip_linear_rope_kv(air_hip_context* ctx, const air_hip_matrix* m, const float* x, uint32_t rows, float* qkv,
+                           const float* bias, const air_hip_kv_layout* kv, const int32_t* positions,
+                           const int32_t* page_tables, uint32_t layer, uint32_t q_heads, uint32_t kv_heads,
+                           uint32_t head_dim, uint32_t rope_dims, const float* table, uint64_t table_positions,
+                           int tactic) {
+    if (!ctx || !m || !x || !qkv || !positions || !page_tables || !table) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    }
+    if (static_cast<const void*>(x) == static_cast<const void*>(qkv)) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "qkv must not alias x");
+    }
+    if (int rc = check_kv(kv); rc != AIR_HIP_OK) return rc;
+    if (layer >= kv->layers) return fail(AIR_HIP_INVALID_ARGUMENT, "layer %u is out of range", layer);
+    if (rope_dims == 0 || rope_dims % 2u != 0 || rope_dims > head_dim || table_positions == 0) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "RoPE needs an even rope_dims <= head_dim and a table");
+    }
+    if (static_cast<uint64_t>(kv_heads) * head_dim != kv->kv_width) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "kv_heads * head_dim must equal the KV width");
+    }
+    const uint64_t q_width = static_cast<uint64_t>(q_heads) * head_dim;
+    if (m->planes.n != q_width + 2u * static_cast<uint64_t>(kv->kv_width)) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "the matrix's %llu outputs are not q|k|v of these heads",
+                    static_cast<unsigned long long>(m->planes.n));
+    }
+    if (rows == 0) return fail(AIR_HIP_INVALID_ARGUMENT, "linear batch width must be non-zero");
+    if (rows > 65535u) return fail(AIR_HIP_UNSUPPORTED, "at most 65535 rows per call");
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const RopeKvArgs args{kv_layout_of(kv), positions, page_tables, layer, q_heads, kv_heads, head_dim, rope_dims,
+                          table, table_positions};
+    const SplitEpilogue e{kEpilogueRopeKv, qkv, nullptr, nullptr, 0.0, &args};
+    bool applied = false;
+    int rc = linear_rows(ctx, m, x, qkv, bias, rows, tactic, &e, &applied);
+    if (rc != AIR_HIP_OK || applied) return rc;
+    const hipError_t err = launch_rope_kv_append(args.kv, qkv, m->planes.n, q_width, rows, positions, page_tables, layer,
+                                                 q_heads, kv_heads, head_dim, rope_dims, table, table_positions,
+                                                 ctx->stream);
+    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "rope_kv_append_kernel");
+}
+
 int air_hip_attention(air_hip_context* ctx, const air_hip_kv_layout* kv, const float* qkv, uint64_t row_stride,
                       uint32_t m, const int32_t* positions, const int32_t* page_tables, uint32_t layer,
                       uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim, uint64_t max_tokens, float* out) {

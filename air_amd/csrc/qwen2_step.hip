@@ -158,11 +158,37 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(KvGeometry g, const
 // column per row): the same arithmetic as rope_kernel followed by
 // kv_append_kernel.  A row whose position lies outside the table is not
 // rotated; a row without a valid page slot is rotated but not stored.
+// Where rope_kv_append_kernel reads q|k|v: the row itself, or (SPLIT) the
+// sum of a K-split linear's partials ([splits][m][stride], split_stride =
+// m * stride floats apart) from zero in split order, plus bias -- the split
+// reduction's arithmetic, so the result is bit-identical to reducing first.
+struct QkvSplit {
+    const float* partials;
+    std::uint32_t splits;
+    std::uint64_t split_stride;
+    const float* bias;
+};
+
+__device__ __forceinline__ float split_sum1(const float* __restrict__ p, std::uint32_t splits, std::uint64_t stride) {
+    float t = 0.0f;
+    for (std::uint32_t s = 0; s < splits; s += 8u) {
+        float q[8];
+#pragma unroll
+        for (std::uint32_t e = 0; e < 8u; ++e) q[e] = p[(s + e < splits ? s + e : splits - 1u) * stride];
+#pragma unroll
+        for (std::uint32_t e = 0; e < 8u; ++e) {
+            if (s + e < splits) t += q[e];
+        }
+    }
+    return t;
+}
+
+template <bool SPLIT>
 __global__ __launch_bounds__(kThreads) void rope_kv_append_kernel(
     KvGeometry g, float* __restrict__ qkv, std::uint64_t stride, std::uint64_t q_width, std::uint32_t m,
     const std::int32_t* __restrict__ positions, const std::int32_t* __restrict__ tables, std::uint32_t layer,
     std::uint32_t q_heads, std::uint32_t kv_heads, std::uint32_t head_dim, std::uint32_t rope_dims,
-    const float2* __restrict__ table, std::uint64_t table_positions) {
+    const float2* __restrict__ table, std::uint64_t table_positions, QkvSplit src) {
 #pragma clang fp contract(off)
     const std::uint32_t r = blockIdx.y;
     if (r >= m) return;
@@ -173,36 +199,50 @@ __global__ __launch_bounds__(kThreads) void rope_kv_append_kernel(
     float* vd = kv_slot(g, ptable, layer, static_cast<std::uint64_t>(pos), true);
     if (!vd) kd = nullptr;  // both or neither, as the separate append
     float* row = qkv + static_cast<std::uint64_t>(r) * stride;
-    float* krow = row + q_width;
+    const float* prow = SPLIT ? src.partials + static_cast<std::uint64_t>(r) * stride : nullptr;
+    // Value of column c of the row's q|k|v.  SPLIT writes every column back
+    // to the row (the plain reduction's output), rotated where RoPE applies.
+    const auto load = [&](std::uint64_t c) __attribute__((always_inline)) -> float {
+        if constexpr (SPLIT) {
+            float t = split_sum1(prow + c, src.splits, src.split_stride);
+            if (src.bias) t += src.bias[c];
+            return t;
+        } else {
+            return row[c];
+        }
+    };
     const std::uint32_t half = rope_dims / 2u;
-    const std::uint32_t tail = head_dim - rope_dims;             // k dims past the rotary part
+    const std::uint32_t tail = head_dim - rope_dims;             // dims past the rotary part
     const std::uint64_t q_items = static_cast<std::uint64_t>(q_heads) * half;
     const std::uint64_t k_items = static_cast<std::uint64_t>(kv_heads) * (half + tail);
-    const std::uint64_t total = q_items + k_items + g.kv_width;  // + the v row
+    const std::uint64_t q_tails = SPLIT ? static_cast<std::uint64_t>(q_heads) * tail : 0u;
+    const std::uint64_t total = q_items + k_items + q_tails + g.kv_width;  // + the v row
     for (std::uint64_t idx = blockIdx.x * static_cast<std::uint64_t>(kThreads) + threadIdx.x; idx < total;
          idx += static_cast<std::uint64_t>(gridDim.x) * kThreads) {
         if (idx < q_items + k_items) {
-            float* base;
+            std::uint64_t base;                                    // first column of the head
             std::uint32_t i;
             float* dst = nullptr;                                  // the k head in the pool
             if (idx < q_items) {
-                base = row + (idx / half) * head_dim;
+                base = (idx / half) * head_dim;
                 i = static_cast<std::uint32_t>(idx % half);
             } else {
                 const std::uint64_t e = idx - q_items;
                 const std::uint32_t h = static_cast<std::uint32_t>(e / (half + tail));
                 const std::uint32_t j = static_cast<std::uint32_t>(e % (half + tail));
-                base = krow + static_cast<std::uint64_t>(h) * head_dim;
+                base = q_width + static_cast<std::uint64_t>(h) * head_dim;
                 if (kd) dst = kd + static_cast<std::uint64_t>(h) * head_dim;
                 if (j >= half) {                                  // unrotated tail dim
                     const std::uint32_t t = rope_dims + (j - half);
-                    if (dst) dst[t] = base[t];
+                    const float v = load(base + t);
+                    if (SPLIT) row[base + t] = v;
+                    if (dst) dst[t] = v;
                     continue;
                 }
                 i = j;
             }
-            const float first = base[i];
-            const float second = base[i + half];
+            const float first = load(base + i);
+            const float second = load(base + i + half);
             float lo = first, hi = second;
             if (rotate) {
                 const float2 cs = table[static_cast<std::uint64_t>(pos) * half + i];
@@ -212,16 +252,29 @@ __global__ __launch_bounds__(kThreads) void rope_kv_append_kernel(
                 const float d = second * cs.x;
                 lo = a - b;
                 hi = c + d;
-                base[i] = lo;
-                base[i + half] = hi;
+            }
+            if (rotate || SPLIT) {
+                row[base + i] = lo;
+                row[base + i + half] = hi;
             }
             if (dst) {
                 dst[i] = lo;
                 dst[i + half] = hi;
             }
-        } else if (vd) {
-            const std::uint64_t i = idx - q_items - k_items;
-            vd[i] = krow[g.kv_width + i];
+        } else if (idx < q_items + k_items + q_tails) {           // SPLIT: q tail dims
+            const std::uint64_t e = idx - q_items - k_items;
+            const std::uint64_t c = (e / tail) * head_dim + rope_dims + e % tail;
+            row[c] = load(c);
+        } else {
+            const std::uint64_t i = idx - q_items - k_items - q_tails;
+            const std::uint64_t c = q_width + g.kv_width + i;
+            if (SPLIT) {
+                const float v = load(c);
+                row[c] = v;
+                if (vd) vd[i] = v;
+            } else if (vd) {
+                vd[i] = row[c];
+            }
         }
     }
 }
@@ -598,21 +651,39 @@ hipError_t launch_attention(const KvLayout& kv, const float* qkv, std::uint64_t 
     return hipGetLastError();
 }
 
+namespace {
+hipError_t rope_kv_append(const KvLayout& kv, float* qkv, std::uint64_t stride, std::uint64_t q_width,
+                          std::uint32_t m, const std::int32_t* positions, const std::int32_t* tables,
+                          std::uint32_t layer, std::uint32_t q_heads, std::uint32_t kv_heads, std::uint32_t head_dim,
+                          std::uint32_t rope_dims, const void* table, std::uint64_t table_positions,
+                          const QkvSplit* split, hipStream_t stream) {
+    const KvGeometry g{kv.pool, kv.page_tokens, kv.kv_width, kv.layers, kv.max_pages, kv.pool_pages};
+    const std::uint64_t per_row = static_cast<std::uint64_t>(q_heads) * (rope_dims / 2u) +
+                                  static_cast<std::uint64_t>(kv_heads) * (rope_dims / 2u + head_dim - rope_dims) +
+                                  (split ? static_cast<std::uint64_t>(q_heads) * (head_dim - rope_dims) : 0u) +
+                                  kv.kv_width;
+    const std::uint64_t blocks = ceil_div(per_row, static_cast<std::uint64_t>(kThreads));
+    const unsigned gx = static_cast<unsigned>(blocks < 64u ? blocks : 64u);
+    if (split) {
+        hipLaunchKernelGGL(rope_kv_append_kernel<true>, dim3(gx, m), dim3(kThreads), 0, stream, g, qkv, stride,
+                           q_width, m, positions, tables, layer, q_heads, kv_heads, head_dim, rope_dims,
+                           static_cast<const float2*>(table), table_positions, *split);
+    } else {
+        hipLaunchKernelGGL(rope_kv_append_kernel<false>, dim3(gx, m), dim3(kThreads), 0, stream, g, qkv, stride,
+                           q_width, m, positions, tables, layer, q_heads, kv_heads, head_dim, rope_dims,
+                           static_cast<const float2*>(table), table_positions, QkvSplit{});
+    }
+    return hipGetLastError();
+}
+} // namespace
+
 hipError_t launch_rope_kv_append(const KvLayout& kv, float* qkv, std::uint64_t stride, std::uint64_t q_width,
                                  std::uint32_t m, const std::int32_t* positions, const std::int32_t* tables,
                                  std::uint32_t layer, std::uint32_t q_heads, std::uint32_t kv_heads,
                                  std::uint32_t head_dim, std::uint32_t rope_dims, const void* table,
                                  std::uint64_t table_positions, hipStream_t stream) {
-    const KvGeometry g{kv.pool, kv.page_tokens, kv.kv_width, kv.layers, kv.max_pages, kv.pool_pages};
-    const std::uint64_t per_row = static_cast<std::uint64_t>(q_heads) * (rope_dims / 2u) +
-                                  static_cast<std::uint64_t>(kv_heads) * (rope_dims / 2u + head_dim - rope_dims) +
-                                  kv.kv_width;
-    const std::uint64_t blocks = ceil_div(per_row, static_cast<std::uint64_t>(kThreads));
-    const unsigned gx = static_cast<unsigned>(blocks < 64u ? blocks : 64u);
-    hipLaunchKernelGGL(rope_kv_append_kernel, dim3(gx, m), dim3(kThreads), 0, stream, g, qkv, stride, q_width, m,
-                       positions, tables, layer, q_heads, kv_heads, head_dim, rope_dims,
-                       static_cast<const float2*>(table), table_positions);
-    return hipGetLastError();
+    return rope_kv_append(kv, qkv, stride, q_width, m, positions, tables, layer, q_heads, kv_heads, head_dim,
+                          rope_dims, table, table_positions, nullptr, stream);
 }
 
 hipError_t launch_silu_mul(const float* gate_up, float* out, std::uint32_t m, std::uint64_t ffn, hipStream_t stream) {
@@ -633,6 +704,7 @@ bool split_epilogue_fits(const SplitEpilogue& e, const float* partials, const fl
     if (e.kind == kEpilogueSwiglu) {
         return n % 8u == 0 && static_cast<std::uint64_t>(m) * n / 4u < (1ull << 32);
     }
+    if (e.kind == kEpilogueRopeKv) return e.rope != nullptr;
     if (e.kind == kEpilogueResidual) {
         return n % 4u == 0 && n <= static_cast<std::uint64_t>(kNormMaxVec) * 4u * kNormThreads &&
                (!e.norm_weight || (aligned(e.norm_weight) && aligned(e.norm_out)));
@@ -643,6 +715,13 @@ bool split_epilogue_fits(const SplitEpilogue& e, const float* partials, const fl
 hipError_t launch_split_epilogue(const float* partials, std::uint32_t splits, std::uint32_t m, std::uint64_t n,
                                  const float* bias, const SplitEpilogue& e, hipStream_t stream) {
     if (!split_epilogue_fits(e, partials, bias, m, n)) return hipErrorInvalidValue;
+    if (e.kind == kEpilogueRopeKv) {
+        const RopeKvArgs& a = *e.rope;
+        const QkvSplit split{partials, splits, static_cast<std::uint64_t>(m) * n, bias};
+        return rope_kv_append(a.kv, e.out, n, static_cast<std::uint64_t>(a.q_heads) * a.head_dim, m, a.positions,
+                              a.tables, a.layer, a.q_heads, a.kv_heads, a.head_dim, a.rope_dims, a.table,
+                              a.table_positions, &split, stream);
+    }
     if (e.kind == kEpilogueSwiglu) {
         const std::uint32_t f4 = static_cast<std::uint32_t>(n / 8u);
         const std::uint32_t total4 = m * f4;

@@ -20,6 +20,7 @@
 
 struct air_hip_context;
 struct air_hip_matrix;
+struct air_hip_kv_layout;
 
 namespace air {
 
@@ -114,6 +115,14 @@ public:
     [[nodiscard]] Status linear_epilogue(std::uint32_t layer, LinearRole role, const float* x, std::uint32_t rows,
                                          float* out, int epilogue, const float* norm_weight, float* norm_out,
                                          double eps, QuantizedLinearExecutionKind tactic) const;
+    // The q|k|v linear with RoPE and the KV append after it
+    // (air_hip_linear_rope_kv; carried by the split reduction at M 2..64).
+    [[nodiscard]] Status linear_rope_kv(std::uint32_t layer, LinearRole role, const float* x, std::uint32_t rows,
+                                        float* qkv, const air_hip_kv_layout* kv, const std::int32_t* positions,
+                                        const std::int32_t* page_tables, std::uint32_t q_heads,
+                                        std::uint32_t kv_heads, std::uint32_t head_dim, std::uint32_t rope_dims,
+                                        const float* rope_table, std::uint64_t table_positions,
+                                        QuantizedLinearExecutionKind tactic) const;
     [[nodiscard]] Result<HipLinearInfo> linear_info(std::uint32_t layer, LinearRole role) const;
     [[nodiscard]] bool fused_qkv() const noexcept { return fused_qkv_; }
     [[nodiscard]] bool fused_gate_up() const noexcept { return fused_gate_up_; }

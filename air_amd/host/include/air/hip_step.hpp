@@ -107,7 +107,7 @@ private:
     [[nodiscard]] Status layers(std::uint32_t m, std::uint64_t max_tokens, std::uint32_t table_pages,
                                 QuantizedLinearExecutionKind tactic, std::uint32_t tiles);
     [[nodiscard]] Status attention(std::uint32_t layer, std::uint32_t m, std::uint64_t max_tokens,
-                                   std::uint32_t table_pages, std::uint32_t tiles);
+                                   std::uint32_t table_pages, std::uint32_t tiles, bool rope_done = false);
     [[nodiscard]] Status project(std::uint32_t layer, LinearRole fused, LinearRole first, LinearRole second,
                                  LinearRole third, const float* x, float* y, std::uint32_t m,
                                  QuantizedLinearExecutionKind tactic);

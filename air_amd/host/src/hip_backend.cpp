@@ -335,6 +335,28 @@ Status HipPreparedModel::linear_epilogue(std::uint32_t layer, LinearRole role, c
         air_hip_linear_epilogue(ctx_, l->matrix, x, rows, out, l->bias, epilogue, norm_weight, norm_out, eps, t));
 }
 
+Status HipPreparedModel::linear_rope_kv(std::uint32_t layer, LinearRole role, const float* x, std::uint32_t rows,
+                                        float* qkv, const air_hip_kv_layout* kv, const std::int32_t* positions,
+                                        const std::int32_t* page_tables, std::uint32_t q_heads,
+                                        std::uint32_t kv_heads, std::uint32_t head_dim, std::uint32_t rope_dims,
+                                        const float* rope_table, std::uint64_t table_positions,
+                                        QuantizedLinearExecutionKind tactic) const {
+    const auto* l = find(layer, role);
+    if (!l) {
+        return Status::invalid_argument(std::string("no resident linear for role ") + to_string(role) + " at layer " +
+                                        std::to_string(layer));
+    }
+    int t = AIR_HIP_LINEAR_AUTO;
+    switch (tactic) {
+    case QuantizedLinearExecutionKind::hip_decode: t = AIR_HIP_LINEAR_DECODE; break;
+    case QuantizedLinearExecutionKind::hip_prefill: t = AIR_HIP_LINEAR_PREFILL; break;
+    default:
+        return Status::unsupported(std::string("HIP backend does not provide linear tactic ") + to_string(tactic));
+    }
+    return hip_status(air_hip_linear_rope_kv(ctx_, l->matrix, x, rows, qkv, l->bias, kv, positions, page_tables, layer,
+                                             q_heads, kv_heads, head_dim, rope_dims, rope_table, table_positions, t));
+}
+
 Status HipPreparedModel::decode_linear_fused(std::uint32_t layer, LinearRole role, const float* x, float* y,
                                              const float* norm_weight, double eps, int epilogue) const {
     const auto* l = find(layer, role);

@@ -377,17 +377,21 @@ Status HipStepEngine::project(std::uint32_t layer, LinearRole fused, LinearRole 
     return Status::ok();
 }
 
-// RoPE and the KV append of layer l, then attention of the step's rows over
-// their sequences' keys (q|k|v in qkv_, output in att_).
+// RoPE and the KV append of layer l (unless the q|k|v linear did them),
+// then attention of the step's rows over their sequences' keys (q|k|v in
+// qkv_, output in att_).
 Status HipStepEngine::attention(std::uint32_t l, std::uint32_t m, std::uint64_t max_tokens, std::uint32_t table_pages,
-                                std::uint32_t tiles) {
+                                std::uint32_t tiles, bool rope_done) {
     const auto& c = prepared_.model().config();
     air_hip_context* ctx = prepared_.context();
     const air_hip_kv_layout kv{pool_, page_tokens_, kv_width_, c.layer_count, table_pages, pool_pages_};
-    int rc = air_hip_rope_kv_append(ctx, &kv, qkv_, qkv_width_, m, positions_dev_, tables_dev_, l,
+    int rc = AIR_HIP_OK;
+    if (!rope_done) {
+        rc = air_hip_rope_kv_append(ctx, &kv, qkv_, qkv_width_, m, positions_dev_, tables_dev_, l,
                                     c.attention_head_count, c.kv_head_count, head_dim_, c.rope_dimension_count,
                                     rope_table_, c.context_length);
-    if (rc != AIR_HIP_OK) return hip_status(rc);
+        if (rc != AIR_HIP_OK) return hip_status(rc);
+    }
     rc = tiles ? air_hip_attention_online(ctx, &kv, qkv_, qkv_width_, m, positions_dev_, tables_dev_, l,
                                           c.attention_head_count, c.kv_head_count, head_dim_,
                                           reinterpret_cast<const air_hip_attention_tile*>(tiles_dev_), tiles,
@@ -451,18 +455,30 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
     // whose split reduction carries them: measured on the 7B shapes at
     // M = 30 that saves three launches of 4-5 us per layer.  Prefill widths
     // keep the separate kernels (the epilogue route would add a context
-    // buffer as large as the step's gate|up rows).
+    // buffer as large as the step's gate|up rows).  The q|k|v linear does
+    // RoPE and the KV append the same way.
     const bool epilogues = tactic == QuantizedLinearExecutionKind::hip_decode && m <= AIR_HIP_MAX_DECODE_ROWS;
     if ((rc = air_hip_rms_norm(ctx, hidden_, attn_norm_[0], normed_, m, embed_, eps)) != AIR_HIP_OK) {
         return hip_status(rc);
     }
     for (std::uint32_t l = 0; l < c.layer_count; ++l) {
-        if (Status s = project(l, LinearRole::attn_qkv, LinearRole::attn_q, LinearRole::attn_k, LinearRole::attn_v,
-                               normed_, qkv_, m, tactic);
-            !s) {
-            return s;
+        if (epilogues && prepared_.fused_qkv()) {
+            const air_hip_kv_layout kv{pool_, page_tokens_, kv_width_, c.layer_count, table_pages, pool_pages_};
+            if (Status s = prepared_.linear_rope_kv(l, LinearRole::attn_qkv, normed_, m, qkv_, &kv, positions_dev_,
+                                                    tables_dev_, c.attention_head_count, c.kv_head_count, head_dim_,
+                                                    c.rope_dimension_count, rope_table_, c.context_length, tactic);
+                !s) {
+                return s;
+            }
+            if (Status s = attention(l, m, max_tokens, table_pages, tiles, true); !s) return s;
+        } else {
+            if (Status s = project(l, LinearRole::attn_qkv, LinearRole::attn_q, LinearRole::attn_k,
+                                   LinearRole::attn_v, normed_, qkv_, m, tactic);
+                !s) {
+                return s;
+            }
+            if (Status s = attention(l, m, max_tokens, table_pages, tiles); !s) return s;
         }
-        if (Status s = attention(l, m, max_tokens, table_pages, tiles); !s) return s;
         if (epilogues) {
             if (Status s = prepared_.linear_epilogue(l, LinearRole::attn_output, att_, m, hidden_,
                                                      AIR_HIP_EPILOGUE_RESIDUAL, ffn_norm_[l], normed_, eps, tactic);

@@ -332,6 +332,21 @@ int air_hip_rope_kv_append(air_hip_context* ctx, const air_hip_kv_layout* kv, fl
                            uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim, uint32_t rope_dims,
                            const float* table, uint64_t table_positions);
 
+/* The q|k|v linear and air_hip_rope_kv_append in one call: qkv [rows][n]
+ * (n = (q_heads + 2 * kv_heads) * head_dim) receives x W^T + bias with the q
+ * and k heads rotated, and k, v are appended to the pool -- bit-identical to
+ * air_hip_linear (same tactic) followed by air_hip_rope_kv_append over rows
+ * of stride n.  Where the linear runs as a skinny launch with a K split
+ * (decode widths 2..64), its split reduction does the RoPE and the append,
+ * so they cost no launch of their own.  qkv must not alias x.  Replaces the
+ * executor's q|k|v projection, apply_rope and KV store sequence
+ * (cuda_backend.cu:883-906, 1156-1173; reference_executor.cpp:37-72). */
+int air_hip_linear_rope_kv(air_hip_context* ctx, const air_hip_matrix* matrix, const float* x, uint32_t rows,
+                           float* qkv, const float* bias, const air_hip_kv_layout* kv, const int32_t* positions,
+                           const int32_t* page_tables, uint32_t layer, uint32_t q_heads, uint32_t kv_heads,
+                           uint32_t head_dim, uint32_t rope_dims, const float* table, uint64_t table_positions,
+                           int tactic);
+
 /* Attention of every row's q heads over tokens 0..positions[r] of its
  * sequence for one layer (attention, reference_executor.cpp:74-138):
  * out[r][q_heads * head_dim].  max_tokens bounds positions[r] + 1 and sizes

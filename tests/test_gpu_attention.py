@@ -14,6 +14,7 @@ import numpy as np
 import pytest
 
 from air_amd import capi
+from tests import helpers
 
 
 def test_tiles_for_decode_and_prefill_runs():
@@ -187,3 +188,71 @@ def test_rope_kv_append_matches_separate_calls(torch_cuda, hip_ctx, q_heads, kv_
                                      tab_d.data_ptr(), layer, q_heads, kv_heads + 1, head, rope_dims,
                                      rope_d.data_ptr(), table_positions)
     assert bad == 1 and b"KV width" in lib.air_hip_last_error()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("q_heads,kv_heads,head,rope_dims", [(28, 4, 128, 128), (4, 2, 64, 32)])
+def test_linear_rope_kv_matches_separate_calls(torch_cuda, hip_ctx, q_heads, kv_heads, head, rope_dims):
+    """air_hip_linear_rope_kv leaves q|k|v and the pool bit-identical to
+    air_hip_linear then air_hip_rope_kv_append, on the routes where the
+    linear's split reduction does the RoPE and the append (skinny kernel
+    with a K split) and where it does not (no split, the single-launch
+    kernel); rows as in the test above (past the table, no page, negative
+    position)."""
+    torch = torch_cuda
+    dev = torch.device("cuda:0")
+    page_tokens, layers, layer, max_pages, pool_pages = 16, 3, 1, 4, 12
+    kv_width = kv_heads * head
+    n, k = q_heads * head + 2 * kv_width, 1024
+    rng = np.random.default_rng(head + rope_dims + 1)
+    table_positions = 40
+    positions = [0, 5, 17, 39, 45, 63, 3, -1]
+    tables = [list(rng.permutation(pool_pages)[:max_pages]) for _ in positions]
+    tables[6][0] = -1
+    m = len(positions)
+    half = rope_dims // 2
+    ang = rng.uniform(0.0, 6.28, (table_positions, half))
+    rope_d = torch.from_numpy(np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)).to(dev)
+    pool_h = rng.standard_normal(pool_pages * layers * 2 * page_tokens * kv_width).astype(np.float32)
+    pos_d = torch.tensor(positions, dtype=torch.int32, device=dev)
+    tab_d = torch.tensor(np.array(tables, dtype=np.int32), device=dev)
+    canon = helpers.weights(capi.TYPE_Q8_0, k, n, seed=n + 3)
+    mat = capi.Matrix(hip_ctx, capi.TYPE_Q8_0, k, n, canon, canon.nbytes, on_device=False)
+    x = torch.from_numpy(helpers.activations(m, k, seed=n) * 2.0).to(dev)
+    bias = torch.from_numpy(helpers.activations(1, n, seed=n + 1)[0] * 0.1).to(dev)
+    lib = capi.lib()
+    h = hip_ctx.handle
+    try:
+        for path in [(0, 0, 0), (2, 1, 1), (2, 1, 3), (2, 2, 2)]:
+            hip_ctx.set_decode_path(*path)
+            outs = []
+            for fused in (False, True):
+                pool = torch.from_numpy(pool_h).to(dev)
+                kv = capi.KvLayout(pool.data_ptr(), page_tokens, kv_width, layers, max_pages, pool_pages)
+                qkv = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+                if fused:
+                    capi.check(lib.air_hip_linear_rope_kv(h, mat.handle, x.data_ptr(), m, qkv.data_ptr(),
+                                                          bias.data_ptr(), ctypes.byref(kv), pos_d.data_ptr(),
+                                                          tab_d.data_ptr(), layer, q_heads, kv_heads, head,
+                                                          rope_dims, rope_d.data_ptr(), table_positions,
+                                                          capi.LINEAR_DECODE))
+                else:
+                    capi.check(lib.air_hip_linear(h, mat.handle, x.data_ptr(), qkv.data_ptr(), bias.data_ptr(), m,
+                                                  capi.LINEAR_DECODE))
+                    capi.check(lib.air_hip_rope_kv_append(h, ctypes.byref(kv), qkv.data_ptr(), n, m,
+                                                          pos_d.data_ptr(), tab_d.data_ptr(), layer, q_heads,
+                                                          kv_heads, head, rope_dims, rope_d.data_ptr(),
+                                                          table_positions))
+                torch.cuda.synchronize()
+                outs.append((qkv.cpu().numpy(), pool.cpu().numpy()))
+            (q0, p0), (q1, p1) = outs
+            assert not np.array_equal(p0, pool_h), path
+            assert np.array_equal(q1.view(np.uint32), q0.view(np.uint32)), path
+            assert np.array_equal(p1.view(np.uint32), p0.view(np.uint32)), path
+        bad = lib.air_hip_linear_rope_kv(h, mat.handle, x.data_ptr(), m, qkv.data_ptr(), None, ctypes.byref(kv),
+                                         pos_d.data_ptr(), tab_d.data_ptr(), layer, q_heads + 1, kv_heads, head,
+                                         rope_dims, rope_d.data_ptr(), table_positions, capi.LINEAR_DECODE)
+        assert bad == 1 and b"q|k|v" in lib.air_hip_last_error()
+    finally:
+        hip_ctx.set_decode_path(0)
+        mat.release()
