@@ -35,6 +35,7 @@ TYPE_NAMES = {TYPE_Q4_0: "q4_0", TYPE_Q8_0: "q8_0", TYPE_Q4_K: "q4_k"}
 EPILOGUE_STORE = 0
 EPILOGUE_RESIDUAL = 1
 EPILOGUE_SWIGLU = 2
+EPILOGUE_RESIDUAL_LOAD = 3
 
 LINEAR_AUTO = 0
 LINEAR_DECODE = 1

@@ -123,4 +123,29 @@ __device__ __forceinline__ void split8(const float (&v)[8], float s, half8v& hi,
     }
 }
 
+// Stores run r (eight consecutive activations v of row m; run r = 4 * block
+// + g) of a row-scaled activation split: hi and lo f16 records of the
+// skinny kernel's tile layout (xs[block][mp / 16][hi, lo][64 lanes]), and
+// for g == 0 the block's scaled sum (block_sums[block][mp]).  The four runs
+// of a block must sit in four adjacent active lanes (their sums are combined
+// across lanes).
+__device__ __forceinline__ void emit_split_run(std::uint64_t r, const float (&v)[8], float s, std::uint32_t m,
+                                               std::uint32_t mp, uint4* __restrict__ xs,
+                                               float* __restrict__ block_sums) {
+    const std::uint32_t mtiles = mp / 16u;
+    const std::uint64_t b = r >> 2;
+    const std::uint32_t g = static_cast<std::uint32_t>(r & 3u);
+    half8v hi, lo;
+    split8(v, s, hi, lo);
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sum += v[e] * s;
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    const std::uint32_t lane = (m & 15u) + 16u * g;
+    xs[((b * mtiles + (m >> 4)) * 2u + 0u) * 64u + lane] = __builtin_bit_cast(uint4, hi);
+    xs[((b * mtiles + (m >> 4)) * 2u + 1u) * 64u + lane] = __builtin_bit_cast(uint4, lo);
+    if (g == 0u) block_sums[b * mp + m] = sum;
+}
+
 } // namespace air_hip

@@ -224,6 +224,9 @@ hipError_t launch_silu_mul(const float* gate_up, float* out, std::uint32_t m, st
 //   kEpilogueResidual: out [m][n] += the reduced rows, then with
 //     norm_weight, norm_out = rms_norm(out) * norm_weight (launch_add_rms_norm;
 //     norm_out must not alias out);
+//     With `load`, norm_out is also split into that activation workspace
+//     as launch_split_activations_rows splits it (kp = 32 * load_blocks), so
+//     the next linear on norm_out needs no split launch;
 //   kEpilogueRopeKv: out [m][n] = the reduced q|k|v rows with RoPE applied
 //     and k, v appended to the KV pool (launch_rope_kv_append over rows of
 //     stride n).
@@ -249,6 +252,8 @@ struct SplitEpilogue {
     float* norm_out{nullptr};
     double eps{0.0};
     const RopeKvArgs* rope{nullptr};
+    const SplitWorkspace* load{nullptr};
+    std::uint32_t load_blocks{0};
 };
 // Whether the reduction can carry `e` for this shape (alignment, widths).
 bool split_epilogue_fits(const SplitEpilogue& e, const float* partials, const float* bias, std::uint32_t m,

@@ -39,6 +39,11 @@ struct air_hip_context {
     std::uint64_t loaded_k{0};       // width of the activations in the workspace
     std::uint32_t loaded_rows{0};    // rows of the activations in the workspace (0 = none)
     bool loaded_row_scaled{false};   // split with one scale per row (skinny kernel layout)
+    // The rows the loaded activations were split from by an epilogue
+    // (AIR_HIP_EPILOGUE_RESIDUAL_LOAD); the next linear on the same rows
+    // uses them instead of splitting again.  Null after any other load and
+    // once used.
+    const void* loaded_source{nullptr};
     DecodeTuning tuning{};
     // Cross-workgroup K-split of the fused decode linear: partial sums and one
     // arrival counter per row group.  Counters are zeroed when allocated and
@@ -151,6 +156,17 @@ int ensure_workspace(air_hip_context* ctx, std::uint64_t bytes) {
     return grow_buffer(ctx, &ctx->workspace, &ctx->workspace_bytes, bytes, "workspace", ctx->loaded_rows != 0);
 }
 
+// Loads x as the activations of a loaded linear unless the epilogue of the
+// call just before it already split exactly these rows (`ready` = the source
+// it recorded, taken by the linear entry point) into the workspace.
+int load_activations_for(air_hip_context* ctx, const float* x, std::uint64_t k, std::uint32_t rows,
+                         const void* ready) {
+    const bool row_scaled = rows <= AIR_HIP_MAX_DECODE_ROWS && ctx->decode_path != 1u;
+    const bool split = ready == x && ctx->loaded_k == k && ctx->loaded_rows == rows &&
+                       ctx->loaded_row_scaled == row_scaled;
+    return split ? AIR_HIP_OK : air_hip_activations_load(ctx, x, k, rows);
+}
+
 int ensure_prefill_workspace(air_hip_context* ctx, std::uint64_t bytes) {
     return grow_buffer(ctx, &ctx->prefill_workspace, &ctx->prefill_workspace_bytes, bytes, "prefill workspace");
 }
@@ -188,7 +204,7 @@ const SplitEpilogue* reduction_epilogue(air_hip_context* ctx, const air_hip_matr
 // Skinny decode linear straight from the f32 rows (M = 2..64): one launch
 // (two with a K split), no activation workspace.
 int run_skinny_x(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y, const float* bias,
-                 std::uint32_t rows, const SplitEpilogue* epilogue = nullptr, bool* applied = nullptr) {
+                 std::uint32_t rows, const SplitEpilogue* epilogue, bool* applied, const void* ready) {
     const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits);
     // The in-workgroup split repeats the activation split in every
     // workgroup: it pays on narrow matrices, where the separate split launch
@@ -197,7 +213,7 @@ int run_skinny_x(air_hip_context* ctx, const air_hip_matrix* m, const float* x, 
     // Q4_K with four activation tiles would also spill in it.
     const bool narrow = m->planes.nt <= 512u && (rows <= 32u || m->planes.k <= 4096u);
     if (!narrow || (m->planes.type == kQ4_K && shape.mt == 4u)) {
-        int rc = air_hip_activations_load(ctx, x, m->planes.k, rows);
+        int rc = load_activations_for(ctx, x, m->planes.k, rows, ready);
         if (rc != AIR_HIP_OK) return rc;
         return linear_loaded(ctx, m, y, bias, AIR_HIP_LINEAR_DECODE, epilogue, applied);
     }
@@ -539,6 +555,7 @@ int air_hip_dequantize_canonical(air_hip_context* ctx, int type, const void* can
 int air_hip_decode_linear_fused(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y,
                                 const float* bias, const float* norm_weight, double eps, int epilogue) {
     if (!ctx || !m || !x || !y) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix, x and y must not be null");
+    ctx->loaded_source = nullptr;
     if (static_cast<const void*>(x) == static_cast<const void*>(y)) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "y must not alias x");
     }
@@ -591,6 +608,7 @@ int air_hip_activations_load(air_hip_context* ctx, const float* x, uint64_t k, u
     ctx->loaded_k = k;
     ctx->loaded_rows = rows;
     ctx->loaded_row_scaled = row_scaled;
+    ctx->loaded_source = nullptr;
     return AIR_HIP_OK;
 }
 
@@ -605,6 +623,7 @@ namespace {
 int linear_loaded(air_hip_context* ctx, const air_hip_matrix* m, float* y, const float* bias, int tactic,
                   const SplitEpilogue* epilogue, bool* applied) {
     if (!ctx || !m || !y) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix and y must not be null");
+    ctx->loaded_source = nullptr;
     if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
     if (tactic != AIR_HIP_LINEAR_AUTO && tactic != AIR_HIP_LINEAR_DECODE && tactic != AIR_HIP_LINEAR_PREFILL) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "unknown linear tactic %d", tactic);
@@ -652,6 +671,8 @@ int linear_loaded(air_hip_context* ctx, const air_hip_matrix* m, float* y, const
 // in its reduction (*applied set, y not written).
 int linear_rows(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y, const float* bias,
                 uint32_t rows, int tactic, const SplitEpilogue* epilogue, bool* applied) {
+    const void* ready = ctx ? ctx->loaded_source : nullptr;  // good for this call only
+    if (ctx) ctx->loaded_source = nullptr;
     if (!ctx || !m || !x || !y) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix, x and y must not be null");
     if (static_cast<const void*>(x) == static_cast<const void*>(y)) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "y must not alias x");
@@ -693,7 +714,7 @@ int linear_rows(air_hip_context* ctx, const air_hip_matrix* m, const float* x, f
                                   ((m->planes.n <= 4096u && m->planes.k <= 4096u) ||
                                    (rows <= 4u && weight_bytes >= (256ull << 20)));
         if (ctx->decode_path == 2u || (ctx->decode_path == 0u && !prefer_fused)) {
-            return run_skinny_x(ctx, m, x, y, bias, rows, epilogue, applied);
+            return run_skinny_x(ctx, m, x, y, bias, rows, epilogue, applied, ready);
         }
         const FusedShape shape = plan_decode_fused(m->planes, rows, ctx->tuning);
         if (shape.k_splits > 1u) {
@@ -712,9 +733,9 @@ int linear_rows(air_hip_context* ctx, const air_hip_matrix* m, const float* x, f
         if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
         DeviceScope scope(ctx->device);
         if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-        return run_skinny_x(ctx, m, x, y, bias, rows, epilogue, applied);
+        return run_skinny_x(ctx, m, x, y, bias, rows, epilogue, applied, ready);
     }
-    int rc = air_hip_activations_load(ctx, x, m->planes.k, rows);
+    int rc = load_activations_for(ctx, x, m->planes.k, rows, ready);
     if (rc != AIR_HIP_OK) return rc;
     return linear_loaded(ctx, m, y, bias, tactic, epilogue, applied);
 }
@@ -732,8 +753,13 @@ int air_hip_linear_epilogue(air_hip_context* ctx, const air_hip_matrix* m, const
                             const float* bias, int epilogue, const float* norm_weight, float* norm_out, double eps,
                             int tactic) {
     if (!ctx || !m || !x || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix, x and out must not be null");
-    if (epilogue != AIR_HIP_EPILOGUE_RESIDUAL && epilogue != AIR_HIP_EPILOGUE_SWIGLU) {
-        return fail(AIR_HIP_INVALID_ARGUMENT, "epilogue must be RESIDUAL or SWIGLU, not %d", epilogue);
+    if (epilogue != AIR_HIP_EPILOGUE_RESIDUAL && epilogue != AIR_HIP_EPILOGUE_SWIGLU &&
+        epilogue != AIR_HIP_EPILOGUE_RESIDUAL_LOAD) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "epilogue must be RESIDUAL, SWIGLU or RESIDUAL_LOAD, not %d", epilogue);
+    }
+    const bool load = epilogue == AIR_HIP_EPILOGUE_RESIDUAL_LOAD;
+    if (load && (!norm_weight || m->planes.n % 32u != 0u)) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "RESIDUAL_LOAD needs a norm and an output width that is a multiple of 32");
     }
     if (static_cast<const void*>(x) == static_cast<const void*>(out)) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "out must not alias x");
@@ -755,20 +781,44 @@ int air_hip_linear_epilogue(air_hip_context* ctx, const air_hip_matrix* m, const
                          static_cast<std::uint64_t>(rows) * n * sizeof(float), "epilogue rows");
     if (rc != AIR_HIP_OK) return rc;
     float* y = static_cast<float*>(ctx->epilogue_rows);
-    const SplitEpilogue e{epilogue == AIR_HIP_EPILOGUE_SWIGLU ? kEpilogueSwiglu : kEpilogueResidual, out, norm_weight,
-                          norm_out, eps};
+    SplitEpilogue e{epilogue == AIR_HIP_EPILOGUE_SWIGLU ? kEpilogueSwiglu : kEpilogueResidual, out, norm_weight,
+                    norm_out, eps};
+    // RESIDUAL_LOAD: the workspace holds the split of norm_out afterwards.
+    // Reserved first for this linear's own activations too, so the linear
+    // cannot move it after the epilogue's pointers are taken.
+    SplitWorkspace ws{};
+    const std::uint64_t kp_out = ceil_div(n, kSplitK) * kSplitK;
+    if (load) {
+        const std::uint64_t kp_in = ceil_div(m->planes.k, kSplitK) * kSplitK;
+        rc = ensure_workspace(ctx, std::max(split_workspace_bytes(kp_out, rows), split_workspace_bytes(kp_in, rows)));
+        if (rc != AIR_HIP_OK) return rc;
+        ws = carve_split_workspace(ctx->workspace, kp_out, rows);
+        if (rows <= AIR_HIP_MAX_DECODE_ROWS && ctx->decode_path != 1u) {
+            e.load = &ws;
+            e.load_blocks = static_cast<std::uint32_t>(kp_out / 32u);
+        }
+    }
     bool applied = false;
     rc = linear_rows(ctx, m, x, y, bias, rows, tactic, &e, &applied);
-    if (rc != AIR_HIP_OK || applied) return rc;
-    hipError_t err;
-    if (epilogue == AIR_HIP_EPILOGUE_SWIGLU) {
-        err = launch_silu_mul(y, out, rows, n / 2u, ctx->stream);
-    } else if (norm_weight) {
-        err = launch_add_rms_norm(out, y, norm_weight, norm_out, rows, n, eps, ctx->stream);
-    } else {
-        err = launch_add(out, y, static_cast<std::uint64_t>(rows) * n, ctx->stream);
+    if (rc != AIR_HIP_OK) return rc;
+    if (!applied) {
+        hipError_t err;
+        if (epilogue == AIR_HIP_EPILOGUE_SWIGLU) {
+            err = launch_silu_mul(y, out, rows, n / 2u, ctx->stream);
+        } else if (norm_weight) {
+            err = launch_add_rms_norm(out, y, norm_weight, norm_out, rows, n, eps, ctx->stream);
+        } else {
+            err = launch_add(out, y, static_cast<std::uint64_t>(rows) * n, ctx->stream);
+        }
+        if (err != hipSuccess) return hip_fail(err, "linear epilogue");
+        if (load && (rc = air_hip_activations_load(ctx, norm_out, n, rows)) != AIR_HIP_OK) return rc;
+    } else if (load) {
+        ctx->loaded_k = n;
+        ctx->loaded_rows = rows;
+        ctx->loaded_row_scaled = true;
     }
-    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "linear epilogue");
+    if (load) ctx->loaded_source = norm_out;
+    return AIR_HIP_OK;
 }
 
 

@@ -302,21 +302,8 @@ __global__ __launch_bounds__(kSplitThreads) void split_rows_kernel(const float* 
     for (unsigned w = 1; w < kSplitThreads / 64; ++w) amax = fmaxf(amax, red[w]);
     float s, inv;
     block_scale(amax, s, inv);
-    const std::uint32_t mtiles = mp / 16u;
     const auto emit = [&](std::uint64_t r, const float (&v)[8]) __attribute__((always_inline)) {
-        const std::uint64_t b = r >> 2;
-        const std::uint32_t g = static_cast<std::uint32_t>(r & 3u);
-        half8v hi, lo;
-        split8(v, s, hi, lo);
-        float sum = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sum += v[e] * s;
-        sum += __shfl_xor(sum, 1);
-        sum += __shfl_xor(sum, 2);
-        const std::uint32_t lane = (m & 15u) + 16u * g;
-        xs[((b * mtiles + (m >> 4)) * 2u + 0u) * 64u + lane] = __builtin_bit_cast(uint4, hi);
-        xs[((b * mtiles + (m >> 4)) * 2u + 1u) * 64u + lane] = __builtin_bit_cast(uint4, lo);
-        if (g == 0u) block_sums[b * mp + m] = sum;
+        emit_split_run(r, v, s, m, mp, xs, block_sums);
     };
     if (held) {
 #pragma unroll

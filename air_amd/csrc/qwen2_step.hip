@@ -441,10 +441,10 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
     }
 }
 
-// RMSNorm of rows of n <= kNormMaxVec * 4 * kNormThreads floats held in
-// registers (one coalesced read of the row by 1024 threads), with the
-// residual add of the reference's add_in_place fused in front when `y` is
-// given: x += y, then out = x * float(1 / sqrt(mean(x^2) + eps)) * w.
+// RMSNorm of rows of n <= 8 * kNormThreads floats (n % 8 == 0), thread t
+// holding elements 8t..8t+7 in registers (one coalesced read of the row),
+// with the residual add of the reference's add_in_place fused in front when
+// `y` is given: x += y, then out = x * float(1 / sqrt(mean(x^2) + eps)) * w.
 // Without y, x and out may alias; with y they must not (x receives the sum).
 //
 // SPLIT: y holds `splits` partial outputs of a K-split linear
@@ -453,8 +453,21 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
 // arithmetic, so the result is bit-identical to reducing first.  The
 // partials are loaded eight splits at a time so their latencies overlap.
 // w == null stops after the add (no norm, out unused).
+//
+// LOAD: out is also split for the skinny kernel as split_rows_kernel splits
+// a row (one power-of-two scale per row from max|out|, runs of eight through
+// emit_split_run), so the next linear needs no split launch; the grid then
+// covers the padded rows (zeros), as split_rows_kernel's does.
 constexpr unsigned kNormThreads = 1024;
-constexpr unsigned kNormMaxVec = 2;
+
+struct NormLoad {
+    uint4* xs;
+    float* block_sums;
+    float* inv_scale;
+    std::uint32_t rows;   // live rows; rows rows..mp-1 are padding
+    std::uint32_t mp;     // 16 * ceil(rows / 16)
+    std::uint32_t nb;     // 32-blocks per split row (kp / 32)
+};
 
 __device__ __forceinline__ float4v split_sum4(const float* __restrict__ p, std::uint32_t splits,
                                              std::uint64_t stride) {
@@ -474,72 +487,87 @@ __device__ __forceinline__ float4v split_sum4(const float* __restrict__ p, std::
     return t;
 }
 
-template <bool SPLIT>
+template <bool SPLIT, bool LOAD>
 __global__ __launch_bounds__(kNormThreads) void rms_norm_vec_kernel(float* x, const float* __restrict__ y,
                                                                     const float* __restrict__ w, float* out,
                                                                     std::uint64_t n, double eps, std::uint32_t splits,
                                                                     std::uint64_t split_stride,
-                                                                    const float* __restrict__ bias) {
+                                                                    const float* __restrict__ bias, NormLoad ld) {
 #pragma clang fp contract(off)
     __shared__ double red[kNormThreads / 64];
-    const std::uint64_t n4 = n / 4u;
-    float* row = x + static_cast<std::uint64_t>(blockIdx.x) * n;
-    float* dst = out + static_cast<std::uint64_t>(blockIdx.x) * n;
-    const float* yrow = y ? y + static_cast<std::uint64_t>(blockIdx.x) * n : nullptr;
-    float4v v[kNormMaxVec], g[kNormMaxVec];
+    __shared__ float redf[kNormThreads / 64];
+    const std::uint32_t r = blockIdx.x;
+    const std::uint32_t t = threadIdx.x;
+    const bool mine = (!LOAD || r < ld.rows) && t < n / 8u;
+    const std::uint64_t at = static_cast<std::uint64_t>(r) * n + 8u * t;
+    float4v v[2], g[2];
 #pragma unroll
-    for (unsigned j = 0; j < kNormMaxVec; ++j) {
-        const std::uint64_t i = threadIdx.x + static_cast<std::uint64_t>(j) * kNormThreads;
-        v[j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-        g[j] = v[j];
-        if (i < n4) {
-            v[j] = *reinterpret_cast<const float4v*>(row + 4u * i);
-            if (w) g[j] = *reinterpret_cast<const float4v*>(w + 4u * i);
-        }
+    for (int h = 0; h < 2; ++h) {
+        v[h] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+        g[h] = v[h];
     }
-    if (yrow) {
+    if (mine) {
 #pragma unroll
-        for (unsigned j = 0; j < kNormMaxVec; ++j) {
-            const std::uint64_t i = threadIdx.x + static_cast<std::uint64_t>(j) * kNormThreads;
-            if (i < n4) {
+        for (int h = 0; h < 2; ++h) {
+            v[h] = *reinterpret_cast<const float4v*>(x + at + 4 * h);
+            if (w) g[h] = *reinterpret_cast<const float4v*>(w + 8u * t + 4 * h);
+        }
+        if (y) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
                 float4v b;
                 if constexpr (SPLIT) {
-                    b = split_sum4(yrow + 4u * i, splits, split_stride);
-                    if (bias) b += *reinterpret_cast<const float4v*>(bias + 4u * i);
+                    b = split_sum4(y + at + 4 * h, splits, split_stride);
+                    if (bias) b += *reinterpret_cast<const float4v*>(bias + 8u * t + 4 * h);
                 } else {
-                    b = *reinterpret_cast<const float4v*>(yrow + 4u * i);
+                    b = *reinterpret_cast<const float4v*>(y + at + 4 * h);
                 }
-                v[j] += b;
-                *reinterpret_cast<float4v*>(row + 4u * i) = v[j];
+                v[h] += b;
+                *reinterpret_cast<float4v*>(x + at + 4 * h) = v[h];
             }
         }
     }
     if (!w) return;
     double sum = 0.0;
 #pragma unroll
-    for (unsigned j = 0; j < kNormMaxVec; ++j) {
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sum += static_cast<double>(v[j][e]) * v[j][e];
+        for (int e = 0; e < 4; ++e) sum += static_cast<double>(v[h][e]) * v[h][e];
     }
     for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = sum;
+    if ((t & 63u) == 0) red[t >> 6] = sum;
     __syncthreads();
     double total = 0.0;
 #pragma unroll
     for (unsigned k = 0; k < kNormThreads / 64; ++k) total += red[k];
     const float scale = static_cast<float>(1.0 / sqrt(total / static_cast<double>(n) + eps));
+    float o[8];
 #pragma unroll
-    for (unsigned j = 0; j < kNormMaxVec; ++j) {
-        const std::uint64_t i = threadIdx.x + static_cast<std::uint64_t>(j) * kNormThreads;
-        if (i < n4) {
-            float4v o;
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float xs = v[j][e] * scale;
-                o[e] = xs * g[j][e];
-            }
-            *reinterpret_cast<float4v*>(dst + 4u * i) = o;
+        for (int e = 0; e < 4; ++e) {
+            const float xs = v[h][e] * scale;
+            o[4 * h + e] = mine ? xs * g[h][e] : 0.0f;
         }
+    }
+    if (mine) {
+        *reinterpret_cast<float4v*>(out + at) = float4v{o[0], o[1], o[2], o[3]};
+        *reinterpret_cast<float4v*>(out + at + 4) = float4v{o[4], o[5], o[6], o[7]};
+    }
+    if constexpr (LOAD) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(o[e]));
+        for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+        if ((t & 63u) == 0) redf[t >> 6] = amax;
+        __syncthreads();
+        amax = redf[0];
+#pragma unroll
+        for (unsigned k = 1; k < kNormThreads / 64; ++k) amax = fmaxf(amax, redf[k]);
+        float s, inv;
+        block_scale(amax, s, inv);
+        if (t < 4u * ld.nb) emit_split_run(t, o, s, r, ld.mp, ld.xs, ld.block_sums);
+        if (t == 0) ld.inv_scale[r] = inv;
     }
 }
 
@@ -577,7 +605,7 @@ __global__ __launch_bounds__(kThreads) void split_swiglu_kernel(const float4v* _
 
 bool norm_vectorizable(const float* x, const float* y, const float* w, const float* out, std::uint64_t n) {
     const auto aligned = [](const void* p) { return reinterpret_cast<std::uintptr_t>(p) % 16u == 0; };
-    return n % 4u == 0 && n <= static_cast<std::uint64_t>(kNormMaxVec) * 4u * kNormThreads && aligned(x) &&
+    return n % 8u == 0 && n <= 8u * static_cast<std::uint64_t>(kNormThreads) && aligned(x) &&
            (!y || aligned(y)) && aligned(w) && aligned(out);
 }
 
@@ -599,9 +627,9 @@ hipError_t launch_matrix_rows(const TilePlanes& p, const std::int32_t* rows, std
 hipError_t launch_rms_norm(const float* x, const float* w, float* out, std::uint32_t m, std::uint64_t n, double eps,
                            hipStream_t stream) {
     if (norm_vectorizable(x, nullptr, w, out, n)) {
-        hipLaunchKernelGGL(rms_norm_vec_kernel<false>, dim3(m), dim3(kNormThreads), 0, stream, const_cast<float*>(x),
-                           static_cast<const float*>(nullptr), w, out, n, eps, 0u, std::uint64_t{0},
-                           static_cast<const float*>(nullptr));
+        hipLaunchKernelGGL((rms_norm_vec_kernel<false, false>), dim3(m), dim3(kNormThreads), 0, stream,
+                           const_cast<float*>(x), static_cast<const float*>(nullptr), w, out, n, eps, 0u,
+                           std::uint64_t{0}, static_cast<const float*>(nullptr), NormLoad{});
     } else {
         hipLaunchKernelGGL(rms_norm_kernel, dim3(m), dim3(kThreads), 0, stream, x, w, out, n, eps);
     }
@@ -611,8 +639,8 @@ hipError_t launch_rms_norm(const float* x, const float* w, float* out, std::uint
 hipError_t launch_add_rms_norm(float* x, const float* y, const float* w, float* out, std::uint32_t m, std::uint64_t n,
                                double eps, hipStream_t stream) {
     if (norm_vectorizable(x, y, w, out, n)) {
-        hipLaunchKernelGGL(rms_norm_vec_kernel<false>, dim3(m), dim3(kNormThreads), 0, stream, x, y, w, out, n, eps, 0u,
-                           std::uint64_t{0}, static_cast<const float*>(nullptr));
+        hipLaunchKernelGGL((rms_norm_vec_kernel<false, false>), dim3(m), dim3(kNormThreads), 0, stream, x, y, w, out,
+                           n, eps, 0u, std::uint64_t{0}, static_cast<const float*>(nullptr), NormLoad{});
         return hipGetLastError();
     }
     hipLaunchKernelGGL(add_kernel, dim3(grid_for(static_cast<std::uint64_t>(m) * n)), dim3(kThreads), 0, stream, x, y,
@@ -706,8 +734,9 @@ bool split_epilogue_fits(const SplitEpilogue& e, const float* partials, const fl
     }
     if (e.kind == kEpilogueRopeKv) return e.rope != nullptr;
     if (e.kind == kEpilogueResidual) {
-        return n % 4u == 0 && n <= static_cast<std::uint64_t>(kNormMaxVec) * 4u * kNormThreads &&
-               (!e.norm_weight || (aligned(e.norm_weight) && aligned(e.norm_out)));
+        return n % 8u == 0 && n <= 8u * static_cast<std::uint64_t>(kNormThreads) &&
+               (!e.norm_weight || (aligned(e.norm_weight) && aligned(e.norm_out))) &&
+               (!e.load || (e.norm_weight && m <= 64u && 4u * e.load_blocks <= kNormThreads));
     }
     return false;
 }
@@ -732,8 +761,17 @@ hipError_t launch_split_epilogue(const float* partials, std::uint32_t splits, st
                            reinterpret_cast<const float4v*>(bias), reinterpret_cast<float4v*>(e.out));
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(rms_norm_vec_kernel<true>, dim3(m), dim3(kNormThreads), 0, stream, e.out, partials, e.norm_weight,
-                       e.norm_out, n, e.eps, splits, static_cast<std::uint64_t>(m) * n, bias);
+    if (e.load) {
+        const NormLoad ld{static_cast<uint4*>(e.load->xs), e.load->block_sums, e.load->inv_scale, m,
+                          static_cast<std::uint32_t>(ceil_div(m, 16u) * 16u), e.load_blocks};
+        hipLaunchKernelGGL((rms_norm_vec_kernel<true, true>), dim3(ld.mp), dim3(kNormThreads), 0, stream, e.out,
+                           partials, e.norm_weight, e.norm_out, n, e.eps, splits, static_cast<std::uint64_t>(m) * n,
+                           bias, ld);
+    } else {
+        hipLaunchKernelGGL((rms_norm_vec_kernel<true, false>), dim3(m), dim3(kNormThreads), 0, stream, e.out,
+                           partials, e.norm_weight, e.norm_out, n, e.eps, splits, static_cast<std::uint64_t>(m) * n,
+                           bias, NormLoad{});
+    }
     return hipGetLastError();
 }
 

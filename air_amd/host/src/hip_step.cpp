@@ -480,8 +480,12 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
             if (Status s = attention(l, m, max_tokens, table_pages, tiles); !s) return s;
         }
         if (epilogues) {
-            if (Status s = prepared_.linear_epilogue(l, LinearRole::attn_output, att_, m, hidden_,
-                                                     AIR_HIP_EPILOGUE_RESIDUAL, ffn_norm_[l], normed_, eps, tactic);
+            // With a fused gate|up next, the FFN norm's output is also split
+            // for it (no split launch of its own).
+            const int o_epilogue = m >= 2U && prepared_.fused_gate_up() ? AIR_HIP_EPILOGUE_RESIDUAL_LOAD
+                                                                        : AIR_HIP_EPILOGUE_RESIDUAL;
+            if (Status s = prepared_.linear_epilogue(l, LinearRole::attn_output, att_, m, hidden_, o_epilogue,
+                                                     ffn_norm_[l], normed_, eps, tactic);
                 !s) {
                 return s;
             }

@@ -242,7 +242,8 @@ int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* matrix,
 enum {
     AIR_HIP_EPILOGUE_STORE = 0,
     AIR_HIP_EPILOGUE_RESIDUAL = 1,
-    AIR_HIP_EPILOGUE_SWIGLU = 2
+    AIR_HIP_EPILOGUE_SWIGLU = 2,
+    AIR_HIP_EPILOGUE_RESIDUAL_LOAD = 3
 };
 int air_hip_decode_linear_fused(air_hip_context* ctx, const air_hip_matrix* matrix, const float* x, float* y,
                                 const float* bias, const float* norm_weight, double eps, int epilogue);
@@ -255,7 +256,13 @@ int air_hip_decode_linear_fused(air_hip_context* ctx, const air_hip_matrix* matr
  *     (air_hip_silu_mul); norm_weight must be null;
  *   AIR_HIP_EPILOGUE_RESIDUAL: out [rows][n] += x W^T + bias, then, with
  *     norm_weight, norm_out[r] = rms_norm(out[r]) * norm_weight
- *     (air_hip_add_rms_norm; norm_out must not alias out).
+ *     (air_hip_add_rms_norm; norm_out must not alias out);
+ *   AIR_HIP_EPILOGUE_RESIDUAL_LOAD: RESIDUAL with its norm (required), and
+ *     norm_out is also split into the context's activation workspace as
+ *     air_hip_activations_load(norm_out, n, rows) would split it; the next
+ *     linear this context runs on x == norm_out with the same width and rows
+ *     uses that split instead of splitting again (the caller must not change
+ *     norm_out in between; any other activation load cancels it).
  * Bit-identical to air_hip_linear (same tactic) followed by that call.  Where
  * the linear runs as a skinny launch with a K split (decode widths 2..64),
  * its split reduction applies the epilogue, so the epilogue costs no launch

@@ -313,12 +313,19 @@ def test_linear_epilogue_matches_separate_kernels(torch_cuda, hip_ctx, type_id, 
     (add_rms_norm) and the add alone, at one row, widths served by the
     single-launch kernel and by the skinny kernel with and without a K split
     (the split reduction then carries the epilogue), and a width (n = 666)
-    whose rows are too ragged for the reduction to carry it."""
+    whose rows are too ragged for the reduction to carry it.  RESIDUAL_LOAD
+    also leaves the norm's output split for the next linear on it: that
+    linear (a wide one, which runs on split activations) must match the
+    same linear over the separately normed rows, and a split must not be
+    reused once another linear ran in between."""
     torch = torch_cuda
     lib = capi.lib()
     f = n // 2
     canon = helpers.weights(type_id, k, n, seed=k + n + 11)
     mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    n2 = 9216                                         # 576 row tiles: runs on split activations
+    canon2 = helpers.weights(capi.TYPE_Q8_0, n, n2, seed=n + 5) if n % 32 == 0 else None
+    mat2 = capi.Matrix(hip_ctx, capi.TYPE_Q8_0, n, n2, canon2, canon2.nbytes, on_device=False) if n % 32 == 0 else None
     dec = capi.LINEAR_DECODE
     h = hip_ctx.handle
 
@@ -365,6 +372,36 @@ def test_linear_epilogue_matches_separate_kernels(torch_cuda, hip_ctx, type_id, 
                 assert np.array_equal(bits(resid), bits(resid_ref)), case
                 assert np.array_equal(bits(normed), bits(normed_ref)), case
                 assert np.array_equal(bits(plain), bits(plain_ref)), case
+                if mat2 is None:
+                    assert lib.air_hip_linear_epilogue(h, mat.handle, x.data_ptr(), m, resid.data_ptr(), None,
+                                                       capi.EPILOGUE_RESIDUAL_LOAD, w.data_ptr(), normed.data_ptr(),
+                                                       eps, dec) == 1
+                    continue
+                # RESIDUAL_LOAD, then the next linear on the norm's output
+                y2_ref = torch.empty((m, n2), dtype=torch.float32, device="cuda:0")
+                capi.check(lib.air_hip_linear(h, mat2.handle, normed_ref.data_ptr(), y2_ref.data_ptr(), None, m, dec))
+                resid = resid0.clone()
+                normed = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+                capi.check(lib.air_hip_linear_epilogue(h, mat.handle, x.data_ptr(), m, resid.data_ptr(),
+                                                       bias.data_ptr(), capi.EPILOGUE_RESIDUAL_LOAD, w.data_ptr(),
+                                                       normed.data_ptr(), eps, dec))
+                y2 = torch.full((m, n2), float("nan"), dtype=torch.float32, device="cuda:0")
+                capi.check(lib.air_hip_linear(h, mat2.handle, normed.data_ptr(), y2.data_ptr(), None, m, dec))
+                torch.cuda.synchronize()
+                assert np.array_equal(bits(resid), bits(resid_ref)), case
+                assert np.array_equal(bits(normed), bits(normed_ref)), case
+                assert np.array_equal(bits(y2), bits(y2_ref)), case
+                # another linear in between: the split is not reused for changed rows
+                capi.check(lib.air_hip_linear_epilogue(h, mat.handle, x.data_ptr(), m, resid.data_ptr(),
+                                                       bias.data_ptr(), capi.EPILOGUE_RESIDUAL_LOAD, w.data_ptr(),
+                                                       normed.data_ptr(), eps, dec))
+                capi.check(lib.air_hip_linear(h, mat.handle, x.data_ptr(), lin.data_ptr(), None, m, dec))
+                normed.mul_(2.0)
+                fresh = normed.clone()
+                capi.check(lib.air_hip_linear(h, mat2.handle, normed.data_ptr(), y2.data_ptr(), None, m, dec))
+                capi.check(lib.air_hip_linear(h, mat2.handle, fresh.data_ptr(), y2_ref.data_ptr(), None, m, dec))
+                torch.cuda.synchronize()
+                assert np.array_equal(bits(y2), bits(y2_ref)), case
         x = _dev(torch, helpers.activations(8, k, seed=1))
         out = torch.empty((8, n), dtype=torch.float32, device="cuda:0")
         assert lib.air_hip_linear_epilogue(h, mat.handle, x.data_ptr(), 8, out.data_ptr(), None,
@@ -380,3 +417,5 @@ def test_linear_epilogue_matches_separate_kernels(torch_cuda, hip_ctx, type_id, 
     finally:
         hip_ctx.set_decode_path(0)
         mat.release()
+        if mat2 is not None:
+            mat2.release()
