@@ -6,10 +6,10 @@
 // time).  Here a workgroup owns a tile of up to 16 query vectors that share a
 // sequence and a KV head -- 16 consecutive prompt rows of one q head in a
 // prefill, or the grouped q heads of one KV head of a decode row -- and walks
-// the keys in chunks of 64 tokens staged through LDS, so each K/V element is
+// the keys in chunks of 32 (decode) or 64 (prefill) tokens staged through LDS, so each K/V element is
 // read from memory once per tile instead of once per query vector:
 //
-//   S = (q . k) * scale        16 x 64 per chunk, 4 dots per thread, float
+//   S = (q . k) * scale        16 x chunk, chunk / 16 dots per thread, float
 //   m' = max(m, rowmax S);  p = exp(S - m');  l = l e^(m-m') + rowsum p
 //   acc = acc e^(m-m') + p . V 8 (D=128) or 4 (D=64) dims per thread
 //
@@ -27,7 +27,10 @@ namespace air_hip {
 namespace {
 
 constexpr unsigned kAttnThreads = 256;
-constexpr unsigned kChunk = 64;      // key tokens per LDS stage
+// Key tokens per LDS stage: 32 for decode-width steps (half the LDS of 64,
+// so three workgroups share a CU, and twice the key splits for short
+// grids), 64 for prefill tiles (half the barriers per key).
+std::uint32_t chunk_for(std::uint32_t m) { return m <= 64u ? 32u : 64u; }
 constexpr unsigned kTileVectors = 16;
 constexpr unsigned kMaxSplits = 64;  // one wave reduces a vector's splits in the merge
 
@@ -46,13 +49,14 @@ __device__ __forceinline__ bool tile_ok(const AttentionTile& t, std::uint32_t m,
     return t.head / group == (t.head + t.heads - 1u) / group;
 }
 
-template <unsigned D>
+template <unsigned D, unsigned kChunk>
 __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
     KvGeometry g, const float* __restrict__ qkv, std::uint64_t stride, std::uint32_t m,
     const std::int32_t* __restrict__ positions,
     const std::int32_t* __restrict__ tables, std::uint32_t layer, std::uint32_t q_heads, std::uint32_t kv_heads,
     const AttentionTile* __restrict__ tiles, std::uint32_t splits, float scale, float* __restrict__ partials,
     float* __restrict__ out) {
+    constexpr unsigned kTokJ = kChunk / 16;   // key tokens per thread in a chunk (16 lanes per query vector)
     constexpr unsigned LD = D + 4;            // padded LDS row (floats), keeps float4 alignment
     constexpr unsigned D4 = D / 4;
     constexpr unsigned ACC = D / 16;          // output dims per thread
@@ -158,15 +162,15 @@ __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
         // Scores of tokens lane16 + 16 j.  Idle vector slots (a decode tile
         // of 7 grouped heads leaves 9 of 16) skip the LDS reads: whole waves
         // of them branch around the loop.
-        float s[4];
+        float s[kTokJ];
 #pragma unroll
-        for (unsigned j = 0; j < 4; ++j) s[j] = 0.0f;
+        for (unsigned j = 0; j < kTokJ; ++j) s[j] = 0.0f;
         if (active) {
 #pragma unroll 4
             for (unsigned d4 = 0; d4 < D4; ++d4) {
                 const float4 q4 = *reinterpret_cast<const float4*>(&qs[qi][4u * d4]);
 #pragma unroll
-                for (unsigned j = 0; j < 4; ++j) {
+                for (unsigned j = 0; j < kTokJ; ++j) {
                     const float4 k4 = *reinterpret_cast<const float4*>(&ks[lane16 + 16u * j][4u * d4]);
                     s[j] += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
                 }
@@ -174,7 +178,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
         }
         float row_max = -__builtin_huge_valf();
 #pragma unroll
-        for (unsigned j = 0; j < 4; ++j) {
+        for (unsigned j = 0; j < kTokJ; ++j) {
             const std::int64_t token = c0 + lane16 + 16u * j;
             const bool valid = active && token <= q_pos;
             s[j] = valid ? s[j] * scale : -__builtin_huge_valf();
@@ -191,7 +195,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
         const float alpha = none ? 1.0f : __expf(mx - m_new);
         float row_sum = 0.0f;
 #pragma unroll
-        for (unsigned j = 0; j < 4; ++j) {
+        for (unsigned j = 0; j < kTokJ; ++j) {
             const float p = none || s[j] == -__builtin_huge_valf() ? 0.0f : __expf(s[j] - m_new);
             row_sum += p;
             ps[qi][lane16 + 16u * j] = p;
@@ -328,8 +332,9 @@ std::uint32_t make_attention_tiles(const std::uint32_t* run_rows, std::uint32_t 
     return count;
 }
 
-std::uint32_t attention_splits(std::uint32_t tiles, std::uint64_t max_tokens) {
-    const std::uint64_t chunks = (max_tokens + kChunk - 1) / kChunk;
+std::uint32_t attention_splits(std::uint32_t tiles, std::uint64_t max_tokens, std::uint32_t m) {
+    const std::uint32_t chunk = chunk_for(m);
+    const std::uint64_t chunks = (max_tokens + chunk - 1) / chunk;
     if (tiles == 0 || chunks <= 1) return 1;
     const std::uint64_t want = (512u + tiles - 1) / tiles;     // about two workgroups per CU
     const std::uint64_t s = want < chunks ? want : chunks;
@@ -349,16 +354,27 @@ hipError_t launch_attention_tiles(const KvLayout& kv, const float* qkv, std::uin
     const KvGeometry g{kv.pool, kv.page_tokens, kv.kv_width, kv.layers, kv.max_pages, kv.pool_pages};
     const float scale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(head_dim)));
     const dim3 grid(tile_count, splits);
+    const bool small = chunk_for(m) == 32u;
     if (head_dim == 128u) {
-        hipLaunchKernelGGL(attention_tile_kernel<128>, grid, dim3(kAttnThreads), 0, stream, g, qkv, stride, m,
-                           positions, tables, layer, q_heads, kv_heads, tiles, splits, scale, partials, out);
+        if (small) {
+            hipLaunchKernelGGL((attention_tile_kernel<128, 32>), grid, dim3(kAttnThreads), 0, stream, g, qkv, stride,
+                               m, positions, tables, layer, q_heads, kv_heads, tiles, splits, scale, partials, out);
+        } else {
+            hipLaunchKernelGGL((attention_tile_kernel<128, 64>), grid, dim3(kAttnThreads), 0, stream, g, qkv, stride,
+                               m, positions, tables, layer, q_heads, kv_heads, tiles, splits, scale, partials, out);
+        }
         if (splits > 1u) {
             hipLaunchKernelGGL(attention_merge_kernel<128>, dim3(tile_count), dim3(kAttnThreads), 0, stream, tiles,
                                splits, m, q_heads, kv_heads, partials, out);
         }
     } else if (head_dim == 64u) {
-        hipLaunchKernelGGL(attention_tile_kernel<64>, grid, dim3(kAttnThreads), 0, stream, g, qkv, stride, m,
-                           positions, tables, layer, q_heads, kv_heads, tiles, splits, scale, partials, out);
+        if (small) {
+            hipLaunchKernelGGL((attention_tile_kernel<64, 32>), grid, dim3(kAttnThreads), 0, stream, g, qkv, stride,
+                               m, positions, tables, layer, q_heads, kv_heads, tiles, splits, scale, partials, out);
+        } else {
+            hipLaunchKernelGGL((attention_tile_kernel<64, 64>), grid, dim3(kAttnThreads), 0, stream, g, qkv, stride,
+                               m, positions, tables, layer, q_heads, kv_heads, tiles, splits, scale, partials, out);
+        }
         if (splits > 1u) {
             hipLaunchKernelGGL(attention_merge_kernel<64>, dim3(tile_count), dim3(kAttnThreads), 0, stream, tiles,
                                splits, m, q_heads, kv_heads, partials, out);

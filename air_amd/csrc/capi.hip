@@ -1057,7 +1057,7 @@ int air_hip_attention_online(air_hip_context* ctx, const air_hip_kv_layout* kv, 
     if (tile_count > 0x7fffffffu) return fail(AIR_HIP_UNSUPPORTED, "too many tiles");
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-    const uint32_t splits = attention_splits(tile_count, max_tokens);
+    const uint32_t splits = attention_splits(tile_count, max_tokens, m);
     if (int rc = ensure_attention_scratch(ctx, attention_partials_bytes(tile_count, splits, head_dim));
         rc != AIR_HIP_OK) {
         return rc;
