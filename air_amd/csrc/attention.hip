@@ -336,7 +336,9 @@ std::uint32_t attention_splits(std::uint32_t tiles, std::uint64_t max_tokens, st
     const std::uint32_t chunk = chunk_for(m);
     const std::uint64_t chunks = (max_tokens + chunk - 1) / chunk;
     if (tiles == 0 || chunks <= 1) return 1;
-    const std::uint64_t want = (512u + tiles - 1) / tiles;     // about two workgroups per CU
+    // 32-token chunks: about as many workgroups as fit in one round (three
+    // per CU on 256 CUs); 64-token chunks (prefill): about 512.
+    const std::uint64_t want = chunk == 32u ? (768u / tiles > 0u ? 768u / tiles : 1u) : (512u + tiles - 1) / tiles;
     const std::uint64_t s = want < chunks ? want : chunks;
     return static_cast<std::uint32_t>(s < 64 ? s : 64);
 }
