@@ -311,8 +311,9 @@ def test_linear_epilogue_matches_separate_kernels(torch_cuda, hip_ctx, type_id, 
     """air_hip_linear_epilogue against air_hip_linear followed by the kernel
     it replaces, bit-exact: SwiGLU (silu_mul), residual add + RMSNorm
     (add_rms_norm) and the add alone, at one row, widths served by the
-    single-launch kernel and by the skinny kernel with and without a K split
-    (the split reduction then carries the epilogue), and a width (n = 666)
+    single-launch kernel, by the skinny kernel with and without a K split
+    (the split reduction then carries the epilogue) and by the K-split kernel
+    past 64 rows, and a width (n = 666)
     whose rows are too ragged for the reduction to carry it.  RESIDUAL_LOAD
     also leaves the norm's output split for the next linear on it: that
     linear (a wide one, which runs on split activations) must match the
@@ -336,7 +337,7 @@ def test_linear_epilogue_matches_separate_kernels(torch_cuda, hip_ctx, type_id, 
         bias = _dev(torch, helpers.activations(1, n, seed=k + 3)[0] * 0.1)
         w = _dev(torch, helpers.activations(1, n, seed=k + 2)[0])
         eps = 1e-6
-        for m in (1, 8, 30, 64):
+        for m in (1, 8, 30, 64, 100):       # 100: the K-split kernel over loaded activations
             x = _dev(torch, helpers.activations(m, k, seed=m + k) * 2.0)
             resid0 = _dev(torch, helpers.activations(m, n, seed=m + 7))
             for path in [(0, 0, 0), (2, 1, 1), (2, 1, 3), (2, 2, 2)]:
