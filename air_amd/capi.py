@@ -142,6 +142,7 @@ SIGNATURES = {
     "air_hip_activations_load": (_I, [_P, _P, _U64, _U32]),
     "air_hip_linear_loaded": (_I, [_P, _P, _P, _P, _I]),
     "air_hip_linear": (_I, [_P, _P, _P, _P, _P, _U32, _I]),
+    "air_hip_linear_plan": (_I, [_P, _P, _U32, _I, ctypes.c_char_p, _U64]),
 }
 
 
@@ -280,6 +281,12 @@ class Matrix:
 
     def linear(self, x, y, m: int, bias=None, tactic: int = LINEAR_AUTO) -> None:
         check(lib().air_hip_linear(self.ctx.handle, self.handle, ptr(x), ptr(y), ptr(bias), m, tactic))
+
+    def plan(self, m: int, tactic: int = LINEAR_AUTO) -> str:
+        """The kernels and launch shape a linear of m rows runs on."""
+        buf = ctypes.create_string_buffer(256)
+        check(lib().air_hip_linear_plan(self.ctx.handle, self.handle, m, tactic, buf, len(buf)))
+        return buf.value.decode()
 
     def linear_loaded(self, y, bias=None, tactic: int = LINEAR_AUTO) -> None:
         """Stage 2 of a linear, over the context's loaded activations."""

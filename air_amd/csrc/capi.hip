@@ -13,6 +13,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <vector>
 #include <cstdarg>
@@ -167,6 +168,11 @@ int load_activations_for(air_hip_context* ctx, const float* x, std::uint64_t k, 
     return split ? AIR_HIP_OK : air_hip_activations_load(ctx, x, k, rows);
 }
 
+// Every entry point that writes device memory through the context forgets
+// the rows an epilogue last split (AIR_HIP_EPILOGUE_RESIDUAL_LOAD): after
+// any such write the split may no longer match its source.
+void forget_loaded_source(air_hip_context* ctx) { ctx->loaded_source = nullptr; }
+
 int ensure_prefill_workspace(air_hip_context* ctx, std::uint64_t bytes) {
     return grow_buffer(ctx, &ctx->prefill_workspace, &ctx->prefill_workspace_bytes, bytes, "prefill workspace");
 }
@@ -201,18 +207,51 @@ const SplitEpilogue* reduction_epilogue(air_hip_context* ctx, const air_hip_matr
     return epilogue;
 }
 
+// Which kernels a linear of `rows` rows runs on, decided in one place for
+// the launch path and for air_hip_linear_plan.
+enum class Route { prefill, gemv, fused, skinny_x, skinny_loaded, decode_linear };
+
+// The skinny kernel straight from the f32 rows, or over activations split
+// into the workspace first.  The in-workgroup split repeats the activation
+// split in every workgroup: it pays on narrow matrices, where the separate
+// split launch dominates (Qwen2-7B q|k|v, o, down at M <= 32: 10-25 %
+// faster), and loses on wide ones (gate|up, lm_head: up to 2x slower) and at
+// M = 64.  Q4_K with four activation tiles would also spill in it.
+Route skinny_route(const air_hip_context* ctx, const air_hip_matrix* m, std::uint32_t rows) {
+    const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits);
+    const bool narrow = m->planes.nt <= 512u && (rows <= 32u || m->planes.k <= 4096u);
+    return (!narrow || (m->planes.type == kQ4_K && shape.mt == 4u)) ? Route::skinny_loaded : Route::skinny_x;
+}
+
+// tactic is already validated; rows >= 1.
+Route route_linear(const air_hip_context* ctx, const air_hip_matrix* m, std::uint32_t rows, int tactic) {
+    if (tactic == AIR_HIP_LINEAR_PREFILL || (tactic == AIR_HIP_LINEAR_AUTO && rows > AIR_HIP_MAX_DECODE_ROWS)) {
+        return Route::prefill;
+    }
+    if (rows == 1u) return Route::gemv;
+    if (rows <= kFusedMaxRows) {
+        // Measured on the Qwen2-7B shapes (M = 2..16): the single-launch fused
+        // kernel wins for small square matrices (o: N, K <= 4096) and for very
+        // large ones at M <= 4; the skinny kernel everywhere else (down, with
+        // its long K, by 10-30 %) and for Q4_K (o at M = 16: 25 %).
+        const std::uint64_t weight_bytes = static_cast<std::uint64_t>(m->planes.nt) * m->planes.kt *
+                                           geometry_of(m->planes.type).code_tile_bytes;
+        const bool prefer_fused = m->planes.type != kQ4_K &&
+                                  ((m->planes.n <= 4096u && m->planes.k <= 4096u) ||
+                                   (rows <= 4u && weight_bytes >= (256ull << 20)));
+        if (ctx->decode_path == 2u || (ctx->decode_path == 0u && !prefer_fused)) return skinny_route(ctx, m, rows);
+        return Route::fused;
+    }
+    if (rows <= AIR_HIP_MAX_DECODE_ROWS && ctx->decode_path != 1u) return skinny_route(ctx, m, rows);
+    return Route::decode_linear;
+}
+
 // Skinny decode linear straight from the f32 rows (M = 2..64): one launch
 // (two with a K split), no activation workspace.
 int run_skinny_x(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y, const float* bias,
                  std::uint32_t rows, const SplitEpilogue* epilogue, bool* applied, const void* ready) {
     const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits);
-    // The in-workgroup split repeats the activation split in every
-    // workgroup: it pays on narrow matrices, where the separate split launch
-    // dominates (Qwen2-7B q|k|v, o, down at M <= 32: 10-25 % faster), and
-    // loses on wide ones (gate|up, lm_head: up to 2x slower) and at M = 64.
-    // Q4_K with four activation tiles would also spill in it.
-    const bool narrow = m->planes.nt <= 512u && (rows <= 32u || m->planes.k <= 4096u);
-    if (!narrow || (m->planes.type == kQ4_K && shape.mt == 4u)) {
+    if (skinny_route(ctx, m, rows) == Route::skinny_loaded) {
         int rc = load_activations_for(ctx, x, m->planes.k, rows, ready);
         if (rc != AIR_HIP_OK) return rc;
         return linear_loaded(ctx, m, y, bias, AIR_HIP_LINEAR_DECODE, epilogue, applied);
@@ -528,6 +567,7 @@ int air_hip_matrix_describe(const air_hip_matrix* m, air_hip_matrix_desc* out) {
 
 int air_hip_matrix_dequantize(air_hip_context* ctx, const air_hip_matrix* m, float* out) {
     if (!ctx || !m || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    forget_loaded_source(ctx);
     if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
@@ -539,6 +579,7 @@ int air_hip_matrix_dequantize(air_hip_context* ctx, const air_hip_matrix* m, flo
 int air_hip_dequantize_canonical(air_hip_context* ctx, int type, const void* canonical,
                                  uint64_t canonical_bytes, uint64_t elements, float* out) {
     if (!ctx || !canonical || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    forget_loaded_source(ctx);
     const auto geo = geometry_of(type);
     if (geo.block_elements == 0) return fail(AIR_HIP_UNSUPPORTED, "tensor type %d is not decoded by the HIP engine", type);
     if (elements % geo.block_elements != 0 || canonical_bytes != (elements / geo.block_elements) * geo.block_bytes) {
@@ -681,63 +722,86 @@ int linear_rows(air_hip_context* ctx, const air_hip_matrix* m, const float* x, f
         return fail(AIR_HIP_INVALID_ARGUMENT, "unknown linear tactic %d", tactic);
     }
     if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
-    const bool prefill = tactic == AIR_HIP_LINEAR_PREFILL ||
-                         (tactic == AIR_HIP_LINEAR_AUTO && rows > AIR_HIP_MAX_DECODE_ROWS);
-    if (prefill) {
-        if (rows == 0) return fail(AIR_HIP_INVALID_ARGUMENT, "linear batch width must be non-zero");
+    if (rows == 0) return fail(AIR_HIP_INVALID_ARGUMENT, "linear batch width must be non-zero");
+    const Route route = route_linear(ctx, m, rows, tactic);
+    if (route == Route::prefill) {
         if (rows > kMaxRows) return fail(AIR_HIP_UNSUPPORTED, "linear batch width %u exceeds %u", rows, kMaxRows);
         if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
         DeviceScope scope(ctx->device);
         if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
         return run_prefill(ctx, m, x, y, bias, rows);
     }
-    if (rows >= 1u && rows <= kFusedMaxRows) {
-        // One launch: the activations are split in registers.
-        if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
-        DeviceScope scope(ctx->device);
-        if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-        if (rows == 1u) {
-            const GemvShape gshape = plan_decode_gemv(m->planes, ctx->tuning);
-            const hipError_t gerr = launch_decode_gemv(m->planes, x, bias, y, gshape, ctx->stream);
-            if (gerr != hipSuccess) return hip_fail(gerr, "decode_gemv_kernel");
-            ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
-            ctx->decode_rows.fetch_add(1, std::memory_order_relaxed);
-            return AIR_HIP_OK;
-        }
-        // Measured on the Qwen2-7B shapes (M = 2..16): the single-launch fused
-        // kernel wins for small square matrices (o: N, K <= 4096) and for very
-        // large ones at M <= 4; the skinny kernel everywhere else (down, with
-        // its long K, by 10-30 %) and for Q4_K (o at M = 16: 25 %).
-        const std::uint64_t weight_bytes = static_cast<std::uint64_t>(m->planes.nt) * m->planes.kt *
-                                           geometry_of(m->planes.type).code_tile_bytes;
-        const bool prefer_fused = m->planes.type != kQ4_K &&
-                                  ((m->planes.n <= 4096u && m->planes.k <= 4096u) ||
-                                   (rows <= 4u && weight_bytes >= (256ull << 20)));
-        if (ctx->decode_path == 2u || (ctx->decode_path == 0u && !prefer_fused)) {
-            return run_skinny_x(ctx, m, x, y, bias, rows, epilogue, applied, ready);
-        }
-        const FusedShape shape = plan_decode_fused(m->planes, rows, ctx->tuning);
-        if (shape.k_splits > 1u) {
-            const int rc = ensure_split_buffers(ctx, fused_split_workspace_bytes(shape), shape.groups);
-            if (rc != AIR_HIP_OK) return rc;
-        }
-        const hipError_t err = launch_decode_fused(m->planes, x, bias, y, rows, shape, ctx->split_partials,
-                                                   ctx->split_counters, ctx->stream);
-        if (err != hipSuccess) return hip_fail(err, "decode_fused_kernel");
+    if (route == Route::decode_linear) {
+        int rc = load_activations_for(ctx, x, m->planes.k, rows, ready);
+        if (rc != AIR_HIP_OK) return rc;
+        return linear_loaded(ctx, m, y, bias, tactic, epilogue, applied);
+    }
+    // The single-launch routes split the activations in registers.
+    if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    if (route == Route::gemv) {
+        const GemvShape gshape = plan_decode_gemv(m->planes, ctx->tuning);
+        const hipError_t gerr = launch_decode_gemv(m->planes, x, bias, y, gshape, ctx->stream);
+        if (gerr != hipSuccess) return hip_fail(gerr, "decode_gemv_kernel");
         ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
-        ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
+        ctx->decode_rows.fetch_add(1, std::memory_order_relaxed);
         return AIR_HIP_OK;
     }
-    if (rows == 0) return fail(AIR_HIP_INVALID_ARGUMENT, "linear batch width must be non-zero");
-    if (rows <= AIR_HIP_MAX_DECODE_ROWS && ctx->decode_path != 1u) {
-        if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
-        DeviceScope scope(ctx->device);
-        if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    if (route == Route::skinny_x || route == Route::skinny_loaded) {
         return run_skinny_x(ctx, m, x, y, bias, rows, epilogue, applied, ready);
     }
-    int rc = load_activations_for(ctx, x, m->planes.k, rows, ready);
-    if (rc != AIR_HIP_OK) return rc;
-    return linear_loaded(ctx, m, y, bias, tactic, epilogue, applied);
+    const FusedShape shape = plan_decode_fused(m->planes, rows, ctx->tuning);
+    if (shape.k_splits > 1u) {
+        const int rc = ensure_split_buffers(ctx, fused_split_workspace_bytes(shape), shape.groups);
+        if (rc != AIR_HIP_OK) return rc;
+    }
+    const hipError_t err = launch_decode_fused(m->planes, x, bias, y, rows, shape, ctx->split_partials,
+                                               ctx->split_counters, ctx->stream);
+    if (err != hipSuccess) return hip_fail(err, "decode_fused_kernel");
+    ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
+    ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
+    return AIR_HIP_OK;
+}
+
+// Text description of the launches of a linear (air_hip_linear_plan).
+std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m, std::uint32_t rows, int tactic) {
+    const char* fmt = m->planes.type == kQ8_0 ? "q8_0" : m->planes.type == kQ4_0 ? "q4_0" : "q4_k";
+    char buf[256];
+    switch (route_linear(ctx, m, rows, tactic)) {
+    case Route::prefill: {
+        const PrefillShape s = plan_prefill(m->planes, rows, ctx->prefill_tuning);
+        std::snprintf(buf, sizeof buf, "prefill_gemm_kernel<%s> tile_m=%u tile_n=%u prefetch=%u m_tiles=%u groups=%u "
+                      "splits=%u", fmt, s.tile_m, s.tile_n, s.prefetch, s.m_tiles, s.groups, s.splits);
+        break;
+    }
+    case Route::gemv: {
+        const GemvShape g = plan_decode_gemv(m->planes, ctx->tuning);
+        std::snprintf(buf, sizeof buf, "decode_gemv_kernel<%s> rows_per_wave=%u depth=%u units_per_chunk=%u "
+                      "waves=%u groups=%u", fmt, g.rows_per_wave, g.depth, g.units_per_chunk, g.waves_per_group,
+                      static_cast<unsigned>(ceil_div(m->planes.nt, g.rows_per_wave)));
+        break;
+    }
+    case Route::fused: {
+        const FusedShape f = plan_decode_fused(m->planes, rows, ctx->tuning);
+        std::snprintf(buf, sizeof buf, "decode_fused_kernel<%s> rows_per_wave=%u waves=%u k_splits=%u groups=%u", fmt,
+                      f.rows_per_wave, f.waves_per_group, f.k_splits, f.groups);
+        break;
+    }
+    case Route::skinny_x:
+    case Route::skinny_loaded: {
+        const bool loaded = route_linear(ctx, m, rows, tactic) == Route::skinny_loaded;
+        const SkinnyShape k = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits);
+        std::snprintf(buf, sizeof buf, "%sskinny_kernel<%s%s> mt=%u tile_n=%u groups=%u splits=%u%s",
+                      loaded ? "split_rows_kernel + " : "", fmt, loaded ? "" : ", f32 input", k.mt, k.tile_n,
+                      k.groups, k.splits, k.splits > 1u ? " + split reduction" : "");
+        break;
+    }
+    case Route::decode_linear:
+        std::snprintf(buf, sizeof buf, "split_activations_kernel + decode_linear_kernel<%s>", fmt);
+        break;
+    }
+    return buf;
 }
 
 } // namespace
@@ -747,6 +811,22 @@ extern "C" {
 int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y,
                    const float* bias, uint32_t rows, int tactic) {
     return linear_rows(ctx, m, x, y, bias, rows, tactic, nullptr, nullptr);
+}
+
+int air_hip_linear_plan(const air_hip_context* ctx, const air_hip_matrix* m, uint32_t rows, int tactic, char* text,
+                        uint64_t capacity) {
+    if (!ctx || !m || !text || capacity == 0) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix and text must not be null, capacity non-zero");
+    }
+    if (tactic != AIR_HIP_LINEAR_AUTO && tactic != AIR_HIP_LINEAR_DECODE && tactic != AIR_HIP_LINEAR_PREFILL) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "unknown linear tactic %d", tactic);
+    }
+    if (rows == 0) return fail(AIR_HIP_INVALID_ARGUMENT, "linear batch width must be non-zero");
+    const std::string d = describe_linear(ctx, m, rows, tactic);
+    const std::size_t n = std::min<std::size_t>(d.size(), capacity - 1u);
+    std::memcpy(text, d.data(), n);
+    text[n] = '\0';
+    return AIR_HIP_OK;
 }
 
 int air_hip_linear_epilogue(air_hip_context* ctx, const air_hip_matrix* m, const float* x, uint32_t rows, float* out,
@@ -827,6 +907,7 @@ int air_hip_linear_epilogue(air_hip_context* ctx, const air_hip_matrix* m, const
 int air_hip_matrix_rows(air_hip_context* ctx, const air_hip_matrix* m, const int32_t* rows, uint32_t count,
                         float* out) {
     if (!ctx || !m || !rows || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    forget_loaded_source(ctx);
     if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
     if (count == 0) return AIR_HIP_OK;
     if (count > 65535u) return fail(AIR_HIP_UNSUPPORTED, "at most 65535 rows per call");
@@ -839,6 +920,7 @@ int air_hip_matrix_rows(air_hip_context* ctx, const air_hip_matrix* m, const int
 int air_hip_rms_norm(air_hip_context* ctx, const float* x, const float* weight, float* out, uint32_t m, uint64_t n,
                      double eps) {
     if (!ctx || !x || !weight || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    forget_loaded_source(ctx);
     if (n == 0 || !(eps >= 0.0)) return fail(AIR_HIP_INVALID_ARGUMENT, "width must be non-zero and eps non-negative");
     if (m == 0) return AIR_HIP_OK;
     DeviceScope scope(ctx->device);
@@ -850,6 +932,7 @@ int air_hip_rms_norm(air_hip_context* ctx, const float* x, const float* weight, 
 int air_hip_add_rms_norm(air_hip_context* ctx, float* x, const float* y, const float* weight, float* out, uint32_t m,
                          uint64_t n, double eps) {
     if (!ctx || !x || !y || !weight || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    forget_loaded_source(ctx);
     if (n == 0 || !(eps >= 0.0)) return fail(AIR_HIP_INVALID_ARGUMENT, "width must be non-zero and eps non-negative");
     if (out == x || out == y) return fail(AIR_HIP_INVALID_ARGUMENT, "out must not alias x or y");
     if (m == 0) return AIR_HIP_OK;
@@ -863,6 +946,7 @@ int air_hip_rope(air_hip_context* ctx, float* qkv, uint64_t row_stride, uint32_t
                  uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim, uint32_t rope_dims, const float* table,
                  uint64_t table_positions) {
     if (!ctx || !qkv || !positions || !table) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    forget_loaded_source(ctx);
     if (rope_dims == 0 || rope_dims % 2u != 0 || rope_dims > head_dim || table_positions == 0) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "RoPE needs an even rope_dims <= head_dim and a table");
     }
@@ -915,6 +999,7 @@ int air_hip_kv_append(air_hip_context* ctx, const air_hip_kv_layout* kv, const f
                       uint64_t q_width, uint32_t m, const int32_t* positions, const int32_t* page_tables,
                       uint32_t layer) {
     if (!ctx || !qkv || !positions || !page_tables) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    forget_loaded_source(ctx);
     if (int rc = check_kv(kv); rc != AIR_HIP_OK) return rc;
     if (layer >= kv->layers) return fail(AIR_HIP_INVALID_ARGUMENT, "layer %u is out of range", layer);
     if (row_stride < q_width + 2u * static_cast<uint64_t>(kv->kv_width)) {
@@ -936,6 +1021,7 @@ int air_hip_rope_kv_append(air_hip_context* ctx, const air_hip_kv_layout* kv, fl
     if (!ctx || !qkv || !positions || !page_tables || !table) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
     }
+    forget_loaded_source(ctx);
     if (int rc = check_kv(kv); rc != AIR_HIP_OK) return rc;
     if (layer >= kv->layers) return fail(AIR_HIP_INVALID_ARGUMENT, "layer %u is out of range", layer);
     if (rope_dims == 0 || rope_dims % 2u != 0 || rope_dims > head_dim || table_positions == 0) {
@@ -1004,6 +1090,7 @@ int air_hip_attention(air_hip_context* ctx, const air_hip_kv_layout* kv, const f
     if (!ctx || !qkv || !positions || !page_tables || !out) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
     }
+    forget_loaded_source(ctx);
     if (int rc = check_kv(kv); rc != AIR_HIP_OK) return rc;
     if (layer >= kv->layers) return fail(AIR_HIP_INVALID_ARGUMENT, "layer %u is out of range", layer);
     if (int rc = check_heads(kv, q_heads, kv_heads, head_dim, max_tokens); rc != AIR_HIP_OK) return rc;
@@ -1042,6 +1129,7 @@ int air_hip_attention_online(air_hip_context* ctx, const air_hip_kv_layout* kv, 
     if (!ctx || !qkv || !positions || !page_tables || !tiles || !out) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
     }
+    forget_loaded_source(ctx);
     if (int rc = check_kv(kv); rc != AIR_HIP_OK) return rc;
     if (layer >= kv->layers) return fail(AIR_HIP_INVALID_ARGUMENT, "layer %u is out of range", layer);
     if (int rc = check_heads(kv, q_heads, kv_heads, head_dim, max_tokens); rc != AIR_HIP_OK) return rc;
@@ -1071,6 +1159,7 @@ int air_hip_attention_online(air_hip_context* ctx, const air_hip_kv_layout* kv, 
 
 int air_hip_silu_mul(air_hip_context* ctx, const float* gate_up, float* out, uint32_t m, uint64_t ffn) {
     if (!ctx || !gate_up || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    forget_loaded_source(ctx);
     if (m == 0 || ffn == 0) return AIR_HIP_OK;
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
@@ -1080,6 +1169,7 @@ int air_hip_silu_mul(air_hip_context* ctx, const float* gate_up, float* out, uin
 
 int air_hip_add(air_hip_context* ctx, float* x, const float* y, uint64_t count) {
     if (!ctx || !x || !y) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    forget_loaded_source(ctx);
     if (count == 0) return AIR_HIP_OK;
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
@@ -1089,6 +1179,7 @@ int air_hip_add(air_hip_context* ctx, float* x, const float* y, uint64_t count) 
 
 int air_hip_argmax(air_hip_context* ctx, const float* logits, uint32_t m, uint64_t n, int32_t* out) {
     if (!ctx || !logits || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    forget_loaded_source(ctx);
     if (n == 0 || n > 0x7fffffffu) return fail(AIR_HIP_INVALID_ARGUMENT, "row width must be in [1, 2^31)");
     if (m == 0) return AIR_HIP_OK;
     DeviceScope scope(ctx->device);

@@ -374,24 +374,38 @@ __global__ __launch_bounds__(kThreads) void add_kernel(float* __restrict__ x, co
 }
 
 // First maximum of each row (std::max_element with operator<): the largest
-// value, the lowest index among equal values.  A NaN never wins (the
-// reference CUDA executor refuses non-finite logits); a row of NaNs gives 0.
+// value, the lowest index among equal values.  A row holding any non-finite
+// value (NaN or +-inf) gives -1 instead of an index: the reference CUDA
+// executor flags such a value and fails the step
+// (src/cuda/cuda_backend.cu:613-624, 2368).
 constexpr unsigned kArgmaxThreads = 1024;
 
-__device__ __forceinline__ void argmax_take(float v, std::uint32_t i, float& bv, std::uint32_t& bi) {
+// Merges a candidate (value, index) into the running best.
+__device__ __forceinline__ void argmax_merge(float v, std::uint32_t i, float& bv, std::uint32_t& bi) {
     if (v > bv || (v == bv && i < bi)) {
         bv = v;
         bi = i;
     }
 }
 
+// One logit: a non-finite value is never selected and marks the row.
+__device__ __forceinline__ void argmax_take(float v, std::uint32_t i, float& bv, std::uint32_t& bi, bool& bad) {
+    if (!__builtin_isfinite(v)) {
+        bad = true;
+        return;
+    }
+    argmax_merge(v, i, bv, bi);
+}
+
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ logits, std::uint64_t n,
                                                                 std::int32_t* __restrict__ out) {
     __shared__ float wave_v[kArgmaxThreads / 64];
     __shared__ std::uint32_t wave_i[kArgmaxThreads / 64];
+    __shared__ std::uint32_t wave_bad[kArgmaxThreads / 64];
     const float* row = logits + static_cast<std::uint64_t>(blockIdx.x) * n;
     float bv = -__builtin_huge_valf();
     std::uint32_t bi = 0xffffffffu;
+    bool bad = false;
     const bool vec = (n % 4u == 0) && (reinterpret_cast<std::uintptr_t>(row) % 16u == 0);
     if (vec) {
         // Coalesced float4 loads, four in flight per thread (the selection
@@ -411,33 +425,41 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
                 const std::uint64_t i = first + j * kArgmaxThreads;
                 if (i >= n4) continue;
                 const std::uint32_t base = static_cast<std::uint32_t>(4u * i);
-                argmax_take(v[j].x, base, bv, bi);
-                argmax_take(v[j].y, base + 1u, bv, bi);
-                argmax_take(v[j].z, base + 2u, bv, bi);
-                argmax_take(v[j].w, base + 3u, bv, bi);
+                argmax_take(v[j].x, base, bv, bi, bad);
+                argmax_take(v[j].y, base + 1u, bv, bi, bad);
+                argmax_take(v[j].z, base + 2u, bv, bi, bad);
+                argmax_take(v[j].w, base + 3u, bv, bi, bad);
             }
         }
     } else {
 #pragma unroll 8
         for (std::uint64_t i = threadIdx.x; i < n; i += kArgmaxThreads) {
-            argmax_take(row[i], static_cast<std::uint32_t>(i), bv, bi);
+            argmax_take(row[i], static_cast<std::uint32_t>(i), bv, bi, bad);
         }
     }
     for (int off = 32; off > 0; off >>= 1) {
         const float ov = __shfl_xor(bv, off);
         const std::uint32_t oi = __shfl_xor(bi, off);
-        argmax_take(ov, oi, bv, bi);
+        argmax_merge(ov, oi, bv, bi);
     }
+    const bool wave_has_bad = __any(bad ? 1 : 0) != 0;
     if ((threadIdx.x & 63u) == 0) {
         wave_v[threadIdx.x >> 6] = bv;
         wave_i[threadIdx.x >> 6] = bi;
+        wave_bad[threadIdx.x >> 6] = wave_has_bad ? 1u : 0u;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
         bv = wave_v[0];
         bi = wave_i[0];
-        for (unsigned w = 1; w < kArgmaxThreads / 64; ++w) argmax_take(wave_v[w], wave_i[w], bv, bi);
-        out[blockIdx.x] = static_cast<std::int32_t>(bi == 0xffffffffu ? 0u : bi);
+        std::uint32_t any_bad = wave_bad[0];
+        for (unsigned w = 1; w < kArgmaxThreads / 64; ++w) {
+            argmax_merge(wave_v[w], wave_i[w], bv, bi);
+            any_bad |= wave_bad[w];
+        }
+        // n >= 1 finite values always select an index; an empty selection
+        // means every value was non-finite, which any_bad already records.
+        out[blockIdx.x] = any_bad != 0u ? -1 : static_cast<std::int32_t>(bi);
     }
 }
 

@@ -63,6 +63,8 @@ struct HipPrepareOptions {
 };
 
 class HipStepEngine;
+struct StepResult;
+enum class RowOutput : std::uint8_t;
 
 class HipPreparedModel final : public runtime_detail::PreparedModel {
 public:
@@ -92,6 +94,14 @@ public:
         std::span<const runtime_detail::PrefillBatchItem> items) override;
     [[nodiscard]] Result<std::vector<TokenId>> decode_greedy_batch(
         std::span<const runtime_detail::GreedyDecodeBatchItem> items) override;
+    // The batched decode step of decode_greedy_batch returning every row's
+    // vocabulary logits instead of its greedy token (one row per sequence, on
+    // the same captured graph).  The reference's differential verifier
+    // compares executors on logits step by step (src/verification/main.cpp:
+    // 319-402); this is that comparison's batched entry point.  No
+    // counterpart in PreparedModel.
+    [[nodiscard]] Result<std::vector<std::vector<float>>> decode_batch_logits(
+        std::span<const runtime_detail::GreedyDecodeBatchItem> items);
 
     // The lm_head matrix and whether it is token_embd (tied embeddings).
     [[nodiscard]] air_hip_matrix* output_matrix() const noexcept { return output_.matrix; }
@@ -161,6 +171,8 @@ private:
     HipPrepareOptions options_{};
     std::unique_ptr<HipStepEngine> engine_;
     [[nodiscard]] Result<HipStepEngine*> engine_for(const ExecutionPlan& plan);
+    [[nodiscard]] Result<StepResult> decode_rows(std::span<const runtime_detail::GreedyDecodeBatchItem> items,
+                                                 RowOutput output);
 };
 
 // Paged fp32 K and V of every layer for max_tokens plus the two page tables,

@@ -477,9 +477,8 @@ Result<runtime_detail::PrefillBatchExecution> HipPreparedModel::prefill_batch(
     return execution;
 }
 
-Result<std::vector<TokenId>> HipPreparedModel::decode_greedy_batch(
-    std::span<const runtime_detail::GreedyDecodeBatchItem> items) {
-    if (items.empty()) return std::vector<TokenId>{};
+Result<StepResult> HipPreparedModel::decode_rows(std::span<const runtime_detail::GreedyDecodeBatchItem> items,
+                                                 RowOutput output) {
     if (!engine_) return Status::invalid_state("no HIP sequence has been created");
     if (items.size() > capabilities_.max_decode_batch_width) {
         return Status::invalid_argument("decode batch exceeds the advertised width");
@@ -500,12 +499,25 @@ Result<std::vector<TokenId>> HipPreparedModel::decode_greedy_batch(
             seq->decode_attention() != first->decode_attention()) {
             return Status::invalid_argument("decode batch mixes execution plans");
         }
-        rows.push_back({seq, item.token, RowOutput::greedy});
+        rows.push_back({seq, item.token, output});
     }
-    auto result = engine_->run(rows, first->decode_block_tactic(), first->decode_output_tactic(),
-                               first->decode_attention());
+    return engine_->run(rows, first->decode_block_tactic(), first->decode_output_tactic(), first->decode_attention());
+}
+
+Result<std::vector<TokenId>> HipPreparedModel::decode_greedy_batch(
+    std::span<const runtime_detail::GreedyDecodeBatchItem> items) {
+    if (items.empty()) return std::vector<TokenId>{};
+    auto result = decode_rows(items, RowOutput::greedy);
     if (!result) return result.status();
     return std::move(result.value().greedy);
+}
+
+Result<std::vector<std::vector<float>>> HipPreparedModel::decode_batch_logits(
+    std::span<const runtime_detail::GreedyDecodeBatchItem> items) {
+    if (items.empty()) return std::vector<std::vector<float>>{};
+    auto result = decode_rows(items, RowOutput::logits);
+    if (!result) return result.status();
+    return std::move(result.value().logits);
 }
 
 Result<std::unique_ptr<runtime_detail::SequenceState>> HipPreparedModel::restore_sequence(

@@ -649,12 +649,13 @@ Result<StepResult> HipStepEngine::run(std::span<const StepRow> rows, QuantizedLi
         }
     }
 
-    // Decode-shaped steps (one row per sequence, every row a greedy output)
-    // go through a graph captured per width: their page tables span the whole
-    // context and the attention is sized for it, so one graph serves every
-    // step of that width.
+    // Decode-shaped steps (one row per sequence, every row an output: greedy
+    // or logits) go through a graph captured per width: their page tables
+    // span the whole context and the attention is sized for it, so one graph
+    // serves every step of that width.  The graph runs the lm_head and the
+    // argmax over every row; logits rows are read back from its output.
     bool decode_shape = prepared_.options().decode_graphs && claims.size() == m && m <= output_rows_;
-    for (std::uint32_t r = 0; r < m && decode_shape; ++r) decode_shape = rows[r].output == RowOutput::greedy;
+    for (std::uint32_t r = 0; r < m && decode_shape; ++r) decode_shape = rows[r].output != RowOutput::none;
     if (decode_shape) table_pages = max_pages_;
 
     // Upload: tokens | positions | page tables [m][table_pages], one copy.
@@ -762,10 +763,24 @@ Result<StepResult> HipStepEngine::run(std::span<const StepRow> rows, QuantizedLi
         }
         if (!status) break;
         if (!(status = runtime_status(hipStreamSynchronize(hs), "hipStreamSynchronize"))) break;
-        for (std::uint32_t j = 0; j < k; ++j) {
-            if (rows[outputs[begin + j]].output == RowOutput::greedy) result.greedy.push_back(argmax_host[j]);
+        // Non-finite logits fail the step, as the reference executor's
+        // device flag and readback check do (cuda_backend.cu:613-624,
+        // 2331, 2368): the argmax marks such a row with -1.
+        for (std::uint32_t j = 0; j < k && status; ++j) {
+            if (rows[outputs[begin + j]].output != RowOutput::greedy) continue;
+            if (argmax_host[j] < 0) {
+                status = Status::internal_error("HIP executor produced non-finite logits");
+            } else {
+                result.greedy.push_back(argmax_host[j]);
+            }
         }
-        for (auto& row : logits) result.logits.push_back(std::move(row));
+        for (auto& row : logits) {
+            if (!std::all_of(row.begin(), row.end(), [](float v) { return std::isfinite(v); })) {
+                status = Status::internal_error("HIP executor produced non-finite logits");
+            }
+            result.logits.push_back(std::move(row));
+        }
+        if (!status) break;
     }
     // Always drain the stream: the staging buffer is reused by the next step.
     const Status drained = runtime_status(hipStreamSynchronize(hs), "hipStreamSynchronize");

@@ -57,6 +57,20 @@ def gate_up_launch_bytes(m: int) -> int:
     return 2 * (w_bytes(HIDDEN, FFN) + 4 * m * FFN) + 4 * m * HIDDEN
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo) and logical CPU count."""
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return f"{name} ({os.cpu_count()} logical CPUs visible)"
+
+
 def cpu_baseline(canon_host, k: int, n: int, target_s: float):
     """Times the reference matvec on the host, single-threaded like the
     reference (src/reference/tensor_reader.cpp:369-394): AIR's own code from
@@ -87,6 +101,7 @@ def cpu_baseline(canon_host, k: int, n: int, target_s: float):
         "value": round(algo / dt / 1e9, 4),
         "unit": "GB/s",
         "cores": 1,
+        "cpu": cpu_model(),
         "kind": kind,
         "sample": f"{reps} x M=1 matvec over one fused 7B gate|up matrix (Q8_0 {n}x{k}, "
                   f"{w_bytes(k, n) / 1e6:.0f} MB), {dt:.1f} s",

@@ -54,7 +54,7 @@ enum {
 };
 
 /* Linear tactics: the HIP members of AIR's QuantizedLinearExecutionKind
- * (include/air/execution.hpp:159-165).
+ * (include/air/execution.hpp:35-41).
  *   DECODE  exact integer codes as f16 MFMA operands, activations split into
  *           f16 hi+lo parts with a per-row power-of-two scale, per-block f32
  *           scale epilogue.  M = 1..64.  Relative L2 error vs the double
@@ -222,6 +222,15 @@ int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* matrix,
                    const float* x, float* y, const float* bias,
                    uint32_t m, int tactic);
 
+/* One line of text naming the kernels and launch shape air_hip_linear would
+ * use for this matrix, m rows and tactic through this context (with its
+ * tuning overrides), e.g. "decode_gemv_kernel<q8_0> rows_per_wave=1 depth=1
+ * units_per_chunk=2 waves=8 groups=2368".  Launches nothing; text is cut to
+ * capacity - 1 characters and NUL-terminated.  For tests and profiles that
+ * name the variant they exercised.  No counterpart in the reference. */
+int air_hip_linear_plan(const air_hip_context* ctx, const air_hip_matrix* matrix, uint32_t m, int tactic,
+                        char* text, uint64_t capacity);
+
 /* The M = 1 decode linear with its element-wise neighbours in the step
  * fused into the one launch, for a single-sequence decode loop: the
  * reference runs them as separate kernels around the projection
@@ -261,8 +270,10 @@ int air_hip_decode_linear_fused(air_hip_context* ctx, const air_hip_matrix* matr
  *     norm_out is also split into the context's activation workspace as
  *     air_hip_activations_load(norm_out, n, rows) would split it; the next
  *     linear this context runs on x == norm_out with the same width and rows
- *     uses that split instead of splitting again (the caller must not change
- *     norm_out in between; any other activation load cancels it).
+ *     uses that split instead of splitting again.  Any other call through
+ *     this context that writes device memory cancels it (that linear then
+ *     splits norm_out itself); changing norm_out by other means in between
+ *     is the caller's error.
  * Bit-identical to air_hip_linear (same tactic) followed by that call.  Where
  * the linear runs as a skinny launch with a K split (decode widths 2..64),
  * its split reduction applies the epilogue, so the epilogue costs no launch
@@ -403,7 +414,10 @@ int air_hip_silu_mul(air_hip_context* ctx, const float* gate_up, float* out, uin
 int air_hip_add(air_hip_context* ctx, float* x, const float* y, uint64_t count);
 
 /* out[r] = index of the first maximum of logits[r][0..n) (greedy selection,
- * src/runtime/sampling.cpp:13-16). */
+ * src/runtime/sampling.cpp:13-16), or -1 when row r holds a non-finite value
+ * (NaN or +-inf): the reference's device selection flags such a value and
+ * fails the step with "non-finite logits" (src/cuda/cuda_backend.cu:613-624,
+ * 2368), so a caller treats -1 as internal_error. */
 int air_hip_argmax(air_hip_context* ctx, const float* logits, uint32_t m, uint64_t n, int32_t* out);
 
 #ifdef __cplusplus

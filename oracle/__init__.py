@@ -44,6 +44,13 @@ def _load_oracle() -> ctypes.CDLL:
         lib.oracle_decode.argtypes = [ctypes.c_int, _P, _U64, _U64, _P]
         lib.oracle_linear_rows.restype = ctypes.c_int
         lib.oracle_linear_rows.argtypes = [ctypes.c_int, _P, _U64, _U64, _U64, ctypes.c_uint32, _P, _P, _P, _U64, _U64]
+        lib.oracle_linear_row_list.restype = ctypes.c_int
+        lib.oracle_linear_row_list.argtypes = [ctypes.c_int, _P, _U64, _U64, _U64, ctypes.c_uint32, _P, _P, _P, _U64,
+                                               _P]
+        lib.oracle_set_threads.restype = None
+        lib.oracle_set_threads.argtypes = [ctypes.c_uint32]
+        lib.oracle_threads.restype = ctypes.c_uint32
+        lib.oracle_threads.argtypes = []
         _oracle = lib
     return _oracle
 
@@ -105,6 +112,34 @@ def linear(type_id: int, data: np.ndarray, k: int, n: int, x: np.ndarray,
     if rc != 0:
         raise ValueError(f"oracle_linear_rows failed with status {rc}")
     return y
+
+
+def linear_row_list(type_id: int, data: np.ndarray, k: int, n: int, x: np.ndarray, rows,
+                    bias: Optional[np.ndarray] = None) -> np.ndarray:
+    """Output rows ``rows`` of the linear: y[m][j] = row rows[j] of input row m,
+    each computed exactly as :func:`linear` computes it."""
+    data = np.ascontiguousarray(data, dtype=np.uint8).reshape(-1)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, k)
+    sel = np.ascontiguousarray(rows, dtype=np.uint64).reshape(-1)
+    m = x.shape[0]
+    y = np.zeros((m, sel.size), dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    rc = _load_oracle().oracle_linear_row_list(type_id, _addr(data), data.nbytes, k, n, m, _addr(x),
+                                               _addr(b) if b is not None else None,
+                                               _addr(sel) if sel.size else None, sel.size, _addr(y))
+    if rc != 0:
+        raise ValueError(f"oracle_linear_row_list failed with status {rc}")
+    return y
+
+
+def set_threads(threads: int) -> None:
+    """Threads the oracle linears split their output rows over (results are
+    bit-identical for every count)."""
+    _load_oracle().oracle_set_threads(max(1, int(threads)))
+
+
+def threads() -> int:
+    return int(_load_oracle().oracle_threads())
 
 
 def ref_decode(type_id: int, data: np.ndarray, elements: int) -> np.ndarray:

@@ -8,6 +8,7 @@
  */
 #include "air_oracle.h"
 
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -200,6 +201,89 @@ static int row_geometry(int type, uint64_t K, uint64_t N, uint64_t nbytes, uint6
     return ORACLE_OK;
 }
 
+static uint32_t g_threads = 1;
+
+void oracle_set_threads(uint32_t threads) { g_threads = threads == 0 ? 1 : (threads > 64 ? 64 : threads); }
+uint32_t oracle_threads(void) { return g_threads; }
+
+/* One output row r of every input row (ReferenceTensorReader::matvec,
+ * src/reference/tensor_reader.cpp:369-394, plus add_optional_bias):
+ * y[m * y_stride + col] = float(sum_k double(w[r,k]) * double(x[m,k])) (+ bias[r]). */
+static int linear_one_row(int type, const uint8_t* bytes, uint64_t row_bytes, uint64_t K, uint32_t M,
+                          const float* x, const float* bias, uint64_t r, float* w, float* y, uint64_t y_stride,
+                          uint64_t col) {
+    int rc = oracle_decode(type, bytes + r * row_bytes, row_bytes, K, w);
+    if (rc != ORACLE_OK) return rc;
+    for (uint32_t m = 0; m < M; ++m) {
+        const float* xm = x + (uint64_t)m * K;
+        double sum = 0.0;
+        for (uint64_t k = 0; k < K; ++k) sum += (double)w[k] * (double)xm[k];
+        float out = (float)sum;
+        if (bias) out += bias[r]; /* add_in_place after the matvec, f32 */
+        y[(uint64_t)m * y_stride + col] = out;
+    }
+    return ORACLE_OK;
+}
+
+/* A slice of the output rows: either the range [begin, end) (rows == NULL,
+ * output column = row) or the listed rows rows[begin..end) (column = index). */
+typedef struct linear_job {
+    int type;
+    const uint8_t* bytes;
+    uint64_t row_bytes, K, y_stride;
+    uint32_t M;
+    const float* x;
+    const float* bias;
+    const uint64_t* rows;
+    uint64_t begin, end;
+    float* y;
+    int rc;
+} linear_job;
+
+static void* linear_job_run(void* arg) {
+    linear_job* j = (linear_job*)arg;
+    /* the reference decodes each row into a fresh heap vector (:384); one
+       buffer per job computes the same values */
+    float* w = (float*)malloc(j->K * sizeof(float));
+    j->rc = w ? ORACLE_OK : ORACLE_DATA_ERROR;
+    for (uint64_t i = j->begin; w && i < j->end && j->rc == ORACLE_OK; ++i) {
+        const uint64_t r = j->rows ? j->rows[i] : i;
+        j->rc = linear_one_row(j->type, j->bytes, j->row_bytes, j->K, j->M, j->x, j->bias, r, w, j->y, j->y_stride,
+                               j->rows ? i : r);
+    }
+    free(w);
+    return NULL;
+}
+
+/* Runs `job` over [begin, end) on up to g_threads threads (contiguous
+ * slices; every row is computed by exactly one thread). */
+static int run_linear_jobs(linear_job job, uint64_t begin, uint64_t end) {
+    const uint64_t count = end - begin;
+    uint64_t threads = g_threads;
+    /* below ~1M multiply-adds a thread costs more than it saves */
+    if (count * job.K * job.M < (1u << 20)) threads = 1;
+    if (threads > count) threads = count ? count : 1;
+    linear_job jobs[64];
+    pthread_t tids[64];
+    int started[64] = {0};
+    for (uint64_t t = 0; t < threads; ++t) {
+        jobs[t] = job;
+        jobs[t].begin = begin + count * t / threads;
+        jobs[t].end = begin + count * (t + 1) / threads;
+        if (t + 1 < threads && pthread_create(&tids[t], NULL, linear_job_run, &jobs[t]) == 0) {
+            started[t] = 1;
+        } else {
+            linear_job_run(&jobs[t]);   /* the last slice (or a failed spawn) on this thread */
+        }
+    }
+    int rc = ORACLE_OK;
+    for (uint64_t t = 0; t < threads; ++t) {
+        if (started[t]) pthread_join(tids[t], NULL);
+        if (rc == ORACLE_OK && jobs[t].rc != ORACLE_OK) rc = jobs[t].rc;
+    }
+    return rc;
+}
+
 /* ReferenceTensorReader::matvec, src/reference/tensor_reader.cpp:369-394. */
 int oracle_linear_rows(int type, const uint8_t* bytes, uint64_t nbytes,
                        uint64_t K, uint64_t N, uint32_t M,
@@ -209,23 +293,23 @@ int oracle_linear_rows(int type, const uint8_t* bytes, uint64_t nbytes,
     int rc = row_geometry(type, K, N, nbytes, &row_bytes);
     if (rc != ORACLE_OK) return rc;
     if (row_begin > row_end || row_end > N) return ORACLE_INVALID_ARGUMENT;
-    for (uint64_t r = row_begin; r < row_end; ++r) {
-        /* the reference decodes each row into a fresh heap vector (:384) */
-        float* w = (float*)malloc(K * sizeof(float));
-        if (!w) return ORACLE_DATA_ERROR;
-        rc = oracle_decode(type, bytes + r * row_bytes, row_bytes, K, w);
-        if (rc != ORACLE_OK) { free(w); return rc; }
-        for (uint32_t m = 0; m < M; ++m) {
-            const float* xm = x + (uint64_t)m * K;
-            double sum = 0.0;
-            for (uint64_t k = 0; k < K; ++k) sum += (double)w[k] * (double)xm[k];
-            float out = (float)sum;
-            if (bias) out += bias[r]; /* add_in_place after the matvec, f32 */
-            y[(uint64_t)m * N + r] = out;
-        }
-        free(w);
+    const linear_job job = {type, bytes, row_bytes, K, N, M, x, bias, NULL, 0, 0, y, ORACLE_OK};
+    return run_linear_jobs(job, row_begin, row_end);
+}
+
+int oracle_linear_row_list(int type, const uint8_t* bytes, uint64_t nbytes,
+                           uint64_t K, uint64_t N, uint32_t M,
+                           const float* x, const float* bias,
+                           const uint64_t* rows, uint64_t count, float* y) {
+    uint64_t row_bytes = 0;
+    int rc = row_geometry(type, K, N, nbytes, &row_bytes);
+    if (rc != ORACLE_OK) return rc;
+    if (count && !rows) return ORACLE_INVALID_ARGUMENT;
+    for (uint64_t i = 0; i < count; ++i) {
+        if (rows[i] >= N) return ORACLE_INVALID_ARGUMENT;
     }
-    return ORACLE_OK;
+    const linear_job job = {type, bytes, row_bytes, K, count, M, x, bias, rows, 0, 0, y, ORACLE_OK};
+    return run_linear_jobs(job, 0, count);
 }
 
 int oracle_linear(int type, const uint8_t* bytes, uint64_t nbytes,

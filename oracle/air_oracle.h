@@ -77,6 +77,23 @@ int oracle_linear_rows(int type, const uint8_t* bytes, uint64_t nbytes,
                        const float* x, const float* bias, float* y,
                        uint64_t row_begin, uint64_t row_end);
 
+/* Rows rows[0..count) of the linear: y[m][j] is output row rows[j] of input
+ * row m (y is [M x count]), computed exactly as oracle_linear computes that
+ * row.  For parity checks of very large matrices on a seeded sample of
+ * rows. */
+int oracle_linear_row_list(int type, const uint8_t* bytes, uint64_t nbytes,
+                           uint64_t K, uint64_t N, uint32_t M,
+                           const float* x, const float* bias,
+                           const uint64_t* rows, uint64_t count, float* y);
+
+/* Worker threads the linears above may split their output rows over (default
+ * 1, at most 64).  Each output row is still one sequential double sum in k
+ * order, computed by one thread, so the results are bit-identical for every
+ * thread count; the reference itself is single-threaded
+ * (tensor_reader.cpp:383-393). */
+void oracle_set_threads(uint32_t threads);
+uint32_t oracle_threads(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -187,9 +187,11 @@ int oracle_qwen2_step(const oracle_qwen2_model* m, oracle_qwen2_cache* c, int32_
         if ((rc = linear_of(&L->down, NULL, gate, proj))) goto done;
         for (uint64_t i = 0; i < e; ++i) hidden[i] += proj[i];
     }
-    if ((rc = vector_of(&m->output_norm, e, wbuf))) goto done;
-    rms_norm(hidden, wbuf, e, m->eps, normed);
-    rc = linear_of(m->output.bytes ? &m->output : &m->token_embd, &m->output_bias, normed, logits);
+    if (logits) {
+        if ((rc = vector_of(&m->output_norm, e, wbuf))) goto done;
+        rms_norm(hidden, wbuf, e, m->eps, normed);
+        rc = linear_of(m->output.bytes ? &m->output : &m->token_embd, &m->output_bias, normed, logits);
+    }
     if (rc == Q_OK) c->tokens = pos + 1;
 done:
     free(hidden); free(normed); free(wbuf); free(q); free(k); free(v);

@@ -55,7 +55,10 @@ typedef struct oracle_qwen2_cache {
 int oracle_qwen2_cache_init(const oracle_qwen2_model* model, oracle_qwen2_cache* cache, uint64_t capacity);
 void oracle_qwen2_cache_free(oracle_qwen2_cache* cache);
 
-/* Appends `token` at position cache->tokens and writes the vocabulary logits. */
+/* Appends `token` at position cache->tokens and writes the vocabulary logits.
+ * logits == NULL skips the final norm and the lm_head (a prompt token whose
+ * logits nobody reads); the cache advances exactly as with logits.  The
+ * linears run on oracle_set_threads() threads (bit-identical results). */
 int oracle_qwen2_step(const oracle_qwen2_model* model, oracle_qwen2_cache* cache, int32_t token, float* logits);
 
 /* Index of the first maximum (std::max_element). */

@@ -403,6 +403,19 @@ def test_linear_epilogue_matches_separate_kernels(torch_cuda, hip_ctx, type_id, 
                 capi.check(lib.air_hip_linear(h, mat2.handle, fresh.data_ptr(), y2_ref.data_ptr(), None, m, dec))
                 torch.cuda.synchronize()
                 assert np.array_equal(bits(y2), bits(y2_ref)), case
+                # another kernel of the context rewriting the norm's output in
+                # between (here the RMSNorm with other weights): the split is
+                # not reused either
+                capi.check(lib.air_hip_linear_epilogue(h, mat.handle, x.data_ptr(), m, resid.data_ptr(),
+                                                       bias.data_ptr(), capi.EPILOGUE_RESIDUAL_LOAD, w.data_ptr(),
+                                                       normed.data_ptr(), eps, dec))
+                w_other = w * 3.0
+                capi.check(lib.air_hip_rms_norm(h, resid.data_ptr(), w_other.data_ptr(), normed.data_ptr(), m, n, eps))
+                fresh = normed.clone()
+                capi.check(lib.air_hip_linear(h, mat2.handle, normed.data_ptr(), y2.data_ptr(), None, m, dec))
+                capi.check(lib.air_hip_linear(h, mat2.handle, fresh.data_ptr(), y2_ref.data_ptr(), None, m, dec))
+                torch.cuda.synchronize()
+                assert np.array_equal(bits(y2), bits(y2_ref)), case
         x = _dev(torch, helpers.activations(8, k, seed=1))
         out = torch.empty((8, n), dtype=torch.float32, device="cuda:0")
         assert lib.air_hip_linear_epilogue(h, mat.handle, x.data_ptr(), 8, out.data_ptr(), None,
@@ -420,3 +433,28 @@ def test_linear_epilogue_matches_separate_kernels(torch_cuda, hip_ctx, type_id, 
         mat.release()
         if mat2 is not None:
             mat2.release()
+
+
+def test_argmax_flags_non_finite_rows(torch_cuda, hip_ctx):
+    """air_hip_argmax: the first maximum of each row (lowest index among
+    equal values, sampling.cpp:13-16), and -1 for a row holding NaN or
+    +-inf anywhere -- the reference refuses such logits
+    (cuda_backend.cu:613-624, 2368).  Both the vectorised and the scalar
+    row paths."""
+    torch = torch_cuda
+    lib = capi.lib()
+    for n in (152064, 1001):                          # float4 rows, and an odd width (scalar loop)
+        rng = np.random.default_rng(n)
+        rows = rng.standard_normal((7, n)).astype(np.float32)
+        rows[1, 5] = np.nan
+        rows[2, n - 1] = np.inf
+        rows[3, n // 2] = -np.inf
+        rows[4, :] = np.nan
+        rows[5, [11, 700]] = 50.0                     # a tie: the lower index wins
+        rows[6, 0] = 50.0
+        x = _dev(torch, rows)
+        out = torch.full((7,), 12345, dtype=torch.int32, device="cuda:0")
+        capi.check(lib.air_hip_argmax(hip_ctx.handle, x.data_ptr(), 7, n, out.data_ptr()))
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().tolist()
+        assert got == [int(np.argmax(rows[0])), -1, -1, -1, -1, 11, 0], (n, got)

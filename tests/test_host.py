@@ -34,3 +34,13 @@ def test_host_cpu():
 def test_host_gpu():
     assert os.path.exists(BINARY), "tests/host/host_tests is not built"
     _run("gpu", 110)
+
+
+@pytest.mark.gpu
+def test_host_gpu_qwen2_7b_width():
+    """configs[4]'s geometry (two layers at the full Qwen2-7B width) through
+    prefill_batch at 512 rows on the MFMA tactic and graph-replayed decode at
+    widths 4, 2 and 1, teacher-forced against the C oracle (logits and
+    margin-certified top-1 per decision)."""
+    assert os.path.exists(BINARY), "tests/host/host_tests is not built"
+    _run("gpu7b", 280)
