@@ -143,6 +143,7 @@ SIGNATURES = {
     "air_hip_linear_loaded": (_I, [_P, _P, _P, _P, _I]),
     "air_hip_linear": (_I, [_P, _P, _P, _P, _P, _U32, _I]),
     "air_hip_linear_plan": (_I, [_P, _P, _U32, _I, ctypes.c_char_p, _U64]),
+    "air_hip_linear_noalloc": (_I, [_P, _P, _P, _P, _P, _U32, _I]),
 }
 
 
@@ -281,6 +282,10 @@ class Matrix:
 
     def linear(self, x, y, m: int, bias=None, tactic: int = LINEAR_AUTO) -> None:
         check(lib().air_hip_linear(self.ctx.handle, self.handle, ptr(x), ptr(y), ptr(bias), m, tactic))
+
+    def linear_noalloc(self, x, y, m: int, bias=None, tactic: int = LINEAR_AUTO) -> None:
+        """air_hip_linear_noalloc: decode widths 1..64, no allocation."""
+        check(lib().air_hip_linear_noalloc(self.ctx.handle, self.handle, ptr(x), ptr(y), ptr(bias), m, tactic))
 
     def plan(self, m: int, tactic: int = LINEAR_AUTO) -> str:
         """The kernels and launch shape a linear of m rows runs on."""

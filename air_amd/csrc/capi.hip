@@ -20,10 +20,19 @@
 #include <cstdio>
 #include <cstring>
 #include <limits>
+#include <mutex>
 #include <new>
 #include <string>
 
 using namespace air_hip;
+
+// Device memory of air_hip_linear_noalloc: one array per GPU, allocated with
+// the code object when the library is loaded on that GPU and held until the
+// process ends.  In host code this name is a host-side stand-in, not a
+// device address: host code uses only the per-device pointer that
+// hipGetSymbolAddress returns for it (noalloc_scratch below).
+constexpr std::uint64_t kNoAllocScratchBytes = 16ull << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 struct air_hip_context {
     int device{0};
@@ -67,6 +76,8 @@ struct air_hip_context {
     std::uint64_t attention_scratch_bytes{0};
     void* epilogue_rows{nullptr};           // linear output of air_hip_linear_epilogue's unfused route
     std::uint64_t epilogue_rows_bytes{0};
+    // This device's `scratch` array (hipGetSymbolAddress at context creation).
+    void* noalloc_scratch{nullptr};
     // Bumped whenever a context-owned buffer is (re)allocated: launches
     // recorded into a graph use the current buffers while it is unchanged.
     std::uint64_t generation{0};
@@ -166,6 +177,25 @@ int load_activations_for(air_hip_context* ctx, const float* x, std::uint64_t k, 
     const bool split = ready == x && ctx->loaded_k == k && ctx->loaded_rows == rows &&
                        ctx->loaded_row_scaled == row_scaled;
     return split ? AIR_HIP_OK : air_hip_activations_load(ctx, x, k, rows);
+}
+
+// Per-device address of `scratch`, looked up once per device with that
+// device current (each GPU holds its own copy at its own address).
+std::mutex g_scratch_mutex;
+std::vector<void*> g_scratch_address;
+
+int noalloc_scratch(int device, void** out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (static_cast<std::size_t>(device) >= g_scratch_address.size()) g_scratch_address.resize(device + 1u, nullptr);
+    if (!g_scratch_address[device]) {
+        void* p = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !p) return hip_fail(err != hipSuccess ? err : hipErrorInvalidSymbol,
+                                                     "hipGetSymbolAddress(scratch)");
+        g_scratch_address[device] = p;
+    }
+    *out = g_scratch_address[device];
+    return AIR_HIP_OK;
 }
 
 // Every entry point that writes device memory through the context forgets
@@ -349,10 +379,17 @@ int air_hip_context_create(int device, void* stream, air_hip_context** out) {
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
         return fail(AIR_HIP_UNSUPPORTED, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
     }
+    void* scratch_ptr = nullptr;
+    {
+        DeviceScope scope(device);
+        if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+        if (int rc = noalloc_scratch(device, &scratch_ptr); rc != AIR_HIP_OK) return rc;
+    }
     auto* ctx = new (std::nothrow) air_hip_context();
     if (!ctx) return fail(AIR_HIP_INTERNAL_ERROR, "out of host memory");
     ctx->device = device;
     ctx->stream = static_cast<hipStream_t>(stream);
+    ctx->noalloc_scratch = scratch_ptr;
     *out = ctx;
     return AIR_HIP_OK;
 }
@@ -811,6 +848,85 @@ extern "C" {
 int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y,
                    const float* bias, uint32_t rows, int tactic) {
     return linear_rows(ctx, m, x, y, bias, rows, tactic, nullptr, nullptr);
+}
+
+int air_hip_linear_noalloc(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y, const float* bias,
+                           uint32_t rows, int tactic) {
+    if (!ctx || !m || !x || !y) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix, x and y must not be null");
+    forget_loaded_source(ctx);
+    if (static_cast<const void*>(x) == static_cast<const void*>(y)) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "y must not alias x");
+    }
+    if (tactic != AIR_HIP_LINEAR_AUTO && tactic != AIR_HIP_LINEAR_DECODE) {
+        return fail(tactic == AIR_HIP_LINEAR_PREFILL ? AIR_HIP_UNSUPPORTED : AIR_HIP_INVALID_ARGUMENT,
+                    "the no-allocation linear runs the decode tactic only (tactic %d)", tactic);
+    }
+    if (rows == 0) return fail(AIR_HIP_INVALID_ARGUMENT, "linear batch width must be non-zero");
+    if (rows > AIR_HIP_MAX_DECODE_ROWS) {
+        return fail(AIR_HIP_UNSUPPORTED, "the no-allocation linear covers decode widths up to %u, not %u",
+                    AIR_HIP_MAX_DECODE_ROWS, rows);
+    }
+    if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
+    if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
+    if (!ctx->noalloc_scratch) return fail(AIR_HIP_INTERNAL_ERROR, "the device scratch array is not mapped");
+    // Same route, plans and kernels as air_hip_linear with this context's
+    // settings, so the results are bit-identical; only the buffers differ:
+    // the split activations at the start of the scratch array, the K-split
+    // partials after them (256-byte aligned).  Each launch writes every
+    // scratch byte it later reads, so nothing needs clearing between calls.
+    const Route route = route_linear(ctx, m, rows, tactic);
+    const TilePlanes& p = m->planes;
+    const std::uint64_t kp = ceil_div(p.k, kSplitK) * kSplitK;
+    std::uint64_t ws_bytes = 0, partial_bytes = 0;
+    SkinnyShape shape{};
+    if (route == Route::skinny_x || route == Route::skinny_loaded) {
+        shape = plan_skinny(p, rows, ctx->skinny_tile_n, ctx->skinny_splits);
+        partial_bytes = skinny_partials_bytes(shape, rows, p.n);
+    }
+    if (route == Route::skinny_loaded || route == Route::decode_linear) {
+        ws_bytes = ceil_div(split_workspace_bytes(kp, rows), 256u) * 256u;
+    }
+    if (route == Route::fused && plan_decode_fused(p, rows, ctx->tuning).k_splits > 1u) {
+        return fail(AIR_HIP_UNSUPPORTED, "the no-allocation linear does not run the fused kernel's cross-workgroup "
+                    "K split (a context tuning override)");
+    }
+    if (ws_bytes + partial_bytes > kNoAllocScratchBytes) {
+        return fail(AIR_HIP_UNSUPPORTED, "this linear needs %llu bytes of scratch; the no-allocation array holds %llu",
+                    static_cast<unsigned long long>(ws_bytes + partial_bytes),
+                    static_cast<unsigned long long>(kNoAllocScratchBytes));
+    }
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    auto* base = static_cast<unsigned char*>(ctx->noalloc_scratch);
+    float* partials = reinterpret_cast<float*>(base + ws_bytes);
+    const SplitWorkspace ws = carve_split_workspace(base, kp, rows);
+    hipError_t err = hipSuccess;
+    switch (route) {
+    case Route::gemv:
+        err = launch_decode_gemv(p, x, bias, y, plan_decode_gemv(p, ctx->tuning), ctx->stream);
+        break;
+    case Route::fused:
+        err = launch_decode_fused(p, x, bias, y, rows, plan_decode_fused(p, rows, ctx->tuning), nullptr, nullptr,
+                                  ctx->stream);
+        break;
+    case Route::skinny_x:
+        err = launch_skinny_linear_x(p, x, bias, y, rows, shape, partials, ctx->stream);
+        break;
+    case Route::skinny_loaded:
+        err = launch_split_activations_rows(x, rows, p.k, kp, ws, ctx->stream);
+        if (err == hipSuccess) err = launch_skinny_linear(p, ws, bias, y, rows, shape, partials, ctx->stream);
+        break;
+    case Route::decode_linear:
+        err = launch_split_activations(x, rows, p.k, kp, ws, ctx->stream);
+        if (err == hipSuccess) err = launch_decode_linear(p, ws, bias, y, rows, ctx->tuning, ctx->stream);
+        break;
+    case Route::prefill:
+        return fail(AIR_HIP_UNSUPPORTED, "the no-allocation linear runs the decode tactic only");
+    }
+    if (err != hipSuccess) return hip_fail(err, "no-allocation decode linear");
+    ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
+    ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
+    return AIR_HIP_OK;
 }
 
 int air_hip_linear_plan(const air_hip_context* ctx, const air_hip_matrix* m, uint32_t rows, int tactic, char* text,

@@ -231,6 +231,24 @@ int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* matrix,
 int air_hip_linear_plan(const air_hip_context* ctx, const air_hip_matrix* matrix, uint32_t m, int tactic,
                         char* text, uint64_t capacity);
 
+/* air_hip_linear for decode widths m = 1..64 (tactic AUTO or DECODE) that
+ * allocates nothing: no hipMalloc / hipFree and no allocating library call,
+ * so code under HIP graph capture, tight serving loops and harnesses that
+ * forbid allocation can call it.  Same kernels and launch shapes as
+ * air_hip_linear through this context (its tuning overrides included), so
+ * the outputs are bit-identical.  Its split activations and K-split partials
+ * live in a 16 MiB device array per GPU, held from library load until the
+ * process ends (every Qwen2-7B projection and lm_head at m <= 64 needs at
+ * most 12.5 MiB); a linear needing more, m > 64, the PREFILL tactic, and the
+ * fused kernel's cross-workgroup K split (a tuning override) return
+ * AIR_HIP_UNSUPPORTED.  The array keeps the last call's contents and is
+ * shared by every call on that GPU: calls that overlap on one GPU (other
+ * streams, other contexts, other threads) race and must be serialised by
+ * the caller.  No counterpart in the reference: it exists for the callers
+ * that cannot allocate. */
+int air_hip_linear_noalloc(air_hip_context* ctx, const air_hip_matrix* matrix, const float* x, float* y,
+                           const float* bias, uint32_t m, int tactic);
+
 /* The M = 1 decode linear with its element-wise neighbours in the step
  * fused into the one launch, for a single-sequence decode loop: the
  * reference runs them as separate kernels around the projection
