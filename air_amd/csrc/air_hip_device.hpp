@@ -54,15 +54,24 @@ __device__ __forceinline__ void q8_dword_to_half(std::uint32_t u, half2v& lo, ha
 }
 
 // One nibble dword (placement kNibblePos) -> eight exact f16 values n - offset.
+// Each half is the nibble under an exponent (f16 0x64nn = 1024 + n, 0x54n0 =
+// 64 + n) minus that bias.  The two exponent patterns are passed through an
+// empty asm so they live in VGPRs: VOP3 takes no literal on this chip, and
+// with the mask in an SGPR and the pattern in a VGPR the mask-and-insert is
+// one v_and_or_b32 instead of an AND and an OR (the asm is not volatile, so
+// its copies are shared and hoisted).
 template <int Offset>
 __device__ __forceinline__ half8v nibble_dword_to_half8(std::uint32_t w) {
     const half2v b_hi = {(_Float16)(1024.0f + Offset), (_Float16)(1024.0f + Offset)};
     const half2v b_lo = {(_Float16)(64.0f + Offset), (_Float16)(64.0f + Offset)};
+    std::uint32_t e_hi = 0x64006400u, e_lo = 0x54005400u;
+    asm("" : "+v"(e_hi));
+    asm("" : "+v"(e_lo));
     const std::uint32_t w8 = w >> 8;
-    const half2v p0 = bits_as_half2((w & 0x000f000fu) | 0x64006400u) - b_hi;
-    const half2v p1 = bits_as_half2((w & 0x00f000f0u) | 0x54005400u) - b_lo;
-    const half2v p2 = bits_as_half2((w8 & 0x000f000fu) | 0x64006400u) - b_hi;
-    const half2v p3 = bits_as_half2((w8 & 0x00f000f0u) | 0x54005400u) - b_lo;
+    const half2v p0 = bits_as_half2((w & 0x000f000fu) | e_hi) - b_hi;
+    const half2v p1 = bits_as_half2((w & 0x00f000f0u) | e_lo) - b_lo;
+    const half2v p2 = bits_as_half2((w8 & 0x000f000fu) | e_hi) - b_hi;
+    const half2v p3 = bits_as_half2((w8 & 0x00f000f0u) | e_lo) - b_lo;
     half8v out;
     out[0] = p0[0]; out[1] = p0[1]; out[2] = p1[0]; out[3] = p1[1];
     out[4] = p2[0]; out[5] = p2[1]; out[6] = p3[0]; out[7] = p3[1];

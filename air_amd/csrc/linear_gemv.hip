@@ -221,33 +221,74 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U, NORM>& ch, 
     }
     const std::uint32_t group = lane >> 4;
 
-    // Sums in the scaled domain, multiplied by inv once at the end.  The
-    // blocks of one tile (Q4_K: of one half tile) own one lane group of D, so
-    // the tile's scale record is masked once per tile: lanes of other groups
-    // add 0 x (a finite product).
+    // Sums in the scaled domain, multiplied by inv once at the end.  Q8_0 /
+    // Q4_0: the blocks of one tile own one lane group of D, so the tile's
+    // scale record is masked once per tile: lanes of other groups add
+    // 0 x (a finite product).
     float4v cacc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) cacc[r] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (FMT == kQ4_K) {
+        // A lane's four D slots hold blocks 4 * group + i - row0 of the unit
+        // (i = 0..3): sub-blocks 4h + i of one tile.  Each block's MFMA result
+        // is selected into the slots of the lane group that owns it, and
+        // only the lane's own four (scale, min) pairs are decoded, once per
+        // unit -- the same value as scaling every block with a scale masked
+        // to zero outside its lane group (those terms add exact zeros).
+        const int first = static_cast<int>(4u * group) - static_cast<int>(row0);
+        const bool lane_owns = first >= 0 && first < static_cast<int>(kChunkBlocks / U);
+        const std::uint32_t lane_tile = lane_owns ? static_cast<std::uint32_t>(first) >> 3 : 0u;
+        const bool upper = (first & 4) != 0;   // sub-blocks 4-7 of the tile
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
+        for (int r = 0; r < R; ++r) {
+            float4v sel{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int rel = t * 8 + j;
+                    const half8v w = tile_block_codes<FMT, R, U, NORM>(ch, t, r, j);
+                    float4v p = mfma16x16x32(hi, w, float4v{0.0f, 0.0f, 0.0f, 0.0f});
+                    p = mfma16x16x32(lo, w, p);
+                    const std::uint32_t owner = (row0 + static_cast<std::uint32_t>(rel)) >> 2;
+                    sel[rel & 3] = group == owner ? p[rel & 3] : sel[rel & 3];
+                }
+            }
+            // The lane's tile record: f16 (d, dmin), then the 12 packed
+            // 6-bit scale / min bytes (src/reference/tensor_reader.cpp:153-165).
+            uint4 rec = ch.sc[0][r];
+#pragma unroll
+            for (int t = 1; t < T; ++t) {
+                if (lane_tile == static_cast<std::uint32_t>(t)) rec = ch.sc[t][r];
+            }
+            // Sub-blocks 0-3: scale = byte j & 63, min = byte j + 4 & 63;
+            // 4-7: low / high nibble of byte j + 4 with bits 6-7 of byte j - 4
+            // / j above them -- four bytes at once.
+            const std::uint32_t scales = upper ? ((rec.w & 0x0f0f0f0fu) | ((rec.y >> 2) & 0x30303030u))
+                                               : (rec.y & 0x3f3f3f3fu);
+            const std::uint32_t mins = upper ? (((rec.w >> 4) & 0x0f0f0f0fu) | ((rec.z >> 2) & 0x30303030u))
+                                             : (rec.z & 0x3f3f3f3fu);
+            const float d = lane_owns ? half_bits_to_float(rec.x & 0xffffu) : 0.0f;
+            const float dmin = lane_owns ? half_bits_to_float(rec.x >> 16) : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float dj = d * static_cast<float>((scales >> (8 * i)) & 0xffu);
+                const float mj = dmin * static_cast<float>((mins >> (8 * i)) & 0xffu);
+                cacc[r][i] = fmaf(-mj, xs[i], fmaf(dj, sel[i], cacc[r][i]));
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < (FMT == kQ4_K ? 0 : T); ++t) {
         const std::uint32_t first_row = row0 + static_cast<std::uint32_t>(t * F::kBlocksPerTile);
         const bool own = group == (first_row >> 2);
         typename F::Scale sc[R];
-        std::uint32_t q4k_packed[R][3];
-        std::uint32_t q4k_dm[R][2];   // Q4_K: f16 pair (d, dmin), for blocks 0-3 and 4-7
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             if constexpr (FMT == kQ8_0) {
                 sc[r] = own ? ch.sc[t][r] : 0u;
             } else if constexpr (FMT == kQ4_0) {
                 sc[r] = own ? ch.sc[t][r] : make_uint2(0u, 0u);
-            } else {
-                const bool own_hi = group == ((first_row >> 2) + 1u);
-                q4k_dm[r][0] = own ? ch.sc[t][r].x : 0u;
-                q4k_dm[r][1] = own_hi ? ch.sc[t][r].x : 0u;
-                q4k_packed[r][0] = ch.sc[t][r].y;
-                q4k_packed[r][1] = ch.sc[t][r].z;
-                q4k_packed[r][2] = ch.sc[t][r].w;
             }
         }
 #pragma unroll
@@ -262,17 +303,10 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U, NORM>& ch, 
                 if constexpr (FMT == kQ8_0) {
                     const float d = half_bits_to_float((sc[r] >> (16 * j)) & 0xffffu);
                     cacc[r][i] = fmaf(d, p[i], cacc[r][i]);
-                } else if constexpr (FMT == kQ4_0) {
+                } else {
                     const std::uint32_t sw = j < 2 ? sc[r].x : sc[r].y;
                     const float d = half_bits_to_float((sw >> (16 * (j & 1))) & 0xffffu);
                     cacc[r][i] = fmaf(d, p[i], cacc[r][i]);
-                } else {
-                    std::uint32_t s6 = 0, m6 = 0;
-                    q4k_scale_min(q4k_packed[r], static_cast<std::uint32_t>(j), s6, m6);
-                    const std::uint32_t dm = q4k_dm[r][j >> 2];
-                    const float dj = half_bits_to_float(dm & 0xffffu) * static_cast<float>(s6);
-                    const float mj = half_bits_to_float(dm >> 16) * static_cast<float>(m6);
-                    cacc[r][i] = fmaf(-mj, xs[i], fmaf(dj, p[i], cacc[r][i]));
                 }
             }
         }

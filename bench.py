@@ -133,12 +133,14 @@ def trace_summary(csv_path: str) -> str:
     return "\n".join(lines)
 
 
-def traffic_probe(ms) -> int:
-    """Launch sequence for the HBM-traffic counter passes: one plain copy of a
-    known size (the calibration kernel), then the fused gate|up linear of four
-    distinct layers at each M.  Run under `rocprofv3 --pmc FETCH_SIZE` and
-    then `--pmc WRITE_SIZE`; `--counter-summary` turns the two CSVs into
-    bytes per launch."""
+def traffic_probe(ms, type_id: int = 8) -> int:
+    """Launch sequence for the counter passes: one plain copy of a known size
+    (the calibration kernel), then the fused gate|up linear of four distinct
+    layers at each M, in GGML format `type_id` (8 = Q8_0).  Run under
+    `rocprofv3 --pmc FETCH_SIZE` and then `--pmc WRITE_SIZE`;
+    `--counter-summary` turns the two CSVs into bytes per launch.  The same
+    sequence serves the instruction counter passes (SQ_*) of the 4-bit
+    formats."""
     import torch
 
     from air_amd import capi, quant
@@ -150,8 +152,8 @@ def traffic_probe(ms) -> int:
     dst = torch.empty_like(src)
     mats = []
     for seed in range(4):
-        canon = quant.synthetic_weights_device(capi.TYPE_Q8_0, HIDDEN, 2 * FFN, 500 + seed, dev)
-        mats.append(capi.Matrix(ctx, capi.TYPE_Q8_0, HIDDEN, 2 * FFN, canon, canon.numel(), on_device=True))
+        canon = quant.synthetic_weights_device(type_id, HIDDEN, 2 * FFN, 500 + seed, dev)
+        mats.append(capi.Matrix(ctx, type_id, HIDDEN, 2 * FFN, canon, canon.numel(), on_device=True))
         del canon
     ctx.reserve(HIDDEN, max(ms))
     x = torch.randn((max(ms), HIDDEN), device=dev)
@@ -424,6 +426,8 @@ def main() -> int:
                     help="summarise a rocprofv3 kernel-trace CSV instead of benchmarking")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run the launch sequence for the FETCH_SIZE / WRITE_SIZE counter passes")
+    ap.add_argument("--probe-format", type=int, default=8,
+                    help="GGML format of --traffic-probe's gate|up matrices (8 Q8_0, 2 Q4_0, 12 Q4_K)")
     ap.add_argument("--counter-summary", nargs=2, default=None, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="bytes per launch from the two counter passes of --traffic-probe")
     args = ap.parse_args()
@@ -432,7 +436,7 @@ def main() -> int:
         print(trace_summary(args.trace_summary))
         return 0
     if args.traffic_probe:
-        return traffic_probe([int(v) for v in args.m.split(",") if v])
+        return traffic_probe([int(v) for v in args.m.split(",") if v], args.probe_format)
     if args.counter_summary:
         fetch_csv, write_csv = args.counter_summary
         print(json.dumps(counter_summary(fetch_csv, write_csv, [int(v) for v in args.m.split(",") if v]), indent=1))
