@@ -95,6 +95,17 @@ __device__ __forceinline__ void q4k_scale_min(const std::uint32_t s[3], std::uin
     }
 }
 
+// The 6-bit scales and mins of Q4_K sub-blocks 4u .. 4u + 3 (u = upper),
+// one per byte, from the same packed dwords: sub-blocks 0-3 have scale =
+// byte j & 63 and min = byte j + 4 & 63; 4-7 the low / high nibble of byte
+// j + 4 with bits 6-7 of byte j - 4 (scale) / byte j (min) above it --
+// q4k_scale_min for four sub-blocks at once.
+__device__ __forceinline__ void q4k_scale_min_x4(const std::uint32_t s[3], bool upper, std::uint32_t& scales,
+                                                 std::uint32_t& mins) {
+    scales = upper ? ((s[2] & 0x0f0f0f0fu) | ((s[0] >> 2) & 0x30303030u)) : (s[0] & 0x3f3f3f3fu);
+    mins = upper ? (((s[2] >> 4) & 0x0f0f0f0fu) | ((s[1] >> 2) & 0x30303030u)) : (s[1] & 0x3f3f3f3fu);
+}
+
 __device__ __forceinline__ float4v mfma16x16x32(const half8v& a, const half8v& b, const float4v& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

@@ -99,11 +99,15 @@ template <int FMT>
 __device__ __forceinline__ void step_scale(const StepCodes<FMT>& in, std::uint32_t s, int b, float& scale,
                                            float& offset) {
     if constexpr (FMT == kQ4_K) {
+        // Sub-block j = 2(s mod 4) + b: the four-byte word of its half of the
+        // super-block (the same for both blocks of the step), then its byte.
         const std::uint32_t packed[3] = {in.h.y, in.h.z, in.h.w};
-        std::uint32_t sc = 0, mn = 0;
-        q4k_scale_min(packed, 2u * (s & 3u) + static_cast<std::uint32_t>(b), sc, mn);
-        scale = f16_bits_value(in.h.x & 0xffffu) * static_cast<float>(sc);
-        offset = f16_bits_value(in.h.x >> 16) * static_cast<float>(mn);
+        const std::uint32_t j = 2u * (s & 3u) + static_cast<std::uint32_t>(b);
+        std::uint32_t scales = 0, mins = 0;
+        q4k_scale_min_x4(packed, j >= 4u, scales, mins);
+        const std::uint32_t shift = 8u * (j & 3u);
+        scale = f16_bits_value(in.h.x & 0xffffu) * static_cast<float>((scales >> shift) & 0xffu);
+        offset = f16_bits_value(in.h.x >> 16) * static_cast<float>((mins >> shift) & 0xffu);
     } else {
         scale = f16_bits_value((in.d >> (16 * b)) & 0xffffu);
         offset = 0.0f;

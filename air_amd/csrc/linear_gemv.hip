@@ -261,13 +261,9 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U, NORM>& ch, 
             for (int t = 1; t < T; ++t) {
                 if (lane_tile == static_cast<std::uint32_t>(t)) rec = ch.sc[t][r];
             }
-            // Sub-blocks 0-3: scale = byte j & 63, min = byte j + 4 & 63;
-            // 4-7: low / high nibble of byte j + 4 with bits 6-7 of byte j - 4
-            // / j above them -- four bytes at once.
-            const std::uint32_t scales = upper ? ((rec.w & 0x0f0f0f0fu) | ((rec.y >> 2) & 0x30303030u))
-                                               : (rec.y & 0x3f3f3f3fu);
-            const std::uint32_t mins = upper ? (((rec.w >> 4) & 0x0f0f0f0fu) | ((rec.z >> 2) & 0x30303030u))
-                                             : (rec.z & 0x3f3f3f3fu);
+            const std::uint32_t packed[3] = {rec.y, rec.z, rec.w};
+            std::uint32_t scales = 0, mins = 0;
+            q4k_scale_min_x4(packed, upper, scales, mins);
             const float d = lane_owns ? half_bits_to_float(rec.x & 0xffffu) : 0.0f;
             const float dmin = lane_owns ? half_bits_to_float(rec.x >> 16) : 0.0f;
 #pragma unroll

@@ -267,6 +267,124 @@ def measure_prefill(torch, ctx, capi, layers, m, steps, dev, stream):
 FORMAT_BLOCKS = {8: (32, 34), 2: (32, 18), 12: (256, 144)}   # GGML id: (block elements, block bytes)
 
 
+QWEN2_05B = (896, 128, 4864, 151936, 24)   # hidden, kv width, ffn, vocab, layers
+C0_K, C0_N = 896, 4864                      # configs[0]: the 0.5B FFN up-projection
+C0_ROTATE_BYTES = 1 << 30                   # configs[0] copies: > 4x the 256 MB Infinity Cache
+
+
+def layer_set_bytes(hidden: int, kv: int, ffn: int, vocab: int, layers: int, m: int) -> int:
+    """Algorithmic bytes of one pass of a Qwen2 layer set at M rows: every
+    separate linear's W_bytes + 4*M*K + 4*M*N (+ 4*N bias), plus lm_head."""
+    per_layer = [(hidden, hidden, True), (hidden, kv, True), (hidden, kv, True), (hidden, hidden, False),
+                 (hidden, ffn, False), (hidden, ffn, False), (ffn, hidden, False)]
+    total = sum(w_bytes(k, n) + 4 * m * k + 4 * m * n + (4 * n if bias else 0) for k, n, bias in per_layer)
+    return total * layers + w_bytes(hidden, vocab) + 4 * m * hidden + 4 * m * vocab
+
+
+def graph_time_ms(torch, ctx, dev, stream, fn, steps: int, warmup: int) -> float:
+    """fn() captured once as a HIP graph, replayed `steps` times after
+    `warmup` replays; mean milliseconds per replay from HIP events on the
+    stream the graph runs on."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    capture = torch.cuda.Stream(dev)
+    ctx.set_stream(capture.cuda_stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=capture):
+        fn()
+    ctx.set_stream(stream.cuda_stream)
+    for _ in range(warmup):
+        graph.replay()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    del graph
+    return e0.elapsed_time(e1) / steps
+
+
+def measure_small_configs(torch, capi, quant, dev, stream, steps: int, warmup: int) -> dict:
+    """one Q8_0 GEMV 4864x896 at M = 1.  Its 4.65 MB weight fits
+    in the 256 MB Infinity Cache, so successive launches rotate over distinct
+    resident copies totalling more than 1 GiB (every launch reads HBM); one
+    replay runs each copy once.  configs[1]: the 24 Qwen2-0.5B layers' linears
+    (q|k|v and gate|up fused) plus lm_head 151936x896 at M = 1, one graph per
+    token.  Both on the reference's algorithmic bytes, against the HBM floor
+    (bytes / 8 TB/s)."""
+    out = {}
+    ctx = capi.Context(0, stream.cuda_stream)
+    # configs[0]
+    per = w_bytes(C0_K, C0_N) + 4 * C0_K + 4 * C0_N
+    copies = -(-C0_ROTATE_BYTES // w_bytes(C0_K, C0_N))
+    canon = quant.synthetic_weights_device(capi.TYPE_Q8_0, C0_K, C0_N, 700, dev)
+    mats = [capi.Matrix(ctx, capi.TYPE_Q8_0, C0_K, C0_N, canon, canon.numel(), on_device=True) for _ in range(copies)]
+    del canon
+    x = torch.randn((1, C0_K), device=dev)
+    y = torch.empty((1, C0_N), device=dev)
+    ms_pass = graph_time_ms(torch, ctx, dev, stream, lambda: [mt.linear(x, y, 1) for mt in mats],
+                            max(3, steps // 3), warmup)
+    us = ms_pass * 1e3 / copies
+    floor_us = per / (HBM_PEAK_GBS * 1e3)
+    out["configs0"] = {"workload": "configs[0]: Q8_0 GEMV 4864x896, M=1", "copies": copies,
+                       "rotated_bytes": copies * w_bytes(C0_K, C0_N), "us_per_gemv": round(us, 3),
+                       "gbps": round(per / (us * 1e3), 1), "hbm_frac": round(floor_us / us, 4),
+                       "floor_us": round(floor_us, 3), "bytes_per_gemv": per, "plan": mats[0].plan(1)}
+    for mt in mats:
+        mt.release()
+    del mats
+    # configs[1]
+    hidden, kv, ffn, vocab, nl = QWEN2_05B
+    layers, seed = [], 800
+    for _ in range(nl):
+        layer = {}
+        for name, k, n in (("qkv", hidden, hidden + 2 * kv), ("o", hidden, hidden),
+                           ("gate_up", hidden, 2 * ffn), ("down", ffn, hidden)):
+            canon = quant.synthetic_weights_device(capi.TYPE_Q8_0, k, n, seed, dev)
+            seed += 1
+            layer[name] = capi.Matrix(ctx, capi.TYPE_Q8_0, k, n, canon, canon.numel(), on_device=True)
+            del canon
+        layers.append(layer)
+    canon = quant.synthetic_weights_device(capi.TYPE_Q8_0, hidden, vocab, seed, dev)
+    head = capi.Matrix(ctx, capi.TYPE_Q8_0, hidden, vocab, canon, canon.numel(), on_device=True)
+    del canon
+    ctx.reserve(ffn, 1)
+    x_h = torch.randn((1, hidden), device=dev)
+    x_f = torch.randn((1, ffn), device=dev)
+    bias = torch.randn((hidden + 2 * kv,), device=dev) * 0.02
+    y_qkv = torch.empty((1, hidden + 2 * kv), device=dev)
+    y_h = torch.empty((1, hidden), device=dev)
+    y_gu = torch.empty((1, 2 * ffn), device=dev)
+    logits = torch.empty((1, vocab), device=dev)
+
+    def token():
+        for layer in layers:
+            layer["qkv"].linear(x_h, y_qkv, 1, bias=bias)
+            layer["o"].linear(x_h, y_h, 1)
+            layer["gate_up"].linear(x_h, y_gu, 1)
+            layer["down"].linear(x_f, y_h, 1)
+        head.linear(x_h, logits, 1)
+
+    ms_tok = graph_time_ms(torch, ctx, dev, stream, token, steps, warmup)
+    algo = layer_set_bytes(hidden, kv, ffn, vocab, nl, 1)
+    floor_us = algo / (HBM_PEAK_GBS * 1e3)
+    out["configs1"] = {"workload": "configs[1]: Qwen2-0.5B Q8_0 linears, 24 layers + lm_head 151936x896, M=1",
+                       "us_per_token": round(ms_tok * 1e3, 2), "tok_s": round(1e3 / ms_tok, 1),
+                       "gbps": round(algo / (ms_tok * 1e-3) / 1e9, 1), "hbm_frac": round(floor_us / (ms_tok * 1e3), 4),
+                       "floor_us": round(floor_us, 2), "bytes_per_token": algo, "launches_per_token": 4 * nl + 1}
+    for layer in layers:
+        for mt in layer.values():
+            mt.release()
+    head.release()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    ctx.close()
+    return out
+
+
 def format_step_bytes(type_id: int, m: int, layers: int) -> int:
     """step_algorithmic_bytes for any of the three formats."""
     be, bb = FORMAT_BLOCKS[type_id]
@@ -414,6 +532,8 @@ def main() -> int:
     ap.add_argument("--graph", type=int, default=1, help="replay each step as a captured HIP graph (1) or launch eagerly (0)")
     ap.add_argument("--prefill-m", type=int, default=512,
                     help="also time the prefill tactic (f16 MFMA GEMM) over the 28 layers' linears at this M (0 = skip)")
+    ap.add_argument("--small", type=int, default=1,
+                    help="also time configs[0] (one GEMV rotated over > 1 GiB of copies) and configs[1] (the 0.5B set)")
     ap.add_argument("--formats", default="2,12",
                     help="configs[3]: also time the linear set in these GGML formats (2 Q4_0, 12 Q4_K; '' = skip)")
     ap.add_argument("--formats-m", default="1,16,64", help="decode rows of the configs[3] leg")
@@ -620,6 +740,13 @@ def main() -> int:
                                   [int(v) for v in args.formats_m.split(",")], args.layers, max(5, args.steps // 3),
                                   args.warmup)
 
+    small = None
+    if args.small:
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        small = measure_small_configs(torch, capi, quant, dev, stream, args.steps, args.warmup)
+        print(f"# configs[0], configs[1]: {small}", file=sys.stderr, flush=True)
+
     e2e = None
     if args.e2e:
         torch.cuda.synchronize()
@@ -656,6 +783,8 @@ def main() -> int:
         "cpu_baseline": cpu,
         "prefill": prefill,
         "formats": formats,
+        "configs0": small["configs0"] if small else None,
+        "configs1": small["configs1"] if small else None,
         "e2e": e2e,
     }
     print(json.dumps(line), flush=True)
