@@ -56,6 +56,10 @@ struct HipPrepareOptions {
     // max_decode_rows sequences of min(context, 4096) tokens, capped at 40%
     // of free device memory.
     std::uint32_t kv_pool_pages{0};
+    // Page size of the plans this model will serve: the pool is sized in
+    // these pages, and sequence_capacity_bytes answers with them before the
+    // first sequence exists (a plan with another size is refused then).
+    std::uint32_t kv_page_tokens{16};
     std::uint32_t max_step_rows{512};   // rows per device step (prefill chunk)
     // Decode steps (one row per sequence, greedy outputs) replay one captured
     // HIP graph per batch width instead of launching ~13 kernels per layer.

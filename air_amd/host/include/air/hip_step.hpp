@@ -86,6 +86,12 @@ public:
                                                                        std::uint32_t max_rows);
     ~HipStepEngine();
 
+    // Bytes of one KV page (every layer's K and V for page_tokens tokens).
+    [[nodiscard]] static std::uint64_t kv_page_bytes(const ModelConfig& c, std::uint32_t page_tokens) noexcept;
+    // Pages of the pool the first sequence allocates (the prepare option, or
+    // the default sizing against the device memory free now).
+    [[nodiscard]] static std::uint32_t planned_pool_pages(const HipPreparedModel& prepared, std::uint32_t page_tokens);
+
     // Rows of several sequences; the positions are each sequence's next
     // tokens in row order.  The batch commits to every sequence on success.
     [[nodiscard]] Result<StepResult> run(std::span<const StepRow> rows, QuantizedLinearExecutionKind block_tactic,

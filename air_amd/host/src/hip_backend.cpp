@@ -566,11 +566,16 @@ std::optional<std::uint64_t> HipPreparedModel::free_device_bytes() const {
     return free;
 }
 
-// Before the first sequence, the free device memory its pool can take; after,
-// the fixed KV pool every sequence lives in.
+// The fixed KV pool every sequence lives in: once the first sequence exists,
+// the pool allocated; before, the pool that sequence will allocate (in the
+// prepare options' page size).  The reference answers free + allocated bytes
+// because its CUDA pool grows (backend.cpp:541-560); this pool is one
+// allocation sized once, so admission is held to what it can actually give.
 std::optional<std::uint64_t> HipPreparedModel::sequence_capacity_bytes() const {
     if (engine_) return engine_->pool_bytes();
-    return free_device_bytes();
+    const std::uint32_t page_tokens = options_.kv_page_tokens;
+    return static_cast<std::uint64_t>(HipStepEngine::planned_pool_pages(*this, page_tokens)) *
+           HipStepEngine::kv_page_bytes(model_->config(), page_tokens);
 }
 
 Result<std::unique_ptr<runtime_detail::PreparedModel>> prepare_hip_model(std::shared_ptr<const ModelDefinition> model,

@@ -163,6 +163,26 @@ HipStepEngine::~HipStepEngine() {
     if (owns_embedding_ && embedding_) air_hip_matrix_release(embedding_);
 }
 
+std::uint64_t HipStepEngine::kv_page_bytes(const ModelConfig& c, std::uint32_t page_tokens) noexcept {
+    if (c.attention_head_count == 0U) return 0U;
+    const std::uint64_t kv_width = static_cast<std::uint64_t>(c.kv_head_count) * (c.embedding_size / c.attention_head_count);
+    return static_cast<std::uint64_t>(c.layer_count) * 2U * page_tokens * kv_width * sizeof(float);
+}
+
+// The fixed pool: room for max_decode_rows sequences of min(context, 4096)
+// tokens, at most 40 % of the device memory free when it is allocated.
+std::uint32_t HipStepEngine::planned_pool_pages(const HipPreparedModel& prepared, std::uint32_t page_tokens) {
+    const auto& c = prepared.model().config();
+    const std::uint64_t page_bytes = kv_page_bytes(c, page_tokens);
+    if (page_tokens == 0U || page_bytes == 0U) return 0U;
+    if (prepared.options().kv_pool_pages) return prepared.options().kv_pool_pages;
+    const std::uint64_t tokens = std::min<std::uint64_t>(c.context_length, 4096U);
+    std::uint64_t pages = static_cast<std::uint64_t>(prepared.options().max_decode_rows) *
+                          ((tokens + page_tokens - 1U) / page_tokens);
+    if (const auto free = prepared.free_device_bytes()) pages = std::min<std::uint64_t>(pages, *free / 10U * 4U / page_bytes);
+    return static_cast<std::uint32_t>(std::min<std::uint64_t>(pages, INT32_MAX));
+}
+
 Result<std::unique_ptr<HipStepEngine>> HipStepEngine::create(const HipPreparedModel& prepared,
                                                              std::uint32_t page_tokens, std::uint32_t pool_pages,
                                                              std::uint32_t max_rows) {
@@ -201,15 +221,9 @@ Result<std::unique_ptr<HipStepEngine>> HipStepEngine::create(const HipPreparedMo
     e->qkv_width_ = e->q_width_ + 2U * e->kv_width_;
     e->ffn_ = c.feed_forward_size;
     e->vocab_ = c.vocabulary_size;
-    e->page_bytes_ = static_cast<std::uint64_t>(c.layer_count) * 2U * page_tokens * e->kv_width_ * sizeof(float);
+    e->page_bytes_ = kv_page_bytes(c, page_tokens);
     if (pool_pages == 0U) {
-        const std::uint64_t tokens = std::min<std::uint64_t>(c.context_length, 4096U);
-        std::uint64_t pages = static_cast<std::uint64_t>(prepared.options().max_decode_rows) *
-                              ((tokens + page_tokens - 1U) / page_tokens);
-        if (const auto free = prepared.free_device_bytes()) {
-            pages = std::min<std::uint64_t>(pages, *free / 10U * 4U / e->page_bytes_);
-        }
-        pool_pages = static_cast<std::uint32_t>(std::min<std::uint64_t>(pages, INT32_MAX));
+        pool_pages = planned_pool_pages(prepared, page_tokens);
         e->pool_pages_ = pool_pages;
     }
     if (pool_pages == 0U) return Status::invalid_state("no device memory for one KV page");

@@ -159,6 +159,7 @@ int air_host_engine_create(const air_host_model* model, const air_host_engine_co
         air::HipPrepareOptions options;
         options.device = config->device;
         if (config->kv_pool_pages) options.kv_pool_pages = config->kv_pool_pages;
+        options.kv_page_tokens = config->page_tokens ? config->page_tokens : 16U;
         if (config->max_step_rows) options.max_step_rows = config->max_step_rows;
         options.decode_graphs = config->eager_decode == 0;
         auto prepared = air::HipPreparedModel::create(model->model, options);
@@ -190,6 +191,26 @@ int air_host_engine_create(const air_host_model* model, const air_host_engine_co
 int air_host_engine_release(air_host_engine* engine) {
     delete engine;
     return AIR_HIP_OK;
+}
+
+int air_host_engine_capacity(const air_host_engine* engine, air_host_capacity* out) {
+    if (!engine || !out) return fail_argument("engine and out must not be null");
+    return guarded([&] {
+        const auto& prepared = *engine->prepared;
+        const auto capacity = prepared.sequence_capacity_bytes();
+        const auto free = prepared.free_device_bytes();
+        if (!capacity || !free) return fail(air::Status::invalid_state("device memory information is unavailable"));
+        *out = air_host_capacity{*capacity, *free, prepared.kv_pool_allocated_bytes(), prepared.kv_pool_free_bytes()};
+        return static_cast<int>(AIR_HIP_OK);
+    });
+}
+
+int air_host_engine_sequence_bytes(const air_host_engine* engine, uint64_t tokens, uint64_t* out) {
+    if (!engine || !out) return fail_argument("engine and out must not be null");
+    return guarded([&] {
+        *out = engine->prepared->estimate_sequence_device_bytes(engine->service->config().plan, tokens);
+        return static_cast<int>(AIR_HIP_OK);
+    });
 }
 
 int air_host_generate_cohort(air_host_engine* engine, const int32_t* prompt_tokens, const uint32_t* prompt_lengths,

@@ -60,6 +60,11 @@ class EngineConfig(ctypes.Structure):
     ]
 
 
+class Capacity(ctypes.Structure):
+    _fields_ = [("sequence_capacity_bytes", _U64), ("free_device_bytes", _U64), ("kv_pool_allocated_bytes", _U64),
+                ("kv_pool_free_bytes", _U64)]
+
+
 class CohortStats(ctypes.Structure):
     _fields_ = [
         ("wall_ms", ctypes.c_double), ("prefill_ms", ctypes.c_double), ("decode_ms", ctypes.c_double),
@@ -85,6 +90,8 @@ SIGNATURES = {
     "air_host_model_tensor": (_I, [_P, _U32, ctypes.POINTER(TensorInfo)]),
     "air_host_engine_create": (_I, [_P, ctypes.POINTER(EngineConfig), _PP]),
     "air_host_engine_release": (_I, [_P]),
+    "air_host_engine_capacity": (_I, [_P, ctypes.POINTER(Capacity)]),
+    "air_host_engine_sequence_bytes": (_I, [_P, _U64, ctypes.POINTER(_U64)]),
     "air_host_generate_cohort": (_I, [_P, ctypes.POINTER(_I32), ctypes.POINTER(_U32), _U32, _U32, _I32,
                                       ctypes.POINTER(_I32), ctypes.POINTER(_U32), ctypes.POINTER(CohortStats)]),
 }
@@ -205,6 +212,18 @@ class Engine:
         for i in range(n):
             result.append([out[i * max_new_tokens + t] for t in range(counts[i])])
         return result, stats
+
+    def capacity(self) -> dict:
+        """sequence_capacity_bytes, free_device_bytes, kv_pool_allocated_bytes, kv_pool_free_bytes."""
+        c = Capacity()
+        check(lib().air_host_engine_capacity(self.handle, ctypes.byref(c)))
+        return {name: getattr(c, name) for name, _ in Capacity._fields_}
+
+    def sequence_bytes(self, tokens: int) -> int:
+        """Device bytes admission reserves for a request of `tokens` prompt + generated tokens."""
+        out = _U64()
+        check(lib().air_host_engine_sequence_bytes(self.handle, tokens, ctypes.byref(out)))
+        return out.value
 
     def close(self) -> None:
         if self.handle:

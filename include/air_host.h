@@ -112,6 +112,23 @@ typedef struct air_host_engine_config {
 int air_host_engine_create(const air_host_model* model, const air_host_engine_config* config, air_host_engine** out);
 int air_host_engine_release(air_host_engine* engine);
 
+typedef struct air_host_capacity {
+    uint64_t sequence_capacity_bytes;  /* what admission reserves against: the fixed KV pool (before the first
+                                          sequence, the pool it will allocate) */
+    uint64_t free_device_bytes;        /* hipMemGetInfo free */
+    uint64_t kv_pool_allocated_bytes;  /* 0 until the first sequence */
+    uint64_t kv_pool_free_bytes;       /* pool pages no sequence holds */
+} air_host_capacity;
+
+/* The engine's capacity answers (PreparedModel::sequence_capacity_bytes,
+ * free_device_bytes, kv_pool_allocated_bytes, kv_pool_free_bytes,
+ * src/runtime/backend.hpp:118-121). */
+int air_host_engine_capacity(const air_host_engine* engine, air_host_capacity* out);
+/* The device bytes admission reserves for a request of `tokens` prompt plus
+ * generated tokens (PreparedModel::estimate_sequence_device_bytes with the
+ * engine's plan). */
+int air_host_engine_sequence_bytes(const air_host_engine* engine, uint64_t tokens, uint64_t* out);
+
 typedef struct air_host_cohort_stats {
     double wall_ms;                /* whole cohort, submission to last token */
     double prefill_ms;             /* inside prefill_batch calls */

@@ -803,7 +803,15 @@ void gpu_prepared_model_contract() {
     }
     const auto free = p.free_device_bytes();
     const auto capacity = p.sequence_capacity_bytes();
-    check(free && *free > (1ULL << 30) && capacity && *capacity >= *free, "capacity from hipMemGetInfo");
+    // The fixed KV pool the first sequence will allocate (16-token pages):
+    // max_decode_rows sequences of min(context, 4096) tokens, at most 40 %
+    // of the memory free now.
+    const auto* hip = dynamic_cast<const air::HipPreparedModel*>(&p);
+    const std::uint64_t page_bytes = air::HipStepEngine::kv_page_bytes(model.value()->config(), 16U);
+    check(hip && free && *free > (1ULL << 30) && capacity && page_bytes > 0U && *capacity % page_bytes == 0U &&
+              *capacity == static_cast<std::uint64_t>(air::HipStepEngine::planned_pool_pages(*hip, 16U)) * page_bytes &&
+              *capacity <= *free / 10U * 4U,
+          "capacity is the KV pool the first sequence allocates");
     check(p.resident_device_bytes() > 0U, "resident bytes are counted");
     auto plan = paged_plan();
     plan.linear = {air::QuantizedLinearExecutionKind::hip_decode, air::QuantizedLinearExecutionKind::hip_decode,

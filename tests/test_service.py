@@ -30,7 +30,7 @@ def _declared():
 def test_host_library_exports_every_declared_entry_point():
     lib = host_api.lib()
     declared = _declared()
-    assert len(declared) == 12
+    assert len(declared) == 14
     for name in declared:
         assert hasattr(lib, name), name
     assert set(host_api.SIGNATURES) == set(declared)
@@ -149,5 +149,51 @@ def test_cohort_validation_fails_before_work(torch_cuda):
     assert [len(t) for t in tokens] == [8, 8]
     tokens2, _ = engine.generate_cohort([[1] * 20, [2] * 20, [3] * 20], 8)
     assert tokens2[:2] == tokens                                # the third waits for pages, same results
+    engine.close()
+    model.close()
+
+
+@pytest.mark.gpu
+def test_admission_holds_to_the_fixed_pool_at_7b_width(torch_cuda):
+    """The KV pool is one allocation sized once (max_decode_rows sequences of
+    min(context, 4096) tokens, at most 40 % of free HBM), so
+    sequence_capacity_bytes answers that pool -- before the first sequence
+    the pool it will allocate -- and admission reserves every request's
+    forecast (PreparedModel::estimate_sequence_device_bytes) against it: a
+    cohort larger than the pool runs at most capacity // forecast requests
+    at once and finishes, with the pool whole afterwards.  Qwen2-7B widths
+    (hidden 3584, 28 / 4 heads of 128, FFN 18944), two layers."""
+    model = host_api.Model.synthetic_qwen2(layers=2, embedding=3584, ffn=18944, heads=28, kv_heads=4, vocab=1024,
+                                           context=4096)
+    page_bytes = 2 * 2 * 16 * 512 * 4                  # layers x (K, V) x page tokens x kv width x f32
+    engine = host_api.Engine(model, page_tokens=16)
+    before = engine.capacity()
+    assert before["kv_pool_allocated_bytes"] == 0
+    planned = 64 * (4096 // 16) * page_bytes            # 64 decode rows x 4096 tokens, far below 40 % of HBM
+    assert before["sequence_capacity_bytes"] == planned
+    tokens, _ = engine.generate_cohort([[5] * 40, [9] * 40], 8)
+    assert [len(t) for t in tokens] == [8, 8]
+    after = engine.capacity()
+    assert after["kv_pool_allocated_bytes"] == planned == after["sequence_capacity_bytes"]
+    assert after["kv_pool_free_bytes"] == planned
+    engine.close()
+
+    # A pool of 12 pages (192 tokens): 48-token requests (3 pages + the
+    # page table) fit three at a time.
+    engine = host_api.Engine(model, page_tokens=16, kv_pool_pages=12)
+    capacity = engine.capacity()["sequence_capacity_bytes"]
+    assert capacity == 12 * page_bytes
+    forecast = engine.sequence_bytes(48)
+    assert forecast == 3 * page_bytes + (4096 // 16) * 2 * 8
+    fits = capacity // forecast
+    assert fits == 3
+    prompts = [[(11 * i + j) % 1024 for j in range(40)] for i in range(8)]
+    print(f"7B-width admission: capacity {capacity} B, forecast {forecast} B, {fits} at a time", flush=True)
+    tokens, stats = engine.generate_cohort(prompts, 8)
+    assert [len(t) for t in tokens] == [8] * 8
+    assert all(0 <= t < 1024 for seq in tokens for t in seq)
+    assert stats.max_decode_width <= fits and stats.max_prefill_sequences <= fits
+    end = engine.capacity()
+    assert end["kv_pool_allocated_bytes"] == end["kv_pool_free_bytes"] == capacity
     engine.close()
     model.close()
