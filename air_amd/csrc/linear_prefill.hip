@@ -359,13 +359,30 @@ hipError_t launch_gemm_fmt(const GemmArgs& args, const PrefillShape& shape, std:
 PrefillShape plan_prefill(const TilePlanes& p, std::uint32_t m, const PrefillTuning& tuning) {
     PrefillShape s;
     // Register tile per wave: TM x TN MFMA tiles (16 x 16 each).  Measured on
-    // the Qwen2-7B shapes at M = 512: long K (down, K = 18944) runs best on
-    // the 8x4 tile with one step of prefetch and a K split; the rest on the
-    // 4x4 tile with two steps of prefetch.
+    // the Qwen2-7B shapes at M = 512 (TFLOP/s, Q8_0 / Q4_0 / Q4_K):
+    //  * long K (down, K = 18944): 8x4, one step of prefetch, 8 K splits
+    //    (623 / 649 / 571; 8x2 with 4 splits 612 / 632 / 562);
+    //  * wide grids (gate|up, 2368 row tiles): Q8_0 8x4 with one step of
+    //    prefetch (694; 8x2 663), the 4-bit formats 8x2 (805 / 708; 8x4
+    //    703 / 550) -- their codes are half the bytes, so the shorter
+    //    register tile keeps more waves resident for the same loads;
+    //  * narrow grids (q|k|v, o): 4x2 with a 2-way K split (381 / 376 / 316
+    //    on q|k|v; 4x4 335 / 328 / 263).
     const bool long_k = p.k >= 8192u;
-    s.tile_m = long_k ? 8u : 4u;
-    s.tile_n = 4u;
-    s.prefetch = long_k ? 1u : 2u;
+    const bool wide = p.nt >= 1024u;
+    if (long_k || (wide && p.type == kQ8_0)) {
+        s.tile_m = 8u;
+        s.tile_n = 4u;
+        s.prefetch = 1u;
+    } else if (wide) {
+        s.tile_m = 8u;
+        s.tile_n = 2u;
+        s.prefetch = 2u;
+    } else {
+        s.tile_m = 4u;
+        s.tile_n = 2u;
+        s.prefetch = 2u;
+    }
     if (tuning.tile_m == 4 || tuning.tile_m == 8) s.tile_m = tuning.tile_m;
     if (tuning.tile_n == 2 || tuning.tile_n == 4) s.tile_n = tuning.tile_n;
     if (tuning.prefetch == 1 || tuning.prefetch == 2) s.prefetch = tuning.prefetch;
@@ -376,11 +393,13 @@ PrefillShape plan_prefill(const TilePlanes& p, std::uint32_t m, const PrefillTun
     s.steps = static_cast<std::uint32_t>(p.kp / kStepK);
     std::uint32_t splits = tuning.k_splits;
     if (splits == 0u) {
-        // Fill the 256 CUs (two workgroups each) when the tile grid alone
-        // cannot, keeping at least 16 steps per split.
+        // Split K while the doubled grid stays within 2.5 workgroups per CU,
+        // keeping at least 16 steps per split: q|k|v (288 tiles) and o (224)
+        // split 2 ways, down (56) 8 ways (measured: q|k|v 4 ways 4 % and o
+        // 4 ways 1 % off their best; down 16 ways 16 % slower).
         const std::uint64_t tiles = static_cast<std::uint64_t>(s.m_tiles) * s.groups;
         splits = 1u;
-        while (tiles * splits * 2u <= 512u && s.steps / (splits * 2u) >= 16u) splits *= 2u;
+        while (tiles * splits * 2u <= 640u && s.steps / (splits * 2u) >= 16u) splits *= 2u;
     }
     splits = splits < 1u ? 1u : (splits > s.steps ? s.steps : splits);
     s.steps_per_split = static_cast<std::uint32_t>(ceil_div(s.steps, splits));

@@ -155,3 +155,51 @@ def test_prefill_rejects_bad_arguments(torch_cuda, hip_ctx):
         hip_ctx.set_prefill_tuning(3, 0, 0, 0)
     assert e.value.status_name == "invalid_argument"
     mat.release()
+
+
+# configs[4]'s prefill linears: the Qwen2-7B projections at M = 512 (a full
+# prefill step of 512 prompt tokens), in Q8_0 and the two 4-bit formats.
+REAL_SHAPES = [("q|k|v", 4608, 3584, True), ("o", 3584, 3584, False), ("gate|up", 37888, 3584, False),
+               ("down", 3584, 18944, False)]
+
+
+@pytest.fixture(scope="module")
+def _oracle_threads():
+    import os
+    before = oracle.threads()
+    oracle.set_threads(min(16, os.cpu_count() or 1))
+    yield
+    oracle.set_threads(before)
+
+
+@pytest.mark.parametrize("type_id", [capi.TYPE_Q8_0, capi.TYPE_Q4_0, capi.TYPE_Q4_K],
+                         ids=lambda t: capi.TYPE_NAMES[t])
+@pytest.mark.parametrize("label,n,k,with_bias", REAL_SHAPES, ids=[s[0] for s in REAL_SHAPES])
+def test_prefill_real_shapes_m512(torch_cuda, hip_ctx, _oracle_threads, type_id, label, n, k, with_bias):
+    """Every 512-row activation block against the oracle on a seeded sample
+    of 256 output rows plus the first and last 16-row tiles (rows checked
+    one by one), on the planner's own launch shape."""
+    torch = torch_cuda
+    dev = torch.device("cuda:0")
+    m = 512
+    seed = 61_000 + n + k + type_id
+    canon_dev = quant.synthetic_weights_device(type_id, k, n, seed, dev)
+    canon = canon_dev.cpu().numpy()
+    mat = capi.Matrix(hip_ctx, type_id, k, n, canon_dev, canon_dev.numel(), on_device=True)
+    del canon_dev
+    bias = np.random.default_rng(seed).standard_normal(n).astype(np.float32) * 0.02 if with_bias else None
+    x = helpers.activations(m, k, seed=seed + 1)
+    rows = np.unique(np.concatenate([np.random.default_rng(seed + 2).choice(n, size=256, replace=False),
+                                     np.arange(16), np.arange(n - 16, n)])).astype(np.uint64)
+    try:
+        plan = mat.plan(m, tactic=capi.LINEAR_PREFILL)
+        got = _run(torch, mat, x, n, m, bias)[:, rows.astype(np.int64)]
+        want = oracle.linear_row_list(type_id, canon, k, n, x, rows, bias=bias)
+        assert np.isfinite(got).all()
+        err = helpers.rel_l2(got, want)
+        print(f"prefill M=512 {capi.TYPE_NAMES[type_id]} {label} {n}x{k}: rel_l2={err:.3e} | {plan}", flush=True)
+        assert err <= PREFILL_EXPECT
+        for r in range(m):
+            assert helpers.rel_l2(got[r], want[r]) <= PREFILL_TOL, r
+    finally:
+        mat.release()
