@@ -103,11 +103,22 @@ struct PrefillTuning {
     std::uint32_t tile_n{0};   // 16-row weight tiles per wave: 2 or 4
     std::uint32_t k_splits{0}; // workgroups splitting K (0 = automatic)
     std::uint32_t prefetch{0}; // weight prefetch distance in steps: 1 or 2 (8x4 tile only)
+    // Operand staging: 0 automatic, 1 registers (prefill_gemm_kernel), 2..4
+    // an LDS ring of that many 64-k steps (prefill_lds_kernel; Q8_0, 8x4 and
+    // 4x2 tiles).
+    std::uint32_t lds_stages{0};
+    std::uint32_t cus{256};        // compute units of the device (round sizes)
 };
 struct PrefillShape {
     std::uint32_t tile_m{8};
     std::uint32_t tile_n{4};
     std::uint32_t prefetch{1};
+    std::uint32_t lds_stages{0};   // 0: registers; 2..4: LDS ring stages
+    // Rows past the first `groups` weight groups (a grid that would end in a
+    // mostly empty round of workgroups) run as a second launch on the 4x2
+    // tile: rem_groups groups of 128 rows from row tile 4 * tile_n * groups.
+    std::uint32_t rem_groups{0};
+    std::uint32_t rem_m_tiles{0};
     std::uint32_t m_tiles{0};
     std::uint32_t groups{0};
     std::uint32_t steps{0};

@@ -390,6 +390,7 @@ int air_hip_context_create(int device, void* stream, air_hip_context** out) {
     ctx->device = device;
     ctx->stream = static_cast<hipStream_t>(stream);
     ctx->noalloc_scratch = scratch_ptr;
+    ctx->prefill_tuning.cus = static_cast<std::uint32_t>(prop.multiProcessorCount);
     *out = ctx;
     return AIR_HIP_OK;
 }
@@ -438,6 +439,13 @@ int air_hip_context_set_decode_path(air_hip_context* ctx, uint32_t path, uint32_
     ctx->decode_path = path;
     ctx->skinny_tile_n = tile_n;
     ctx->skinny_splits = k_splits;
+    return AIR_HIP_OK;
+}
+
+int air_hip_context_set_prefill_pipeline(air_hip_context* ctx, uint32_t lds_stages) {
+    if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
+    if (lds_stages > 4u) return fail(AIR_HIP_INVALID_ARGUMENT, "lds_stages must be 0 .. 4");
+    ctx->prefill_tuning.lds_stages = lds_stages;
     return AIR_HIP_OK;
 }
 
@@ -808,8 +816,18 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
     switch (route_linear(ctx, m, rows, tactic)) {
     case Route::prefill: {
         const PrefillShape s = plan_prefill(m->planes, rows, ctx->prefill_tuning);
-        std::snprintf(buf, sizeof buf, "prefill_gemm_kernel<%s> tile_m=%u tile_n=%u prefetch=%u m_tiles=%u groups=%u "
-                      "splits=%u", fmt, s.tile_m, s.tile_n, s.prefetch, s.m_tiles, s.groups, s.splits);
+        if (s.lds_stages) {
+            std::snprintf(buf, sizeof buf, "prefill_lds_kernel<%s> tile_m=%u tile_n=%u stages=%u m_tiles=%u groups=%u "
+                          "splits=%u", fmt, s.tile_m, s.tile_n, s.lds_stages, s.m_tiles, s.groups, s.splits);
+        } else {
+            std::snprintf(buf, sizeof buf, "prefill_gemm_kernel<%s> tile_m=%u tile_n=%u prefetch=%u m_tiles=%u "
+                          "groups=%u splits=%u", fmt, s.tile_m, s.tile_n, s.prefetch, s.m_tiles, s.groups, s.splits);
+        }
+        if (s.rem_groups) {
+            const std::size_t used = std::strlen(buf);
+            std::snprintf(buf + used, sizeof buf - used, " + remainder tile_m=4 tile_n=2 m_tiles=%u groups=%u",
+                          s.rem_m_tiles, s.rem_groups);
+        }
         break;
     }
     case Route::gemv: {

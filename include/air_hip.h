@@ -156,6 +156,12 @@ int air_hip_context_set_tuning(air_hip_context* ctx, uint32_t rows_per_wave, uin
  * split (1..64); 0 keeps the automatic choice.  No counterpart in the
  * reference. */
 int air_hip_context_set_decode_path(air_hip_context* ctx, uint32_t path, uint32_t tile_n, uint32_t k_splits);
+/* Chooses how the prefill GEMM stages its operands (autotuning): 0 =
+ * automatic, 1 = through registers (prefill_gemm_kernel), 2..4 = an LDS ring
+ * of that many 64-k steps filled by direct global -> LDS loads
+ * (prefill_lds_kernel; Q8_0 with the 8x4 or 4x2 tile, others keep the
+ * register path).  No counterpart in the reference. */
+int air_hip_context_set_prefill_pipeline(air_hip_context* ctx, uint32_t lds_stages);
 /* Overrides the prefill GEMM's launch shape for this context: tile_m =
  * 16-row activation tiles per wavefront (4 or 8), tile_n = 16-row weight
  * tiles per wavefront (2 or 4), k_splits = workgroups splitting K (1..64; a

@@ -203,3 +203,77 @@ def test_prefill_real_shapes_m512(torch_cuda, hip_ctx, _oracle_threads, type_id,
             assert helpers.rel_l2(got[r], want[r]) <= PREFILL_TOL, r
     finally:
         mat.release()
+
+
+@pytest.mark.parametrize("stages", [2, 3, 4])
+@pytest.mark.parametrize("k,n,m,tile", [(3584, 4608, 512, (4, 2, 2)), (18944, 3584, 512, (8, 4, 8)),
+                                         (896, 4864, 65, (8, 4, 1)), (512, 3584, 257, (4, 2, 1)),
+                                         (96, 37, 100, (8, 4, 1)), (3584, 1000, 130, (4, 2, 3))])
+def test_prefill_lds_pipeline_matches_register_path(torch_cuda, stages, k, n, m, tile):
+    """The LDS-pipelined GEMM (operands streamed global -> LDS through a ring
+    of `stages` steps) runs the register kernel's arithmetic in the same
+    order, so on the same tile shape and K split its outputs are
+    bit-identical; both are held to the oracle (Q8_0; ragged N, M and K
+    splits that leave a short last split included)."""
+    torch = torch_cuda
+    stream = torch.cuda.current_stream(torch.device("cuda:0")).cuda_stream
+    ctx = capi.Context(0, stream)
+    canon = helpers.weights(capi.TYPE_Q8_0, k, n, seed=k + 7 * n)
+    mat = capi.Matrix(ctx, capi.TYPE_Q8_0, k, n, canon, canon.nbytes, on_device=False)
+    x = helpers.activations(m, k, seed=k + m + 1)
+    bias = np.random.default_rng(n + 1).standard_normal(n).astype(np.float32) * 0.02
+    try:
+        tm, tn, splits = tile
+        ctx.set_prefill_tuning(tm, tn, splits, 0)
+        ctx.set_prefill_pipeline(1)
+        ref = _run(torch, mat, x, n, m, bias)
+        ctx.set_prefill_pipeline(stages)
+        plan = mat.plan(m, tactic=capi.LINEAR_PREFILL)
+        assert plan.startswith("prefill_lds_kernel"), plan
+        got = _run(torch, mat, x, n, m, bias)
+        again = _run(torch, mat, x, n, m, bias)
+        print(f"lds pipeline {stages} stages {n}x{k} M={m}: {plan}", flush=True)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+        assert np.array_equal(again.view(np.uint32), got.view(np.uint32))
+        rows = np.unique(np.concatenate([np.arange(min(n, 16)), np.arange(max(0, n - 16), n),
+                                         np.random.default_rng(k).choice(n, size=min(n, 128), replace=False)]))
+        want = oracle.linear_row_list(capi.TYPE_Q8_0, canon, k, n, x, rows.astype(np.uint64), bias=bias)
+        assert helpers.rel_l2(got[:, rows], want) <= PREFILL_EXPECT
+    finally:
+        mat.release()
+        ctx.close()
+
+
+def test_prefill_remainder_launch_is_bit_identical(torch_cuda):
+    """A grid of 8x4 tiles that would end in a mostly empty round of
+    workgroups (here 532 on 512 slots) runs its whole rounds on the 8x4 tile
+    and the remaining rows as a second launch on the 4x2 tile.  Without a K
+    split every output is the same sequence of MFMAs whatever the register
+    tile, so the result equals one 4x2 launch bit for bit (N = 33800 also
+    leaves a ragged last row tile in the remainder); both are held to the
+    oracle."""
+    torch = torch_cuda
+    stream = torch.cuda.current_stream(torch.device("cuda:0")).cuda_stream
+    ctx = capi.Context(0, stream)
+    k, n, m = 512, 33800, 512
+    canon = helpers.weights(capi.TYPE_Q8_0, k, n, seed=33800)
+    mat = capi.Matrix(ctx, capi.TYPE_Q8_0, k, n, canon, canon.nbytes, on_device=False)
+    x = helpers.activations(m, k, seed=17)
+    bias = np.random.default_rng(5).standard_normal(n).astype(np.float32) * 0.02
+    try:
+        ctx.set_prefill_tuning(8, 4, 1, 1)
+        plan = mat.plan(m, tactic=capi.LINEAR_PREFILL)
+        print(f"remainder split {n}x{k} M={m}: {plan}", flush=True)
+        assert "remainder" in plan and "groups=128" in plan, plan
+        got = _run(torch, mat, x, n, m, bias)
+        ctx.set_prefill_tuning(4, 2, 1, 2)
+        ctx.set_prefill_pipeline(1)
+        ref = _run(torch, mat, x, n, m, bias)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+        rows = np.unique(np.concatenate([np.arange(16), np.arange(32768 - 16, 32768 + 16), np.arange(n - 24, n),
+                                         np.random.default_rng(1).choice(n, size=256, replace=False)]))
+        want = oracle.linear_row_list(capi.TYPE_Q8_0, canon, k, n, x, rows.astype(np.uint64), bias=bias)
+        assert helpers.rel_l2(got[:, rows], want) <= PREFILL_EXPECT
+    finally:
+        mat.release()
+        ctx.close()
