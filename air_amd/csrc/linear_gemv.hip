@@ -530,9 +530,9 @@ GemvShape plan_decode_gemv(const TilePlanes& p, const DecodeTuning& tuning) {
     //    on wide grids) -- 4-7 % faster on those shapes.  The 4-bit formats
     //    are bound by instruction issue, and a unit split doubles the
     //    activation-split work per weight byte (measured 4-5 % slower);
-    //  * otherwise (down; the 4-bit formats): the chunks split over up to 8
-    //    waves until the grid holds about 8192 waves, double-buffered when a
-    //    wave owns several.
+    //  * otherwise (down; the 4-bit formats): the chunks split over the
+    //    waves until the grid holds about 8192 waves, up to 16 single-
+    //    buffered ones (down) or double-buffered when a wave owns several.
     g.rows_per_wave = 1u;
     if (tuning.rows_per_wave == 1u || tuning.rows_per_wave == 2u || tuning.rows_per_wave == 4u) {
         g.rows_per_wave = tuning.rows_per_wave;
@@ -559,12 +559,22 @@ GemvShape plan_decode_gemv(const TilePlanes& p, const DecodeTuning& tuning) {
     const auto depth_for = [&](std::uint64_t waves) -> std::uint32_t {
         return (wide || ceil_div(units, waves) <= 1u) ? 1u : 2u;
     };
+    const std::uint64_t wanted = w;
     std::uint32_t depth = depth_for(w);
     for (int pass = 0; pass < 2; ++pass) {
         const std::uint64_t cap = static_cast<std::uint64_t>(gemv_max_waves(static_cast<int>(g.rows_per_wave),
                                                                             static_cast<int>(depth)));
         if (w > cap) w = cap;
         depth = depth_for(w);
+    }
+    // Long K on a narrow grid (down: 224 row tiles, 37 chunks each) wants
+    // more than eight waves per row tile: sixteen single-buffered waves (twice
+    // the waves resident on the same CUs) beat eight double-buffered ones by
+    // 6 % in Q8_0 and 4-8 % in the 4-bit formats on back-to-back launches,
+    // 0.5 % on the whole Q8_0 step (where down follows gate|up).
+    if (tuning.waves_per_group == 0u && !wide && g.units_per_chunk == 1u && g.rows_per_wave == 1u && wanted > 8u) {
+        w = wanted > 16u ? 16u : wanted;
+        depth = 1u;
     }
     g.waves_per_group = static_cast<std::uint32_t>(w);
     g.depth = depth;
