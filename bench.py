@@ -652,6 +652,13 @@ def main() -> int:
             for _ in range(args.warmup):
                 graph.replay()
             torch.cuda.synchronize()
+            # Clocks settle under sustained load: keep replaying for at least
+            # 0.2 s before the timed steps (a cold GPU reads ~4 % slow).
+            settle = time.perf_counter()
+            while time.perf_counter() - settle < 0.2:
+                for _ in range(10):
+                    graph.replay()
+                torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
