@@ -213,8 +213,7 @@ struct AttentionTile {
 // `capacity` tiles (tiles may be null) and returns the count.
 std::uint32_t make_attention_tiles(const std::uint32_t* run_rows, std::uint32_t runs, std::uint32_t q_heads,
                                    std::uint32_t kv_heads, AttentionTile* tiles, std::uint32_t capacity);
-// Workgroups splitting the keys of each tile (1 = no merge pass).
-// Workgroups per tile over the key range of a step of m rows.
+// Workgroups per tile over the key range of a step of m rows (1 = no merge).
 std::uint32_t attention_splits(std::uint32_t tiles, std::uint64_t max_tokens, std::uint32_t m);
 std::uint64_t attention_partials_bytes(std::uint32_t tiles, std::uint32_t splits, std::uint32_t head_dim);
 // head_dim 64 or 128.  tiles: device array; partials: attention_partials_bytes.

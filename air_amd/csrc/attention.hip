@@ -15,7 +15,10 @@
 //
 // Causality: row r attends tokens 0..positions[r].  Long key ranges with few
 // tiles are split over workgroups (flash-decoding); each split writes its
-// (m, l, acc) and a second kernel merges them.  All arithmetic is f32 and
+// (m, l, acc) and a second kernel merges them.  (A merge by the tile's last
+// workgroup, found with an arrival counter, needs agent-scope fences around
+// the partials, which write back and invalidate L2 per workgroup: measured
+// slower than the second launch.)  All arithmetic is f32 and
 // unfused-exact products are not required: the result differs from the
 // reference's double softmax by ~1e-6 relative (the tactic's tolerance is
 // that of the linears).
@@ -32,7 +35,7 @@ constexpr unsigned kAttnThreads = 256;
 // grids), 64 for prefill tiles (half the barriers per key).
 std::uint32_t chunk_for(std::uint32_t m) { return m <= 64u ? 32u : 64u; }
 constexpr unsigned kTileVectors = 16;
-constexpr unsigned kMaxSplits = 64;  // one wave reduces a vector's splits in the merge
+constexpr unsigned kMaxSplits = 64;  // bounds the partials of a tile
 
 __device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
@@ -76,16 +79,29 @@ __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
     const std::uint32_t kvh = static_cast<std::uint32_t>((static_cast<std::uint64_t>(tile.head) * kv_heads) / q_heads);
     const std::int32_t* table = tables + static_cast<std::uint64_t>(tile.row) * g.max_pages;
 
-    // Keys of the tile: 0 .. max position + 1, in chunks; this split's share.
+    // Split s takes key chunks s, s + splits, s + 2 splits, ...: its first
+    // chunk is known before the positions are, so that chunk's page slots
+    // are looked up while they load.  Slots past a row's position are read
+    // and masked (their pages exist or read as absent).
+    const auto resolve = [&](std::uint32_t c, unsigned buf) __attribute__((always_inline)) {
+        if (tid < kChunk) {   // page table lookup, once per token
+            const std::uint64_t token = static_cast<std::uint64_t>(c) * kChunk + tid;
+            const float* kp = kv_slot(g, table, layer, token, false);
+            slot_off[buf][tid] = kp ? kp - g.pool : -1;
+        }
+    };
+    resolve(split, 0u);
+
+    // Keys of the tile: 0 .. max position + 1.  Splits holding no chunk of
+    // them leave at once (every workgroup of the tile agrees on `live`).
     std::int64_t tmax = 0;
     for (unsigned r = 0; r < tile.rows; ++r) {
         const std::int64_t p = positions[tile.row + r];
         tmax = p + 1 > tmax ? p + 1 : tmax;
     }
     const std::uint32_t chunks = static_cast<std::uint32_t>((tmax + kChunk - 1) / kChunk);
-    const std::uint32_t per_split = (chunks + splits - 1) / splits;
-    const std::uint32_t c_begin = split * per_split;
-    const std::uint32_t c_end = c_begin + per_split < chunks ? c_begin + per_split : chunks;
+    const std::uint32_t live = chunks < splits ? chunks : splits;   // splits with at least one chunk
+    if (split >= live) return;
 
     // This thread's query vector: (row, head) and its position.
     const bool active = qi < nq;
@@ -112,19 +128,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
     // V of a token sits page_tokens * kv_width floats after its K in the page.
     const std::uint64_t v_after_k = static_cast<std::uint64_t>(g.page_tokens) * g.kv_width;
     constexpr unsigned kIters = kChunk * D4 / kAttnThreads;   // float4 of K (and of V) per thread per chunk
-    // Two-stage pipeline: chunk c+1's page slots are resolved and its K and V
-    // loads issued into registers before chunk c is computed from LDS.
-    const auto resolve = [&](std::uint32_t c, unsigned buf) __attribute__((always_inline)) {
-        if (tid < kChunk) {   // page table lookup, once per token
-            const std::int64_t token = static_cast<std::int64_t>(c) * kChunk + tid;
-            std::int64_t off = -1;
-            if (token < tmax) {
-                const float* kp = kv_slot(g, table, layer, static_cast<std::uint64_t>(token), false);
-                if (kp) off = kp - g.pool;
-            }
-            slot_off[buf][tid] = off;
-        }
-    };
+    // Two-stage pipeline: chunk c + splits' page slots are resolved and its
+    // K and V loads issued into registers before chunk c is computed from LDS.
     float4 kr[kIters], vr[kIters];
     const auto fetch = [&](unsigned buf) __attribute__((always_inline)) {
 #pragma unroll
@@ -141,12 +146,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
             }
         }
     };
-    if (c_begin < c_end) resolve(c_begin, 0u);
     __syncthreads();
-    if (c_begin < c_end) fetch(0u);
-    for (std::uint32_t c = c_begin; c < c_end; ++c) {
+    fetch(0u);
+    unsigned buf = 0u;
+    for (std::uint32_t c = split; c < chunks; c += splits, buf ^= 1u) {
         const std::int64_t c0 = static_cast<std::int64_t>(c) * kChunk;
-        const unsigned buf = (c - c_begin) & 1u;
+        const std::uint32_t next = c + splits;
         __syncthreads();  // previous chunk's K, V and P are consumed
 #pragma unroll
         for (unsigned it = 0; it < kIters; ++it) {
@@ -155,9 +160,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
             *reinterpret_cast<float4*>(&ks[t][4u * d4]) = kr[it];
             *reinterpret_cast<float4*>(&vs[t][4u * d4]) = vr[it];
         }
-        if (c + 1u < c_end) resolve(c + 1u, buf ^ 1u);
+        if (next < chunks) resolve(next, buf ^ 1u);
         __syncthreads();
-        if (c + 1u < c_end) fetch(buf ^ 1u);   // in flight while chunk c computes
+        if (next < chunks) fetch(buf ^ 1u);   // in flight while chunk c computes
 
         // Scores of tokens lane16 + 16 j.  Idle vector slots (a decode tile
         // of 7 grouped heads leaves 9 of 16) skip the LDS reads: whole waves
@@ -224,8 +229,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
         }
     }
 
-    if (!active) return;
-    if (splits == 1u) {
+    if (live == 1u) {
+        if (!active) return;
         const float inv = 1.0f / l;
         float* dst = out + static_cast<std::uint64_t>(q_row) * q_heads * D + static_cast<std::uint64_t>(q_head) * D;
 #pragma unroll
@@ -237,6 +242,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
         return;
     }
     // Partial of this split: [tile][split][vector] {m, l, pad, pad, acc[D]}.
+    if (!active) return;
     float* part = partials + ((static_cast<std::uint64_t>(blockIdx.x) * splits + split) * kTileVectors + qi) * (D + 4u);
     if (lane16 == 0) {
         part[0] = mx;
@@ -249,54 +255,76 @@ __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
     }
 }
 
-// Merges the splits of each tile: o = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M).
+// Merges the live splits of each tile (those holding a chunk at or before
+// the tile's last position): o = sum_s acc_s e^(m_s - M) / sum_s l_s
+// e^(m_s - M), accumulated with a running M.  The positions and the first
+// kBatch splits' partials are loaded together (dead splits' stale partials
+// are read and ignored), so a decode tile merges in one round trip.
 template <unsigned D>
 __global__ __launch_bounds__(kAttnThreads) void attention_merge_kernel(const AttentionTile* __restrict__ tiles,
-                                                                       std::uint32_t splits, std::uint32_t m,
-                                                                       std::uint32_t q_heads, std::uint32_t kv_heads,
+                                                                       std::uint32_t splits, std::uint32_t chunk,
+                                                                       std::uint32_t m, std::uint32_t q_heads,
+                                                                       std::uint32_t kv_heads,
+                                                                       const std::int32_t* __restrict__ positions,
                                                                        const float* __restrict__ partials,
                                                                        float* __restrict__ out) {
-    __shared__ float weight[kTileVectors][kMaxSplits];   // e^(m_s - M) / L
-    const AttentionTile tile = tiles[blockIdx.x];
-    if (!tile_ok(tile, m, q_heads, kv_heads) || splits > kMaxSplits) return;
-    const unsigned nq = tile.rows * tile.heads;
-    const std::uint64_t step = static_cast<std::uint64_t>(kTileVectors) * (D + 4u);   // floats between splits
-    const float* tile_base = partials + static_cast<std::uint64_t>(blockIdx.x) * splits * step;
-    // One thread per (vector, split) reads its (m, l); a wave reduces each vector.
-    for (unsigned idx = threadIdx.x; idx < nq * kMaxSplits; idx += kAttnThreads) {
-        const unsigned v = idx / kMaxSplits, s = idx % kMaxSplits;
-        float ms = -__builtin_huge_valf(), ls = 0.0f;
-        if (s < splits) {
-            ms = tile_base[s * step + static_cast<std::uint64_t>(v) * (D + 4u)];
-            ls = tile_base[s * step + static_cast<std::uint64_t>(v) * (D + 4u) + 1u];
-        }
-        float mx = ms;
-        for (int off = 32; off > 0; off >>= 1) {
-            const float o = __shfl_xor(mx, off);
-            mx = o > mx ? o : mx;
-        }
-        const float w = ms == -__builtin_huge_valf() ? 0.0f : __expf(ms - mx);
-        float den = ls * w;
-        for (int off = 32; off > 0; off >>= 1) den += __shfl_xor(den, off);
-        weight[v][s] = w / den;
-    }
-    __syncthreads();
     constexpr unsigned D4 = D / 4;
+    constexpr unsigned kBatch = 16;   // splits whose partials are in flight at once
+    const AttentionTile tile = tiles[blockIdx.x];
+    if (!tile_ok(tile, m, q_heads, kv_heads)) return;
+    const unsigned nq = tile.rows * tile.heads;
+    const std::uint64_t part_step = static_cast<std::uint64_t>(kTileVectors) * (D + 4u);   // floats between splits
+    const float* tile_part = partials + static_cast<std::uint64_t>(blockIdx.x) * splits * part_step;
     for (unsigned idx = threadIdx.x; idx < nq * D4; idx += kAttnThreads) {
         const unsigned v = idx / D4, d4 = idx % D4;
-        const float* base = tile_base + static_cast<std::uint64_t>(v) * (D + 4u) + 4u + 4u * d4;
+        const float* vbase = tile_part + static_cast<std::uint64_t>(v) * (D + 4u);
+        float run_m = -__builtin_huge_valf(), run_l = 0.0f;
         float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (std::uint32_t s = 0; s < splits; ++s) {
-            const float w = weight[v][s];
-            const float4 a = load4(base + s * step);
-            o.x += a.x * w;
-            o.y += a.y * w;
-            o.z += a.z * w;
-            o.w += a.w * w;
+        std::uint32_t live = splits;
+        for (std::uint32_t s0 = 0; s0 < live; s0 += kBatch) {
+            float ms[kBatch], ls[kBatch];
+            float4 as[kBatch];
+#pragma unroll
+            for (unsigned j = 0; j < kBatch; ++j) {
+                // Every load is issued (a clamped split index): a guarded
+                // load would wait at its join.
+                const std::uint32_t sj = s0 + j < splits ? s0 + j : splits - 1u;
+                const float* b = vbase + sj * part_step;
+                ms[j] = b[0];
+                ls[j] = b[1];
+                as[j] = load4(b + 4u + 4u * d4);
+            }
+            if (s0 == 0) {
+                std::int64_t tmax = 0;
+                for (unsigned r = 0; r < tile.rows; ++r) {
+                    const std::int64_t p = positions[tile.row + r];
+                    tmax = p + 1 > tmax ? p + 1 : tmax;
+                }
+                const std::uint64_t chunks = (static_cast<std::uint64_t>(tmax) + chunk - 1u) / chunk;
+                live = chunks < splits ? static_cast<std::uint32_t>(chunks) : splits;
+                if (live <= 1u) return;   // the split kernel wrote this tile's output
+            }
+#pragma unroll
+            for (unsigned j = 0; j < kBatch; ++j) {
+                // A split with no key at or before this vector's position
+                // holds m = -inf and adds nothing.
+                if (s0 + j >= live || ms[j] == -__builtin_huge_valf()) continue;
+                const float m_new = ms[j] > run_m ? ms[j] : run_m;
+                const float c_old = __expf(run_m - m_new);   // 0 while run_m = -inf
+                const float c_new = __expf(ms[j] - m_new);
+                o.x = o.x * c_old + as[j].x * c_new;
+                o.y = o.y * c_old + as[j].y * c_new;
+                o.z = o.z * c_old + as[j].z * c_new;
+                o.w = o.w * c_old + as[j].w * c_new;
+                run_l = run_l * c_old + ls[j] * c_new;
+                run_m = m_new;
+            }
         }
+        const float inv = 1.0f / run_l;
         const unsigned row = tile.row + v / tile.heads, head = tile.head + v % tile.heads;
         *reinterpret_cast<float4*>(out + static_cast<std::uint64_t>(row) * q_heads * D +
-                                   static_cast<std::uint64_t>(head) * D + 4u * d4) = o;
+                                   static_cast<std::uint64_t>(head) * D + 4u * d4) =
+            make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
     }
 }
 
@@ -340,7 +368,7 @@ std::uint32_t attention_splits(std::uint32_t tiles, std::uint64_t max_tokens, st
     // per CU on 256 CUs); 64-token chunks (prefill): about 512.
     const std::uint64_t want = chunk == 32u ? (768u / tiles > 0u ? 768u / tiles : 1u) : (512u + tiles - 1) / tiles;
     const std::uint64_t s = want < chunks ? want : chunks;
-    return static_cast<std::uint32_t>(s < 64 ? s : 64);
+    return static_cast<std::uint32_t>(s < kMaxSplits ? s : kMaxSplits);
 }
 
 std::uint64_t attention_partials_bytes(std::uint32_t tiles, std::uint32_t splits, std::uint32_t head_dim) {
@@ -356,34 +384,32 @@ hipError_t launch_attention_tiles(const KvLayout& kv, const float* qkv, std::uin
     const KvGeometry g{kv.pool, kv.page_tokens, kv.kv_width, kv.layers, kv.max_pages, kv.pool_pages};
     const float scale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(head_dim)));
     const dim3 grid(tile_count, splits);
-    const bool small = chunk_for(m) == 32u;
+    const std::uint32_t chunk = chunk_for(m);
+#define AIR_ATTENTION_LAUNCH(D, C)                                                                               \
+    hipLaunchKernelGGL((attention_tile_kernel<D, C>), grid, dim3(kAttnThreads), 0, stream, g, qkv, stride, m,     \
+                       positions, tables, layer, q_heads, kv_heads, tiles, splits, scale, partials, out)
+#define AIR_ATTENTION_MERGE(D)                                                                                   \
+    hipLaunchKernelGGL(attention_merge_kernel<D>, dim3(tile_count), dim3(kAttnThreads), 0, stream, tiles, splits, \
+                       chunk, m, q_heads, kv_heads, positions, partials, out)
     if (head_dim == 128u) {
-        if (small) {
-            hipLaunchKernelGGL((attention_tile_kernel<128, 32>), grid, dim3(kAttnThreads), 0, stream, g, qkv, stride,
-                               m, positions, tables, layer, q_heads, kv_heads, tiles, splits, scale, partials, out);
+        if (chunk == 32u) {
+            AIR_ATTENTION_LAUNCH(128, 32);
         } else {
-            hipLaunchKernelGGL((attention_tile_kernel<128, 64>), grid, dim3(kAttnThreads), 0, stream, g, qkv, stride,
-                               m, positions, tables, layer, q_heads, kv_heads, tiles, splits, scale, partials, out);
+            AIR_ATTENTION_LAUNCH(128, 64);
         }
-        if (splits > 1u) {
-            hipLaunchKernelGGL(attention_merge_kernel<128>, dim3(tile_count), dim3(kAttnThreads), 0, stream, tiles,
-                               splits, m, q_heads, kv_heads, partials, out);
-        }
+        if (splits > 1u) AIR_ATTENTION_MERGE(128);
     } else if (head_dim == 64u) {
-        if (small) {
-            hipLaunchKernelGGL((attention_tile_kernel<64, 32>), grid, dim3(kAttnThreads), 0, stream, g, qkv, stride,
-                               m, positions, tables, layer, q_heads, kv_heads, tiles, splits, scale, partials, out);
+        if (chunk == 32u) {
+            AIR_ATTENTION_LAUNCH(64, 32);
         } else {
-            hipLaunchKernelGGL((attention_tile_kernel<64, 64>), grid, dim3(kAttnThreads), 0, stream, g, qkv, stride,
-                               m, positions, tables, layer, q_heads, kv_heads, tiles, splits, scale, partials, out);
+            AIR_ATTENTION_LAUNCH(64, 64);
         }
-        if (splits > 1u) {
-            hipLaunchKernelGGL(attention_merge_kernel<64>, dim3(tile_count), dim3(kAttnThreads), 0, stream, tiles,
-                               splits, m, q_heads, kv_heads, partials, out);
-        }
+        if (splits > 1u) AIR_ATTENTION_MERGE(64);
     } else {
         return hipErrorInvalidValue;
     }
+#undef AIR_ATTENTION_LAUNCH
+#undef AIR_ATTENTION_MERGE
     return hipGetLastError();
 }
 

@@ -135,6 +135,54 @@ def test_online_rejects_bad_geometry(torch_cuda, hip_ctx):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("q_heads,kv_heads,head", [(28, 4, 128), (64, 2, 64), (4, 4, 64)])
+def test_decode_rows_at_graph_max_tokens(torch_cuda, hip_ctx, q_heads, kv_heads, head):
+    """Decode rows of distinct sequences (lengths 1 .. 2049) with max_tokens
+    at the decode graphs' 4096 -- 64 key splits per tile, most of them past
+    every row's keys, the merge taking only the live ones -- and at the
+    step's own maximum: both within 1e-5 of the float64 attention.  Group
+    sizes 7 (one tile per KV head), 32 (two tiles) and 1."""
+    torch = torch_cuda
+    dev = torch.device("cuda:0")
+    page_tokens, layers, layer = 16, 2, 1
+    kv_width = kv_heads * head
+    lengths = [1, 5, 33, 700, 2049]
+    max_pages = 4096 // page_tokens
+    rng = np.random.default_rng(q_heads + head)
+    pool_pages = sum((n + page_tokens - 1) // page_tokens for n in lengths) + 2
+    perm = rng.permutation(pool_pages)
+    tables, used = [], 0
+    for n in lengths:
+        need = (n + page_tokens - 1) // page_tokens
+        tables.append(list(perm[used:used + need]) + [-1] * (max_pages - need))
+        used += need
+    positions = [n - 1 for n in lengths]
+    m = len(positions)
+    print(f"decode rows q={q_heads} kv={kv_heads} head={head} lengths={lengths}", flush=True)
+    pool_h = rng.standard_normal(pool_pages * layers * 2 * page_tokens * kv_width).astype(np.float32)
+    qkv_h = rng.standard_normal((m, q_heads * head + 2 * kv_width)).astype(np.float32)
+    pool = torch.from_numpy(pool_h).to(dev)
+    qkv = torch.from_numpy(qkv_h).to(dev)
+    pos_d = torch.tensor(positions, dtype=torch.int32, device=dev)
+    tab_d = torch.tensor(np.array(tables, dtype=np.int32), device=dev)
+    kv = capi.KvLayout(pool.data_ptr(), page_tokens, kv_width, layers, max_pages, pool_pages)
+    tiles_h = capi.attention_tiles([1] * m, q_heads, kv_heads)
+    tiles_d = torch.tensor(np.array(tiles_h, dtype=np.uint32).view(np.int32), device=dev)
+    stride = q_heads * head + 2 * kv_width
+    lib = capi.lib()
+    ref = _reference(pool_h, tables, positions, qkv_h, layer, q_heads, kv_heads, head, page_tokens, layers)
+    for max_tokens in (4096, max(lengths)):
+        out = torch.full((m, q_heads * head), float("nan"), device=dev)
+        capi.check(lib.air_hip_attention_online(hip_ctx.handle, ctypes.byref(kv), qkv.data_ptr(), stride, m,
+                                                pos_d.data_ptr(), tab_d.data_ptr(), layer, q_heads, kv_heads,
+                                                head, tiles_d.data_ptr(), len(tiles_h), max_tokens, out.data_ptr()))
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().astype(np.float64)
+        err = np.abs(got - ref).max() / np.abs(ref).max()
+        assert err <= 1e-5, (max_tokens, err)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("q_heads,kv_heads,head,rope_dims", [(28, 4, 128, 128), (4, 2, 64, 32)])
 def test_rope_kv_append_matches_separate_calls(torch_cuda, hip_ctx, q_heads, kv_heads, head, rope_dims):
     """air_hip_rope_kv_append leaves q|k|v and the pool bit-identical to
