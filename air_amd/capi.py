@@ -118,6 +118,7 @@ SIGNATURES = {
     "air_hip_context_set_prefill_tuning": (_I, [_P, _U32, _U32, _U32, _U32]),
     "air_hip_context_set_decode_path": (_I, [_P, _U32, _U32, _U32]),
     "air_hip_context_set_prefill_pipeline": (_I, [_P, _U32]),
+    "air_hip_context_set_decode_pipeline": (_I, [_P, _U32]),
     "air_hip_matrix_rows": (_I, [_P, _P, _P, _U32, _P]),
     "air_hip_rms_norm": (_I, [_P, _P, _P, _P, _U32, _U64, ctypes.c_double]),
     "air_hip_rope": (_I, [_P, _P, _U64, _U32, _P, _U32, _U32, _U32, _U32, _P, _U64]),
@@ -231,6 +232,10 @@ class Context:
 
     def set_decode_path(self, path: int = 0, tile_n: int = 0, k_splits: int = 0) -> None:
         check(lib().air_hip_context_set_decode_path(self.handle, path, tile_n, k_splits))
+
+    def set_decode_pipeline(self, lds_stages: int = 0) -> None:
+        """Decode (skinny) operand staging: 0 automatic, 1 registers, 2..4 LDS ring stages."""
+        check(lib().air_hip_context_set_decode_pipeline(self.handle, lds_stages))
 
     def set_prefill_pipeline(self, lds_stages: int = 0) -> None:
         """Prefill operand staging: 0 automatic, 1 registers, 2..4 LDS ring stages."""

@@ -71,6 +71,7 @@ struct air_hip_context {
     std::uint32_t decode_path{0};
     std::uint32_t skinny_tile_n{0};
     std::uint32_t skinny_splits{0};
+    std::uint32_t skinny_lds_stages{0};   // 0 automatic, 1 registers, 2..4 LDS ring stages
     std::uint32_t* bound_scratch{nullptr};  // one uint32 for the weight exponent at residency
     void* attention_scratch{nullptr};       // attention scores, grown on demand
     std::uint64_t attention_scratch_bytes{0};
@@ -248,7 +249,13 @@ enum class Route { prefill, gemv, fused, skinny_x, skinny_loaded, decode_linear 
 // faster), and loses on wide ones (gate|up, lm_head: up to 2x slower) and at
 // M = 64.  Q4_K with four activation tiles would also spill in it.
 Route skinny_route(const air_hip_context* ctx, const air_hip_matrix* m, std::uint32_t rows) {
-    const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits);
+    const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages);
+    // Q8_0 from 17 rows: the split activations feed the LDS pipeline, which
+    // beats the f32-input kernel on the narrow 7B matrices too, split launch
+    // included (M = 32: q|k|v 18.4 -> 16.2 us, o 16.3 -> 14.7, down 41.5 ->
+    // 32.1).  At M = 8 the two are even per call, and in a graph the split's
+    // extra launch made the step slower (2.60 -> 2.78 ms).
+    if (m->planes.type == kQ8_0 && rows > 16u && shape.lds_stages >= 2u) return Route::skinny_loaded;
     const bool narrow = m->planes.nt <= 512u && (rows <= 32u || m->planes.k <= 4096u);
     return (!narrow || (m->planes.type == kQ4_K && shape.mt == 4u)) ? Route::skinny_loaded : Route::skinny_x;
 }
@@ -280,7 +287,7 @@ Route route_linear(const air_hip_context* ctx, const air_hip_matrix* m, std::uin
 // (two with a K split), no activation workspace.
 int run_skinny_x(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y, const float* bias,
                  std::uint32_t rows, const SplitEpilogue* epilogue, bool* applied, const void* ready) {
-    const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits);
+    const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages);
     if (skinny_route(ctx, m, rows) == Route::skinny_loaded) {
         int rc = load_activations_for(ctx, x, m->planes.k, rows, ready);
         if (rc != AIR_HIP_OK) return rc;
@@ -439,6 +446,13 @@ int air_hip_context_set_decode_path(air_hip_context* ctx, uint32_t path, uint32_
     ctx->decode_path = path;
     ctx->skinny_tile_n = tile_n;
     ctx->skinny_splits = k_splits;
+    return AIR_HIP_OK;
+}
+
+int air_hip_context_set_decode_pipeline(air_hip_context* ctx, uint32_t lds_stages) {
+    if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
+    if (lds_stages > 4u) return fail(AIR_HIP_INVALID_ARGUMENT, "lds_stages must be 0 .. 4");
+    ctx->skinny_lds_stages = lds_stages;
     return AIR_HIP_OK;
 }
 
@@ -732,7 +746,7 @@ int linear_loaded(air_hip_context* ctx, const air_hip_matrix* m, float* y, const
         return fail(AIR_HIP_INVALID_STATE, "activations were loaded for another decode path; load them again");
     }
     if (skinny) {
-        const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits);
+        const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages);
         const std::uint64_t partial_bytes = skinny_partials_bytes(shape, rows, m->planes.n);
         if (partial_bytes > 0u) {
             const int rc = ensure_split_buffers(ctx, partial_bytes, 0u);
@@ -846,10 +860,14 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
     case Route::skinny_x:
     case Route::skinny_loaded: {
         const bool loaded = route_linear(ctx, m, rows, tactic) == Route::skinny_loaded;
-        const SkinnyShape k = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits);
-        std::snprintf(buf, sizeof buf, "%sskinny_kernel<%s%s> mt=%u tile_n=%u groups=%u splits=%u%s",
-                      loaded ? "split_rows_kernel + " : "", fmt, loaded ? "" : ", f32 input", k.mt, k.tile_n,
-                      k.groups, k.splits, k.splits > 1u ? " + split reduction" : "");
+        const SkinnyShape k = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages);
+        const bool lds = loaded && k.lds_stages >= 2u && m->planes.type == kQ8_0;
+        char stages[32] = "";
+        if (lds) std::snprintf(stages, sizeof stages, " lds_stages=%u", k.lds_stages);
+        std::snprintf(buf, sizeof buf, "%s%s<%s%s> mt=%u tile_n=%u groups=%u splits=%u%s%s",
+                      loaded ? "split_rows_kernel + " : "", lds ? "skinny_lds_kernel" : "skinny_kernel", fmt,
+                      loaded ? "" : ", f32 input", k.mt, k.tile_n, k.groups, k.splits, stages,
+                      k.splits > 1u ? " + split reduction" : "");
         break;
     }
     case Route::decode_linear:
@@ -898,7 +916,7 @@ int air_hip_linear_noalloc(air_hip_context* ctx, const air_hip_matrix* m, const 
     std::uint64_t ws_bytes = 0, partial_bytes = 0;
     SkinnyShape shape{};
     if (route == Route::skinny_x || route == Route::skinny_loaded) {
-        shape = plan_skinny(p, rows, ctx->skinny_tile_n, ctx->skinny_splits);
+        shape = plan_skinny(p, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages);
         partial_bytes = skinny_partials_bytes(shape, rows, p.n);
     }
     if (route == Route::skinny_loaded || route == Route::decode_linear) {

@@ -253,6 +253,191 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_kernel(SkinnyArgs a) {
     }
 }
 
+// ---- LDS-pipelined variant (Q8_0, split activations) ----------------------
+//
+// The same arithmetic as skinny_kernel<kQ8_0, MT, TN, false>, with every
+// operand of a 64-k step moved by direct global -> LDS loads into one of NS
+// stages, so up to NS - 1 steps of weight codes per wave are in flight
+// without holding registers (the register pipeline above has room for two).
+// A stage holds the step's 4 MT activation fragments (each wave loads MT of
+// them), then each wave's TN weight-code records (1 KiB) and scale records
+// (64 lanes x 4 bytes).  Each KiB is one 64-lane x 16-byte fragment in lane
+// order, read back at lane * 16 (no bank conflicts).  One bare barrier per
+// step publishes the stage and frees the oldest one; a wave waits only for
+// its own loads of the stage (vmcnt).
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
+
+// Lane l's 16 (or 4) bytes land at lds_wave_base + l * 16 (l * 4).
+__device__ __forceinline__ void lds_load16(const void* src, void* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds((global_void_t*)(const_cast<void*>(src)), (lds_void_t*)(lds_wave_base), 16, 0, 0);
+}
+__device__ __forceinline__ void lds_load4(const void* src, void* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds((global_void_t*)(const_cast<void*>(src)), (lds_void_t*)(lds_wave_base), 4, 0, 0);
+}
+
+// s_waitcnt for vmcnt <= n only (expcnt and lgkmcnt at their maxima).
+template <unsigned n>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(n < 64u, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((n & 0xfu) | ((n >> 4) << 14) | (0x7u << 4) | (0xfu << 8));
+}
+
+template <int MT, int TN>
+constexpr unsigned skinny_stage_bytes() {
+    return 4u * MT * 1024u + 4u * TN * 1024u + 4u * TN * 256u;
+}
+
+template <int MT, int TN, int NS>
+__global__ __launch_bounds__(kThreads, 2) void skinny_lds_kernel(SkinnyArgs a) {
+    constexpr unsigned kStage = skinny_stage_bytes<MT, TN>();
+    constexpr unsigned kCodes = 4u * MT * 1024u;            // offset of the weight codes in a stage
+    constexpr unsigned kScales = kCodes + 4u * TN * 1024u;  // offset of the weight scales
+    constexpr unsigned kLoads = MT + 2u * TN;               // load instructions per wave per stage
+    static_assert(NS >= 2 && NS <= 4, "two to four stages");
+    // One LDS object per stage, addressed with compile-time stage numbers:
+    // the compiler's wait-count pass then sees that a stage's direct loads
+    // and another stage's reads touch different objects.
+    __shared__ __attribute__((aligned(1024))) unsigned char stage0[kStage];
+    __shared__ __attribute__((aligned(1024))) unsigned char stage1[kStage];
+    __shared__ __attribute__((aligned(1024))) unsigned char stage2[NS > 2 ? kStage : 16];
+    __shared__ __attribute__((aligned(1024))) unsigned char stage3[NS > 3 ? kStage : 16];
+    const auto stage = [&](unsigned st) __attribute__((always_inline)) -> unsigned char* {
+        return st == 0u ? stage0 : st == 1u ? stage1 : st == 2u ? stage2 : stage3;
+    };
+
+    const std::uint32_t lane = threadIdx.x & 63u;
+    const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const std::uint32_t group = blockIdx.x % a.groups;
+    const std::uint32_t split = blockIdx.x / a.groups;
+    const std::uint32_t rt0 = (group * 4u + wave) * TN;
+    const std::uint32_t s_begin = split * a.steps_per_split;
+    const std::uint32_t s_end = min(a.steps, s_begin + a.steps_per_split);
+
+    float4v acc[TN][MT];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[j][t] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Padded weight rows (rt >= nt) read the last real tile: their outputs
+    // are never stored.
+    std::uint64_t wtile[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const std::uint32_t rt = min(rt0 + static_cast<std::uint32_t>(j), a.nt - 1u);
+        wtile[j] = static_cast<std::uint64_t>(rt) * a.kt;
+    }
+    const u32x4* xs = reinterpret_cast<const u32x4*>(a.xs);
+    const auto issue = [&](std::uint32_t s, unsigned st) __attribute__((always_inline)) {
+        unsigned char* base = stage(st);
+        // Fragment f of the step: block f / (2 MT), tile (f / 2) % MT, part f % 2.
+#pragma unroll
+        for (unsigned j = 0; j < static_cast<unsigned>(MT); ++j) {
+            const unsigned f = wave + 4u * j;
+            lds_load16(xs + (static_cast<std::uint64_t>(s) * (4u * MT) + f) * 64u + lane, base + f * 1024u);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const std::uint64_t tile = wtile[j] + s;
+            const unsigned slot = wave * TN + static_cast<unsigned>(j);
+            lds_load16(static_cast<const u32x4*>(a.codes) + tile * 64u + lane, base + kCodes + slot * 1024u);
+            lds_load4(static_cast<const std::uint32_t*>(a.scales) + tile * 16u + (lane & 15u),
+                      base + kScales + slot * 256u);
+        }
+    };
+    const auto compute = [&](std::uint32_t s, unsigned st) __attribute__((always_inline)) {
+        const unsigned char* base = stage(st);
+        StepCodes<kQ8_0> w_in[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const unsigned slot = wave * TN + static_cast<unsigned>(j);
+            w_in[j].c = *reinterpret_cast<const u32x4*>(base + kCodes + slot * 1024u + lane * 16u);
+            w_in[j].d = *reinterpret_cast<const std::uint32_t*>(base + kScales + slot * 256u + lane * 4u);
+        }
+        half8v xf[2][MT][2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int part = 0; part < 2; ++part) {
+                    const unsigned f = (static_cast<unsigned>(b) * MT + t) * 2u + part;
+                    xf[b][t][part] = *reinterpret_cast<const half8v*>(base + f * 1024u + lane * 16u);
+                }
+        __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the arithmetic
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const half8v w = step_codes<kQ8_0>(w_in[j], b);
+                float ws, wo;
+                step_scale<kQ8_0>(w_in[j], s, b, ws, wo);
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    float4v p = mfma16x16x32(xf[b][t][0], w, float4v{0.f, 0.f, 0.f, 0.f});
+                    p = mfma16x16x32(xf[b][t][1], w, p);
+                    acc[j][t] += ws * p;
+                }
+            }
+        }
+    };
+
+    const std::uint32_t steps = s_end > s_begin ? s_end - s_begin : 0u;
+#pragma unroll
+    for (unsigned q = 0; q + 1u < NS; ++q) {
+        if (q < steps) issue(s_begin + q, q);
+    }
+    // Step q of the split computes stage q mod NS (ST, a constant).
+    const auto step = [&](std::uint32_t q, auto st_tag) __attribute__((always_inline)) {
+        constexpr unsigned ST = decltype(st_tag)::value;
+        // Stage ST is complete once at most the later stages' loads are in
+        // flight; near the end fewer follow it, so wait for everything.
+        if (q + NS - 2u < steps) {
+            wait_vm<kLoads * (NS - 2u)>();
+        } else {
+            wait_vm<0u>();
+        }
+        // Every wave's reads of the previous stage are complete before the
+        // barrier, after which that stage takes new loads; a bare s_barrier
+        // (a fence would also wait for the loads still in flight).
+        __builtin_amdgcn_s_waitcnt(0xc07fu);   // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        if (q + NS - 1u < steps) issue(s_begin + q + NS - 1u, (ST + NS - 1u) % NS);
+        compute(s_begin + q, ST);
+    };
+    for (std::uint32_t q = 0; q < steps; q += NS) {
+        step(q, std::integral_constant<unsigned, 0>{});
+        if (q + 1u < steps) step(q + 1u, std::integral_constant<unsigned, 1>{});
+        if constexpr (NS > 2) {
+            if (q + 2u < steps) step(q + 2u, std::integral_constant<unsigned, 2>{});
+        }
+        if constexpr (NS > 3) {
+            if (q + 3u < steps) step(q + 3u, std::integral_constant<unsigned, 3>{});
+        }
+    }
+
+    // D[row = activation row][col = weight row], as skinny_kernel.
+    float4v inv[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) inv[t] = reinterpret_cast<const float4v*>(a.inv_scale)[t * 4 + (lane >> 4)];
+    float* out = a.out + (a.partial ? static_cast<std::uint64_t>(split) * a.m * a.n : 0u);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const std::uint64_t n = static_cast<std::uint64_t>(rt0 + static_cast<std::uint32_t>(j)) * 16u + (lane & 15u);
+        if (n >= a.n) continue;
+        const float bn = a.bias ? a.bias[n] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const std::uint32_t m = static_cast<std::uint32_t>(t) * 16u + 4u * (lane >> 4) + static_cast<std::uint32_t>(i);
+                if (m < a.m) out[static_cast<std::uint64_t>(m) * a.n + n] = acc[j][t][i] * inv[t][i] + bn;
+            }
+        }
+    }
+}
+
 // Row-scaled activation split: one workgroup per padded row.  Pass 1 finds
 // the row's max |x|; pass 2 writes the hi/lo fragments of every (block,
 // eighth) run and the block sums of the scaled values.
@@ -357,6 +542,35 @@ hipError_t launch_fmt(const SkinnyArgs& a, const SkinnyShape& shape, std::uint32
     }
 }
 
+template <int MT>
+hipError_t launch_lds_mt(const SkinnyArgs& a, const SkinnyShape& shape, std::uint32_t blocks, hipStream_t stream) {
+    const bool two = shape.tile_n == 2u;
+    switch (shape.lds_stages) {
+    case 2:
+        if (two) hipLaunchKernelGGL((skinny_lds_kernel<MT, 2, 2>), dim3(blocks), dim3(kThreads), 0, stream, a);
+        else hipLaunchKernelGGL((skinny_lds_kernel<MT, 1, 2>), dim3(blocks), dim3(kThreads), 0, stream, a);
+        break;
+    case 3:
+        if (two) hipLaunchKernelGGL((skinny_lds_kernel<MT, 2, 3>), dim3(blocks), dim3(kThreads), 0, stream, a);
+        else hipLaunchKernelGGL((skinny_lds_kernel<MT, 1, 3>), dim3(blocks), dim3(kThreads), 0, stream, a);
+        break;
+    default:
+        if (two) hipLaunchKernelGGL((skinny_lds_kernel<MT, 2, 4>), dim3(blocks), dim3(kThreads), 0, stream, a);
+        else hipLaunchKernelGGL((skinny_lds_kernel<MT, 1, 4>), dim3(blocks), dim3(kThreads), 0, stream, a);
+        break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_lds(const SkinnyArgs& a, const SkinnyShape& shape, std::uint32_t blocks, hipStream_t stream) {
+    switch (shape.mt) {
+    case 1: return launch_lds_mt<1>(a, shape, blocks, stream);
+    case 2: return launch_lds_mt<2>(a, shape, blocks, stream);
+    case 3: return launch_lds_mt<3>(a, shape, blocks, stream);
+    default: return launch_lds_mt<4>(a, shape, blocks, stream);
+    }
+}
+
 template <bool XF>
 hipError_t launch_any(const TilePlanes& p, const SkinnyArgs& a, const SkinnyShape& shape, std::uint32_t blocks,
                       hipStream_t stream) {
@@ -379,7 +593,8 @@ hipError_t launch_split_activations_rows(const float* x, std::uint32_t m, std::u
     return hipGetLastError();
 }
 
-SkinnyShape plan_skinny(const TilePlanes& p, std::uint32_t m, std::uint32_t tile_n, std::uint32_t k_splits) {
+SkinnyShape plan_skinny(const TilePlanes& p, std::uint32_t m, std::uint32_t tile_n, std::uint32_t k_splits,
+                        std::uint32_t lds_stages) {
     SkinnyShape s;
     s.mt = static_cast<std::uint32_t>(ceil_div(m, 16u));
     // Two weight tiles per wave halve the LDS activation reads per weight
@@ -387,8 +602,10 @@ SkinnyShape plan_skinny(const TilePlanes& p, std::uint32_t m, std::uint32_t tile
     // (the in-workgroup split of the f32 variant holds more live values).
     // Automatic choice, measured on the Qwen2-7B shapes: two tiles only pay
     // for matrices of 2000..4096 row tiles (gate|up) at M <= 32.
+    // lm_head-sized matrices (9504 row tiles) also take two at M <= 32 on the
+    // register pipeline (M = 32: 155 -> 132 us).
     const std::uint32_t tn2_max_mt = 2u;
-    const std::uint32_t want = tile_n != 0u ? tile_n : ((s.mt <= 2u && p.nt >= 2000u && p.nt <= 4096u) ? 2u : 1u);
+    const std::uint32_t want = tile_n != 0u ? tile_n : ((s.mt <= 2u && p.nt >= 2000u) ? 2u : 1u);
     s.tile_n = (want == 2u && s.mt <= tn2_max_mt) ? 2u : 1u;
     s.groups = static_cast<std::uint32_t>(ceil_div(p.nt, 4u * s.tile_n));
     s.steps = static_cast<std::uint32_t>(p.kp / kStepK);
@@ -411,6 +628,14 @@ SkinnyShape plan_skinny(const TilePlanes& p, std::uint32_t m, std::uint32_t tile
     splits = splits < 1u ? 1u : (splits > s.steps ? s.steps : splits);
     s.steps_per_split = static_cast<std::uint32_t>(ceil_div(s.steps, splits));
     s.splits = static_cast<std::uint32_t>(ceil_div(s.steps, s.steps_per_split));
+    // The LDS pipeline (Q8_0, split activations): two stages measured best
+    // (three and four never helped) on every 7B matrix except the lm_head at
+    // M <= 32, where the register pipeline with two tiles per wave wins
+    // (132 vs 146 us).
+    if (lds_stages == 0u) {
+        lds_stages = p.type == kQ8_0 && (p.nt <= 4096u || s.mt >= 3u) ? 2u : 1u;
+    }
+    s.lds_stages = lds_stages >= 2u ? lds_stages : 0u;
     return s;
 }
 
@@ -440,7 +665,8 @@ hipError_t launch_skinny_linear(const TilePlanes& p, const SplitWorkspace& ws, c
     a.bias = split ? nullptr : bias;
     a.out = split ? partials : y;
     const std::uint32_t blocks = shape.groups * shape.splits;
-    const hipError_t err = launch_any<false>(p, a, shape, blocks, stream);
+    const hipError_t err = shape.lds_stages >= 2u && p.type == kQ8_0 ? launch_lds(a, shape, blocks, stream)
+                                                                     : launch_any<false>(p, a, shape, blocks, stream);
     if (err != hipSuccess || !split) return err;
     if (epilogue) return launch_split_epilogue(partials, shape.splits, m, p.n, bias, *epilogue, stream);
     return launch_split_reduce(partials, shape.splits, m, p.n, bias, y, stream);

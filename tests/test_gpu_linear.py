@@ -198,6 +198,44 @@ def test_skinny_shapes_agree(torch_cuda, hip_ctx, type_id, k, n):
         mat.release()
 
 
+@pytest.mark.parametrize("k,n", [(3584, 8200), (1024, 9000)])
+def test_skinny_lds_pipeline_matches_registers(torch_cuda, hip_ctx, k, n):
+    """The LDS-pipelined skinny kernel (Q8_0 on split activations: matrices
+    of more than 512 row tiles, a ragged last tile here) gives the register
+    pipeline's bits for 2..4 stages, one and two weight tiles per wave, with
+    and without a K split, at every activation-tile count; the register
+    pipeline matches the oracle to 1e-4."""
+    torch = torch_cuda
+    type_id = capi.TYPE_Q8_0
+    canon = helpers.weights(type_id, k, n, seed=k + 7 * n)
+    mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    try:
+        for m in (2, 16, 17, 32, 33, 64):
+            x = helpers.activations(m, k, seed=m + 11)
+            xd = _dev(torch, x)
+            for tile_n, splits in [(1, 1), (2, 1), (2, 3), (1, 2)]:
+                hip_ctx.set_decode_path(2, tile_n, splits)
+                outs = {}
+                for stages in (1, 2, 3, 4):
+                    hip_ctx.set_decode_pipeline(stages)
+                    plan = mat.plan(m)
+                    assert ("skinny_lds_kernel" in plan) == (stages >= 2), (plan, stages)
+                    y = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+                    mat.linear(xd, y, m)
+                    torch.cuda.synchronize()
+                    outs[stages] = y.cpu().numpy()
+                for stages in (2, 3, 4):
+                    assert np.array_equal(outs[stages].view(np.uint32), outs[1].view(np.uint32)), (
+                        m, tile_n, splits, stages)
+                if m in (17, 64) and (tile_n, splits) == (2, 3):
+                    want = oracle.linear(type_id, canon, k, n, x)
+                    assert helpers.rel_l2(outs[1], want) <= DECODE_TOL, m
+    finally:
+        hip_ctx.set_decode_pipeline(0)
+        hip_ctx.set_decode_path(0)
+        mat.release()
+
+
 def test_graph_replay_after_workspace_growth(torch_cuda):
     """A HIP graph captured before the context grows its K-split partials
     replays on the buffer it captured (kept, not freed, until the context is

@@ -24,9 +24,10 @@ pytestmark = pytest.mark.gpu
 
 # (format, N, K, bias, (first M, second M)): one case per route the planner
 # takes at these shapes -- skinny over split activations with an 8-way K
-# split (down), two weight tiles per wave and a 2-way split (gate|up),
-# skinny straight from f32 rows (q|k|v), the single-launch fused kernel and
-# the M = 1 GEMV (o).
+# split (down), two weight tiles per wave and a 2-way split (gate|up), both
+# on the LDS pipeline, skinny straight from f32 rows (q|k|v at M = 3; M = 16
+# takes the split route), the single-launch fused kernel and the M = 1 GEMV
+# (o).
 CASES = [
     (capi.TYPE_Q8_0, 3584, 18944, False, (64, 8)),
     (capi.TYPE_Q8_0, 37888, 3584, False, (32, 16)),
