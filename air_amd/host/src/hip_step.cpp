@@ -525,8 +525,13 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
         }
         const float* next_norm = l + 1U < c.layer_count ? attn_norm_[l + 1U] : output_norm_;
         if (epilogues) {
-            if (Status s = prepared_.linear_epilogue(l, LinearRole::ffn_down, act_, m, hidden_,
-                                                     AIR_HIP_EPILOGUE_RESIDUAL, next_norm, normed_, eps, tactic);
+            // The next norm's output is split for its consumer too (the next
+            // layer's q|k|v, or the lm_head): the split route, which Q8_0
+            // q|k|v takes above 16 rows and the lm_head above 4, then needs
+            // no split launch of its own.
+            const int down_epilogue = m >= 2U ? AIR_HIP_EPILOGUE_RESIDUAL_LOAD : AIR_HIP_EPILOGUE_RESIDUAL;
+            if (Status s = prepared_.linear_epilogue(l, LinearRole::ffn_down, act_, m, hidden_, down_epilogue,
+                                                     next_norm, normed_, eps, tactic);
                 !s) {
                 return s;
             }
