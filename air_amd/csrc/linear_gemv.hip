@@ -175,9 +175,17 @@ __device__ __forceinline__ half8v tile_block_codes(const Chunk<FMT, R, U, NORM>&
     }
 }
 
+// The RMS norm's per-element step, (x * scale) * w, without contraction (the
+// norm kernel's arithmetic).
+__device__ __forceinline__ float norm_apply(float x, float scale, float w) {
+#pragma clang fp contract(off)
+    const float xs = x * scale;
+    return xs * w;
+}
+
 template <int FMT, int R, int U, bool NORM>
 __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U, NORM>& ch, std::uint32_t unit,
-                                              std::uint32_t lane, double& ss, float4v (&acc)[R]) {
+                                              std::uint32_t lane, float norm_scale, float4v (&acc)[R]) {
     using F = GemvFormat<FMT>;
     constexpr int T = Chunk<FMT, R, U, NORM>::kTiles;
     // First A / D row of the unit: a multiple of 16 / U >= 4, so the D slot
@@ -188,10 +196,7 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U, NORM>& ch, 
         const float w[8] = {ch.nw[0][0], ch.nw[0][1], ch.nw[0][2], ch.nw[0][3],
                             ch.nw[1][0], ch.nw[1][1], ch.nw[1][2], ch.nw[1][3]};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            ss += static_cast<double>(v[e]) * v[e];   // exact product, one rounding
-            v[e] = v[e] * w[e];
-        }
+        for (int e = 0; e < 8; ++e) v[e] = norm_apply(v[e], norm_scale, w[e]);
     }
     // One power-of-two scale for the whole unit (all 64 lanes).  The f16
     // hi + lo split keeps ~21 significant bits of every element, however far
@@ -320,6 +325,15 @@ __device__ __forceinline__ float swiglu(float g, float u) {
     return s * u;
 }
 
+__device__ __forceinline__ double square_sum4(double acc, float4 v) {
+#pragma clang fp contract(off)
+    acc += static_cast<double>(v.x) * v.x;
+    acc += static_cast<double>(v.y) * v.y;
+    acc += static_cast<double>(v.z) * v.z;
+    acc += static_cast<double>(v.w) * v.w;
+    return acc;
+}
+
 // Workgroup = W waves on the same R row tiles; the chunks of K are split
 // across the waves.  P = 2: each wave double-buffers whole chunks.  P = 1:
 // one chunk buffer, loaded and consumed in turn -- the lower register count
@@ -327,12 +341,9 @@ __device__ __forceinline__ float swiglu(float g, float u) {
 // occupancy instead.
 //
 // Fused step work around the linear (R = 1 only):
-//   NORM     x is RMS-normalised: y = scale * (W (x * w)) + b with scale =
-//            1 / sqrt(mean(x^2) + eps) (rms_norm, reference_executor.cpp:
-//            17-27, with the row's one scale factored out of the dot
-//            products).  The double sum of squares accumulates from the x
-//            each wave loads for its chunks, so the norm costs no pass of
-//            its own and no barrier before the first MFMA;
+//   NORM     x is RMS-normalised first: scale = 1 / sqrt(mean(x^2) + eps)
+//            from a double sum of squares over the whole row (every
+//            workgroup reduces it, each wave a slice), then x * scale * w;
 //   EPI = 0  y = W x + b;  1  y += W x + b (the residual stream);
 //   EPI = 2  SwiGLU over a fused gate|up matrix (N = 2F): the workgroup
 //            owns gate tile t (waves [0, W/2)) and up tile t + NT/2 (waves
@@ -366,12 +377,25 @@ decode_gemv_kernel(const void* __restrict__ codes_, const void* __restrict__ sca
 
     Ch a, b;
 
-    double ss = 0.0;   // NORM: this lane's share of the row's sum of squares
+    float norm_scale = 1.0f;
+    if constexpr (NORM) {
+        __shared__ double norm_red[16];
+        double ss = 0.0;
+        for (std::uint64_t i = threadIdx.x; i < K / 4u; i += blockDim.x) {
+            ss = square_sum4(ss, reinterpret_cast<const float4*>(x)[i]);
+        }
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+        if (lane == 0u) norm_red[wave] = ss;
+        __syncthreads();
+        double total = 0.0;
+        for (std::uint32_t w = 0; w < W; ++w) total += norm_red[w];
+        norm_scale = static_cast<float>(1.0 / sqrt(total / static_cast<double>(K) + eps));
+    }
 
     if constexpr (P == 1) {
         for (std::uint32_t c = c_begin; c < c_end; ++c) {
             load_chunk<FMT, R, U, NORM>(a, codes_, scales_, rt0, NT, KT, c, lane, x, norm_w, nblocks);
-            compute_chunk<FMT, R, U, NORM>(a, c, lane, ss, acc);
+            compute_chunk<FMT, R, U, NORM>(a, c, lane, norm_scale, acc);
         }
     } else {
         if (c_begin < c_end) {
@@ -381,12 +405,12 @@ decode_gemv_kernel(const void* __restrict__ codes_, const void* __restrict__ sca
             if (c + 1u < c_end) {
                 load_chunk<FMT, R, U, NORM>(b, codes_, scales_, rt0, NT, KT, c + 1u, lane, x, norm_w, nblocks);
             }
-            compute_chunk<FMT, R, U, NORM>(a, c, lane, ss, acc);
+            compute_chunk<FMT, R, U, NORM>(a, c, lane, norm_scale, acc);
             if (c + 1u >= c_end) break;
             if (c + 2u < c_end) {
                 load_chunk<FMT, R, U, NORM>(a, codes_, scales_, rt0, NT, KT, c + 2u, lane, x, norm_w, nblocks);
             }
-            compute_chunk<FMT, R, U, NORM>(b, c + 1u, lane, ss, acc);
+            compute_chunk<FMT, R, U, NORM>(b, c + 1u, lane, norm_scale, acc);
         }
     }
 
@@ -399,27 +423,13 @@ decode_gemv_kernel(const void* __restrict__ codes_, const void* __restrict__ sca
         t += __shfl_xor(t, 32);
         total[r] = t;
     }
-    // NORM: the waves of one row tile (the gate half for EPI 2) together saw
-    // every element of x once.
-    __shared__ double norm_red[NORM ? 16 : 1];
-    if constexpr (NORM) {
-        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-    }
     float up_total = 0.0f;   // EPI 2: the up tile's sum
     if (W > 1u) {
         if (wave > 0u && lane < 16u) {
 #pragma unroll
             for (int r = 0; r < R; ++r) wave_sums[((wave - 1u) * R + r) * 16u + lane] = total[r];
         }
-        if constexpr (NORM) {
-            if (wave > 0u && lane == 0u) norm_red[wave] = ss;
-        }
         __syncthreads();
-        if constexpr (NORM) {
-            if (wave == 0u) {
-                for (std::uint32_t w = 1; w < group_waves; ++w) ss += norm_red[w];
-            }
-        }
         if (wave == 0u && lane < 16u) {
             if constexpr (EPI == 2) {
                 for (std::uint32_t w = 1; w < group_waves; ++w) total[0] += wave_sums[(w - 1u) * 16u + lane];
@@ -434,15 +444,6 @@ decode_gemv_kernel(const void* __restrict__ codes_, const void* __restrict__ sca
         }
     }
     if (wave != 0u || lane >= 16u) return;
-    // NORM: the dot products ran on x * w; the norm's scale is one factor of
-    // the whole row, applied to the totals.
-    float norm_scale = 1.0f;
-    if constexpr (NORM) norm_scale = static_cast<float>(1.0 / sqrt(ss / static_cast<double>(K) + eps));
-    if constexpr (NORM) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) total[r] *= norm_scale;
-        up_total *= norm_scale;
-    }
     if constexpr (EPI == 2) {
         const std::uint64_t F = N / 2u;
         const std::uint64_t n = static_cast<std::uint64_t>(blockIdx.x) * 16u + lane;
