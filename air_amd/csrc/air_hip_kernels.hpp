@@ -276,7 +276,11 @@ bool split_epilogue_fits(const SplitEpilogue& e, const float* partials, const fl
 hipError_t launch_split_epilogue(const float* partials, std::uint32_t splits, std::uint32_t m, std::uint64_t n,
                                  const float* bias, const SplitEpilogue& e, hipStream_t stream);
 hipError_t launch_add(float* x, const float* y, std::uint64_t count, hipStream_t stream);
-hipError_t launch_argmax(const float* logits, std::uint32_t m, std::uint64_t n, std::int32_t* out, hipStream_t stream);
+// Greedy selection in two passes (slices of a row, then each row's slices);
+// scratch holds argmax_scratch_bytes(m, n) bytes.
+std::uint64_t argmax_scratch_bytes(std::uint32_t m, std::uint64_t n);
+hipError_t launch_argmax(const float* logits, std::uint32_t m, std::uint64_t n, std::int32_t* out, void* scratch,
+                         hipStream_t stream);
 
 // Sets planes.prefill_scale / prefill_unscale from the largest dequantized
 // magnitude of the resident matrix (synchronous; `bound_scratch` is one

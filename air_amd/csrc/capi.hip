@@ -74,6 +74,8 @@ struct air_hip_context {
     std::uint32_t skinny_lds_stages{0};   // 0 automatic, 1 registers, 2..4 LDS ring stages
     std::uint32_t* bound_scratch{nullptr};  // one uint32 for the weight exponent at residency
     void* attention_scratch{nullptr};       // attention scores, grown on demand
+    void* argmax_partials{nullptr};         // per-slice partials of the greedy selection
+    std::uint64_t argmax_partials_bytes{0};
     std::uint64_t attention_scratch_bytes{0};
     void* epilogue_rows{nullptr};           // linear output of air_hip_linear_epilogue's unfused route
     std::uint64_t epilogue_rows_bytes{0};
@@ -413,6 +415,7 @@ int air_hip_context_destroy(air_hip_context* ctx) {
         if (ctx->prefill_workspace) (void)hipFree(ctx->prefill_workspace);
         if (ctx->bound_scratch) (void)hipFree(ctx->bound_scratch);
         if (ctx->attention_scratch) (void)hipFree(ctx->attention_scratch);
+        if (ctx->argmax_partials) (void)hipFree(ctx->argmax_partials);
         if (ctx->epilogue_rows) (void)hipFree(ctx->epilogue_rows);
         for (void* p : ctx->retired) (void)hipFree(p);
     }
@@ -1334,10 +1337,16 @@ int air_hip_argmax(air_hip_context* ctx, const float* logits, uint32_t m, uint64
     forget_loaded_source(ctx);
     if (n == 0 || n > 0x7fffffffu) return fail(AIR_HIP_INVALID_ARGUMENT, "row width must be in [1, 2^31)");
     if (m == 0) return AIR_HIP_OK;
+    if (m > 65535u) return fail(AIR_HIP_UNSUPPORTED, "at most 65535 rows per call");
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-    const hipError_t err = launch_argmax(logits, m, n, out, ctx->stream);
-    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "argmax_kernel");
+    if (int rc = grow_buffer(ctx, &ctx->argmax_partials, &ctx->argmax_partials_bytes, argmax_scratch_bytes(m, n),
+                             "argmax partials");
+        rc != AIR_HIP_OK) {
+        return rc;
+    }
+    const hipError_t err = launch_argmax(logits, m, n, out, ctx->argmax_partials, ctx->stream);
+    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "argmax_slice_kernel");
 }
 
 } // extern "C"

@@ -378,7 +378,8 @@ __global__ __launch_bounds__(kThreads) void add_kernel(float* __restrict__ x, co
 // value (NaN or +-inf) gives -1 instead of an index: the reference CUDA
 // executor flags such a value and fails the step
 // (src/cuda/cuda_backend.cu:613-624, 2368).
-constexpr unsigned kArgmaxThreads = 1024;
+constexpr unsigned kArgmaxThreads = 256;
+constexpr unsigned kArgmaxSlice = 4096;   // logits per workgroup of the first pass
 
 // Merges a candidate (value, index) into the running best.
 __device__ __forceinline__ void argmax_merge(float v, std::uint32_t i, float& bv, std::uint32_t& bi) {
@@ -397,43 +398,54 @@ __device__ __forceinline__ void argmax_take(float v, std::uint32_t i, float& bv,
     argmax_merge(v, i, bv, bi);
 }
 
-__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ logits, std::uint64_t n,
-                                                                std::int32_t* __restrict__ out) {
+// The selection rule does not depend on the visiting order, so a row is cut
+// into slices of kArgmaxSlice logits, each reduced by its own workgroup to
+// (best value, its index, any non-finite) -- partial (row, slice) -- and a
+// second pass merges a row's slices.
+struct ArgmaxPartial {
+    float value;
+    std::uint32_t index;
+    std::uint32_t bad;
+    std::uint32_t pad;
+};
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_slice_kernel(const float* __restrict__ logits,
+                                                                      std::uint64_t n, std::uint32_t slices,
+                                                                      ArgmaxPartial* __restrict__ partials) {
     __shared__ float wave_v[kArgmaxThreads / 64];
     __shared__ std::uint32_t wave_i[kArgmaxThreads / 64];
     __shared__ std::uint32_t wave_bad[kArgmaxThreads / 64];
-    const float* row = logits + static_cast<std::uint64_t>(blockIdx.x) * n;
+    const std::uint32_t slice = blockIdx.x, r = blockIdx.y;
+    const float* row = logits + static_cast<std::uint64_t>(r) * n;
+    const std::uint64_t begin = static_cast<std::uint64_t>(slice) * kArgmaxSlice;
+    const std::uint64_t end = begin + kArgmaxSlice < n ? begin + kArgmaxSlice : n;
     float bv = -__builtin_huge_valf();
     std::uint32_t bi = 0xffffffffu;
     bool bad = false;
     const bool vec = (n % 4u == 0) && (reinterpret_cast<std::uintptr_t>(row) % 16u == 0);
     if (vec) {
-        // Coalesced float4 loads, four in flight per thread (the selection
-        // rule does not depend on the visiting order).
-        const std::uint64_t n4 = n / 4u;
-        for (std::uint64_t first = threadIdx.x; first < n4; first += 4u * kArgmaxThreads) {
-            float4 v[4];
+        // Four float4 per thread, all loads issued before the first compare.
+        constexpr unsigned kPer = kArgmaxSlice / 4u / kArgmaxThreads;
+        float4 v[kPer];
 #pragma unroll
-            for (unsigned j = 0; j < 4; ++j) {
-                const std::uint64_t i = first + j * kArgmaxThreads;
-                v[j] = i < n4 ? *reinterpret_cast<const float4*>(row + 4u * i)
-                              : make_float4(-__builtin_huge_valf(), -__builtin_huge_valf(), -__builtin_huge_valf(),
-                                            -__builtin_huge_valf());
-            }
+        for (unsigned j = 0; j < kPer; ++j) {
+            const std::uint64_t e = begin + 4u * (threadIdx.x + j * kArgmaxThreads);
+            v[j] = e < end ? *reinterpret_cast<const float4*>(row + e)
+                           : make_float4(-__builtin_huge_valf(), -__builtin_huge_valf(), -__builtin_huge_valf(),
+                                         -__builtin_huge_valf());
+        }
 #pragma unroll
-            for (unsigned j = 0; j < 4; ++j) {
-                const std::uint64_t i = first + j * kArgmaxThreads;
-                if (i >= n4) continue;
-                const std::uint32_t base = static_cast<std::uint32_t>(4u * i);
-                argmax_take(v[j].x, base, bv, bi, bad);
-                argmax_take(v[j].y, base + 1u, bv, bi, bad);
-                argmax_take(v[j].z, base + 2u, bv, bi, bad);
-                argmax_take(v[j].w, base + 3u, bv, bi, bad);
-            }
+        for (unsigned j = 0; j < kPer; ++j) {
+            const std::uint64_t e = begin + 4u * (threadIdx.x + j * kArgmaxThreads);
+            if (e >= end) continue;
+            const std::uint32_t base = static_cast<std::uint32_t>(e);
+            argmax_take(v[j].x, base, bv, bi, bad);
+            argmax_take(v[j].y, base + 1u, bv, bi, bad);
+            argmax_take(v[j].z, base + 2u, bv, bi, bad);
+            argmax_take(v[j].w, base + 3u, bv, bi, bad);
         }
     } else {
-#pragma unroll 8
-        for (std::uint64_t i = threadIdx.x; i < n; i += kArgmaxThreads) {
+        for (std::uint64_t i = begin + threadIdx.x; i < end; i += kArgmaxThreads) {
             argmax_take(row[i], static_cast<std::uint32_t>(i), bv, bi, bad);
         }
     }
@@ -457,10 +469,31 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
             argmax_merge(wave_v[w], wave_i[w], bv, bi);
             any_bad |= wave_bad[w];
         }
-        // n >= 1 finite values always select an index; an empty selection
-        // means every value was non-finite, which any_bad already records.
-        out[blockIdx.x] = any_bad != 0u ? -1 : static_cast<std::int32_t>(bi);
+        partials[static_cast<std::uint64_t>(r) * slices + slice] = ArgmaxPartial{bv, bi, any_bad, 0u};
     }
+}
+
+// One wave per row merges its slices' partials.  n >= 1 finite values always
+// select an index; an empty selection means every value was non-finite,
+// which the flag already records.
+__global__ __launch_bounds__(64) void argmax_rows_kernel(const ArgmaxPartial* __restrict__ partials,
+                                                         std::uint32_t slices, std::int32_t* __restrict__ out) {
+    const std::uint32_t r = blockIdx.x;
+    float bv = -__builtin_huge_valf();
+    std::uint32_t bi = 0xffffffffu;
+    bool bad = false;
+    for (std::uint32_t s = threadIdx.x; s < slices; s += 64u) {
+        const ArgmaxPartial p = partials[static_cast<std::uint64_t>(r) * slices + s];
+        bad = bad || p.bad != 0u;
+        argmax_merge(p.value, p.index, bv, bi);
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const std::uint32_t oi = __shfl_xor(bi, off);
+        argmax_merge(ov, oi, bv, bi);
+    }
+    const bool any_bad = __any(bad ? 1 : 0) != 0;
+    if (threadIdx.x == 0) out[r] = any_bad ? -1 : static_cast<std::int32_t>(bi);
 }
 
 // RMSNorm of rows of n <= 8 * kNormThreads floats (n % 8 == 0), thread t
@@ -797,8 +830,19 @@ hipError_t launch_split_epilogue(const float* partials, std::uint32_t splits, st
     return hipGetLastError();
 }
 
-hipError_t launch_argmax(const float* logits, std::uint32_t m, std::uint64_t n, std::int32_t* out, hipStream_t stream) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(m), dim3(kArgmaxThreads), 0, stream, logits, n, out);
+std::uint64_t argmax_scratch_bytes(std::uint32_t m, std::uint64_t n) {
+    return static_cast<std::uint64_t>(m) * ceil_div(n, kArgmaxSlice) * sizeof(ArgmaxPartial);
+}
+
+hipError_t launch_argmax(const float* logits, std::uint32_t m, std::uint64_t n, std::int32_t* out, void* scratch,
+                         hipStream_t stream) {
+    const std::uint64_t slices = ceil_div(n, kArgmaxSlice);
+    if (m == 0u || slices == 0u || slices > 0x7fffffffu || m > 65535u) return hipErrorInvalidValue;
+    auto* partials = static_cast<ArgmaxPartial*>(scratch);
+    hipLaunchKernelGGL(argmax_slice_kernel, dim3(static_cast<unsigned>(slices), m), dim3(kArgmaxThreads), 0, stream,
+                       logits, n, static_cast<std::uint32_t>(slices), partials);
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3(m), dim3(64), 0, stream, partials,
+                       static_cast<std::uint32_t>(slices), out);
     return hipGetLastError();
 }
 

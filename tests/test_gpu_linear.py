@@ -478,21 +478,25 @@ def test_argmax_flags_non_finite_rows(torch_cuda, hip_ctx):
     equal values, sampling.cpp:13-16), and -1 for a row holding NaN or
     +-inf anywhere -- the reference refuses such logits
     (cuda_backend.cu:613-624, 2368).  Both the vectorised and the scalar
-    row paths."""
+    row paths; ties within one 4096-logit slice of the first pass and
+    across slices."""
     torch = torch_cuda
     lib = capi.lib()
     for n in (152064, 1001):                          # float4 rows, and an odd width (scalar loop)
         rng = np.random.default_rng(n)
-        rows = rng.standard_normal((7, n)).astype(np.float32)
+        rows = rng.standard_normal((9, n)).astype(np.float32)
         rows[1, 5] = np.nan
         rows[2, n - 1] = np.inf
         rows[3, n // 2] = -np.inf
         rows[4, :] = np.nan
         rows[5, [11, 700]] = 50.0                     # a tie: the lower index wins
         rows[6, 0] = 50.0
+        far = [5000, 130000] if n > 130000 else [500, 900]
+        rows[7, far] = 60.0                           # a tie across slices
+        rows[8, n - 1] = 70.0                         # the maximum in the last (partial) slice
         x = _dev(torch, rows)
-        out = torch.full((7,), 12345, dtype=torch.int32, device="cuda:0")
-        capi.check(lib.air_hip_argmax(hip_ctx.handle, x.data_ptr(), 7, n, out.data_ptr()))
+        out = torch.full((9,), 12345, dtype=torch.int32, device="cuda:0")
+        capi.check(lib.air_hip_argmax(hip_ctx.handle, x.data_ptr(), 9, n, out.data_ptr()))
         torch.cuda.synchronize()
         got = out.cpu().numpy().tolist()
-        assert got == [int(np.argmax(rows[0])), -1, -1, -1, -1, 11, 0], (n, got)
+        assert got == [int(np.argmax(rows[0])), -1, -1, -1, -1, 11, 0, far[0], n - 1], (n, got)
