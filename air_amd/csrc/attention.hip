@@ -22,6 +22,7 @@
 // unfused-exact products are not required: the result differs from the
 // reference's double softmax by ~1e-6 relative (the tactic's tolerance is
 // that of the linears).
+#include "air_hip_device.hpp"
 #include "air_hip_kernels.hpp"
 #include "air_hip_kv.hpp"
 #include "air_hip_layout.hpp"
@@ -255,6 +256,252 @@ __global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
     }
 }
 
+// The 64-key chunk steps on the f32 matrix cores (v_mfma_f32_16x16x4_f32:
+// fp32 products summed in fp32, the VALU kernel's precision).  Wave w owns
+// keys 16w .. 16w + 15 of every chunk and keeps its own online softmax over
+// them; the four waves' (m, l, acc) merge once at the end.  Per chunk:
+//
+//   S^T = K Q^T   A = 16 keys x 4 dims, B = 4 dims x 16 query vectors: D
+//                 leaves lane l with the scores of vector l % 16 for keys
+//                 4 (l / 16) + r -- its own row of S, so the softmax needs
+//                 two lane swaps and no LDS;
+//   O  += P V     P enters as the A operand as it lies: in MFMA step j lane
+//                 group g supplies key 4 g + j (the sum over keys is the
+//                 same in any order), and B takes V's rows in that order.
+//
+// The reduction dimensions are laid out for 16-byte LDS reads: in S^T lane
+// group g covers dims [g D / 4, (g + 1) D / 4) (step s: dim g D / 4 + s),
+// and the output column n of PV tile t is dim n D / 16 + t.  Q's operand
+// values are loaded once per tile into registers.
+template <unsigned D>
+__global__ __launch_bounds__(kAttnThreads) void attention_mfma_kernel(
+    KvGeometry g, const float* __restrict__ qkv, std::uint64_t stride, std::uint32_t m,
+    const std::int32_t* __restrict__ positions,
+    const std::int32_t* __restrict__ tables, std::uint32_t layer, std::uint32_t q_heads, std::uint32_t kv_heads,
+    const AttentionTile* __restrict__ tiles, std::uint32_t splits, float scale, float* __restrict__ partials,
+    float* __restrict__ out) {
+    constexpr unsigned kChunk = 64;           // keys per stage, 16 per wave
+    constexpr unsigned LD = D + 4;            // padded LDS row (floats), keeps float4 alignment
+    constexpr unsigned D4 = D / 4;
+    constexpr unsigned kQuarter = D / 4;      // dims per lane group in S^T
+    constexpr unsigned kDT = D / 16;          // 16-column tiles of the output
+    __shared__ float qs[kTileVectors][LD];
+    __shared__ float ks[kChunk][LD];
+    __shared__ float vs[kChunk][LD];
+    __shared__ std::int64_t slot_off[2][kChunk];
+    __shared__ float wave_m[4][kTileVectors];
+    __shared__ float wave_l[4][kTileVectors];
+
+    const AttentionTile tile = tiles[blockIdx.x];
+    if (!tile_ok(tile, m, q_heads, kv_heads)) return;
+    const std::uint32_t split = blockIdx.y;
+    const unsigned tid = threadIdx.x;
+    const unsigned lane = tid & 63u;
+    const unsigned wave = tid >> 6;
+    const unsigned grp = lane >> 4;           // lane group
+    const unsigned col = lane & 15u;          // query vector of this lane's S column
+    const unsigned nq = tile.rows * tile.heads;
+    const std::uint32_t kvh = static_cast<std::uint32_t>((static_cast<std::uint64_t>(tile.head) * kv_heads) / q_heads);
+    const std::int32_t* table = tables + static_cast<std::uint64_t>(tile.row) * g.max_pages;
+
+    const auto resolve = [&](std::uint32_t c, unsigned buf) __attribute__((always_inline)) {
+        if (tid < kChunk) {   // page table lookup, once per token
+            const std::uint64_t token = static_cast<std::uint64_t>(c) * kChunk + tid;
+            const float* kp = kv_slot(g, table, layer, token, false);
+            slot_off[buf][tid] = kp ? kp - g.pool : -1;
+        }
+    };
+    resolve(split, 0u);
+
+    std::int64_t tmax = 0;
+    for (unsigned r = 0; r < tile.rows; ++r) {
+        const std::int64_t p = positions[tile.row + r];
+        tmax = p + 1 > tmax ? p + 1 : tmax;
+    }
+    const std::uint32_t chunks = static_cast<std::uint32_t>((tmax + kChunk - 1) / kChunk);
+    const std::uint32_t live = chunks < splits ? chunks : splits;
+    if (split >= live) return;
+
+    const bool col_active = col < nq;
+    const std::int64_t col_pos = col_active ? positions[tile.row + col / tile.heads] : -1;
+
+    for (unsigned idx = tid; idx < kTileVectors * D4; idx += kAttnThreads) {
+        const unsigned v = idx / D4, d4 = idx % D4;
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (v < nq) {
+            const unsigned row = tile.row + v / tile.heads, head = tile.head + v % tile.heads;
+            x = load4(qkv + static_cast<std::uint64_t>(row) * stride + static_cast<std::uint64_t>(head) * D + 4u * d4);
+        }
+        *reinterpret_cast<float4*>(&qs[v][4u * d4]) = x;
+    }
+
+    float mx = -__builtin_huge_valf();   // running maximum of vector `col`'s scores (this wave's keys)
+    float lsum = 0.0f;
+    float4v o[kDT];
+#pragma unroll
+    for (unsigned t = 0; t < kDT; ++t) o[t] = float4v{0.f, 0.f, 0.f, 0.f};
+
+    const std::uint64_t v_after_k = static_cast<std::uint64_t>(g.page_tokens) * g.kv_width;
+    constexpr unsigned kIters = kChunk * D4 / kAttnThreads;
+    float4 kr[kIters], vr[kIters];
+    const auto fetch = [&](unsigned buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (unsigned it = 0; it < kIters; ++it) {
+            const unsigned idx = tid + it * kAttnThreads;
+            const unsigned t = idx / D4, d4 = idx % D4;
+            const std::int64_t off = slot_off[buf][t];
+            kr[it] = make_float4(0.f, 0.f, 0.f, 0.f);
+            vr[it] = kr[it];
+            if (off >= 0) {
+                const float* kp = g.pool + off + static_cast<std::uint64_t>(kvh) * D + 4u * d4;
+                kr[it] = load4(kp);
+                vr[it] = load4(kp + v_after_k);
+            }
+        }
+    };
+    __syncthreads();
+    fetch(0u);
+    // This lane's B operands of S^T: vector col, dims grp * D / 4 .. + D / 4.
+    float4 qf[kQuarter / 4];
+#pragma unroll
+    for (unsigned i = 0; i < kQuarter / 4; ++i) qf[i] = *reinterpret_cast<const float4*>(&qs[col][grp * kQuarter + 4u * i]);
+
+    unsigned buf = 0u;
+    for (std::uint32_t c = split; c < chunks; c += splits, buf ^= 1u) {
+        const std::int64_t c0 = static_cast<std::int64_t>(c) * kChunk;
+        const std::uint32_t next = c + splits;
+        __syncthreads();  // previous chunk's K and V are consumed
+#pragma unroll
+        for (unsigned it = 0; it < kIters; ++it) {
+            const unsigned idx = tid + it * kAttnThreads;
+            const unsigned t = idx / D4, d4 = idx % D4;
+            *reinterpret_cast<float4*>(&ks[t][4u * d4]) = kr[it];
+            *reinterpret_cast<float4*>(&vs[t][4u * d4]) = vr[it];
+        }
+        if (next < chunks) resolve(next, buf ^ 1u);
+        __syncthreads();
+        if (next < chunks) fetch(buf ^ 1u);   // in flight while chunk c computes
+
+        // S^T for keys 16 wave .. + 15: lane (col, grp) ends with keys 4 grp + r.
+        const float* krow = &ks[wave * 16u + col][grp * kQuarter];
+        float4v st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (unsigned i = 0; i < kQuarter / 4; ++i) {
+            const float4 a = *reinterpret_cast<const float4*>(krow + 4u * i);
+            st = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, qf[i].x, st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, qf[i].y, st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, qf[i].z, st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, qf[i].w, st, 0, 0, 0);
+        }
+        // Online softmax of vector col over its four keys here (lane groups
+        // hold the wave's other twelve).
+        float sv[4];
+        float cmax = -__builtin_huge_valf();
+#pragma unroll
+        for (unsigned r = 0; r < 4; ++r) {
+            const std::int64_t key = c0 + wave * 16u + 4u * grp + r;
+            sv[r] = col_active && key <= col_pos ? st[r] * scale : -__builtin_huge_valf();
+            cmax = sv[r] > cmax ? sv[r] : cmax;
+        }
+        {
+            float o1 = __shfl_xor(cmax, 16);
+            cmax = o1 > cmax ? o1 : cmax;
+            o1 = __shfl_xor(cmax, 32);
+            cmax = o1 > cmax ? o1 : cmax;
+        }
+        const float m_new = cmax > mx ? cmax : mx;
+        const bool none = m_new == -__builtin_huge_valf();
+        const float alpha = none ? 1.0f : __expf(mx - m_new);
+        float pv[4];
+        float rs = 0.0f;
+#pragma unroll
+        for (unsigned r = 0; r < 4; ++r) {
+            pv[r] = none || sv[r] == -__builtin_huge_valf() ? 0.0f : __expf(sv[r] - m_new);
+            rs += pv[r];
+        }
+        rs += __shfl_xor(rs, 16);
+        rs += __shfl_xor(rs, 32);
+        lsum = lsum * alpha + rs;
+        mx = m_new;
+        // The output rows of this lane are vectors 4 grp + r: their alphas.
+#pragma unroll
+        for (unsigned r = 0; r < 4; ++r) {
+            const float ar = __shfl(alpha, 4 * grp + r);
+#pragma unroll
+            for (unsigned t = 0; t < kDT; ++t) o[t][r] *= ar;
+        }
+        // O += P V: step j takes key 4 grp + j from lane group grp.
+#pragma unroll
+        for (unsigned j = 0; j < 4; ++j) {
+            const float* vrow = &vs[wave * 16u + 4u * grp + j][col * kDT];
+            float vb[kDT];
+#pragma unroll
+            for (unsigned t = 0; t < kDT; t += 4) {
+                const float4 v4 = *reinterpret_cast<const float4*>(vrow + t);
+                vb[t] = v4.x;
+                vb[t + 1] = v4.y;
+                vb[t + 2] = v4.z;
+                vb[t + 3] = v4.w;
+            }
+#pragma unroll
+            for (unsigned t = 0; t < kDT; ++t) o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[j], vb[t], o[t], 0, 0, 0);
+        }
+    }
+
+    // Merge the four waves: per vector M = max m_w, e_w = e^(m_w - M),
+    // L = sum e_w l_w, O = sum e_w O_w.  The waves' O go through ks
+    // ([w * 16 + vector][dim], the K stage is free after the last chunk).
+    __syncthreads();
+    if (grp == 0u) {
+        wave_m[wave][col] = mx;
+        wave_l[wave][col] = lsum;
+    }
+#pragma unroll
+    for (unsigned t = 0; t < kDT; ++t) {
+#pragma unroll
+        for (unsigned r = 0; r < 4; ++r) ks[wave * 16u + 4u * grp + r][col * kDT + t] = o[t][r];
+    }
+    __syncthreads();
+    for (unsigned idx = tid; idx < nq * D4; idx += kAttnThreads) {
+        const unsigned v = idx / D4, d4 = idx % D4;
+        float mw[4], big = -__builtin_huge_valf();
+#pragma unroll
+        for (unsigned w = 0; w < 4; ++w) {
+            mw[w] = wave_m[w][v];
+            big = mw[w] > big ? mw[w] : big;
+        }
+        float lt = 0.0f;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (unsigned w = 0; w < 4; ++w) {
+            const float e = mw[w] == -__builtin_huge_valf() ? 0.0f : __expf(mw[w] - big);
+            lt += e * wave_l[w][v];
+            const float4 a = *reinterpret_cast<const float4*>(&ks[w * 16u + v][4u * d4]);
+            acc.x += e * a.x;
+            acc.y += e * a.y;
+            acc.z += e * a.z;
+            acc.w += e * a.w;
+        }
+        const unsigned row = tile.row + v / tile.heads, head = tile.head + v % tile.heads;
+        // ks holds dims in the PV column order: column n of tile t is dim
+        // n * kDT + t, i.e. LDS column c is dim c (n * kDT + t = c).
+        if (live == 1u) {
+            const float inv = 1.0f / lt;
+            *reinterpret_cast<float4*>(out + static_cast<std::uint64_t>(row) * q_heads * D +
+                                       static_cast<std::uint64_t>(head) * D + 4u * d4) =
+                make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+        } else {
+            float* part = partials + ((static_cast<std::uint64_t>(blockIdx.x) * splits + split) * kTileVectors + v) *
+                                         (D + 4u);
+            if (d4 == 0u) {
+                part[0] = big;
+                part[1] = lt;
+            }
+            *reinterpret_cast<float4*>(part + 4u + 4u * d4) = acc;
+        }
+    }
+}
+
 // Merges the live splits of each tile (those holding a chunk at or before
 // the tile's last position): o = sum_s acc_s e^(m_s - M) / sum_s l_s
 // e^(m_s - M), accumulated with a running M.  The positions and the first
@@ -391,18 +638,22 @@ hipError_t launch_attention_tiles(const KvLayout& kv, const float* qkv, std::uin
 #define AIR_ATTENTION_MERGE(D)                                                                                   \
     hipLaunchKernelGGL(attention_merge_kernel<D>, dim3(tile_count), dim3(kAttnThreads), 0, stream, tiles, splits, \
                        chunk, m, q_heads, kv_heads, positions, partials, out)
+#define AIR_ATTENTION_MFMA(D)                                                                                    \
+    hipLaunchKernelGGL(attention_mfma_kernel<D>, grid, dim3(kAttnThreads), 0, stream, g, qkv, stride, m, positions, \
+                       tables, layer, q_heads, kv_heads, tiles, splits, scale, partials, out)
+    // 64-key chunks (steps of more than 64 rows) on the matrix cores.
     if (head_dim == 128u) {
         if (chunk == 32u) {
             AIR_ATTENTION_LAUNCH(128, 32);
         } else {
-            AIR_ATTENTION_LAUNCH(128, 64);
+            AIR_ATTENTION_MFMA(128);
         }
         if (splits > 1u) AIR_ATTENTION_MERGE(128);
     } else if (head_dim == 64u) {
         if (chunk == 32u) {
             AIR_ATTENTION_LAUNCH(64, 32);
         } else {
-            AIR_ATTENTION_LAUNCH(64, 64);
+            AIR_ATTENTION_MFMA(64);
         }
         if (splits > 1u) AIR_ATTENTION_MERGE(64);
     } else {
@@ -410,6 +661,7 @@ hipError_t launch_attention_tiles(const KvLayout& kv, const float* qkv, std::uin
     }
 #undef AIR_ATTENTION_LAUNCH
 #undef AIR_ATTENTION_MERGE
+#undef AIR_ATTENTION_MFMA
     return hipGetLastError();
 }
 

@@ -6,7 +6,8 @@ gpu: at Qwen2-7B head geometry (28 q heads, 4 KV heads of 128) and at the
      rows of many lengths with a 100-row prompt run: the online tactic equals
      the baseline (the reference executor's double softmax) within 1e-5
      relative, and both equal a float64 CPU attention computed from the same
-     pool.  Split tiles (few rows, long keys) go through the merge pass.
+     pool.  Split tiles (few rows, long keys) go through the merge pass;
+     steps of more than 64 rows take the f32 MFMA kernel.
 """
 import ctypes
 
@@ -59,6 +60,7 @@ def _reference(pool, tables, positions, qkv, layer, q_heads, kv_heads, head, pag
     (28, 4, 128, [1, 17, 64, 65, 300, 700], (50, 100)),   # split tiles, merge pass
     (28, 4, 128, [3], (0, 60)),                           # one key chunk: no split
     (4, 2, 64, [1, 2, 63, 129], (0, 37)),
+    (4, 2, 64, [1, 5, 300], (0, 90)),                     # over 64 rows: 64-key chunks on the matrix cores
 ])
 def test_online_matches_baseline(torch_cuda, hip_ctx, q_heads, kv_heads, head, decode_lengths, prompt):
     torch = torch_cuda
