@@ -6,22 +6,22 @@
 // time).  Here a workgroup owns a tile of up to 16 query vectors that share a
 // sequence and a KV head -- 16 consecutive prompt rows of one q head in a
 // prefill, or the grouped q heads of one KV head of a decode row -- and walks
-// the keys in chunks of 32 (decode) or 64 (prefill) tokens staged through LDS, so each K/V element is
-// read from memory once per tile instead of once per query vector:
+// the keys in chunks of 64 tokens staged through LDS, so each K/V element is
+// read from memory once per tile instead of once per query vector, with the
+// products on the f32 matrix cores (attention_mfma_kernel):
 //
-//   S = (q . k) * scale        16 x chunk, chunk / 16 dots per thread, float
+//   S = (q . k) * scale        16 vectors x 64 keys, 16 keys per wave
 //   m' = max(m, rowmax S);  p = exp(S - m');  l = l e^(m-m') + rowsum p
-//   acc = acc e^(m-m') + p . V 8 (D=128) or 4 (D=64) dims per thread
+//   acc = acc e^(m-m') + p . V
 //
 // Causality: row r attends tokens 0..positions[r].  Long key ranges with few
 // tiles are split over workgroups (flash-decoding); each split writes its
 // (m, l, acc) and a second kernel merges them.  (A merge by the tile's last
 // workgroup, found with an arrival counter, needs agent-scope fences around
 // the partials, which write back and invalidate L2 per workgroup: measured
-// slower than the second launch.)  All arithmetic is f32 and
-// unfused-exact products are not required: the result differs from the
-// reference's double softmax by ~1e-6 relative (the tactic's tolerance is
-// that of the linears).
+// slower than the second launch.)  All arithmetic is f32: the result differs
+// from the reference's double softmax by ~1e-6 relative (the tactic's
+// tolerance is that of the linears).
 #include "air_hip_device.hpp"
 #include "air_hip_kernels.hpp"
 #include "air_hip_kv.hpp"
@@ -31,10 +31,10 @@ namespace air_hip {
 namespace {
 
 constexpr unsigned kAttnThreads = 256;
-// Key tokens per LDS stage: 32 for decode-width steps (half the LDS of 64,
-// so three workgroups share a CU, and twice the key splits for short
-// grids), 64 for prefill tiles (half the barriers per key).
-std::uint32_t chunk_for(std::uint32_t m) { return m <= 64u ? 32u : 64u; }
+// Key tokens per LDS stage (16 per wave).  The VALU kernel this replaced
+// used 32 for decode widths; the matrix-core kernel at 64 is faster there
+// too (M = 1: 2.305 -> 2.252 ms per token; 32 rows 6.8k -> 6.9k tok/s).
+constexpr std::uint32_t kChunkKeys = 64;
 constexpr unsigned kTileVectors = 16;
 constexpr unsigned kMaxSplits = 64;  // bounds the partials of a tile
 
@@ -51,209 +51,6 @@ __device__ __forceinline__ bool tile_ok(const AttentionTile& t, std::uint32_t m,
     if (t.row >= m || t.rows > m - t.row || t.head >= q_heads || t.heads > q_heads - t.head) return false;
     const std::uint32_t group = q_heads / kv_heads;
     return t.head / group == (t.head + t.heads - 1u) / group;
-}
-
-template <unsigned D, unsigned kChunk>
-__global__ __launch_bounds__(kAttnThreads) void attention_tile_kernel(
-    KvGeometry g, const float* __restrict__ qkv, std::uint64_t stride, std::uint32_t m,
-    const std::int32_t* __restrict__ positions,
-    const std::int32_t* __restrict__ tables, std::uint32_t layer, std::uint32_t q_heads, std::uint32_t kv_heads,
-    const AttentionTile* __restrict__ tiles, std::uint32_t splits, float scale, float* __restrict__ partials,
-    float* __restrict__ out) {
-    constexpr unsigned kTokJ = kChunk / 16;   // key tokens per thread in a chunk (16 lanes per query vector)
-    constexpr unsigned LD = D + 4;            // padded LDS row (floats), keeps float4 alignment
-    constexpr unsigned D4 = D / 4;
-    constexpr unsigned ACC = D / 16;          // output dims per thread
-    __shared__ float qs[kTileVectors][LD];
-    __shared__ float ks[kChunk][LD];
-    __shared__ float vs[kChunk][LD];
-    __shared__ float ps[kTileVectors][kChunk + 1];
-    __shared__ std::int64_t slot_off[2][kChunk];   // pool offset of each chunk token's K slot, -1 if absent
-
-    const AttentionTile tile = tiles[blockIdx.x];
-    if (!tile_ok(tile, m, q_heads, kv_heads)) return;
-    const std::uint32_t split = blockIdx.y;
-    const unsigned tid = threadIdx.x;
-    const unsigned qi = tid >> 4;             // query vector of this thread
-    const unsigned lane16 = tid & 15u;
-    const unsigned nq = tile.rows * tile.heads;
-    const std::uint32_t kvh = static_cast<std::uint32_t>((static_cast<std::uint64_t>(tile.head) * kv_heads) / q_heads);
-    const std::int32_t* table = tables + static_cast<std::uint64_t>(tile.row) * g.max_pages;
-
-    // Split s takes key chunks s, s + splits, s + 2 splits, ...: its first
-    // chunk is known before the positions are, so that chunk's page slots
-    // are looked up while they load.  Slots past a row's position are read
-    // and masked (their pages exist or read as absent).
-    const auto resolve = [&](std::uint32_t c, unsigned buf) __attribute__((always_inline)) {
-        if (tid < kChunk) {   // page table lookup, once per token
-            const std::uint64_t token = static_cast<std::uint64_t>(c) * kChunk + tid;
-            const float* kp = kv_slot(g, table, layer, token, false);
-            slot_off[buf][tid] = kp ? kp - g.pool : -1;
-        }
-    };
-    resolve(split, 0u);
-
-    // Keys of the tile: 0 .. max position + 1.  Splits holding no chunk of
-    // them leave at once (every workgroup of the tile agrees on `live`).
-    std::int64_t tmax = 0;
-    for (unsigned r = 0; r < tile.rows; ++r) {
-        const std::int64_t p = positions[tile.row + r];
-        tmax = p + 1 > tmax ? p + 1 : tmax;
-    }
-    const std::uint32_t chunks = static_cast<std::uint32_t>((tmax + kChunk - 1) / kChunk);
-    const std::uint32_t live = chunks < splits ? chunks : splits;   // splits with at least one chunk
-    if (split >= live) return;
-
-    // This thread's query vector: (row, head) and its position.
-    const bool active = qi < nq;
-    const unsigned q_row = tile.row + (active ? qi / tile.heads : 0u);
-    const unsigned q_head = tile.head + (active ? qi % tile.heads : 0u);
-    const std::int64_t q_pos = active ? positions[q_row] : -1;
-
-    for (unsigned idx = tid; idx < kTileVectors * D4; idx += kAttnThreads) {
-        const unsigned v = idx / D4, d4 = idx % D4;
-        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (v < nq) {
-            const unsigned row = tile.row + v / tile.heads, head = tile.head + v % tile.heads;
-            x = load4(qkv + static_cast<std::uint64_t>(row) * stride + static_cast<std::uint64_t>(head) * D + 4u * d4);
-        }
-        *reinterpret_cast<float4*>(&qs[v][4u * d4]) = x;
-    }
-
-    float mx = -__builtin_huge_valf();   // running maximum of the scores
-    float l = 0.0f;
-    float acc[ACC];
-#pragma unroll
-    for (unsigned i = 0; i < ACC; ++i) acc[i] = 0.0f;
-
-    // V of a token sits page_tokens * kv_width floats after its K in the page.
-    const std::uint64_t v_after_k = static_cast<std::uint64_t>(g.page_tokens) * g.kv_width;
-    constexpr unsigned kIters = kChunk * D4 / kAttnThreads;   // float4 of K (and of V) per thread per chunk
-    // Two-stage pipeline: chunk c + splits' page slots are resolved and its
-    // K and V loads issued into registers before chunk c is computed from LDS.
-    float4 kr[kIters], vr[kIters];
-    const auto fetch = [&](unsigned buf) __attribute__((always_inline)) {
-#pragma unroll
-        for (unsigned it = 0; it < kIters; ++it) {
-            const unsigned idx = tid + it * kAttnThreads;
-            const unsigned t = idx / D4, d4 = idx % D4;
-            const std::int64_t off = slot_off[buf][t];
-            kr[it] = make_float4(0.f, 0.f, 0.f, 0.f);
-            vr[it] = kr[it];
-            if (off >= 0) {
-                const float* kp = g.pool + off + static_cast<std::uint64_t>(kvh) * D + 4u * d4;
-                kr[it] = load4(kp);
-                vr[it] = load4(kp + v_after_k);
-            }
-        }
-    };
-    __syncthreads();
-    fetch(0u);
-    unsigned buf = 0u;
-    for (std::uint32_t c = split; c < chunks; c += splits, buf ^= 1u) {
-        const std::int64_t c0 = static_cast<std::int64_t>(c) * kChunk;
-        const std::uint32_t next = c + splits;
-        __syncthreads();  // previous chunk's K, V and P are consumed
-#pragma unroll
-        for (unsigned it = 0; it < kIters; ++it) {
-            const unsigned idx = tid + it * kAttnThreads;
-            const unsigned t = idx / D4, d4 = idx % D4;
-            *reinterpret_cast<float4*>(&ks[t][4u * d4]) = kr[it];
-            *reinterpret_cast<float4*>(&vs[t][4u * d4]) = vr[it];
-        }
-        if (next < chunks) resolve(next, buf ^ 1u);
-        __syncthreads();
-        if (next < chunks) fetch(buf ^ 1u);   // in flight while chunk c computes
-
-        // Scores of tokens lane16 + 16 j.  Idle vector slots (a decode tile
-        // of 7 grouped heads leaves 9 of 16) skip the LDS reads: whole waves
-        // of them branch around the loop.
-        float s[kTokJ];
-#pragma unroll
-        for (unsigned j = 0; j < kTokJ; ++j) s[j] = 0.0f;
-        if (active) {
-#pragma unroll 4
-            for (unsigned d4 = 0; d4 < D4; ++d4) {
-                const float4 q4 = *reinterpret_cast<const float4*>(&qs[qi][4u * d4]);
-#pragma unroll
-                for (unsigned j = 0; j < kTokJ; ++j) {
-                    const float4 k4 = *reinterpret_cast<const float4*>(&ks[lane16 + 16u * j][4u * d4]);
-                    s[j] += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
-                }
-            }
-        }
-        float row_max = -__builtin_huge_valf();
-#pragma unroll
-        for (unsigned j = 0; j < kTokJ; ++j) {
-            const std::int64_t token = c0 + lane16 + 16u * j;
-            const bool valid = active && token <= q_pos;
-            s[j] = valid ? s[j] * scale : -__builtin_huge_valf();
-            row_max = s[j] > row_max ? s[j] : row_max;
-        }
-        // The 16 threads of one query vector are lanes 16q..16q+15 of a wave.
-#pragma unroll
-        for (int off = 8; off > 0; off >>= 1) {
-            const float o = __shfl_xor(row_max, off, 16);
-            row_max = o > row_max ? o : row_max;
-        }
-        const float m_new = row_max > mx ? row_max : mx;
-        const bool none = m_new == -__builtin_huge_valf();   // no key of this vector yet
-        const float alpha = none ? 1.0f : __expf(mx - m_new);
-        float row_sum = 0.0f;
-#pragma unroll
-        for (unsigned j = 0; j < kTokJ; ++j) {
-            const float p = none || s[j] == -__builtin_huge_valf() ? 0.0f : __expf(s[j] - m_new);
-            row_sum += p;
-            ps[qi][lane16 + 16u * j] = p;
-        }
-#pragma unroll
-        for (int off = 8; off > 0; off >>= 1) row_sum += __shfl_xor(row_sum, off, 16);
-        l = l * alpha + row_sum;
-        mx = m_new;
-#pragma unroll
-        for (unsigned i = 0; i < ACC; ++i) acc[i] *= alpha;
-        __syncthreads();
-
-        // acc[dims 4 (lane16 + 16 j) ..] += sum over tokens of p * v.
-        const std::int64_t last = q_pos - c0;            // tokens past it have p = 0
-        const unsigned count = last < 0 ? 0u : (last >= kChunk ? kChunk : static_cast<unsigned>(last) + 1u);
-        for (unsigned t = 0; t < count; ++t) {
-            const float p = ps[qi][t];
-#pragma unroll
-            for (unsigned j = 0; j < ACC / 4; ++j) {
-                const float4 v4 = *reinterpret_cast<const float4*>(&vs[t][4u * (lane16 + 16u * j)]);
-                acc[4 * j + 0] += p * v4.x;
-                acc[4 * j + 1] += p * v4.y;
-                acc[4 * j + 2] += p * v4.z;
-                acc[4 * j + 3] += p * v4.w;
-            }
-        }
-    }
-
-    if (live == 1u) {
-        if (!active) return;
-        const float inv = 1.0f / l;
-        float* dst = out + static_cast<std::uint64_t>(q_row) * q_heads * D + static_cast<std::uint64_t>(q_head) * D;
-#pragma unroll
-        for (unsigned j = 0; j < ACC / 4; ++j) {
-            const float4 o = make_float4(acc[4 * j] * inv, acc[4 * j + 1] * inv, acc[4 * j + 2] * inv,
-                                         acc[4 * j + 3] * inv);
-            *reinterpret_cast<float4*>(dst + 4u * (lane16 + 16u * j)) = o;
-        }
-        return;
-    }
-    // Partial of this split: [tile][split][vector] {m, l, pad, pad, acc[D]}.
-    if (!active) return;
-    float* part = partials + ((static_cast<std::uint64_t>(blockIdx.x) * splits + split) * kTileVectors + qi) * (D + 4u);
-    if (lane16 == 0) {
-        part[0] = mx;
-        part[1] = l;
-    }
-#pragma unroll
-    for (unsigned j = 0; j < ACC / 4; ++j) {
-        *reinterpret_cast<float4*>(part + 4u + 4u * (lane16 + 16u * j)) =
-            make_float4(acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]);
-    }
 }
 
 // The 64-key chunk steps on the f32 matrix cores (v_mfma_f32_16x16x4_f32:
@@ -280,7 +77,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_mfma_kernel(
     const std::int32_t* __restrict__ tables, std::uint32_t layer, std::uint32_t q_heads, std::uint32_t kv_heads,
     const AttentionTile* __restrict__ tiles, std::uint32_t splits, float scale, float* __restrict__ partials,
     float* __restrict__ out) {
-    constexpr unsigned kChunk = 64;           // keys per stage, 16 per wave
+    constexpr unsigned kChunk = kChunkKeys;   // keys per stage, 16 per wave
     constexpr unsigned LD = D + 4;            // padded LDS row (floats), keeps float4 alignment
     constexpr unsigned D4 = D / 4;
     constexpr unsigned kQuarter = D / 4;      // dims per lane group in S^T
@@ -608,12 +405,11 @@ std::uint32_t make_attention_tiles(const std::uint32_t* run_rows, std::uint32_t 
 }
 
 std::uint32_t attention_splits(std::uint32_t tiles, std::uint64_t max_tokens, std::uint32_t m) {
-    const std::uint32_t chunk = chunk_for(m);
-    const std::uint64_t chunks = (max_tokens + chunk - 1) / chunk;
+    (void)m;
+    const std::uint64_t chunks = (max_tokens + kChunkKeys - 1) / kChunkKeys;
     if (tiles == 0 || chunks <= 1) return 1;
-    // 32-token chunks: about as many workgroups as fit in one round (three
-    // per CU on 256 CUs); 64-token chunks (prefill): about 512.
-    const std::uint64_t want = chunk == 32u ? (768u / tiles > 0u ? 768u / tiles : 1u) : (512u + tiles - 1) / tiles;
+    // About 512 workgroups (two per CU on 256 CUs).
+    const std::uint64_t want = (512u + tiles - 1) / tiles;
     const std::uint64_t s = want < chunks ? want : chunks;
     return static_cast<std::uint32_t>(s < kMaxSplits ? s : kMaxSplits);
 }
@@ -631,37 +427,23 @@ hipError_t launch_attention_tiles(const KvLayout& kv, const float* qkv, std::uin
     const KvGeometry g{kv.pool, kv.page_tokens, kv.kv_width, kv.layers, kv.max_pages, kv.pool_pages};
     const float scale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(head_dim)));
     const dim3 grid(tile_count, splits);
-    const std::uint32_t chunk = chunk_for(m);
-#define AIR_ATTENTION_LAUNCH(D, C)                                                                               \
-    hipLaunchKernelGGL((attention_tile_kernel<D, C>), grid, dim3(kAttnThreads), 0, stream, g, qkv, stride, m,     \
-                       positions, tables, layer, q_heads, kv_heads, tiles, splits, scale, partials, out)
-#define AIR_ATTENTION_MERGE(D)                                                                                   \
-    hipLaunchKernelGGL(attention_merge_kernel<D>, dim3(tile_count), dim3(kAttnThreads), 0, stream, tiles, splits, \
-                       chunk, m, q_heads, kv_heads, positions, partials, out)
 #define AIR_ATTENTION_MFMA(D)                                                                                    \
     hipLaunchKernelGGL(attention_mfma_kernel<D>, grid, dim3(kAttnThreads), 0, stream, g, qkv, stride, m, positions, \
                        tables, layer, q_heads, kv_heads, tiles, splits, scale, partials, out)
-    // 64-key chunks (steps of more than 64 rows) on the matrix cores.
+#define AIR_ATTENTION_MERGE(D)                                                                                   \
+    hipLaunchKernelGGL(attention_merge_kernel<D>, dim3(tile_count), dim3(kAttnThreads), 0, stream, tiles, splits, \
+                       kChunkKeys, m, q_heads, kv_heads, positions, partials, out)
     if (head_dim == 128u) {
-        if (chunk == 32u) {
-            AIR_ATTENTION_LAUNCH(128, 32);
-        } else {
-            AIR_ATTENTION_MFMA(128);
-        }
+        AIR_ATTENTION_MFMA(128);
         if (splits > 1u) AIR_ATTENTION_MERGE(128);
     } else if (head_dim == 64u) {
-        if (chunk == 32u) {
-            AIR_ATTENTION_LAUNCH(64, 32);
-        } else {
-            AIR_ATTENTION_MFMA(64);
-        }
+        AIR_ATTENTION_MFMA(64);
         if (splits > 1u) AIR_ATTENTION_MERGE(64);
     } else {
         return hipErrorInvalidValue;
     }
-#undef AIR_ATTENTION_LAUNCH
-#undef AIR_ATTENTION_MERGE
 #undef AIR_ATTENTION_MFMA
+#undef AIR_ATTENTION_MERGE
     return hipGetLastError();
 }
 

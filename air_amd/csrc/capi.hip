@@ -1309,7 +1309,7 @@ int air_hip_attention_online(air_hip_context* ctx, const air_hip_kv_layout* kv, 
                                                   q_heads, kv_heads, head_dim,
                                                   reinterpret_cast<const AttentionTile*>(tiles), tile_count, splits,
                                                   static_cast<float*>(ctx->attention_scratch), out, ctx->stream);
-    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "attention_tile_kernel");
+    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "attention_mfma_kernel");
 }
 
 int air_hip_silu_mul(air_hip_context* ctx, const float* gate_up, float* out, uint32_t m, uint64_t ffn) {
