@@ -667,7 +667,7 @@ int air_hip_decode_linear_fused(air_hip_context* ctx, const air_hip_matrix* m, c
         return fail(AIR_HIP_INVALID_ARGUMENT, "unknown epilogue %d", epilogue);
     }
     const bool norm = norm_weight != nullptr;
-    if ((norm && epilogue == AIR_HIP_EPILOGUE_RESIDUAL) || (!norm && epilogue == AIR_HIP_EPILOGUE_SWIGLU)) {
+    if (norm && epilogue == AIR_HIP_EPILOGUE_RESIDUAL) {
         return fail(AIR_HIP_UNSUPPORTED, "this norm / epilogue combination is not provided");
     }
     if (norm && !(eps >= 0.0)) return fail(AIR_HIP_INVALID_ARGUMENT, "eps must be non-negative");

@@ -499,6 +499,7 @@ hipError_t launch_gemv_fmt(const TilePlanes& p, const float* x, const float* bia
     if (norm || f.epilogue != 0) {
         if (g.rows_per_wave != 1u) return hipErrorInvalidConfiguration;
         if (!norm && f.epilogue == 1) return launch_gemv_r1<FMT, false, 1>(p, x, bias, y, g, f, s);
+        if (!norm && f.epilogue == 2) return launch_gemv_r1<FMT, false, 2>(p, x, bias, y, g, f, s);
         if (norm && f.epilogue == 0) return launch_gemv_r1<FMT, true, 0>(p, x, bias, y, g, f, s);
         if (norm && f.epilogue == 2) return launch_gemv_r1<FMT, true, 2>(p, x, bias, y, g, f, s);
         return hipErrorInvalidValue;

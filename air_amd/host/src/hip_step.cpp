@@ -426,12 +426,13 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
     if (rc != AIR_HIP_OK) return hip_status(rc);
     // One row on the decode tactic (single-sequence decode): the attention
     // norm runs inside the q|k|v linear and both residual adds inside the o
-    // and down linears, the hidden state updated in place.  The FFN norm and
-    // SiLU stay kernels of their own: measured at M = 1 on the 7B shapes, a
-    // norm prologue in each of gate|up's 1184 workgroups costs more than the
-    // norm launch it saves (q|k|v 9.3 us fused vs 10.3 us; o + add 6.2 vs
-    // 9.8; down + add 16.4 vs 20.0; gate|up with norm and SwiGLU 34.4 vs
-    // 31.6 for norm, linear and SiLU).
+    // and down linears, the hidden state updated in place, and the SwiGLU
+    // inside gate|up.  The FFN norm stays a kernel of its own: measured at
+    // M = 1 on the 7B shapes, a norm prologue in each of gate|up's 1184
+    // workgroups costs more than the norm launch it saves (q|k|v 9.3 us fused
+    // vs 10.3 us; o + add 6.2 vs 9.8; down + add 16.4 vs 20.0; gate|up with
+    // norm and SwiGLU 34.4 vs 31.6 for norm, linear and SiLU; gate|up with
+    // SwiGLU alone 29.2 vs 30.4 for linear and SiLU, in graphs).
     const bool fuse = m == 1U && tactic == QuantizedLinearExecutionKind::hip_decode && prepared_.fused_qkv() &&
                       prepared_.fused_gate_up();
     const double eps = c.rms_norm_epsilon;
@@ -451,8 +452,11 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
             if ((rc = air_hip_rms_norm(ctx, hidden_, ffn_norm_[l], normed_, m, embed_, eps)) != AIR_HIP_OK) {
                 return hip_status(rc);
             }
-            if (Status s = prepared_.linear(l, LinearRole::ffn_gate_up, normed_, gate_up_, m, tactic); !s) return s;
-            if ((rc = air_hip_silu_mul(ctx, gate_up_, act_, m, ffn_)) != AIR_HIP_OK) return hip_status(rc);
+            if (Status s = prepared_.decode_linear_fused(l, LinearRole::ffn_gate_up, normed_, act_, nullptr, 0.0,
+                                                         AIR_HIP_EPILOGUE_SWIGLU);
+                !s) {
+                return s;
+            }
             if (Status s = prepared_.decode_linear_fused(l, LinearRole::ffn_down, act_, hidden_, nullptr, 0.0,
                                                          AIR_HIP_EPILOGUE_RESIDUAL);
                 !s) {

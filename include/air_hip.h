@@ -275,7 +275,7 @@ int air_hip_linear_noalloc(air_hip_context* ctx, const air_hip_matrix* matrix, c
  *                SWIGLU    the matrix is a fused gate|up of n = 2F rows
  *                          (F a multiple of 16): y[i] = silu(g_i) * u_i for
  *                          the F outputs, silu(g) = g / (1 + e^-g).
- * Every combination but (norm, RESIDUAL) and (no norm, SWIGLU).  x is one
+ * Every combination but (norm, RESIDUAL).  x is one
  * 16-byte aligned row of k floats and must not alias y.  Same tolerance as
  * the DECODE tactic.  No counterpart in the reference's linear API. */
 enum {

@@ -291,8 +291,9 @@ def test_graph_replay_after_workspace_growth(torch_cuda):
 def test_decode_linear_fused_matches_separate_kernels(torch_cuda, hip_ctx, type_id, k, f):
     """air_hip_decode_linear_fused against the separate kernels it replaces:
     RMSNorm then the linear (1e-6: the norm's sum runs in another order),
-    the linear then a residual add (bit-exact: same launch plan), and
-    RMSNorm, the gate|up linear and SwiGLU (1e-6)."""
+    the linear then a residual add (bit-exact: same launch plan), RMSNorm,
+    the gate|up linear and SwiGLU (1e-6), and the gate|up linear and SwiGLU
+    alone."""
     torch = torch_cuda
     lib = capi.lib()
     n = 2 * f
@@ -330,9 +331,19 @@ def test_decode_linear_fused_matches_separate_kernels(torch_cuda, hip_ctx, type_
                                                    bias.data_ptr(), w.data_ptr(), eps, capi.EPILOGUE_SWIGLU))
         torch.cuda.synchronize()
         assert helpers.rel_l2(act.cpu().numpy(), act_ref.cpu().numpy()) <= 1e-6
-        # combinations that are not provided, and a bad epilogue
-        assert lib.air_hip_decode_linear_fused(hip_ctx.handle, mat.handle, x.data_ptr(), act.data_ptr(), None,
-                                               None, 0.0, capi.EPILOGUE_SWIGLU) == 6
+        # the gate|up linear and SwiGLU without the norm (1e-6: a workgroup
+        # of twice the waves may split K over the waves differently; bit-exact
+        # where the halves get the plain plan's wave count)
+        act_ref = torch.empty((1, f), dtype=torch.float32, device="cuda:0")
+        capi.check(lib.air_hip_silu_mul(hip_ctx.handle, lin.data_ptr(), act_ref.data_ptr(), 1, f))
+        act = torch.full((1, f), float("nan"), dtype=torch.float32, device="cuda:0")
+        capi.check(lib.air_hip_decode_linear_fused(hip_ctx.handle, mat.handle, x.data_ptr(), act.data_ptr(),
+                                                   bias.data_ptr(), None, 0.0, capi.EPILOGUE_SWIGLU))
+        torch.cuda.synchronize()
+        assert helpers.rel_l2(act.cpu().numpy(), act_ref.cpu().numpy()) <= 1e-6
+        if (type_id, k) == (capi.TYPE_Q8_0, 1056):
+            assert np.array_equal(act.cpu().numpy().view(np.uint32), act_ref.cpu().numpy().view(np.uint32))
+        # a combination that is not provided, and a bad epilogue
         assert lib.air_hip_decode_linear_fused(hip_ctx.handle, mat.handle, x.data_ptr(), resid.data_ptr(), None,
                                                w.data_ptr(), eps, capi.EPILOGUE_RESIDUAL) == 6
         assert lib.air_hip_decode_linear_fused(hip_ctx.handle, mat.handle, x.data_ptr(), resid.data_ptr(), None,
