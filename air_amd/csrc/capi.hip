@@ -252,12 +252,12 @@ enum class Route { prefill, gemv, fused, skinny_x, skinny_loaded, decode_linear 
 // M = 64.  Q4_K with four activation tiles would also spill in it.
 Route skinny_route(const air_hip_context* ctx, const air_hip_matrix* m, std::uint32_t rows) {
     const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages);
-    // Q8_0 from 17 rows: the split activations feed the LDS pipeline, which
-    // beats the f32-input kernel on the narrow 7B matrices too, split launch
-    // included (M = 32: q|k|v 18.4 -> 16.2 us, o 16.3 -> 14.7, down 41.5 ->
-    // 32.1).  At M = 8 the two are even per call, and in a graph the split's
-    // extra launch made the step slower (2.60 -> 2.78 ms).
-    if (m->planes.type == kQ8_0 && rows > 16u && shape.lds_stages >= 2u) return Route::skinny_loaded;
+    // From 17 rows the split activations feed the LDS pipeline, which beats
+    // the f32-input kernel on the narrow 7B matrices too, split launch
+    // included (Q8_0, M = 32: q|k|v 18.4 -> 16.2 us, o 16.3 -> 14.7, down
+    // 41.5 -> 32.1).  At M = 8 the two are even per call, and in a graph the
+    // split's extra launch made the step slower (2.60 -> 2.78 ms).
+    if (rows > 16u && shape.lds_stages >= 2u) return Route::skinny_loaded;
     const bool narrow = m->planes.nt <= 512u && (rows <= 32u || m->planes.k <= 4096u);
     return (!narrow || (m->planes.type == kQ4_K && shape.mt == 4u)) ? Route::skinny_loaded : Route::skinny_x;
 }
@@ -864,7 +864,7 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
     case Route::skinny_loaded: {
         const bool loaded = route_linear(ctx, m, rows, tactic) == Route::skinny_loaded;
         const SkinnyShape k = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages);
-        const bool lds = loaded && k.lds_stages >= 2u && m->planes.type == kQ8_0;
+        const bool lds = loaded && k.lds_stages >= 2u;
         char stages[32] = "";
         if (lds) std::snprintf(stages, sizeof stages, " lds_stages=%u", k.lds_stages);
         std::snprintf(buf, sizeof buf, "%s%s<%s%s> mt=%u tile_n=%u groups=%u splits=%u%s%s",

@@ -253,18 +253,22 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_kernel(SkinnyArgs a) {
     }
 }
 
-// ---- LDS-pipelined variant (Q8_0, split activations) ----------------------
+// ---- LDS-pipelined variant (split activations) ------------------------------
 //
-// The same arithmetic as skinny_kernel<kQ8_0, MT, TN, false>, with every
+// The same arithmetic as skinny_kernel<FMT, MT, TN, false>, with every
 // operand of a 64-k step moved by direct global -> LDS loads into one of NS
 // stages, so up to NS - 1 steps of weight codes per wave are in flight
 // without holding registers (the register pipeline above has room for two).
 // A stage holds the step's 4 MT activation fragments (each wave loads MT of
-// them), then each wave's TN weight-code records (1 KiB) and scale records
-// (64 lanes x 4 bytes).  Each KiB is one 64-lane x 16-byte fragment in lane
-// order, read back at lane * 16 (no bank conflicts).  One bare barrier per
-// step publishes the stage and frees the oldest one; a wave waits only for
-// its own loads of the stage (vmcnt).
+// them), then each wave's TN weight-code records and scale records, then
+// (Q4_K) the step's activation block sums.  Per 16-row tile and step the
+// codes are one 64-lane x 16-byte fragment (Q8_0), or the lane's half of its
+// 16-byte record (Q4_0, Q4_K: two 64-lane x 4-byte loads); the scales are
+// 64 lanes x 4 bytes (Q8_0, Q4_0: the lane's row's two block scales; Q4_K:
+// the tile's 16 super-block headers, 256 contiguous bytes).  Everything is
+// read back in lane order (no bank conflicts).  One bare barrier per step
+// publishes the stage and frees the oldest one; a wave waits only for its
+// own loads of the stage (vmcnt).
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void global_void_t;
 
@@ -283,18 +287,29 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((n & 0xfu) | ((n >> 4) << 14) | (0x7u << 4) | (0xfu << 8));
 }
 
-template <int MT, int TN>
-constexpr unsigned skinny_stage_bytes() {
-    return 4u * MT * 1024u + 4u * TN * 1024u + 4u * TN * 256u;
+template <int FMT>
+constexpr unsigned lds_code_bytes() {
+    return FMT == kQ8_0 ? 1024u : 512u;   // per tile and step
 }
 
-template <int MT, int TN, int NS>
+template <int FMT, int MT, int TN>
+constexpr unsigned skinny_stage_bytes() {
+    return 4u * MT * 1024u + 4u * TN * (lds_code_bytes<FMT>() + 256u) + (FMT == kQ4_K ? 1024u : 0u);
+}
+
+template <int FMT, int MT, int TN, int NS>
 __global__ __launch_bounds__(kThreads, 2) void skinny_lds_kernel(SkinnyArgs a) {
-    constexpr unsigned kStage = skinny_stage_bytes<MT, TN>();
-    constexpr unsigned kCodes = 4u * MT * 1024u;            // offset of the weight codes in a stage
-    constexpr unsigned kScales = kCodes + 4u * TN * 1024u;  // offset of the weight scales
-    constexpr unsigned kLoads = MT + 2u * TN;               // load instructions per wave per stage
+    constexpr unsigned kStage = skinny_stage_bytes<FMT, MT, TN>();
+    constexpr unsigned kCodeBytes = lds_code_bytes<FMT>();
+    constexpr unsigned kCodes = 4u * MT * 1024u;                  // offset of the weight codes in a stage
+    constexpr unsigned kScales = kCodes + 4u * TN * kCodeBytes;   // offset of the weight scales
+    constexpr unsigned kSumsAt = kScales + 4u * TN * 256u;        // offset of the block sums (Q4_K)
+    constexpr bool kSums = FMT == kQ4_K;
+    constexpr unsigned kMp = 16u * MT;
+    // Load instructions per wave per stage.
+    constexpr unsigned kLoads = MT + TN * (FMT == kQ8_0 ? 2u : 3u) + (kSums ? 1u : 0u);
     static_assert(NS >= 2 && NS <= 4, "two to four stages");
+    static_assert(2u * kMp <= 4u * 64u, "one block-sum load per wave covers a step");
     // One LDS object per stage, addressed with compile-time stage numbers:
     // the compiler's wait-count pass then sees that a stage's direct loads
     // and another stage's reads touch different objects.
@@ -329,6 +344,12 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_lds_kernel(SkinnyArgs a) {
         wtile[j] = static_cast<std::uint64_t>(rt) * a.kt;
     }
     const u32x4* xs = reinterpret_cast<const u32x4*>(a.xs);
+    const std::uint32_t* codes32 = static_cast<const std::uint32_t*>(a.codes);
+    const std::uint32_t* scales32 = static_cast<const std::uint32_t*>(a.scales);
+    // Q4_K: this lane's block-sum load, the step's 2 * kMp sums spread over
+    // the four waves (lanes past them repeat the last one into unused slots).
+    const std::uint32_t sum_slot = wave * 64u + lane;
+    const std::uint32_t sum_src = min(sum_slot, 2u * kMp - 1u);
     const auto issue = [&](std::uint32_t s, unsigned st) __attribute__((always_inline)) {
         unsigned char* base = stage(st);
         // Fragment f of the step: block f / (2 MT), tile (f / 2) % MT, part f % 2.
@@ -339,21 +360,54 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_lds_kernel(SkinnyArgs a) {
         }
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const std::uint64_t tile = wtile[j] + s;
             const unsigned slot = wave * TN + static_cast<unsigned>(j);
-            lds_load16(static_cast<const u32x4*>(a.codes) + tile * 64u + lane, base + kCodes + slot * 1024u);
-            lds_load4(static_cast<const std::uint32_t*>(a.scales) + tile * 16u + (lane & 15u),
-                      base + kScales + slot * 256u);
+            unsigned char* code_dst = base + kCodes + slot * kCodeBytes;
+            unsigned char* scale_dst = base + kScales + slot * 256u;
+            if constexpr (FMT == kQ8_0) {
+                const std::uint64_t tile = wtile[j] + s;
+                lds_load16(static_cast<const u32x4*>(a.codes) + tile * 64u + lane, code_dst);
+                lds_load4(scales32 + tile * 16u + (lane & 15u), scale_dst);
+            } else if constexpr (FMT == kQ4_0) {
+                // 128-k tiles: the step is half (s & 1) of the lane's record.
+                const std::uint64_t tile = wtile[j] + (s >> 1);
+                const std::uint64_t rec = ((tile * 64u + lane) * 2u + (s & 1u)) * 2u;   // dword index
+                lds_load4(codes32 + rec, code_dst);
+                lds_load4(codes32 + rec + 1u, code_dst + 256u);
+                lds_load4(scales32 + (tile * 16u + (lane & 15u)) * 2u + (s & 1u), scale_dst);
+            } else {
+                // 256-k super-blocks: sub-block pair s & 3 of two 16-byte records.
+                const std::uint64_t tile = wtile[j] + (s >> 2);
+                const std::uint32_t sub = s & 3u;
+                const std::uint64_t rec = (((tile * 2u + (sub >> 1)) * 64u + lane) * 2u + (sub & 1u)) * 2u;
+                lds_load4(codes32 + rec, code_dst);
+                lds_load4(codes32 + rec + 1u, code_dst + 256u);
+                lds_load4(scales32 + tile * 64u + lane, scale_dst);   // the 16 rows' headers
+            }
+        }
+        if constexpr (kSums) {
+            lds_load4(a.block_sums + static_cast<std::uint64_t>(s) * 2u * kMp + sum_src, base + kSumsAt + wave * 256u);
         }
     };
     const auto compute = [&](std::uint32_t s, unsigned st) __attribute__((always_inline)) {
         const unsigned char* base = stage(st);
-        StepCodes<kQ8_0> w_in[TN];
+        StepCodes<FMT> w_in[TN];
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             const unsigned slot = wave * TN + static_cast<unsigned>(j);
-            w_in[j].c = *reinterpret_cast<const u32x4*>(base + kCodes + slot * 1024u + lane * 16u);
-            w_in[j].d = *reinterpret_cast<const std::uint32_t*>(base + kScales + slot * 256u + lane * 4u);
+            const unsigned char* code_src = base + kCodes + slot * kCodeBytes;
+            const unsigned char* scale_src = base + kScales + slot * 256u;
+            if constexpr (FMT == kQ8_0) {
+                w_in[j].c = *reinterpret_cast<const u32x4*>(code_src + lane * 16u);
+                w_in[j].d = *reinterpret_cast<const std::uint32_t*>(scale_src + lane * 4u);
+            } else {
+                w_in[j].c.x = *reinterpret_cast<const std::uint32_t*>(code_src + lane * 4u);
+                w_in[j].c.y = *reinterpret_cast<const std::uint32_t*>(code_src + 256u + lane * 4u);
+                if constexpr (FMT == kQ4_0) {
+                    w_in[j].d = *reinterpret_cast<const std::uint32_t*>(scale_src + lane * 4u);
+                } else {
+                    w_in[j].h = *reinterpret_cast<const u32x4*>(scale_src + (lane & 15u) * 16u);
+                }
+            }
         }
         half8v xf[2][MT][2];
 #pragma unroll
@@ -365,19 +419,30 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_lds_kernel(SkinnyArgs a) {
                     const unsigned f = (static_cast<unsigned>(b) * MT + t) * 2u + part;
                     xf[b][t][part] = *reinterpret_cast<const half8v*>(base + f * 1024u + lane * 16u);
                 }
+        float4v sum4[kSums ? 2 : 1][kSums ? MT : 1];
+        if constexpr (kSums) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    const unsigned at = (static_cast<unsigned>(b) * kMp + t * 16u + 4u * (lane >> 4)) * 4u;
+                    sum4[b][t] = *reinterpret_cast<const float4v*>(base + kSumsAt + at);
+                }
+        }
         __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the arithmetic
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
-                const half8v w = step_codes<kQ8_0>(w_in[j], b);
+                const half8v w = step_codes<FMT>(w_in[j], b);
                 float ws, wo;
-                step_scale<kQ8_0>(w_in[j], s, b, ws, wo);
+                step_scale<FMT>(w_in[j], s, b, ws, wo);
 #pragma unroll
                 for (int t = 0; t < MT; ++t) {
                     float4v p = mfma16x16x32(xf[b][t][0], w, float4v{0.f, 0.f, 0.f, 0.f});
                     p = mfma16x16x32(xf[b][t][1], w, p);
                     acc[j][t] += ws * p;
+                    if constexpr (kSums) acc[j][t] -= wo * sum4[b][t];
                 }
             }
         }
@@ -542,32 +607,43 @@ hipError_t launch_fmt(const SkinnyArgs& a, const SkinnyShape& shape, std::uint32
     }
 }
 
-template <int MT>
+template <int FMT, int MT>
 hipError_t launch_lds_mt(const SkinnyArgs& a, const SkinnyShape& shape, std::uint32_t blocks, hipStream_t stream) {
     const bool two = shape.tile_n == 2u;
     switch (shape.lds_stages) {
     case 2:
-        if (two) hipLaunchKernelGGL((skinny_lds_kernel<MT, 2, 2>), dim3(blocks), dim3(kThreads), 0, stream, a);
-        else hipLaunchKernelGGL((skinny_lds_kernel<MT, 1, 2>), dim3(blocks), dim3(kThreads), 0, stream, a);
+        if (two) hipLaunchKernelGGL((skinny_lds_kernel<FMT, MT, 2, 2>), dim3(blocks), dim3(kThreads), 0, stream, a);
+        else hipLaunchKernelGGL((skinny_lds_kernel<FMT, MT, 1, 2>), dim3(blocks), dim3(kThreads), 0, stream, a);
         break;
     case 3:
-        if (two) hipLaunchKernelGGL((skinny_lds_kernel<MT, 2, 3>), dim3(blocks), dim3(kThreads), 0, stream, a);
-        else hipLaunchKernelGGL((skinny_lds_kernel<MT, 1, 3>), dim3(blocks), dim3(kThreads), 0, stream, a);
+        if (two) hipLaunchKernelGGL((skinny_lds_kernel<FMT, MT, 2, 3>), dim3(blocks), dim3(kThreads), 0, stream, a);
+        else hipLaunchKernelGGL((skinny_lds_kernel<FMT, MT, 1, 3>), dim3(blocks), dim3(kThreads), 0, stream, a);
         break;
     default:
-        if (two) hipLaunchKernelGGL((skinny_lds_kernel<MT, 2, 4>), dim3(blocks), dim3(kThreads), 0, stream, a);
-        else hipLaunchKernelGGL((skinny_lds_kernel<MT, 1, 4>), dim3(blocks), dim3(kThreads), 0, stream, a);
+        if (two) hipLaunchKernelGGL((skinny_lds_kernel<FMT, MT, 2, 4>), dim3(blocks), dim3(kThreads), 0, stream, a);
+        else hipLaunchKernelGGL((skinny_lds_kernel<FMT, MT, 1, 4>), dim3(blocks), dim3(kThreads), 0, stream, a);
         break;
     }
     return hipGetLastError();
 }
 
-hipError_t launch_lds(const SkinnyArgs& a, const SkinnyShape& shape, std::uint32_t blocks, hipStream_t stream) {
+template <int FMT>
+hipError_t launch_lds_fmt(const SkinnyArgs& a, const SkinnyShape& shape, std::uint32_t blocks, hipStream_t stream) {
     switch (shape.mt) {
-    case 1: return launch_lds_mt<1>(a, shape, blocks, stream);
-    case 2: return launch_lds_mt<2>(a, shape, blocks, stream);
-    case 3: return launch_lds_mt<3>(a, shape, blocks, stream);
-    default: return launch_lds_mt<4>(a, shape, blocks, stream);
+    case 1: return launch_lds_mt<FMT, 1>(a, shape, blocks, stream);
+    case 2: return launch_lds_mt<FMT, 2>(a, shape, blocks, stream);
+    case 3: return launch_lds_mt<FMT, 3>(a, shape, blocks, stream);
+    default: return launch_lds_mt<FMT, 4>(a, shape, blocks, stream);
+    }
+}
+
+hipError_t launch_lds(int type, const SkinnyArgs& a, const SkinnyShape& shape, std::uint32_t blocks,
+                      hipStream_t stream) {
+    switch (type) {
+    case kQ8_0: return launch_lds_fmt<kQ8_0>(a, shape, blocks, stream);
+    case kQ4_0: return launch_lds_fmt<kQ4_0>(a, shape, blocks, stream);
+    case kQ4_K: return launch_lds_fmt<kQ4_K>(a, shape, blocks, stream);
+    default: return hipErrorInvalidValue;
     }
 }
 
@@ -597,15 +673,34 @@ SkinnyShape plan_skinny(const TilePlanes& p, std::uint32_t m, std::uint32_t tile
                         std::uint32_t lds_stages) {
     SkinnyShape s;
     s.mt = static_cast<std::uint32_t>(ceil_div(m, 16u));
+    // The LDS pipeline (split activations): two stages measured best (three
+    // and four never helped).  Q8_0 takes it on every 7B matrix except the
+    // lm_head at M <= 32, where the register pipeline with two tiles per wave
+    // wins (132 vs 146 us); Q4_K everywhere (gate|up 70 -> 48 us at M = 32,
+    // 105 -> 75 at M = 64; down 55 -> 37 at M = 32; lm_head M = 32 157 us
+    // against 208); Q4_0 from 17 rows (M = 64: q|k|v 31 -> 21 us, gate|up
+    // 66 -> 57, down 51 -> 44), except its lm_head at M <= 32 (132 us on
+    // registers with two tiles, 157 on LDS); at M <= 16 its gate|up is
+    // faster on registers (29 vs 33 us).
+    if (lds_stages == 0u) {
+        const bool narrow_or_tall = p.nt <= 4096u || s.mt >= 3u;
+        const bool lds = p.type == kQ8_0   ? narrow_or_tall
+                         : p.type == kQ4_0 ? s.mt >= 2u && narrow_or_tall
+                                           : true;
+        lds_stages = lds ? 2u : 1u;
+    }
+    s.lds_stages = lds_stages >= 2u ? lds_stages : 0u;
     // Two weight tiles per wave halve the LDS activation reads per weight
     // byte; with three or more activation tiles they would spill registers
     // (the in-workgroup split of the f32 variant holds more live values).
     // Automatic choice, measured on the Qwen2-7B shapes: two tiles only pay
-    // for matrices of 2000..4096 row tiles (gate|up) at M <= 32.
+    // for matrices of 2000..4096 row tiles (gate|up) at M <= 32, and not for
+    // the 4-bit formats on the LDS pipeline (Q4_K gate|up M = 32: 52 vs 48 us).
     // lm_head-sized matrices (9504 row tiles) also take two at M <= 32 on the
     // register pipeline (M = 32: 155 -> 132 us).
     const std::uint32_t tn2_max_mt = 2u;
-    const std::uint32_t want = tile_n != 0u ? tile_n : ((s.mt <= 2u && p.nt >= 2000u) ? 2u : 1u);
+    const bool tn2_auto = s.mt <= 2u && p.nt >= 2000u && (p.type == kQ8_0 || s.lds_stages == 0u);
+    const std::uint32_t want = tile_n != 0u ? tile_n : (tn2_auto ? 2u : 1u);
     s.tile_n = (want == 2u && s.mt <= tn2_max_mt) ? 2u : 1u;
     s.groups = static_cast<std::uint32_t>(ceil_div(p.nt, 4u * s.tile_n));
     s.steps = static_cast<std::uint32_t>(p.kp / kStepK);
@@ -628,14 +723,6 @@ SkinnyShape plan_skinny(const TilePlanes& p, std::uint32_t m, std::uint32_t tile
     splits = splits < 1u ? 1u : (splits > s.steps ? s.steps : splits);
     s.steps_per_split = static_cast<std::uint32_t>(ceil_div(s.steps, splits));
     s.splits = static_cast<std::uint32_t>(ceil_div(s.steps, s.steps_per_split));
-    // The LDS pipeline (Q8_0, split activations): two stages measured best
-    // (three and four never helped) on every 7B matrix except the lm_head at
-    // M <= 32, where the register pipeline with two tiles per wave wins
-    // (132 vs 146 us).
-    if (lds_stages == 0u) {
-        lds_stages = p.type == kQ8_0 && (p.nt <= 4096u || s.mt >= 3u) ? 2u : 1u;
-    }
-    s.lds_stages = lds_stages >= 2u ? lds_stages : 0u;
     return s;
 }
 
@@ -665,8 +752,8 @@ hipError_t launch_skinny_linear(const TilePlanes& p, const SplitWorkspace& ws, c
     a.bias = split ? nullptr : bias;
     a.out = split ? partials : y;
     const std::uint32_t blocks = shape.groups * shape.splits;
-    const hipError_t err = shape.lds_stages >= 2u && p.type == kQ8_0 ? launch_lds(a, shape, blocks, stream)
-                                                                     : launch_any<false>(p, a, shape, blocks, stream);
+    const hipError_t err = shape.lds_stages >= 2u ? launch_lds(p.type, a, shape, blocks, stream)
+                                                  : launch_any<false>(p, a, shape, blocks, stream);
     if (err != hipSuccess || !split) return err;
     if (epilogue) return launch_split_epilogue(partials, shape.splits, m, p.n, bias, *epilogue, stream);
     return launch_split_reduce(partials, shape.splits, m, p.n, bias, y, stream);

@@ -159,8 +159,9 @@ int air_hip_context_set_decode_path(air_hip_context* ctx, uint32_t path, uint32_
 /* Chooses how the decode linear (2..64 rows, skinny route) stages its
  * operands (autotuning): 0 = automatic, 1 = through registers
  * (skinny_kernel), 2..4 = an LDS ring of that many 64-k steps filled by
- * direct global -> LDS loads (skinny_lds_kernel; Q8_0 on split activations,
- * others keep the register path).  No counterpart in the reference. */
+ * direct global -> LDS loads (skinny_lds_kernel, every format; above 16
+ * rows the linear then runs on split activations).  No counterpart in the
+ * reference. */
 int air_hip_context_set_decode_pipeline(air_hip_context* ctx, uint32_t lds_stages);
 /* Chooses how the prefill GEMM stages its operands (autotuning): 0 =
  * automatic, 1 = through registers (prefill_gemm_kernel), 2..4 = an LDS ring

@@ -198,15 +198,16 @@ def test_skinny_shapes_agree(torch_cuda, hip_ctx, type_id, k, n):
         mat.release()
 
 
-@pytest.mark.parametrize("k,n", [(3584, 8200), (1024, 9000)])
-def test_skinny_lds_pipeline_matches_registers(torch_cuda, hip_ctx, k, n):
-    """The LDS-pipelined skinny kernel (Q8_0 on split activations: matrices
-    of more than 512 row tiles, a ragged last tile here) gives the register
+@pytest.mark.parametrize("type_id,k,n", [(capi.TYPE_Q8_0, 3584, 8200), (capi.TYPE_Q8_0, 1024, 9000),
+                                         (capi.TYPE_Q4_0, 3584, 8200), (capi.TYPE_Q4_K, 1024, 9000)])
+def test_skinny_lds_pipeline_matches_registers(torch_cuda, hip_ctx, type_id, k, n):
+    """The LDS-pipelined skinny kernel (on split activations: matrices of
+    more than 512 row tiles, a ragged last tile here) gives the register
     pipeline's bits for 2..4 stages, one and two weight tiles per wave, with
-    and without a K split, at every activation-tile count; the register
-    pipeline matches the oracle to 1e-4."""
+    and without a K split (three splits start mid-tile for the 128-k and
+    256-k tiles of Q4_0 and Q4_K), at every activation-tile count; the
+    register pipeline matches the oracle to 1e-4."""
     torch = torch_cuda
-    type_id = capi.TYPE_Q8_0
     canon = helpers.weights(type_id, k, n, seed=k + 7 * n)
     mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
     try:
