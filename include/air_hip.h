@@ -421,7 +421,8 @@ typedef struct air_hip_attention_tile {
 /* Host helper: the tiles of a step whose rows form `runs` consecutive runs,
  * run i holding run_rows[i] rows of one sequence at consecutive positions.
  * A one-row run (decode) gives a tile per KV head of its grouped q heads; a
- * longer run (prefill) tiles of 16 rows per q head.  tiles may be NULL (the
+ * longer run (prefill) tiles of 16 rows per q head, its last rows (the
+ * longest key ranges) first.  tiles may be NULL (the
  * count is still returned). */
 int air_hip_attention_make_tiles(const uint32_t* run_rows, uint32_t runs, uint32_t q_heads, uint32_t kv_heads,
                                  air_hip_attention_tile* tiles, uint32_t capacity, uint32_t* count);

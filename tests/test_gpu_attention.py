@@ -22,13 +22,13 @@ def test_tiles_for_decode_and_prefill_runs():
     # Two decode rows at 7B geometry: one tile per KV head with its 7 q heads.
     tiles = capi.attention_tiles([1, 1], 28, 4)
     assert tiles == [(r, 1, 7 * h, 7) for r in range(2) for h in range(4)]
-    # A 37-row prompt run: 16-row tiles of one q head.
+    # A 37-row prompt run: 16-row tiles of one q head, the last rows first.
     tiles = capi.attention_tiles([37], 4, 2)
-    assert tiles == [(r, min(16, 37 - r), h, 1) for h in range(4) for r in (0, 16, 32)]
+    assert tiles == [(r, min(16, 37 - r), h, 1) for r in (32, 16, 0) for h in range(4)]
     # Mixed: rows continue across runs.
     tiles = capi.attention_tiles([1, 20], 2, 2)
     assert tiles[:2] == [(0, 1, 0, 1), (0, 1, 1, 1)]
-    assert tiles[2:] == [(1, 16, 0, 1), (17, 4, 0, 1), (1, 16, 1, 1), (17, 4, 1, 1)]
+    assert tiles[2:] == [(17, 4, 0, 1), (17, 4, 1, 1), (1, 16, 0, 1), (1, 16, 1, 1)]
     with pytest.raises(capi.HipError):
         capi.attention_tiles([1], 6, 4)           # q heads not a multiple of KV heads
     with pytest.raises(capi.HipError):
