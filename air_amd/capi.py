@@ -133,6 +133,8 @@ SIGNATURES = {
     "air_hip_attention_make_tiles": (_I, [_P, _U32, _U32, _U32, _P, _U32, _P]),
     "air_hip_attention_online": (_I, [_P, _P, _P, _U64, _U32, _P, _P, _U32, _U32, _U32, _U32, _P, _U32, _U64, _P]),
     "air_hip_silu_mul": (_I, [_P, _P, _P, _U32, _U64]),
+    "air_hip_silu_mul_prefill": (_I, [_P, _P, _P, _U32, _U64]),
+    "air_hip_rms_norm_prefill": (_I, [_P, _P, _P, _P, _P, _U32, _U64, ctypes.c_double]),
     "air_hip_add": (_I, [_P, _P, _P, _U64]),
     "air_hip_argmax": (_I, [_P, _P, _U32, _U64, _P]),
     "air_hip_canonical_bytes": (_U64, [_I, _U64, _U64]),

@@ -128,9 +128,13 @@ struct PrefillShape {
 PrefillShape plan_prefill(const TilePlanes& planes, std::uint32_t m, const PrefillTuning& tuning);
 // Workspace of one prefill linear: f16 activations, row scales and (with a K
 // split) the f32 partials.
+// Padded f16 row stride and padded row count of the prefill operand.
+std::uint64_t prefill_ldx(std::uint64_t k);
+std::uint32_t prefill_rows_padded(std::uint32_t m);
 std::uint64_t prefill_workspace_bytes(std::uint64_t k, std::uint32_t m, const PrefillShape& shape, std::uint64_t n);
 hipError_t launch_prefill_linear(const TilePlanes& planes, const float* x, const float* bias, float* y,
-                                 std::uint32_t m, const PrefillShape& shape, void* workspace, hipStream_t stream);
+                                 std::uint32_t m, const PrefillShape& shape, void* workspace, hipStream_t stream,
+                                 bool converted = false);
 // y[m][n] = sum over splits of partials[s][m][n] (in split order) + bias[n].
 hipError_t launch_split_reduce(const float* partials, std::uint32_t splits, std::uint32_t m, std::uint64_t n,
                                const float* bias, float* y, hipStream_t stream);
@@ -229,6 +233,17 @@ hipError_t launch_attention_tiles(const KvLayout& kv, const float* qkv, std::uin
                                   const AttentionTile* tiles, std::uint32_t tile_count, std::uint32_t splits,
                                   float* partials, float* out, hipStream_t stream);
 hipError_t launch_silu_mul(const float* gate_up, float* out, std::uint32_t m, std::uint64_t ffn, hipStream_t stream);
+// The RMSNorm (with the residual add first when y is given) and the SwiGLU,
+// each also writing its output as the next prefill linear's operand
+// (xh [mp][ldx] f16 rows scaled by a power of two per row, row_inv [mp]),
+// bit-identical to that linear converting the f32 output itself.
+bool prefill_norm_fits(std::uint64_t n, std::uint64_t ldx);
+hipError_t launch_rms_norm_prefill(float* x, const float* y, const float* w, float* out, std::uint32_t m,
+                                   std::uint64_t n, double eps, _Float16* xh, float* row_inv, std::uint32_t mp,
+                                   std::uint64_t ldx, hipStream_t stream);
+bool silu_prefill_fits(std::uint64_t ffn, std::uint64_t ldx);
+hipError_t launch_silu_mul_prefill(const float* gate_up, float* out, std::uint32_t m, std::uint64_t ffn, _Float16* xh,
+                                   float* row_inv, std::uint32_t mp, std::uint64_t ldx, hipStream_t stream);
 
 // The step's element-wise work after a K-split linear, run by the launch
 // that sums the split partials (partials[s][m][n]) instead of a plain

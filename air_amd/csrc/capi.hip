@@ -54,6 +54,12 @@ struct air_hip_context {
     // uses them instead of splitting again.  Null after any other load and
     // once used.
     const void* loaded_source{nullptr};
+    // The last call left the next prefill linear's operand for these f32
+    // rows in the prefill workspace (air_hip_rms_norm_prefill /
+    // air_hip_silu_mul_prefill); good for the next call only.
+    const void* prefill_source{nullptr};
+    std::uint64_t prefill_source_k{0};
+    std::uint32_t prefill_source_rows{0};
     DecodeTuning tuning{};
     // Cross-workgroup K-split of the fused decode linear: partial sums and one
     // arrival counter per row group.  Counters are zeroed when allocated and
@@ -202,21 +208,30 @@ int noalloc_scratch(int device, void** out) {
 }
 
 // Every entry point that writes device memory through the context forgets
-// the rows an epilogue last split (AIR_HIP_EPILOGUE_RESIDUAL_LOAD): after
-// any such write the split may no longer match its source.
-void forget_loaded_source(air_hip_context* ctx) { ctx->loaded_source = nullptr; }
-
-int ensure_prefill_workspace(air_hip_context* ctx, std::uint64_t bytes) {
-    return grow_buffer(ctx, &ctx->prefill_workspace, &ctx->prefill_workspace_bytes, bytes, "prefill workspace");
+// the rows an epilogue last split (AIR_HIP_EPILOGUE_RESIDUAL_LOAD) and the
+// rows a *_prefill call last converted: after any such write the split or
+// the f16 operand may no longer match its source.
+void forget_loaded_source(air_hip_context* ctx) {
+    ctx->loaded_source = nullptr;
+    ctx->prefill_source = nullptr;
 }
 
-// Prefill linear: x [rows][k] -> y [rows][n] on the f16 MFMA GEMM.
+int ensure_prefill_workspace(air_hip_context* ctx, std::uint64_t bytes, bool keep = false) {
+    return grow_buffer(ctx, &ctx->prefill_workspace, &ctx->prefill_workspace_bytes, bytes, "prefill workspace", keep);
+}
+
+// Prefill linear: x [rows][k] -> y [rows][n] on the f16 MFMA GEMM; `ready`
+// (taken by the linear entry point) names rows whose f16 operand the call
+// before left in the workspace, which then skips the conversion.
 int run_prefill(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y, const float* bias,
-                std::uint32_t rows) {
+                std::uint32_t rows, const void* ready = nullptr, std::uint64_t ready_k = 0,
+                std::uint32_t ready_rows = 0) {
     const PrefillShape shape = plan_prefill(m->planes, rows, ctx->prefill_tuning);
-    int rc = ensure_prefill_workspace(ctx, prefill_workspace_bytes(m->planes.k, rows, shape, m->planes.n));
+    const bool converted = ready == x && ready_k == m->planes.k && ready_rows == rows;
+    int rc = ensure_prefill_workspace(ctx, prefill_workspace_bytes(m->planes.k, rows, shape, m->planes.n), converted);
     if (rc != AIR_HIP_OK) return rc;
-    const hipError_t err = launch_prefill_linear(m->planes, x, bias, y, rows, shape, ctx->prefill_workspace, ctx->stream);
+    const hipError_t err = launch_prefill_linear(m->planes, x, bias, y, rows, shape, ctx->prefill_workspace, ctx->stream,
+                                                 converted);
     if (err != hipSuccess) return hip_fail(err, "prefill_gemm_kernel");
     ctx->prefill_linear_calls.fetch_add(1, std::memory_order_relaxed);
     ctx->prefill_rows.fetch_add(rows, std::memory_order_relaxed);
@@ -658,7 +673,7 @@ int air_hip_dequantize_canonical(air_hip_context* ctx, int type, const void* can
 int air_hip_decode_linear_fused(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y,
                                 const float* bias, const float* norm_weight, double eps, int epilogue) {
     if (!ctx || !m || !x || !y) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix, x and y must not be null");
-    ctx->loaded_source = nullptr;
+    forget_loaded_source(ctx);
     if (static_cast<const void*>(x) == static_cast<const void*>(y)) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "y must not alias x");
     }
@@ -711,7 +726,7 @@ int air_hip_activations_load(air_hip_context* ctx, const float* x, uint64_t k, u
     ctx->loaded_k = k;
     ctx->loaded_rows = rows;
     ctx->loaded_row_scaled = row_scaled;
-    ctx->loaded_source = nullptr;
+    forget_loaded_source(ctx);
     return AIR_HIP_OK;
 }
 
@@ -726,7 +741,7 @@ namespace {
 int linear_loaded(air_hip_context* ctx, const air_hip_matrix* m, float* y, const float* bias, int tactic,
                   const SplitEpilogue* epilogue, bool* applied) {
     if (!ctx || !m || !y) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix and y must not be null");
-    ctx->loaded_source = nullptr;
+    forget_loaded_source(ctx);
     if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
     if (tactic != AIR_HIP_LINEAR_AUTO && tactic != AIR_HIP_LINEAR_DECODE && tactic != AIR_HIP_LINEAR_PREFILL) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "unknown linear tactic %d", tactic);
@@ -775,7 +790,8 @@ int linear_loaded(air_hip_context* ctx, const air_hip_matrix* m, float* y, const
 int linear_rows(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y, const float* bias,
                 uint32_t rows, int tactic, const SplitEpilogue* epilogue, bool* applied) {
     const void* ready = ctx ? ctx->loaded_source : nullptr;  // good for this call only
-    if (ctx) ctx->loaded_source = nullptr;
+    const void* prefill_ready = ctx ? ctx->prefill_source : nullptr;
+    if (ctx) forget_loaded_source(ctx);
     if (!ctx || !m || !x || !y) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix, x and y must not be null");
     if (static_cast<const void*>(x) == static_cast<const void*>(y)) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "y must not alias x");
@@ -791,7 +807,7 @@ int linear_rows(air_hip_context* ctx, const air_hip_matrix* m, const float* x, f
         if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
         DeviceScope scope(ctx->device);
         if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-        return run_prefill(ctx, m, x, y, bias, rows);
+        return run_prefill(ctx, m, x, y, bias, rows, prefill_ready, ctx->prefill_source_k, ctx->prefill_source_rows);
     }
     if (route == Route::decode_linear) {
         int rc = load_activations_for(ctx, x, m->planes.k, rows, ready);
@@ -1095,6 +1111,84 @@ int air_hip_add_rms_norm(air_hip_context* ctx, float* x, const float* y, const f
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
     const hipError_t err = launch_add_rms_norm(x, y, weight, out, m, n, eps, ctx->stream);
     return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "rms_norm_vec_kernel");
+}
+
+// The prefill workspace's operand area for rows of width k: xh then row_inv
+// (the layout launch_prefill_linear reads).
+struct PrefillOperand {
+    _Float16* xh;
+    float* row_inv;
+    std::uint32_t mp;
+    std::uint64_t ldx;
+};
+
+int prefill_operand(air_hip_context* ctx, std::uint64_t k, std::uint32_t m, PrefillOperand* op) {
+    const std::uint64_t mp = prefill_rows_padded(m);
+    const std::uint64_t ldx = prefill_ldx(k);
+    const std::uint64_t xh_bytes = ceil_div(mp * ldx * 2u, 256u) * 256u;
+    const int rc = ensure_prefill_workspace(ctx, xh_bytes + ceil_div(mp * 4u, 256u) * 256u);
+    if (rc != AIR_HIP_OK) return rc;
+    auto* base = static_cast<std::uint8_t*>(ctx->prefill_workspace);
+    *op = PrefillOperand{reinterpret_cast<_Float16*>(base), reinterpret_cast<float*>(base + xh_bytes),
+                         static_cast<std::uint32_t>(mp), ldx};
+    return AIR_HIP_OK;
+}
+
+void remember_prefill(air_hip_context* ctx, const void* source, std::uint64_t k, std::uint32_t m) {
+    ctx->prefill_source = source;
+    ctx->prefill_source_k = k;
+    ctx->prefill_source_rows = m;
+}
+
+int air_hip_rms_norm_prefill(air_hip_context* ctx, float* x, const float* y, const float* weight, float* out,
+                             uint32_t m, uint64_t n, double eps) {
+    if (!ctx || !x || !weight || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    forget_loaded_source(ctx);
+    if (n == 0 || !(eps >= 0.0)) return fail(AIR_HIP_INVALID_ARGUMENT, "width must be non-zero and eps non-negative");
+    if (y && (out == x || out == y)) return fail(AIR_HIP_INVALID_ARGUMENT, "out must not alias x or y");
+    if (m == 0) return AIR_HIP_OK;
+    if (m > kMaxRows) return fail(AIR_HIP_UNSUPPORTED, "batch width %u exceeds %u", m, kMaxRows);
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    PrefillOperand op{};
+    if (prefill_norm_fits(n, prefill_ldx(n))) {
+        int rc = prefill_operand(ctx, n, m, &op);
+        if (rc != AIR_HIP_OK) return rc;
+        const hipError_t err = launch_rms_norm_prefill(x, y, weight, out, m, n, eps, op.xh, op.row_inv, op.mp, op.ldx,
+                                                       ctx->stream);
+        if (err == hipSuccess) {
+            remember_prefill(ctx, out, n, m);
+            return AIR_HIP_OK;
+        }
+        if (err != hipErrorInvalidValue) return hip_fail(err, "rms_norm_vec_kernel");
+    }
+    // Rows the fused kernel does not take: the plain norm (the linear then converts).
+    const hipError_t err = y ? launch_add_rms_norm(x, y, weight, out, m, n, eps, ctx->stream)
+                             : launch_rms_norm(x, weight, out, m, n, eps, ctx->stream);
+    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "rms_norm_kernel");
+}
+
+int air_hip_silu_mul_prefill(air_hip_context* ctx, const float* gate_up, float* out, uint32_t m, uint64_t ffn) {
+    if (!ctx || !gate_up || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    forget_loaded_source(ctx);
+    if (m == 0 || ffn == 0) return AIR_HIP_OK;
+    if (m > kMaxRows) return fail(AIR_HIP_UNSUPPORTED, "batch width %u exceeds %u", m, kMaxRows);
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    if (silu_prefill_fits(ffn, prefill_ldx(ffn))) {
+        PrefillOperand op{};
+        int rc = prefill_operand(ctx, ffn, m, &op);
+        if (rc != AIR_HIP_OK) return rc;
+        const hipError_t err = launch_silu_mul_prefill(gate_up, out, m, ffn, op.xh, op.row_inv, op.mp, op.ldx,
+                                                       ctx->stream);
+        if (err == hipSuccess) {
+            remember_prefill(ctx, out, ffn, m);
+            return AIR_HIP_OK;
+        }
+        if (err != hipErrorInvalidValue) return hip_fail(err, "silu_rows_prefill_kernel");
+    }
+    const hipError_t err = launch_silu_mul(gate_up, out, m, ffn, ctx->stream);
+    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "silu_mul_kernel");
 }
 
 int air_hip_rope(air_hip_context* ctx, float* qkv, uint64_t row_stride, uint32_t m, const int32_t* positions,

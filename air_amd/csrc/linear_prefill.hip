@@ -654,7 +654,7 @@ std::uint64_t prefill_workspace_bytes(std::uint64_t k, std::uint32_t m, const Pr
 }
 
 hipError_t launch_prefill_linear(const TilePlanes& p, const float* x, const float* bias, float* y, std::uint32_t m,
-                                 const PrefillShape& shape, void* workspace, hipStream_t stream) {
+                                 const PrefillShape& shape, void* workspace, hipStream_t stream, bool converted) {
     const std::uint64_t mp = prefill_rows_padded(m);
     const std::uint64_t ldx = prefill_ldx(p.k);
     auto* base = static_cast<std::uint8_t*>(workspace);
@@ -664,8 +664,11 @@ hipError_t launch_prefill_linear(const TilePlanes& p, const float* x, const floa
     base += ceil_div(mp * 4u, 256u) * 256u;
     auto* partials = reinterpret_cast<float*>(base);
 
-    hipLaunchKernelGGL(prefill_activations_kernel, dim3(static_cast<unsigned>(mp)), dim3(kThreads), 0, stream, x, m,
-                       p.k, ldx, xh, row_inv);
+    // `converted`: the operand of these rows is already in the workspace.
+    if (!converted) {
+        hipLaunchKernelGGL(prefill_activations_kernel, dim3(static_cast<unsigned>(mp)), dim3(kThreads), 0, stream, x,
+                           m, p.k, ldx, xh, row_inv);
+    }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
 

@@ -542,18 +542,30 @@ __device__ __forceinline__ float4v split_sum4(const float* __restrict__ p, std::
     return t;
 }
 
-template <bool SPLIT, bool LOAD>
+// PF: out is also converted for the next prefill linear on it, as
+// prefill_activations_kernel converts a row (f16 of out * s, s the power of
+// two that puts the row's max |out| in [2^14, 2^15), zero past n up to ldx;
+// row_inv = 1 / s); the grid covers the padded rows (zeros, row_inv 1).
+struct PrefillRows {
+    _Float16* xh;
+    float* row_inv;
+    std::uint32_t rows;   // live rows; rows rows..mp-1 are padding
+    std::uint64_t ldx;    // f16 row stride (>= n, a multiple of 8)
+};
+
+template <bool SPLIT, bool LOAD, bool PF = false>
 __global__ __launch_bounds__(kNormThreads) void rms_norm_vec_kernel(float* x, const float* __restrict__ y,
                                                                     const float* __restrict__ w, float* out,
                                                                     std::uint64_t n, double eps, std::uint32_t splits,
                                                                     std::uint64_t split_stride,
-                                                                    const float* __restrict__ bias, NormLoad ld) {
+                                                                    const float* __restrict__ bias, NormLoad ld,
+                                                                    PrefillRows pf = PrefillRows{}) {
 #pragma clang fp contract(off)
     __shared__ double red[kNormThreads / 64];
     __shared__ float redf[kNormThreads / 64];
     const std::uint32_t r = blockIdx.x;
     const std::uint32_t t = threadIdx.x;
-    const bool mine = (!LOAD || r < ld.rows) && t < n / 8u;
+    const bool mine = (!LOAD || r < ld.rows) && (!PF || r < pf.rows) && t < n / 8u;
     const std::uint64_t at = static_cast<std::uint64_t>(r) * n + 8u * t;
     float4v v[2], g[2];
 #pragma unroll
@@ -609,7 +621,7 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_vec_kernel(float* x, co
         *reinterpret_cast<float4v*>(out + at) = float4v{o[0], o[1], o[2], o[3]};
         *reinterpret_cast<float4v*>(out + at + 4) = float4v{o[4], o[5], o[6], o[7]};
     }
-    if constexpr (LOAD) {
+    if constexpr (LOAD || PF) {
         float amax = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(o[e]));
@@ -621,8 +633,18 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_vec_kernel(float* x, co
         for (unsigned k = 1; k < kNormThreads / 64; ++k) amax = fmaxf(amax, redf[k]);
         float s, inv;
         block_scale(amax, s, inv);
-        if (t < 4u * ld.nb) emit_split_run(t, o, s, r, ld.mp, ld.xs, ld.block_sums);
-        if (t == 0) ld.inv_scale[r] = inv;
+        if constexpr (LOAD) {
+            if (t < 4u * ld.nb) emit_split_run(t, o, s, r, ld.mp, ld.xs, ld.block_sums);
+            if (t == 0) ld.inv_scale[r] = inv;
+        } else {
+            if (8u * t < pf.ldx) {
+                half8v h;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) h[e] = static_cast<_Float16>(mine ? o[e] * s : 0.0f);
+                *reinterpret_cast<half8v*>(pf.xh + static_cast<std::uint64_t>(r) * pf.ldx + 8u * t) = h;
+            }
+            if (t == 0) pf.row_inv[r] = inv;
+        }
     }
 }
 
@@ -656,6 +678,75 @@ __global__ __launch_bounds__(kThreads) void split_swiglu_kernel(const float4v* _
         }
         out[idx] = o;
     }
+}
+
+// silu_mul_kernel's SwiGLU over one padded row per workgroup with PF
+// emission as rms_norm_vec_kernel has it (the row's outputs held in
+// registers between the max and the conversion: f <= 24576).
+constexpr unsigned kSiluHeldRuns = 3;
+
+__global__ __launch_bounds__(kNormThreads) void silu_rows_prefill_kernel(const float* __restrict__ gate_up,
+                                                                         float* __restrict__ out, std::uint64_t f,
+                                                                         PrefillRows pf) {
+#pragma clang fp contract(off)
+    __shared__ float redf[kNormThreads / 64];
+    const std::uint32_t r = blockIdx.x;
+    const std::uint32_t t = threadIdx.x;
+    const bool row_live = r < pf.rows;
+    const std::uint64_t runs = f / 8u;
+    const float* row = gate_up + static_cast<std::uint64_t>(row_live ? r : 0u) * 2u * f;
+    float4v g[kSiluHeldRuns][2], u[kSiluHeldRuns][2];
+#pragma unroll
+    for (unsigned i = 0; i < kSiluHeldRuns; ++i) {
+        const std::uint64_t run = t + kNormThreads * i;
+        const std::uint64_t at = 8u * (run < runs ? run : 0u);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            g[i][h] = *reinterpret_cast<const float4v*>(row + at + 4 * h);
+            u[i][h] = *reinterpret_cast<const float4v*>(row + f + at + 4 * h);
+        }
+    }
+    float o[kSiluHeldRuns][8];
+    float amax = 0.0f;
+#pragma unroll
+    for (unsigned i = 0; i < kSiluHeldRuns; ++i) {
+        const std::uint64_t run = t + kNormThreads * i;
+        const bool live = row_live && run < runs;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float sg = g[i][h][e] / (1.0f + expf(-g[i][h][e]));
+                o[i][4 * h + e] = live ? sg * u[i][h][e] : 0.0f;
+            }
+        }
+        if (live) {
+            float* dst = out + static_cast<std::uint64_t>(r) * f + 8u * run;
+            *reinterpret_cast<float4v*>(dst) = float4v{o[i][0], o[i][1], o[i][2], o[i][3]};
+            *reinterpret_cast<float4v*>(dst + 4) = float4v{o[i][4], o[i][5], o[i][6], o[i][7]};
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(o[i][e]));
+    }
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    if ((t & 63u) == 0) redf[t >> 6] = amax;
+    __syncthreads();
+    amax = redf[0];
+#pragma unroll
+    for (unsigned k = 1; k < kNormThreads / 64; ++k) amax = fmaxf(amax, redf[k]);
+    float s, inv;
+    block_scale(amax, s, inv);
+#pragma unroll
+    for (unsigned i = 0; i < kSiluHeldRuns + 1u; ++i) {
+        // Runs past f (up to ldx) are zeros; f <= 24576 and ldx < f + 256.
+        const std::uint64_t run = t + kNormThreads * i;
+        if (8u * run >= pf.ldx) break;
+        half8v h;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = static_cast<_Float16>(i < kSiluHeldRuns ? o[i < kSiluHeldRuns ? i : 0][e] * s : 0.0f);
+        *reinterpret_cast<half8v*>(pf.xh + static_cast<std::uint64_t>(r) * pf.ldx + 8u * run) = h;
+    }
+    if (t == 0) pf.row_inv[r] = inv;
 }
 
 bool norm_vectorizable(const float* x, const float* y, const float* w, const float* out, std::uint64_t n) {
@@ -767,6 +858,37 @@ hipError_t launch_rope_kv_append(const KvLayout& kv, float* qkv, std::uint64_t s
                                  std::uint64_t table_positions, hipStream_t stream) {
     return rope_kv_append(kv, qkv, stride, q_width, m, positions, tables, layer, q_heads, kv_heads, head_dim,
                           rope_dims, table, table_positions, nullptr, stream);
+}
+
+bool prefill_norm_fits(std::uint64_t n, std::uint64_t ldx) {
+    return n % 8u == 0 && n <= 8u * static_cast<std::uint64_t>(kNormThreads) && ldx >= n && ldx % 8u == 0 &&
+           ldx <= 8u * static_cast<std::uint64_t>(kNormThreads);
+}
+
+hipError_t launch_rms_norm_prefill(float* x, const float* y, const float* w, float* out, std::uint32_t m,
+                                   std::uint64_t n, double eps, _Float16* xh, float* row_inv, std::uint32_t mp,
+                                   std::uint64_t ldx, hipStream_t stream) {
+    if (!prefill_norm_fits(n, ldx) || !norm_vectorizable(x, y, w, out, n) || mp < m) return hipErrorInvalidValue;
+    const PrefillRows pf{xh, row_inv, m, ldx};
+    hipLaunchKernelGGL((rms_norm_vec_kernel<false, false, true>), dim3(mp), dim3(kNormThreads), 0, stream, x, y, w,
+                       out, n, eps, 0u, std::uint64_t{0}, static_cast<const float*>(nullptr), NormLoad{}, pf);
+    return hipGetLastError();
+}
+
+bool silu_prefill_fits(std::uint64_t ffn, std::uint64_t ldx) {
+    return ffn % 8u == 0 && ffn <= 8u * kSiluHeldRuns * static_cast<std::uint64_t>(kNormThreads) && ldx >= ffn &&
+           ldx % 8u == 0 && ldx <= 8u * (kSiluHeldRuns + 1u) * static_cast<std::uint64_t>(kNormThreads);
+}
+
+hipError_t launch_silu_mul_prefill(const float* gate_up, float* out, std::uint32_t m, std::uint64_t ffn, _Float16* xh,
+                                   float* row_inv, std::uint32_t mp, std::uint64_t ldx, hipStream_t stream) {
+    const auto aligned = [](const void* p) { return reinterpret_cast<std::uintptr_t>(p) % 16u == 0; };
+    if (!silu_prefill_fits(ffn, ldx) || !aligned(gate_up) || !aligned(out) || !aligned(xh) || mp < m) {
+        return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(silu_rows_prefill_kernel, dim3(mp), dim3(kNormThreads), 0, stream, gate_up, out, ffn,
+                       PrefillRows{xh, row_inv, m, ldx});
+    return hipGetLastError();
 }
 
 hipError_t launch_silu_mul(const float* gate_up, float* out, std::uint32_t m, std::uint64_t ffn, hipStream_t stream) {

@@ -476,7 +476,16 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
     // buffer as large as the step's gate|up rows).  The q|k|v linear does
     // RoPE and the KV append the same way.
     const bool epilogues = tactic == QuantizedLinearExecutionKind::hip_decode && m <= AIR_HIP_MAX_DECODE_ROWS;
-    if ((rc = air_hip_rms_norm(ctx, hidden_, attn_norm_[0], normed_, m, embed_, eps)) != AIR_HIP_OK) {
+    // Prefill steps: the norms and the SwiGLU also leave the next prefill
+    // linear's f16 operand (air_hip_rms_norm_prefill, air_hip_silu_mul_prefill),
+    // so q|k|v, gate|up and down skip their conversion pass.
+    const bool prefill_operands = tactic == QuantizedLinearExecutionKind::hip_prefill;
+    const auto norm = [&](float* x, const float* y, const float* w, bool next_prefill) {
+        if (prefill_operands && next_prefill) return air_hip_rms_norm_prefill(ctx, x, y, w, normed_, m, embed_, eps);
+        return y ? air_hip_add_rms_norm(ctx, x, y, w, normed_, m, embed_, eps)
+                 : air_hip_rms_norm(ctx, x, w, normed_, m, embed_, eps);
+    };
+    if ((rc = norm(hidden_, nullptr, attn_norm_[0], true)) != AIR_HIP_OK) {
         return hip_status(rc);
     }
     for (std::uint32_t l = 0; l < c.layer_count; ++l) {
@@ -509,7 +518,7 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
             }
         } else {
             if (Status s = prepared_.linear(l, LinearRole::attn_output, att_, proj_, m, tactic); !s) return s;
-            if ((rc = air_hip_add_rms_norm(ctx, hidden_, proj_, ffn_norm_[l], normed_, m, embed_, eps)) != AIR_HIP_OK) {
+            if ((rc = norm(hidden_, proj_, ffn_norm_[l], true)) != AIR_HIP_OK) {
                 return hip_status(rc);
             }
         }
@@ -525,7 +534,9 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
                 !s) {
                 return s;
             }
-            if ((rc = air_hip_silu_mul(ctx, gate_up_, act_, m, ffn_)) != AIR_HIP_OK) return hip_status(rc);
+            rc = prefill_operands ? air_hip_silu_mul_prefill(ctx, gate_up_, act_, m, ffn_)
+                                  : air_hip_silu_mul(ctx, gate_up_, act_, m, ffn_);
+            if (rc != AIR_HIP_OK) return hip_status(rc);
         }
         const float* next_norm = l + 1U < c.layer_count ? attn_norm_[l + 1U] : output_norm_;
         if (epilogues) {
@@ -541,7 +552,7 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
             }
         } else {
             if (Status s = prepared_.linear(l, LinearRole::ffn_down, act_, proj_, m, tactic); !s) return s;
-            if ((rc = air_hip_add_rms_norm(ctx, hidden_, proj_, next_norm, normed_, m, embed_, eps)) != AIR_HIP_OK) {
+            if ((rc = norm(hidden_, proj_, next_norm, l + 1U < c.layer_count)) != AIR_HIP_OK) {
                 return hip_status(rc);
             }
         }

@@ -342,6 +342,19 @@ int air_hip_rms_norm(air_hip_context* ctx, const float* x, const float* weight, 
 int air_hip_add_rms_norm(air_hip_context* ctx, float* x, const float* y, const float* weight, float* out, uint32_t m,
                          uint64_t n, double eps);
 
+/* air_hip_add_rms_norm (y given) or air_hip_rms_norm (y NULL; out may then
+ * alias x), and out is also converted into the context's prefill
+ * workspace as the next prefill linear converts its f32 input (f16 rows,
+ * one power-of-two scale per row): the next linear this context runs on
+ * x == out with the prefill route, the same width and rows uses that
+ * operand instead of converting again (bit-identical).  Any other call
+ * through the context in between cancels it, as for
+ * AIR_HIP_EPILOGUE_RESIDUAL_LOAD.  Rows wider than 8192 get the plain norm.
+ * No counterpart in the reference: it replaces the norm and the conversion
+ * pass of the prefill GEMM's input. */
+int air_hip_rms_norm_prefill(air_hip_context* ctx, float* x, const float* y, const float* weight, float* out,
+                             uint32_t m, uint64_t n, double eps);
+
 /* In-place rotary embedding of the q and k heads of fused q|k|v rows
  * (apply_rope, reference_executor.cpp:37-72): row r (stride floats apart)
  * rotates by position positions[r] with table[position][i] = {cos, sin} of
@@ -441,6 +454,11 @@ int air_hip_attention_online(air_hip_context* ctx, const air_hip_kv_layout* kv, 
 /* out[r][i] = silu(gate_up[r][i]) * gate_up[r][ffn + i] over fused gate|up
  * rows (reference_executor.cpp:33-35, 400). */
 int air_hip_silu_mul(air_hip_context* ctx, const float* gate_up, float* out, uint32_t m, uint64_t ffn);
+
+/* air_hip_silu_mul with out also converted for the next prefill linear, as
+ * air_hip_rms_norm_prefill does (ffn up to 24576; wider rows get the plain
+ * SwiGLU).  No counterpart in the reference. */
+int air_hip_silu_mul_prefill(air_hip_context* ctx, const float* gate_up, float* out, uint32_t m, uint64_t ffn);
 
 /* x[i] += y[i] (the residual adds, add_in_place, reference_executor.cpp:29-31). */
 int air_hip_add(air_hip_context* ctx, float* x, const float* y, uint64_t count);

@@ -277,3 +277,83 @@ def test_prefill_remainder_launch_is_bit_identical(torch_cuda):
     finally:
         mat.release()
         ctx.close()
+
+
+@pytest.mark.parametrize("k,f,m", [(3584, 18944, 512), (96, 600, 70), (992, 200, 65)])
+def test_prefill_operand_from_norm_and_swiglu(torch_cuda, hip_ctx, k, f, m):
+    """air_hip_rms_norm_prefill and air_hip_silu_mul_prefill leave the next
+    prefill linear's f16 operand: that linear gives the bits of the plain
+    norm / SwiGLU followed by the linear converting its input itself, with
+    and without the residual add, at the 7B widths (k 3584, FFN 18944), at
+    widths whose f16 rows are padded (96, 600 and 992 -> 256, 768 and 1024
+    columns).  Another call in between cancels the operand (the linear
+    converts again and still matches)."""
+    torch = torch_cuda
+    lib = capi.lib()
+    h = hip_ctx.handle
+    pf = capi.LINEAR_PREFILL
+    canon_q = helpers.weights(capi.TYPE_Q8_0, k, 512, seed=k + 1)
+    mat_q = capi.Matrix(hip_ctx, capi.TYPE_Q8_0, k, 512, canon_q, canon_q.nbytes, on_device=False)
+    kf = (f + 31) // 32 * 32
+    canon_d = helpers.weights(capi.TYPE_Q8_0, kf, 256, seed=f + 2) if kf == f else None
+    mat_d = capi.Matrix(hip_ctx, capi.TYPE_Q8_0, f, 256, canon_d, canon_d.nbytes, on_device=False) if kf == f else None
+
+    def bits(t):
+        return t.cpu().numpy().view(np.uint32)
+
+    try:
+        w = _dev(torch, helpers.activations(1, k, seed=k + 3)[0])
+        x0 = _dev(torch, helpers.activations(m, k, seed=m + 4) * 3.0)
+        resid = _dev(torch, helpers.activations(m, k, seed=m + 5))
+        for with_resid in (False, True):
+            # reference: plain norm, then the linear converting its input
+            xa = x0.clone()
+            normed_ref = torch.empty((m, k), dtype=torch.float32, device="cuda:0")
+            if with_resid:
+                capi.check(lib.air_hip_add_rms_norm(h, xa.data_ptr(), resid.data_ptr(), w.data_ptr(),
+                                                    normed_ref.data_ptr(), m, k, 1e-6))
+            else:
+                capi.check(lib.air_hip_rms_norm(h, xa.data_ptr(), w.data_ptr(), normed_ref.data_ptr(), m, k, 1e-6))
+            y_ref = torch.empty((m, 512), dtype=torch.float32, device="cuda:0")
+            mat_q.linear(normed_ref, y_ref, m, tactic=pf)
+            # fused: the norm leaves the operand
+            xb = x0.clone()
+            normed = torch.full((m, k), float("nan"), dtype=torch.float32, device="cuda:0")
+            capi.check(lib.air_hip_rms_norm_prefill(h, xb.data_ptr(), resid.data_ptr() if with_resid else None,
+                                                    w.data_ptr(), normed.data_ptr(), m, k, 1e-6))
+            y = torch.full((m, 512), float("nan"), dtype=torch.float32, device="cuda:0")
+            mat_q.linear(normed, y, m, tactic=pf)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(normed), bits(normed_ref)), (k, m, with_resid)
+            assert np.array_equal(bits(xb), bits(xa)), (k, m, with_resid)
+            assert np.array_equal(bits(y), bits(y_ref)), (k, m, with_resid)
+            # another call in between: the operand is not used, the result still matches
+            capi.check(lib.air_hip_rms_norm_prefill(h, xb.data_ptr(), None, w.data_ptr(), normed.data_ptr(), m, k,
+                                                    1e-6))
+            normed.mul_(2.0)
+            capi.check(lib.air_hip_rms_norm(h, normed.data_ptr(), w.data_ptr(), normed.data_ptr(), m, k, 1e-6))
+            fresh = normed.clone()
+            mat_q.linear(normed, y, m, tactic=pf)
+            mat_q.linear(fresh, y_ref, m, tactic=pf)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(y), bits(y_ref)), (k, m, "cancelled")
+        # SwiGLU
+        gu = _dev(torch, helpers.activations(m, 2 * f, seed=f + 6) * 2.0)
+        act_ref = torch.empty((m, f), dtype=torch.float32, device="cuda:0")
+        capi.check(lib.air_hip_silu_mul(h, gu.data_ptr(), act_ref.data_ptr(), m, f))
+        act = torch.full((m, f), float("nan"), dtype=torch.float32, device="cuda:0")
+        capi.check(lib.air_hip_silu_mul_prefill(h, gu.data_ptr(), act.data_ptr(), m, f))
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(act), bits(act_ref)), (f, m)
+        if mat_d is not None:
+            y_ref = torch.empty((m, 256), dtype=torch.float32, device="cuda:0")
+            capi.check(lib.air_hip_silu_mul_prefill(h, gu.data_ptr(), act.data_ptr(), m, f))
+            yd = torch.full((m, 256), float("nan"), dtype=torch.float32, device="cuda:0")
+            mat_d.linear(act, yd, m, tactic=pf)
+            mat_d.linear(act_ref, y_ref, m, tactic=pf)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(yd), bits(y_ref)), (f, m)
+    finally:
+        mat_q.release()
+        if mat_d is not None:
+            mat_d.release()
