@@ -36,6 +36,7 @@ EPILOGUE_STORE = 0
 EPILOGUE_RESIDUAL = 1
 EPILOGUE_SWIGLU = 2
 EPILOGUE_RESIDUAL_LOAD = 3
+EPILOGUE_RESIDUAL_PREFILL = 4
 
 LINEAR_AUTO = 0
 LINEAR_DECODE = 1

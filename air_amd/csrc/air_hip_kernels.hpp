@@ -6,6 +6,8 @@
 
 namespace air_hip {
 
+struct SplitEpilogue;  // below, with the step kernels
+
 // Resident planes of one matrix in the wavefront tile layout.
 struct TilePlanes {
     int type{0};
@@ -128,13 +130,18 @@ struct PrefillShape {
 PrefillShape plan_prefill(const TilePlanes& planes, std::uint32_t m, const PrefillTuning& tuning);
 // Workspace of one prefill linear: f16 activations, row scales and (with a K
 // split) the f32 partials.
-// Padded f16 row stride and padded row count of the prefill operand.
+// Padded f16 row stride and padded row count of the prefill operand, and
+// the byte offset of the K-split partials after the operand in the workspace.
 std::uint64_t prefill_ldx(std::uint64_t k);
 std::uint32_t prefill_rows_padded(std::uint32_t m);
+std::uint64_t prefill_partials_offset(std::uint64_t k, std::uint32_t m);
 std::uint64_t prefill_workspace_bytes(std::uint64_t k, std::uint32_t m, const PrefillShape& shape, std::uint64_t n);
+// With `epilogue`, a K-split launch's reduction applies it instead of
+// writing y (the caller checks split_epilogue_fits on the partials, which
+// follow the operand in the workspace).
 hipError_t launch_prefill_linear(const TilePlanes& planes, const float* x, const float* bias, float* y,
                                  std::uint32_t m, const PrefillShape& shape, void* workspace, hipStream_t stream,
-                                 bool converted = false);
+                                 bool converted = false, const SplitEpilogue* epilogue = nullptr);
 // y[m][n] = sum over splits of partials[s][m][n] (in split order) + bias[n].
 hipError_t launch_split_reduce(const float* partials, std::uint32_t splits, std::uint32_t m, std::uint64_t n,
                                const float* bias, float* y, hipStream_t stream);
@@ -148,7 +155,6 @@ hipError_t launch_split_activations_rows(const float* x, std::uint32_t m, std::u
 // Skinny decode linear (M = 1..64) over split activations: activations staged
 // once per workgroup in LDS, exact weight codes streamed per wave, optional K
 // split with a deterministic reduction.
-struct SplitEpilogue;  // below, with the step kernels
 struct SkinnyShape {
     std::uint32_t mt{1};       // 16-row activation tiles (all M rows)
     std::uint32_t tile_n{1};   // 16-row weight tiles per wave (1 or 2)
@@ -275,6 +281,13 @@ struct RopeKvArgs {
     const void* table{nullptr};
     std::uint64_t table_positions{0};
 };
+// The f16 operand area of a prefill linear (xh [mp][ldx], row_inv [mp]).
+struct PrefillOperandArgs {
+    _Float16* xh{nullptr};
+    float* row_inv{nullptr};
+    std::uint32_t mp{0};
+    std::uint64_t ldx{0};
+};
 struct SplitEpilogue {
     int kind{0};
     float* out{nullptr};
@@ -284,6 +297,9 @@ struct SplitEpilogue {
     const RopeKvArgs* rope{nullptr};
     const SplitWorkspace* load{nullptr};
     std::uint32_t load_blocks{0};
+    // kEpilogueResidual with a norm: norm_out also converted into this
+    // prefill operand (as launch_rms_norm_prefill converts it).
+    const PrefillOperandArgs* prefill{nullptr};
 };
 // Whether the reduction can carry `e` for this shape (alignment, widths).
 bool split_epilogue_fits(const SplitEpilogue& e, const float* partials, const float* bias, std::uint32_t m,

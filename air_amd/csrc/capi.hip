@@ -220,18 +220,48 @@ int ensure_prefill_workspace(air_hip_context* ctx, std::uint64_t bytes, bool kee
     return grow_buffer(ctx, &ctx->prefill_workspace, &ctx->prefill_workspace_bytes, bytes, "prefill workspace", keep);
 }
 
+// The prefill workspace's operand area for rows of width k: xh then row_inv
+// (the layout launch_prefill_linear reads).
+using PrefillOperand = PrefillOperandArgs;
+
+int prefill_operand(air_hip_context* ctx, std::uint64_t k, std::uint32_t m, PrefillOperand* op) {
+    const std::uint64_t mp = prefill_rows_padded(m);
+    const std::uint64_t ldx = prefill_ldx(k);
+    const std::uint64_t xh_bytes = ceil_div(mp * ldx * 2u, 256u) * 256u;
+    const int rc = ensure_prefill_workspace(ctx, xh_bytes + ceil_div(mp * 4u, 256u) * 256u);
+    if (rc != AIR_HIP_OK) return rc;
+    auto* base = static_cast<std::uint8_t*>(ctx->prefill_workspace);
+    *op = PrefillOperand{reinterpret_cast<_Float16*>(base), reinterpret_cast<float*>(base + xh_bytes),
+                         static_cast<std::uint32_t>(mp), ldx};
+    return AIR_HIP_OK;
+}
+
+void remember_prefill(air_hip_context* ctx, const void* source, std::uint64_t k, std::uint32_t m) {
+    ctx->prefill_source = source;
+    ctx->prefill_source_k = k;
+    ctx->prefill_source_rows = m;
+}
+
 // Prefill linear: x [rows][k] -> y [rows][n] on the f16 MFMA GEMM; `ready`
 // (taken by the linear entry point) names rows whose f16 operand the call
 // before left in the workspace, which then skips the conversion.
 int run_prefill(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y, const float* bias,
                 std::uint32_t rows, const void* ready = nullptr, std::uint64_t ready_k = 0,
-                std::uint32_t ready_rows = 0) {
+                std::uint32_t ready_rows = 0, const SplitEpilogue* epilogue = nullptr, bool* applied = nullptr) {
     const PrefillShape shape = plan_prefill(m->planes, rows, ctx->prefill_tuning);
     const bool converted = ready == x && ready_k == m->planes.k && ready_rows == rows;
     int rc = ensure_prefill_workspace(ctx, prefill_workspace_bytes(m->planes.k, rows, shape, m->planes.n), converted);
     if (rc != AIR_HIP_OK) return rc;
+    // A K-split launch's reduction carries the epilogue when it fits.
+    const auto* partials = reinterpret_cast<const float*>(static_cast<const std::uint8_t*>(ctx->prefill_workspace) +
+                                                          prefill_partials_offset(m->planes.k, rows));
+    const SplitEpilogue* epi = epilogue && applied && shape.splits > 1u &&
+                                       split_epilogue_fits(*epilogue, partials, bias, rows, m->planes.n)
+                                   ? epilogue
+                                   : nullptr;
+    if (epi) *applied = true;
     const hipError_t err = launch_prefill_linear(m->planes, x, bias, y, rows, shape, ctx->prefill_workspace, ctx->stream,
-                                                 converted);
+                                                 converted, epi);
     if (err != hipSuccess) return hip_fail(err, "prefill_gemm_kernel");
     ctx->prefill_linear_calls.fetch_add(1, std::memory_order_relaxed);
     ctx->prefill_rows.fetch_add(rows, std::memory_order_relaxed);
@@ -807,7 +837,8 @@ int linear_rows(air_hip_context* ctx, const air_hip_matrix* m, const float* x, f
         if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
         DeviceScope scope(ctx->device);
         if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-        return run_prefill(ctx, m, x, y, bias, rows, prefill_ready, ctx->prefill_source_k, ctx->prefill_source_rows);
+        return run_prefill(ctx, m, x, y, bias, rows, prefill_ready, ctx->prefill_source_k, ctx->prefill_source_rows,
+                           epilogue, applied);
     }
     if (route == Route::decode_linear) {
         int rc = load_activations_for(ctx, x, m->planes.k, rows, ready);
@@ -1005,13 +1036,16 @@ int air_hip_linear_epilogue(air_hip_context* ctx, const air_hip_matrix* m, const
                             int tactic) {
     if (!ctx || !m || !x || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix, x and out must not be null");
     if (epilogue != AIR_HIP_EPILOGUE_RESIDUAL && epilogue != AIR_HIP_EPILOGUE_SWIGLU &&
-        epilogue != AIR_HIP_EPILOGUE_RESIDUAL_LOAD) {
-        return fail(AIR_HIP_INVALID_ARGUMENT, "epilogue must be RESIDUAL, SWIGLU or RESIDUAL_LOAD, not %d", epilogue);
+        epilogue != AIR_HIP_EPILOGUE_RESIDUAL_LOAD && epilogue != AIR_HIP_EPILOGUE_RESIDUAL_PREFILL) {
+        return fail(AIR_HIP_INVALID_ARGUMENT,
+                    "epilogue must be RESIDUAL, SWIGLU, RESIDUAL_LOAD or RESIDUAL_PREFILL, not %d", epilogue);
     }
     const bool load = epilogue == AIR_HIP_EPILOGUE_RESIDUAL_LOAD;
+    const bool prefill_out = epilogue == AIR_HIP_EPILOGUE_RESIDUAL_PREFILL;
     if (load && (!norm_weight || m->planes.n % 32u != 0u)) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "RESIDUAL_LOAD needs a norm and an output width that is a multiple of 32");
     }
+    if (prefill_out && !norm_weight) return fail(AIR_HIP_INVALID_ARGUMENT, "RESIDUAL_PREFILL needs a norm");
     if (static_cast<const void*>(x) == static_cast<const void*>(out)) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "out must not alias x");
     }
@@ -1049,9 +1083,54 @@ int air_hip_linear_epilogue(air_hip_context* ctx, const air_hip_matrix* m, const
             e.load_blocks = static_cast<std::uint32_t>(kp_out / 32u);
         }
     }
+    // RESIDUAL_PREFILL: the prefill workspace holds norm_out's f16 operand
+    // afterwards.  Reserved first for this linear too (so it cannot move after
+    // the pointers are taken); carried by a prefill reduction only when that
+    // operand ends before the partials it reads.
+    PrefillOperandArgs pf_args{};
+    const std::uint64_t pf_ldx = prefill_ldx(n);
+    const std::uint64_t pf_mp = prefill_rows_padded(rows);
+    const std::uint64_t pf_xh_bytes = ceil_div(pf_mp * pf_ldx * 2u, 256u) * 256u;
+    const std::uint64_t pf_bytes = pf_xh_bytes + ceil_div(pf_mp * 4u, 256u) * 256u;
+    const bool prefill_route = route_linear(ctx, m, rows, tactic) == Route::prefill;
+    if (prefill_out && prefill_route && prefill_norm_fits(n, pf_ldx) && rows <= kMaxRows) {
+        const PrefillShape shape = plan_prefill(m->planes, rows, ctx->prefill_tuning);
+        rc = ensure_prefill_workspace(
+            ctx, std::max(prefill_workspace_bytes(m->planes.k, rows, shape, m->planes.n), pf_bytes),
+            ctx->prefill_source != nullptr);
+        if (rc != AIR_HIP_OK) return rc;
+        if (pf_bytes <= prefill_partials_offset(m->planes.k, rows)) {
+            auto* base = static_cast<std::uint8_t*>(ctx->prefill_workspace);
+            pf_args = PrefillOperandArgs{reinterpret_cast<_Float16*>(base), reinterpret_cast<float*>(base + pf_xh_bytes),
+                                         static_cast<std::uint32_t>(pf_mp), pf_ldx};
+            e.prefill = &pf_args;
+        }
+    }
     bool applied = false;
     rc = linear_rows(ctx, m, x, y, bias, rows, tactic, &e, &applied);
     if (rc != AIR_HIP_OK) return rc;
+    if (prefill_out) {
+        if (applied) {
+            remember_prefill(ctx, norm_out, n, rows);
+            return AIR_HIP_OK;
+        }
+        // The linear wrote y: the residual add and the norm with the operand.
+        PrefillOperand op{};
+        hipError_t err = hipErrorInvalidValue;
+        if (prefill_norm_fits(n, pf_ldx) && rows <= kMaxRows) {
+            rc = prefill_operand(ctx, n, rows, &op);
+            if (rc != AIR_HIP_OK) return rc;
+            err = launch_rms_norm_prefill(out, y, norm_weight, norm_out, rows, n, eps, op.xh, op.row_inv, op.mp, op.ldx,
+                                          ctx->stream);
+            if (err == hipSuccess) {
+                remember_prefill(ctx, norm_out, n, rows);
+                return AIR_HIP_OK;
+            }
+            if (err != hipErrorInvalidValue) return hip_fail(err, "rms_norm_vec_kernel");
+        }
+        err = launch_add_rms_norm(out, y, norm_weight, norm_out, rows, n, eps, ctx->stream);
+        return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "linear epilogue");
+    }
     if (!applied) {
         hipError_t err;
         if (epilogue == AIR_HIP_EPILOGUE_SWIGLU) {
@@ -1063,10 +1142,12 @@ int air_hip_linear_epilogue(air_hip_context* ctx, const air_hip_matrix* m, const
         }
         if (err != hipSuccess) return hip_fail(err, "linear epilogue");
         if (load && (rc = air_hip_activations_load(ctx, norm_out, n, rows)) != AIR_HIP_OK) return rc;
-    } else if (load) {
+    } else if (load && e.load) {
         ctx->loaded_k = n;
         ctx->loaded_rows = rows;
         ctx->loaded_row_scaled = true;
+    } else if (load && (rc = air_hip_activations_load(ctx, norm_out, n, rows)) != AIR_HIP_OK) {
+        return rc;   // a prefill reduction applied the norm without the split
     }
     if (load) ctx->loaded_source = norm_out;
     return AIR_HIP_OK;
@@ -1111,33 +1192,6 @@ int air_hip_add_rms_norm(air_hip_context* ctx, float* x, const float* y, const f
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
     const hipError_t err = launch_add_rms_norm(x, y, weight, out, m, n, eps, ctx->stream);
     return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "rms_norm_vec_kernel");
-}
-
-// The prefill workspace's operand area for rows of width k: xh then row_inv
-// (the layout launch_prefill_linear reads).
-struct PrefillOperand {
-    _Float16* xh;
-    float* row_inv;
-    std::uint32_t mp;
-    std::uint64_t ldx;
-};
-
-int prefill_operand(air_hip_context* ctx, std::uint64_t k, std::uint32_t m, PrefillOperand* op) {
-    const std::uint64_t mp = prefill_rows_padded(m);
-    const std::uint64_t ldx = prefill_ldx(k);
-    const std::uint64_t xh_bytes = ceil_div(mp * ldx * 2u, 256u) * 256u;
-    const int rc = ensure_prefill_workspace(ctx, xh_bytes + ceil_div(mp * 4u, 256u) * 256u);
-    if (rc != AIR_HIP_OK) return rc;
-    auto* base = static_cast<std::uint8_t*>(ctx->prefill_workspace);
-    *op = PrefillOperand{reinterpret_cast<_Float16*>(base), reinterpret_cast<float*>(base + xh_bytes),
-                         static_cast<std::uint32_t>(mp), ldx};
-    return AIR_HIP_OK;
-}
-
-void remember_prefill(air_hip_context* ctx, const void* source, std::uint64_t k, std::uint32_t m) {
-    ctx->prefill_source = source;
-    ctx->prefill_source_k = k;
-    ctx->prefill_source_rows = m;
 }
 
 int air_hip_rms_norm_prefill(air_hip_context* ctx, float* x, const float* y, const float* weight, float* out,

@@ -654,7 +654,8 @@ std::uint64_t prefill_workspace_bytes(std::uint64_t k, std::uint32_t m, const Pr
 }
 
 hipError_t launch_prefill_linear(const TilePlanes& p, const float* x, const float* bias, float* y, std::uint32_t m,
-                                 const PrefillShape& shape, void* workspace, hipStream_t stream, bool converted) {
+                                 const PrefillShape& shape, void* workspace, hipStream_t stream, bool converted,
+                                 const SplitEpilogue* epilogue) {
     const std::uint64_t mp = prefill_rows_padded(m);
     const std::uint64_t ldx = prefill_ldx(p.k);
     auto* base = static_cast<std::uint8_t*>(workspace);
@@ -720,7 +721,13 @@ hipError_t launch_prefill_linear(const TilePlanes& p, const float* x, const floa
         err = launch(r, rem);
     }
     if (err != hipSuccess || !split) return err;
+    if (epilogue) return launch_split_epilogue(partials, shape.splits, m, p.n, bias, *epilogue, stream);
     return launch_split_reduce(partials, shape.splits, m, p.n, bias, y, stream);
+}
+
+std::uint64_t prefill_partials_offset(std::uint64_t k, std::uint32_t m) {
+    const std::uint64_t mp = prefill_rows_padded(m);
+    return ceil_div(mp * prefill_ldx(k) * 2u, 256u) * 256u + ceil_div(mp * 4u, 256u) * 256u;
 }
 
 hipError_t launch_split_reduce(const float* partials, std::uint32_t splits, std::uint32_t m, std::uint64_t n,

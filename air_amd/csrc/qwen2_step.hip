@@ -913,7 +913,9 @@ bool split_epilogue_fits(const SplitEpilogue& e, const float* partials, const fl
     if (e.kind == kEpilogueResidual) {
         return n % 8u == 0 && n <= 8u * static_cast<std::uint64_t>(kNormThreads) &&
                (!e.norm_weight || (aligned(e.norm_weight) && aligned(e.norm_out))) &&
-               (!e.load || (e.norm_weight && m <= 64u && 4u * e.load_blocks <= kNormThreads));
+               (!e.load || (e.norm_weight && m <= 64u && 4u * e.load_blocks <= kNormThreads)) &&
+               (!e.prefill || (e.norm_weight && !e.load && e.prefill->mp >= m && aligned(e.prefill->xh) &&
+                               prefill_norm_fits(n, e.prefill->ldx)));
     }
     return false;
 }
@@ -936,6 +938,13 @@ hipError_t launch_split_epilogue(const float* partials, std::uint32_t splits, st
                            dim3(kThreads), 0, stream, reinterpret_cast<const float4v*>(partials), splits,
                            static_cast<std::uint32_t>(static_cast<std::uint64_t>(m) * n / 4u), total4, f4,
                            reinterpret_cast<const float4v*>(bias), reinterpret_cast<float4v*>(e.out));
+        return hipGetLastError();
+    }
+    if (e.prefill) {
+        const PrefillRows pf{e.prefill->xh, e.prefill->row_inv, m, e.prefill->ldx};
+        hipLaunchKernelGGL((rms_norm_vec_kernel<true, false, true>), dim3(e.prefill->mp), dim3(kNormThreads), 0,
+                           stream, e.out, partials, e.norm_weight, e.norm_out, n, e.eps, splits,
+                           static_cast<std::uint64_t>(m) * n, bias, NormLoad{}, pf);
         return hipGetLastError();
     }
     if (e.load) {

@@ -471,10 +471,14 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
     // input of the next projection.  Decode widths up to 64 hand the add +
     // norm and the SwiGLU to the linear itself (air_hip_linear_epilogue),
     // whose split reduction carries them: measured on the 7B shapes at
-    // M = 30 that saves three launches of 4-5 us per layer.  Prefill widths
-    // keep the separate kernels (the epilogue route would add a context
-    // buffer as large as the step's gate|up rows).  The q|k|v linear does
-    // RoPE and the KV append the same way.
+    // M = 30 that saves three launches of 4-5 us per layer.  Prefill steps
+    // hand the add + norm to o's reduction (its GEMM splits K two ways;
+    // measured at M = 512: 45.9 us against 46.8 for the reduction and the
+    // norm).  A row per workgroup summing down's eight splits, or q|k|v's
+    // two for the RoPE and the KV append, is slower than the wide reduction
+    // and the separate kernel (down 125.9 vs 121.1 us, RoPE 18.4 vs 15.6),
+    // and the SwiGLU would need a context buffer as large as the step's
+    // gate|up rows; those stay separate.
     const bool epilogues = tactic == QuantizedLinearExecutionKind::hip_decode && m <= AIR_HIP_MAX_DECODE_ROWS;
     // Prefill steps: the norms and the SwiGLU also leave the next prefill
     // linear's f16 operand (air_hip_rms_norm_prefill, air_hip_silu_mul_prefill),
@@ -513,6 +517,15 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
                                                                         : AIR_HIP_EPILOGUE_RESIDUAL;
             if (Status s = prepared_.linear_epilogue(l, LinearRole::attn_output, att_, m, hidden_, o_epilogue,
                                                      ffn_norm_[l], normed_, eps, tactic);
+                !s) {
+                return s;
+            }
+        } else if (prefill_operands) {
+            // Prefill: o's K-split reduction does the residual add and the
+            // norm, and leaves gate|up's f16 operand.
+            if (Status s = prepared_.linear_epilogue(l, LinearRole::attn_output, att_, m, hidden_,
+                                                     AIR_HIP_EPILOGUE_RESIDUAL_PREFILL, ffn_norm_[l], normed_, eps,
+                                                     tactic);
                 !s) {
                 return s;
             }

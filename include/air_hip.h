@@ -283,7 +283,8 @@ enum {
     AIR_HIP_EPILOGUE_STORE = 0,
     AIR_HIP_EPILOGUE_RESIDUAL = 1,
     AIR_HIP_EPILOGUE_SWIGLU = 2,
-    AIR_HIP_EPILOGUE_RESIDUAL_LOAD = 3
+    AIR_HIP_EPILOGUE_RESIDUAL_LOAD = 3,
+    AIR_HIP_EPILOGUE_RESIDUAL_PREFILL = 4
 };
 int air_hip_decode_linear_fused(air_hip_context* ctx, const air_hip_matrix* matrix, const float* x, float* y,
                                 const float* bias, const float* norm_weight, double eps, int epilogue);
@@ -305,11 +306,15 @@ int air_hip_decode_linear_fused(air_hip_context* ctx, const air_hip_matrix* matr
  *     this context that writes device memory cancels it (that linear then
  *     splits norm_out itself); changing norm_out by other means in between
  *     is the caller's error.
+ *   AIR_HIP_EPILOGUE_RESIDUAL_PREFILL: RESIDUAL with its norm (required), and
+ *     norm_out is also converted for the next prefill linear as
+ *     air_hip_rms_norm_prefill converts it, with the same reuse rules.
+ *     Prefill-width linears with a K split carry it in their reduction.
  * Bit-identical to air_hip_linear (same tactic) followed by that call.  Where
- * the linear runs as a skinny launch with a K split (decode widths 2..64),
- * its split reduction applies the epilogue, so the epilogue costs no launch
- * of its own; other routes run the linear into a context buffer and the
- * separate kernel.  out must not alias x.  No counterpart in the reference's
+ * the linear runs with a K split (a skinny launch at decode widths 2..64,
+ * or a prefill GEMM), its split reduction
+ * applies the epilogue, so the epilogue costs no launch of its own; other
+ * routes run the linear into a context buffer and the separate kernel.  out must not alias x.  No counterpart in the reference's
  * linear API: it replaces the executor's linear then add / SiLU sequence
  * (cuda_backend.cu:789, 849-860). */
 int air_hip_linear_epilogue(air_hip_context* ctx, const air_hip_matrix* matrix, const float* x, uint32_t rows,
@@ -398,9 +403,9 @@ int air_hip_rope_kv_append(air_hip_context* ctx, const air_hip_kv_layout* kv, fl
  * (n = (q_heads + 2 * kv_heads) * head_dim) receives x W^T + bias with the q
  * and k heads rotated, and k, v are appended to the pool -- bit-identical to
  * air_hip_linear (same tactic) followed by air_hip_rope_kv_append over rows
- * of stride n.  Where the linear runs as a skinny launch with a K split
- * (decode widths 2..64), its split reduction does the RoPE and the append,
- * so they cost no launch of their own.  qkv must not alias x.  Replaces the
+ * of stride n.  Where the linear runs with a K split (a skinny launch at
+ * decode widths 2..64, or a prefill GEMM), its split reduction does the RoPE
+ * and the append, so they cost no launch of their own.  qkv must not alias x.  Replaces the
  * executor's q|k|v projection, apply_rope and KV store sequence
  * (cuda_backend.cu:883-906, 1156-1173; reference_executor.cpp:37-72). */
 int air_hip_linear_rope_kv(air_hip_context* ctx, const air_hip_matrix* matrix, const float* x, uint32_t rows,

@@ -245,10 +245,10 @@ def test_rope_kv_append_matches_separate_calls(torch_cuda, hip_ctx, q_heads, kv_
 def test_linear_rope_kv_matches_separate_calls(torch_cuda, hip_ctx, q_heads, kv_heads, head, rope_dims):
     """air_hip_linear_rope_kv leaves q|k|v and the pool bit-identical to
     air_hip_linear then air_hip_rope_kv_append, on the routes where the
-    linear's split reduction does the RoPE and the append (skinny kernel
-    with a K split) and where it does not (no split, the single-launch
-    kernel); rows as in the test above (past the table, no page, negative
-    position)."""
+    linear's split reduction does the RoPE and the append (skinny kernel or
+    prefill GEMM with a K split) and where it does not (no split, the
+    single-launch kernel); rows as in the test above (past the table, no
+    page, negative position)."""
     torch = torch_cuda
     dev = torch.device("cuda:0")
     page_tokens, layers, layer, max_pages, pool_pages = 16, 3, 1, 4, 12
@@ -273,8 +273,13 @@ def test_linear_rope_kv_matches_separate_calls(torch_cuda, hip_ctx, q_heads, kv_
     lib = capi.lib()
     h = hip_ctx.handle
     try:
-        for path in [(0, 0, 0), (2, 1, 1), (2, 1, 3), (2, 2, 2)]:
+        # decode routes (skinny with and without a K split, the fused kernel),
+        # then the prefill GEMM without and with a K split
+        runs = [(capi.LINEAR_DECODE, p, 0) for p in [(0, 0, 0), (2, 1, 1), (2, 1, 3), (2, 2, 2)]]
+        runs += [(capi.LINEAR_PREFILL, (0, 0, 0), s) for s in (1, 2)]
+        for tactic, path, pf_splits in runs:
             hip_ctx.set_decode_path(*path)
+            hip_ctx.set_prefill_tuning(0, 0, pf_splits, 0)
             outs = []
             for fused in (False, True):
                 pool = torch.from_numpy(pool_h).to(dev)
@@ -284,11 +289,10 @@ def test_linear_rope_kv_matches_separate_calls(torch_cuda, hip_ctx, q_heads, kv_
                     capi.check(lib.air_hip_linear_rope_kv(h, mat.handle, x.data_ptr(), m, qkv.data_ptr(),
                                                           bias.data_ptr(), ctypes.byref(kv), pos_d.data_ptr(),
                                                           tab_d.data_ptr(), layer, q_heads, kv_heads, head,
-                                                          rope_dims, rope_d.data_ptr(), table_positions,
-                                                          capi.LINEAR_DECODE))
+                                                          rope_dims, rope_d.data_ptr(), table_positions, tactic))
                 else:
                     capi.check(lib.air_hip_linear(h, mat.handle, x.data_ptr(), qkv.data_ptr(), bias.data_ptr(), m,
-                                                  capi.LINEAR_DECODE))
+                                                  tactic))
                     capi.check(lib.air_hip_rope_kv_append(h, ctypes.byref(kv), qkv.data_ptr(), n, m,
                                                           pos_d.data_ptr(), tab_d.data_ptr(), layer, q_heads,
                                                           kv_heads, head, rope_dims, rope_d.data_ptr(),
@@ -296,13 +300,15 @@ def test_linear_rope_kv_matches_separate_calls(torch_cuda, hip_ctx, q_heads, kv_
                 torch.cuda.synchronize()
                 outs.append((qkv.cpu().numpy(), pool.cpu().numpy()))
             (q0, p0), (q1, p1) = outs
-            assert not np.array_equal(p0, pool_h), path
-            assert np.array_equal(q1.view(np.uint32), q0.view(np.uint32)), path
-            assert np.array_equal(p1.view(np.uint32), p0.view(np.uint32)), path
+            case = (tactic, path, pf_splits)
+            assert not np.array_equal(p0, pool_h), case
+            assert np.array_equal(q1.view(np.uint32), q0.view(np.uint32)), case
+            assert np.array_equal(p1.view(np.uint32), p0.view(np.uint32)), case
         bad = lib.air_hip_linear_rope_kv(h, mat.handle, x.data_ptr(), m, qkv.data_ptr(), None, ctypes.byref(kv),
                                          pos_d.data_ptr(), tab_d.data_ptr(), layer, q_heads + 1, kv_heads, head,
                                          rope_dims, rope_d.data_ptr(), table_positions, capi.LINEAR_DECODE)
         assert bad == 1 and b"q|k|v" in lib.air_hip_last_error()
     finally:
         hip_ctx.set_decode_path(0)
+        hip_ctx.set_prefill_tuning(0, 0, 0, 0)
         mat.release()

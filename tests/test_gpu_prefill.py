@@ -357,3 +357,56 @@ def test_prefill_operand_from_norm_and_swiglu(torch_cuda, hip_ctx, k, f, m):
         mat_q.release()
         if mat_d is not None:
             mat_d.release()
+
+
+@pytest.mark.parametrize("k,n,m,splits", [(3584, 3584, 512, 0), (2048, 1024, 100, 4), (1024, 512, 65, 1)])
+def test_prefill_residual_epilogues(torch_cuda, hip_ctx, k, n, m, splits):
+    """air_hip_linear_epilogue on the prefill tactic: RESIDUAL and
+    RESIDUAL_PREFILL give the bits of the prefill linear followed by
+    air_hip_add_rms_norm, with the K split's reduction carrying them (auto
+    and forced splits) and without a split; RESIDUAL_PREFILL also leaves the
+    next prefill linear's operand (that linear matches the same linear on
+    the separately normed rows)."""
+    torch = torch_cuda
+    lib = capi.lib()
+    h = hip_ctx.handle
+    pf = capi.LINEAR_PREFILL
+    canon = helpers.weights(capi.TYPE_Q8_0, k, n, seed=k + n + 13)
+    mat = capi.Matrix(hip_ctx, capi.TYPE_Q8_0, k, n, canon, canon.nbytes, on_device=False)
+    canon2 = helpers.weights(capi.TYPE_Q8_0, n, 640, seed=n + 17)
+    mat2 = capi.Matrix(hip_ctx, capi.TYPE_Q8_0, n, 640, canon2, canon2.nbytes, on_device=False)
+
+    def bits(t):
+        return t.cpu().numpy().view(np.uint32)
+
+    try:
+        hip_ctx.set_prefill_tuning(0, 0, splits, 0)
+        x = _dev(torch, helpers.activations(m, k, seed=m + k) * 2.0)
+        resid0 = _dev(torch, helpers.activations(m, n, seed=m + 7))
+        bias = _dev(torch, helpers.activations(1, n, seed=k + 3)[0] * 0.1)
+        w = _dev(torch, helpers.activations(1, n, seed=k + 2)[0])
+        lin = torch.empty((m, n), dtype=torch.float32, device="cuda:0")
+        capi.check(lib.air_hip_linear(h, mat.handle, x.data_ptr(), lin.data_ptr(), bias.data_ptr(), m, pf))
+        resid_ref = resid0.clone()
+        normed_ref = torch.empty((m, n), dtype=torch.float32, device="cuda:0")
+        capi.check(lib.air_hip_add_rms_norm(h, resid_ref.data_ptr(), lin.data_ptr(), w.data_ptr(),
+                                            normed_ref.data_ptr(), m, n, 1e-6))
+        y2_ref = torch.empty((m, 640), dtype=torch.float32, device="cuda:0")
+        capi.check(lib.air_hip_linear(h, mat2.handle, normed_ref.data_ptr(), y2_ref.data_ptr(), None, m, pf))
+        for epi in (capi.EPILOGUE_RESIDUAL, capi.EPILOGUE_RESIDUAL_PREFILL):
+            resid = resid0.clone()
+            normed = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+            capi.check(lib.air_hip_linear_epilogue(h, mat.handle, x.data_ptr(), m, resid.data_ptr(), bias.data_ptr(),
+                                                   epi, w.data_ptr(), normed.data_ptr(), 1e-6, pf))
+            y2 = torch.full((m, 640), float("nan"), dtype=torch.float32, device="cuda:0")
+            capi.check(lib.air_hip_linear(h, mat2.handle, normed.data_ptr(), y2.data_ptr(), None, m, pf))
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(resid), bits(resid_ref)), (epi, k, n, m, splits)
+            assert np.array_equal(bits(normed), bits(normed_ref)), (epi, k, n, m, splits)
+            assert np.array_equal(bits(y2), bits(y2_ref)), (epi, k, n, m, splits)
+        assert lib.air_hip_linear_epilogue(h, mat.handle, x.data_ptr(), m, resid0.data_ptr(), None,
+                                           capi.EPILOGUE_RESIDUAL_PREFILL, None, None, 0.0, pf) == 1
+    finally:
+        hip_ctx.set_prefill_tuning(0, 0, 0, 0)
+        mat.release()
+        mat2.release()
