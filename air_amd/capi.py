@@ -27,10 +27,16 @@ STATUS_NAMES = {
     7: "internal_error",
 }
 
+TYPE_F32 = 0
+TYPE_F16 = 1
 TYPE_Q4_0 = 2
+TYPE_Q5_0 = 6
 TYPE_Q8_0 = 8
 TYPE_Q4_K = 12
-TYPE_NAMES = {TYPE_Q4_0: "q4_0", TYPE_Q8_0: "q8_0", TYPE_Q4_K: "q4_k"}
+TYPE_Q6_K = 14
+TYPE_BF16 = 30
+TYPE_NAMES = {TYPE_F32: "f32", TYPE_F16: "f16", TYPE_Q4_0: "q4_0", TYPE_Q5_0: "q5_0", TYPE_Q8_0: "q8_0",
+              TYPE_Q4_K: "q4_k", TYPE_Q6_K: "q6_k", TYPE_BF16: "bf16"}
 
 EPILOGUE_STORE = 0
 EPILOGUE_RESIDUAL = 1

@@ -42,9 +42,14 @@
 namespace air_hip {
 
 enum GgmlType : int {
+    kF32 = 0,
+    kF16 = 1,
     kQ4_0 = 2,
+    kQ5_0 = 6,
     kQ8_0 = 8,
     kQ4_K = 12,
+    kQ6_K = 14,
+    kBF16 = 30,
 };
 
 struct FormatGeometry {
@@ -67,6 +72,31 @@ constexpr FormatGeometry geometry_of(int type) {
 }
 
 constexpr bool supported_type(int type) { return geometry_of(type).block_elements != 0; }
+
+// Canonical (GGUF) block of every encoding a matrix may arrive in: the three
+// with a resident tile format, Q5_0 (rewritten exactly as Q8_0 blocks) and
+// the dense ones (decoded once into f32 rows).
+struct CanonicalBlock {
+    std::uint32_t elements;
+    std::uint32_t bytes;
+};
+
+constexpr CanonicalBlock canonical_block(int type) {
+    switch (type) {
+    case kF32: return {1, 4};
+    case kF16: return {1, 2};
+    case kBF16: return {1, 2};
+    case kQ4_0: return {32, 18};
+    case kQ5_0: return {32, 22};
+    case kQ8_0: return {32, 34};
+    case kQ4_K: return {256, 144};
+    case kQ6_K: return {256, 210};
+    default: return {0, 0};
+    }
+}
+
+// Held as dense f32 rows [n][k] (no resident tile format for them).
+constexpr bool dense_type(int type) { return type == kF32 || type == kF16 || type == kBF16 || type == kQ6_K; }
 
 constexpr std::uint64_t ceil_div(std::uint64_t a, std::uint64_t b) { return (a + b - 1) / b; }
 

@@ -98,7 +98,9 @@ struct air_hip_context {
 
 struct air_hip_matrix {
     air_hip_context* owner{nullptr};
-    TilePlanes planes;
+    TilePlanes planes;             // planes.type is the resident format (Q5_0 arrives as Q8_0)
+    int type{0};                   // the canonical type it was prepared from
+    float* dense{nullptr};         // dense_type(type): f32 rows [n][k] instead of tile planes
     std::uint64_t canonical_bytes{0};
     std::uint64_t resident_bytes{0};
 };
@@ -287,7 +289,7 @@ const SplitEpilogue* reduction_epilogue(air_hip_context* ctx, const air_hip_matr
 
 // Which kernels a linear of `rows` rows runs on, decided in one place for
 // the launch path and for air_hip_linear_plan.
-enum class Route { prefill, gemv, fused, skinny_x, skinny_loaded, decode_linear };
+enum class Route { prefill, gemv, fused, skinny_x, skinny_loaded, decode_linear, dense };
 
 // The skinny kernel straight from the f32 rows, or over activations split
 // into the workspace first.  The in-workgroup split repeats the activation
@@ -309,6 +311,7 @@ Route skinny_route(const air_hip_context* ctx, const air_hip_matrix* m, std::uin
 
 // tactic is already validated; rows >= 1.
 Route route_linear(const air_hip_context* ctx, const air_hip_matrix* m, std::uint32_t rows, int tactic) {
+    if (m->dense) return Route::dense;   // every tactic and width
     if (tactic == AIR_HIP_LINEAR_PREFILL || (tactic == AIR_HIP_LINEAR_AUTO && rows > AIR_HIP_MAX_DECODE_ROWS)) {
         return Route::prefill;
     }
@@ -373,6 +376,64 @@ int ensure_split_buffers(air_hip_context* ctx, std::uint64_t partial_bytes, std:
         ctx->split_counter_count = count;
         ++ctx->generation;
     }
+    return AIR_HIP_OK;
+}
+
+// A matrix of a dense type (F32, F16, BF16, Q6_K): its canonical bytes
+// decoded once into f32 rows [n][k], bit for bit as decode_element
+// (cuda_backend.cu:241-344) decodes each element.  k is a multiple of 32.
+int prepare_dense(air_hip_context* ctx, int type, std::uint64_t k, std::uint64_t n, const void* canonical,
+                  std::uint64_t canonical_bytes, int bytes_on_device, air_hip_matrix** out) {
+    const std::uint64_t expected = air_hip_canonical_bytes(type, k, n);
+    if (expected == 0 || canonical_bytes != expected) {
+        return fail(AIR_HIP_DATA_ERROR, "canonical size %llu does not match %llu for {%llu, %llu}",
+                    static_cast<unsigned long long>(canonical_bytes), static_cast<unsigned long long>(expected),
+                    static_cast<unsigned long long>(k), static_cast<unsigned long long>(n));
+    }
+    if (n > std::numeric_limits<std::uint64_t>::max() / sizeof(float) / k) {
+        return fail(AIR_HIP_UNSUPPORTED, "matrix is too large");
+    }
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    auto* m = new (std::nothrow) air_hip_matrix();
+    if (!m) return fail(AIR_HIP_INTERNAL_ERROR, "out of host memory");
+    m->owner = ctx;
+    m->type = type;
+    m->canonical_bytes = canonical_bytes;
+    m->planes.type = type;
+    m->planes.k = k;
+    m->planes.n = n;
+    const std::uint64_t bytes = k * n * sizeof(float);
+    void* dense = nullptr;
+    hipError_t err = hipMalloc(&dense, bytes);
+    if (err != hipSuccess) {
+        delete m;
+        return hip_fail(err, "hipMalloc(dense rows)");
+    }
+    const std::uint8_t* src = static_cast<const std::uint8_t*>(canonical);
+    void* staging = nullptr;
+    if (!bytes_on_device) {
+        err = hipMalloc(&staging, canonical_bytes);
+        if (err == hipSuccess) err = hipMemcpyAsync(staging, canonical, canonical_bytes, hipMemcpyHostToDevice, ctx->stream);
+        if (err == hipSuccess) ctx->host_to_device_bytes.fetch_add(canonical_bytes, std::memory_order_relaxed);
+        src = static_cast<const std::uint8_t*>(staging);
+    }
+    if (err == hipSuccess) err = launch_dequantize_canonical(type, src, k * n, static_cast<float*>(dense), ctx->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
+    if (staging) {
+        if (err != hipSuccess) (void)hipStreamSynchronize(ctx->stream);
+        (void)hipFree(staging);
+    }
+    if (err != hipSuccess) {
+        (void)hipFree(dense);
+        delete m;
+        return hip_fail(err, "decode of dense rows");
+    }
+    m->dense = static_cast<float*>(dense);
+    m->resident_bytes = bytes;
+    ctx->resident_matrix_bytes.fetch_add(bytes, std::memory_order_relaxed);
+    ctx->prepared_matrices.fetch_add(1, std::memory_order_relaxed);
+    *out = m;
     return AIR_HIP_OK;
 }
 
@@ -554,11 +615,11 @@ int air_hip_context_stats(const air_hip_context* ctx, air_hip_stats* out) {
 }
 
 uint64_t air_hip_canonical_bytes(int type, uint64_t k, uint64_t n) {
-    const auto geo = geometry_of(type);
-    if (geo.block_elements == 0 || k % geo.block_elements != 0) return 0;
-    const std::uint64_t blocks = k / geo.block_elements;
-    if (n != 0 && blocks > std::numeric_limits<std::uint64_t>::max() / geo.block_bytes / n) return 0;
-    return blocks * geo.block_bytes * n;
+    const auto geo = canonical_block(type);
+    if (geo.elements == 0 || k % geo.elements != 0) return 0;
+    const std::uint64_t blocks = k / geo.elements;
+    if (n != 0 && blocks > std::numeric_limits<std::uint64_t>::max() / geo.bytes / n) return 0;
+    return blocks * geo.bytes * n;
 }
 
 int air_hip_matrix_prepare(air_hip_context* ctx, int type, uint64_t k, uint64_t n,
@@ -567,13 +628,23 @@ int air_hip_matrix_prepare(air_hip_context* ctx, int type, uint64_t k, uint64_t 
     if (!out) return fail(AIR_HIP_INVALID_ARGUMENT, "out must not be null");
     *out = nullptr;
     if (!ctx || !canonical) return fail(AIR_HIP_INVALID_ARGUMENT, "context and bytes must not be null");
-    const auto geo = geometry_of(type);
-    if (geo.block_elements == 0) return fail(AIR_HIP_UNSUPPORTED, "tensor type %d is not executed by the HIP engine", type);
+    const auto block = canonical_block(type);
+    if (block.elements == 0) return fail(AIR_HIP_UNSUPPORTED, "tensor type %d is not executed by the HIP engine", type);
     if (k == 0 || n == 0) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix dims must be non-zero");
-    if (k % geo.block_elements != 0) {
+    if (k % block.elements != 0) {
         return fail(AIR_HIP_UNSUPPORTED, "input width %llu is not a multiple of the %u-element block",
-                    static_cast<unsigned long long>(k), geo.block_elements);
+                    static_cast<unsigned long long>(k), block.elements);
     }
+    if (dense_type(type)) {
+        if (k % 32u != 0) {
+            return fail(AIR_HIP_UNSUPPORTED, "input width %llu of a dense matrix is not a multiple of 32",
+                        static_cast<unsigned long long>(k));
+        }
+        return prepare_dense(ctx, type, k, n, canonical, canonical_bytes, bytes_on_device, out);
+    }
+    // Q5_0 runs as Q8_0 (rewritten exactly on the device below).
+    const int resident_type = type == kQ5_0 ? static_cast<int>(kQ8_0) : type;
+    const auto geo = geometry_of(resident_type);
     const std::uint64_t expected = air_hip_canonical_bytes(type, k, n);
     if (expected == 0 || canonical_bytes != expected) {
         return fail(AIR_HIP_DATA_ERROR, "canonical size %llu does not match %llu for {%llu, %llu}",
@@ -592,9 +663,10 @@ int air_hip_matrix_prepare(air_hip_context* ctx, int type, uint64_t k, uint64_t 
     auto* m = new (std::nothrow) air_hip_matrix();
     if (!m) return fail(AIR_HIP_INTERNAL_ERROR, "out of host memory");
     m->owner = ctx;
+    m->type = type;
     m->canonical_bytes = canonical_bytes;
     TilePlanes& p = m->planes;
-    p.type = type;
+    p.type = resident_type;
     p.k = k;
     p.n = n;
     p.nt = static_cast<std::uint32_t>(nt64);
@@ -626,9 +698,28 @@ int air_hip_matrix_prepare(air_hip_context* ctx, int type, uint64_t k, uint64_t 
         src = static_cast<const std::uint8_t*>(staging);
         ctx->host_to_device_bytes.fetch_add(canonical_bytes, std::memory_order_relaxed);
     }
+    void* transcoded = nullptr;
+    if (type == kQ5_0) {
+        const std::uint64_t blocks = canonical_bytes / canonical_block(kQ5_0).bytes;
+        err = hipMalloc(&transcoded, blocks * canonical_block(kQ8_0).bytes);
+        if (err == hipSuccess) {
+            err = launch_q5_0_to_q8_0(src, blocks, static_cast<std::uint8_t*>(transcoded), ctx->stream);
+        }
+        if (err != hipSuccess) {
+            if (transcoded) (void)hipStreamSynchronize(ctx->stream);
+            (void)hipFree(transcoded);
+            if (staging) (void)hipFree(staging);
+            (void)hipFree(p.codes);
+            (void)hipFree(p.scales);
+            delete m;
+            return hip_fail(err, "Q5_0 -> Q8_0");
+        }
+        src = static_cast<const std::uint8_t*>(transcoded);
+    }
     err = launch_repack(p, src, ctx->stream);
     if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
     if (staging) (void)hipFree(staging);
+    if (transcoded) (void)hipFree(transcoded);
     if (err == hipSuccess && !ctx->bound_scratch) {
         void* b = nullptr;
         err = hipMalloc(&b, 256);
@@ -655,6 +746,7 @@ int air_hip_matrix_release(air_hip_matrix* m) {
         (void)hipStreamSynchronize(m->owner->stream);
         (void)hipFree(m->planes.codes);
         (void)hipFree(m->planes.scales);
+        (void)hipFree(m->dense);
     }
     m->owner->resident_matrix_bytes.fetch_sub(m->resident_bytes, std::memory_order_relaxed);
     delete m;
@@ -663,7 +755,7 @@ int air_hip_matrix_release(air_hip_matrix* m) {
 
 int air_hip_matrix_describe(const air_hip_matrix* m, air_hip_matrix_desc* out) {
     if (!m || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
-    out->type = m->planes.type;
+    out->type = m->type;
     out->device = m->owner->device;
     out->k = m->planes.k;
     out->n = m->planes.n;
@@ -678,6 +770,11 @@ int air_hip_matrix_dequantize(air_hip_context* ctx, const air_hip_matrix* m, flo
     if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    if (m->dense) {
+        const hipError_t err = hipMemcpyAsync(out, m->dense, m->planes.k * m->planes.n * sizeof(float),
+                                              hipMemcpyDeviceToDevice, ctx->stream);
+        return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "hipMemcpyAsync(dense rows)");
+    }
     const hipError_t err = launch_dequantize_tiles(m->planes, out, ctx->stream);
     if (err != hipSuccess) return hip_fail(err, "dequantize_tiles_kernel");
     return AIR_HIP_OK;
@@ -687,9 +784,9 @@ int air_hip_dequantize_canonical(air_hip_context* ctx, int type, const void* can
                                  uint64_t canonical_bytes, uint64_t elements, float* out) {
     if (!ctx || !canonical || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
     forget_loaded_source(ctx);
-    const auto geo = geometry_of(type);
-    if (geo.block_elements == 0) return fail(AIR_HIP_UNSUPPORTED, "tensor type %d is not decoded by the HIP engine", type);
-    if (elements % geo.block_elements != 0 || canonical_bytes != (elements / geo.block_elements) * geo.block_bytes) {
+    const auto geo = canonical_block(type);
+    if (geo.elements == 0) return fail(AIR_HIP_UNSUPPORTED, "tensor type %d is not decoded by the HIP engine", type);
+    if (elements % geo.elements != 0 || canonical_bytes != (elements / geo.elements) * geo.bytes) {
         return fail(AIR_HIP_DATA_ERROR, "canonical storage geometry mismatch");
     }
     DeviceScope scope(ctx->device);
@@ -716,6 +813,7 @@ int air_hip_decode_linear_fused(air_hip_context* ctx, const air_hip_matrix* m, c
         return fail(AIR_HIP_UNSUPPORTED, "this norm / epilogue combination is not provided");
     }
     if (norm && !(eps >= 0.0)) return fail(AIR_HIP_INVALID_ARGUMENT, "eps must be non-negative");
+    if (m->dense) return fail(AIR_HIP_UNSUPPORTED, "the fused decode GEMV runs the quantized tile formats only");
     if (epilogue == AIR_HIP_EPILOGUE_SWIGLU && m->planes.n % 32u != 0u) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "a fused gate|up matrix needs n = 2F with F a multiple of 16");
     }
@@ -779,6 +877,7 @@ int linear_loaded(air_hip_context* ctx, const air_hip_matrix* m, float* y, const
     if (tactic == AIR_HIP_LINEAR_PREFILL) {
         return fail(AIR_HIP_UNSUPPORTED, "the prefill tactic runs through air_hip_linear, not loaded activations");
     }
+    if (m->dense) return fail(AIR_HIP_UNSUPPORTED, "a dense matrix takes f32 rows through air_hip_linear");
     if (ctx->loaded_rows == 0) return fail(AIR_HIP_INVALID_STATE, "no activations are loaded in this context");
     if (ctx->loaded_k != m->planes.k) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "loaded activations have width %llu, matrix expects %llu",
@@ -832,6 +931,18 @@ int linear_rows(air_hip_context* ctx, const air_hip_matrix* m, const float* x, f
     if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
     if (rows == 0) return fail(AIR_HIP_INVALID_ARGUMENT, "linear batch width must be non-zero");
     const Route route = route_linear(ctx, m, rows, tactic);
+    if (route == Route::dense) {
+        if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
+        DeviceScope scope(ctx->device);
+        if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+        const hipError_t err = launch_dense_linear(m->dense, m->planes.k, m->planes.n, x, bias, y, rows, ctx->stream);
+        if (err != hipSuccess) return hip_fail(err, "dense_rows_kernel / dense_gemm_kernel");
+        const bool prefill = tactic == AIR_HIP_LINEAR_PREFILL ||
+                             (tactic == AIR_HIP_LINEAR_AUTO && rows > AIR_HIP_MAX_DECODE_ROWS);
+        (prefill ? ctx->prefill_linear_calls : ctx->decode_linear_calls).fetch_add(1, std::memory_order_relaxed);
+        (prefill ? ctx->prefill_rows : ctx->decode_rows).fetch_add(rows, std::memory_order_relaxed);
+        return AIR_HIP_OK;
+    }
     if (route == Route::prefill) {
         if (rows > kMaxRows) return fail(AIR_HIP_UNSUPPORTED, "linear batch width %u exceeds %u", rows, kMaxRows);
         if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
@@ -875,9 +986,16 @@ int linear_rows(air_hip_context* ctx, const air_hip_matrix* m, const float* x, f
 
 // Text description of the launches of a linear (air_hip_linear_plan).
 std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m, std::uint32_t rows, int tactic) {
-    const char* fmt = m->planes.type == kQ8_0 ? "q8_0" : m->planes.type == kQ4_0 ? "q4_0" : "q4_k";
+    const char* fmt = m->planes.type == kQ8_0 ? (m->type == kQ5_0 ? "q8_0 from q5_0" : "q8_0")
+                      : m->planes.type == kQ4_0 ? "q4_0" : "q4_k";
     char buf[256];
     switch (route_linear(ctx, m, rows, tactic)) {
+    case Route::dense: {
+        const char* t = m->type == kF32 ? "f32" : m->type == kF16 ? "f16" : m->type == kBF16 ? "bf16" : "q6_k";
+        std::snprintf(buf, sizeof buf, "%s (dense f32 rows from %s)",
+                      rows <= 16u ? "dense_rows_kernel" : "dense_gemm_kernel tile=64x64", t);
+        break;
+    }
     case Route::prefill: {
         const PrefillShape s = plan_prefill(m->planes, rows, ctx->prefill_tuning);
         if (s.lds_stages) {
@@ -954,6 +1072,15 @@ int air_hip_linear_noalloc(air_hip_context* ctx, const air_hip_matrix* m, const 
     }
     if (m->owner->device != ctx->device) return fail(AIR_HIP_INVALID_ARGUMENT, "matrix belongs to another device");
     if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
+    if (m->dense) {   // no scratch: the same launch as air_hip_linear
+        DeviceScope scope(ctx->device);
+        if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+        const hipError_t err = launch_dense_linear(m->dense, m->planes.k, m->planes.n, x, bias, y, rows, ctx->stream);
+        if (err != hipSuccess) return hip_fail(err, "dense_rows_kernel / dense_gemm_kernel");
+        ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
+        ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
+        return AIR_HIP_OK;
+    }
     if (!ctx->noalloc_scratch) return fail(AIR_HIP_INTERNAL_ERROR, "the device scratch array is not mapped");
     // Same route, plans and kernels as air_hip_linear with this context's
     // settings, so the results are bit-identical; only the buffers differ:
@@ -1007,6 +1134,7 @@ int air_hip_linear_noalloc(air_hip_context* ctx, const air_hip_matrix* m, const 
         if (err == hipSuccess) err = launch_decode_linear(p, ws, bias, y, rows, ctx->tuning, ctx->stream);
         break;
     case Route::prefill:
+    case Route::dense:
         return fail(AIR_HIP_UNSUPPORTED, "the no-allocation linear runs the decode tactic only");
     }
     if (err != hipSuccess) return hip_fail(err, "no-allocation decode linear");
@@ -1165,7 +1293,8 @@ int air_hip_matrix_rows(air_hip_context* ctx, const air_hip_matrix* m, const int
     if (count > 65535u) return fail(AIR_HIP_UNSUPPORTED, "at most 65535 rows per call");
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-    const hipError_t err = launch_matrix_rows(m->planes, rows, count, out, ctx->stream);
+    const hipError_t err = m->dense ? launch_dense_rows(m->dense, m->planes.k, m->planes.n, rows, count, out, ctx->stream)
+                                    : launch_matrix_rows(m->planes, rows, count, out, ctx->stream);
     return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "matrix_rows_kernel");
 }
 

@@ -1,0 +1,185 @@
+// linear_dense.hip -- linears over matrices held as dense f32 rows.
+//
+// The encodings with no resident tile format here (F32, F16, BF16 and Q6_K;
+// decode_element, src/cuda/cuda_backend.cu:241-344, decodes them per
+// element inside every GEMV) are decoded once at prepare time, bit for bit,
+// into f32 rows w[n][k].  A real Qwen2.5 Q4_K_M file carries Q6_K tensors
+// (lm_head, half the ffn_down / attn_v) and F16 / BF16 files carry every
+// linear this way.  These kernels are the coverage route for them: plain f32
+// FMA with f32 accumulation, weights read at 4 bytes per element, one launch
+// per linear, no workspace.
+//   rows 1..16: dense_rows_kernel, four output columns per wave, every row
+//               of x per pass over K (the weights are read once);
+//   more rows:  dense_gemm_kernel, 64 x 64 output tiles staged through LDS.
+#include "air_hip_device.hpp"
+#include "air_hip_kernels.hpp"
+
+namespace air_hip {
+namespace {
+
+constexpr unsigned kDenseThreads = 256;
+constexpr unsigned kDenseCols = 4;       // output columns per wave (rows kernel)
+constexpr unsigned kDenseMaxRows = 16;   // rows kernel covers m <= 16
+constexpr unsigned kGemmTile = 64;
+constexpr unsigned kGemmK = 32;
+
+template <unsigned MB>
+__global__ __launch_bounds__(kDenseThreads) void dense_rows_kernel(const float* __restrict__ w,
+                                                                   const float* __restrict__ x,
+                                                                   const float* __restrict__ bias,
+                                                                   float* __restrict__ y, std::uint32_t m,
+                                                                   std::uint64_t k, std::uint64_t n) {
+    const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const std::uint64_t n0 =
+        (static_cast<std::uint64_t>(blockIdx.x) * (kDenseThreads / 64u) + wave) * kDenseCols;
+    if (n0 >= n) return;   // no barrier in this kernel
+    const float* wr[kDenseCols];
+#pragma unroll
+    for (unsigned c = 0; c < kDenseCols; ++c) {
+        const std::uint64_t col = n0 + c < n ? n0 + c : n - 1u;   // clamped; not stored
+        wr[c] = w + col * k;
+    }
+    float acc[MB][kDenseCols];
+#pragma unroll
+    for (unsigned i = 0; i < MB; ++i)
+#pragma unroll
+        for (unsigned c = 0; c < kDenseCols; ++c) acc[i][c] = 0.0f;
+    for (std::uint64_t kk = 4u * lane; kk < k; kk += 256u) {
+        float4 wv[kDenseCols];
+#pragma unroll
+        for (unsigned c = 0; c < kDenseCols; ++c) wv[c] = *reinterpret_cast<const float4*>(wr[c] + kk);
+#pragma unroll
+        for (unsigned i = 0; i < MB; ++i) {
+            if (i < m) {
+                const float4 xv = *reinterpret_cast<const float4*>(x + i * k + kk);
+#pragma unroll
+                for (unsigned c = 0; c < kDenseCols; ++c) {
+                    acc[i][c] = fmaf(wv[c].x, xv.x, acc[i][c]);
+                    acc[i][c] = fmaf(wv[c].y, xv.y, acc[i][c]);
+                    acc[i][c] = fmaf(wv[c].z, xv.z, acc[i][c]);
+                    acc[i][c] = fmaf(wv[c].w, xv.w, acc[i][c]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (unsigned i = 0; i < MB; ++i) {
+        if (i < m) {
+#pragma unroll
+            for (unsigned c = 0; c < kDenseCols; ++c) {
+                float v = acc[i][c];
+                for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+                if (lane == 0u && n0 + c < n) y[i * n + n0 + c] = bias ? v + bias[n0 + c] : v;
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(kDenseThreads) void dense_gemm_kernel(const float* __restrict__ w,
+                                                                   const float* __restrict__ x,
+                                                                   const float* __restrict__ bias,
+                                                                   float* __restrict__ y, std::uint32_t m,
+                                                                   std::uint64_t k, std::uint64_t n) {
+    // k-major tiles (4 floats of padding keep float4 reads aligned).
+    __shared__ float xs[kGemmK][kGemmTile + 4];
+    __shared__ float ws[kGemmK][kGemmTile + 4];
+    const unsigned t = threadIdx.x, tx = t & 15u, ty = t >> 4;
+    const std::uint64_t n0 = static_cast<std::uint64_t>(blockIdx.x) * kGemmTile;
+    const std::uint64_t m0 = static_cast<std::uint64_t>(blockIdx.y) * kGemmTile;
+    float acc[4][4];
+#pragma unroll
+    for (unsigned i = 0; i < 4; ++i)
+#pragma unroll
+        for (unsigned j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+    for (std::uint64_t k0 = 0; k0 < k; k0 += kGemmK) {
+        // 64 rows x 32 k of each operand: 512 float4, two per thread.
+#pragma unroll
+        for (unsigned h = 0; h < 2; ++h) {
+            const unsigned idx = t + kDenseThreads * h, row = idx >> 3, kq = (idx & 7u) * 4u;
+            float4 xv = make_float4(0.f, 0.f, 0.f, 0.f), wv = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (m0 + row < m) xv = *reinterpret_cast<const float4*>(x + (m0 + row) * k + k0 + kq);
+            if (n0 + row < n) wv = *reinterpret_cast<const float4*>(w + (n0 + row) * k + k0 + kq);
+            xs[kq + 0][row] = xv.x;
+            xs[kq + 1][row] = xv.y;
+            xs[kq + 2][row] = xv.z;
+            xs[kq + 3][row] = xv.w;
+            ws[kq + 0][row] = wv.x;
+            ws[kq + 1][row] = wv.y;
+            ws[kq + 2][row] = wv.z;
+            ws[kq + 3][row] = wv.w;
+        }
+        __syncthreads();
+#pragma unroll 8
+        for (unsigned kk = 0; kk < kGemmK; ++kk) {
+            const float4 a = *reinterpret_cast<const float4*>(&xs[kk][4u * ty]);
+            const float4 b = *reinterpret_cast<const float4*>(&ws[kk][4u * tx]);
+            const float av[4] = {a.x, a.y, a.z, a.w};
+            const float bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (unsigned i = 0; i < 4; ++i)
+#pragma unroll
+                for (unsigned j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (unsigned i = 0; i < 4; ++i) {
+        const std::uint64_t row = m0 + 4u * ty + i;
+#pragma unroll
+        for (unsigned j = 0; j < 4; ++j) {
+            const std::uint64_t col = n0 + 4u * tx + j;
+            if (row < m && col < n) y[row * n + col] = bias ? acc[i][j] + bias[col] : acc[i][j];
+        }
+    }
+}
+
+__global__ __launch_bounds__(kDenseThreads) void dense_rows_gather_kernel(const float* __restrict__ w,
+                                                                          std::uint64_t k, std::uint64_t n,
+                                                                          const std::int32_t* __restrict__ rows,
+                                                                          std::uint32_t count,
+                                                                          float* __restrict__ out) {
+    const std::uint32_t i = blockIdx.y;
+    if (i >= count) return;
+    const std::int32_t row = rows[i];
+    if (row < 0 || static_cast<std::uint64_t>(row) >= n) return;
+    const float* src = w + static_cast<std::uint64_t>(row) * k;
+    float* dst = out + static_cast<std::uint64_t>(i) * k;
+    for (std::uint64_t c = blockIdx.x * static_cast<std::uint64_t>(kDenseThreads) + threadIdx.x; c < k;
+         c += static_cast<std::uint64_t>(gridDim.x) * kDenseThreads) {
+        dst[c] = src[c];
+    }
+}
+
+} // namespace
+
+hipError_t launch_dense_linear(const float* w, std::uint64_t k, std::uint64_t n, const float* x, const float* bias,
+                               float* y, std::uint32_t m, hipStream_t stream) {
+    if (m == 0u || k == 0u || n == 0u || k % kGemmK != 0u) return hipErrorInvalidValue;
+    if (m <= kDenseMaxRows) {
+        const std::uint64_t cols_per_group = (kDenseThreads / 64u) * kDenseCols;
+        const dim3 grid(static_cast<unsigned>(ceil_div(n, cols_per_group)));
+        if (m == 1u) {
+            hipLaunchKernelGGL(dense_rows_kernel<1>, grid, dim3(kDenseThreads), 0, stream, w, x, bias, y, m, k, n);
+        } else if (m <= 4u) {
+            hipLaunchKernelGGL(dense_rows_kernel<4>, grid, dim3(kDenseThreads), 0, stream, w, x, bias, y, m, k, n);
+        } else {
+            hipLaunchKernelGGL(dense_rows_kernel<kDenseMaxRows>, grid, dim3(kDenseThreads), 0, stream, w, x, bias, y,
+                               m, k, n);
+        }
+    } else {
+        const dim3 grid(static_cast<unsigned>(ceil_div(n, kGemmTile)), static_cast<unsigned>(ceil_div(m, kGemmTile)));
+        hipLaunchKernelGGL(dense_gemm_kernel, grid, dim3(kDenseThreads), 0, stream, w, x, bias, y, m, k, n);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_dense_rows(const float* w, std::uint64_t k, std::uint64_t n, const std::int32_t* rows,
+                             std::uint32_t count, float* out, hipStream_t stream) {
+    if (count == 0u) return hipSuccess;
+    const unsigned gx = static_cast<unsigned>(std::min<std::uint64_t>(ceil_div(k, kDenseThreads), 64u));
+    hipLaunchKernelGGL(dense_rows_gather_kernel, dim3(gx, count), dim3(kDenseThreads), 0, stream, w, k, n, rows, count,
+                       out);
+    return hipGetLastError();
+}
+
+} // namespace air_hip

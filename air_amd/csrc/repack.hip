@@ -230,7 +230,7 @@ __global__ void dequantize_canonical_kernel(int type, const std::uint8_t* src, s
                 out[b * 32u + i] = d * static_cast<float>(static_cast<int>(p & 0x0fu) - 8);
                 out[b * 32u + i + 16u] = d * static_cast<float>(static_cast<int>(p >> 4) - 8);
             }
-        } else {
+        } else if (type == kQ4_K) {
             const std::uint8_t* blk = src + b * 144u;
             const float d = f16_bits_to_f32(rd16(blk));
             const float dmin = f16_bits_to_f32(rd16(blk + 2));
@@ -248,6 +248,67 @@ __global__ void dequantize_canonical_kernel(int type, const std::uint8_t* src, s
                     out[b * 256u + grp * 64u + 32u + i] = d1 * static_cast<float>(p >> 4) - mm1;
                 }
             }
+        } else if (type == kQ5_0) {   // [d:f16][qh:4][qs:16]; element i's fifth bit is bit i of qh
+            const std::uint8_t* blk = src + b * 22u;
+            const float d = f16_bits_to_f32(rd16(blk));
+            const std::uint32_t qh = rd16(blk + 2) | (rd16(blk + 4) << 16);
+            for (std::uint32_t i = 0; i < 16; ++i) {
+                const std::uint32_t p = blk[6 + i];
+                const int q0 = static_cast<int>((p & 0x0fu) | (((qh >> i) & 1u) << 4)) - 16;
+                const int q1 = static_cast<int>((p >> 4) | (((qh >> (i + 16u)) & 1u) << 4)) - 16;
+                out[b * 32u + i] = d * static_cast<float>(q0);
+                out[b * 32u + i + 16u] = d * static_cast<float>(q1);
+            }
+        } else if (type == kQ6_K) {   // [ql:128][qh:64][scales:16 x int8][d:f16], two halves of 128
+            const std::uint8_t* blk = src + b * 210u;
+            const float d = f16_bits_to_f32(rd16(blk + 208));
+            for (std::uint32_t half = 0; half < 2; ++half) {
+                const std::uint8_t* lo = blk + 64u * half;
+                const std::uint8_t* hi = blk + 128u + 32u * half;
+                const auto* sc = reinterpret_cast<const std::int8_t*>(blk + 192u + 8u * half);
+                float* h = out + b * 256u + 128u * half;
+                for (std::uint32_t i = 0; i < 32; ++i) {
+                    const std::uint32_t pair = i / 16u;
+                    // Element i + 32 j: nibble j >> 1 of lo[i + 32 (j & 1)],
+                    // high bits 2j..2j+1 of hi[i]; scale sc[pair + 2j].
+                    for (std::uint32_t j = 0; j < 4; ++j) {
+                        const std::uint32_t l = lo[i + 32u * (j & 1u)];
+                        const std::uint32_t nib = (j >> 1) ? (l >> 4) : (l & 0x0fu);
+                        const int q = static_cast<int>(nib | (((hi[i] >> (2u * j)) & 3u) << 4)) - 32;
+                        // (d * scale) * q, the order of decode_element
+                        h[i + 32u * j] = d * static_cast<float>(sc[pair + 2u * j]) * static_cast<float>(q);
+                    }
+                }
+            }
+        } else if (type == kF32) {
+            std::uint32_t bits = rd16(src + 4u * b) | (rd16(src + 4u * b + 2u) << 16);
+            out[b] = __uint_as_float(bits);
+        } else if (type == kF16) {
+            out[b] = f16_bits_to_f32(rd16(src + 2u * b));
+        } else if (type == kBF16) {
+            out[b] = __uint_as_float(rd16(src + 2u * b) << 16);
+        }
+    }
+}
+
+// Q5_0 blocks rewritten as Q8_0 blocks of the same values: the scale is
+// kept and each 5-bit code q becomes the int8 q - 16, so d * (q - 16) is
+// unchanged bit for bit.
+__global__ void q5_0_to_q8_0_kernel(const std::uint8_t* __restrict__ src, std::uint64_t blocks,
+                                    std::uint8_t* __restrict__ dst) {
+    for (std::uint64_t b = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x; b < blocks;
+         b += static_cast<std::uint64_t>(gridDim.x) * blockDim.x) {
+        const std::uint8_t* blk = src + b * 22u;
+        std::uint8_t* out = dst + b * 34u;
+        out[0] = blk[0];
+        out[1] = blk[1];
+        const std::uint32_t qh = rd16(blk + 2) | (rd16(blk + 4) << 16);
+        for (std::uint32_t i = 0; i < 16; ++i) {
+            const std::uint32_t p = blk[6 + i];
+            const int q0 = static_cast<int>((p & 0x0fu) | (((qh >> i) & 1u) << 4)) - 16;
+            const int q1 = static_cast<int>((p >> 4) | (((qh >> (i + 16u)) & 1u) << 4)) - 16;
+            out[2 + i] = static_cast<std::uint8_t>(static_cast<std::int8_t>(q0));
+            out[18 + i] = static_cast<std::uint8_t>(static_cast<std::int8_t>(q1));
         }
     }
 }
@@ -288,11 +349,17 @@ hipError_t launch_dequantize_tiles(const TilePlanes& p, float* out, hipStream_t 
 
 hipError_t launch_dequantize_canonical(int type, const std::uint8_t* canonical, std::uint64_t elements,
                                        float* out, hipStream_t stream) {
-    const auto geo = geometry_of(type);
-    if (geo.block_elements == 0) return hipErrorInvalidValue;
-    const std::uint64_t blocks = elements / geo.block_elements;
+    const auto geo = canonical_block(type);
+    if (geo.elements == 0) return hipErrorInvalidValue;
+    const std::uint64_t blocks = elements / geo.elements;
     if (blocks == 0) return hipSuccess;
     dequantize_canonical_kernel<<<grid_for(blocks), kThreads, 0, stream>>>(type, canonical, blocks, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_q5_0_to_q8_0(const std::uint8_t* q5_0, std::uint64_t blocks, std::uint8_t* q8_0, hipStream_t stream) {
+    if (blocks == 0) return hipSuccess;
+    q5_0_to_q8_0_kernel<<<grid_for(blocks), kThreads, 0, stream>>>(q5_0, blocks, q8_0);
     return hipGetLastError();
 }
 

@@ -140,6 +140,9 @@ public:
     [[nodiscard]] Result<HipLinearInfo> linear_info(std::uint32_t layer, LinearRole role) const;
     [[nodiscard]] bool fused_qkv() const noexcept { return fused_qkv_; }
     [[nodiscard]] bool fused_gate_up() const noexcept { return fused_gate_up_; }
+    // Every block linear is in a tile format (Q8_0, Q5_0, Q4_0, Q4_K), so the
+    // fused M = 1 GEMV (air_hip_decode_linear_fused) takes all of them.
+    [[nodiscard]] bool tile_formats() const noexcept { return tile_formats_; }
     [[nodiscard]] Status set_stream(void* stream);
     [[nodiscard]] Status synchronize() const;
     [[nodiscard]] air_hip_context* context() const noexcept { return ctx_; }
@@ -170,6 +173,7 @@ private:
     Linear output_{};
     bool fused_qkv_{false};
     bool fused_gate_up_{false};
+    bool tile_formats_{true};
     bool output_is_embedding_{false};
     std::uint64_t bias_bytes_{0};
     HipPrepareOptions options_{};

@@ -27,8 +27,11 @@ enum class GgmlType : std::uint32_t {
     f32 = 0,
     f16 = 1,
     q4_0 = 2,
+    q5_0 = 6,
     q8_0 = 8,
     q4_k = 12,
+    q6_k = 14,
+    bf16 = 30,
 };
 
 struct FormatGeometry {

@@ -38,6 +38,11 @@ struct SyntheticQwen2Spec {
     ModelConfig config{};
     std::uint32_t weight_format{static_cast<std::uint32_t>(GgmlType::q8_0)};
     std::uint32_t embedding_format{static_cast<std::uint32_t>(GgmlType::q8_0)};
+    // attn_v / ffn_down and output.weight formats (kSameFormat: weight_format),
+    // e.g. Q6_K beside Q4_K as in a Q4_K_M file.
+    static constexpr std::uint32_t kSameFormat = 0xFFFFFFFFU;
+    std::uint32_t v_down_format{kSameFormat};
+    std::uint32_t output_format{kSameFormat};
     std::uint64_t seed{0xA17C0DEULL};
     float sigma{0.02f};
     bool qkv_bias{true};

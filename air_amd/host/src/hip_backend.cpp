@@ -225,6 +225,15 @@ Result<std::unique_ptr<HipPreparedModel>> HipPreparedModel::create(std::shared_p
         const TensorDescriptor* gate_up[] = {tensor(l, "ffn_gate.weight"), tensor(l, "ffn_up.weight")};
         fused_qkv = fused_qkv && same_format(qkv);
         fused_gate_up = fused_gate_up && same_format(gate_up);
+        const TensorDescriptor* linears[] = {qkv[0], qkv[1], qkv[2], gate_up[0], gate_up[1],
+                                             tensor(l, "attn_output.weight"), tensor(l, "ffn_down.weight")};
+        for (const TensorDescriptor* t : linears) {
+            const int type = t ? static_cast<int>(t->format_type) : -1;
+            if (type != AIR_HIP_TYPE_Q8_0 && type != AIR_HIP_TYPE_Q5_0 && type != AIR_HIP_TYPE_Q4_0 &&
+                type != AIR_HIP_TYPE_Q4_K) {
+                prepared->tile_formats_ = false;
+            }
+        }
     }
     prepared->fused_qkv_ = fused_qkv;
     prepared->fused_gate_up_ = fused_gate_up;

@@ -434,7 +434,7 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
     // norm and SwiGLU 34.4 vs 31.6 for norm, linear and SiLU; gate|up with
     // SwiGLU alone 29.2 vs 30.4 for linear and SiLU, in graphs).
     const bool fuse = m == 1U && tactic == QuantizedLinearExecutionKind::hip_decode && prepared_.fused_qkv() &&
-                      prepared_.fused_gate_up();
+                      prepared_.fused_gate_up() && prepared_.tile_formats();
     const double eps = c.rms_norm_epsilon;
     if (fuse) {
         for (std::uint32_t l = 0; l < c.layer_count; ++l) {

@@ -17,9 +17,12 @@ FormatGeometry format_geometry(std::uint32_t format_type) noexcept {
     switch (static_cast<GgmlType>(format_type)) {
     case GgmlType::f32: return {1, 4};
     case GgmlType::f16: return {1, 2};
+    case GgmlType::bf16: return {1, 2};
     case GgmlType::q4_0: return {32, 18};
+    case GgmlType::q5_0: return {32, 22};
     case GgmlType::q8_0: return {32, 34};
     case GgmlType::q4_k: return {256, 144};
+    case GgmlType::q6_k: return {256, 210};
     }
     return {0, 0};
 }
@@ -28,9 +31,12 @@ const char* format_name(std::uint32_t format_type) noexcept {
     switch (static_cast<GgmlType>(format_type)) {
     case GgmlType::f32: return "f32";
     case GgmlType::f16: return "f16";
+    case GgmlType::bf16: return "bf16";
     case GgmlType::q4_0: return "q4_0";
+    case GgmlType::q5_0: return "q5_0";
     case GgmlType::q8_0: return "q8_0";
     case GgmlType::q4_k: return "q4_K";
+    case GgmlType::q6_k: return "q6_K";
     }
     return "unknown";
 }

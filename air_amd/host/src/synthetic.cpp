@@ -107,6 +107,83 @@ void quantize_q4_0_block(const float* b, std::byte* out) noexcept {
     for (int i = 0; i < 16; ++i) out[2 + i] = static_cast<std::byte>(q[i] | (q[i + 16] << 4));
 }
 
+// Q5_0: d = -vmax / 16 (vmax the value of largest magnitude), code
+// q = clamp(floor(x / d + 16.5), 0, 31); low nibbles in qs (elements i and
+// i + 16 share byte i), fifth bits in the 32-bit qh (bit j for element j).
+void quantize_q5_0_block(const float* b, std::byte* out) noexcept {
+    float vmax = 0.0f;
+    for (int i = 0; i < 32; ++i) {
+        if (std::fabs(b[i]) > std::fabs(vmax)) vmax = b[i];
+    }
+    const float d = vmax / -16.0f;
+    const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+    put_f16(out, d);
+    std::uint32_t qh = 0;
+    std::uint8_t q[32];
+    for (int i = 0; i < 32; ++i) {
+        q[i] = static_cast<std::uint8_t>(std::clamp(std::floor(b[i] * inv + 16.5f), 0.0f, 31.0f));
+        qh |= static_cast<std::uint32_t>(q[i] >> 4) << i;
+    }
+    std::memcpy(out + 2, &qh, 4);
+    for (int i = 0; i < 16; ++i) out[6 + i] = static_cast<std::byte>((q[i] & 0x0f) | ((q[i + 16] & 0x0f) << 4));
+}
+
+// Q6_K: sixteen sub-blocks of 16 with an int8 scale each under one f16 d;
+// codes q in [0, 63] stand for q - 32.  Sub-block s covers elements 16 s ..
+// 16 s + 15.  In each half of 128, element i + 32 j (i < 32, j < 4) keeps
+// its low four bits in nibble j >> 1 of ql[i + 32 (j & 1)] and its high two
+// bits at bits 2j, 2j + 1 of qh[i].
+void quantize_q6_k_block(const float* b, std::byte* out) noexcept {
+    float step[16];
+    float max_step = 0.0f;
+    for (int s = 0; s < 16; ++s) {
+        float vmax = 0.0f;
+        for (int i = 0; i < 16; ++i) {
+            if (std::fabs(b[16 * s + i]) > std::fabs(vmax)) vmax = b[16 * s + i];
+        }
+        step[s] = vmax / -32.0f;
+        if (std::fabs(step[s]) > std::fabs(max_step)) max_step = step[s];
+    }
+    const float d = max_step / -128.0f;
+    const float dq = f16_bits_to_f32(f32_to_f16_bits(d));
+    std::int8_t sc[16];
+    for (int s = 0; s < 16; ++s) {
+        sc[s] = static_cast<std::int8_t>(dq != 0.0f ? std::clamp(round_half_away(step[s] / dq), -128.0f, 127.0f) : 0.0f);
+    }
+    std::uint8_t q[256];
+    for (int s = 0; s < 16; ++s) {
+        const float unit = dq * static_cast<float>(sc[s]);
+        const float inv = unit != 0.0f ? 1.0f / unit : 0.0f;
+        for (int i = 0; i < 16; ++i) {
+            q[16 * s + i] = static_cast<std::uint8_t>(std::clamp(round_half_away(b[16 * s + i] * inv) + 32.0f, 0.0f, 63.0f));
+        }
+    }
+    std::memset(out, 0, 210);
+    for (int half = 0; half < 2; ++half) {
+        const std::uint8_t* h = q + 128 * half;
+        for (int i = 0; i < 32; ++i) {
+            for (int j = 0; j < 4; ++j) {
+                const std::uint8_t v = h[i + 32 * j];
+                auto& lo = out[64 * half + i + 32 * (j & 1)];
+                lo = static_cast<std::byte>(std::to_integer<std::uint8_t>(lo) | ((v & 0x0f) << (4 * (j >> 1))));
+                auto& hi = out[128 + 32 * half + i];
+                hi = static_cast<std::byte>(std::to_integer<std::uint8_t>(hi) | ((v >> 4) << (2 * j)));
+            }
+        }
+    }
+    std::memcpy(out + 192, sc, 16);
+    put_f16(out + 208, d);
+}
+
+// BF16: the high half of the f32 bits, rounded to nearest even.
+void put_bf16(std::byte* dst, float v) noexcept {
+    std::uint32_t bits = 0;
+    std::memcpy(&bits, &v, 4);
+    bits += 0x7fffu + ((bits >> 16) & 1u);
+    const auto h = static_cast<std::uint16_t>(bits >> 16);
+    std::memcpy(dst, &h, 2);
+}
+
 void quantize_q4_k_block(const float* b, std::byte* out) noexcept {
     float lo[8], step[8];
     float max_step = 0.0f, max_neg = 0.0f;
@@ -162,9 +239,12 @@ void quantize_blocks(std::uint32_t format_type, const float* w, std::uint64_t bl
         switch (static_cast<GgmlType>(format_type)) {
         case GgmlType::f32: std::memcpy(dst, src, 4); break;
         case GgmlType::f16: put_f16(dst, *src); break;
+        case GgmlType::bf16: put_bf16(dst, *src); break;
         case GgmlType::q8_0: quantize_q8_0_block(src, dst); break;
         case GgmlType::q4_0: quantize_q4_0_block(src, dst); break;
+        case GgmlType::q5_0: quantize_q5_0_block(src, dst); break;
         case GgmlType::q4_k: quantize_q4_k_block(src, dst); break;
+        case GgmlType::q6_k: quantize_q6_k_block(src, dst); break;
         }
     }
 }
@@ -245,14 +325,16 @@ Result<std::shared_ptr<const ModelDefinition>> make_synthetic_qwen2(const Synthe
     std::vector<Pending> pending;
     pending.push_back({"token_embd.weight", spec.embedding_format, e, vocab, Pending::normal, false});
     pending.push_back({"output_norm.weight", f32, e, 1, Pending::ones, true});
-    if (!spec.tied_output) pending.push_back({"output.weight", spec.weight_format, e, vocab, Pending::normal, false});
+    const auto pick = [&](std::uint32_t f) { return f == SyntheticQwen2Spec::kSameFormat ? spec.weight_format : f; };
+    const std::uint32_t v_down = pick(spec.v_down_format);
+    if (!spec.tied_output) pending.push_back({"output.weight", pick(spec.output_format), e, vocab, Pending::normal, false});
     if (spec.output_bias) pending.push_back({"output.bias", f32, vocab, 1, Pending::normal, true});
     for (std::uint32_t l = 0; l < c.layer_count; ++l) {
         const auto n = [l](const char* s) { return block_tensor_name(l, s); };
         pending.push_back({n("attn_norm.weight"), f32, e, 1, Pending::ones, true});
         pending.push_back({n("attn_q.weight"), spec.weight_format, e, qw, Pending::normal, false});
         pending.push_back({n("attn_k.weight"), spec.weight_format, e, kvw, Pending::normal, false});
-        pending.push_back({n("attn_v.weight"), spec.weight_format, e, kvw, Pending::normal, false});
+        pending.push_back({n("attn_v.weight"), v_down, e, kvw, Pending::normal, false});
         if (spec.qkv_bias) {
             pending.push_back({n("attn_q.bias"), f32, qw, 1, Pending::normal, true});
             pending.push_back({n("attn_k.bias"), f32, kvw, 1, Pending::normal, true});
@@ -262,7 +344,7 @@ Result<std::shared_ptr<const ModelDefinition>> make_synthetic_qwen2(const Synthe
         pending.push_back({n("ffn_norm.weight"), f32, e, 1, Pending::ones, true});
         pending.push_back({n("ffn_gate.weight"), spec.weight_format, e, ffn, Pending::normal, false});
         pending.push_back({n("ffn_up.weight"), spec.weight_format, e, ffn, Pending::normal, false});
-        pending.push_back({n("ffn_down.weight"), spec.weight_format, ffn, e, Pending::normal, false});
+        pending.push_back({n("ffn_down.weight"), v_down, ffn, e, Pending::normal, false});
     }
 
     std::vector<TensorDescriptor> tensors;

@@ -46,11 +46,21 @@ typedef enum air_hip_status {
     AIR_HIP_INTERNAL_ERROR = 7
 } air_hip_status;
 
-/* GGML type ids this engine executes. */
+/* GGML type ids this engine executes: every encoding the reference's
+ * decode_element takes (cuda_backend.cu:241-344).  Q8_0, Q4_0 and Q4_K run
+ * on their resident tile formats; Q5_0 is rewritten exactly as Q8_0 (same
+ * scale, code q - 16) and runs as Q8_0; F32, F16, BF16 and Q6_K are decoded
+ * once into dense f32 rows and run on plain f32 FMA kernels (the coverage
+ * route: 4 bytes of weights per element). */
 enum {
+    AIR_HIP_TYPE_F32 = 0,
+    AIR_HIP_TYPE_F16 = 1,
     AIR_HIP_TYPE_Q4_0 = 2,
+    AIR_HIP_TYPE_Q5_0 = 6,
     AIR_HIP_TYPE_Q8_0 = 8,
-    AIR_HIP_TYPE_Q4_K = 12
+    AIR_HIP_TYPE_Q4_K = 12,
+    AIR_HIP_TYPE_Q6_K = 14,
+    AIR_HIP_TYPE_BF16 = 30
 };
 
 /* Linear tactics: the HIP members of AIR's QuantizedLinearExecutionKind
@@ -191,7 +201,12 @@ uint64_t air_hip_canonical_bytes(int type, uint64_t k, uint64_t n);
  * of Impl::initialize (cuda_backend.cu:1790-1822) plus the one-time repack
  * the reference does only for dp4a (pack_signed32_weights_kernel,
  * cuda_backend.cu:398-427).  k must be a multiple of the block size
- * (cuda_backend.cu:1797-1801).  Blocks until the repack has finished. */
+ * (cuda_backend.cu:1797-1801).  Blocks until the repack has finished.
+ * Dense types (F32, F16, BF16, Q6_K) need k a multiple of 32; their
+ * matrices take f32 rows through air_hip_linear (any tactic and width, the
+ * epilogue entry points running their epilogues as separate launches), not
+ * air_hip_linear_loaded or air_hip_decode_linear_fused (UNSUPPORTED).
+ * air_hip_matrix_describe reports the type the matrix was prepared from. */
 int air_hip_matrix_prepare(air_hip_context* ctx, int type, uint64_t k, uint64_t n,
                            const void* canonical, uint64_t canonical_bytes,
                            int bytes_on_device, air_hip_matrix** out);

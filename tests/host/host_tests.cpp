@@ -480,7 +480,7 @@ void test_quantizers() {
     for (float v : w) var += (v - mean) * (v - mean);
     var /= w.size();
     check(std::fabs(mean) < 0.002 && std::fabs(std::sqrt(var) - 0.02) < 0.002, "normal_fill has sigma 0.02");
-    for (std::uint32_t type : {8U, 2U, 12U}) {
+    for (std::uint32_t type : {8U, 2U, 12U, 6U, 14U, 1U, 30U}) {
         auto q = air::quantize_rows(type, w, 512, 4);
         check(q.is_ok(), "quantize_rows succeeds");
         if (!q) continue;
@@ -494,7 +494,9 @@ void test_quantizers() {
             den += w[i] * w[i];
         }
         const double rel = std::sqrt(num / den);
-        const double bound = type == 8U ? 0.01 : 0.12;
+        // RMS step error of each code width (Q6_K: 6-bit codes over 16 values)
+        const double bound = type == 8U ? 0.01 : type == 14U ? 0.03 : type == 6U ? 0.06
+                             : type == 1U ? 0.001 : type == 30U ? 0.005 : 0.12;
         check(rel < bound, std::string("quantization error of ") + air::format_name(type) + " is " +
                                std::to_string(rel));
     }
@@ -1000,12 +1002,21 @@ void gpu_golden_sequences(bool fuse, std::uint32_t page_tokens, std::uint32_t st
 
 // A longer sequence across many pages against the C oracle (bit-exact with
 // the reference), interleaved with a second sequence in batched decode.
-void gpu_long_sequences_vs_oracle(std::uint32_t format) {
+// v_down / output: the attn_v + ffn_down and output.weight formats (a
+// Q4_K_M-like mix when Q6_K beside Q4_K).
+void gpu_long_sequences_vs_oracle(std::uint32_t format,
+                                  std::uint32_t v_down = air::SyntheticQwen2Spec::kSameFormat,
+                                  std::uint32_t output = air::SyntheticQwen2Spec::kSameFormat) {
     air::SyntheticQwen2Spec spec;
     spec.config = air::qwen2_config(2, 256, 512, 4, 2, 512, 96);
     spec.weight_format = format;
+    spec.v_down_format = v_down;
+    spec.output_format = output;
     spec.seed = 0xA17C0DE5ULL + format;
-    const std::string tag = "long sequences format " + std::to_string(format) + attention_name();
+    std::string tag = "long sequences format " + std::string(air::format_name(format));
+    if (v_down != air::SyntheticQwen2Spec::kSameFormat) tag += std::string(" v/down ") + air::format_name(v_down);
+    if (output != air::SyntheticQwen2Spec::kSameFormat) tag += std::string(" output ") + air::format_name(output);
+    tag += attention_name();
     std::cout << tag << std::endl;
     auto model = air::make_synthetic_qwen2(spec);
     if (!model) {
@@ -1410,6 +1421,11 @@ int run_gpu() {
         gpu_long_sequences_vs_oracle(2U);
         gpu_long_sequences_vs_oracle(12U);
     }
+    // The encodings without a tile format of their own (dense f32 rows) and
+    // Q5_0 (run as Q8_0), alone and in a Q4_K_M-like mix.
+    for (const std::uint32_t format : {14U, 6U, 1U, 30U}) gpu_long_sequences_vs_oracle(format);
+    gpu_long_sequences_vs_oracle(12U, 14U, 14U);
+    gpu_long_sequences_vs_oracle(8U, 6U, 14U);
     g_attention = air::AttentionExecutionKind::baseline;
     gpu_nonfinite_logits(0x7E00U);
     gpu_nonfinite_logits(0x7C00U);

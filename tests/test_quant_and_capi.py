@@ -76,7 +76,13 @@ def test_library_basics_without_device_work():
     assert capi.canonical_bytes(capi.TYPE_Q4_0, 3584, 18944) == 38_191_104
     assert capi.canonical_bytes(capi.TYPE_Q4_K, 3584, 18944) == 38_191_104
     assert capi.canonical_bytes(capi.TYPE_Q4_K, 896, 4864) == 0   # K not a multiple of 256
-    assert capi.canonical_bytes(30, 64, 64) == 0                  # bf16 is not executed here
+    assert capi.canonical_bytes(capi.TYPE_BF16, 64, 64) == 8192     # every type decode_element takes
+    assert capi.canonical_bytes(capi.TYPE_Q6_K, 3584, 18944) == 55_695_360
+    assert capi.canonical_bytes(capi.TYPE_Q5_0, 896, 4864) == 2_996_224
+    assert capi.canonical_bytes(capi.TYPE_F16, 896, 896) == 1_605_632
+    assert capi.canonical_bytes(capi.TYPE_F32, 32, 3) == 384
+    assert capi.canonical_bytes(capi.TYPE_Q6_K, 896, 4864) == 0   # K not a multiple of 256
+    assert capi.canonical_bytes(3, 64, 64) == 0                   # Q4_1 is not executed here
     with pytest.raises(capi.HipError) as e:
         capi.check(lib.air_hip_context_create(0, None, None))
     assert e.value.status_name == "invalid_argument"
