@@ -993,7 +993,7 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
     case Route::dense: {
         const char* t = m->type == kF32 ? "f32" : m->type == kF16 ? "f16" : m->type == kBF16 ? "bf16" : "q6_k";
         std::snprintf(buf, sizeof buf, "%s (dense f32 rows from %s)",
-                      rows <= 16u ? "dense_rows_kernel" : "dense_gemm_kernel tile=64x64", t);
+                      rows <= 64u ? "dense_rows_kernel" : "dense_gemm_kernel tile=64x64", t);
         break;
     }
     case Route::prefill: {

@@ -8,9 +8,12 @@
 // linear this way.  These kernels are the coverage route for them: plain f32
 // FMA with f32 accumulation, weights read at 4 bytes per element, one launch
 // per linear, no workspace.
-//   rows 1..16: dense_rows_kernel, four output columns per wave, every row
-//               of x per pass over K (the weights are read once);
-//   more rows:  dense_gemm_kernel, 64 x 64 output tiles staged through LDS.
+//   rows 1..64: dense_rows_kernel, four output columns per workgroup for up
+//               to 16 rows of x (K split over its four waves); the weights
+//               are read once per 16 rows (M = 1 at 7B shapes: 5-6 TB/s of
+//               f32 weights);
+//   more rows:  dense_gemm_kernel, 64 x 64 output tiles staged through LDS
+//               (45 TFLOP/s at 512 rows).
 #include "air_hip_device.hpp"
 #include "air_hip_kernels.hpp"
 
@@ -19,20 +22,29 @@ namespace {
 
 constexpr unsigned kDenseThreads = 256;
 constexpr unsigned kDenseCols = 4;       // output columns per wave (rows kernel)
-constexpr unsigned kDenseMaxRows = 16;   // rows kernel covers m <= 16
+constexpr unsigned kDenseMaxRows = 16;   // rows of x per workgroup of the rows kernel
+constexpr unsigned kDenseRowsKernelMax = 64;   // wider x: the tiled GEMM
 constexpr unsigned kGemmTile = 64;
 constexpr unsigned kGemmK = 32;
 
+// One workgroup per kDenseCols output columns and MB rows of x; its four
+// waves split K (wave w takes the 256-element steps w, w + 4, ...), each
+// lane strides its wave's steps by float4, and the four partial sums meet in
+// LDS in a fixed order.
 template <unsigned MB>
 __global__ __launch_bounds__(kDenseThreads) void dense_rows_kernel(const float* __restrict__ w,
                                                                    const float* __restrict__ x,
                                                                    const float* __restrict__ bias,
                                                                    float* __restrict__ y, std::uint32_t m,
                                                                    std::uint64_t k, std::uint64_t n) {
+    constexpr unsigned kWaves = kDenseThreads / 64u;
+    __shared__ float red[kWaves][MB][kDenseCols];
     const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const std::uint64_t n0 =
-        (static_cast<std::uint64_t>(blockIdx.x) * (kDenseThreads / 64u) + wave) * kDenseCols;
-    if (n0 >= n) return;   // no barrier in this kernel
+    const std::uint64_t n0 = static_cast<std::uint64_t>(blockIdx.x) * kDenseCols;
+    const std::uint32_t r0 = blockIdx.y * MB;
+    const std::uint32_t rows = m - r0 < MB ? m - r0 : MB;
+    x += static_cast<std::uint64_t>(r0) * k;
+    y += static_cast<std::uint64_t>(r0) * n;
     const float* wr[kDenseCols];
 #pragma unroll
     for (unsigned c = 0; c < kDenseCols; ++c) {
@@ -44,13 +56,13 @@ __global__ __launch_bounds__(kDenseThreads) void dense_rows_kernel(const float* 
     for (unsigned i = 0; i < MB; ++i)
 #pragma unroll
         for (unsigned c = 0; c < kDenseCols; ++c) acc[i][c] = 0.0f;
-    for (std::uint64_t kk = 4u * lane; kk < k; kk += 256u) {
+    for (std::uint64_t kk = 4u * (lane + 64u * wave); kk < k; kk += 4u * kDenseThreads) {
         float4 wv[kDenseCols];
 #pragma unroll
         for (unsigned c = 0; c < kDenseCols; ++c) wv[c] = *reinterpret_cast<const float4*>(wr[c] + kk);
 #pragma unroll
         for (unsigned i = 0; i < MB; ++i) {
-            if (i < m) {
+            if (i < rows) {
                 const float4 xv = *reinterpret_cast<const float4*>(x + i * k + kk);
 #pragma unroll
                 for (unsigned c = 0; c < kDenseCols; ++c) {
@@ -64,13 +76,21 @@ __global__ __launch_bounds__(kDenseThreads) void dense_rows_kernel(const float* 
     }
 #pragma unroll
     for (unsigned i = 0; i < MB; ++i) {
-        if (i < m) {
 #pragma unroll
-            for (unsigned c = 0; c < kDenseCols; ++c) {
-                float v = acc[i][c];
-                for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-                if (lane == 0u && n0 + c < n) y[i * n + n0 + c] = bias ? v + bias[n0 + c] : v;
-            }
+        for (unsigned c = 0; c < kDenseCols; ++c) {
+            float v = acc[i][c];
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            if (lane == 0u) red[wave][i][c] = v;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < MB * kDenseCols) {
+        const unsigned i = threadIdx.x / kDenseCols, c = threadIdx.x % kDenseCols;
+        if (i < rows && n0 + c < n) {
+            float v = red[0][i][c];
+#pragma unroll
+            for (unsigned q = 1; q < kWaves; ++q) v += red[q][i][c];
+            y[static_cast<std::uint64_t>(i) * n + n0 + c] = bias ? v + bias[n0 + c] : v;
         }
     }
 }
@@ -155,9 +175,8 @@ __global__ __launch_bounds__(kDenseThreads) void dense_rows_gather_kernel(const 
 hipError_t launch_dense_linear(const float* w, std::uint64_t k, std::uint64_t n, const float* x, const float* bias,
                                float* y, std::uint32_t m, hipStream_t stream) {
     if (m == 0u || k == 0u || n == 0u || k % kGemmK != 0u) return hipErrorInvalidValue;
-    if (m <= kDenseMaxRows) {
-        const std::uint64_t cols_per_group = (kDenseThreads / 64u) * kDenseCols;
-        const dim3 grid(static_cast<unsigned>(ceil_div(n, cols_per_group)));
+    if (m <= kDenseRowsKernelMax) {
+        const dim3 grid(static_cast<unsigned>(ceil_div(n, kDenseCols)), static_cast<unsigned>(ceil_div(m, kDenseMaxRows)));
         if (m == 1u) {
             hipLaunchKernelGGL(dense_rows_kernel<1>, grid, dim3(kDenseThreads), 0, stream, w, x, bias, y, m, k, n);
         } else if (m <= 4u) {
