@@ -234,7 +234,9 @@ def test_missing_file_is_io_error(tmp_path):
     assert _load_status(str(tmp_path / "absent.gguf"))[0] == IO_ERROR
 
 
-@pytest.mark.parametrize("weight_format,tied,bias", [(8, False, True), (2, True, False), (12, False, False)])
+@pytest.mark.parametrize("weight_format,tied,bias", [(8, False, True), (2, True, False), (12, False, False),
+                                                    (14, False, False), (6, True, False), (1, False, True),
+                                                    (30, False, False)])
 def test_written_model_round_trips(tmp_path, weight_format, tied, bias):
     m = host_api.Model.synthetic_qwen2(2, 256, 512, 4, 2, 600, context=96, weight_format=weight_format,
                                        embedding_format=8, seed=77 + weight_format, qkv_bias=bias,
