@@ -33,12 +33,14 @@ hipError_t launch_dequantize_canonical(int type, const std::uint8_t* canonical,
                                        std::uint64_t elements, float* out, hipStream_t stream);
 // Q5_0 blocks (device) -> Q8_0 blocks of the same values.
 hipError_t launch_q5_0_to_q8_0(const std::uint8_t* q5_0, std::uint64_t blocks, std::uint8_t* q8_0, hipStream_t stream);
-// Linears over dense f32 rows w[n][k] (k a multiple of 32, x and y 16-byte
-// aligned): y[m][n] = sum_k x[m][k] w[n][k] (+ bias[n]).
-hipError_t launch_dense_linear(const float* w, std::uint64_t k, std::uint64_t n, const float* x, const float* bias,
-                               float* y, std::uint32_t m, hipStream_t stream);
-// out[i][k] = w[rows[i]][k] for rows in [0, n); other ids leave out[i] as is.
-hipError_t launch_dense_rows(const float* w, std::uint64_t k, std::uint64_t n, const std::int32_t* rows,
+// Linears over dense rows w[n][k] stored as `storage` (kF32, or the f16 /
+// bf16 bits of kF16 / kBF16; k a multiple of 32, x and y 16-byte aligned):
+// y[m][n] = sum_k x[m][k] w[n][k] (+ bias[n]).
+hipError_t launch_dense_linear(const void* w, int storage, std::uint64_t k, std::uint64_t n, const float* x,
+                               const float* bias, float* y, std::uint32_t m, hipStream_t stream);
+// out[i][k] = w[rows[i]][k], decoded exactly, for rows in [0, n); other ids
+// leave out[i] as is.
+hipError_t launch_dense_rows(const void* w, int storage, std::uint64_t k, std::uint64_t n, const std::int32_t* rows,
                              std::uint32_t count, float* out, hipStream_t stream);
 
 // Workspace of the split activations for `m` rows of width kp (padded).

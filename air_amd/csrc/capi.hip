@@ -100,7 +100,8 @@ struct air_hip_matrix {
     air_hip_context* owner{nullptr};
     TilePlanes planes;             // planes.type is the resident format (Q5_0 arrives as Q8_0)
     int type{0};                   // the canonical type it was prepared from
-    float* dense{nullptr};         // dense_type(type): f32 rows [n][k] instead of tile planes
+    void* dense{nullptr};          // dense_type(type): rows [n][k] instead of tile planes
+    int dense_storage{0};          // kF32 (F32, Q6_K decoded) or kF16 / kBF16 (the file's own bits)
     std::uint64_t canonical_bytes{0};
     std::uint64_t resident_bytes{0};
 };
@@ -379,9 +380,11 @@ int ensure_split_buffers(air_hip_context* ctx, std::uint64_t partial_bytes, std:
     return AIR_HIP_OK;
 }
 
-// A matrix of a dense type (F32, F16, BF16, Q6_K): its canonical bytes
-// decoded once into f32 rows [n][k], bit for bit as decode_element
-// (cuda_backend.cu:241-344) decodes each element.  k is a multiple of 32.
+// A matrix of a dense type (F32, F16, BF16, Q6_K): rows [n][k].  F32, F16
+// and BF16 keep the file's own rows (the kernels convert as they load, 2
+// bytes per weight for the 16-bit types); Q6_K is decoded once into f32
+// rows, bit for bit as decode_element (cuda_backend.cu:241-344) decodes
+// each element.  k is a multiple of 32.
 int prepare_dense(air_hip_context* ctx, int type, std::uint64_t k, std::uint64_t n, const void* canonical,
                   std::uint64_t canonical_bytes, int bytes_on_device, air_hip_matrix** out) {
     const std::uint64_t expected = air_hip_canonical_bytes(type, k, n);
@@ -403,7 +406,8 @@ int prepare_dense(air_hip_context* ctx, int type, std::uint64_t k, std::uint64_t
     m->planes.type = type;
     m->planes.k = k;
     m->planes.n = n;
-    const std::uint64_t bytes = k * n * sizeof(float);
+    const int storage = type == kQ6_K ? static_cast<int>(kF32) : type;
+    const std::uint64_t bytes = storage == kF32 ? k * n * sizeof(float) : canonical_bytes;
     void* dense = nullptr;
     hipError_t err = hipMalloc(&dense, bytes);
     if (err != hipSuccess) {
@@ -412,13 +416,24 @@ int prepare_dense(air_hip_context* ctx, int type, std::uint64_t k, std::uint64_t
     }
     const std::uint8_t* src = static_cast<const std::uint8_t*>(canonical);
     void* staging = nullptr;
-    if (!bytes_on_device) {
-        err = hipMalloc(&staging, canonical_bytes);
-        if (err == hipSuccess) err = hipMemcpyAsync(staging, canonical, canonical_bytes, hipMemcpyHostToDevice, ctx->stream);
-        if (err == hipSuccess) ctx->host_to_device_bytes.fetch_add(canonical_bytes, std::memory_order_relaxed);
-        src = static_cast<const std::uint8_t*>(staging);
+    if (type != kQ6_K) {
+        // The rows as they are (F32 little-endian, F16 / BF16 bits).
+        err = hipMemcpyAsync(dense, canonical, canonical_bytes,
+                             bytes_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, ctx->stream);
+        if (err == hipSuccess && !bytes_on_device) {
+            ctx->host_to_device_bytes.fetch_add(canonical_bytes, std::memory_order_relaxed);
+        }
+    } else {
+        if (!bytes_on_device) {
+            err = hipMalloc(&staging, canonical_bytes);
+            if (err == hipSuccess) {
+                err = hipMemcpyAsync(staging, canonical, canonical_bytes, hipMemcpyHostToDevice, ctx->stream);
+            }
+            if (err == hipSuccess) ctx->host_to_device_bytes.fetch_add(canonical_bytes, std::memory_order_relaxed);
+            src = static_cast<const std::uint8_t*>(staging);
+        }
+        if (err == hipSuccess) err = launch_dequantize_canonical(type, src, k * n, static_cast<float*>(dense), ctx->stream);
     }
-    if (err == hipSuccess) err = launch_dequantize_canonical(type, src, k * n, static_cast<float*>(dense), ctx->stream);
     if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
     if (staging) {
         if (err != hipSuccess) (void)hipStreamSynchronize(ctx->stream);
@@ -429,7 +444,8 @@ int prepare_dense(air_hip_context* ctx, int type, std::uint64_t k, std::uint64_t
         delete m;
         return hip_fail(err, "decode of dense rows");
     }
-    m->dense = static_cast<float*>(dense);
+    m->dense = dense;
+    m->dense_storage = storage;
     m->resident_bytes = bytes;
     ctx->resident_matrix_bytes.fetch_add(bytes, std::memory_order_relaxed);
     ctx->prepared_matrices.fetch_add(1, std::memory_order_relaxed);
@@ -771,9 +787,13 @@ int air_hip_matrix_dequantize(air_hip_context* ctx, const air_hip_matrix* m, flo
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
     if (m->dense) {
-        const hipError_t err = hipMemcpyAsync(out, m->dense, m->planes.k * m->planes.n * sizeof(float),
-                                              hipMemcpyDeviceToDevice, ctx->stream);
-        return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "hipMemcpyAsync(dense rows)");
+        const std::uint64_t elements = m->planes.k * m->planes.n;
+        const hipError_t err =
+            m->dense_storage == kF32
+                ? hipMemcpyAsync(out, m->dense, elements * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream)
+                : launch_dequantize_canonical(m->dense_storage, static_cast<const std::uint8_t*>(m->dense), elements,
+                                              out, ctx->stream);
+        return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "decode of dense rows");
     }
     const hipError_t err = launch_dequantize_tiles(m->planes, out, ctx->stream);
     if (err != hipSuccess) return hip_fail(err, "dequantize_tiles_kernel");
@@ -935,7 +955,8 @@ int linear_rows(air_hip_context* ctx, const air_hip_matrix* m, const float* x, f
         if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
         DeviceScope scope(ctx->device);
         if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-        const hipError_t err = launch_dense_linear(m->dense, m->planes.k, m->planes.n, x, bias, y, rows, ctx->stream);
+        const hipError_t err = launch_dense_linear(m->dense, m->dense_storage, m->planes.k, m->planes.n, x, bias, y, rows,
+                                                     ctx->stream);
         if (err != hipSuccess) return hip_fail(err, "dense_rows_kernel / dense_gemm_kernel");
         const bool prefill = tactic == AIR_HIP_LINEAR_PREFILL ||
                              (tactic == AIR_HIP_LINEAR_AUTO && rows > AIR_HIP_MAX_DECODE_ROWS);
@@ -992,7 +1013,7 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
     switch (route_linear(ctx, m, rows, tactic)) {
     case Route::dense: {
         const char* t = m->type == kF32 ? "f32" : m->type == kF16 ? "f16" : m->type == kBF16 ? "bf16" : "q6_k";
-        std::snprintf(buf, sizeof buf, "%s (dense f32 rows from %s)",
+        std::snprintf(buf, sizeof buf, m->dense_storage == kF32 ? "%s (dense f32 rows from %s)" : "%s (dense %s rows)",
                       rows <= 64u ? "dense_rows_kernel" : "dense_gemm_kernel tile=64x64", t);
         break;
     }
@@ -1075,7 +1096,8 @@ int air_hip_linear_noalloc(air_hip_context* ctx, const air_hip_matrix* m, const 
     if (m->dense) {   // no scratch: the same launch as air_hip_linear
         DeviceScope scope(ctx->device);
         if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-        const hipError_t err = launch_dense_linear(m->dense, m->planes.k, m->planes.n, x, bias, y, rows, ctx->stream);
+        const hipError_t err = launch_dense_linear(m->dense, m->dense_storage, m->planes.k, m->planes.n, x, bias, y, rows,
+                                                     ctx->stream);
         if (err != hipSuccess) return hip_fail(err, "dense_rows_kernel / dense_gemm_kernel");
         ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
         ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
@@ -1293,7 +1315,8 @@ int air_hip_matrix_rows(air_hip_context* ctx, const air_hip_matrix* m, const int
     if (count > 65535u) return fail(AIR_HIP_UNSUPPORTED, "at most 65535 rows per call");
     DeviceScope scope(ctx->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-    const hipError_t err = m->dense ? launch_dense_rows(m->dense, m->planes.k, m->planes.n, rows, count, out, ctx->stream)
+    const hipError_t err = m->dense ? launch_dense_rows(m->dense, m->dense_storage, m->planes.k, m->planes.n, rows,
+                                                        count, out, ctx->stream)
                                     : launch_matrix_rows(m->planes, rows, count, out, ctx->stream);
     return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "matrix_rows_kernel");
 }

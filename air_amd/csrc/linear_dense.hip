@@ -2,12 +2,13 @@
 //
 // The encodings with no resident tile format here (F32, F16, BF16 and Q6_K;
 // decode_element, src/cuda/cuda_backend.cu:241-344, decodes them per
-// element inside every GEMV) are decoded once at prepare time, bit for bit,
-// into f32 rows w[n][k].  A real Qwen2.5 Q4_K_M file carries Q6_K tensors
+// element inside every GEMV) are held as dense rows w[n][k]: F32, F16 and
+// BF16 as their own GGUF rows (converted exactly to f32 as they are loaded),
+// Q6_K decoded once at prepare time, bit for bit, into f32 rows.  A real Qwen2.5 Q4_K_M file carries Q6_K tensors
 // (lm_head, half the ffn_down / attn_v) and F16 / BF16 files carry every
 // linear this way.  These kernels are the coverage route for them: plain f32
-// FMA with f32 accumulation, weights read at 4 bytes per element, one launch
-// per linear, no workspace.
+// FMA with f32 accumulation, weights read at 4 (F32, Q6_K) or 2 (F16, BF16)
+// bytes per element, one launch per linear, no workspace.
 //   rows 1..64: dense_rows_kernel, four output columns per workgroup for up
 //               to 16 rows of x (K split over its four waves); the weights
 //               are read once per 16 rows (M = 1 at 7B shapes: 5-6 TB/s of
@@ -27,12 +28,32 @@ constexpr unsigned kDenseRowsKernelMax = 64;   // wider x: the tiled GEMM
 constexpr unsigned kGemmTile = 64;
 constexpr unsigned kGemmK = 32;
 
+// Four consecutive weights w[idx .. idx + 3] (idx a multiple of 4) of a
+// dense matrix stored as WT (f32, or f16 / bf16 bits), as exact f32.
+template <int WT>
+__device__ __forceinline__ float4 load_w4(const void* __restrict__ w, std::uint64_t idx) {
+    if constexpr (WT == kF32) {
+        return *reinterpret_cast<const float4*>(static_cast<const float*>(w) + idx);
+    } else {
+        const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const std::uint16_t*>(w) + idx);
+        if constexpr (WT == kF16) {
+            const auto h = [](std::uint32_t b) {
+                return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<std::uint16_t>(b)));
+            };
+            return make_float4(h(v.x & 0xffffu), h(v.x >> 16), h(v.y & 0xffffu), h(v.y >> 16));
+        } else {
+            return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                               __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u));
+        }
+    }
+}
+
 // One workgroup per kDenseCols output columns and MB rows of x; its four
 // waves split K (wave w takes the 256-element steps w, w + 4, ...), each
 // lane strides its wave's steps by float4, and the four partial sums meet in
 // LDS in a fixed order.
-template <unsigned MB>
-__global__ __launch_bounds__(kDenseThreads) void dense_rows_kernel(const float* __restrict__ w,
+template <unsigned MB, int WT>
+__global__ __launch_bounds__(kDenseThreads) void dense_rows_kernel(const void* __restrict__ w,
                                                                    const float* __restrict__ x,
                                                                    const float* __restrict__ bias,
                                                                    float* __restrict__ y, std::uint32_t m,
@@ -45,11 +66,11 @@ __global__ __launch_bounds__(kDenseThreads) void dense_rows_kernel(const float* 
     const std::uint32_t rows = m - r0 < MB ? m - r0 : MB;
     x += static_cast<std::uint64_t>(r0) * k;
     y += static_cast<std::uint64_t>(r0) * n;
-    const float* wr[kDenseCols];
+    std::uint64_t wr[kDenseCols];   // element index of each column's row
 #pragma unroll
     for (unsigned c = 0; c < kDenseCols; ++c) {
         const std::uint64_t col = n0 + c < n ? n0 + c : n - 1u;   // clamped; not stored
-        wr[c] = w + col * k;
+        wr[c] = col * k;
     }
     float acc[MB][kDenseCols];
 #pragma unroll
@@ -59,7 +80,7 @@ __global__ __launch_bounds__(kDenseThreads) void dense_rows_kernel(const float* 
     for (std::uint64_t kk = 4u * (lane + 64u * wave); kk < k; kk += 4u * kDenseThreads) {
         float4 wv[kDenseCols];
 #pragma unroll
-        for (unsigned c = 0; c < kDenseCols; ++c) wv[c] = *reinterpret_cast<const float4*>(wr[c] + kk);
+        for (unsigned c = 0; c < kDenseCols; ++c) wv[c] = load_w4<WT>(w, wr[c] + kk);
 #pragma unroll
         for (unsigned i = 0; i < MB; ++i) {
             if (i < rows) {
@@ -95,7 +116,8 @@ __global__ __launch_bounds__(kDenseThreads) void dense_rows_kernel(const float* 
     }
 }
 
-__global__ __launch_bounds__(kDenseThreads) void dense_gemm_kernel(const float* __restrict__ w,
+template <int WT>
+__global__ __launch_bounds__(kDenseThreads) void dense_gemm_kernel(const void* __restrict__ w,
                                                                    const float* __restrict__ x,
                                                                    const float* __restrict__ bias,
                                                                    float* __restrict__ y, std::uint32_t m,
@@ -118,7 +140,7 @@ __global__ __launch_bounds__(kDenseThreads) void dense_gemm_kernel(const float* 
             const unsigned idx = t + kDenseThreads * h, row = idx >> 3, kq = (idx & 7u) * 4u;
             float4 xv = make_float4(0.f, 0.f, 0.f, 0.f), wv = make_float4(0.f, 0.f, 0.f, 0.f);
             if (m0 + row < m) xv = *reinterpret_cast<const float4*>(x + (m0 + row) * k + k0 + kq);
-            if (n0 + row < n) wv = *reinterpret_cast<const float4*>(w + (n0 + row) * k + k0 + kq);
+            if (n0 + row < n) wv = load_w4<WT>(w, (n0 + row) * k + k0 + kq);
             xs[kq + 0][row] = xv.x;
             xs[kq + 1][row] = xv.y;
             xs[kq + 2][row] = xv.z;
@@ -153,7 +175,10 @@ __global__ __launch_bounds__(kDenseThreads) void dense_gemm_kernel(const float* 
     }
 }
 
-__global__ __launch_bounds__(kDenseThreads) void dense_rows_gather_kernel(const float* __restrict__ w,
+// Embedding rows: out[i] = w[rows[i]] decoded exactly (f16 bits through
+// f16_bits_to_f32, the canonical decode's conversion).
+template <int WT>
+__global__ __launch_bounds__(kDenseThreads) void dense_rows_gather_kernel(const void* __restrict__ w,
                                                                           std::uint64_t k, std::uint64_t n,
                                                                           const std::int32_t* __restrict__ rows,
                                                                           std::uint32_t count,
@@ -162,42 +187,72 @@ __global__ __launch_bounds__(kDenseThreads) void dense_rows_gather_kernel(const 
     if (i >= count) return;
     const std::int32_t row = rows[i];
     if (row < 0 || static_cast<std::uint64_t>(row) >= n) return;
-    const float* src = w + static_cast<std::uint64_t>(row) * k;
+    const std::uint64_t base = static_cast<std::uint64_t>(row) * k;
     float* dst = out + static_cast<std::uint64_t>(i) * k;
     for (std::uint64_t c = blockIdx.x * static_cast<std::uint64_t>(kDenseThreads) + threadIdx.x; c < k;
          c += static_cast<std::uint64_t>(gridDim.x) * kDenseThreads) {
-        dst[c] = src[c];
+        if constexpr (WT == kF32) {
+            dst[c] = static_cast<const float*>(w)[base + c];
+        } else if constexpr (WT == kF16) {
+            dst[c] = f16_bits_to_f32(static_cast<const std::uint16_t*>(w)[base + c]);
+        } else {
+            dst[c] = __uint_as_float(static_cast<std::uint32_t>(static_cast<const std::uint16_t*>(w)[base + c]) << 16);
+        }
     }
 }
 
 } // namespace
 
-hipError_t launch_dense_linear(const float* w, std::uint64_t k, std::uint64_t n, const float* x, const float* bias,
-                               float* y, std::uint32_t m, hipStream_t stream) {
-    if (m == 0u || k == 0u || n == 0u || k % kGemmK != 0u) return hipErrorInvalidValue;
+template <int WT>
+hipError_t launch_dense_typed(const void* w, std::uint64_t k, std::uint64_t n, const float* x, const float* bias,
+                              float* y, std::uint32_t m, hipStream_t stream) {
     if (m <= kDenseRowsKernelMax) {
         const dim3 grid(static_cast<unsigned>(ceil_div(n, kDenseCols)), static_cast<unsigned>(ceil_div(m, kDenseMaxRows)));
         if (m == 1u) {
-            hipLaunchKernelGGL(dense_rows_kernel<1>, grid, dim3(kDenseThreads), 0, stream, w, x, bias, y, m, k, n);
+            hipLaunchKernelGGL((dense_rows_kernel<1, WT>), grid, dim3(kDenseThreads), 0, stream, w, x, bias, y, m, k, n);
         } else if (m <= 4u) {
-            hipLaunchKernelGGL(dense_rows_kernel<4>, grid, dim3(kDenseThreads), 0, stream, w, x, bias, y, m, k, n);
+            hipLaunchKernelGGL((dense_rows_kernel<4, WT>), grid, dim3(kDenseThreads), 0, stream, w, x, bias, y, m, k, n);
         } else {
-            hipLaunchKernelGGL(dense_rows_kernel<kDenseMaxRows>, grid, dim3(kDenseThreads), 0, stream, w, x, bias, y,
-                               m, k, n);
+            hipLaunchKernelGGL((dense_rows_kernel<kDenseMaxRows, WT>), grid, dim3(kDenseThreads), 0, stream, w, x, bias,
+                               y, m, k, n);
         }
     } else {
         const dim3 grid(static_cast<unsigned>(ceil_div(n, kGemmTile)), static_cast<unsigned>(ceil_div(m, kGemmTile)));
-        hipLaunchKernelGGL(dense_gemm_kernel, grid, dim3(kDenseThreads), 0, stream, w, x, bias, y, m, k, n);
+        hipLaunchKernelGGL(dense_gemm_kernel<WT>, grid, dim3(kDenseThreads), 0, stream, w, x, bias, y, m, k, n);
     }
     return hipGetLastError();
 }
 
-hipError_t launch_dense_rows(const float* w, std::uint64_t k, std::uint64_t n, const std::int32_t* rows,
+hipError_t launch_dense_linear(const void* w, int storage, std::uint64_t k, std::uint64_t n, const float* x,
+                               const float* bias, float* y, std::uint32_t m, hipStream_t stream) {
+    if (m == 0u || k == 0u || n == 0u || k % kGemmK != 0u) return hipErrorInvalidValue;
+    switch (storage) {
+    case kF32: return launch_dense_typed<kF32>(w, k, n, x, bias, y, m, stream);
+    case kF16: return launch_dense_typed<kF16>(w, k, n, x, bias, y, m, stream);
+    case kBF16: return launch_dense_typed<kBF16>(w, k, n, x, bias, y, m, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_dense_rows(const void* w, int storage, std::uint64_t k, std::uint64_t n, const std::int32_t* rows,
                              std::uint32_t count, float* out, hipStream_t stream) {
     if (count == 0u) return hipSuccess;
     const unsigned gx = static_cast<unsigned>(std::min<std::uint64_t>(ceil_div(k, kDenseThreads), 64u));
-    hipLaunchKernelGGL(dense_rows_gather_kernel, dim3(gx, count), dim3(kDenseThreads), 0, stream, w, k, n, rows, count,
-                       out);
+    const dim3 grid(gx, count);
+    switch (storage) {
+    case kF32:
+        hipLaunchKernelGGL(dense_rows_gather_kernel<kF32>, grid, dim3(kDenseThreads), 0, stream, w, k, n, rows, count, out);
+        break;
+    case kF16:
+        hipLaunchKernelGGL(dense_rows_gather_kernel<kF16>, grid, dim3(kDenseThreads), 0, stream, w, k, n, rows, count, out);
+        break;
+    case kBF16:
+        hipLaunchKernelGGL(dense_rows_gather_kernel<kBF16>, grid, dim3(kDenseThreads), 0, stream, w, k, n, rows, count,
+                           out);
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
