@@ -49,9 +49,9 @@ typedef enum air_hip_status {
 /* GGML type ids this engine executes: every encoding the reference's
  * decode_element takes (cuda_backend.cu:241-344).  Q8_0, Q4_0 and Q4_K run
  * on their resident tile formats; Q5_0 is rewritten exactly as Q8_0 (same
- * scale, code q - 16) and runs as Q8_0; F32, F16, BF16 and Q6_K are decoded
- * once into dense f32 rows and run on plain f32 FMA kernels (the coverage
- * route: 4 bytes of weights per element). */
+ * scale, code q - 16) and runs as Q8_0; F32, F16 and BF16 keep their own
+ * rows and Q6_K is decoded once into f32 rows, all run on plain f32 FMA
+ * kernels (the coverage route: 2 or 4 bytes of weights per element). */
 enum {
     AIR_HIP_TYPE_F32 = 0,
     AIR_HIP_TYPE_F16 = 1,
