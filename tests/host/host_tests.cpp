@@ -1111,6 +1111,66 @@ void gpu_long_sequences_vs_oracle(std::uint32_t format,
     check(!bad && bad.status().code() == air::ErrorCode::invalid_argument, tag + ": out-of-vocabulary token refused");
 }
 
+// One sequence decoded alone (M = 1 steps) on a model with dense matrices:
+// the step then takes its unfused one-row path (the fused GEMV runs tile
+// formats only).  Greedy tokens and the prompt logits against the oracle.
+void gpu_single_decode_vs_oracle(std::uint32_t format, std::uint32_t v_down, std::uint32_t output) {
+    air::SyntheticQwen2Spec spec;
+    spec.config = air::qwen2_config(2, 256, 512, 4, 2, 512, 96);
+    spec.weight_format = format;
+    spec.v_down_format = v_down;
+    spec.output_format = output;
+    spec.seed = 0xA17C0DE9ULL + format + v_down;
+    const std::string tag = std::string("single decode ") + air::format_name(format) + " v/down " +
+                            air::format_name(v_down) + " output " + air::format_name(output);
+    std::cout << tag << std::endl;
+    auto model = air::make_synthetic_qwen2(spec);
+    if (!model) {
+        check(false, tag + ": model");
+        return;
+    }
+    const auto view = fixture::oracle_view(*model.value());
+    auto prepared = air::HipPreparedModel::create(model.value(), air::HipPrepareOptions{});
+    check(prepared.is_ok(), tag + ": prepare");
+    if (!prepared || !view) return;
+    auto& p = *prepared.value();
+    const std::uint64_t vocab = spec.config.vocabulary_size;
+    std::vector<std::int32_t> prompt;
+    for (int i = 0; i < 11; ++i) prompt.push_back(static_cast<std::int32_t>((37 * i + 5) % vocab));
+    oracle_qwen2_cache cache{};
+    oracle_qwen2_cache_init(&view->model, &cache, spec.config.context_length);
+    std::vector<float> logits(vocab);
+    for (auto t : prompt) oracle_qwen2_step(&view->model, &cache, t, logits.data());
+    const std::vector<float> prompt_logits = logits;
+    std::vector<std::int32_t> expect{static_cast<std::int32_t>(oracle_greedy(logits.data(), vocab))};
+    for (int i = 0; i < 12; ++i) {
+        oracle_qwen2_step(&view->model, &cache, expect.back(), logits.data());
+        expect.push_back(static_cast<std::int32_t>(oracle_greedy(logits.data(), vocab)));
+    }
+    oracle_qwen2_cache_free(&cache);
+    auto seq = p.create_sequence(hip_plan(air::QuantizedLinearExecutionKind::hip_decode, 4U));
+    if (!seq) {
+        check(false, tag + ": create_sequence");
+        return;
+    }
+    auto first = seq.value()->prefill(prompt);
+    if (!first) {
+        check(false, tag + ": prefill");
+        return;
+    }
+    check(rel_l2(first.value(), prompt_logits) <= kDecodeTolerance, tag + ": prompt logits");
+    std::vector<std::int32_t> got{first_max(first.value())};
+    for (int i = 0; i < 12; ++i) {
+        auto next = seq.value()->decode_greedy(got.back());
+        if (!next) {
+            check(false, tag + ": decode: " + next.status().message());
+            return;
+        }
+        got.push_back(next.value());
+    }
+    check(got == expect, tag + ": one-row greedy tokens equal the oracle's");
+}
+
 // KV pool exhaustion: a step that needs more pages than are free fails, its
 // sequence keeps its committed state and the pages stay in the pool.
 void gpu_pool_exhaustion() {
@@ -1426,6 +1486,8 @@ int run_gpu() {
     for (const std::uint32_t format : {14U, 6U, 1U, 30U}) gpu_long_sequences_vs_oracle(format);
     gpu_long_sequences_vs_oracle(12U, 14U, 14U);
     gpu_long_sequences_vs_oracle(8U, 6U, 14U);
+    gpu_single_decode_vs_oracle(12U, 14U, 14U);
+    gpu_single_decode_vs_oracle(1U, 30U, 14U);
     g_attention = air::AttentionExecutionKind::baseline;
     gpu_nonfinite_logits(0x7E00U);
     gpu_nonfinite_logits(0x7C00U);
