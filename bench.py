@@ -521,6 +521,55 @@ def measure_e2e(sequences: int, prompt_tokens: int, new_tokens: int, layers: int
     }
 
 
+def eager_time_ms(torch, stream, fn, steps: int, warmup: int) -> float:
+    """Mean milliseconds per fn() launched eagerly, from HIP events on its stream."""
+    for _ in range(warmup):
+        fn()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def measure_dense(torch, capi, dev, stream, ctx, steps: int, warmup: int, graph: bool = True) -> dict:
+    """The dense route (encodings without a tile format) at Qwen2-7B shapes:
+    F16 (2-byte rows) and Q6_K (decoded f32 rows) down and lm_head, one
+    linear per graph replay.  Random weights of a sane magnitude."""
+    out = {}
+    gen = torch.Generator(device=dev)
+    cases = [(capi.TYPE_F16, "down", FFN, HIDDEN, (1, 16, 32, 64, 512)), (capi.TYPE_F16, "lm_head", HIDDEN, VOCAB, (1,)),
+             (capi.TYPE_Q6_K, "down", FFN, HIDDEN, (1, 16, 32, 64, 512)), (capi.TYPE_Q6_K, "lm_head", HIDDEN, VOCAB, (1,))]
+    for type_id, label, k, n, ms in cases:
+        gen.manual_seed(k + n + type_id)
+        if type_id == capi.TYPE_F16:
+            canon = (torch.randn(n, k, generator=gen, device=dev) * 0.02).half().view(torch.uint8).reshape(-1)
+            stored = n * k * 2
+        else:
+            canon = torch.randint(0, 256, (n * (k // 256), 210), generator=gen, device=dev, dtype=torch.uint8)
+            d = (torch.rand(n * (k // 256), generator=gen, device=dev) * 1e-4 + 1e-5).to(torch.float16)
+            canon[:, 208:210] = d.view(torch.uint8).reshape(-1, 2)
+            canon = canon.reshape(-1)
+            stored = n * k * 4
+        mat = capi.Matrix(ctx, type_id, k, n, canon, canon.numel(), on_device=True)
+        del canon
+        for m in ms:
+            x = torch.randn(m, k, device=dev)
+            y = torch.empty(m, n, device=dev)
+            run = lambda: mat.linear(x, y, m)   # noqa: E731
+            t = graph_time_ms(torch, ctx, dev, stream, run, steps, warmup) if graph else \
+                eager_time_ms(torch, stream, run, steps, warmup)
+            key = f"{capi.TYPE_NAMES[type_id]} {label} {n}x{k} M={m}"
+            out[key] = {"us": round(t * 1e3, 2), "stored_gbps": round(stored / t / 1e6, 1),
+                        "tflops": round(2.0 * m * n * k / t / 1e9, 2), "plan": mat.plan(m)}
+            print(f"# dense {key}: {out[key]}", file=sys.stderr, flush=True)
+        mat.release()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -540,6 +589,8 @@ def main() -> int:
     ap.add_argument("--e2e", default="32,512,128",
                     help="configs[4] end to end: sequences,prompt,new tokens through TokenService ('' = skip)")
     ap.add_argument("--e2e-only", action="store_true", help="run only the end-to-end leg and print its JSON")
+    ap.add_argument("--dense-only", action="store_true",
+                    help="run only the dense-route leg (F16 / Q6_K matrices at 7B shapes) and print its JSON")
     ap.add_argument("--e2e-eager", action="store_true",
                     help="decode steps launch kernel by kernel instead of replaying graphs (for kernel traces)")
     ap.add_argument("--trace-summary", default=None, metavar="CSV",
@@ -582,6 +633,10 @@ def main() -> int:
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream(dev)
     ctx = capi.Context(0, stream.cuda_stream)
+    if args.dense_only:
+        print(json.dumps({"dense": measure_dense(torch, capi, dev, stream, ctx, args.steps, args.warmup,
+                                                 bool(args.graph))}), flush=True)
+        return 0
 
     t_build = time.perf_counter()
     layers = []
