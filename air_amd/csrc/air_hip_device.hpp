@@ -128,7 +128,9 @@ __device__ __forceinline__ void block_scale(float amax, float& s, float& inv) {
 }
 
 // Splits eight scaled activations v*s into f16 hi + lo with hi + lo = v*s to
-// ~21 significant bits (hi truncated, the exact f32 residual rounded).
+// ~21 significant bits: cvt_pkrtz rounds toward zero, so hi is v*s truncated
+// to 11 bits, the residual v*s - hi is exact in f32, and lo is that residual
+// truncated to 11 bits as well (the error is below one ulp of lo).
 __device__ __forceinline__ void split8(const float (&v)[8], float s, half8v& hi, half8v& lo) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
