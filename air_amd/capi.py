@@ -90,6 +90,8 @@ class KvLayout(ctypes.Structure):
         ("layers", ctypes.c_uint32),
         ("max_pages", ctypes.c_uint32),
         ("pool_pages", ctypes.c_uint32),
+        ("chunks", ctypes.c_void_p),       # device chunk table (null: one pool)
+        ("chunk_shift", ctypes.c_uint32),
     ]
 
 

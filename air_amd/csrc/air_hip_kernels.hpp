@@ -1,6 +1,8 @@
 // air_hip_kernels.hpp -- host-side launchers of the HIP kernels (internal).
 #pragma once
 
+#include "air_hip_kv.hpp"
+
 #include <hip/hip_runtime.h>
 #include <cstdint>
 
@@ -195,15 +197,9 @@ hipError_t launch_skinny_linear_x(const TilePlanes& planes, const float* x, cons
 
 // ---- the Qwen2 step around the linears ----------------------------------
 
-// Paged fp32 KV pool: page p holds [layer][2 (K, V)][page_tokens][kv_width].
-struct KvLayout {
-    float* pool{nullptr};
-    std::uint32_t page_tokens{0};
-    std::uint32_t kv_width{0};
-    std::uint32_t layers{0};
-    std::uint32_t max_pages{0};    // page-table row length (int32 entries)
-    std::uint32_t pool_pages{0};
-};
+// Paged fp32 KV pool: page p holds [layer][2 (K, V)][page_tokens][kv_width]
+// floats, in one allocation or in a table of chunks (air_hip_kv.hpp).
+using KvLayout = KvGeometry;
 hipError_t launch_matrix_rows(const TilePlanes& planes, const std::int32_t* rows, std::uint32_t m, float* out,
                               hipStream_t stream);
 hipError_t launch_rms_norm(const float* x, const float* w, float* out, std::uint32_t m, std::uint64_t n, double eps,

@@ -85,7 +85,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_mfma_kernel(
     __shared__ float qs[kTileVectors][LD];
     __shared__ float ks[kChunk][LD];
     __shared__ float vs[kChunk][LD];
-    __shared__ std::int64_t slot_off[2][kChunk];
+    __shared__ std::uint64_t slot_addr[2][kChunk];   // K row of each token's slot (0: absent)
     __shared__ float wave_m[4][kTileVectors];
     __shared__ float wave_l[4][kTileVectors];
 
@@ -105,7 +105,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_mfma_kernel(
         if (tid < kChunk) {   // page table lookup, once per token
             const std::uint64_t token = static_cast<std::uint64_t>(c) * kChunk + tid;
             const float* kp = kv_slot(g, table, layer, token, false);
-            slot_off[buf][tid] = kp ? kp - g.pool : -1;
+            slot_addr[buf][tid] = reinterpret_cast<std::uint64_t>(kp);
         }
     };
     resolve(split, 0u);
@@ -146,11 +146,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_mfma_kernel(
         for (unsigned it = 0; it < kIters; ++it) {
             const unsigned idx = tid + it * kAttnThreads;
             const unsigned t = idx / D4, d4 = idx % D4;
-            const std::int64_t off = slot_off[buf][t];
+            const std::uint64_t addr = slot_addr[buf][t];
             kr[it] = make_float4(0.f, 0.f, 0.f, 0.f);
             vr[it] = kr[it];
-            if (off >= 0) {
-                const float* kp = g.pool + off + static_cast<std::uint64_t>(kvh) * D + 4u * d4;
+            if (addr != 0u) {
+                const float* kp = reinterpret_cast<const float*>(addr) + static_cast<std::uint64_t>(kvh) * D + 4u * d4;
                 kr[it] = load4(kp);
                 vr[it] = load4(kp + v_after_k);
             }
@@ -428,7 +428,7 @@ hipError_t launch_attention_tiles(const KvLayout& kv, const float* qkv, std::uin
                                   std::uint32_t q_heads, std::uint32_t kv_heads, std::uint32_t head_dim,
                                   const AttentionTile* tiles, std::uint32_t tile_count, std::uint32_t splits,
                                   float* partials, float* out, hipStream_t stream) {
-    const KvGeometry g{kv.pool, kv.page_tokens, kv.kv_width, kv.layers, kv.max_pages, kv.pool_pages};
+    const KvGeometry g = kv;
     const float scale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(head_dim)));
     const dim3 grid(tile_count, splits);
 #define AIR_ATTENTION_MFMA(D)                                                                                    \

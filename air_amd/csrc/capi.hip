@@ -1420,14 +1420,24 @@ int air_hip_rope(air_hip_context* ctx, float* qkv, uint64_t row_stride, uint32_t
 
 namespace {
 int check_kv(const air_hip_kv_layout* kv) {
-    if (!kv || !kv->pool) return fail(AIR_HIP_INVALID_ARGUMENT, "KV layout and pool must not be null");
+    if (!kv || (!kv->pool && !kv->chunks)) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "KV layout and its pool (or chunk table) must not be null");
+    }
     if (kv->page_tokens == 0 || kv->kv_width == 0 || kv->layers == 0 || kv->max_pages == 0 || kv->pool_pages == 0) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "KV layout has a zero dimension");
+    }
+    if (kv->pool_pages > static_cast<uint32_t>(INT32_MAX)) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "KV pool pages must fit int32 page ids");
+    }
+    if (kv->chunks && (kv->chunk_shift > 30u || kv->pool_pages % (1u << kv->chunk_shift) != 0u)) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "chunked KV pool: pool_pages must be a whole number of 2^chunk_shift chunks");
     }
     return AIR_HIP_OK;
 }
 KvLayout kv_layout_of(const air_hip_kv_layout* kv) {
-    return KvLayout{kv->pool, kv->page_tokens, kv->kv_width, kv->layers, kv->max_pages, kv->pool_pages};
+    // A chunk table takes precedence: the kernels then never read `pool`.
+    return KvLayout{kv->chunks ? nullptr : kv->pool, kv->page_tokens, kv->kv_width, kv->layers, kv->max_pages,
+                    kv->pool_pages, kv->chunks, kv->chunks ? kv->chunk_shift : 0u};
 }
 int check_heads(const air_hip_kv_layout* kv, uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim,
                 uint64_t max_tokens) {

@@ -807,7 +807,7 @@ hipError_t launch_rope(float* qkv, std::uint64_t stride, std::uint32_t m, const 
 hipError_t launch_kv_append(const KvLayout& kv, const float* qkv, std::uint64_t stride, std::uint64_t q_width,
                             std::uint32_t m, const std::int32_t* positions, const std::int32_t* tables,
                             std::uint32_t layer, hipStream_t stream) {
-    const KvGeometry g{kv.pool, kv.page_tokens, kv.kv_width, kv.layers, kv.max_pages, kv.pool_pages};
+    const KvGeometry g = kv;
     const unsigned gx = static_cast<unsigned>(ceil_div(kv.kv_width, kThreads));
     hipLaunchKernelGGL(kv_append_kernel, dim3(gx, m), dim3(kThreads), 0, stream, g, qkv, stride, q_width, m,
                        positions, tables, layer);
@@ -819,7 +819,7 @@ hipError_t launch_attention(const KvLayout& kv, const float* qkv, std::uint64_t 
                             std::uint32_t q_heads, std::uint32_t kv_heads, std::uint32_t head_dim, double* scratch,
                             std::uint64_t score_stride, float* out, hipStream_t stream) {
     if (head_dim > 512u) return hipErrorInvalidValue;
-    const KvGeometry g{kv.pool, kv.page_tokens, kv.kv_width, kv.layers, kv.max_pages, kv.pool_pages};
+    const KvGeometry g = kv;
     hipLaunchKernelGGL(attention_kernel, dim3(m * q_heads), dim3(kThreads), 0, stream, g, qkv, stride, m, positions,
                        tables, layer, q_heads, kv_heads, head_dim, scratch, score_stride, out);
     return hipGetLastError();
@@ -831,7 +831,7 @@ hipError_t rope_kv_append(const KvLayout& kv, float* qkv, std::uint64_t stride, 
                           std::uint32_t layer, std::uint32_t q_heads, std::uint32_t kv_heads, std::uint32_t head_dim,
                           std::uint32_t rope_dims, const void* table, std::uint64_t table_positions,
                           const QkvSplit* split, hipStream_t stream) {
-    const KvGeometry g{kv.pool, kv.page_tokens, kv.kv_width, kv.layers, kv.max_pages, kv.pool_pages};
+    const KvGeometry g = kv;
     const std::uint64_t per_row = static_cast<std::uint64_t>(q_heads) * (rope_dims / 2u) +
                                   static_cast<std::uint64_t>(kv_heads) * (rope_dims / 2u + head_dim - rope_dims) +
                                   (split ? static_cast<std::uint64_t>(q_heads) * (head_dim - rope_dims) : 0u) +

@@ -52,13 +52,18 @@ struct HipPrepareOptions {
     void* stream{nullptr};              // hipStream_t the engine launches on (null: a stream of its own)
     std::uint32_t max_decode_rows{64};  // workspace reserved for decode widths
     bool fuse{true};                    // concatenate q|k|v and gate|up when formats agree
-    // KV pages allocated with the first sequence; 0 sizes the pool for
-    // max_decode_rows sequences of min(context, 4096) tokens, capped at 40%
-    // of free device memory.
+    // 0 (default): the KV pool grows on demand, a chunk of kv_chunk_pages
+    // pages at a time, and sequence_capacity_bytes answers the device memory
+    // free plus the pool allocated, as the reference's growing pool does
+    // (src/runtime/backend.cpp:541-560).  Otherwise a pool of exactly this
+    // many pages, allocated with the first sequence, which admission is then
+    // held to (a cap on KV memory).
     std::uint32_t kv_pool_pages{0};
-    // Page size of the plans this model will serve: the pool is sized in
-    // these pages, and sequence_capacity_bytes answers with them before the
-    // first sequence exists (a plan with another size is refused then).
+    // Pages per chunk of a growing pool, rounded down to a power of two;
+    // 0: about 256 MiB of pages.
+    std::uint32_t kv_chunk_pages{0};
+    // Page size of the plans this model will serve: a fixed pool is sized in
+    // these pages, and a plan with another page size is refused.
     std::uint32_t kv_page_tokens{16};
     std::uint32_t max_step_rows{512};   // rows per device step (prefill chunk)
     // Decode steps (one row per sequence, greedy outputs) replay one captured
@@ -94,6 +99,8 @@ public:
     [[nodiscard]] std::optional<std::uint64_t> free_device_bytes() const override;
     [[nodiscard]] std::uint64_t kv_pool_allocated_bytes() const noexcept override;
     [[nodiscard]] std::uint64_t kv_pool_free_bytes() const noexcept override;
+    // Pages per growth chunk of the KV pool (0: a fixed pool, or no sequence yet).
+    [[nodiscard]] std::uint32_t engine_chunk_pages() const noexcept;
     [[nodiscard]] Result<runtime_detail::PrefillBatchExecution> prefill_batch(
         std::span<const runtime_detail::PrefillBatchItem> items) override;
     [[nodiscard]] Result<std::vector<TokenId>> decode_greedy_batch(

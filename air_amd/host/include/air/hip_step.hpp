@@ -13,13 +13,18 @@
 // (src/cuda/cuda_backend.cu:2661-3619).
 //
 // KV: fp32 pages of `page_tokens` tokens of every layer (the reference CUDA
-// executor's page pool, cuda_backend.cu:1186-1300), one device pool, a host
-// free list; a sequence owns the pages of its committed tokens.
+// executor's page pool, cuda_backend.cu:1186-1300) and a host free list; a
+// sequence owns the pages of its committed tokens.  By default the pool grows
+// on demand in chunks of 2^k pages, each its own allocation named in a device
+// chunk table (pages never move, so captured decode graphs stay valid), and
+// like the reference's it never shrinks; a pool of a fixed page count is one
+// allocation made with the first sequence.
 #pragma once
 
 #include "air/backend.hpp"
 #include "air/hip_backend.hpp"
 
+#include <atomic>
 #include <cstdint>
 #include <map>
 #include <memory>
@@ -88,9 +93,14 @@ public:
 
     // Bytes of one KV page (every layer's K and V for page_tokens tokens).
     [[nodiscard]] static std::uint64_t kv_page_bytes(const ModelConfig& c, std::uint32_t page_tokens) noexcept;
-    // Pages of the pool the first sequence allocates (the prepare option, or
-    // the default sizing against the device memory free now).
+    // Pages of a fixed pool (HipPrepareOptions::kv_pool_pages), allocated
+    // with the first sequence; 0 when the pool grows on demand.
     [[nodiscard]] static std::uint32_t planned_pool_pages(const HipPreparedModel& prepared, std::uint32_t page_tokens);
+    // log2 of the pages per chunk of a growing pool: `requested` rounded down
+    // to a power of two, or (0) about 256 MiB of pages; 1 to 65536 pages.
+    [[nodiscard]] static std::uint32_t chunk_shift_for(std::uint64_t page_bytes, std::uint32_t requested) noexcept;
+    // Chunk table entries: the most chunks a growing pool can hold.
+    static constexpr std::uint32_t kMaxKvChunks = 4096U;
 
     // Rows of several sequences; the positions are each sequence's next
     // tokens in row order.  The batch commits to every sequence on success.
@@ -100,9 +110,14 @@ public:
 
     [[nodiscard]] std::uint32_t page_tokens() const noexcept { return page_tokens_; }
     [[nodiscard]] std::uint64_t page_bytes() const noexcept { return page_bytes_; }
-    [[nodiscard]] std::uint64_t pool_bytes() const noexcept { return page_bytes_ * pool_pages_; }
+    // Pages allocated so far (a fixed pool: all of them from the start).
+    [[nodiscard]] std::uint64_t pool_bytes() const noexcept { return page_bytes_ * allocated_pages_.load(std::memory_order_relaxed); }
     [[nodiscard]] std::uint64_t free_pool_bytes() const noexcept;
-    [[nodiscard]] std::uint64_t resident_bytes() const noexcept { return resident_bytes_; }
+    [[nodiscard]] bool pool_grows() const noexcept { return growable_; }
+    [[nodiscard]] std::uint32_t chunk_pages() const noexcept { return growable_ ? 1U << chunk_shift_ : 0U; }
+    [[nodiscard]] std::uint64_t resident_bytes() const noexcept {
+        return resident_bytes_ + chunk_bytes_.load(std::memory_order_relaxed);
+    }
     [[nodiscard]] std::uint32_t max_rows() const noexcept { return max_rows_; }
 
     void release_pages(std::vector<std::int32_t>& pages);
@@ -110,6 +125,11 @@ public:
 private:
     explicit HipStepEngine(const HipPreparedModel& prepared) : prepared_(prepared) {}
     [[nodiscard]] Status allocate(void** ptr, std::uint64_t bytes, const char* what);
+    // Adds chunks to a growing pool until `missing` more pages are free
+    // (pool_mutex_ held): each chunk zeroed and its base written to the
+    // device table on the engine's stream, ahead of the step that uses it.
+    [[nodiscard]] Status grow_pool(std::uint64_t missing);
+    [[nodiscard]] air_hip_kv_layout kv_layout(std::uint32_t table_pages) const noexcept;
     [[nodiscard]] Status layers(std::uint32_t m, std::uint64_t max_tokens, std::uint32_t table_pages,
                                 QuantizedLinearExecutionKind tactic, std::uint32_t tiles);
     [[nodiscard]] Status attention(std::uint32_t layer, std::uint32_t m, std::uint64_t max_tokens,
@@ -145,6 +165,14 @@ private:
     std::vector<std::int32_t> free_pages_;
     mutable std::mutex pool_mutex_;
     std::vector<void*> allocations_;  // device buffers, released by the destructor
+
+    // KV pool: one allocation (fixed) or chunks named by a device table.
+    bool growable_{false};
+    std::uint32_t chunk_shift_{0};
+    std::vector<void*> chunks_;              // chunk bases in page-id order, freed by the destructor
+    float** chunk_table_{nullptr};           // device: kMaxKvChunks bases, null where not allocated
+    float** chunk_host_{nullptr};            // pinned host copy each table entry is uploaded from
+    std::atomic<std::uint64_t> allocated_pages_{0}, chunk_bytes_{0};
 
     // device memory
     float* pool_{nullptr};

@@ -390,6 +390,11 @@ Status HipPreparedModel::synchronize() const {
 Result<HipStepEngine*> HipPreparedModel::engine_for(const ExecutionPlan& plan) {
     const std::uint32_t page_tokens = plan.kv.page_tokens.value_or(0U);
     if (page_tokens == 0U) return Status::invalid_argument("HIP sequences need a KV page size");
+    if (page_tokens != options_.kv_page_tokens) {
+        // Capacity and admission are answered in the prepared page size.
+        return Status::invalid_argument("HIP model is prepared for " + std::to_string(options_.kv_page_tokens) +
+                                        "-token KV pages, plan asks for " + std::to_string(page_tokens));
+    }
     if (engine_) {
         if (engine_->page_tokens() != page_tokens) {
             return Status::invalid_argument("HIP KV pool already uses " + std::to_string(engine_->page_tokens()) +
@@ -413,6 +418,10 @@ Result<std::unique_ptr<runtime_detail::SequenceState>> HipPreparedModel::create_
 
 std::uint64_t HipPreparedModel::kv_pool_allocated_bytes() const noexcept {
     return engine_ ? engine_->pool_bytes() : 0U;
+}
+
+std::uint32_t HipPreparedModel::engine_chunk_pages() const noexcept {
+    return engine_ ? engine_->chunk_pages() : 0U;
 }
 
 std::uint64_t HipPreparedModel::kv_pool_free_bytes() const noexcept {
@@ -575,16 +584,21 @@ std::optional<std::uint64_t> HipPreparedModel::free_device_bytes() const {
     return free;
 }
 
-// The fixed KV pool every sequence lives in: once the first sequence exists,
-// the pool allocated; before, the pool that sequence will allocate (in the
-// prepare options' page size).  The reference answers free + allocated bytes
-// because its CUDA pool grows (backend.cpp:541-560); this pool is one
-// allocation sized once, so admission is held to what it can actually give.
+// A growing pool (the default): the device memory free now plus the pool
+// already allocated, the reference's answer (src/runtime/backend.cpp:541-560);
+// unknown when the free memory cannot be read.  A fixed pool: that pool (before
+// the first sequence, the pool it will allocate), since it never grows.
 std::optional<std::uint64_t> HipPreparedModel::sequence_capacity_bytes() const {
-    if (engine_) return engine_->pool_bytes();
-    const std::uint32_t page_tokens = options_.kv_page_tokens;
-    return static_cast<std::uint64_t>(HipStepEngine::planned_pool_pages(*this, page_tokens)) *
-           HipStepEngine::kv_page_bytes(model_->config(), page_tokens);
+    if (options_.kv_pool_pages) {
+        if (engine_) return engine_->pool_bytes();
+        return static_cast<std::uint64_t>(HipStepEngine::planned_pool_pages(*this, options_.kv_page_tokens)) *
+               HipStepEngine::kv_page_bytes(model_->config(), options_.kv_page_tokens);
+    }
+    const auto free = free_device_bytes();
+    if (!free) return std::nullopt;
+    const std::uint64_t pool = kv_pool_allocated_bytes();
+    if (*free > std::numeric_limits<std::uint64_t>::max() - pool) return std::numeric_limits<std::uint64_t>::max();
+    return *free + pool;
 }
 
 Result<std::unique_ptr<runtime_detail::PreparedModel>> prepare_hip_model(std::shared_ptr<const ModelDefinition> model,

@@ -159,7 +159,9 @@ HipStepEngine::~HipStepEngine() {
         if (graph.exec) (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph.exec));
     }
     for (void* p : allocations_) (void)hipFree(p);
+    for (void* p : chunks_) (void)hipFree(p);
     if (staging_) (void)hipHostFree(staging_);
+    if (chunk_host_) (void)hipHostFree(chunk_host_);
     if (owns_embedding_ && embedding_) air_hip_matrix_release(embedding_);
 }
 
@@ -169,18 +171,66 @@ std::uint64_t HipStepEngine::kv_page_bytes(const ModelConfig& c, std::uint32_t p
     return static_cast<std::uint64_t>(c.layer_count) * 2U * page_tokens * kv_width * sizeof(float);
 }
 
-// The fixed pool: room for max_decode_rows sequences of min(context, 4096)
-// tokens, at most 40 % of the device memory free when it is allocated.
 std::uint32_t HipStepEngine::planned_pool_pages(const HipPreparedModel& prepared, std::uint32_t page_tokens) {
-    const auto& c = prepared.model().config();
-    const std::uint64_t page_bytes = kv_page_bytes(c, page_tokens);
-    if (page_tokens == 0U || page_bytes == 0U) return 0U;
-    if (prepared.options().kv_pool_pages) return prepared.options().kv_pool_pages;
-    const std::uint64_t tokens = std::min<std::uint64_t>(c.context_length, 4096U);
-    std::uint64_t pages = static_cast<std::uint64_t>(prepared.options().max_decode_rows) *
-                          ((tokens + page_tokens - 1U) / page_tokens);
-    if (const auto free = prepared.free_device_bytes()) pages = std::min<std::uint64_t>(pages, *free / 10U * 4U / page_bytes);
-    return static_cast<std::uint32_t>(std::min<std::uint64_t>(pages, INT32_MAX));
+    if (page_tokens == 0U || kv_page_bytes(prepared.model().config(), page_tokens) == 0U) return 0U;
+    return prepared.options().kv_pool_pages;
+}
+
+std::uint32_t HipStepEngine::chunk_shift_for(std::uint64_t page_bytes, std::uint32_t requested) noexcept {
+    std::uint64_t pages = requested;
+    if (pages == 0U) pages = page_bytes ? (256ULL << 20) / page_bytes : 1U;
+    pages = std::clamp<std::uint64_t>(pages, 1U, 65536U);
+    std::uint32_t shift = 0;
+    while ((2ULL << shift) <= pages) ++shift;
+    return shift;
+}
+
+air_hip_kv_layout HipStepEngine::kv_layout(std::uint32_t table_pages) const noexcept {
+    const auto& c = prepared_.model().config();
+    return air_hip_kv_layout{pool_, page_tokens_, kv_width_, c.layer_count, table_pages, pool_pages_,
+                             growable_ ? chunk_table_ : nullptr, growable_ ? chunk_shift_ : 0U};
+}
+
+// A growing pool takes chunks as steps need pages: each chunk is zeroed (the
+// attention reads whole chunks of keys, and a slot not yet written must hold
+// finite values) and its base uploaded into the device table, both on the
+// engine's stream, so the step that takes its pages runs after them.  The
+// pages of a new chunk go on the free list lowest id last (taken first).
+Status HipStepEngine::grow_pool(std::uint64_t missing) {
+    const std::uint64_t per_chunk = 1ULL << chunk_shift_;
+    const auto stream_ = static_cast<hipStream_t>(stream());
+    while (missing > 0U) {
+        const std::size_t c = chunks_.size();
+        if (c >= kMaxKvChunks) {
+            return Status::invalid_state("HIP KV page pool exhausted: its chunk table holds " +
+                                         std::to_string(kMaxKvChunks) + " chunks");
+        }
+        const std::uint64_t bytes = per_chunk * page_bytes_;
+        void* chunk = nullptr;
+        if (hipMalloc(&chunk, bytes) != hipSuccess) {
+            (void)hipGetLastError();
+            return Status::invalid_state("HIP KV page pool exhausted: " + std::to_string(missing) +
+                                         " more pages needed and no device memory for a chunk of " +
+                                         std::to_string(per_chunk));
+        }
+        chunks_.push_back(chunk);
+        chunk_host_[c] = static_cast<float*>(chunk);
+        if (Status s = runtime_status(hipMemsetAsync(chunk, 0, bytes, stream_), "hipMemsetAsync(kv chunk)"); !s) {
+            return s;
+        }
+        if (Status s = runtime_status(hipMemcpyAsync(chunk_table_ + c, chunk_host_ + c, sizeof(float*),
+                                                     hipMemcpyHostToDevice, stream_),
+                                      "hipMemcpyAsync(kv chunk table)");
+            !s) {
+            return s;
+        }
+        const auto first = static_cast<std::int32_t>(c * per_chunk);
+        for (std::uint64_t i = per_chunk; i-- > 0U;) free_pages_.push_back(first + static_cast<std::int32_t>(i));
+        allocated_pages_.fetch_add(per_chunk, std::memory_order_relaxed);
+        chunk_bytes_.fetch_add(bytes, std::memory_order_relaxed);
+        missing = missing > per_chunk ? missing - per_chunk : 0U;
+    }
+    return Status::ok();
 }
 
 Result<std::unique_ptr<HipStepEngine>> HipStepEngine::create(const HipPreparedModel& prepared,
@@ -222,12 +272,13 @@ Result<std::unique_ptr<HipStepEngine>> HipStepEngine::create(const HipPreparedMo
     e->ffn_ = c.feed_forward_size;
     e->vocab_ = c.vocabulary_size;
     e->page_bytes_ = kv_page_bytes(c, page_tokens);
-    if (pool_pages == 0U) {
-        pool_pages = planned_pool_pages(prepared, page_tokens);
-        e->pool_pages_ = pool_pages;
-    }
-    if (pool_pages == 0U) return Status::invalid_state("no device memory for one KV page");
+    if (e->page_bytes_ == 0U) return Status::invalid_state("KV pages of zero bytes");
     if (pool_pages > static_cast<std::uint32_t>(INT32_MAX)) return Status::invalid_argument("KV pool is too large");
+    e->growable_ = pool_pages == 0U;
+    if (e->growable_) {
+        e->chunk_shift_ = chunk_shift_for(e->page_bytes_, prepared.options().kv_chunk_pages);
+        e->pool_pages_ = kMaxKvChunks << e->chunk_shift_;   // every page id the table can name
+    }
 
     if (Status s = runtime_status(hipSetDevice(prepared.device()), "hipSetDevice"); !s) return s;
     const auto upload = [&](float** dst, const std::vector<float>& host, const char* what) -> Status {
@@ -296,16 +347,39 @@ Result<std::unique_ptr<HipStepEngine>> HipStepEngine::create(const HipPreparedMo
         if (air_hip_matrix_describe(m, &desc) == AIR_HIP_OK) e->resident_bytes_ += desc.resident_bytes;
     }
 
-    // KV pool, zeroed once.
-    if (Status s = e->allocate(reinterpret_cast<void**>(&e->pool_), e->page_bytes_ * pool_pages, "hipMalloc(kv pool)");
-        !s) {
-        return s;
+    if (e->growable_) {
+        // An empty chunk table; chunks come with the steps that need pages.
+        if (Status s = e->allocate(reinterpret_cast<void**>(&e->chunk_table_), kMaxKvChunks * sizeof(float*),
+                                   "hipMalloc(kv chunk table)");
+            !s) {
+            return s;
+        }
+        if (Status s = runtime_status(hipMemset(e->chunk_table_, 0, kMaxKvChunks * sizeof(float*)),
+                                      "hipMemset(kv chunk table)");
+            !s) {
+            return s;
+        }
+        void* mirror = nullptr;
+        if (Status s = runtime_status(hipHostMalloc(&mirror, kMaxKvChunks * sizeof(float*)), "hipHostMalloc(kv chunks)");
+            !s) {
+            return s;
+        }
+        e->chunk_host_ = static_cast<float**>(mirror);
+    } else {
+        // A fixed pool, zeroed once.
+        if (Status s = e->allocate(reinterpret_cast<void**>(&e->pool_), e->page_bytes_ * pool_pages,
+                                   "hipMalloc(kv pool)");
+            !s) {
+            return s;
+        }
+        if (Status s = runtime_status(hipMemset(e->pool_, 0, e->page_bytes_ * pool_pages), "hipMemset(kv pool)");
+            !s) {
+            return s;
+        }
+        e->free_pages_.resize(pool_pages);
+        for (std::uint32_t i = 0; i < pool_pages; ++i) e->free_pages_[i] = static_cast<std::int32_t>(pool_pages - 1U - i);
+        e->allocated_pages_.store(pool_pages, std::memory_order_relaxed);
     }
-    if (Status s = runtime_status(hipMemset(e->pool_, 0, e->page_bytes_ * pool_pages), "hipMemset(kv pool)"); !s) {
-        return s;
-    }
-    e->free_pages_.resize(pool_pages);
-    for (std::uint32_t i = 0; i < pool_pages; ++i) e->free_pages_[i] = static_cast<std::int32_t>(pool_pages - 1U - i);
 
     // Step buffers.
     const std::uint64_t rows = max_rows;
@@ -398,7 +472,7 @@ Status HipStepEngine::attention(std::uint32_t l, std::uint32_t m, std::uint64_t 
                                 std::uint32_t tiles, bool rope_done) {
     const auto& c = prepared_.model().config();
     air_hip_context* ctx = prepared_.context();
-    const air_hip_kv_layout kv{pool_, page_tokens_, kv_width_, c.layer_count, table_pages, pool_pages_};
+    const air_hip_kv_layout kv = kv_layout(table_pages);
     int rc = AIR_HIP_OK;
     if (!rope_done) {
         rc = air_hip_rope_kv_append(ctx, &kv, qkv_, qkv_width_, m, positions_dev_, tables_dev_, l,
@@ -494,7 +568,7 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
     }
     for (std::uint32_t l = 0; l < c.layer_count; ++l) {
         if (epilogues && prepared_.fused_qkv()) {
-            const air_hip_kv_layout kv{pool_, page_tokens_, kv_width_, c.layer_count, table_pages, pool_pages_};
+            const air_hip_kv_layout kv = kv_layout(table_pages);
             if (Status s = prepared_.linear_rope_kv(l, LinearRole::attn_qkv, normed_, m, qkv_, &kv, positions_dev_,
                                                     tables_dev_, c.attention_head_count, c.kv_head_count, head_dim_,
                                                     c.rope_dimension_count, rope_table_, c.context_length, tactic);
@@ -682,6 +756,9 @@ Result<StepResult> HipStepEngine::run(std::span<const StepRow> rows, QuantizedLi
             const std::uint64_t pages = (claim.sequence->tokens_ + claim.rows + page_tokens_ - 1U) / page_tokens_;
             needed += pages - std::min<std::uint64_t>(pages, claim.sequence->pages_.size());
             table_pages = std::max<std::uint32_t>(table_pages, static_cast<std::uint32_t>(pages));
+        }
+        if (needed > free_pages_.size() && growable_) {
+            if (Status s = grow_pool(needed - free_pages_.size()); !s) return s;
         }
         if (needed > free_pages_.size()) {
             return Status::invalid_state("HIP KV page pool exhausted: " + std::to_string(needed) + " pages needed, " +

@@ -158,7 +158,8 @@ int air_host_engine_create(const air_host_model* model, const air_host_engine_co
     return guarded([&] {
         air::HipPrepareOptions options;
         options.device = config->device;
-        if (config->kv_pool_pages) options.kv_pool_pages = config->kv_pool_pages;
+        options.kv_pool_pages = config->kv_pool_pages;
+        options.kv_chunk_pages = config->kv_chunk_pages;
         options.kv_page_tokens = config->page_tokens ? config->page_tokens : 16U;
         if (config->max_step_rows) options.max_step_rows = config->max_step_rows;
         options.decode_graphs = config->eager_decode == 0;

@@ -57,6 +57,7 @@ class EngineConfig(ctypes.Structure):
         ("device", _I32), ("page_tokens", _U32), ("kv_pool_pages", _U32), ("max_step_rows", _U32),
         ("prefill_tactic", _I32), ("prefill_quantum_tokens", _U32), ("token_budget_per_cycle", _U32),
         ("max_active_requests", _U32), ("attention_tactic", _I32), ("eager_decode", _I32),
+        ("kv_chunk_pages", _U32),
     ]
 
 
@@ -188,10 +189,13 @@ class Engine:
     def __init__(self, model: Model, device: int = 0, page_tokens: int = 16, kv_pool_pages: int = 0,
                  max_step_rows: int = 512, prefill_tactic: int = capi.LINEAR_PREFILL,
                  prefill_quantum_tokens: int = 512, token_budget_per_cycle: int = 512,
-                 max_active_requests: int = 64, attention: int = ATTENTION_ONLINE, eager_decode: bool = False):
+                 max_active_requests: int = 64, attention: int = ATTENTION_ONLINE, eager_decode: bool = False,
+                 kv_chunk_pages: int = 0):
+        # kv_pool_pages 0: the KV pool grows in chunks of kv_chunk_pages pages
+        # (0: about 256 MiB) and capacity is free device memory plus the pool.
         config = EngineConfig(device, page_tokens, kv_pool_pages, max_step_rows, prefill_tactic,
                               prefill_quantum_tokens, token_budget_per_cycle, max_active_requests, attention,
-                              int(eager_decode))
+                              int(eager_decode), kv_chunk_pages)
         out = ctypes.c_void_p()
         check(lib().air_host_engine_create(model.handle, ctypes.byref(config), ctypes.byref(out)))
         self.handle = out.value

@@ -384,10 +384,18 @@ int air_hip_rope(air_hip_context* ctx, float* qkv, uint64_t row_stride, uint32_t
                  uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim, uint32_t rope_dims,
                  const float* table, uint64_t table_positions);
 
-/* Paged fp32 KV cache.  Page p of `pool` holds [layer][K, V][page_tokens]
- * [kv_width] floats for `layers` layers; a sequence is the list of its pages
- * (int32), max_pages entries per page-table row.  Entries outside
- * [0, pool_pages) are skipped by the kernels. */
+/* Paged fp32 KV cache.  A page holds [layer][K, V][page_tokens][kv_width]
+ * floats for `layers` layers; a sequence is the list of its pages (int32),
+ * max_pages entries per page-table row.  The pages live either in one
+ * allocation (`pool`: page p at pool + p pages; `chunks` null) or, for a pool
+ * that grows, in separately allocated chunks of 2^chunk_shift pages: `chunks`
+ * is a device array of pool_pages >> chunk_shift chunk bases, page p lives at
+ * page p & (2^chunk_shift - 1) of chunks[p >> chunk_shift], and a null base is
+ * a chunk not allocated yet.  Entries outside [0, pool_pages), and pages of
+ * unallocated chunks, are skipped by the kernels.  The reference's CUDA pool
+ * grows page by page (src/cuda/cuda_backend.cu:1186-1300); a chunk table
+ * keeps every page where it was, so launches captured before the pool grew
+ * stay valid. */
 typedef struct air_hip_kv_layout {
     float* pool;
     uint32_t page_tokens;
@@ -395,6 +403,8 @@ typedef struct air_hip_kv_layout {
     uint32_t layers;
     uint32_t max_pages;
     uint32_t pool_pages;
+    float* const* chunks;    /* device chunk table, or null for a single pool */
+    uint32_t chunk_shift;    /* log2 of the pages per chunk (<= 30) */
 } air_hip_kv_layout;
 
 /* Writes each row's k and v (the q|k|v row after RoPE) into the slot of

@@ -96,7 +96,8 @@ int air_host_model_tensor(const air_host_model* model, uint32_t index, air_host_
 typedef struct air_host_engine_config {
     int32_t device;
     uint32_t page_tokens;          /* KV page size in tokens (16 in the reference's CUDA plans) */
-    uint32_t kv_pool_pages;        /* KV pages allocated with the first sequence */
+    uint32_t kv_pool_pages;        /* 0: the KV pool grows on demand (capacity = free + allocated); else a
+                                      fixed pool of this many pages, allocated with the first sequence */
     uint32_t max_step_rows;        /* rows per device step (prefill width) */
     int32_t prefill_tactic;        /* AIR_HIP_LINEAR_DECODE or AIR_HIP_LINEAR_PREFILL for prompt blocks */
     uint32_t prefill_quantum_tokens;
@@ -105,6 +106,7 @@ typedef struct air_host_engine_config {
     int32_t attention_tactic;      /* 0 baseline (the reference's double softmax), 1 online softmax (tiled f32) */
     int32_t eager_decode;          /* 1: launch decode steps kernel by kernel instead of replaying a captured
                                       graph per batch width (for kernel-level profiling) */
+    uint32_t kv_chunk_pages;       /* pages per growth chunk of a growing pool (0: about 256 MiB of pages) */
 } air_host_engine_config;
 
 /* Prepares the model on `device` (weights resident, repacked) and creates
@@ -113,10 +115,10 @@ int air_host_engine_create(const air_host_model* model, const air_host_engine_co
 int air_host_engine_release(air_host_engine* engine);
 
 typedef struct air_host_capacity {
-    uint64_t sequence_capacity_bytes;  /* what admission reserves against: the fixed KV pool (before the first
-                                          sequence, the pool it will allocate) */
+    uint64_t sequence_capacity_bytes;  /* what admission reserves against: free device memory plus the KV pool
+                                          allocated (a growing pool), or the fixed pool */
     uint64_t free_device_bytes;        /* hipMemGetInfo free */
-    uint64_t kv_pool_allocated_bytes;  /* 0 until the first sequence */
+    uint64_t kv_pool_allocated_bytes;  /* KV pages allocated so far (0 before any step of a growing pool) */
     uint64_t kv_pool_free_bytes;       /* pool pages no sequence holds */
 } air_host_capacity;
 

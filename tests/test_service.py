@@ -154,29 +154,54 @@ def test_cohort_validation_fails_before_work(torch_cuda):
 
 
 @pytest.mark.gpu
-def test_admission_holds_to_the_fixed_pool_at_7b_width(torch_cuda):
-    """The KV pool is one allocation sized once (max_decode_rows sequences of
-    min(context, 4096) tokens, at most 40 % of free HBM), so
-    sequence_capacity_bytes answers that pool -- before the first sequence
-    the pool it will allocate -- and admission reserves every request's
-    forecast (PreparedModel::estimate_sequence_device_bytes) against it: a
-    cohort larger than the pool runs at most capacity // forecast requests
-    at once and finishes, with the pool whole afterwards.  Qwen2-7B widths
-    (hidden 3584, 28 / 4 heads of 128, FFN 18944), two layers."""
+def test_capacity_is_free_plus_growing_pool_at_7b_width(torch_cuda):
+    """By default the KV pool grows on demand in chunks (each its own
+    allocation, named in a device chunk table), so sequence_capacity_bytes
+    answers the device memory free plus the pool allocated, the reference's
+    answer (src/runtime/backend.cpp:541-560), and admission sees the whole
+    HBM.  With one-page chunks every page boundary a decode step crosses adds
+    a chunk between graph replays; the greedy tokens must equal those of a
+    fixed pool that never grows.  Qwen2-7B widths (hidden 3584, 28 / 4 heads
+    of 128, FFN 18944), two layers."""
     model = host_api.Model.synthetic_qwen2(layers=2, embedding=3584, ffn=18944, heads=28, kv_heads=4, vocab=1024,
                                            context=4096)
     page_bytes = 2 * 2 * 16 * 512 * 4                  # layers x (K, V) x page tokens x kv width x f32
-    engine = host_api.Engine(model, page_tokens=16)
+    prompts = [[(13 * i + 7 * j) % 1024 for j in range(14)] for i in range(3)]
+    fixed = host_api.Engine(model, page_tokens=16, kv_pool_pages=64)
+    expect, _ = fixed.generate_cohort(prompts, 40)
+    fixed.close()
+
+    engine = host_api.Engine(model, page_tokens=16, kv_chunk_pages=1)
     before = engine.capacity()
     assert before["kv_pool_allocated_bytes"] == 0
-    planned = 64 * (4096 // 16) * page_bytes            # 64 decode rows x 4096 tokens, far below 40 % of HBM
-    assert before["sequence_capacity_bytes"] == planned
-    tokens, _ = engine.generate_cohort([[5] * 40, [9] * 40], 8)
-    assert [len(t) for t in tokens] == [8, 8]
+    assert before["sequence_capacity_bytes"] == before["free_device_bytes"]
+    assert before["sequence_capacity_bytes"] > 64 * 2**30    # most of the HBM, not a pool sized up front
+    tokens, stats = engine.generate_cohort(prompts, 40)
+    assert tokens == expect, "graph replays after pool growth differ from a fixed pool"
+    assert stats.max_decode_width == 3
     after = engine.capacity()
-    assert after["kv_pool_allocated_bytes"] == planned == after["sequence_capacity_bytes"]
-    assert after["kv_pool_free_bytes"] == planned
+    # 54 tokens per sequence: 4 pages each, every one a chunk of its own.
+    assert after["kv_pool_allocated_bytes"] == 12 * page_bytes
+    assert after["kv_pool_free_bytes"] == after["kv_pool_allocated_bytes"]
+    assert after["sequence_capacity_bytes"] == after["free_device_bytes"] + after["kv_pool_allocated_bytes"]
+    print(f"7B-width growing pool: capacity {after['sequence_capacity_bytes']} B, "
+          f"{after['kv_pool_allocated_bytes']} B allocated in 12 chunks", flush=True)
     engine.close()
+    model.close()
+
+
+@pytest.mark.gpu
+def test_admission_holds_to_a_fixed_pool_at_7b_width(torch_cuda):
+    """A pool of a fixed page count (kv_pool_pages) is one allocation made
+    with the first sequence and never grows, so sequence_capacity_bytes
+    answers that pool and admission reserves every request's forecast
+    (PreparedModel::estimate_sequence_device_bytes) against it: a cohort
+    larger than the pool runs at most capacity // forecast requests at once
+    and finishes, with the pool whole afterwards.  Qwen2-7B widths, two
+    layers."""
+    model = host_api.Model.synthetic_qwen2(layers=2, embedding=3584, ffn=18944, heads=28, kv_heads=4, vocab=1024,
+                                           context=4096)
+    page_bytes = 2 * 2 * 16 * 512 * 4
 
     # A pool of 12 pages (192 tokens): 48-token requests (3 pages + the
     # page table) fit three at a time.
