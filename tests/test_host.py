@@ -44,3 +44,15 @@ def test_host_gpu_qwen2_7b_width():
     margin-certified top-1 per decision)."""
     assert os.path.exists(BINARY), "tests/host/host_tests is not built"
     _run("gpu7b", 280)
+
+
+@pytest.mark.gpu
+def test_host_gpu_qwen2_7b_decode_widths_64_32():
+    """configs[4]'s decode widths at the Qwen2-7B width (two layers): 64
+    sequences of 8-token prompts in one 512-row prefill_batch step, then
+    graph-replayed decode at width 64 and width 32 and device greedy at
+    width 32, teacher-forced against the C oracle (logits and
+    margin-certified top-1 per decision), after an MFMA and an exact
+    prefill."""
+    assert os.path.exists(BINARY), "tests/host/host_tests is not built"
+    _run("gpu7b-wide", 280)
