@@ -62,16 +62,53 @@ template <> struct GemvFormat<kQ4_K> {
     using Scale = uint4;
 };
 
+// Which D rows a chunk's blocks land in.  The MFMA of a tile's block has its
+// useful output in one D row (= A row), and D row r lives in lane group r / 4,
+// slot r % 4; the lane group owning a block applies its scale.  The rows are
+// laid out so that each lane group owns whole tiles whose scale records it
+// can load itself, one coalesced load per four tiles:
+//   Q8_0 (8 tiles of 2 blocks): tile t, block j -> row 4 (t % 4) + 2 (t / 4)
+//        + j, so group g owns tiles g and g + 4.  A unit of half a chunk (U =
+//        2, tiles 4h .. 4h + 3 of the chunk, its own A operand) puts unit tile
+//        t in rows 4 t + j: group g owns tile g in slots 0 and 1;
+//   Q4_0 (4 tiles of 4 blocks): tile t, block j -> row 4 t + j (group t);
+//   Q4_K (2 tiles of 8 blocks): tile t, block j -> row 8 t + j (groups 2t,
+//        2t + 1 each own four blocks of the tile).
+// A row r of unit h therefore holds chunk block block_of_row(r, h), and is
+// zero unless row_of_unit(r) (Q8_0 half-chunk units use slots 0 and 1 only).
+template <int FMT, int U>
+__device__ __forceinline__ std::uint32_t block_of_row(std::uint32_t r, std::uint32_t h) {
+    if constexpr (FMT == kQ8_0 && U == 1) return 2u * (r >> 2) + 8u * ((r & 3u) >> 1) + (r & 1u);
+    if constexpr (FMT == kQ8_0) return 8u * h + 2u * (r >> 2) + (r & 1u);
+    return r;
+}
+template <int FMT, int U>
+__device__ __forceinline__ bool row_of_unit(std::uint32_t r) {
+    return FMT != kQ8_0 || U == 1 || (r & 3u) < 2u;
+}
+// Tiles of a unit whose scale records a lane loads, and the i-th of them
+// (unit-relative) for lane group g.
+template <int FMT, int T>
+constexpr int own_tiles() { return FMT == kQ8_0 ? T / 4 : 1; }
+template <int FMT>
+__device__ __forceinline__ std::uint32_t own_tile(std::uint32_t g, int i) {
+    if constexpr (FMT == kQ8_0) return g + 4u * static_cast<std::uint32_t>(i);
+    if constexpr (FMT == kQ4_0) return g;
+    return g >> 1;
+}
+
 // One work unit of R row tiles plus the lane's activations: a chunk (16
-// blocks) split into U units of 16/U blocks each.  The activation operand
-// always spans the whole chunk (A row r = block r of the chunk); a unit's
-// tiles use rows [row0, row0 + 16/U).  NORM: the activations are RMS-
-// normalised in the kernel, and nw holds the norm weights of the lane's x.
+// blocks) split into U units of 16/U blocks each (U = 2 for Q8_0 only).  The
+// activation operand spans the whole chunk; a unit's tiles use the rows of
+// its own blocks.  sc holds the scale records of the lane's own tiles.
+// NORM: the activations are RMS-normalised in the kernel, and nw holds the
+// norm weights of the lane's x.
 template <int FMT, int R, int U, bool NORM>
 struct Chunk {
     static constexpr int kTiles = kChunkBlocks / GemvFormat<FMT>::kBlocksPerTile / U;
+    static constexpr int kOwn = own_tiles<FMT, kTiles>();
     uint4 c[kTiles][R][GemvFormat<FMT>::kCodeVecs];
-    typename GemvFormat<FMT>::Scale sc[kTiles][R];
+    typename GemvFormat<FMT>::Scale sc[kOwn][R];
     float4 x[2];
     float4v nw[NORM ? 2 : 1];    // native vectors: struct copies would go to scratch
 };
@@ -82,11 +119,16 @@ __device__ __forceinline__ void load_chunk(Chunk<FMT, R, U, NORM>& ch, const voi
                                            std::uint32_t KT, std::uint32_t unit, std::uint32_t lane,
                                            const float* __restrict__ x, const float* __restrict__ norm_w,
                                            std::uint64_t nblocks) {
+    // Issue order = return order: the activations first (the split they
+    // feed can start while the codes stream), then the scale records,
+    // then the codes tile by tile.
     using F = GemvFormat<FMT>;
     using Scale = typename F::Scale;
     constexpr int T = Chunk<FMT, R, U, NORM>::kTiles;
+    constexpr int kOwn = Chunk<FMT, R, U, NORM>::kOwn;
     const std::uint32_t chunk = unit / U;
     const std::uint32_t kt0 = unit * T;   // first k tile of the unit
+    const std::uint32_t group = lane >> 4;
     if (rt0 + R <= NT && kt0 + T <= KT) {
         // Every tile live (all but the last unit of a ragged K): no fill.
 #pragma unroll
@@ -94,6 +136,10 @@ __device__ __forceinline__ void load_chunk(Chunk<FMT, R, U, NORM>& ch, const voi
             const std::uint64_t tile0 = static_cast<std::uint64_t>(rt0 + r) * KT + kt0;
             const u32x4* cbase = static_cast<const u32x4*>(codes_) + tile0 * F::kCodeVecs * 64u;
             const Scale* sbase = static_cast<const Scale*>(scales_) + tile0 * 16u;
+            // The lane's own tiles' records: consecutive lanes, consecutive
+            // records (Q8_0: 256 contiguous bytes per load).
+#pragma unroll
+            for (int i = 0; i < kOwn; ++i) ch.sc[i][r] = sbase[own_tile<FMT>(group, i) * 16u + (lane & 15u)];
 #pragma unroll
             for (int j = 0; j < T; ++j) {
 #pragma unroll
@@ -101,7 +147,6 @@ __device__ __forceinline__ void load_chunk(Chunk<FMT, R, U, NORM>& ch, const voi
                     const u32x4 word = __builtin_nontemporal_load(cbase + (j * F::kCodeVecs + v) * 64u + lane);
                     ch.c[j][r][v] = make_uint4(word.x, word.y, word.z, word.w);
                 }
-                ch.sc[j][r] = sbase[j * 16u + (lane & 15u)];
             }
         }
     } else {
@@ -114,6 +159,12 @@ __device__ __forceinline__ void load_chunk(Chunk<FMT, R, U, NORM>& ch, const voi
         const Scale* sbase = static_cast<const Scale*>(scales_) + tile0 * 16u;
         const bool row_live = (rt0 + r) < NT;
 #pragma unroll
+        for (int i = 0; i < kOwn; ++i) {
+            const std::uint32_t t = own_tile<FMT>(group, i);
+            const bool live = row_live && kt0 + t < KT;
+            ch.sc[i][r] = live ? sbase[t * 16u + (lane & 15u)] : Scale{};
+        }
+#pragma unroll
         for (int j = 0; j < T; ++j) {
             const bool live = row_live && kt0 + j < KT;
 #pragma unroll
@@ -124,16 +175,14 @@ __device__ __forceinline__ void load_chunk(Chunk<FMT, R, U, NORM>& ch, const voi
                 if (live) word = __builtin_nontemporal_load(cbase + (j * F::kCodeVecs + v) * 64u + lane);
                 ch.c[j][r][v] = make_uint4(word.x, word.y, word.z, word.w);
             }
-            ch.sc[j][r] = live ? sbase[j * 16u + (lane & 15u)] : Scale{};
         }
     }
     }
-    // A row r = lane % 16 holds block chunk*16 + r, elements 8*(lane/16)..+7;
-    // only the unit's own rows are read.
-    constexpr std::uint32_t kUnitBlocks = kChunkBlocks / U;
-    const std::uint32_t row0 = (unit % U) * kUnitBlocks;
-    const std::uint64_t kb = static_cast<std::uint64_t>(chunk) * kChunkBlocks + (lane & 15u);
-    const bool row_used = U == 1 || ((lane & 15u) - row0) < kUnitBlocks;
+    // A row r = lane % 16 holds chunk block block_of_row(r, h), elements
+    // 8*(lane/16)..+7; rows the unit does not use stay zero.
+    const std::uint32_t arow = lane & 15u;
+    const std::uint64_t kb = static_cast<std::uint64_t>(chunk) * kChunkBlocks + block_of_row<FMT, U>(arow, unit % U);
+    const bool row_used = row_of_unit<FMT, U>(arow);
     if (kb < nblocks && row_used) {
         const float4* src = reinterpret_cast<const float4*>(x + kb * 32u + 8u * (lane >> 4));
         ch.x[0] = src[0];
@@ -188,8 +237,7 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U, NORM>& ch, 
                                               std::uint32_t lane, float norm_scale, float4v (&acc)[R]) {
     using F = GemvFormat<FMT>;
     constexpr int T = Chunk<FMT, R, U, NORM>::kTiles;
-    // First A / D row of the unit: a multiple of 16 / U >= 4, so the D slot
-    // (row % 4) of each block is a compile-time constant.
+    // Q4_K's first A / D row of the unit (U = 1 for the 4-bit formats: 0).
     const std::uint32_t row0 = (unit % U) * (kChunkBlocks / U);
     float v[8] = {ch.x[0].x, ch.x[0].y, ch.x[0].z, ch.x[0].w, ch.x[1].x, ch.x[1].y, ch.x[1].z, ch.x[1].w};
     if constexpr (NORM) {
@@ -237,7 +285,6 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U, NORM>& ch, 
         // to zero outside its lane group (those terms add exact zeros).
         const int first = static_cast<int>(4u * group) - static_cast<int>(row0);
         const bool lane_owns = first >= 0 && first < static_cast<int>(kChunkBlocks / U);
-        const std::uint32_t lane_tile = lane_owns ? static_cast<std::uint32_t>(first) >> 3 : 0u;
         const bool upper = (first & 4) != 0;   // sub-blocks 4-7 of the tile
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -254,13 +301,10 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U, NORM>& ch, 
                     sel[rel & 3] = group == owner ? p[rel & 3] : sel[rel & 3];
                 }
             }
-            // The lane's tile record: f16 (d, dmin), then the 12 packed
-            // 6-bit scale / min bytes (src/reference/tensor_reader.cpp:153-165).
-            uint4 rec = ch.sc[0][r];
-#pragma unroll
-            for (int t = 1; t < T; ++t) {
-                if (lane_tile == static_cast<std::uint32_t>(t)) rec = ch.sc[t][r];
-            }
+            // The record of the lane's own tile (first / 8, loaded by
+            // load_chunk): f16 (d, dmin), then the 12 packed 6-bit scale / min
+            // bytes (src/reference/tensor_reader.cpp:153-165).
+            const uint4 rec = ch.sc[0][r];
             const std::uint32_t packed[3] = {rec.y, rec.z, rec.w};
             std::uint32_t scales = 0, mins = 0;
             q4k_scale_min_x4(packed, upper, scales, mins);
@@ -276,21 +320,24 @@ __device__ __forceinline__ void compute_chunk(const Chunk<FMT, R, U, NORM>& ch, 
     }
 #pragma unroll
     for (int t = 0; t < (FMT == kQ4_K ? 0 : T); ++t) {
-        const std::uint32_t first_row = row0 + static_cast<std::uint32_t>(t * F::kBlocksPerTile);
-        const bool own = group == (first_row >> 2);
+        // Owner lane group and the D slot of block j: Q8_0 tile t of a whole
+        // chunk is owned by group t % 4 in slots 2 (t / 4) + j, tile t of a
+        // half chunk by group t in slots j; Q4_0 tile t by group t in slots j.
+        const std::uint32_t owner = FMT == kQ8_0 ? static_cast<std::uint32_t>(t & 3) : static_cast<std::uint32_t>(t);
+        const bool own = group == owner;
         typename F::Scale sc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             if constexpr (FMT == kQ8_0) {
-                sc[r] = own ? ch.sc[t][r] : 0u;
+                sc[r] = own ? ch.sc[t >> 2][r] : 0u;
             } else if constexpr (FMT == kQ4_0) {
-                sc[r] = own ? ch.sc[t][r] : make_uint2(0u, 0u);
+                sc[r] = own ? ch.sc[0][r] : make_uint2(0u, 0u);
             }
         }
+        const int slot0 = FMT == kQ8_0 && U == 1 ? 2 * (t >> 2) : 0;
 #pragma unroll
         for (int j = 0; j < F::kBlocksPerTile; ++j) {
-            const int rel = t * F::kBlocksPerTile + j;             // row within the unit
-            const int i = rel & 3;                                  // D slot of this block
+            const int i = slot0 + j;                                // D slot of this block
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const half8v w = tile_block_codes<FMT, R, U, NORM>(ch, t, r, j);
