@@ -12,6 +12,7 @@
 #include "air_hip_layout.hpp"
 
 #include <hip/hip_runtime.h>
+#include <rocprofiler-sdk-roctx/roctx.h>
 
 #include <algorithm>
 #include <atomic>
@@ -107,6 +108,17 @@ struct air_hip_matrix {
 };
 
 namespace {
+
+// ROCTX range around a linear entry point: air.hip.matvec (one row) or
+// air.hip.matmul, the names of the reference's ranges around its linears
+// (src/cuda/cuda_backend.cu:1899,1958, air.cuda.*), for rocprofv3
+// --marker-trace.
+struct LinearRange {
+    explicit LinearRange(uint32_t rows) noexcept { roctxRangePushA(rows == 1u ? "air.hip.matvec" : "air.hip.matmul"); }
+    ~LinearRange() { roctxRangePop(); }
+    LinearRange(const LinearRange&) = delete;
+    LinearRange& operator=(const LinearRange&) = delete;
+};
 
 thread_local std::string g_last_error;
 
@@ -819,6 +831,7 @@ int air_hip_dequantize_canonical(air_hip_context* ctx, int type, const void* can
 
 int air_hip_decode_linear_fused(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y,
                                 const float* bias, const float* norm_weight, double eps, int epilogue) {
+    const LinearRange range(1u);
     if (!ctx || !m || !x || !y) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix, x and y must not be null");
     forget_loaded_source(ctx);
     if (static_cast<const void*>(x) == static_cast<const void*>(y)) {
@@ -1072,6 +1085,7 @@ extern "C" {
 
 int air_hip_linear(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y,
                    const float* bias, uint32_t rows, int tactic) {
+    const LinearRange range(rows);
     return linear_rows(ctx, m, x, y, bias, rows, tactic, nullptr, nullptr);
 }
 
@@ -1184,6 +1198,7 @@ int air_hip_linear_plan(const air_hip_context* ctx, const air_hip_matrix* m, uin
 int air_hip_linear_epilogue(air_hip_context* ctx, const air_hip_matrix* m, const float* x, uint32_t rows, float* out,
                             const float* bias, int epilogue, const float* norm_weight, float* norm_out, double eps,
                             int tactic) {
+    const LinearRange range(rows);
     if (!ctx || !m || !x || !out) return fail(AIR_HIP_INVALID_ARGUMENT, "context, matrix, x and out must not be null");
     if (epilogue != AIR_HIP_EPILOGUE_RESIDUAL && epilogue != AIR_HIP_EPILOGUE_SWIGLU &&
         epilogue != AIR_HIP_EPILOGUE_RESIDUAL_LOAD && epilogue != AIR_HIP_EPILOGUE_RESIDUAL_PREFILL) {
@@ -1514,6 +1529,7 @@ int air_hip_linear_rope_kv(air_hip_context* ctx, const air_hip_matrix* m, const 
                            const int32_t* page_tables, uint32_t layer, uint32_t q_heads, uint32_t kv_heads,
                            uint32_t head_dim, uint32_t rope_dims, const float* table, uint64_t table_positions,
                            int tactic) {
+    const LinearRange range(rows);
     if (!ctx || !m || !x || !qkv || !positions || !page_tables || !table) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
     }

@@ -156,6 +156,7 @@ private:
         std::uint64_t generation{0};  // context buffers the launches point into
     };
     std::map<std::uint64_t, DecodeGraph> graphs_;
+    const char* layer_range_{"air.prefill.layer"};   // ROCTX range name of the current step's layers
 
     const HipPreparedModel& prepared_;
     std::uint32_t page_tokens_{0}, pool_pages_{0}, max_rows_{0}, max_pages_{0}, output_rows_{0};

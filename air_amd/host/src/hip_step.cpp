@@ -8,6 +8,7 @@
 // 325-428) operation by operation; its validation messages are the
 // reference's (reference_executor.cpp:328-335).
 #include "air/hip_step.hpp"
+#include "air/profile.hpp"
 
 #include "air/synthetic.hpp"
 #include "air_hip.h"
@@ -473,6 +474,8 @@ Status HipStepEngine::attention(std::uint32_t l, std::uint32_t m, std::uint64_t 
     const auto& c = prepared_.model().config();
     air_hip_context* ctx = prepared_.context();
     const air_hip_kv_layout kv = kv_layout(table_pages);
+    const bool decode = layer_range_[4] == 'd';   // "air.decode..." (cuda_backend.cu:2202,2232)
+    const ScopedRange range(decode ? "air.hip.attention_decode" : "air.hip.attention_prefill");
     int rc = AIR_HIP_OK;
     if (!rope_done) {
         rc = air_hip_rope_kv_append(ctx, &kv, qkv_, qkv_width_, m, positions_dev_, tables_dev_, l,
@@ -510,8 +513,10 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
     const bool fuse = m == 1U && tactic == QuantizedLinearExecutionKind::hip_decode && prepared_.fused_qkv() &&
                       prepared_.fused_gate_up() && prepared_.tile_formats();
     const double eps = c.rms_norm_epsilon;
+    const char* layer_range = layer_range_;
     if (fuse) {
         for (std::uint32_t l = 0; l < c.layer_count; ++l) {
+            const ScopedRange range(layer_range);
             if (Status s = prepared_.decode_linear_fused(l, LinearRole::attn_qkv, hidden_, qkv_, attn_norm_[l], eps,
                                                          AIR_HIP_EPILOGUE_STORE);
                 !s) {
@@ -567,6 +572,7 @@ Status HipStepEngine::layers(std::uint32_t m, std::uint64_t max_tokens, std::uin
         return hip_status(rc);
     }
     for (std::uint32_t l = 0; l < c.layer_count; ++l) {
+        const ScopedRange range(layer_range);
         if (epilogues && prepared_.fused_qkv()) {
             const air_hip_kv_layout kv = kv_layout(table_pages);
             if (Status s = prepared_.linear_rope_kv(l, LinearRole::attn_qkv, normed_, m, qkv_, &kv, positions_dev_,
@@ -656,7 +662,11 @@ Status HipStepEngine::decode_device(std::uint32_t m, std::uint64_t max_tokens, s
                                     QuantizedLinearExecutionKind block, QuantizedLinearExecutionKind output,
                                     std::uint32_t tiles) {
     if (Status s = layers(m, max_tokens, table_pages, block, tiles); !s) return s;
-    if (Status s = prepared_.linear(0, LinearRole::output, normed_, logits_, m, output); !s) return s;
+    {
+        const ScopedRange range(m == 1U ? "air.decode.output_projection" : "air.decode.batch.output_projection");
+        if (Status s = prepared_.linear(0, LinearRole::output, normed_, logits_, m, output); !s) return s;
+    }
+    const ScopedRange range("air.hip.greedy_select");
     return hip_status(air_hip_argmax(prepared_.context(), logits_, m, vocab_, argmax_dev_));
 }
 
@@ -834,8 +844,16 @@ Result<StepResult> HipStepEngine::run(std::span<const StepRow> rows, QuantizedLi
     positions_dev_ = positions_dev;
     tables_dev_ = tables_dev;
 
-    Status status = decode_shape ? decode_graph(m, max_tokens, table_pages, block_tactic, output_tactic, tiles)
-                                 : layers(m, max_tokens, table_pages, block_tactic, tiles);
+    // The reference's stage names (cuda_backend.cu:2678,2894,3099,3253).
+    layer_range_ = decode_shape ? (m == 1U ? "air.decode.layer" : "air.decode.batch.layer")
+                                : (claims.size() > 1U ? "air.prefill.multi_sequence.layer" : "air.prefill.layer");
+    Status status;
+    {
+        const ScopedRange range(decode_shape ? (m == 1U ? "air.decode.step" : "air.decode.batch")
+                                             : (claims.size() > 1U ? "air.prefill.multi_sequence" : "air.prefill.chunk"));
+        status = decode_shape ? decode_graph(m, max_tokens, table_pages, block_tactic, output_tactic, tiles)
+                              : layers(m, max_tokens, table_pages, block_tactic, tiles);
+    }
 
     // Output rows: lm_head (+bias) over their final-normed rows, argmax, in
     // chunks of the logits buffer.
@@ -866,6 +884,8 @@ Result<StepResult> HipStepEngine::run(std::span<const StepRow> rows, QuantizedLi
         }
         if (!status) break;
         if (!decode_shape) {  // a decode-shaped step has its logits and argmax already
+            const ScopedRange range(claims.size() > 1U ? "air.prefill.multi_sequence.output_projection"
+                                                       : "air.prefill.output_projection");
             if (!(status = prepared_.linear(0, LinearRole::output, x, logits_, k, output_tactic))) break;
             if (const int rc = air_hip_argmax(ctx, logits_, k, vocab_, argmax_dev_); rc != AIR_HIP_OK) {
                 status = hip_status(rc);
@@ -877,6 +897,7 @@ Result<StepResult> HipStepEngine::run(std::span<const StepRow> rows, QuantizedLi
                                       "hipMemcpyAsync(argmax)"))) {
             break;
         }
+        const ScopedRange readback("air.hip.logit_readback");
         std::vector<std::vector<float>> logits;
         for (std::uint32_t j = 0; j < k && status; ++j) {
             if (rows[outputs[begin + j]].output != RowOutput::logits) continue;

@@ -227,6 +227,34 @@ def read_traffic(m: int):
         return None
 
 
+def measure_copy_peak(torch, dev, gib: int = 2, reps: int = 20) -> dict:
+    """The device's own streaming rate beside the 8 TB/s spec: a device-to-
+    device copy of `gib` GiB (torch's copy kernel), read + write bytes per
+    second, best of three timed groups of `reps` copies."""
+    n = gib * (1 << 30) // 4
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(3):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            dst.copy_(src)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        best = ms if best is None else min(best, ms)
+    del src, dst
+    torch.cuda.empty_cache()
+    gbps = 2.0 * n * 4 / (best * 1e-3) / 1e9
+    return {"measured_copy_gbps": round(gbps, 1), "frac_of_spec": round(gbps / HBM_PEAK_GBS, 4),
+            "how": f"torch device-to-device copy of {gib} GiB, read + write bytes, best of 3 x {reps}"}
+
+
 def measure_prefill(torch, ctx, capi, layers, m, steps, dev, stream):
     """One prefill pass over the layers' linears at M rows on the prefill
     tactic (the f16 MFMA GEMM), timed with HIP events on the context's
@@ -778,6 +806,10 @@ def main() -> int:
                 "unit": "GB/s",
                 "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
                 "traffic": read_traffic(m),
+                # FETCH_SIZE + WRITE_SIZE per gate|up launch from the committed
+                # counter passes, not measured in this run.
+                "traffic_source": "profiles/traffic_gate_up_q8_0.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE "
+                                  "over bench.py --traffic-probe, calibrated on a copy kernel)",
                 "m": m,
                 "bytes_per_launch": gate_up_launch_bytes(m),
                 "avg_launch_us": round(gu_avg_ms * 1e3, 2),
@@ -817,6 +849,12 @@ def main() -> int:
         e2e = measure_e2e(seqs, prompt, new, args.layers)
         print(f"# e2e: {e2e}", file=sys.stderr, flush=True)
 
+    hbm = measure_copy_peak(torch, dev)
+    print(f"# hbm: {hbm}", file=sys.stderr, flush=True)
+    if roofline is not None:
+        roofline["measured_copy_gbps"] = hbm["measured_copy_gbps"]
+        roofline["frac_of_measured_copy"] = round(roofline["achieved"] / hbm["measured_copy_gbps"], 4)
+
     head = ms[0]
     line = {
         "metric": "Q8_0 linear HBM GB/s (% of peak) + Qwen2-7B-shape decode tok/s at M=1/32",
@@ -842,6 +880,7 @@ def main() -> int:
             "model_build_s": round(build_s, 1),
         },
         "roofline": roofline,
+        "hbm": hbm,
         "cpu_baseline": cpu,
         "prefill": prefill,
         "formats": formats,
