@@ -42,6 +42,23 @@ hipError_t launch_dense_linear(const void* w, int storage, std::uint64_t k, std:
                                const float* bias, float* y, std::uint32_t m, hipStream_t stream);
 // out[i][k] = w[rows[i]][k], decoded exactly, for rows in [0, n); other ids
 // leave out[i] as is.
+// Resident bytes of a dense matrix stored as `storage` (kQ6_K: 208-byte
+// super-block records plus 2 bytes of d each; 0 when k does not fit).
+std::uint64_t dense_resident_bytes(int storage, std::uint64_t k, std::uint64_t n);
+// Launch shape of the M = 1 Q6_K GEMV: output columns per workgroup and
+// waves splitting K (compiled: 4x4, 4x8, 4x16, 8x4, 8x8);
+// set_q6k_gemv_shape overrides the planner for sweeps ({0, 0} restores it).
+struct Q6kGemvShape {
+    unsigned columns{0};
+    unsigned waves{0};
+};
+Q6kGemvShape q6k_gemv_shape(std::uint64_t k, std::uint64_t n);
+void set_q6k_gemv_shape(const Q6kGemvShape& shape);
+// Canonical Q6_K blocks (device) -> 208-byte records and the d plane.
+hipError_t launch_q6k_records(const void* canonical, std::uint64_t blocks, void* records, hipStream_t stream);
+// Dense matrix -> f32 [n][k], bit-exact decode.
+hipError_t launch_dense_dequantize(const void* w, int storage, std::uint64_t k, std::uint64_t n, float* out,
+                                   hipStream_t stream);
 hipError_t launch_dense_rows(const void* w, int storage, std::uint64_t k, std::uint64_t n, const std::int32_t* rows,
                              std::uint32_t count, float* out, hipStream_t stream);
 

@@ -102,7 +102,7 @@ struct air_hip_matrix {
     TilePlanes planes;             // planes.type is the resident format (Q5_0 arrives as Q8_0)
     int type{0};                   // the canonical type it was prepared from
     void* dense{nullptr};          // dense_type(type): rows [n][k] instead of tile planes
-    int dense_storage{0};          // kF32 (F32, Q6_K decoded) or kF16 / kBF16 (the file's own bits)
+    int dense_storage{0};          // the type of the rows: kF32, kF16 / kBF16 (GGUF rows) or kQ6_K (212-byte records)
     std::uint64_t canonical_bytes{0};
     std::uint64_t resident_bytes{0};
 };
@@ -392,11 +392,12 @@ int ensure_split_buffers(air_hip_context* ctx, std::uint64_t partial_bytes, std:
     return AIR_HIP_OK;
 }
 
-// A matrix of a dense type (F32, F16, BF16, Q6_K): rows [n][k].  F32, F16
-// and BF16 keep the file's own rows (the kernels convert as they load, 2
-// bytes per weight for the 16-bit types); Q6_K is decoded once into f32
-// rows, bit for bit as decode_element (cuda_backend.cu:241-344) decodes
-// each element.  k is a multiple of 32.
+// A matrix of a dense type (F32, F16, BF16, Q6_K): rows [n][k] in the
+// file's own encoding.  F32, F16 and BF16 keep the GGUF rows; Q6_K keeps its
+// super-blocks, each padded from 210 to 212 bytes (4-byte aligned words).
+// The kernels decode as they load, bit for bit as decode_element
+// (cuda_backend.cu:241-344) decodes each element.  k is a multiple of 32
+// (256 for Q6_K, its super-block).
 int prepare_dense(air_hip_context* ctx, int type, std::uint64_t k, std::uint64_t n, const void* canonical,
                   std::uint64_t canonical_bytes, int bytes_on_device, air_hip_matrix** out) {
     const std::uint64_t expected = air_hip_canonical_bytes(type, k, n);
@@ -418,8 +419,10 @@ int prepare_dense(air_hip_context* ctx, int type, std::uint64_t k, std::uint64_t
     m->planes.type = type;
     m->planes.k = k;
     m->planes.n = n;
-    const int storage = type == kQ6_K ? static_cast<int>(kF32) : type;
-    const std::uint64_t bytes = storage == kF32 ? k * n * sizeof(float) : canonical_bytes;
+    const int storage = type;
+    const std::uint64_t bytes = dense_resident_bytes(storage, k, n);
+    if (bytes == 0) return fail(AIR_HIP_UNSUPPORTED, "dense storage of type %d does not fit k = %llu", type,
+                                static_cast<unsigned long long>(k));
     void* dense = nullptr;
     hipError_t err = hipMalloc(&dense, bytes);
     if (err != hipSuccess) {
@@ -444,7 +447,7 @@ int prepare_dense(air_hip_context* ctx, int type, std::uint64_t k, std::uint64_t
             if (err == hipSuccess) ctx->host_to_device_bytes.fetch_add(canonical_bytes, std::memory_order_relaxed);
             src = static_cast<const std::uint8_t*>(staging);
         }
-        if (err == hipSuccess) err = launch_dequantize_canonical(type, src, k * n, static_cast<float*>(dense), ctx->stream);
+        if (err == hipSuccess) err = launch_q6k_records(src, k * n / 256u, dense, ctx->stream);
     }
     if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
     if (staging) {
@@ -454,7 +457,7 @@ int prepare_dense(air_hip_context* ctx, int type, std::uint64_t k, std::uint64_t
     if (err != hipSuccess) {
         (void)hipFree(dense);
         delete m;
-        return hip_fail(err, "decode of dense rows");
+        return hip_fail(err, "dense rows");
     }
     m->dense = dense;
     m->dense_storage = storage;
@@ -803,8 +806,7 @@ int air_hip_matrix_dequantize(air_hip_context* ctx, const air_hip_matrix* m, flo
         const hipError_t err =
             m->dense_storage == kF32
                 ? hipMemcpyAsync(out, m->dense, elements * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream)
-                : launch_dequantize_canonical(m->dense_storage, static_cast<const std::uint8_t*>(m->dense), elements,
-                                              out, ctx->stream);
+                : launch_dense_dequantize(m->dense, m->dense_storage, m->planes.k, m->planes.n, out, ctx->stream);
         return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "decode of dense rows");
     }
     const hipError_t err = launch_dequantize_tiles(m->planes, out, ctx->stream);
@@ -1026,7 +1028,13 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
     switch (route_linear(ctx, m, rows, tactic)) {
     case Route::dense: {
         const char* t = m->type == kF32 ? "f32" : m->type == kF16 ? "f16" : m->type == kBF16 ? "bf16" : "q6_k";
-        std::snprintf(buf, sizeof buf, m->dense_storage == kF32 ? "%s (dense f32 rows from %s)" : "%s (dense %s rows)",
+        if (m->type == kQ6_K && rows == 1u) {
+            const Q6kGemvShape q = q6k_gemv_shape(m->planes.k, m->planes.n);
+            std::snprintf(buf, sizeof buf, "q6k_gemv_kernel columns=%u waves=%u (dense q6_k super-block rows)", q.columns,
+                          q.waves);
+            break;
+        }
+        std::snprintf(buf, sizeof buf, m->type == kQ6_K ? "%s (dense %s super-block rows)" : "%s (dense %s rows)",
                       rows <= 64u ? "dense_rows_kernel" : "dense_gemm_kernel tile=64x64", t);
         break;
     }

@@ -49,9 +49,9 @@ typedef enum air_hip_status {
 /* GGML type ids this engine executes: every encoding the reference's
  * decode_element takes (cuda_backend.cu:241-344).  Q8_0, Q4_0 and Q4_K run
  * on their resident tile formats; Q5_0 is rewritten exactly as Q8_0 (same
- * scale, code q - 16) and runs as Q8_0; F32, F16 and BF16 keep their own
- * rows and Q6_K is decoded once into f32 rows, all run on plain f32 FMA
- * kernels (the coverage route: 2 or 4 bytes of weights per element). */
+ * scale, code q - 16) and runs as Q8_0; F32, F16, BF16 and Q6_K keep their
+ * own rows (Q6_K its 210-byte super-blocks padded to 212 bytes: 0.83 bytes
+ * per weight) and run on plain f32 FMA kernels that decode as they load. */
 enum {
     AIR_HIP_TYPE_F32 = 0,
     AIR_HIP_TYPE_F16 = 1,
@@ -202,7 +202,7 @@ uint64_t air_hip_canonical_bytes(int type, uint64_t k, uint64_t n);
  * the reference does only for dp4a (pack_signed32_weights_kernel,
  * cuda_backend.cu:398-427).  k must be a multiple of the block size
  * (cuda_backend.cu:1797-1801).  Blocks until the repack has finished.
- * Dense types (F32, F16, BF16, Q6_K) need k a multiple of 32; their
+ * Dense types (F32, F16, BF16, Q6_K) need k a multiple of 32 (Q6_K: 256); their
  * matrices take f32 rows through air_hip_linear (any tactic and width, the
  * epilogue entry points running their epilogues as separate launches), not
  * air_hip_linear_loaded or air_hip_decode_linear_fused (UNSUPPORTED).

@@ -1133,6 +1133,31 @@ void gpu_long_sequences_vs_oracle(std::uint32_t format,
     const std::int32_t bad_token = static_cast<std::int32_t>(vocab);
     const auto bad = seqs[1]->decode_greedy(bad_token);
     check(!bad && bad.status().code() == air::ErrorCode::invalid_argument, tag + ": out-of-vocabulary token refused");
+
+    // The same prompts on the prefill tactic, one two-sequence prefill_batch
+    // step: the f16 MFMA prefill GEMM, the norms and the SwiGLU writing the
+    // next GEMM's operand, o's residual epilogue (or, for a dense o, its
+    // separate residual + norm); prompt logits within the MFMA path's 1e-2.
+    const auto prefill_plan = hip_plan(air::QuantizedLinearExecutionKind::hip_prefill, 4U);
+    std::unique_ptr<air::runtime_detail::SequenceState> prefilled[2];
+    std::vector<air::runtime_detail::PrefillBatchItem> items;
+    for (int s = 0; s < 2; ++s) {
+        auto created = p.create_sequence(prefill_plan);
+        if (!created) {
+            check(false, tag + ": prefill-tactic sequence");
+            return;
+        }
+        prefilled[s] = std::move(created).value();
+        items.push_back({prefilled[s].get(), prompts[s], air::runtime_detail::PrefillBatchOutput::logits});
+    }
+    auto batch = p.prefill_batch(items);
+    check(batch.is_ok() && batch.value().items.size() == 2U, tag + ": prefill-tactic batch step");
+    if (batch) {
+        for (int s = 0; s < 2; ++s) {
+            const double err = rel_l2(batch.value().items[s].logits, expect_logits[s][0]);
+            check(err <= kPrefillTolerance, tag + ": prefill-tactic prompt logits rel-L2 " + std::to_string(err));
+        }
+    }
 }
 
 // One sequence decoded alone (M = 1 steps) on a model with dense matrices:

@@ -102,6 +102,12 @@ def test_new_types_match_oracle(torch_cuda, hip_ctx, type_id, k, n):
     try:
         desc = mat.describe()
         assert desc["type"] == type_id and desc["k"] == k and desc["n"] == n
+        # Resident bytes: the file's own encoding (Q6_K: 210 bytes per
+        # super-block, as records plus a plane of scales), never f32 rows.
+        resident = {capi.TYPE_F32: 4 * k * n, capi.TYPE_F16: 2 * k * n, capi.TYPE_BF16: 2 * k * n,
+                    capi.TYPE_Q6_K: k * n // 256 * 210}
+        if type_id in resident:
+            assert desc["resident_bytes"] == resident[type_id], (desc, resident[type_id])
         # resident decode and embedding rows, bit for bit
         want_w = oracle.decode(type_id, canon, k * n).reshape(n, k)
         got_w = torch.empty((n, k), dtype=torch.float32, device="cuda:0")
