@@ -46,7 +46,7 @@ hipError_t launch_dense_linear(const void* w, int storage, std::uint64_t k, std:
 // super-block records plus 2 bytes of d each; 0 when k does not fit).
 std::uint64_t dense_resident_bytes(int storage, std::uint64_t k, std::uint64_t n);
 // Launch shape of the M = 1 Q6_K GEMV: output columns per workgroup and
-// waves splitting K (compiled: 4x4, 4x8, 4x16, 8x4, 8x8);
+// waves splitting K (compiled: 2x4, 4x4);
 // set_q6k_gemv_shape overrides the planner for sweeps ({0, 0} restores it).
 struct Q6kGemvShape {
     unsigned columns{0};

@@ -245,70 +245,89 @@ __global__ __launch_bounds__(kDenseThreads) void dense_rows_gather_kernel(const 
 // group of a super-block -- group g = 8 h + 2 j + g1 holds elements
 // 128 h + 32 j + 16 g1 .. + 15, its low nibbles in 16 bytes of ql (nibble
 // j >> 1), its high bits in 16 bytes of qh (bits 2j, 2j + 1), one 6-bit
-// sub-block scale -- for the workgroup's C consecutive output columns, four
-// at a time, so its 16 activations are loaded once per super-block and C
-// columns.  Sixteen lanes cover a super-block, a wave four, the workgroup's
-// kWaves waves 4 kWaves per step.  Each weight is fma(d * sc, q, -32 * d * sc),
+// sub-block scale -- for the workgroup's C consecutive output columns, so
+// its 16 activations are loaded once per super-block and C columns.
+// Sixteen lanes cover a super-block, a wave four, the workgroup's kWaves
+// waves 4 kWaves per step.  Software-pipelined: a wave holds the loads of its
+// next step (activations and every column's codes) in flight while it
+// computes the current one.  Each weight is fma(d * sc, q, -32 * d * sc),
 // which rounds once and so equals the reference's (d * sc) * (q - 32), then
 // enters an f32 FMA with x; lane and wave partials meet in a fixed order.
-constexpr unsigned kQ6Chunk = 4;   // columns whose codes are in flight together
 template <unsigned C, unsigned kWaves>
-__global__ __launch_bounds__(64 * kWaves) void q6k_gemv_kernel(const unsigned char* __restrict__ w,
-                                                                 const float* __restrict__ x,
-                                                                 const float* __restrict__ bias,
-                                                                 float* __restrict__ y, std::uint64_t k,
-                                                                 std::uint64_t n) {
+__global__ __launch_bounds__(64 * kWaves) void q6k_gemv_pipe_kernel(const unsigned char* __restrict__ w,
+                                                                    const float* __restrict__ x,
+                                                                    const float* __restrict__ bias,
+                                                                    float* __restrict__ y, std::uint64_t k,
+                                                                    std::uint64_t n) {
     __shared__ float red[kWaves][C];
     const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const std::uint64_t sbs = k / 256u;                  // super-blocks per row
+    const std::uint64_t sbs = k / 256u;
     const std::uint16_t* dplane = q6k_d_plane(w, sbs * n);
     const std::uint64_t c0 = static_cast<std::uint64_t>(blockIdx.x) * C;
     const std::uint32_t g = lane & 15u, h = g >> 3, j = (g >> 1) & 3u, g1 = g & 1u;
-    const std::uint32_t e0 = 128u * h + 32u * j + 16u * g1;   // first element of the group
+    const std::uint32_t e0 = 128u * h + 32u * j + 16u * g1;
     const std::uint32_t ql_off = 64u * h + 32u * (j & 1u) + 16u * g1;
     const std::uint32_t qh_off = 128u + 32u * h + 16u * g1;
     const std::uint32_t sc_off = 192u + 8u * h + 2u * j + g1;
+    struct Step {
+        float4 x[4];
+        u32x4 ql[C], qh[C];
+        std::uint32_t sc[C], d[C];
+    };
+    const auto load = [&](Step& st, std::uint64_t sb) __attribute__((always_inline)) {
+        const float4* xp = reinterpret_cast<const float4*>(x + sb * 256u + e0);
+#pragma unroll
+        for (unsigned i = 0; i < 4; ++i) st.x[i] = xp[i];
+#pragma unroll
+        for (unsigned c = 0; c < C; ++c) {
+            const std::uint64_t col = c0 + c < n ? c0 + c : n - 1u;   // clamped; not stored
+            const std::uint64_t blk = col * sbs + sb;
+            const unsigned char* rec = w + blk * kQ6kRecord;
+            st.ql[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rec + ql_off));
+            st.qh[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rec + qh_off));
+            st.sc[c] = rec[sc_off];
+            st.d[c] = dplane[blk];
+        }
+    };
     float acc[C];
 #pragma unroll
     for (unsigned c = 0; c < C; ++c) acc[c] = 0.0f;
-    for (std::uint64_t sb = 4u * wave + (lane >> 4); sb < sbs; sb += 4u * kWaves) {
-        const float4* xp = reinterpret_cast<const float4*>(x + sb * 256u + e0);
-        const float4 xa = xp[0], xb = xp[1], xc = xp[2], xd = xp[3];
-        const float xv[16] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w,
-                              xc.x, xc.y, xc.z, xc.w, xd.x, xd.y, xd.z, xd.w};
+    const auto compute = [&](const Step& st) __attribute__((always_inline)) {
+        const float xv[16] = {st.x[0].x, st.x[0].y, st.x[0].z, st.x[0].w, st.x[1].x, st.x[1].y, st.x[1].z, st.x[1].w,
+                              st.x[2].x, st.x[2].y, st.x[2].z, st.x[2].w, st.x[3].x, st.x[3].y, st.x[3].z, st.x[3].w};
 #pragma unroll
-        for (unsigned c4 = 0; c4 < C; c4 += kQ6Chunk) {
-            u32x4 ql[kQ6Chunk], qh[kQ6Chunk];
-            std::uint32_t sc[kQ6Chunk], dbits[kQ6Chunk];
+        for (unsigned c = 0; c < C; ++c) {
+            const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<std::uint16_t>(st.d[c])));
+            const float ds = d * static_cast<float>(static_cast<int>(static_cast<std::int8_t>(st.sc[c])));
+            const float bias32 = -32.0f * ds;
 #pragma unroll
-            for (unsigned c = 0; c < kQ6Chunk; ++c) {
-                const std::uint64_t col = c0 + c4 + c < n ? c0 + c4 + c : n - 1u;   // clamped; not stored
-                const std::uint64_t blk = col * sbs + sb;
-                const unsigned char* rec = w + blk * kQ6kRecord;
-                ql[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rec + ql_off));
-                qh[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rec + qh_off));
-                sc[c] = rec[sc_off];
-                dbits[c] = dplane[blk];
-            }
+            for (unsigned t = 0; t < 4; ++t) {
+                const std::uint32_t lo = st.ql[c][t], hi = st.qh[c][t];
+                const std::uint32_t nib = (j >> 1) ? (lo >> 4) & 0x0f0f0f0fu : lo & 0x0f0f0f0fu;
+                const std::uint32_t q = nib | (((hi >> (2u * j)) & 0x03030303u) << 4);
 #pragma unroll
-            for (unsigned c = 0; c < kQ6Chunk; ++c) {
-                // Hardware f16 -> f32: exact for every finite half and infinity.
-                const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<std::uint16_t>(dbits[c])));
-                const float ds = d * static_cast<float>(static_cast<int>(static_cast<std::int8_t>(sc[c])));
-                const float bias32 = -32.0f * ds;
-#pragma unroll
-                for (unsigned t = 0; t < 4; ++t) {
-                    const std::uint32_t lo = ql[c][t], hi = qh[c][t];
-                    const std::uint32_t nib = (j >> 1) ? (lo >> 4) & 0x0f0f0f0fu : lo & 0x0f0f0f0fu;
-                    const std::uint32_t q = nib | (((hi >> (2u * j)) & 0x03030303u) << 4);
-#pragma unroll
-                    for (unsigned b = 0; b < 4; ++b) {
-                        const float wq = fmaf(ds, static_cast<float>((q >> (8u * b)) & 0xffu), bias32);
-                        acc[c4 + c] = fmaf(wq, xv[4u * t + b], acc[c4 + c]);
-                    }
+                for (unsigned b = 0; b < 4; ++b) {
+                    const float wq = fmaf(ds, static_cast<float>((q >> (8u * b)) & 0xffu), bias32);
+                    acc[c] = fmaf(wq, xv[4u * t + b], acc[c]);
                 }
             }
         }
+    };
+    const std::uint64_t stride = 4u * kWaves;
+    std::uint64_t sb = 4u * wave + (lane >> 4);
+    // Lanes past the last super-block stay in the loop (uniform trip count
+    // per wave is not needed: each lane's loads are its own) but load nothing.
+    Step a, b;
+    if (sb < sbs) load(a, sb);
+    while (sb < sbs) {
+        const std::uint64_t next = sb + stride;
+        if (next < sbs) load(b, next);
+        compute(a);
+        if (next >= sbs) break;
+        const std::uint64_t after = next + stride;
+        if (after < sbs) load(a, after);
+        compute(b);
+        sb = after;
     }
 #pragma unroll
     for (unsigned c = 0; c < C; ++c) {
@@ -368,12 +387,13 @@ void set_q6k_gemv_shape(const Q6kGemvShape& shape) { g_q6k_shape = shape; }
 Q6kGemvShape q6k_gemv_shape(std::uint64_t k, std::uint64_t n) {
     if (g_q6k_shape.columns != 0u) return g_q6k_shape;
     (void)n;
-    // Measured on the Qwen2-7B shapes (graphs of distinct matrices): long K
-    // (down, 74 super-blocks per row) 8 columns per workgroup, 26.2 us
-    // against 28.4 with 4; short K (o, lm_head) 4 columns (o 7.0 us, lm_head
-    // 168 us against 7.8 and 175).  More waves splitting K were slower
-    // everywhere.
-    return k >= 8192u ? Q6kGemvShape{8u, 4u} : Q6kGemvShape{4u, 4u};
+    // Measured on the Qwen2-7B shapes (graphs of distinct matrices, so no
+    // matrix is served from the Infinity Cache): long K (down, 74
+    // super-blocks per row) 4 columns per workgroup, 21.9 us (2.5 TB/s of its
+    // own bytes; without the pipeline 26.5 us at its best shape, f32 rows
+    // 42 us); short K (o, lm_head: one step per wave) 2 columns, 6.9 and
+    // 167 us.  Eight columns, or more waves splitting K, were slower.
+    return k >= 8192u ? Q6kGemvShape{4u, 4u} : Q6kGemvShape{2u, 4u};
 }
 
 std::uint64_t dense_resident_bytes(int storage, std::uint64_t k, std::uint64_t n) {
@@ -417,10 +437,10 @@ hipError_t launch_dense_typed(const void* w, std::uint64_t k, std::uint64_t n, c
         const dim3 grid(static_cast<unsigned>(ceil_div(n, shape.columns)));
 #define AIR_Q6K_GEMV(C, W)                                                                                          \
         if (shape.columns == C && shape.waves == W) {                                                               \
-            hipLaunchKernelGGL((q6k_gemv_kernel<C, W>), grid, dim3(64 * W), 0, stream, wb, x, bias, y, k, n);       \
+            hipLaunchKernelGGL((q6k_gemv_pipe_kernel<C, W>), grid, dim3(64 * W), 0, stream, wb, x, bias, y, k, n);  \
             return hipGetLastError();                                                                               \
         }
-        AIR_Q6K_GEMV(4, 4) AIR_Q6K_GEMV(4, 8) AIR_Q6K_GEMV(4, 16) AIR_Q6K_GEMV(8, 4) AIR_Q6K_GEMV(8, 8)
+        AIR_Q6K_GEMV(2, 4) AIR_Q6K_GEMV(4, 4)
 #undef AIR_Q6K_GEMV
         return hipErrorInvalidConfiguration;
     }
