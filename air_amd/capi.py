@@ -118,6 +118,7 @@ SIGNATURES = {
     "air_hip_last_error": (ctypes.c_char_p, []),
     "air_hip_device_count": (_I, [ctypes.POINTER(_I)]),
     "air_hip_mem_info": (_I, [_I, ctypes.POINTER(_U64), ctypes.POINTER(_U64)]),
+    "air_hip_stream_read": (_I, [_P, _P, _U64, _P, _U64]),
     "air_hip_context_create": (_I, [_I, _P, ctypes.POINTER(_P)]),
     "air_hip_context_destroy": (_I, [_P]),
     "air_hip_context_set_stream": (_I, [_P, _P]),
@@ -254,6 +255,12 @@ class Context:
 
     def set_prefill_tuning(self, tile_m: int = 0, tile_n: int = 0, k_splits: int = 0, prefetch: int = 0) -> None:
         check(lib().air_hip_context_set_prefill_tuning(self.handle, tile_m, tile_n, k_splits, prefetch))
+
+    def stream_read(self, data, nbytes: int, sink, sink_words: int) -> None:
+        """air_hip_stream_read: one read of `nbytes` device bytes, the XOR of
+        each chunk's words stored in a word of the zeroed uint32 `sink`
+        (`sink_words` long); the checksum is the XOR of the sink's words."""
+        check(lib().air_hip_stream_read(self.handle, ptr(data), nbytes, ptr(sink), sink_words))
 
     def stats(self) -> dict:
         s = Stats()

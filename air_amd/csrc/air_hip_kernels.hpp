@@ -42,6 +42,12 @@ hipError_t launch_dense_linear(const void* w, int storage, std::uint64_t k, std:
                                const float* bias, float* y, std::uint32_t m, hipStream_t stream);
 // out[i][k] = w[rows[i]][k], decoded exactly, for rows in [0, n); other ids
 // leave out[i] as is.
+// XOR checksum of `bytes` (a multiple of 16) of device memory: one word per
+// chunk stored in `sink` (sink_words >= 1; the caller zeroes it and XORs
+// its words), read once with the decode GEMV's access pattern -- the
+// streaming floor of a launch of that size.
+hipError_t launch_stream_read(const void* data, std::uint64_t bytes, unsigned* sink, std::uint64_t sink_words,
+                              hipStream_t stream);
 // Resident bytes of a dense matrix stored as `storage` (kQ6_K: 208-byte
 // super-block records plus 2 bytes of d each; 0 when k does not fit).
 std::uint64_t dense_resident_bytes(int storage, std::uint64_t k, std::uint64_t n);

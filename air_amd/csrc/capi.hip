@@ -645,6 +645,20 @@ int air_hip_context_stats(const air_hip_context* ctx, air_hip_stats* out) {
     return AIR_HIP_OK;
 }
 
+int air_hip_stream_read(air_hip_context* ctx, const void* data, uint64_t bytes, uint32_t* sink,
+                        uint64_t sink_words) {
+    if (!ctx || !data || !sink) return fail(AIR_HIP_INVALID_ARGUMENT, "arguments must not be null");
+    if (sink_words == 0u) return fail(AIR_HIP_INVALID_ARGUMENT, "the sink needs at least one word");
+    if (bytes % 16u != 0u) return fail(AIR_HIP_INVALID_ARGUMENT, "byte count must be a multiple of 16");
+    if (reinterpret_cast<std::uintptr_t>(data) % 16u != 0u) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "data must be 16-byte aligned");
+    }
+    DeviceScope scope(ctx->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    const hipError_t err = launch_stream_read(data, bytes, sink, sink_words, ctx->stream);
+    return err == hipSuccess ? AIR_HIP_OK : hip_fail(err, "stream_read_kernel");
+}
+
 uint64_t air_hip_canonical_bytes(int type, uint64_t k, uint64_t n) {
     const auto geo = canonical_block(type);
     if (geo.elements == 0 || k % geo.elements != 0) return 0;

@@ -255,6 +255,32 @@ def measure_copy_peak(torch, dev, gib: int = 2, reps: int = 20) -> dict:
             "how": f"torch device-to-device copy of {gib} GiB, read + write bytes, best of 3 x {reps}"}
 
 
+def measure_stream_floor(torch, ctx, dev, stream, steps: int, warmup: int, layers: int) -> dict:
+    """The floor of each M = 1 linear of the configs[2] step as launched
+    here: one air_hip_stream_read pass (read the matrix's resident bytes once,
+    the decode GEMV's access pattern, nothing else) per launch, over as many
+    distinct buffers as the step has of that matrix, replayed as a graph like
+    the step.  The step's floor is 28 launches of each layer matrix plus the
+    lm_head: what 113 separate launches can reach whatever the arithmetic."""
+    shapes = {"qkv": w_bytes(HIDDEN, HIDDEN + 2 * KV), "o": w_bytes(HIDDEN, HIDDEN),
+              "gate_up": w_bytes(HIDDEN, 2 * FFN), "down": w_bytes(FFN, HIDDEN), "lm_head": w_bytes(HIDDEN, VOCAB)}
+    sink_words = 1 << 16
+    sink = torch.zeros(sink_words, dtype=torch.int32, device=dev)
+    us = {}
+    for name, nbytes in shapes.items():
+        count = 1 if name == "lm_head" else layers
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(max(count, 4 if name == "lm_head" else 1))]
+        run = lambda: [ctx.stream_read(b, nbytes, sink, sink_words) for b in bufs]   # noqa: E731
+        us[name] = round(graph_time_ms(torch, ctx, dev, stream, run, steps, warmup) * 1e3 / len(bufs), 2)
+        del bufs
+        torch.cuda.empty_cache()
+    step_ms = (layers * (us["qkv"] + us["o"] + us["gate_up"] + us["down"]) + us["lm_head"]) / 1e3
+    algo = step_algorithmic_bytes(1, layers)
+    return {"us_per_launch": us, "step_ms": round(step_ms, 4),
+            "step_pct_of_hbm_peak": round(100.0 * algo / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+            "how": "air_hip_stream_read over each matrix's resident bytes, one launch each, graphs of distinct buffers"}
+
+
 def measure_prefill(torch, ctx, capi, layers, m, steps, dev, stream):
     """One prefill pass over the layers' linears at M rows on the prefill
     tactic (the f16 MFMA GEMM), timed with HIP events on the context's
@@ -855,6 +881,11 @@ def main() -> int:
         print(f"# e2e: {e2e}", file=sys.stderr, flush=True)
 
     hbm = measure_copy_peak(torch, dev)
+    if 1 in results:
+        hbm["stream_floor_m1"] = measure_stream_floor(torch, ctx, dev, stream, max(5, args.steps // 2), args.warmup,
+                                                      args.layers)
+        hbm["stream_floor_m1"]["step_frac_of_floor"] = round(hbm["stream_floor_m1"]["step_ms"] /
+                                                             results[1]["ms_per_step"], 4)
     print(f"# hbm: {hbm}", file=sys.stderr, flush=True)
     if roofline is not None:
         roofline["measured_copy_gbps"] = hbm["measured_copy_gbps"]

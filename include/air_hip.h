@@ -173,6 +173,16 @@ int air_hip_context_set_decode_path(air_hip_context* ctx, uint32_t path, uint32_
  * rows the linear then runs on split activations).  No counterpart in the
  * reference. */
 int air_hip_context_set_decode_pipeline(air_hip_context* ctx, uint32_t lds_stages);
+/* Reads `bytes` (a multiple of 16) of device memory once on the context's
+ * stream and stores the XOR of each chunk's 32-bit words in a word of
+ * `sink` (sink_words >= 1 words of device memory the caller zeroes; the
+ * checksum, the XOR of all sink words, does not depend on the chunking): the
+ * streaming floor of one launch of that size, with the decode GEMV's access
+ * pattern (a workgroup per contiguous chunk, 16-byte non-temporal loads).
+ * The benchmark prices each linear against it.  No counterpart in the
+ * reference. */
+int air_hip_stream_read(air_hip_context* ctx, const void* data, uint64_t bytes, uint32_t* sink,
+                        uint64_t sink_words);
 /* Chooses how the prefill GEMM stages its operands (autotuning): 0 =
  * automatic, 1 = through registers (prefill_gemm_kernel), 2..4 = an LDS ring
  * of that many 64-k steps filled by direct global -> LDS loads
