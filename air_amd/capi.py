@@ -127,6 +127,7 @@ SIGNATURES = {
     "air_hip_context_set_tuning": (_I, [_P, _U32, _U32, _U32]),
     "air_hip_context_set_prefill_tuning": (_I, [_P, _U32, _U32, _U32, _U32]),
     "air_hip_context_set_decode_path": (_I, [_P, _U32, _U32, _U32]),
+    "air_hip_context_set_wsplit": (_I, [_P, _U32, _U32, _U32, _U32, _U32, _U32]),
     "air_hip_context_set_prefill_pipeline": (_I, [_P, _U32]),
     "air_hip_context_set_decode_pipeline": (_I, [_P, _U32]),
     "air_hip_matrix_rows": (_I, [_P, _P, _P, _U32, _P]),
@@ -244,6 +245,13 @@ class Context:
 
     def set_decode_path(self, path: int = 0, tile_n: int = 0, k_splits: int = 0) -> None:
         check(lib().air_hip_context_set_decode_path(self.handle, path, tile_n, k_splits))
+
+    def set_wsplit(self, mode: int = 0, tile_n: int = 0, waves: int = 0, depth: int = 0, k_splits: int = 0,
+                   split_x: int = 0) -> None:
+        """Wave-split decode kernel for 2..64 rows: mode 0 automatic, 1 always,
+        2 never, plus launch-shape overrides (0 = automatic; split_x 1 = split
+        into the workspace first, 2 = in each wave)."""
+        check(lib().air_hip_context_set_wsplit(self.handle, mode, tile_n, waves, depth, k_splits, split_x))
 
     def set_decode_pipeline(self, lds_stages: int = 0) -> None:
         """Decode (skinny) operand staging: 0 automatic, 1 registers, 2..4 LDS ring stages."""

@@ -218,6 +218,40 @@ hipError_t launch_skinny_linear_x(const TilePlanes& planes, const float* x, cons
                                   std::uint32_t m, const SkinnyShape& shape, float* partials, hipStream_t stream,
                                   const SplitEpilogue* epilogue = nullptr);
 
+// Decode linear (M = 2..64) with K split over the waves of a workgroup
+// (linear_wsplit.hip): TN weight tiles per workgroup, every activation row,
+// `waves` waves each streaming a contiguous K range with `depth` - 1 steps of
+// weight codes in flight; K split over workgroups only for narrow matrices.
+struct WsplitShape {
+    std::uint32_t mt{1};
+    std::uint32_t tile_n{1};     // 16-row weight tiles per workgroup: 1, 2 or 4
+    std::uint32_t waves{1};      // waves per workgroup (1..8)
+    std::uint32_t depth{4};      // weight-code steps per wave ring: 2 or 4
+    std::uint32_t groups{0};
+    std::uint32_t steps{0};
+    std::uint32_t steps_per_split{0};
+    std::uint32_t splits{1};
+    std::uint32_t split_x{0};    // 1: activations split once into the workspace first
+};
+// 0 = automatic choice for each field (split_x: 1 = split into the
+// workspace first, 2 = in each wave).
+struct WsplitTuning {
+    std::uint32_t tile_n{0};
+    std::uint32_t waves{0};
+    std::uint32_t depth{0};
+    std::uint32_t k_splits{0};
+    std::uint32_t split_x{0};
+};
+// Whether the automatic route takes the wave-split kernel for m rows.
+bool wsplit_preferred(const TilePlanes& planes, std::uint32_t m);
+WsplitShape plan_wsplit(const TilePlanes& planes, std::uint32_t m, const WsplitTuning& tuning);
+std::uint64_t wsplit_partials_bytes(const WsplitShape& shape, std::uint32_t m, std::uint64_t n);
+// x: f32 rows [m][k] (split in the kernel) when ws is null, else the
+// row-scaled split in ws (split_rows_kernel's layout).
+hipError_t launch_wsplit_linear(const TilePlanes& planes, const float* x, const SplitWorkspace* ws, const float* bias,
+                                float* y, std::uint32_t m, const WsplitShape& shape, float* partials,
+                                hipStream_t stream, const SplitEpilogue* epilogue = nullptr);
+
 // ---- the Qwen2 step around the linears ----------------------------------
 
 // Paged fp32 KV pool: page p holds [layer][2 (K, V)][page_tokens][kv_width]

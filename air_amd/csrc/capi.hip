@@ -79,6 +79,10 @@ struct air_hip_context {
     std::uint32_t skinny_tile_n{0};
     std::uint32_t skinny_splits{0};
     std::uint32_t skinny_lds_stages{0};   // 0 automatic, 1 registers, 2..4 LDS ring stages
+    // Decode widths 2..64 on the wave-split kernel: 0 = automatic, 1 = always,
+    // 2 = never; and its launch-shape overrides.
+    std::uint32_t wsplit_mode{0};
+    WsplitTuning wsplit_tuning{};
     std::uint32_t* bound_scratch{nullptr};  // one uint32 for the weight exponent at residency
     void* attention_scratch{nullptr};       // attention scores, grown on demand
     void* argmax_partials{nullptr};         // per-slice partials of the greedy selection
@@ -302,7 +306,7 @@ const SplitEpilogue* reduction_epilogue(air_hip_context* ctx, const air_hip_matr
 
 // Which kernels a linear of `rows` rows runs on, decided in one place for
 // the launch path and for air_hip_linear_plan.
-enum class Route { prefill, gemv, fused, skinny_x, skinny_loaded, decode_linear, dense };
+enum class Route { prefill, gemv, fused, skinny_x, skinny_loaded, decode_linear, dense, wsplit };
 
 // The skinny kernel straight from the f32 rows, or over activations split
 // into the workspace first.  The in-workgroup split repeats the activation
@@ -329,6 +333,11 @@ Route route_linear(const air_hip_context* ctx, const air_hip_matrix* m, std::uin
         return Route::prefill;
     }
     if (rows == 1u) return Route::gemv;
+    if (rows <= AIR_HIP_MAX_DECODE_ROWS &&
+        (ctx->wsplit_mode == 1u ||
+         (ctx->wsplit_mode == 0u && ctx->decode_path == 0u && wsplit_preferred(m->planes, rows)))) {
+        return Route::wsplit;
+    }
     if (rows <= kFusedMaxRows) {
         // Measured on the Qwen2-7B shapes (M = 2..16): the single-launch fused
         // kernel wins for small square matrices (o: N, K <= 4096) and for very
@@ -365,6 +374,39 @@ int run_skinny_x(air_hip_context* ctx, const air_hip_matrix* m, const float* x, 
     const hipError_t err = launch_skinny_linear_x(m->planes, x, bias, y, rows, shape,
                                                   static_cast<float*>(ctx->split_partials), ctx->stream, epi);
     if (err != hipSuccess) return hip_fail(err, "skinny_kernel");
+    ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
+    ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
+    return AIR_HIP_OK;
+}
+
+// The wave-split decode linear (M = 2..64): one launch from the f32 rows,
+// or from the row-scaled split when the plan asks for it; a K split over
+// workgroups adds the deterministic reduction (which may carry `epilogue`).
+int run_wsplit(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y, const float* bias,
+               std::uint32_t rows, const SplitEpilogue* epilogue, bool* applied, const void* ready) {
+    const WsplitShape shape = plan_wsplit(m->planes, rows, ctx->wsplit_tuning);
+    SplitWorkspace ws{};
+    if (shape.split_x) {
+        const int rc = load_activations_for(ctx, x, m->planes.k, rows, ready);
+        if (rc != AIR_HIP_OK) return rc;
+        forget_loaded_source(ctx);
+        if (!ctx->loaded_row_scaled) return fail(AIR_HIP_INVALID_STATE, "activations were not split per row");
+        ws = carve_split_workspace(ctx->workspace, ceil_div(m->planes.k, kSplitK) * kSplitK, rows);
+    }
+    const std::uint64_t partial_bytes = wsplit_partials_bytes(shape, rows, m->planes.n);
+    if (partial_bytes > 0u) {
+        const int rc = ensure_split_buffers(ctx, partial_bytes, 0u);
+        if (rc != AIR_HIP_OK) return rc;
+    }
+    const SplitEpilogue* epi = nullptr;
+    if (epilogue && shape.splits >= 2u &&
+        split_epilogue_fits(*epilogue, static_cast<const float*>(ctx->split_partials), bias, rows, m->planes.n)) {
+        *applied = true;
+        epi = epilogue;
+    }
+    const hipError_t err = launch_wsplit_linear(m->planes, x, shape.split_x ? &ws : nullptr, bias, y, rows, shape,
+                                                static_cast<float*>(ctx->split_partials), ctx->stream, epi);
+    if (err != hipSuccess) return hip_fail(err, "wsplit_kernel");
     ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
     ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
     return AIR_HIP_OK;
@@ -586,6 +628,22 @@ int air_hip_context_set_decode_path(air_hip_context* ctx, uint32_t path, uint32_
     ctx->decode_path = path;
     ctx->skinny_tile_n = tile_n;
     ctx->skinny_splits = k_splits;
+    return AIR_HIP_OK;
+}
+
+int air_hip_context_set_wsplit(air_hip_context* ctx, uint32_t mode, uint32_t tile_n, uint32_t waves, uint32_t depth,
+                               uint32_t k_splits, uint32_t split_x) {
+    if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
+    if (mode > 2u) return fail(AIR_HIP_INVALID_ARGUMENT, "mode must be 0, 1 or 2");
+    if (tile_n != 0u && tile_n != 1u && tile_n != 2u && tile_n != 4u) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "tile_n must be 0, 1, 2 or 4");
+    }
+    if (waves > 8u) return fail(AIR_HIP_INVALID_ARGUMENT, "waves must be 0 .. 8");
+    if (depth != 0u && depth != 2u && depth != 4u) return fail(AIR_HIP_INVALID_ARGUMENT, "depth must be 0, 2 or 4");
+    if (k_splits > 64u) return fail(AIR_HIP_INVALID_ARGUMENT, "k_splits must be at most 64");
+    if (split_x > 2u) return fail(AIR_HIP_INVALID_ARGUMENT, "split_x must be 0, 1 or 2");
+    ctx->wsplit_mode = mode;
+    ctx->wsplit_tuning = WsplitTuning{tile_n, waves, depth, k_splits, split_x};
     return AIR_HIP_OK;
 }
 
@@ -1021,6 +1079,7 @@ int linear_rows(air_hip_context* ctx, const air_hip_matrix* m, const float* x, f
     if (route == Route::skinny_x || route == Route::skinny_loaded) {
         return run_skinny_x(ctx, m, x, y, bias, rows, epilogue, applied, ready);
     }
+    if (route == Route::wsplit) return run_wsplit(ctx, m, x, y, bias, rows, epilogue, applied, ready);
     const FusedShape shape = plan_decode_fused(m->planes, rows, ctx->tuning);
     if (shape.k_splits > 1u) {
         const int rc = ensure_split_buffers(ctx, fused_split_workspace_bytes(shape), shape.groups);
@@ -1097,6 +1156,13 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
     case Route::decode_linear:
         std::snprintf(buf, sizeof buf, "split_activations_kernel + decode_linear_kernel<%s>", fmt);
         break;
+    case Route::wsplit: {
+        const WsplitShape w = plan_wsplit(m->planes, rows, ctx->wsplit_tuning);
+        std::snprintf(buf, sizeof buf, "%swsplit_kernel<%s%s> mt=%u tile_n=%u waves=%u depth=%u groups=%u splits=%u%s",
+                      w.split_x ? "split_rows_kernel + " : "", fmt, w.split_x ? "" : ", f32 input", w.mt, w.tile_n,
+                      w.waves, w.depth, w.groups, w.splits, w.splits > 1u ? " + split reduction" : "");
+        break;
+    }
     }
     return buf;
 }
@@ -1150,11 +1216,16 @@ int air_hip_linear_noalloc(air_hip_context* ctx, const air_hip_matrix* m, const 
     const std::uint64_t kp = ceil_div(p.k, kSplitK) * kSplitK;
     std::uint64_t ws_bytes = 0, partial_bytes = 0;
     SkinnyShape shape{};
+    WsplitShape wshape{};
     if (route == Route::skinny_x || route == Route::skinny_loaded) {
         shape = plan_skinny(p, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages);
         partial_bytes = skinny_partials_bytes(shape, rows, p.n);
     }
-    if (route == Route::skinny_loaded || route == Route::decode_linear) {
+    if (route == Route::wsplit) {
+        wshape = plan_wsplit(p, rows, ctx->wsplit_tuning);
+        partial_bytes = wsplit_partials_bytes(wshape, rows, p.n);
+    }
+    if (route == Route::skinny_loaded || route == Route::decode_linear || (route == Route::wsplit && wshape.split_x)) {
         ws_bytes = ceil_div(split_workspace_bytes(kp, rows), 256u) * 256u;
     }
     if (route == Route::fused && plan_decode_fused(p, rows, ctx->tuning).k_splits > 1u) {
@@ -1186,6 +1257,13 @@ int air_hip_linear_noalloc(air_hip_context* ctx, const air_hip_matrix* m, const 
     case Route::skinny_loaded:
         err = launch_split_activations_rows(x, rows, p.k, kp, ws, ctx->stream);
         if (err == hipSuccess) err = launch_skinny_linear(p, ws, bias, y, rows, shape, partials, ctx->stream);
+        break;
+    case Route::wsplit:
+        if (wshape.split_x) err = launch_split_activations_rows(x, rows, p.k, kp, ws, ctx->stream);
+        if (err == hipSuccess) {
+            err = launch_wsplit_linear(p, x, wshape.split_x ? &ws : nullptr, bias, y, rows, wshape, partials,
+                                       ctx->stream);
+        }
         break;
     case Route::decode_linear:
         err = launch_split_activations(x, rows, p.k, kp, ws, ctx->stream);

@@ -173,6 +173,18 @@ int air_hip_context_set_decode_path(air_hip_context* ctx, uint32_t path, uint32_
  * rows the linear then runs on split activations).  No counterpart in the
  * reference. */
 int air_hip_context_set_decode_pipeline(air_hip_context* ctx, uint32_t lds_stages);
+/* Chooses the wave-split decode kernel for 2..64 rows (autotuning): mode 0 =
+ * automatic, 1 = always, 2 = never.  A workgroup owns tile_n 16-row weight
+ * tiles (1, 2 or 4) and every activation row; its `waves` waves (1..8) split
+ * K, each keeping depth - 1 steps of weight codes in flight (depth 2 or 4);
+ * k_splits workgroups split K further (1..64, with a deterministic
+ * reduction); split_x = 1 splits the activations into the workspace first,
+ * 2 in each wave.  0 keeps the automatic choice.  Mode 0 takes the kernel
+ * where it measured faster than the skinny kernels (every 7B matrix but the
+ * lm_head at M <= 16, the narrow ones above) and only while the decode path
+ * is automatic.  No counterpart in the reference. */
+int air_hip_context_set_wsplit(air_hip_context* ctx, uint32_t mode, uint32_t tile_n, uint32_t waves, uint32_t depth,
+                               uint32_t k_splits, uint32_t split_x);
 /* Reads `bytes` (a multiple of 16) of device memory once on the context's
  * stream and stores the XOR of each chunk's 32-bit words in a word of
  * `sink` (sink_words >= 1 words of device memory the caller zeroes; the

@@ -198,6 +198,75 @@ def test_skinny_shapes_agree(torch_cuda, hip_ctx, type_id, k, n):
         mat.release()
 
 
+@pytest.mark.parametrize("type_id,k,n", [(capi.TYPE_Q8_0, 3584, 200), (capi.TYPE_Q4_0, 1152, 333),
+                                         (capi.TYPE_Q4_K, 2304, 96), (capi.TYPE_Q8_0, 18944, 64),
+                                         (capi.TYPE_Q8_0, 96, 37), (capi.TYPE_Q4_K, 3584, 512)])
+def test_wsplit_shapes_agree(torch_cuda, hip_ctx, type_id, k, n):
+    """The wave-split decode kernel (M = 2..64, K split over the waves of a
+    workgroup): every activation-tile count, one, two and four weight tiles
+    per workgroup, one to eight waves, one and three steps of codes in
+    flight, K split over one to three workgroups (mid-tile for the 128-k and
+    256-k tiles), activations split in each wave and once into the
+    workspace, a ragged last tile in N and a K that ends inside a 64-k step
+    (96); each matches the oracle to 1e-4 per row and repeats
+    bit-identically."""
+    torch = torch_cuda
+    canon = helpers.weights(type_id, k, n, seed=k * 5 + n)
+    mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    shapes = [(1, 1, 2, 1, 2), (2, 3, 4, 1, 2), (4, 8, 2, 3, 2), (1, 4, 4, 3, 1), (2, 8, 2, 1, 1),
+              (4, 2, 2, 2, 1), (0, 0, 0, 0, 0)]
+    try:
+        for m in (2, 9, 16, 17, 33, 48, 64):
+            x = helpers.activations(m, k, seed=m + 23)
+            want = oracle.linear(type_id, canon, k, n, x)
+            xd = _dev(torch, x)
+            for tile_n, waves, depth, splits, split_x in shapes:
+                hip_ctx.set_wsplit(1, tile_n, waves, depth, splits, split_x)
+                plan = mat.plan(m)
+                assert "wsplit_kernel" in plan, plan
+                outs = []
+                for _ in range(2):
+                    y = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+                    mat.linear(xd, y, m)
+                    torch.cuda.synchronize()
+                    outs.append(y.cpu().numpy())
+                assert np.isfinite(outs[0]).all(), plan
+                for r in range(m):
+                    assert helpers.rel_l2(outs[0][r], want[r]) <= DECODE_TOL, (m, plan, r)
+                assert np.array_equal(outs[1].view(np.uint32), outs[0].view(np.uint32)), (m, plan)
+    finally:
+        hip_ctx.set_wsplit(0)
+        mat.release()
+
+
+def test_wsplit_scale_extremes_and_bias(torch_cuda, hip_ctx):
+    """Rows 1e-6 .. 6e4 apart in one activation tile keep their own relative
+    precision (a power-of-two scale per row and step), with a fused bias and
+    with the bias added by the split reduction; the automatic route takes
+    the wave-split kernel at these widths."""
+    torch = torch_cuda
+    k, n = 3584, 512
+    canon = helpers.weights(capi.TYPE_Q8_0, k, n, seed=29)
+    mat = capi.Matrix(hip_ctx, capi.TYPE_Q8_0, k, n, canon, canon.nbytes, on_device=False)
+    bias = np.random.default_rng(3).standard_normal(n).astype(np.float32) * 0.02
+    try:
+        base = helpers.activations(8, k, seed=8)
+        x = base * np.array([[1e-6], [1.0], [3e3], [6e4], [2e-3], [1.0], [7.0], [1e2]], dtype=np.float32)
+        want = oracle.linear(capi.TYPE_Q8_0, canon, k, n, x, bias=bias)
+        assert "wsplit_kernel" in mat.plan(8), mat.plan(8)
+        for splits in (0, 1, 3):
+            hip_ctx.set_wsplit(0, 0, 0, 0, splits, 0)
+            y = torch.empty((8, n), dtype=torch.float32, device="cuda:0")
+            mat.linear(_dev(torch, x), y, 8, bias=_dev(torch, bias))
+            torch.cuda.synchronize()
+            got = y.cpu().numpy()
+            for i in range(8):
+                assert helpers.rel_l2(got[i], want[i]) <= DECODE_TOL, (splits, i)
+    finally:
+        hip_ctx.set_wsplit(0)
+        mat.release()
+
+
 @pytest.mark.parametrize("type_id,k,n", [(capi.TYPE_Q8_0, 3584, 8200), (capi.TYPE_Q8_0, 1024, 9000),
                                          (capi.TYPE_Q4_0, 3584, 8200), (capi.TYPE_Q4_K, 1024, 9000)])
 def test_skinny_lds_pipeline_matches_registers(torch_cuda, hip_ctx, type_id, k, n):

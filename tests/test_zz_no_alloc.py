@@ -22,12 +22,14 @@ from tests import helpers
 
 pytestmark = pytest.mark.gpu
 
-# (format, N, K, bias, (first M, second M)): one case per route the planner
-# takes at these shapes -- skinny over split activations with an 8-way K
-# split (down), two weight tiles per wave and a 2-way split (gate|up), both
-# on the LDS pipeline, skinny straight from f32 rows (q|k|v at M = 3; M = 16
-# takes the split route), the single-launch fused kernel and the M = 1 GEMV
-# (o).
+# (format, N, K, bias, (first M, second M)): the routes the planner takes at
+# these shapes -- the skinny LDS pipeline over split activations (down at M =
+# 64 with an 8-way K split, gate|up at M = 32 with two weight tiles per wave
+# and a 2-way split, Q4_0 gate|up at M = 64), the wave-split kernel straight
+# from f32 rows (down at M = 8 with a K split, q|k|v at M = 16 and 3, o at M
+# = 4, Q4_0 gate|up at M = 2) and over the row-scaled split (gate|up at M =
+# 16, Q4_K o at M = 17), Q4_K o at M = 64 on the LDS pipeline, and the M = 1
+# GEMV (o).
 CASES = [
     (capi.TYPE_Q8_0, 3584, 18944, False, (64, 8)),
     (capi.TYPE_Q8_0, 37888, 3584, False, (32, 16)),
