@@ -128,6 +128,7 @@ SIGNATURES = {
     "air_hip_context_set_prefill_tuning": (_I, [_P, _U32, _U32, _U32, _U32]),
     "air_hip_context_set_decode_path": (_I, [_P, _U32, _U32, _U32]),
     "air_hip_context_set_wsplit": (_I, [_P, _U32, _U32, _U32, _U32, _U32, _U32]),
+    "air_hip_context_set_dense_path": (_I, [_P, _U32, _U32, _U32, _U32]),
     "air_hip_context_set_prefill_pipeline": (_I, [_P, _U32]),
     "air_hip_context_set_decode_pipeline": (_I, [_P, _U32]),
     "air_hip_matrix_rows": (_I, [_P, _P, _P, _U32, _P]),
@@ -252,6 +253,11 @@ class Context:
         2 never, plus launch-shape overrides (0 = automatic; split_x 1 = split
         into the workspace first, 2 = in each wave)."""
         check(lib().air_hip_context_set_wsplit(self.handle, mode, tile_n, waves, depth, k_splits, split_x))
+
+    def set_dense_path(self, path: int = 0, tile_n: int = 0, waves: int = 0, depth: int = 0) -> None:
+        """Dense matrices (F16 / BF16 / Q6_K): path 0 automatic, 1 the matrix-core
+        kernel at every width, 2 the FMA kernels; shape overrides (0 = automatic)."""
+        check(lib().air_hip_context_set_dense_path(self.handle, path, tile_n, waves, depth))
 
     def set_decode_pipeline(self, lds_stages: int = 0) -> None:
         """Decode (skinny) operand staging: 0 automatic, 1 registers, 2..4 LDS ring stages."""

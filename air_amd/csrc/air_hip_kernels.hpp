@@ -38,8 +38,34 @@ hipError_t launch_q5_0_to_q8_0(const std::uint8_t* q5_0, std::uint64_t blocks, s
 // Linears over dense rows w[n][k] stored as `storage` (kF32, or the f16 /
 // bf16 bits of kF16 / kBF16; k a multiple of 32, x and y 16-byte aligned):
 // y[m][n] = sum_k x[m][k] w[n][k] (+ bias[n]).
+// Dense linears on the matrix cores (linear_dense_mfma.hip): F16, BF16 and
+// Q6_K storage, any m (one launch per 64 rows).  A shape field of 0 is the
+// planner's choice.
+struct DenseMfmaShape {
+    std::uint32_t tile_n{0};   // 16-row weight tiles per workgroup: 1, 2 or 4
+    std::uint32_t waves{0};    // waves splitting K (1..8)
+    std::uint32_t depth{0};    // weight steps per wave ring: 2 or 4
+};
+// path 0 = automatic (the matrix-core kernel for 2..64 rows), 1 = the
+// matrix-core kernel wherever it applies, 2 = the FMA kernels (dense_rows /
+// dense_gemm / q6k_gemv).
+struct DenseTuning {
+    std::uint32_t path{0};
+    DenseMfmaShape shape{};
+};
+// Activation rows per launch of the matrix-core kernel.
+std::uint32_t dense_mfma_rows(int storage);
+DenseMfmaShape plan_dense_mfma(int storage, std::uint64_t k, std::uint64_t n, std::uint32_t m,
+                               const DenseMfmaShape& tuning);
+bool dense_mfma_supported(int storage, std::uint64_t k);
+// Whether a linear of m rows over `storage` runs on the matrix-core kernel.
+bool dense_mfma_route(int storage, std::uint64_t k, std::uint64_t n, std::uint32_t m, const DenseTuning& tuning);
+hipError_t launch_dense_mfma(const void* w, int storage, std::uint64_t k, std::uint64_t n, const float* x,
+                             const float* bias, float* y, std::uint32_t m, const DenseMfmaShape& tuning,
+                             hipStream_t stream);
 hipError_t launch_dense_linear(const void* w, int storage, std::uint64_t k, std::uint64_t n, const float* x,
-                               const float* bias, float* y, std::uint32_t m, hipStream_t stream);
+                               const float* bias, float* y, std::uint32_t m, hipStream_t stream,
+                               const DenseTuning& tuning = DenseTuning{});
 // out[i][k] = w[rows[i]][k], decoded exactly, for rows in [0, n); other ids
 // leave out[i] as is.
 // XOR checksum of `bytes` (a multiple of 16) of device memory: one word per

@@ -83,6 +83,8 @@ struct air_hip_context {
     // 2 = never; and its launch-shape overrides.
     std::uint32_t wsplit_mode{0};
     WsplitTuning wsplit_tuning{};
+    // Dense matrices (F16 / BF16 / Q6_K storage): kernel choice and shape.
+    DenseTuning dense_tuning{};
     std::uint32_t* bound_scratch{nullptr};  // one uint32 for the weight exponent at residency
     void* attention_scratch{nullptr};       // attention scores, grown on demand
     void* argmax_partials{nullptr};         // per-slice partials of the greedy selection
@@ -647,6 +649,19 @@ int air_hip_context_set_wsplit(air_hip_context* ctx, uint32_t mode, uint32_t til
     return AIR_HIP_OK;
 }
 
+int air_hip_context_set_dense_path(air_hip_context* ctx, uint32_t path, uint32_t tile_n, uint32_t waves,
+                                   uint32_t depth) {
+    if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
+    if (path > 2u) return fail(AIR_HIP_INVALID_ARGUMENT, "path must be 0, 1 or 2");
+    if (tile_n != 0u && tile_n != 1u && tile_n != 2u && tile_n != 4u) {
+        return fail(AIR_HIP_INVALID_ARGUMENT, "tile_n must be 0, 1, 2 or 4");
+    }
+    if (waves > 8u) return fail(AIR_HIP_INVALID_ARGUMENT, "waves must be 0 .. 8");
+    if (depth != 0u && depth != 2u && depth != 4u) return fail(AIR_HIP_INVALID_ARGUMENT, "depth must be 0, 2 or 4");
+    ctx->dense_tuning = DenseTuning{path, DenseMfmaShape{tile_n, waves, depth}};
+    return AIR_HIP_OK;
+}
+
 int air_hip_context_set_decode_pipeline(air_hip_context* ctx, uint32_t lds_stages) {
     if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
     if (lds_stages > 4u) return fail(AIR_HIP_INVALID_ARGUMENT, "lds_stages must be 0 .. 4");
@@ -1043,7 +1058,7 @@ int linear_rows(air_hip_context* ctx, const air_hip_matrix* m, const float* x, f
         DeviceScope scope(ctx->device);
         if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
         const hipError_t err = launch_dense_linear(m->dense, m->dense_storage, m->planes.k, m->planes.n, x, bias, y, rows,
-                                                     ctx->stream);
+                                                     ctx->stream, ctx->dense_tuning);
         if (err != hipSuccess) return hip_fail(err, "dense_rows_kernel / dense_gemm_kernel");
         const bool prefill = tactic == AIR_HIP_LINEAR_PREFILL ||
                              (tactic == AIR_HIP_LINEAR_AUTO && rows > AIR_HIP_MAX_DECODE_ROWS);
@@ -1101,10 +1116,20 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
     switch (route_linear(ctx, m, rows, tactic)) {
     case Route::dense: {
         const char* t = m->type == kF32 ? "f32" : m->type == kF16 ? "f16" : m->type == kBF16 ? "bf16" : "q6_k";
-        if (m->type == kQ6_K && rows == 1u) {
+        if (m->type == kQ6_K && rows == 1u &&
+            !dense_mfma_route(m->dense_storage, m->planes.k, m->planes.n, rows, ctx->dense_tuning)) {
             const Q6kGemvShape q = q6k_gemv_shape(m->planes.k, m->planes.n);
             std::snprintf(buf, sizeof buf, "q6k_gemv_kernel columns=%u waves=%u (dense q6_k super-block rows)", q.columns,
                           q.waves);
+            break;
+        }
+        if (dense_mfma_route(m->dense_storage, m->planes.k, m->planes.n, rows, ctx->dense_tuning)) {
+            const DenseMfmaShape d = plan_dense_mfma(m->dense_storage, m->planes.k, m->planes.n, rows,
+                                                     ctx->dense_tuning.shape);
+            std::snprintf(buf, sizeof buf, "dense_mfma_kernel<%s> tile_n=%u waves=%u depth=%u launches=%u (dense %s %s)",
+                          t, d.tile_n, d.waves, d.depth,
+                          static_cast<unsigned>(ceil_div(rows, dense_mfma_rows(m->dense_storage))), t,
+                          m->type == kQ6_K ? "super-block rows" : "rows");
             break;
         }
         std::snprintf(buf, sizeof buf, m->type == kQ6_K ? "%s (dense %s super-block rows)" : "%s (dense %s rows)",
@@ -1199,7 +1224,7 @@ int air_hip_linear_noalloc(air_hip_context* ctx, const air_hip_matrix* m, const 
         DeviceScope scope(ctx->device);
         if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
         const hipError_t err = launch_dense_linear(m->dense, m->dense_storage, m->planes.k, m->planes.n, x, bias, y, rows,
-                                                     ctx->stream);
+                                                     ctx->stream, ctx->dense_tuning);
         if (err != hipSuccess) return hip_fail(err, "dense_rows_kernel / dense_gemm_kernel");
         ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
         ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);

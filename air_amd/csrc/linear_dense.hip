@@ -461,9 +461,26 @@ hipError_t launch_dense_typed(const void* w, std::uint64_t k, std::uint64_t n, c
     return hipGetLastError();
 }
 
+bool dense_mfma_route(int storage, std::uint64_t k, std::uint64_t n, std::uint32_t m, const DenseTuning& tuning) {
+    (void)n;
+    if (tuning.path == 2u || !dense_mfma_supported(storage, k)) return false;
+    if (tuning.path == 1u) return true;
+    // Measured on the Qwen2-7B shapes: the matrix cores win from two rows to
+    // 64 (F16 down M = 16 120 -> 57 us, gate|up M = 32 514 -> 107; Q6_K down
+    // M = 32 272 -> 129); a single row streams faster through the FMA GEMV
+    // (F16 down 29 against 39 us, Q6_K 23 against 74), and at M = 512 the
+    // launches per 64 rows re-read the weights (gate|up 1964 against 2284
+    // us, Q6_K down 1589 against 2045).
+    return m >= 2u && m <= 64u;
+}
+
 hipError_t launch_dense_linear(const void* w, int storage, std::uint64_t k, std::uint64_t n, const float* x,
-                               const float* bias, float* y, std::uint32_t m, hipStream_t stream) {
+                               const float* bias, float* y, std::uint32_t m, hipStream_t stream,
+                               const DenseTuning& tuning) {
     if (m == 0u || k == 0u || n == 0u || k % kGemmK != 0u) return hipErrorInvalidValue;
+    if (dense_mfma_route(storage, k, n, m, tuning)) {
+        return launch_dense_mfma(w, storage, k, n, x, bias, y, m, tuning.shape, stream);
+    }
     switch (storage) {
     case kF32: return launch_dense_typed<kF32>(w, k, n, x, bias, y, m, stream);
     case kF16: return launch_dense_typed<kF16>(w, k, n, x, bias, y, m, stream);

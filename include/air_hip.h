@@ -185,6 +185,14 @@ int air_hip_context_set_decode_pipeline(air_hip_context* ctx, uint32_t lds_stage
  * is automatic.  No counterpart in the reference. */
 int air_hip_context_set_wsplit(air_hip_context* ctx, uint32_t mode, uint32_t tile_n, uint32_t waves, uint32_t depth,
                                uint32_t k_splits, uint32_t split_x);
+/* Chooses the kernel of the dense matrices (F16, BF16 and Q6_K storage;
+ * autotuning): path 0 = automatic (the matrix-core kernel for 2..64 rows),
+ * 1 = the matrix-core kernel at every width, 2 = the FMA kernels.
+ * tile_n = 16-row weight tiles per workgroup (1, 2 or 4), waves = waves
+ * splitting K (1..8), depth = weight steps per wave ring (2 or 4); 0 keeps
+ * the automatic choice.  No counterpart in the reference. */
+int air_hip_context_set_dense_path(air_hip_context* ctx, uint32_t path, uint32_t tile_n, uint32_t waves,
+                                   uint32_t depth);
 /* Reads `bytes` (a multiple of 16) of device memory once on the context's
  * stream and stores the XOR of each chunk's 32-bit words in a word of
  * `sink` (sink_words >= 1 words of device memory the caller zeroes; the

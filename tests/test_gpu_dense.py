@@ -1,6 +1,7 @@
 """The encodings without a resident tile format: F32, F16, BF16 and Q6_K
-(decoded once into dense f32 rows, f32 FMA kernels) and Q5_0 (rewritten
-exactly as Q8_0 blocks, then the Q8_0 kernels).  The reference decodes all
+(held as the file's rows -- Q6_K as super-block records -- on f32 FMA
+kernels, and for F16, BF16 and Q6_K at two or more rows on the matrix
+cores) and Q5_0 (rewritten exactly as Q8_0 blocks, then the Q8_0 kernels).  The reference decodes all
 of them per element in decode_element (src/cuda/cuda_backend.cu:241-344);
 a Qwen2.5 Q4_K_M file mixes Q6_K and Q5_0 tensors with Q4_K and Q8_0.
 
@@ -150,6 +151,50 @@ def test_new_types_match_oracle(torch_cuda, hip_ctx, type_id, k, n):
                     err = helpers.rel_l2(got[r], want[r])
                     assert err <= tol, (m, tactic, r, err, plan)
     finally:
+        mat.release()
+
+
+MFMA_CASES = [(capi.TYPE_F16, 96, 37), (capi.TYPE_F16, 3584, 300), (capi.TYPE_BF16, 1056, 129),
+              (capi.TYPE_BF16, 256, 5), (capi.TYPE_Q6_K, 512, 300), (capi.TYPE_Q6_K, 768, 33)]
+
+
+@pytest.mark.parametrize("type_id,k,n", MFMA_CASES, ids=[f"{capi.TYPE_NAMES[t]}-{n}x{k}" for t, k, n in MFMA_CASES])
+def test_dense_mfma_shapes_match_oracle(torch_cuda, hip_ctx, type_id, k, n):
+    """The matrix-core kernel of the dense encodings (F16 and BF16 weights as
+    exact MFMA operands, Q6_K codes decoded to exact f16 integers with the
+    sub-block scales in the f32 epilogue) at every activation-tile count and
+    past one launch's rows (65, 100), for one, two and four weight tiles per
+    workgroup, one to eight waves splitting K, one and three steps in flight,
+    a ragged last row tile and a K ending inside a 64-k step (96, 1056):
+    within 1e-5 of the oracle per row, repeats bit-identical."""
+    torch = torch_cuda
+    canon = _weights(type_id, k, n, seed=k * 11 + n + type_id)
+    mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    bias = helpers.activations(1, n, seed=n + 1)[0] * 0.1
+    bias_d = _dev(torch, bias)
+    shapes = [(0, 0, 0), (1, 1, 2), (2, 3, 4), (4, 8, 2), (1, 8, 4)]
+    try:
+        for m in (1, 2, 16, 17, 32, 33, 64, 65, 100):
+            x = helpers.activations(m, k, seed=m * 3 + k)
+            want = oracle.linear(type_id, canon, k, n, x, bias=bias)
+            x_d = _dev(torch, x)
+            for tile_n, waves, depth in shapes:
+                hip_ctx.set_dense_path(1, tile_n, waves, depth)
+                plan = mat.plan(m)
+                assert "dense_mfma_kernel" in plan, plan
+                outs = []
+                for _ in range(2):
+                    y = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+                    mat.linear(x_d, y, m, bias=bias_d)
+                    torch.cuda.synchronize()
+                    outs.append(y.cpu().numpy())
+                assert np.isfinite(outs[0]).all(), plan
+                for r in range(m):
+                    err = helpers.rel_l2(outs[0][r], want[r])
+                    assert err <= 1e-5, (m, plan, r, err)
+                assert np.array_equal(outs[1].view(np.uint32), outs[0].view(np.uint32)), (m, plan)
+    finally:
+        hip_ctx.set_dense_path(0)
         mat.release()
 
 
