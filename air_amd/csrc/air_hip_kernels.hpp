@@ -407,6 +407,9 @@ hipError_t launch_argmax(const float* logits, std::uint32_t m, std::uint64_t n, 
 // Sets planes.prefill_scale / prefill_unscale from the largest dequantized
 // magnitude of the resident matrix (synchronous; `bound_scratch` is one
 // device uint32).
+// The prefill GEMM over dense storage (planes.type kF16 / kBF16 / kQ6_K,
+// planes.codes the rows or records, planes.kt = k): its weight exponent.
+hipError_t compute_dense_prefill_scale(TilePlanes& planes, std::uint32_t* bound_scratch, hipStream_t stream);
 hipError_t compute_prefill_scale(TilePlanes& planes, std::uint32_t* bound_scratch, hipStream_t stream);
 
 } // namespace air_hip

@@ -32,6 +32,66 @@ struct StepCodes<kQ4_K> {
     u32x4 h;               // the 16-byte super-block header of the lane's row
 };
 
+// Dense storage (F16 / BF16 rows, Q6_K super-block records): a lane's share of
+// one 64-k step of one 16-row tile as the prefill GEMM's A fragment (row
+// l % 16, elements 8 (l / 16)..+7 of both 32-element blocks).
+template <>
+struct StepCodes<kF16> {
+    u32x4 v[2];            // f16 bits of blocks 0 and 1
+};
+template <>
+struct StepCodes<kBF16> {
+    u32x4 v[2];            // bf16 bits of blocks 0 and 1
+};
+template <>
+struct StepCodes<kQ6_K> {
+    u32x2 ql[2];           // [block]: the eight low-nibble bytes
+    u32x2 qh;              // the eight high-bit-pair bytes (both blocks)
+    std::uint32_t sc;      // the step's four int8 sub-block scales
+    std::uint32_t d;       // f16 bits of the super-block's d
+};
+
+constexpr bool dense_storage(int fmt) { return fmt == kF16 || fmt == kBF16 || fmt == kQ6_K; }
+
+// Rows of a dense matrix of n rows and k columns; rows past n read as zero
+// weights.  Q6_K: step s is quadrant pair q = s % 4 of super-block s / 4 --
+// half h = q / 2 of the record, quadrants j = 2 (q % 2) + b for its blocks b;
+// element 8 g + e of a quadrant has its low nibble (nibble q % 2) in ql byte
+// 64 h + 32 b + 8 g + e, its high pair (bits 2 j) in qh byte 32 h + 8 g + e,
+// its scale in scales byte 8 h + 2 j + g / 2 (src/reference/tensor_reader.cpp:197-242).
+template <int FMT>
+__device__ __forceinline__ void load_dense_step(const void* w, std::uint64_t n, std::uint64_t k, std::uint32_t rt,
+                                                std::uint32_t s, std::uint32_t lane, StepCodes<FMT>& out) {
+    const std::uint64_t row = static_cast<std::uint64_t>(rt) * 16u + (lane & 15u);
+    const std::uint32_t g = lane >> 4;
+    if constexpr (FMT == kQ6_K) {
+        if (row >= n) {
+            out.ql[0] = out.ql[1] = out.qh = u32x2{0u, 0u};
+            out.sc = 0u;
+            out.d = 0u;
+            return;
+        }
+        const std::uint64_t sbs = k / 256u;
+        const std::uint64_t blk = row * sbs + s / 4u;
+        const unsigned char* rec = static_cast<const unsigned char*>(w) + blk * 208u;
+        const std::uint32_t q = s & 3u, h = q >> 1;
+        out.ql[0] = *reinterpret_cast<const u32x2*>(rec + 64u * h + 8u * g);
+        out.ql[1] = *reinterpret_cast<const u32x2*>(rec + 64u * h + 32u + 8u * g);
+        out.qh = *reinterpret_cast<const u32x2*>(rec + 128u + 32u * h + 8u * g);
+        out.sc = *reinterpret_cast<const std::uint32_t*>(rec + 192u + 8u * h + 4u * (q & 1u));
+        out.d = reinterpret_cast<const std::uint16_t*>(static_cast<const unsigned char*>(w) + n * sbs * 208u)[blk];
+    } else {
+        const std::uint64_t k0 = static_cast<std::uint64_t>(s) * kStepK + 8u * g;
+        out.v[0] = u32x4{0u, 0u, 0u, 0u};
+        out.v[1] = u32x4{0u, 0u, 0u, 0u};
+        if (row < n) {
+            const std::uint16_t* base = static_cast<const std::uint16_t*>(w) + row * k;
+            if (k0 < k) out.v[0] = *reinterpret_cast<const u32x4*>(base + k0);
+            if (k0 + 32u < k) out.v[1] = *reinterpret_cast<const u32x4*>(base + k0 + 32u);
+        }
+    }
+}
+
 // Streaming (read-once) code loads use non-temporal hints so they do not
 // displace reused data in the caches; NT = false for kernels whose
 // workgroups share weight tiles through L2.  Only Q8_0 takes the hint: a

@@ -108,7 +108,10 @@ struct air_hip_matrix {
     TilePlanes planes;             // planes.type is the resident format (Q5_0 arrives as Q8_0)
     int type{0};                   // the canonical type it was prepared from
     void* dense{nullptr};          // dense_type(type): rows [n][k] instead of tile planes
-    int dense_storage{0};          // the type of the rows: kF32, kF16 / kBF16 (GGUF rows) or kQ6_K (212-byte records)
+    int dense_storage{0};          // the type of the rows: kF32, kF16 / kBF16 (GGUF rows) or kQ6_K (208-byte
+                                   // super-block records, then a plane of f16 d)
+    TilePlanes gemm;               // F16 / BF16 / Q6_K storage as the prefill GEMM's weight operand (codes =
+                                   // dense, kt = k); codes null when the GEMM does not take it
     std::uint64_t canonical_bytes{0};
     std::uint64_t resident_bytes{0};
 };
@@ -269,9 +272,10 @@ void remember_prefill(air_hip_context* ctx, const void* source, std::uint64_t k,
 int run_prefill(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y, const float* bias,
                 std::uint32_t rows, const void* ready = nullptr, std::uint64_t ready_k = 0,
                 std::uint32_t ready_rows = 0, const SplitEpilogue* epilogue = nullptr, bool* applied = nullptr) {
-    const PrefillShape shape = plan_prefill(m->planes, rows, ctx->prefill_tuning);
-    const bool converted = ready == x && ready_k == m->planes.k && ready_rows == rows;
-    int rc = ensure_prefill_workspace(ctx, prefill_workspace_bytes(m->planes.k, rows, shape, m->planes.n), converted);
+    const TilePlanes& planes = m->dense ? m->gemm : m->planes;
+    const PrefillShape shape = plan_prefill(planes, rows, ctx->prefill_tuning);
+    const bool converted = ready == x && ready_k == planes.k && ready_rows == rows;
+    int rc = ensure_prefill_workspace(ctx, prefill_workspace_bytes(planes.k, rows, shape, planes.n), converted);
     if (rc != AIR_HIP_OK) return rc;
     // A K-split launch's reduction carries the epilogue when it fits.
     const auto* partials = reinterpret_cast<const float*>(static_cast<const std::uint8_t*>(ctx->prefill_workspace) +
@@ -281,7 +285,7 @@ int run_prefill(air_hip_context* ctx, const air_hip_matrix* m, const float* x, f
                                    ? epilogue
                                    : nullptr;
     if (epi) *applied = true;
-    const hipError_t err = launch_prefill_linear(m->planes, x, bias, y, rows, shape, ctx->prefill_workspace, ctx->stream,
+    const hipError_t err = launch_prefill_linear(planes, x, bias, y, rows, shape, ctx->prefill_workspace, ctx->stream,
                                                  converted, epi);
     if (err != hipSuccess) return hip_fail(err, "prefill_gemm_kernel");
     ctx->prefill_linear_calls.fetch_add(1, std::memory_order_relaxed);
@@ -304,6 +308,15 @@ const SplitEpilogue* reduction_epilogue(air_hip_context* ctx, const air_hip_matr
     }
     *applied = true;
     return epilogue;
+}
+
+// A dense matrix (F16 / BF16 / Q6_K storage) at prefill widths runs the f16
+// MFMA prefill GEMM on its rows (measured at M = 512 on 3584 x 18944: F16
+// 1411 -> 133 us, Q6_K 1590 -> 208 against the FMA GEMM); F32 and the
+// autotuning paths 1 and 2 keep their kernels.
+bool dense_prefill(const air_hip_context* ctx, const air_hip_matrix* m, std::uint32_t rows, int tactic) {
+    if (!m->dense || !m->gemm.codes || ctx->dense_tuning.path != 0u || rows > kMaxRows) return false;
+    return tactic == AIR_HIP_LINEAR_PREFILL || (tactic == AIR_HIP_LINEAR_AUTO && rows > AIR_HIP_MAX_DECODE_ROWS);
 }
 
 // Which kernels a linear of `rows` rows runs on, decided in one place for
@@ -505,6 +518,28 @@ int prepare_dense(air_hip_context* ctx, int type, std::uint64_t k, std::uint64_t
     }
     m->dense = dense;
     m->dense_storage = storage;
+    if ((storage == kF16 || storage == kBF16 || storage == kQ6_K) && k % 32u == 0u && k <= 0xffffffffu) {
+        TilePlanes g{};
+        g.type = storage;
+        g.k = k;
+        g.n = n;
+        g.nt = static_cast<std::uint32_t>(ceil_div(n, 16u));
+        g.kt = static_cast<std::uint32_t>(k);   // the row length, for the dense loads
+        g.kp = ceil_div(k, 64u) * 64u;          // whole 64-k steps
+        g.codes = dense;
+        if (!ctx->bound_scratch) {
+            void* b = nullptr;
+            err = hipMalloc(&b, 256);
+            ctx->bound_scratch = static_cast<std::uint32_t*>(b);
+        }
+        if (err == hipSuccess) err = compute_dense_prefill_scale(g, ctx->bound_scratch, ctx->stream);
+        if (err != hipSuccess) {
+            (void)hipFree(dense);
+            delete m;
+            return hip_fail(err, "dense prefill scale");
+        }
+        m->gemm = g;
+    }
     m->resident_bytes = bytes;
     ctx->resident_matrix_bytes.fetch_add(bytes, std::memory_order_relaxed);
     ctx->prepared_matrices.fetch_add(1, std::memory_order_relaxed);
@@ -1057,6 +1092,10 @@ int linear_rows(air_hip_context* ctx, const air_hip_matrix* m, const float* x, f
         if (reinterpret_cast<std::uintptr_t>(x) % 16u != 0) return fail(AIR_HIP_INVALID_ARGUMENT, "x must be 16-byte aligned");
         DeviceScope scope(ctx->device);
         if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+        if (dense_prefill(ctx, m, rows, tactic)) {
+            return run_prefill(ctx, m, x, y, bias, rows, prefill_ready, ctx->prefill_source_k, ctx->prefill_source_rows,
+                               epilogue, applied);
+        }
         const hipError_t err = launch_dense_linear(m->dense, m->dense_storage, m->planes.k, m->planes.n, x, bias, y, rows,
                                                      ctx->stream, ctx->dense_tuning);
         if (err != hipSuccess) return hip_fail(err, "dense_rows_kernel / dense_gemm_kernel");
@@ -1116,6 +1155,18 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
     switch (route_linear(ctx, m, rows, tactic)) {
     case Route::dense: {
         const char* t = m->type == kF32 ? "f32" : m->type == kF16 ? "f16" : m->type == kBF16 ? "bf16" : "q6_k";
+        if (dense_prefill(ctx, m, rows, tactic)) {
+            const PrefillShape s = plan_prefill(m->gemm, rows, ctx->prefill_tuning);
+            std::snprintf(buf, sizeof buf, "prefill_gemm_kernel<%s> tile_m=%u tile_n=%u prefetch=%u m_tiles=%u "
+                          "groups=%u splits=%u (dense %s %s)", t, s.tile_m, s.tile_n, s.prefetch, s.m_tiles, s.groups,
+                          s.splits, t, m->type == kQ6_K ? "super-block rows" : "rows");
+            if (s.rem_groups) {
+                const std::size_t used = std::strlen(buf);
+                std::snprintf(buf + used, sizeof buf - used, " + remainder tile_m=4 tile_n=2 m_tiles=%u groups=%u",
+                              s.rem_m_tiles, s.rem_groups);
+            }
+            break;
+        }
         if (m->type == kQ6_K && rows == 1u &&
             !dense_mfma_route(m->dense_storage, m->planes.k, m->planes.n, rows, ctx->dense_tuning)) {
             const Q6kGemvShape q = q6k_gemv_shape(m->planes.k, m->planes.n);

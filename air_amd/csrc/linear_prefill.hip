@@ -109,6 +109,40 @@ __device__ __forceinline__ half8v dequant_block(const StepCodes<FMT>& in, std::u
     } else if constexpr (FMT == kQ4_0) {
         const _Float16 d = scaled_half((in.d >> (16 * b)) & 0xffffu, w_scale);
         w = nibble_dword_to_half8<8>(b == 0 ? in.c.x : in.c.y) * d;
+    } else if constexpr (FMT == kF16) {
+        // Exact f16 rows: the weight exponent of F16 storage is 0.
+        (void)w_scale;
+        w = __builtin_bit_cast(half8v, in.v[b]);
+    } else if constexpr (FMT == kBF16) {
+        // bf16 -> f32 (exact) -> scaled -> f16 (one rounding).
+        const u32x4 v = in.v[b];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            w[2 * e] = static_cast<_Float16>(__uint_as_float(v[e] << 16) * w_scale);
+            w[2 * e + 1] = static_cast<_Float16>(__uint_as_float(v[e] & 0xffff0000u) * w_scale);
+        }
+    } else if constexpr (FMT == kQ6_K) {
+        // Codes q - 32 as exact f16 (1024 + q under the exponent byte 0x64,
+        // minus 1056) times f16(d * sc * 2^-e): one rounding per weight.
+        const std::uint32_t q = s & 3u;
+        const std::uint32_t j = 2u * (q & 1u) + static_cast<std::uint32_t>(b);
+        const std::uint32_t g = (threadIdx.x & 63u) >> 4;
+        const int sc = static_cast<int>(static_cast<std::int8_t>((in.sc >> (8u * (2u * b + (g >> 1)))) & 0xffu));
+        const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<std::uint16_t>(in.d)));
+        const _Float16 ds = static_cast<_Float16>(d * static_cast<float>(sc) * w_scale);
+        const half2v dd = {ds, ds};
+        const half2v bias = {(_Float16)1056.0f, (_Float16)1056.0f};
+        const u32x2 lq = in.ql[b];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const std::uint32_t nib = ((q & 1u) ? (lq[e] >> 4) : lq[e]) & 0x0f0f0f0fu;
+            const std::uint32_t hq = in.qh[e];
+            const std::uint32_t hib = (j <= 2u ? (hq << (4u - 2u * j)) : (hq >> (2u * j - 4u))) & 0x30303030u;
+            const std::uint32_t u = nib | hib;
+            const half2v lo = (bits_as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias) * dd;
+            const half2v hi = (bits_as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias) * dd;
+            w[4 * e] = lo[0]; w[4 * e + 1] = lo[1]; w[4 * e + 2] = hi[0]; w[4 * e + 3] = hi[1];
+        }
     } else {
         const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<std::uint16_t>(in.h.x & 0xffffu)));
         const float dmin = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<std::uint16_t>(in.h.x >> 16)));
@@ -250,7 +284,11 @@ __global__ __launch_bounds__(kThreads, (TM * TN >= 32 && PF == 2) ? 1 : 2) void 
 #pragma unroll
         for (int t = 0; t < TN; ++t) {
             const std::uint32_t rt = rt0 + static_cast<std::uint32_t>(t);
-            load_step<FMT>(a.codes, a.scales, rt, a.kt, s, lane, rt < a.nt, dst[t]);
+            if constexpr (dense_storage(FMT)) {
+                load_dense_step<FMT>(a.codes, a.n, a.kt, rt, s, lane, dst[t]);
+            } else {
+                load_step<FMT>(a.codes, a.scales, rt, a.kt, s, lane, rt < a.nt, dst[t]);
+            }
         }
     };
     // One pipeline step over codes `cur`; refills `cur` with step s+PF once
@@ -530,6 +568,26 @@ __global__ __launch_bounds__(kThreads) void prefill_bound_kernel(int type, const
     if ((threadIdx.x & 63u) == 0) atomicMax(bound_bits, __float_as_uint(local) & 0x7fffffffu);
 }
 
+// Largest |weight| bound of dense storage, as float bits: BF16 the values
+// themselves (`count` of them), Q6_K |d| * 32 * 128 over the d plane
+// (`count` super-blocks).
+__global__ __launch_bounds__(kThreads) void dense_bound_kernel(int storage, const void* w, std::uint64_t count,
+                                                               std::uint32_t* bound_bits) {
+    float local = 0.0f;
+    for (std::uint64_t i = blockIdx.x * static_cast<std::uint64_t>(kThreads) + threadIdx.x; i < count;
+         i += static_cast<std::uint64_t>(gridDim.x) * kThreads) {
+        const std::uint16_t bits = static_cast<const std::uint16_t*>(w)[i];
+        const float b = storage == kBF16 ? fabsf(__uint_as_float(static_cast<std::uint32_t>(bits) << 16))
+                                         : fabsf(f16_bits_to_f32(bits)) * 4096.0f;
+        local = (b > local || b != b) ? b : local;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float o = __shfl_xor(local, off);
+        local = (o > local || o != o) ? o : local;
+    }
+    if ((threadIdx.x & 63u) == 0) atomicMax(bound_bits, __float_as_uint(local) & 0x7fffffffu);
+}
+
 template <int TM, int TN>
 hipError_t launch_lds(const GemmArgs& args, std::uint32_t stages, std::uint32_t blocks, hipStream_t stream) {
     const dim3 grid(blocks), block(kThreads);
@@ -701,6 +759,9 @@ hipError_t launch_prefill_linear(const TilePlanes& p, const float* x, const floa
         case kQ8_0: return launch_gemm_fmt<kQ8_0>(args, sh, blocks, stream);
         case kQ4_0: return launch_gemm_fmt<kQ4_0>(args, sh, blocks, stream);
         case kQ4_K: return launch_gemm_fmt<kQ4_K>(args, sh, blocks, stream);
+        case kF16: return launch_gemm_fmt<kF16>(args, sh, blocks, stream);
+        case kBF16: return launch_gemm_fmt<kBF16>(args, sh, blocks, stream);
+        case kQ6_K: return launch_gemm_fmt<kQ6_K>(args, sh, blocks, stream);
         default: return hipErrorInvalidValue;
         }
     };
@@ -749,6 +810,47 @@ hipError_t launch_split_reduce(const float* partials, std::uint32_t splits, std:
     return hipGetLastError();
 }
 
+namespace {
+// e = smallest integer with bound * 2^-e <= 2^15 (scale 1 for a zero or
+// non-finite bound).
+void set_prefill_exponent(TilePlanes& p, float bound) {
+    p.prefill_scale = 1.0f;
+    p.prefill_unscale = 1.0f;
+    if (bound > 0.0f && bound < 3.0e38f) {
+        int e = 0;
+        (void)std::frexp(bound, &e);          // bound = f * 2^e, f in [0.5, 1)
+        e -= 15;                              // bound * 2^-e < 2^15
+        e = e < -100 ? -100 : (e > 100 ? 100 : e);
+        p.prefill_scale = std::ldexp(1.0f, -e);
+        p.prefill_unscale = std::ldexp(1.0f, e);
+    }
+}
+} // namespace
+
+hipError_t compute_dense_prefill_scale(TilePlanes& p, std::uint32_t* bound_scratch, hipStream_t stream) {
+    p.prefill_scale = 1.0f;
+    p.prefill_unscale = 1.0f;
+    if (p.type == kF16) return hipSuccess;   // the rows are the f16 operands themselves
+    const std::uint64_t count = p.type == kBF16 ? p.k * p.n : p.k * p.n / 256u;
+    const void* src = p.type == kBF16 ? p.codes
+                                      : static_cast<const void*>(static_cast<const unsigned char*>(p.codes) + count * 208u);
+    hipError_t err = hipMemsetAsync(bound_scratch, 0, sizeof(std::uint32_t), stream);
+    if (err != hipSuccess) return err;
+    const std::uint64_t grid = ceil_div(count, kThreads);
+    hipLaunchKernelGGL(dense_bound_kernel, dim3(static_cast<unsigned>(grid < 4096u ? grid : 4096u)), dim3(kThreads), 0,
+                       stream, p.type, src, count, bound_scratch);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    std::uint32_t bits = 0;
+    err = hipMemcpyAsync(&bits, bound_scratch, sizeof(bits), hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(stream);
+    if (err != hipSuccess) return err;
+    float bound;
+    std::memcpy(&bound, &bits, sizeof(bound));
+    set_prefill_exponent(p, bound);
+    return hipSuccess;
+}
+
 hipError_t compute_prefill_scale(TilePlanes& p, std::uint32_t* bound_scratch, hipStream_t stream) {
     const auto geo = geometry_of(p.type);
     const std::uint64_t tiles = static_cast<std::uint64_t>(p.nt) * p.kt;
@@ -767,17 +869,7 @@ hipError_t compute_prefill_scale(TilePlanes& p, std::uint32_t* bound_scratch, hi
     if (err != hipSuccess) return err;
     float bound;
     std::memcpy(&bound, &bits, sizeof(bound));
-    p.prefill_scale = 1.0f;
-    p.prefill_unscale = 1.0f;
-    if (bound > 0.0f && bound < 3.0e38f) {
-        // e = smallest integer with bound * 2^-e <= 2^15
-        int e = 0;
-        (void)std::frexp(bound, &e);          // bound = f * 2^e, f in [0.5, 1)
-        e -= 15;                              // bound * 2^-e < 2^15
-        e = e < -100 ? -100 : (e > 100 ? 100 : e);
-        p.prefill_scale = std::ldexp(1.0f, -e);
-        p.prefill_unscale = std::ldexp(1.0f, e);
-    }
+    set_prefill_exponent(p, bound);
     return hipSuccess;
 }
 

@@ -186,8 +186,10 @@ int air_hip_context_set_decode_pipeline(air_hip_context* ctx, uint32_t lds_stage
 int air_hip_context_set_wsplit(air_hip_context* ctx, uint32_t mode, uint32_t tile_n, uint32_t waves, uint32_t depth,
                                uint32_t k_splits, uint32_t split_x);
 /* Chooses the kernel of the dense matrices (F16, BF16 and Q6_K storage;
- * autotuning): path 0 = automatic (the matrix-core kernel for 2..64 rows),
- * 1 = the matrix-core kernel at every width, 2 = the FMA kernels.
+ * autotuning): path 0 = automatic (the matrix-core kernel for 2..64 rows,
+ * the f16 prefill GEMM on the rows at prefill widths, FMA kernels
+ * otherwise), 1 = the matrix-core kernel at every width, 2 = the FMA
+ * kernels.
  * tile_n = 16-row weight tiles per workgroup (1, 2 or 4), waves = waves
  * splitting K (1..8), depth = weight steps per wave ring (2 or 4); 0 keeps
  * the automatic choice.  No counterpart in the reference. */

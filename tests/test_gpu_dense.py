@@ -1,7 +1,8 @@
 """The encodings without a resident tile format: F32, F16, BF16 and Q6_K
 (held as the file's rows -- Q6_K as super-block records -- on f32 FMA
-kernels, and for F16, BF16 and Q6_K at two or more rows on the matrix
-cores) and Q5_0 (rewritten exactly as Q8_0 blocks, then the Q8_0 kernels).  The reference decodes all
+kernels, and for F16, BF16 and Q6_K on the matrix cores at 2..64 rows and
+through the f16 prefill GEMM above) and Q5_0 (rewritten exactly as Q8_0
+blocks, then the Q8_0 kernels).  The reference decodes all
 of them per element in decode_element (src/cuda/cuda_backend.cu:241-344);
 a Qwen2.5 Q4_K_M file mixes Q6_K and Q5_0 tensors with Q4_K and Q8_0.
 
@@ -126,10 +127,11 @@ def test_new_types_match_oracle(torch_cuda, hip_ctx, type_id, k, n):
                 assert helpers.same_bits(e[i], want_w[r]), (i, r)
             else:
                 assert (e[i] == 7.0).all(), (i, r)
-        # Q5_0 runs the Q8_0 kernels: split-f16 decode (1e-4) and the
-        # prefill GEMM's single f16 operand (its 1e-2 gate).
+        # Q5_0 runs the Q8_0 kernels: split-f16 decode (1e-4); the prefill
+        # GEMM (Q5_0 as Q8_0, and the F16 / BF16 / Q6_K rows) has single f16
+        # operands (its 1e-2 gate); F32 rows stay on the f32 FMA GEMM.
         tol_decode = 1e-4 if type_id == capi.TYPE_Q5_0 else 1e-5
-        tol_prefill = 1e-2 if type_id == capi.TYPE_Q5_0 else 1e-5
+        tol_prefill = 1e-2
         bias = helpers.activations(1, n, seed=n)[0] * 0.1
         bias_d = _dev(torch, bias)
         for m in (1, 3, 16, 17, 64, 100):
@@ -146,6 +148,8 @@ def test_new_types_match_oracle(torch_cuda, hip_ctx, type_id, k, n):
                 mat.linear(x_d, y, m, bias=bias_d, tactic=tactic)
                 torch.cuda.synchronize()
                 got = y.cpu().numpy()
+                assert plan.startswith("prefill") == (type_id != capi.TYPE_F32 and (
+                    tactic == capi.LINEAR_PREFILL or (tactic == capi.LINEAR_AUTO and m > 64))), plan
                 tol = tol_prefill if plan.startswith("prefill") else tol_decode
                 for r in range(m):
                     err = helpers.rel_l2(got[r], want[r])
@@ -194,6 +198,48 @@ def test_dense_mfma_shapes_match_oracle(torch_cuda, hip_ctx, type_id, k, n):
                     assert err <= 1e-5, (m, plan, r, err)
                 assert np.array_equal(outs[1].view(np.uint32), outs[0].view(np.uint32)), (m, plan)
     finally:
+        hip_ctx.set_dense_path(0)
+        mat.release()
+
+
+PREFILL_CASES = [(capi.TYPE_F16, 1056, 300), (capi.TYPE_BF16, 512, 200), (capi.TYPE_Q6_K, 768, 130)]
+
+
+@pytest.mark.parametrize("type_id,k,n", PREFILL_CASES,
+                         ids=[f"{capi.TYPE_NAMES[t]}-{n}x{k}" for t, k, n in PREFILL_CASES])
+def test_dense_prefill_gemm_matches_oracle(torch_cuda, hip_ctx, type_id, k, n):
+    """Prefill widths over dense storage run the f16 MFMA prefill GEMM on the
+    rows themselves (F16 as they are, BF16 and Q6_K formed in f16 under the
+    matrix's power-of-two weight exponent): within the prefill GEMM's 1e-2 of
+    the oracle per row at 65..512 rows, every register tile and a K split,
+    with a ragged last row tile and a K ending inside a 64-k step (1056);
+    the FMA GEMM (dense path 2) stays within 1e-5."""
+    torch = torch_cuda
+    canon = _weights(type_id, k, n, seed=k + 13 * n + type_id)
+    mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    bias = helpers.activations(1, n, seed=n + 2)[0] * 0.1
+    bias_d = _dev(torch, bias)
+    try:
+        for m in (65, 200, 512):
+            x = helpers.activations(m, k, seed=m + 7 * k)
+            want = oracle.linear(type_id, canon, k, n, x, bias=bias)
+            x_d = _dev(torch, x)
+            for path, tiling in [(0, (0, 0, 0, 0)), (0, (4, 2, 0, 0)), (0, (8, 4, 3, 1)), (0, (8, 2, 0, 0)),
+                                 (2, (0, 0, 0, 0))]:
+                hip_ctx.set_dense_path(path)
+                hip_ctx.set_prefill_tuning(*tiling)
+                plan = mat.plan(m)
+                assert plan.startswith("prefill_gemm_kernel") == (path == 0), plan
+                y = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+                mat.linear(x_d, y, m, bias=bias_d)
+                torch.cuda.synchronize()
+                got = y.cpu().numpy()
+                tol = 1e-2 if path == 0 else 1e-5
+                for r in range(m):
+                    err = helpers.rel_l2(got[r], want[r])
+                    assert err <= tol, (m, plan, r, err)
+    finally:
+        hip_ctx.set_prefill_tuning(0, 0, 0, 0)
         hip_ctx.set_dense_path(0)
         mat.release()
 
