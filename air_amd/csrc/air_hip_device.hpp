@@ -106,6 +106,32 @@ __device__ __forceinline__ void q4k_scale_min_x4(const std::uint32_t s[3], bool 
     mins = upper ? (((s[2] >> 4) & 0x0f0f0f0fu) | ((s[1] >> 2) & 0x30303030u)) : (s[1] & 0x3f3f3f3fu);
 }
 
+// Q6_K super-block record (linear_dense.hip): byte b (0..47) of lane group
+// g's codes lies at 48 g + b, so a lane group reads its whole super-block in
+// three 16-byte loads.  Group g's bytes: 4-byte runs 12 (2 h + s) + {0, 4:
+// low nibbles of quadrants with j % 2 = 0, 1; 8: high pairs} for half h,
+// half-quadrant s, elements 4 g..+3.
+__host__ __device__ constexpr std::uint32_t q6k_code_offset(std::uint32_t g, std::uint32_t b) { return 48u * g + b; }
+
+__device__ __forceinline__ float lane_value(float v, int src) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
+}
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp_float(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, false));
+}
+
+// Maximum over the 64 lanes: within each 16-lane row by DPP (quad swaps,
+// half-row and row mirrors), then across the four rows by readlane.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_float<0xb1>(v));    // quad_perm [1, 0, 3, 2]
+    v = fmaxf(v, dpp_float<0x4e>(v));    // quad_perm [2, 3, 0, 1]
+    v = fmaxf(v, dpp_float<0x141>(v));   // row_half_mirror
+    v = fmaxf(v, dpp_float<0x140>(v));   // row_mirror
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+
 __device__ __forceinline__ float4v mfma16x16x32(const half8v& a, const half8v& b, const float4v& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

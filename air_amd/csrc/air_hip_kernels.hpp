@@ -77,15 +77,19 @@ hipError_t launch_stream_read(const void* data, std::uint64_t bytes, unsigned* s
 // Resident bytes of a dense matrix stored as `storage` (kQ6_K: 208-byte
 // super-block records plus 2 bytes of d each; 0 when k does not fit).
 std::uint64_t dense_resident_bytes(int storage, std::uint64_t k, std::uint64_t n);
-// Launch shape of the M = 1 Q6_K GEMV: output columns per workgroup and
-// waves splitting K (compiled: 2x4, 4x4);
-// set_q6k_gemv_shape overrides the planner for sweeps ({0, 0} restores it).
-struct Q6kGemvShape {
-    unsigned columns{0};
-    unsigned waves{0};
+// Waves per workgroup of the M = 1 Q6_K GEMV (one 16-row tile per
+// workgroup); `waves` != 0 overrides the planner (1..16).
+std::uint32_t q6k_gemv_waves(std::uint64_t k, std::uint64_t n, std::uint32_t waves);
+// Its launch: waves, super-blocks per work unit (1, 2), units in flight per
+// wave (1, 2); sweeps override them through DenseTuning's shape (waves;
+// tile_n = 2 for two super-blocks per unit; depth = 4 for one unit in
+// flight, 2 for two).
+struct Q6kGemvPlan {
+    std::uint32_t waves{1};
+    std::uint32_t units{1};
+    std::uint32_t depth{2};
 };
-Q6kGemvShape q6k_gemv_shape(std::uint64_t k, std::uint64_t n);
-void set_q6k_gemv_shape(const Q6kGemvShape& shape);
+Q6kGemvPlan plan_q6k_gemv(std::uint64_t k, std::uint64_t n, const DenseMfmaShape& tuning);
 // Canonical Q6_K blocks (device) -> 208-byte records and the d plane.
 hipError_t launch_q6k_records(const void* canonical, std::uint64_t blocks, void* records, hipStream_t stream);
 // Dense matrix -> f32 [n][k], bit-exact decode.

@@ -55,10 +55,12 @@ constexpr bool dense_storage(int fmt) { return fmt == kF16 || fmt == kBF16 || fm
 
 // Rows of a dense matrix of n rows and k columns; rows past n read as zero
 // weights.  Q6_K: step s is quadrant pair q = s % 4 of super-block s / 4 --
-// half h = q / 2 of the record, quadrants j = 2 (q % 2) + b for its blocks b;
-// element 8 g + e of a quadrant has its low nibble (nibble q % 2) in ql byte
-// 64 h + 32 b + 8 g + e, its high pair (bits 2 j) in qh byte 32 h + 8 g + e,
-// its scale in scales byte 8 h + 2 j + g / 2 (src/reference/tensor_reader.cpp:197-242).
+// half h = q / 2, quadrants j = 2 (q % 2) + b for its blocks b; element
+// 8 g + e of a quadrant (half-quadrant g / 2, element i = 8 (g % 2) + e of
+// it) has its low nibble (nibble q % 2) and its high pair (bits 2 j) in the
+// record's runs for lane group i / 4 and half-quadrant pair 2 h + g / 2
+// (linear_dense.hip), its scale in scales byte 8 h + 2 j + g / 2
+// (src/reference/tensor_reader.cpp:197-242).
 template <int FMT>
 __device__ __forceinline__ void load_dense_step(const void* w, std::uint64_t n, std::uint64_t k, std::uint32_t rt,
                                                 std::uint32_t s, std::uint32_t lane, StepCodes<FMT>& out) {
@@ -75,9 +77,15 @@ __device__ __forceinline__ void load_dense_step(const void* w, std::uint64_t n, 
         const std::uint64_t blk = row * sbs + s / 4u;
         const unsigned char* rec = static_cast<const unsigned char*>(w) + blk * 208u;
         const std::uint32_t q = s & 3u, h = q >> 1;
-        out.ql[0] = *reinterpret_cast<const u32x2*>(rec + 64u * h + 8u * g);
-        out.ql[1] = *reinterpret_cast<const u32x2*>(rec + 64u * h + 32u + 8u * g);
-        out.qh = *reinterpret_cast<const u32x2*>(rec + 128u + 32u * h + 8u * g);
+        // Runs of lane groups 2 (g % 2) and 2 (g % 2) + 1 (q6k_code_offset).
+        const std::uint32_t b = 12u * (2u * h + (g >> 1));
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const std::uint32_t gg = 2u * (g & 1u) + static_cast<std::uint32_t>(r);
+            out.ql[0][r] = *reinterpret_cast<const std::uint32_t*>(rec + q6k_code_offset(gg, b));
+            out.ql[1][r] = *reinterpret_cast<const std::uint32_t*>(rec + q6k_code_offset(gg, b + 4u));
+            out.qh[r] = *reinterpret_cast<const std::uint32_t*>(rec + q6k_code_offset(gg, b + 8u));
+        }
         out.sc = *reinterpret_cast<const std::uint32_t*>(rec + 192u + 8u * h + 4u * (q & 1u));
         out.d = reinterpret_cast<const std::uint16_t*>(static_cast<const unsigned char*>(w) + n * sbs * 208u)[blk];
     } else {

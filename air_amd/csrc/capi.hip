@@ -691,7 +691,7 @@ int air_hip_context_set_dense_path(air_hip_context* ctx, uint32_t path, uint32_t
     if (tile_n != 0u && tile_n != 1u && tile_n != 2u && tile_n != 4u) {
         return fail(AIR_HIP_INVALID_ARGUMENT, "tile_n must be 0, 1, 2 or 4");
     }
-    if (waves > 8u) return fail(AIR_HIP_INVALID_ARGUMENT, "waves must be 0 .. 8");
+    if (waves > 16u) return fail(AIR_HIP_INVALID_ARGUMENT, "waves must be 0 .. 16");
     if (depth != 0u && depth != 2u && depth != 4u) return fail(AIR_HIP_INVALID_ARGUMENT, "depth must be 0, 2 or 4");
     ctx->dense_tuning = DenseTuning{path, DenseMfmaShape{tile_n, waves, depth}};
     return AIR_HIP_OK;
@@ -1167,11 +1167,10 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
             }
             break;
         }
-        if (m->type == kQ6_K && rows == 1u &&
-            !dense_mfma_route(m->dense_storage, m->planes.k, m->planes.n, rows, ctx->dense_tuning)) {
-            const Q6kGemvShape q = q6k_gemv_shape(m->planes.k, m->planes.n);
-            std::snprintf(buf, sizeof buf, "q6k_gemv_kernel columns=%u waves=%u (dense q6_k super-block rows)", q.columns,
-                          q.waves);
+        if (m->type == kQ6_K && rows == 1u && ctx->dense_tuning.path == 0u) {
+            const Q6kGemvPlan g = plan_q6k_gemv(m->planes.k, m->planes.n, ctx->dense_tuning.shape);
+            std::snprintf(buf, sizeof buf, "q6k_gemv_kernel waves=%u units=%u depth=%u (dense q6_k super-block rows)",
+                          g.waves, g.units, g.depth);
             break;
         }
         if (dense_mfma_route(m->dense_storage, m->planes.k, m->planes.n, rows, ctx->dense_tuning)) {

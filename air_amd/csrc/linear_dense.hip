@@ -29,9 +29,39 @@ constexpr unsigned kDenseRowsKernelMax = 64;   // wider x: the tiled GEMM
 constexpr unsigned kGemmTile = 64;
 constexpr unsigned kGemmK = 32;
 
-// Q6_K super-block record: [ql:128][qh:64][scales:16 x int8]; block b's f16
-// d is entry b of the plane that follows all `nblocks` records.
+// Q6_K super-block record: 192 bytes of codes, then the 16 int8 sub-block
+// scales; block b's f16 d is entry b of the plane that follows all
+// `nblocks` records.  The codes are the canonical block's ql / qh bytes
+// regrouped by the lane that reads them: element e = 128 h + 32 j + 16 s + i
+// (half h, quadrant j, half-quadrant s, i < 16) has its low nibble (nibble
+// j / 2) in canonical ql byte 64 h + 32 (j % 2) + 16 s + i and its high pair
+// (bits 2j, 2j + 1) in qh byte 32 h + 16 s + i (src/reference/tensor_reader.cpp:197-242);
+// with g = i / 4, lane group g's 48 bytes hold those 4-byte runs at
+//     b = 12 (2 h + s) + {0: ql of j % 2 = 0, 4: ql of j % 2 = 1, 8: qh},
+// and its byte b lies at q6k_code_offset(g, b) = 48 g + b: a lane group
+// reads its whole super-block (its four elements of each of the 16
+// sub-blocks) in three 16-byte loads.
 constexpr std::uint32_t kQ6kRecord = 208;
+
+// Byte offset in a record of the 4-byte run of element e's low nibbles
+// (qh = false) or high pairs (qh = true); e a multiple of 4.
+__device__ __forceinline__ std::uint32_t q6k_run(std::uint32_t e, bool qh) {
+    const std::uint32_t h = e >> 7, j = (e >> 5) & 3u, s = (e >> 4) & 1u, g = (e >> 2) & 3u;
+    return q6k_code_offset(g, 12u * (2u * h + s) + (qh ? 8u : 4u * (j & 1u)));
+}
+
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+
+// Four Q6_K codes (low nibbles in the low half of `nib`'s bytes, high pairs
+// in bits 4-5 of `hib`'s bytes) as exact f16 values q - 32: 1024 + q under
+// the exponent byte 0x64, minus 1056.
+__device__ __forceinline__ half4v q6_codes4(std::uint32_t nib, std::uint32_t hib) {
+    const std::uint32_t u = (nib & 0x0f0f0f0fu) | (hib & 0x30303030u);
+    const half2v bias = {(_Float16)1056.0f, (_Float16)1056.0f};
+    const half2v lo = bits_as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias;
+    const half2v hi = bits_as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias;
+    return half4v{lo[0], lo[1], hi[0], hi[1]};
+}
 
 __device__ __forceinline__ const std::uint16_t* q6k_d_plane(const void* w, std::uint64_t nblocks) {
     return reinterpret_cast<const std::uint16_t*>(static_cast<const unsigned char*>(w) + nblocks * kQ6kRecord);
@@ -40,24 +70,22 @@ __device__ __forceinline__ const std::uint16_t* q6k_d_plane(const void* w, std::
 // Four consecutive weights w[idx .. idx + 3] (idx a multiple of 4) of a
 // dense matrix stored as WT (f32, f16 / bf16 bits, or Q6_K records of a
 // matrix of nblocks super-blocks), as exact f32.  Q6_K: a row is whole
-// super-blocks (k a multiple of 256), so
-// element idx lies in record idx / 256 at position e = idx % 256: half
-// h = e / 128, quadrant j and offset i within it; its low nibble is nibble
-// j >> 1 of ql[64 h + 32 (j & 1) + i], its high bits are bits 2j, 2j + 1 of
-// qh[32 h + i], its scale is scales[8 h + i / 16 + 2 j]; four weights share
-// the quadrant and the scale (src/reference/tensor_reader.cpp:197-242).
+// super-blocks (k a multiple of 256), so element idx lies in record idx /
+// 256 at position e = idx % 256 (quadrant j = e / 32 % 4); four weights
+// share a 4-byte run of low nibbles (nibble j / 2), one of high pairs (bits
+// 2j, 2j + 1) and the sub-block scale e / 16; each is (d * sc) * (q - 32),
+// the reference's decode (src/reference/tensor_reader.cpp:197-242).
 template <int WT>
 __device__ __forceinline__ float4 load_w4(const void* __restrict__ w, std::uint64_t idx, std::uint64_t nblocks) {
     if constexpr (WT == kQ6_K) {
         const unsigned char* rec = static_cast<const unsigned char*>(w) + (idx >> 8) * kQ6kRecord;
         const std::uint32_t e = static_cast<std::uint32_t>(idx & 255u);
-        const std::uint32_t h = e >> 7, j = (e >> 5) & 3u, i = e & 31u;
-        const std::uint32_t ql = *reinterpret_cast<const std::uint32_t*>(rec + 64u * h + 32u * (j & 1u) + i);
-        const std::uint32_t qh = *reinterpret_cast<const std::uint32_t*>(rec + 128u + 32u * h + i);
-        const std::uint32_t scw = *reinterpret_cast<const std::uint32_t*>(rec + 192u + 8u * h + 4u * (j >> 1));
+        const std::uint32_t j = (e >> 5) & 3u;
+        const std::uint32_t ql = *reinterpret_cast<const std::uint32_t*>(rec + q6k_run(e, false));
+        const std::uint32_t qh = *reinterpret_cast<const std::uint32_t*>(rec + q6k_run(e, true));
         const float d = f16_bits_to_f32(q6k_d_plane(w, nblocks)[idx >> 8]);
-        // scales[8h + i/16 + 2j]: byte (i/16 + 2j) - 4 (j >> 1) of the word.
-        const int sc = static_cast<int>(static_cast<std::int8_t>((scw >> (8u * ((i >> 4) + 2u * (j & 1u)))) & 0xffu));
+        // Sub-block e / 16 = 8 h + 2 j + s.
+        const int sc = static_cast<int>(static_cast<std::int8_t>(rec[192u + (e >> 4)]));
         const float ds = d * static_cast<float>(sc);
         const std::uint32_t nib = (j >> 1) ? (ql >> 4) & 0x0f0f0f0fu : ql & 0x0f0f0f0fu;
         const std::uint32_t hb = (qh >> (2u * j)) & 0x03030303u;
@@ -241,106 +269,140 @@ __global__ __launch_bounds__(kDenseThreads) void dense_rows_gather_kernel(const 
     }
 }
 
-// One row of x through Q6_K records (M = 1).  A lane takes one 16-weight
-// group of a super-block -- group g = 8 h + 2 j + g1 holds elements
-// 128 h + 32 j + 16 g1 .. + 15, its low nibbles in 16 bytes of ql (nibble
-// j >> 1), its high bits in 16 bytes of qh (bits 2j, 2j + 1), one 6-bit
-// sub-block scale -- for the workgroup's C consecutive output columns, so
-// its 16 activations are loaded once per super-block and C columns.
-// Sixteen lanes cover a super-block, a wave four, the workgroup's kWaves
-// waves 4 kWaves per step.  Software-pipelined: a wave holds the loads of its
-// next step (activations and every column's codes) in flight while it
-// computes the current one.  Each weight is fma(d * sc, q, -32 * d * sc),
-// which rounds once and so equals the reference's (d * sc) * (q - 32), then
-// enters an f32 FMA with x; lane and wave partials meet in a fixed order.
-template <unsigned C, unsigned kWaves>
-__global__ __launch_bounds__(64 * kWaves) void q6k_gemv_pipe_kernel(const unsigned char* __restrict__ w,
-                                                                    const float* __restrict__ x,
-                                                                    const float* __restrict__ bias,
-                                                                    float* __restrict__ y, std::uint64_t k,
-                                                                    std::uint64_t n) {
-    __shared__ float red[kWaves][C];
-    const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+// One row of x through Q6_K records (M = 1) on the matrix cores.  A
+// workgroup owns one 16-row tile; its W waves split the row's super-blocks.
+// Per super-block the 16 sub-blocks of 16 weights form a block-diagonal
+// problem (the M = 1 GEMV's trick, linear_gemv.hip): A row r holds the
+// activations of sub-block r (lane l: row l % 16, elements 4 (l / 16)..+3),
+// split into f16 hi + lo under one power-of-two scale per super-block; the
+// 16x16x16 MFMAs of sub-block j take the exact f16 codes q - 32 of the 16
+// rows (lane l: row l % 16, the same four elements, from the lane group's
+// contiguous 48 bytes of the record) against A with only row j live, so
+// they accumulate and D row j (lane group j / 4, slot j % 4) ends with the
+// sub-block's products, which take its own scale sc (exact in f32; the lane
+// group's four scales are one dword of the record).  Per super-block, the
+// scaled slots times d * (inverse activation scale); the waves' row sums
+// meet in LDS in wave order.
+// U super-blocks per work unit (their loads issued together), P units in
+// flight per wave (2: the next unit loads while the current computes).
+template <int U, int P>
+__global__ __launch_bounds__(1024) void q6k_gemv_kernel(const unsigned char* __restrict__ w,
+                                                        const float* __restrict__ x, const float* __restrict__ bias,
+                                                        float* __restrict__ y, std::uint64_t k, std::uint64_t n) {
+    __shared__ float red[16][16];
+    const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
+    const unsigned g = lane >> 4;
     const std::uint64_t sbs = k / 256u;
+    const std::uint64_t row = static_cast<std::uint64_t>(blockIdx.x) * 16u + (lane & 15u);
+    const bool live = row < n;
+    const std::uint64_t rrow = live ? row : n - 1u;   // padded rows read the last real row, not stored
     const std::uint16_t* dplane = q6k_d_plane(w, sbs * n);
-    const std::uint64_t c0 = static_cast<std::uint64_t>(blockIdx.x) * C;
-    const std::uint32_t g = lane & 15u, h = g >> 3, j = (g >> 1) & 3u, g1 = g & 1u;
-    const std::uint32_t e0 = 128u * h + 32u * j + 16u * g1;
-    const std::uint32_t ql_off = 64u * h + 32u * (j & 1u) + 16u * g1;
-    const std::uint32_t qh_off = 128u + 32u * h + 16u * g1;
-    const std::uint32_t sc_off = 192u + 8u * h + 2u * j + g1;
-    struct Step {
-        float4 x[4];
-        u32x4 ql[C], qh[C];
-        std::uint32_t sc[C], d[C];
+    const std::uint64_t units = (sbs + U - 1u) / U;
+    const std::uint64_t u0 = units * wave / W, u1 = units * (wave + 1u) / W;
+    // Loads of one super-block (plain vector variables: a struct of them
+    // would live in scratch memory).
+    const auto load = [&](std::uint64_t sb, u32x4& c0, u32x4& c1, u32x4& c2, std::uint32_t& scw, std::uint32_t& dbits,
+                          float4v& xv) __attribute__((always_inline)) {
+        const std::uint64_t blk = rrow * sbs + sb;
+        const unsigned char* rec = w + blk * kQ6kRecord;
+        const u32x4* cp = reinterpret_cast<const u32x4*>(rec + 48u * g);
+        c0 = cp[0];   // group bytes 0..15; plain loads: the four groups' loads
+        c1 = cp[1];   // of one instruction interleave with the next ones' in
+        c2 = cp[2];   // the same lines, which L2 then serves
+        scw = *reinterpret_cast<const std::uint32_t*>(rec + 192u + 4u * g);
+        dbits = dplane[blk];
+        xv = *reinterpret_cast<const float4v*>(x + sb * 256u + 16u * (lane & 15u) + 4u * g);
     };
-    const auto load = [&](Step& st, std::uint64_t sb) __attribute__((always_inline)) {
-        const float4* xp = reinterpret_cast<const float4*>(x + sb * 256u + e0);
+    float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const auto compute = [&](const u32x4& c0, const u32x4& c1, const u32x4& c2, std::uint32_t scw, std::uint32_t dbits,
+                             const float4v& xv) __attribute__((always_inline)) {
+        const float amax = wave_max(fmaxf(fmaxf(fabsf(xv[0]), fabsf(xv[1])), fmaxf(fabsf(xv[2]), fabsf(xv[3]))));
+        float s, inv;
+        block_scale(amax, s, inv);
+        const float e8[8] = {xv[0], xv[1], xv[2], xv[3], 0.0f, 0.0f, 0.0f, 0.0f};
+        half8v h8, l8;
+        split8(e8, s, h8, l8);
+        const half4v hi = {h8[0], h8[1], h8[2], h8[3]};
+        const half4v lo = {l8[0], l8[1], l8[2], l8[3]};
+        // Sub-block jb's MFMAs take A with only row jb live (the other rows
+        // zero), so D row jb collects exactly its products and the MFMAs
+        // accumulate: four accumulators, jb % 4, keep four chains in flight.
+        const half4v zero4 = {(_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+        const unsigned arow = lane & 15u;
+        float4v dacc0 = {0.0f, 0.0f, 0.0f, 0.0f}, dacc1 = dacc0, dacc2 = dacc0, dacc3 = dacc0;
 #pragma unroll
-        for (unsigned i = 0; i < 4; ++i) st.x[i] = xp[i];
+        for (int jb = 0; jb < 16; ++jb) {
+            // Sub-block jb = 8 h + 2 j + s: group word 3 (2 h + s) + part.
+            const int h = jb >> 3, j = (jb >> 1) & 3, sh = jb & 1;
+            const int wl = 3 * (2 * h + sh) + (j & 1), wh = 3 * (2 * h + sh) + 2;
+            const u32x4& vl = wl < 4 ? c0 : wl < 8 ? c1 : c2;
+            const u32x4& vh = wh < 4 ? c0 : wh < 8 ? c1 : c2;
+            const std::uint32_t ql = vl[wl & 3];
+            const std::uint32_t qh = vh[wh & 3];
+            const std::uint32_t nib = (j >> 1) ? (ql >> 4) : ql;
+            const std::uint32_t hib = 2 * j <= 4 ? (qh << (4 - 2 * j)) : (qh >> (2 * j - 4));
+            const half4v wq = q6_codes4(nib, hib);
+            const bool row_live = arow == static_cast<unsigned>(jb);
+            const half4v ah = row_live ? hi : zero4;
+            const half4v al = row_live ? lo : zero4;
+            float4v& dacc = (jb & 3) == 0 ? dacc0 : (jb & 3) == 1 ? dacc1 : (jb & 3) == 2 ? dacc2 : dacc3;
+            dacc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, wq, dacc, 0, 0, 0);
+            dacc = __builtin_amdgcn_mfma_f32_16x16x16f16(al, wq, dacc, 0, 0, 0);
+        }
+        // Lane group g holds D rows 4 g + i: sub-block 4 g + i, in slot i of
+        // accumulator i; its scale is byte i of the group's scale dword.
+        const auto scale = [&](int i) {
+            return static_cast<float>(static_cast<std::int8_t>((scw >> (8 * i)) & 0xffu));
+        };
+        const float4v cacc = {scale(0) * dacc0[0], scale(1) * dacc1[1], scale(2) * dacc2[2], scale(3) * dacc3[3]};
+        const float dv = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<std::uint16_t>(dbits))) * inv;
+        acc += dv * cacc;
+    };
+    // A unit's super-blocks past the row's end load nothing and add nothing.
+    u32x4 ac0[U], ac1[U], ac2[U], bc0[U], bc1[U], bc2[U];
+    std::uint32_t asc[U], ad[U], bsc[U], bd[U];
+    float4v ax[U], bx[U];
+    const auto load_unit = [&](std::uint64_t u, u32x4 (&c0)[U], u32x4 (&c1)[U], u32x4 (&c2)[U], std::uint32_t (&sc)[U],
+                               std::uint32_t (&d)[U], float4v (&xv)[U]) __attribute__((always_inline)) {
 #pragma unroll
-        for (unsigned c = 0; c < C; ++c) {
-            const std::uint64_t col = c0 + c < n ? c0 + c : n - 1u;   // clamped; not stored
-            const std::uint64_t blk = col * sbs + sb;
-            const unsigned char* rec = w + blk * kQ6kRecord;
-            st.ql[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rec + ql_off));
-            st.qh[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rec + qh_off));
-            st.sc[c] = rec[sc_off];
-            st.d[c] = dplane[blk];
+        for (int i = 0; i < U; ++i) {
+            const std::uint64_t sb = u * U + i;
+            if (sb < sbs) load(sb, c0[i], c1[i], c2[i], sc[i], d[i], xv[i]);
         }
     };
-    float acc[C];
+    const auto compute_unit = [&](std::uint64_t u, const u32x4 (&c0)[U], const u32x4 (&c1)[U], const u32x4 (&c2)[U],
+                                  const std::uint32_t (&sc)[U], const std::uint32_t (&d)[U], const float4v (&xv)[U])
+        __attribute__((always_inline)) {
 #pragma unroll
-    for (unsigned c = 0; c < C; ++c) acc[c] = 0.0f;
-    const auto compute = [&](const Step& st) __attribute__((always_inline)) {
-        const float xv[16] = {st.x[0].x, st.x[0].y, st.x[0].z, st.x[0].w, st.x[1].x, st.x[1].y, st.x[1].z, st.x[1].w,
-                              st.x[2].x, st.x[2].y, st.x[2].z, st.x[2].w, st.x[3].x, st.x[3].y, st.x[3].z, st.x[3].w};
-#pragma unroll
-        for (unsigned c = 0; c < C; ++c) {
-            const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<std::uint16_t>(st.d[c])));
-            const float ds = d * static_cast<float>(static_cast<int>(static_cast<std::int8_t>(st.sc[c])));
-            const float bias32 = -32.0f * ds;
-#pragma unroll
-            for (unsigned t = 0; t < 4; ++t) {
-                const std::uint32_t lo = st.ql[c][t], hi = st.qh[c][t];
-                const std::uint32_t nib = (j >> 1) ? (lo >> 4) & 0x0f0f0f0fu : lo & 0x0f0f0f0fu;
-                const std::uint32_t q = nib | (((hi >> (2u * j)) & 0x03030303u) << 4);
-#pragma unroll
-                for (unsigned b = 0; b < 4; ++b) {
-                    const float wq = fmaf(ds, static_cast<float>((q >> (8u * b)) & 0xffu), bias32);
-                    acc[c] = fmaf(wq, xv[4u * t + b], acc[c]);
-                }
-            }
+        for (int i = 0; i < U; ++i) {
+            if (u * U + i < sbs) compute(c0[i], c1[i], c2[i], sc[i], d[i], xv[i]);
         }
     };
-    const std::uint64_t stride = 4u * kWaves;
-    std::uint64_t sb = 4u * wave + (lane >> 4);
-    // Lanes past the last super-block stay in the loop (uniform trip count
-    // per wave is not needed: each lane's loads are its own) but load nothing.
-    Step a, b;
-    if (sb < sbs) load(a, sb);
-    while (sb < sbs) {
-        const std::uint64_t next = sb + stride;
-        if (next < sbs) load(b, next);
-        compute(a);
-        if (next >= sbs) break;
-        const std::uint64_t after = next + stride;
-        if (after < sbs) load(a, after);
-        compute(b);
-        sb = after;
+    if constexpr (P == 1) {
+        for (std::uint64_t u = u0; u < u1; ++u) {
+            load_unit(u, ac0, ac1, ac2, asc, ad, ax);
+            compute_unit(u, ac0, ac1, ac2, asc, ad, ax);
+        }
+    } else {
+        if (u0 < u1) load_unit(u0, ac0, ac1, ac2, asc, ad, ax);
+        for (std::uint64_t u = u0; u < u1; u += 2u) {
+            if (u + 1u < u1) load_unit(u + 1u, bc0, bc1, bc2, bsc, bd, bx);
+            compute_unit(u, ac0, ac1, ac2, asc, ad, ax);
+            if (u + 1u >= u1) break;
+            if (u + 2u < u1) load_unit(u + 2u, ac0, ac1, ac2, asc, ad, ax);
+            compute_unit(u + 1u, bc0, bc1, bc2, bsc, bd, bx);
+        }
     }
-#pragma unroll
-    for (unsigned c = 0; c < C; ++c) {
-        float v = acc[c];
-        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-        if (lane == 0u) red[wave][c] = v;
-    }
+    // Row l % 16's sum: the four slots, then the four lane groups.
+    float t = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    t += __shfl_xor(t, 16);
+    t += __shfl_xor(t, 32);
+    if (lane < 16u) red[wave][lane] = t;
     __syncthreads();
-    if (threadIdx.x < C && c0 + threadIdx.x < n) {
-        float v = red[0][threadIdx.x];
-#pragma unroll
-        for (unsigned q = 1; q < kWaves; ++q) v += red[q][threadIdx.x];
-        y[c0 + threadIdx.x] = bias ? v + bias[c0 + threadIdx.x] : v;
+    if (wave == 0u && lane < 16u && live) {
+        float v = red[0][lane];
+        for (unsigned q = 1; q < W; ++q) v += red[q][lane];
+        y[row] = bias ? v + bias[row] : v;
     }
 }
 
@@ -354,9 +416,10 @@ __global__ __launch_bounds__(kDenseThreads) void dense_dequantize_kernel(const v
     }
 }
 
-// Canonical Q6_K blocks (210 bytes: [ql][qh][scales][d]) -> 208-byte
-// records and the d plane after them; thread t writes output word t of the
-// records, or one d entry.
+// Canonical Q6_K blocks (210 bytes: [ql 128][qh 64][scales 16][d 2]) ->
+// 208-byte records (the codes in lane-group order, then the scales) and the
+// d plane after them; thread t writes output word t of the records, or one
+// d entry.
 __global__ __launch_bounds__(kDenseThreads) void q6k_records_kernel(const unsigned char* __restrict__ src,
                                                                     std::uint64_t blocks,
                                                                     std::uint32_t* __restrict__ dst) {
@@ -367,7 +430,19 @@ __global__ __launch_bounds__(kDenseThreads) void q6k_records_kernel(const unsign
         if (t < blocks * kWords) {
             const std::uint64_t b = t / kWords;
             const std::uint32_t word = static_cast<std::uint32_t>(t % kWords);
-            const unsigned char* bytes = src + b * 210u + 4u * word;
+            std::uint32_t from;   // canonical byte offset of the word's 4-byte run
+            if (word < 48u) {
+                // Record byte 4 word = q6k_code_offset(g, b): group word b / 4
+                // = 3 (2 h + s) + part, part 0 / 1 the low nibbles of
+                // quadrants with j % 2 = part, part 2 the high pairs.
+                const std::uint32_t g = word / 12u, gw = word % 12u;
+                const std::uint32_t run = gw / 3u, part = gw % 3u;
+                const std::uint32_t h = run >> 1, s = run & 1u;
+                from = part < 2u ? 64u * h + 32u * part + 16u * s + 4u * g : 128u + 32u * h + 16u * s + 4u * g;
+            } else {
+                from = 192u + 4u * (word - 48u);   // the scales as they are
+            }
+            const unsigned char* bytes = src + b * 210u + from;
             dst[t] = static_cast<std::uint32_t>(bytes[0]) | (static_cast<std::uint32_t>(bytes[1]) << 8) |
                      (static_cast<std::uint32_t>(bytes[2]) << 16) | (static_cast<std::uint32_t>(bytes[3]) << 24);
         } else {
@@ -380,20 +455,28 @@ __global__ __launch_bounds__(kDenseThreads) void q6k_records_kernel(const unsign
 
 } // namespace
 
-// Launch shape of the Q6_K GEMV (a sweep may set it; zeros = the measured
-// default).
-static Q6kGemvShape g_q6k_shape{};
-void set_q6k_gemv_shape(const Q6kGemvShape& shape) { g_q6k_shape = shape; }
-Q6kGemvShape q6k_gemv_shape(std::uint64_t k, std::uint64_t n) {
-    if (g_q6k_shape.columns != 0u) return g_q6k_shape;
-    (void)n;
-    // Measured on the Qwen2-7B shapes (graphs of distinct matrices, so no
-    // matrix is served from the Infinity Cache): long K (down, 74
-    // super-blocks per row) 4 columns per workgroup, 21.9 us (2.5 TB/s of its
-    // own bytes; without the pipeline 26.5 us at its best shape, f32 rows
-    // 42 us); short K (o, lm_head: one step per wave) 2 columns, 6.9 and
-    // 167 us.  Eight columns, or more waves splitting K, were slower.
-    return k >= 8192u ? Q6kGemvShape{4u, 4u} : Q6kGemvShape{2u, 4u};
+// Launch of the Q6_K GEMV (one 16-row tile per workgroup).  Measured on the
+// Qwen2-7B shapes (graphs over copies larger than the Infinity Cache): waves
+// until the grid holds about 8192, at least two and at most 16 (one per
+// super-block); one super-block per work unit; one unit in flight for long
+// rows (down, 74 super-blocks: 22.3 us, flat within 0.5 us over 4..16 waves
+// and both depths), two for short ones (o 6.5 us, lm_head 127 us; the FMA
+// GEMV it replaced took 22.9, 6.9 and 192).
+std::uint32_t q6k_gemv_waves(std::uint64_t k, std::uint64_t n, std::uint32_t waves) {
+    const std::uint64_t sbs = k / 256u, tiles = ceil_div(n, 16u);
+    std::uint64_t w = waves != 0u ? waves : ceil_div(8192u, tiles);
+    if (waves == 0u && w < 2u) w = 2u;
+    if (w > 16u) w = 16u;
+    if (w > sbs) w = sbs;
+    return static_cast<std::uint32_t>(w < 1u ? 1u : w);
+}
+
+Q6kGemvPlan plan_q6k_gemv(std::uint64_t k, std::uint64_t n, const DenseMfmaShape& tuning) {
+    Q6kGemvPlan g;
+    g.waves = q6k_gemv_waves(k, n, tuning.waves);
+    g.units = tuning.tile_n == 2u ? 2u : 1u;
+    g.depth = tuning.depth == 4u ? 1u : tuning.depth == 2u ? 2u : (k / 256u >= 32u ? 1u : 2u);
+    return g;
 }
 
 std::uint64_t dense_resident_bytes(int storage, std::uint64_t k, std::uint64_t n) {
@@ -430,19 +513,21 @@ hipError_t launch_dense_dequantize(const void* w, int storage, std::uint64_t k, 
 
 template <int WT>
 hipError_t launch_dense_typed(const void* w, std::uint64_t k, std::uint64_t n, const float* x, const float* bias,
-                              float* y, std::uint32_t m, hipStream_t stream) {
-    if (WT == kQ6_K && m == 1u) {
+                              float* y, std::uint32_t m, hipStream_t stream, const DenseTuning& tuning) {
+    if (WT == kQ6_K && m == 1u && tuning.path != 2u) {
+        const std::uint64_t tiles = ceil_div(n, 16u);
+        if (tiles > 0x7fffffffu) return hipErrorInvalidValue;
+        const Q6kGemvPlan g = plan_q6k_gemv(k, n, tuning.shape);
         const auto* wb = static_cast<const unsigned char*>(w);
-        const Q6kGemvShape shape = q6k_gemv_shape(k, n);
-        const dim3 grid(static_cast<unsigned>(ceil_div(n, shape.columns)));
-#define AIR_Q6K_GEMV(C, W)                                                                                          \
-        if (shape.columns == C && shape.waves == W) {                                                               \
-            hipLaunchKernelGGL((q6k_gemv_pipe_kernel<C, W>), grid, dim3(64 * W), 0, stream, wb, x, bias, y, k, n);  \
-            return hipGetLastError();                                                                               \
+        const dim3 grid(static_cast<unsigned>(tiles)), block(64u * g.waves);
+        if (g.units == 2u) {
+            if (g.depth == 2u) hipLaunchKernelGGL((q6k_gemv_kernel<2, 2>), grid, block, 0, stream, wb, x, bias, y, k, n);
+            else hipLaunchKernelGGL((q6k_gemv_kernel<2, 1>), grid, block, 0, stream, wb, x, bias, y, k, n);
+        } else {
+            if (g.depth == 2u) hipLaunchKernelGGL((q6k_gemv_kernel<1, 2>), grid, block, 0, stream, wb, x, bias, y, k, n);
+            else hipLaunchKernelGGL((q6k_gemv_kernel<1, 1>), grid, block, 0, stream, wb, x, bias, y, k, n);
         }
-        AIR_Q6K_GEMV(2, 4) AIR_Q6K_GEMV(4, 4)
-#undef AIR_Q6K_GEMV
-        return hipErrorInvalidConfiguration;
+        return hipGetLastError();
     }
     if (m <= kDenseRowsKernelMax) {
         const dim3 grid(static_cast<unsigned>(ceil_div(n, kDenseCols)), static_cast<unsigned>(ceil_div(m, kDenseMaxRows)));
@@ -482,10 +567,10 @@ hipError_t launch_dense_linear(const void* w, int storage, std::uint64_t k, std:
         return launch_dense_mfma(w, storage, k, n, x, bias, y, m, tuning.shape, stream);
     }
     switch (storage) {
-    case kF32: return launch_dense_typed<kF32>(w, k, n, x, bias, y, m, stream);
-    case kF16: return launch_dense_typed<kF16>(w, k, n, x, bias, y, m, stream);
-    case kBF16: return launch_dense_typed<kBF16>(w, k, n, x, bias, y, m, stream);
-    case kQ6_K: return k % 256u == 0u ? launch_dense_typed<kQ6_K>(w, k, n, x, bias, y, m, stream) : hipErrorInvalidValue;
+    case kF32: return launch_dense_typed<kF32>(w, k, n, x, bias, y, m, stream, tuning);
+    case kF16: return launch_dense_typed<kF16>(w, k, n, x, bias, y, m, stream, tuning);
+    case kBF16: return launch_dense_typed<kBF16>(w, k, n, x, bias, y, m, stream, tuning);
+    case kQ6_K: return k % 256u == 0u ? launch_dense_typed<kQ6_K>(w, k, n, x, bias, y, m, stream, tuning) : hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
     }
 }

@@ -87,14 +87,15 @@ __device__ __forceinline__ void load_dense_step(const DmArgs& a, std::uint32_t r
         const std::uint64_t blk = static_cast<std::uint64_t>(row) * sbs + s / 4u;
         const unsigned char* rec = a.w + blk * kQ6kRec;
         const std::uint32_t q = s & 3u, h = q >> 1;
+        // Group g's runs of half-quadrant pair (h, h2): low nibbles of
+        // quadrants with j % 2 = 0, then 1, then high pairs (q6k_code_offset).
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-                out.ql[b][h2] = *reinterpret_cast<const std::uint32_t*>(rec + 64u * h + 32u * b + 16u * h2 + 4u * g);
-            }
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) out.qh[h2] = *reinterpret_cast<const std::uint32_t*>(rec + 128u + 32u * h + 16u * h2 + 4u * g);
+        for (int h2 = 0; h2 < 2; ++h2) {
+            const std::uint32_t b = 12u * (2u * h + h2);
+            out.ql[0][h2] = *reinterpret_cast<const std::uint32_t*>(rec + q6k_code_offset(g, b));
+            out.ql[1][h2] = *reinterpret_cast<const std::uint32_t*>(rec + q6k_code_offset(g, b + 4u));
+            out.qh[h2] = *reinterpret_cast<const std::uint32_t*>(rec + q6k_code_offset(g, b + 8u));
+        }
         out.sc = *reinterpret_cast<const std::uint32_t*>(rec + 192u + 8u * h + 4u * (q & 1u));
         const std::uint16_t* dplane = reinterpret_cast<const std::uint16_t*>(a.w + static_cast<std::uint64_t>(a.n) * sbs * kQ6kRec);
         out.d = dplane[blk];

@@ -26,25 +26,6 @@ __device__ __forceinline__ float half_bits_to_float(std::uint32_t bits16) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<std::uint16_t>(bits16)));
 }
 
-__device__ __forceinline__ float lane_value(float v, int src) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
-}
-
-template <int kCtrl>
-__device__ __forceinline__ float dpp_float(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, false));
-}
-
-// Maximum over the 64 lanes: within each 16-lane row by DPP (quad swaps,
-// half-row and row mirrors), then across the four rows by readlane.
-__device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, dpp_float<0xb1>(v));    // quad_perm [1, 0, 3, 2]
-    v = fmaxf(v, dpp_float<0x4e>(v));    // quad_perm [2, 3, 0, 1]
-    v = fmaxf(v, dpp_float<0x141>(v));   // row_half_mirror
-    v = fmaxf(v, dpp_float<0x140>(v));   // row_mirror
-    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
-}
-
 template <int FMT> struct GemvFormat;
 template <> struct GemvFormat<kQ8_0> {
     static constexpr int kBlocksPerTile = 2;

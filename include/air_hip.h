@@ -191,8 +191,10 @@ int air_hip_context_set_wsplit(air_hip_context* ctx, uint32_t mode, uint32_t til
  * otherwise), 1 = the matrix-core kernel at every width, 2 = the FMA
  * kernels.
  * tile_n = 16-row weight tiles per workgroup (1, 2 or 4), waves = waves
- * splitting K (1..8), depth = weight steps per wave ring (2 or 4); 0 keeps
- * the automatic choice.  No counterpart in the reference. */
+ * splitting K (1..8; the one-row Q6_K GEMV 1..16), depth = weight steps per
+ * wave ring (2 or 4); for the one-row Q6_K GEMV tile_n = 2 takes two
+ * super-blocks per work unit and depth 4 / 2 one / two units in flight.  0
+ * keeps the automatic choice.  No counterpart in the reference. */
 int air_hip_context_set_dense_path(air_hip_context* ctx, uint32_t path, uint32_t tile_n, uint32_t waves,
                                    uint32_t depth);
 /* Reads `bytes` (a multiple of 16) of device memory once on the context's
