@@ -110,6 +110,9 @@ struct DecodeTuning {
     std::uint32_t rows_per_wave{0};   // 16-row tiles per wave: 1, 2 or 4
     std::uint32_t waves_per_group{0}; // waves splitting K inside a workgroup
     std::uint32_t k_splits{0};        // workgroups splitting K (fused path)
+    std::uint32_t pair_split{0};      // M = 1 GEMV pair split: 0 automatic, 1 never, 2 always (where it applies)
+    std::uint32_t units_per_chunk{0}; // M = 1 GEMV work units per 16-block chunk: 0 automatic, 1 or 2
+    std::uint32_t depth{0};           // M = 1 GEMV chunk buffers per wave: 0 automatic, 1 or 2
 };
 std::uint64_t split_workspace_bytes(std::uint64_t kp, std::uint32_t m);
 SplitWorkspace carve_split_workspace(void* base, std::uint64_t kp, std::uint32_t m);
@@ -149,10 +152,16 @@ struct GemvShape {
     std::uint32_t waves_per_group{1};
     std::uint32_t depth{2};           // chunk buffers per wave (1 or 2)
     std::uint32_t units_per_chunk{1}; // work units per 16-block chunk (1, or 2 for one-tile waves)
+    // Two workgroups per row tile, each half the work units, meeting through
+    // one 64-bit slot per output row (waves_per_group is per workgroup).
+    std::uint32_t pair_split{0};
 };
+// Rows a pair-split GEMV can address: the slot array holds this many 64-bit
+// words, zero between launches.
+constexpr std::uint64_t kGemvPairSlots = 8192;
 GemvShape plan_decode_gemv(const TilePlanes& planes, const DecodeTuning& tuning);
 hipError_t launch_decode_gemv(const TilePlanes& planes, const float* x, const float* bias, float* y,
-                              const GemvShape& shape, hipStream_t stream);
+                              const GemvShape& shape, std::uint64_t* pair_slots, hipStream_t stream);
 // The M = 1 linear with the step's element-wise neighbours fused in:
 // norm_weight != null RMS-normalises x first (eps); epilogue 0 stores
 // y = W x + b, 1 adds it to y (residual), 2 writes silu(g) * u of a fused
@@ -164,7 +173,8 @@ struct GemvFusion {
 };
 GemvShape plan_decode_gemv_fused(const TilePlanes& planes, const DecodeTuning& tuning, int epilogue);
 hipError_t launch_decode_gemv_fused(const TilePlanes& planes, const float* x, const float* bias, float* y,
-                                    const GemvShape& shape, const GemvFusion& fusion, hipStream_t stream);
+                                    const GemvShape& shape, const GemvFusion& fusion, std::uint64_t* pair_slots,
+                                    hipStream_t stream);
 
 // Prefill linear on f16 MFMA (M = 1..4096; planned for M >= 65).
 struct PrefillTuning {

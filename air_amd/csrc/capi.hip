@@ -34,6 +34,10 @@ using namespace air_hip;
 // hipGetSymbolAddress returns for it (noalloc_scratch below).
 constexpr std::uint64_t kNoAllocScratchBytes = 16ull << 20;
 __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+// The pair-split GEMV's row slots for air_hip_linear_noalloc: zero when the
+// code object is loaded, and every launch leaves them zero (the scratch
+// array's contents are not, so the slots cannot live there).
+__device__ __align__(256) std::uint64_t noalloc_pair_slots[kGemvPairSlots];
 
 struct air_hip_context {
     int device{0};
@@ -94,6 +98,11 @@ struct air_hip_context {
     std::uint64_t epilogue_rows_bytes{0};
     // This device's `scratch` array (hipGetSymbolAddress at context creation).
     void* noalloc_scratch{nullptr};
+    // The pair-split GEMV's row slots: kGemvPairSlots words, zeroed at
+    // context creation and left zero by every launch (noalloc_pairs: the
+    // device's noalloc_pair_slots array, for air_hip_linear_noalloc).
+    std::uint64_t* gemv_pairs{nullptr};
+    std::uint64_t* noalloc_pairs{nullptr};
     // Bumped whenever a context-owned buffer is (re)allocated: launches
     // recorded into a graph use the current buffers while it is unchanged.
     std::uint64_t generation{0};
@@ -216,18 +225,28 @@ int load_activations_for(air_hip_context* ctx, const float* x, std::uint64_t k, 
 // device current (each GPU holds its own copy at its own address).
 std::mutex g_scratch_mutex;
 std::vector<void*> g_scratch_address;
+std::vector<void*> g_pair_slots_address;
 
-int noalloc_scratch(int device, void** out) {
+int noalloc_scratch(int device, void** out, void** pairs_out) {
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
-    if (static_cast<std::size_t>(device) >= g_scratch_address.size()) g_scratch_address.resize(device + 1u, nullptr);
+    if (static_cast<std::size_t>(device) >= g_scratch_address.size()) {
+        g_scratch_address.resize(device + 1u, nullptr);
+        g_pair_slots_address.resize(device + 1u, nullptr);
+    }
     if (!g_scratch_address[device]) {
         void* p = nullptr;
-        const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (err != hipSuccess || !p) return hip_fail(err != hipSuccess ? err : hipErrorInvalidSymbol,
                                                      "hipGetSymbolAddress(scratch)");
+        void* q = nullptr;
+        err = hipGetSymbolAddress(&q, HIP_SYMBOL(noalloc_pair_slots));
+        if (err != hipSuccess || !q) return hip_fail(err != hipSuccess ? err : hipErrorInvalidSymbol,
+                                                     "hipGetSymbolAddress(noalloc_pair_slots)");
         g_scratch_address[device] = p;
+        g_pair_slots_address[device] = q;
     }
     *out = g_scratch_address[device];
+    *pairs_out = g_pair_slots_address[device];
     return AIR_HIP_OK;
 }
 
@@ -605,16 +624,33 @@ int air_hip_context_create(int device, void* stream, air_hip_context** out) {
         return fail(AIR_HIP_UNSUPPORTED, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
     }
     void* scratch_ptr = nullptr;
+    void* noalloc_pairs = nullptr;
+    void* pairs = nullptr;
     {
         DeviceScope scope(device);
         if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-        if (int rc = noalloc_scratch(device, &scratch_ptr); rc != AIR_HIP_OK) return rc;
+        if (int rc = noalloc_scratch(device, &scratch_ptr, &noalloc_pairs); rc != AIR_HIP_OK) return rc;
+        const std::size_t bytes = kGemvPairSlots * sizeof(std::uint64_t);
+        err = hipMalloc(&pairs, bytes);
+        if (err != hipSuccess) return hip_fail(err, "hipMalloc (GEMV pair slots)");
+        err = hipMemset(pairs, 0, bytes);
+        if (err == hipSuccess) err = hipDeviceSynchronize();
+        if (err != hipSuccess) {
+            (void)hipFree(pairs);
+            return hip_fail(err, "hipMemset (GEMV pair slots)");
+        }
     }
     auto* ctx = new (std::nothrow) air_hip_context();
-    if (!ctx) return fail(AIR_HIP_INTERNAL_ERROR, "out of host memory");
+    if (!ctx) {
+        DeviceScope scope(device);
+        (void)hipFree(pairs);
+        return fail(AIR_HIP_INTERNAL_ERROR, "out of host memory");
+    }
     ctx->device = device;
     ctx->stream = static_cast<hipStream_t>(stream);
     ctx->noalloc_scratch = scratch_ptr;
+    ctx->noalloc_pairs = static_cast<std::uint64_t*>(noalloc_pairs);
+    ctx->gemv_pairs = static_cast<std::uint64_t*>(pairs);
     ctx->prefill_tuning.cus = static_cast<std::uint32_t>(prop.multiProcessorCount);
     *out = ctx;
     return AIR_HIP_OK;
@@ -633,6 +669,7 @@ int air_hip_context_destroy(air_hip_context* ctx) {
         if (ctx->attention_scratch) (void)hipFree(ctx->attention_scratch);
         if (ctx->argmax_partials) (void)hipFree(ctx->argmax_partials);
         if (ctx->epilogue_rows) (void)hipFree(ctx->epilogue_rows);
+        if (ctx->gemv_pairs) (void)hipFree(ctx->gemv_pairs);
         for (void* p : ctx->retired) (void)hipFree(p);
     }
     delete ctx;
@@ -736,6 +773,18 @@ int air_hip_context_set_tuning(air_hip_context* ctx, uint32_t rows_per_wave, uin
     ctx->tuning.rows_per_wave = rows_per_wave;
     ctx->tuning.waves_per_group = waves_per_group;
     ctx->tuning.k_splits = k_splits;
+    return AIR_HIP_OK;
+}
+
+int air_hip_context_set_gemv_shape(air_hip_context* ctx, uint32_t pair_mode, uint32_t units_per_chunk,
+                                   uint32_t depth) {
+    if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
+    if (pair_mode > 2u) return fail(AIR_HIP_INVALID_ARGUMENT, "pair_mode must be 0, 1 or 2");
+    if (units_per_chunk > 2u) return fail(AIR_HIP_INVALID_ARGUMENT, "units_per_chunk must be 0, 1 or 2");
+    if (depth > 2u) return fail(AIR_HIP_INVALID_ARGUMENT, "depth must be 0, 1 or 2");
+    ctx->tuning.pair_split = pair_mode;
+    ctx->tuning.units_per_chunk = units_per_chunk;
+    ctx->tuning.depth = depth;
     return AIR_HIP_OK;
 }
 
@@ -983,7 +1032,8 @@ int air_hip_decode_linear_fused(air_hip_context* ctx, const air_hip_matrix* m, c
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
     const GemvShape shape = plan_decode_gemv_fused(m->planes, ctx->tuning, epilogue);
     const hipError_t err = launch_decode_gemv_fused(m->planes, x, bias, y, shape,
-                                                    GemvFusion{norm_weight, eps, epilogue}, ctx->stream);
+                                                    GemvFusion{norm_weight, eps, epilogue}, ctx->gemv_pairs,
+                                                    ctx->stream);
     if (err != hipSuccess) return hip_fail(err, "decode_gemv_kernel (fused)");
     ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
     ctx->decode_rows.fetch_add(1, std::memory_order_relaxed);
@@ -1124,7 +1174,7 @@ int linear_rows(air_hip_context* ctx, const air_hip_matrix* m, const float* x, f
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
     if (route == Route::gemv) {
         const GemvShape gshape = plan_decode_gemv(m->planes, ctx->tuning);
-        const hipError_t gerr = launch_decode_gemv(m->planes, x, bias, y, gshape, ctx->stream);
+        const hipError_t gerr = launch_decode_gemv(m->planes, x, bias, y, gshape, ctx->gemv_pairs, ctx->stream);
         if (gerr != hipSuccess) return hip_fail(gerr, "decode_gemv_kernel");
         ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
         ctx->decode_rows.fetch_add(1, std::memory_order_relaxed);
@@ -1205,8 +1255,9 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
     case Route::gemv: {
         const GemvShape g = plan_decode_gemv(m->planes, ctx->tuning);
         std::snprintf(buf, sizeof buf, "decode_gemv_kernel<%s> rows_per_wave=%u depth=%u units_per_chunk=%u "
-                      "waves=%u groups=%u", fmt, g.rows_per_wave, g.depth, g.units_per_chunk, g.waves_per_group,
-                      static_cast<unsigned>(ceil_div(m->planes.nt, g.rows_per_wave)));
+                      "waves=%u groups=%u%s", fmt, g.rows_per_wave, g.depth, g.units_per_chunk, g.waves_per_group,
+                      static_cast<unsigned>(ceil_div(m->planes.nt, g.rows_per_wave)),
+                      g.pair_split ? " pair_split" : "");
         break;
     }
     case Route::fused: {
@@ -1320,7 +1371,7 @@ int air_hip_linear_noalloc(air_hip_context* ctx, const air_hip_matrix* m, const 
     hipError_t err = hipSuccess;
     switch (route) {
     case Route::gemv:
-        err = launch_decode_gemv(p, x, bias, y, plan_decode_gemv(p, ctx->tuning), ctx->stream);
+        err = launch_decode_gemv(p, x, bias, y, plan_decode_gemv(p, ctx->tuning), ctx->noalloc_pairs, ctx->stream);
         break;
     case Route::fused:
         err = launch_decode_fused(p, x, bias, y, rows, plan_decode_fused(p, rows, ctx->tuning), nullptr, nullptr,

@@ -376,12 +376,23 @@ __device__ __forceinline__ double square_sum4(double acc, float4 v) {
 //   EPI = 2  SwiGLU over a fused gate|up matrix (N = 2F): the workgroup
 //            owns gate tile t (waves [0, W/2)) and up tile t + NT/2 (waves
 //            [W/2, W)) and writes y[n] = silu(g[n] + b[n]) * (u[n] + b[F + n]).
+//
+// Pair split (pair_slots != null; R = 1, EPI 0 or 1): two workgroups share a
+// row tile, workgroup 2t + h taking half h of its work units, so a narrow
+// grid (224 row tiles on 256 CUs) spreads over twice the workgroups.  Each
+// half deposits its row sums with one 64-bit atomic exchange per row of
+// (float bits << 32 | 1 + h) into pair_slots[n]; the half that finds its
+// partner's word there adds the two, writes y and puts the slot back to
+// zero.  Value and flag travel in the same atomic word, so no fence is
+// needed, and IEEE addition is commutative, so y is the same whichever half
+// arrives second.  The slots start at zero and every launch leaves them so;
+// launches on one slot array must not overlap.
 template <int FMT, int R, int P, int U, bool NORM, int EPI>
 __global__ void __launch_bounds__(64 * gemv_max_waves(R, P))
 decode_gemv_kernel(const void* __restrict__ codes_, const void* __restrict__ scales_,
                    const float* __restrict__ x, const float* __restrict__ bias, float* __restrict__ y,
                    std::uint64_t K, std::uint64_t N, std::uint32_t NT, std::uint32_t KT,
-                   const float* __restrict__ norm_w, double eps) {
+                   const float* __restrict__ norm_w, double eps, std::uint64_t* __restrict__ pair_slots) {
     extern __shared__ float wave_sums[];
     using Ch = Chunk<FMT, R, U, NORM>;
     const std::uint32_t lane = threadIdx.x & 63u;
@@ -391,13 +402,19 @@ decode_gemv_kernel(const void* __restrict__ codes_, const void* __restrict__ sca
     const std::uint32_t group_waves = EPI == 2 ? W / 2u : W;       // waves per row tile
     const bool up_half = EPI == 2 && wave >= group_waves;
     const std::uint32_t gw = up_half ? wave - group_waves : wave;
-    const std::uint32_t rt0 = EPI == 2 ? blockIdx.x + (up_half ? NT / 2u : 0u) : blockIdx.x * R;
+    const bool pair = EPI != 2 && R == 1 && pair_slots != nullptr;
+    const std::uint32_t half = pair ? (blockIdx.x & 1u) : 0u;
+    const std::uint32_t group = pair ? (blockIdx.x >> 1) : blockIdx.x;
+    const std::uint32_t rt0 = EPI == 2 ? group + (up_half ? NT / 2u : 0u) : group * R;
     const std::uint64_t nblocks = K / 32u;
-    // Work units of Ch::kTiles k tiles (U per 16-block chunk), split over the waves.
+    // Work units of Ch::kTiles k tiles (U per 16-block chunk), split over the
+    // waves of the row tile (of both workgroups of a pair).
     const std::uint32_t chunks = static_cast<std::uint32_t>(ceil_div(KT, static_cast<std::uint64_t>(Ch::kTiles) * U));
     const std::uint64_t units = static_cast<std::uint64_t>(chunks) * U;
-    const std::uint32_t c_begin = static_cast<std::uint32_t>((units * gw) / group_waves);
-    const std::uint32_t c_end = static_cast<std::uint32_t>((units * (gw + 1u)) / group_waves);
+    const std::uint32_t tile_waves = pair ? 2u * group_waves : group_waves;
+    const std::uint32_t vw = half * group_waves + gw;
+    const std::uint32_t c_begin = static_cast<std::uint32_t>((units * vw) / tile_waves);
+    const std::uint32_t c_end = static_cast<std::uint32_t>((units * (vw + 1u)) / tile_waves);
 
     float4v acc[R];
 #pragma unroll
@@ -474,7 +491,7 @@ decode_gemv_kernel(const void* __restrict__ codes_, const void* __restrict__ sca
     if (wave != 0u || lane >= 16u) return;
     if constexpr (EPI == 2) {
         const std::uint64_t F = N / 2u;
-        const std::uint64_t n = static_cast<std::uint64_t>(blockIdx.x) * 16u + lane;
+        const std::uint64_t n = static_cast<std::uint64_t>(group) * 16u + lane;
         if (n < F) {
             const float g = total[0] + (bias ? bias[n] : 0.0f);
             const float u = up_total + (bias ? bias[F + n] : 0.0f);
@@ -485,7 +502,17 @@ decode_gemv_kernel(const void* __restrict__ codes_, const void* __restrict__ sca
         for (int r = 0; r < R; ++r) {
             const std::uint64_t n = static_cast<std::uint64_t>(rt0 + r) * 16u + lane;
             if ((rt0 + r) >= NT || n >= N) continue;
-            const float out = total[r] + (bias ? bias[n] : 0.0f);
+            float sum = total[r];
+            if (pair) {
+                const std::uint64_t mine =
+                    (static_cast<std::uint64_t>(__float_as_uint(sum)) << 32) | static_cast<std::uint64_t>(1u + half);
+                const std::uint64_t other =
+                    __hip_atomic_exchange(pair_slots + n, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (other == 0u) continue;   // the partner finishes the row
+                __hip_atomic_store(pair_slots + n, std::uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                sum = sum + __uint_as_float(static_cast<std::uint32_t>(other >> 32));
+            }
+            const float out = sum + (bias ? bias[n] : 0.0f);
             if constexpr (EPI == 1) {
                 y[n] = y[n] + out;
             } else {
@@ -497,49 +524,52 @@ decode_gemv_kernel(const void* __restrict__ codes_, const void* __restrict__ sca
 
 template <int FMT, int R, int P, int U, bool NORM, int EPI>
 hipError_t launch_gemv_variant(const TilePlanes& p, const float* x, const float* bias, float* y,
-                               std::uint32_t W, const GemvFusion& f, hipStream_t stream) {
+                               std::uint32_t W, const GemvFusion& f, std::uint64_t* pair_slots, hipStream_t stream) {
     if (W == 0u || W > static_cast<std::uint32_t>(gemv_max_waves(R, P))) return hipErrorInvalidConfiguration;
     if (EPI == 2 && (W % 2u != 0u || p.nt % 2u != 0u)) return hipErrorInvalidConfiguration;
+    if (pair_slots && (EPI == 2 || R != 1 || p.n > kGemvPairSlots)) return hipErrorInvalidConfiguration;
     const unsigned groups = EPI == 2 ? p.nt / 2u : static_cast<unsigned>(ceil_div(p.nt, R));
     const std::size_t lds = static_cast<std::size_t>(W - 1u) * R * 16u * sizeof(float);
-    decode_gemv_kernel<FMT, R, P, U, NORM, EPI><<<dim3(groups), 64u * W, lds, stream>>>(
-        p.codes, p.scales, x, bias, y, p.k, p.n, p.nt, p.kt, f.norm_weight, f.eps);
+    decode_gemv_kernel<FMT, R, P, U, NORM, EPI><<<dim3(pair_slots ? 2u * groups : groups), 64u * W, lds, stream>>>(
+        p.codes, p.scales, x, bias, y, p.k, p.n, p.nt, p.kt, f.norm_weight, f.eps, pair_slots);
     return hipGetLastError();
 }
 
 // One row tile per wave (the fused step variants).
 template <int FMT, bool NORM, int EPI>
 hipError_t launch_gemv_r1(const TilePlanes& p, const float* x, const float* bias, float* y, const GemvShape& g,
-                          const GemvFusion& f, hipStream_t s) {
+                          const GemvFusion& f, std::uint64_t* pairs, hipStream_t s) {
     const std::uint32_t W = g.waves_per_group, P = g.depth;
     if (g.units_per_chunk == 2u) {
-        return P == 1u ? launch_gemv_variant<FMT, 1, 1, 2, NORM, EPI>(p, x, bias, y, W, f, s)
-                       : launch_gemv_variant<FMT, 1, 2, 2, NORM, EPI>(p, x, bias, y, W, f, s);
+        return P == 1u ? launch_gemv_variant<FMT, 1, 1, 2, NORM, EPI>(p, x, bias, y, W, f, pairs, s)
+                       : launch_gemv_variant<FMT, 1, 2, 2, NORM, EPI>(p, x, bias, y, W, f, pairs, s);
     }
-    return P == 1u ? launch_gemv_variant<FMT, 1, 1, 1, NORM, EPI>(p, x, bias, y, W, f, s)
-                   : launch_gemv_variant<FMT, 1, 2, 1, NORM, EPI>(p, x, bias, y, W, f, s);
+    return P == 1u ? launch_gemv_variant<FMT, 1, 1, 1, NORM, EPI>(p, x, bias, y, W, f, pairs, s)
+                   : launch_gemv_variant<FMT, 1, 2, 1, NORM, EPI>(p, x, bias, y, W, f, pairs, s);
 }
 
 template <int FMT>
 hipError_t launch_gemv_fmt(const TilePlanes& p, const float* x, const float* bias, float* y, const GemvShape& g,
-                           const GemvFusion& f, hipStream_t s) {
+                           const GemvFusion& f, std::uint64_t* pair_slots, hipStream_t s) {
     const bool norm = f.norm_weight != nullptr;
+    std::uint64_t* pairs = g.pair_split ? pair_slots : nullptr;
+    if (g.pair_split && !pairs) return hipErrorInvalidValue;
     if (norm || f.epilogue != 0) {
         if (g.rows_per_wave != 1u) return hipErrorInvalidConfiguration;
-        if (!norm && f.epilogue == 1) return launch_gemv_r1<FMT, false, 1>(p, x, bias, y, g, f, s);
-        if (!norm && f.epilogue == 2) return launch_gemv_r1<FMT, false, 2>(p, x, bias, y, g, f, s);
-        if (norm && f.epilogue == 0) return launch_gemv_r1<FMT, true, 0>(p, x, bias, y, g, f, s);
-        if (norm && f.epilogue == 2) return launch_gemv_r1<FMT, true, 2>(p, x, bias, y, g, f, s);
+        if (!norm && f.epilogue == 1) return launch_gemv_r1<FMT, false, 1>(p, x, bias, y, g, f, pairs, s);
+        if (!norm && f.epilogue == 2) return launch_gemv_r1<FMT, false, 2>(p, x, bias, y, g, f, pairs, s);
+        if (norm && f.epilogue == 0) return launch_gemv_r1<FMT, true, 0>(p, x, bias, y, g, f, pairs, s);
+        if (norm && f.epilogue == 2) return launch_gemv_r1<FMT, true, 2>(p, x, bias, y, g, f, pairs, s);
         return hipErrorInvalidValue;
     }
     const std::uint32_t R = g.rows_per_wave, W = g.waves_per_group, P = g.depth;
-    if (R == 1u) return launch_gemv_r1<FMT, false, 0>(p, x, bias, y, g, f, s);
+    if (R == 1u) return launch_gemv_r1<FMT, false, 0>(p, x, bias, y, g, f, pairs, s);
     if (R == 2u) {
-        return P == 1u ? launch_gemv_variant<FMT, 2, 1, 1, false, 0>(p, x, bias, y, W, f, s)
-                       : launch_gemv_variant<FMT, 2, 2, 1, false, 0>(p, x, bias, y, W, f, s);
+        return P == 1u ? launch_gemv_variant<FMT, 2, 1, 1, false, 0>(p, x, bias, y, W, f, pairs, s)
+                       : launch_gemv_variant<FMT, 2, 2, 1, false, 0>(p, x, bias, y, W, f, pairs, s);
     }
-    return P == 1u ? launch_gemv_variant<FMT, 4, 1, 1, false, 0>(p, x, bias, y, W, f, s)
-                   : launch_gemv_variant<FMT, 4, 2, 1, false, 0>(p, x, bias, y, W, f, s);
+    return P == 1u ? launch_gemv_variant<FMT, 4, 1, 1, false, 0>(p, x, bias, y, W, f, pairs, s)
+                   : launch_gemv_variant<FMT, 4, 2, 1, false, 0>(p, x, bias, y, W, f, pairs, s);
 }
 
 } // namespace
@@ -571,6 +601,11 @@ GemvShape plan_decode_gemv(const TilePlanes& p, const DecodeTuning& tuning) {
     const bool wide = groups >= 2048u;
     const bool short_k = chunks <= 8u;
     g.units_per_chunk = (p.type == kQ8_0 && g.rows_per_wave == 1u && short_k && !huge) ? 2u : 1u;
+    // Half-chunk units exist for Q8_0 only (a 4-bit chunk's tiles do not
+    // split in two): the override asks for them there alone.
+    if (g.rows_per_wave == 1u && (tuning.units_per_chunk == 1u || (tuning.units_per_chunk == 2u && p.type == kQ8_0))) {
+        g.units_per_chunk = tuning.units_per_chunk;
+    }
     const std::uint64_t units = static_cast<std::uint64_t>(chunks) * g.units_per_chunk;
     std::uint64_t w;
     if (huge) {
@@ -605,13 +640,34 @@ GemvShape plan_decode_gemv(const TilePlanes& p, const DecodeTuning& tuning) {
         w = wanted > 16u ? 16u : wanted;
         depth = 1u;
     }
+    // A grid just past one workgroup per CU (q|k|v: 288 row tiles on 256
+    // CUs) ends in a round of few workgroups: split each tile's units over a
+    // pair of workgroups with half the waves each.
+    const bool pair_fits = g.rows_per_wave == 1u && p.n <= kGemvPairSlots && units >= 2u;
+    bool pair = pair_fits && groups > 256u && groups <= 320u;
+    if (tuning.pair_split == 1u) pair = false;
+    if (tuning.pair_split == 2u) pair = pair_fits;
+    if (pair && tuning.waves_per_group == 0u) {
+        w = (w + 1u) / 2u;
+        depth = depth_for(2u * w);
+    }
+    if (tuning.depth == 1u || tuning.depth == 2u) depth = tuning.depth;
+    {
+        const std::uint64_t cap = static_cast<std::uint64_t>(gemv_max_waves(static_cast<int>(g.rows_per_wave),
+                                                                            static_cast<int>(depth)));
+        if (w > cap) w = cap;
+    }
     g.waves_per_group = static_cast<std::uint32_t>(w);
     g.depth = depth;
+    g.pair_split = pair ? 1u : 0u;
     return g;
 }
 
 GemvShape plan_decode_gemv_fused(const TilePlanes& p, const DecodeTuning& tuning, int epilogue) {
-    GemvShape g = plan_decode_gemv(p, tuning);
+    // The SwiGLU workgroup holds a gate tile and its up tile: no pair split.
+    DecodeTuning t = tuning;
+    if (epilogue == 2) t.pair_split = 1u;
+    GemvShape g = plan_decode_gemv(p, t);
     g.rows_per_wave = 1u;
     if (g.units_per_chunk == 2u && p.type != kQ8_0) g.units_per_chunk = 1u;
     if (epilogue == 2) {
@@ -626,16 +682,17 @@ GemvShape plan_decode_gemv_fused(const TilePlanes& p, const DecodeTuning& tuning
 }
 
 hipError_t launch_decode_gemv(const TilePlanes& p, const float* x, const float* bias, float* y,
-                              const GemvShape& g, hipStream_t stream) {
-    return launch_decode_gemv_fused(p, x, bias, y, g, GemvFusion{}, stream);
+                              const GemvShape& g, std::uint64_t* pair_slots, hipStream_t stream) {
+    return launch_decode_gemv_fused(p, x, bias, y, g, GemvFusion{}, pair_slots, stream);
 }
 
 hipError_t launch_decode_gemv_fused(const TilePlanes& p, const float* x, const float* bias, float* y,
-                                    const GemvShape& g, const GemvFusion& f, hipStream_t stream) {
+                                    const GemvShape& g, const GemvFusion& f, std::uint64_t* pair_slots,
+                                    hipStream_t stream) {
     switch (p.type) {
-    case kQ8_0: return launch_gemv_fmt<kQ8_0>(p, x, bias, y, g, f, stream);
-    case kQ4_0: return launch_gemv_fmt<kQ4_0>(p, x, bias, y, g, f, stream);
-    case kQ4_K: return launch_gemv_fmt<kQ4_K>(p, x, bias, y, g, f, stream);
+    case kQ8_0: return launch_gemv_fmt<kQ8_0>(p, x, bias, y, g, f, pair_slots, stream);
+    case kQ4_0: return launch_gemv_fmt<kQ4_0>(p, x, bias, y, g, f, pair_slots, stream);
+    case kQ4_K: return launch_gemv_fmt<kQ4_K>(p, x, bias, y, g, f, pair_slots, stream);
     default: return hipErrorInvalidValue;
     }
 }

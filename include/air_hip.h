@@ -157,6 +157,17 @@ int air_hip_context_stats(const air_hip_context* ctx, air_hip_stats* out);
  * clamped to its maximum. */
 int air_hip_context_set_tuning(air_hip_context* ctx, uint32_t rows_per_wave, uint32_t waves_per_group,
                                uint32_t k_splits);
+/* One-row decode GEMV launch shape (autotuning; 0 keeps the automatic
+ * choice).  pair_mode 1 = one workgroup per 16-row tile, 2 = two wherever
+ * it applies (at most 8192 output rows, not the fused gate|up SwiGLU): each
+ * takes half the tile's K and they combine through a per-row 64-bit slot
+ * that the context zeroes at creation and every launch leaves zero, so
+ * launches of one context must not overlap in time.  units_per_chunk =
+ * work units per 512-weight chunk (1, or 2 for Q8_0; other formats keep 1),
+ * depth = chunk buffers per wave (1 or 2).  Same kernels as specialized_matvec_kernel's replacement
+ * (src/cuda/cuda_backend.cu:585-606). */
+int air_hip_context_set_gemv_shape(air_hip_context* ctx, uint32_t pair_mode, uint32_t units_per_chunk,
+                                   uint32_t depth);
 /* Chooses the decode kernel for 2..64 rows (autotuning): path 0 = automatic
  * (the skinny kernel: activations split once into the workspace and staged
  * through LDS, every weight read once, K split over workgroups when the

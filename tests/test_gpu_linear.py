@@ -166,6 +166,89 @@ def test_linear_k_split_shapes_agree(torch_cuda, hip_ctx, type_id, k, n):
         mat.release()
 
 
+@pytest.mark.parametrize("type_id,k,n", [(capi.TYPE_Q8_0, 18944, 3584), (capi.TYPE_Q8_0, 4096, 1000),
+                                         (capi.TYPE_Q4_0, 2048, 777), (capi.TYPE_Q4_K, 3584, 512),
+                                         (capi.TYPE_Q8_0, 3584, 8192)])
+def test_gemv_pair_split(torch_cuda, hip_ctx, type_id, k, n):
+    """The one-row GEMV with two workgroups per row tile (their halves meet
+    through one 64-bit slot per output row): the oracle's result with and
+    without bias and at every wave count, the same bits on every repeat and
+    after a launch on another shape (the slots return to zero), and the
+    residual epilogue bit-exact against the linear plus the add."""
+    torch = torch_cuda
+    lib = capi.lib()
+    canon = helpers.weights(type_id, k, n, seed=k + 3 * n + type_id)
+    mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    small_canon = helpers.weights(capi.TYPE_Q8_0, 1024, 48, seed=5)
+    small = capi.Matrix(hip_ctx, capi.TYPE_Q8_0, 1024, 48, small_canon, small_canon.nbytes, on_device=False)
+    try:
+        x = helpers.activations(1, k, seed=k + 29)
+        xd = _dev(torch, x)
+        bias = helpers.activations(1, n, seed=n + 31)[0] * 0.05
+        bias_d = _dev(torch, bias)
+        xs = _dev(torch, helpers.activations(1, 1024, seed=6))
+        ys = torch.empty((1, 48), dtype=torch.float32, device="cuda:0")
+        for b, bd in ((None, None), (bias, bias_d)):
+            want = oracle.linear(type_id, canon, k, n, x, bias=b)
+            for mode in (1, 2):
+                hip_ctx.set_gemv_shape(mode)
+                assert ("pair_split" in mat.plan(1)) == (mode == 2), mat.plan(1)
+                for waves in (0, 1, 3, 8):
+                    hip_ctx.set_tuning(0, waves, 0)
+                    outs = []
+                    for _ in range(3):
+                        y = torch.full((1, n), float("nan"), dtype=torch.float32, device="cuda:0")
+                        mat.linear(xd, y, 1, bias=bd)
+                        small.linear(xs, ys, 1)
+                        torch.cuda.synchronize()
+                        outs.append(y.cpu().numpy())
+                    assert helpers.rel_l2(outs[0], want) <= DECODE_TOL, (mode, waves, b is None)
+                    assert all(np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)) for o in outs[1:])
+        # the residual epilogue on the paired launch
+        hip_ctx.set_tuning(0, 0, 0)
+        hip_ctx.set_gemv_shape(2)
+        resid = _dev(torch, helpers.activations(1, n, seed=n + 37))
+        lin = torch.empty((1, n), dtype=torch.float32, device="cuda:0")
+        mat.linear(xd, lin, 1, bias=bias_d)
+        want = (resid + lin).cpu().numpy()
+        capi.check(lib.air_hip_decode_linear_fused(hip_ctx.handle, mat.handle, xd.data_ptr(), resid.data_ptr(),
+                                                   bias_d.data_ptr(), None, 0.0, capi.EPILOGUE_RESIDUAL))
+        torch.cuda.synchronize()
+        assert np.array_equal(resid.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    finally:
+        hip_ctx.set_tuning(0, 0, 0)
+        hip_ctx.set_gemv_shape(0)
+        small.release()
+        mat.release()
+
+
+def test_gemv_pair_split_limits(torch_cuda, hip_ctx):
+    """Past 8192 output rows (the slot array) and on wide grids the GEMV
+    keeps one workgroup per row tile; half-chunk work units stay Q8_0's (a
+    4-bit chunk does not split); bad values are refused."""
+    k, n = 1024, 8208
+    canon = helpers.weights(capi.TYPE_Q8_0, k, n, seed=8)
+    wide = capi.Matrix(hip_ctx, capi.TYPE_Q8_0, k, n, canon, canon.nbytes, on_device=False)
+    canon4 = helpers.weights(capi.TYPE_Q4_0, k, 512, seed=9)
+    q4 = capi.Matrix(hip_ctx, capi.TYPE_Q4_0, k, 512, canon4, canon4.nbytes, on_device=False)
+    lib = capi.lib()
+    try:
+        hip_ctx.set_gemv_shape(2)
+        assert "pair_split" not in wide.plan(1)
+        hip_ctx.set_gemv_shape(0)
+        assert "pair_split" not in wide.plan(1)
+        hip_ctx.set_gemv_shape(1, 2, 0)
+        assert "units_per_chunk=1" in q4.plan(1), q4.plan(1)
+        assert "units_per_chunk=2" in wide.plan(1), wide.plan(1)
+        assert lib.air_hip_context_set_gemv_shape(hip_ctx.handle, 3, 0, 0) == 1
+        assert lib.air_hip_context_set_gemv_shape(hip_ctx.handle, 0, 3, 0) == 1
+        assert lib.air_hip_context_set_gemv_shape(hip_ctx.handle, 0, 0, 3) == 1
+    finally:
+        hip_ctx.set_gemv_shape(0)
+        q4.release()
+        wide.release()
+
+
 @pytest.mark.parametrize("type_id,k,n", [(capi.TYPE_Q8_0, 3584, 200), (capi.TYPE_Q4_0, 1152, 333),
                                          (capi.TYPE_Q4_K, 2304, 96), (capi.TYPE_Q8_0, 18944, 64)])
 def test_skinny_shapes_agree(torch_cuda, hip_ctx, type_id, k, n):
@@ -404,6 +487,10 @@ def test_decode_linear_fused_matches_separate_kernels(torch_cuda, hip_ctx, type_
         # the gate|up linear and SwiGLU without the norm (1e-6: a workgroup
         # of twice the waves may split K over the waves differently; bit-exact
         # where the halves get the plain plan's wave count)
+        # (the SwiGLU workgroup never pairs: the reference linear neither)
+        hip_ctx.set_gemv_shape(1)
+        mat.linear(x, lin, 1, bias=bias)
+        hip_ctx.set_gemv_shape(0)
         act_ref = torch.empty((1, f), dtype=torch.float32, device="cuda:0")
         capi.check(lib.air_hip_silu_mul(hip_ctx.handle, lin.data_ptr(), act_ref.data_ptr(), 1, f))
         act = torch.full((1, f), float("nan"), dtype=torch.float32, device="cuda:0")
@@ -421,6 +508,7 @@ def test_decode_linear_fused_matches_separate_kernels(torch_cuda, hip_ctx, type_
         assert lib.air_hip_decode_linear_fused(hip_ctx.handle, mat.handle, x.data_ptr(), x.data_ptr(), None,
                                                None, 0.0, capi.EPILOGUE_STORE) == 1
     finally:
+        hip_ctx.set_gemv_shape(0)
         mat.release()
 
 
