@@ -126,6 +126,7 @@ SIGNATURES = {
     "air_hip_context_stats": (_I, [_P, ctypes.POINTER(Stats)]),
     "air_hip_context_set_tuning": (_I, [_P, _U32, _U32, _U32]),
     "air_hip_context_set_gemv_shape": (_I, [_P, _U32, _U32, _U32]),
+    "air_hip_context_set_split_chain": (_I, [_P, _U32]),
     "air_hip_context_set_prefill_tuning": (_I, [_P, _U32, _U32, _U32, _U32]),
     "air_hip_context_set_decode_path": (_I, [_P, _U32, _U32, _U32]),
     "air_hip_context_set_wsplit": (_I, [_P, _U32, _U32, _U32, _U32, _U32, _U32]),
@@ -244,6 +245,11 @@ class Context:
 
     def set_tuning(self, rows_per_wave: int = 0, waves_per_group: int = 0, k_splits: int = 0) -> None:
         check(lib().air_hip_context_set_tuning(self.handle, rows_per_wave, waves_per_group, k_splits))
+
+    def set_split_chain(self, mode: int = 0) -> None:
+        """K splits of the 2..64-row kernels: 0 automatic, 1 reduction launch,
+        2 summed in the kernel."""
+        check(lib().air_hip_context_set_split_chain(self.handle, mode))
 
     def set_gemv_shape(self, pair_mode: int = 0, units_per_chunk: int = 0, depth: int = 0) -> None:
         """One-row GEMV: pair split (0 automatic, 1 never, 2 wherever it

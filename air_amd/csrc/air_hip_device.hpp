@@ -196,4 +196,28 @@ __device__ __forceinline__ void emit_split_run(std::uint64_t r, const float (&v)
     if (g == 0u) block_sums[b * mp + m] = sum;
 }
 
+// K-split partials combined without a reduction launch.  Element e of split
+// `split` joins the left-deep chain ((0 + p0) + p1) + ... + p(splits-1) --
+// the split-order sum a reduction launch computes -- through the 64-bit
+// words slots[i * elems + e], i = 0 .. splits - 2, which are zero between
+// launches.  Slot i joins the chain of splits 0..i with p(i+1): each side
+// exchanges (float bits << 32 | 1) into it; the one that finds the other's
+// word adds the two (IEEE addition is commutative, so the bits do not depend
+// on the order of arrival), clears the slot and carries the sum on to slot
+// i + 1.  The value and its flag travel in one atomic word, so no fence is
+// needed.  Returns true for the caller left holding the whole chain in v.
+__device__ __forceinline__ bool chain_combine(std::uint64_t* slots, std::uint64_t elems, std::uint64_t e,
+                                              std::uint32_t split, std::uint32_t splits, float& v) {
+    if (split == 0u) v = 0.0f + v;
+    for (std::uint32_t i = split == 0u ? 0u : split - 1u; i + 1u < splits; ++i) {
+        std::uint64_t* slot = slots + static_cast<std::uint64_t>(i) * elems + e;
+        const std::uint64_t mine = (static_cast<std::uint64_t>(__float_as_uint(v)) << 32) | 1u;
+        const std::uint64_t other = __hip_atomic_exchange(slot, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (other == 0u) return false;
+        __hip_atomic_store(slot, std::uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        v = v + __uint_as_float(static_cast<std::uint32_t>(other >> 32));
+    }
+    return true;
+}
+
 } // namespace air_hip

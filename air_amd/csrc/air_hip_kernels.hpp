@@ -247,16 +247,23 @@ SkinnyShape plan_skinny(const TilePlanes& planes, std::uint32_t m, std::uint32_t
                         std::uint32_t lds_stages = 0);
 std::uint64_t skinny_partials_bytes(const SkinnyShape& shape, std::uint32_t m, std::uint64_t n);
 // With `epilogue` (only when shape.splits > 1 and split_epilogue_fits), the
-// split reduction applies it and y is not written.
+// split reduction applies it and y is not written.  Without one, a non-null
+// `chain` (chain_slot_bytes(shape.splits, m, n) of slots, zero between
+// launches) combines a K split inside the kernel instead of a reduction
+// launch, with the reduction's bits.
 hipError_t launch_skinny_linear(const TilePlanes& planes, const SplitWorkspace& ws, const float* bias, float* y,
                                 std::uint32_t m, const SkinnyShape& shape, float* partials, hipStream_t stream,
-                                const SplitEpilogue* epilogue = nullptr);
+                                const SplitEpilogue* epilogue = nullptr, std::uint64_t* chain = nullptr);
 // The same linear straight from f32 activations x [m][k]: each workgroup
 // splits the activations it stages (one power-of-two scale per (row,
 // 32-block)), so no split launch and no activation workspace.
 hipError_t launch_skinny_linear_x(const TilePlanes& planes, const float* x, const float* bias, float* y,
                                   std::uint32_t m, const SkinnyShape& shape, float* partials, hipStream_t stream,
-                                  const SplitEpilogue* epilogue = nullptr);
+                                  const SplitEpilogue* epilogue = nullptr, std::uint64_t* chain = nullptr);
+// Bytes of the in-kernel K-split chain's slots: splits - 1 words per output.
+constexpr std::uint64_t chain_slot_bytes(std::uint32_t splits, std::uint32_t m, std::uint64_t n) {
+    return splits > 1u ? static_cast<std::uint64_t>(splits - 1u) * m * n * 8u : 0u;
+}
 
 // Decode linear (M = 2..64) with K split over the waves of a workgroup
 // (linear_wsplit.hip): TN weight tiles per workgroup, every activation row,
@@ -290,7 +297,8 @@ std::uint64_t wsplit_partials_bytes(const WsplitShape& shape, std::uint32_t m, s
 // row-scaled split in ws (split_rows_kernel's layout).
 hipError_t launch_wsplit_linear(const TilePlanes& planes, const float* x, const SplitWorkspace* ws, const float* bias,
                                 float* y, std::uint32_t m, const WsplitShape& shape, float* partials,
-                                hipStream_t stream, const SplitEpilogue* epilogue = nullptr);
+                                hipStream_t stream, const SplitEpilogue* epilogue = nullptr,
+                                std::uint64_t* chain = nullptr);
 
 // ---- the Qwen2 step around the linears ----------------------------------
 

@@ -103,6 +103,13 @@ struct air_hip_context {
     // device's noalloc_pair_slots array, for air_hip_linear_noalloc).
     std::uint64_t* gemv_pairs{nullptr};
     std::uint64_t* noalloc_pairs{nullptr};
+    // Slots of the in-kernel K-split chain (chain_combine) of the skinny and
+    // wave-split kernels, zeroed when allocated and left zero by every
+    // launch; chain_mode 0 = automatic, 1 = reduction launches, 2 = chain
+    // for every split.
+    std::uint64_t* chain_slots{nullptr};
+    std::uint64_t chain_slots_bytes{0};
+    std::uint32_t chain_mode{0};
     // Bumped whenever a context-owned buffer is (re)allocated: launches
     // recorded into a graph use the current buffers while it is unchanged.
     std::uint64_t generation{0};
@@ -313,6 +320,7 @@ int run_prefill(air_hip_context* ctx, const air_hip_matrix* m, const float* x, f
 }
 
 int ensure_split_buffers(air_hip_context* ctx, std::uint64_t partial_bytes, std::uint32_t counters);
+std::uint64_t* chain_for(air_hip_context* ctx, std::uint32_t splits, std::uint32_t m, std::uint64_t n);
 int linear_loaded(air_hip_context* ctx, const air_hip_matrix* m, float* y, const float* bias, int tactic,
                   const SplitEpilogue* epilogue, bool* applied);
 
@@ -405,8 +413,9 @@ int run_skinny_x(air_hip_context* ctx, const air_hip_matrix* m, const float* x, 
         if (rc != AIR_HIP_OK) return rc;
     }
     const SplitEpilogue* epi = reduction_epilogue(ctx, m, shape, bias, rows, epilogue, applied);
+    std::uint64_t* chain = epi ? nullptr : chain_for(ctx, shape.splits, rows, m->planes.n);
     const hipError_t err = launch_skinny_linear_x(m->planes, x, bias, y, rows, shape,
-                                                  static_cast<float*>(ctx->split_partials), ctx->stream, epi);
+                                                  static_cast<float*>(ctx->split_partials), ctx->stream, epi, chain);
     if (err != hipSuccess) return hip_fail(err, "skinny_kernel");
     ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
     ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
@@ -438,12 +447,51 @@ int run_wsplit(air_hip_context* ctx, const air_hip_matrix* m, const float* x, fl
         *applied = true;
         epi = epilogue;
     }
+    std::uint64_t* chain = epi ? nullptr : chain_for(ctx, shape.splits, rows, m->planes.n);
     const hipError_t err = launch_wsplit_linear(m->planes, x, shape.split_x ? &ws : nullptr, bias, y, rows, shape,
-                                                static_cast<float*>(ctx->split_partials), ctx->stream, epi);
+                                                static_cast<float*>(ctx->split_partials), ctx->stream, epi, chain);
     if (err != hipSuccess) return hip_fail(err, "wsplit_kernel");
     ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
     ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
     return AIR_HIP_OK;
+}
+
+// Whether the automatic mode sums a K split in the kernel.  Measured per
+// linear on the Qwen2-7B shapes (graph replay, all three formats): a 2-way
+// split gains 0.2-1.2 us over the reduction launch up to about 230k outputs
+// (o at 64 rows) and loses 9 us on gate|up at 32 rows (1.2M outputs); every
+// further split adds a level of exchanges that an output passes in turn, so
+// 8-way splits gain only at about 50k outputs (down at 2 rows) and lose 3-42
+// us beyond.
+bool chain_auto(std::uint32_t splits, std::uint32_t m, std::uint64_t n) {
+    const std::uint64_t outputs = static_cast<std::uint64_t>(m) * n;
+    return (splits == 2u && outputs <= (256u << 10)) || outputs * (splits - 1u) <= (56u << 10);
+}
+
+// The chain slots for a K split of `splits` over m x n outputs, or null for
+// the reduction launch: the mode asks for it, or the slots would have to grow
+// (and be zeroed) while the stream is being captured.
+std::uint64_t* chain_for(air_hip_context* ctx, std::uint32_t splits, std::uint32_t m, std::uint64_t n) {
+    if (splits < 2u || ctx->chain_mode == 1u) return nullptr;
+    if (ctx->chain_mode == 0u && !chain_auto(splits, m, n)) return nullptr;
+    const std::uint64_t bytes = chain_slot_bytes(splits, m, n);
+    if (bytes <= ctx->chain_slots_bytes) return ctx->chain_slots;
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(ctx->stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone) {
+        return nullptr;
+    }
+    const std::uint64_t grown = std::max<std::uint64_t>(bytes, ctx->chain_slots_bytes + ctx->chain_slots_bytes / 2);
+    void* p = nullptr;
+    if (hipMalloc(&p, grown) != hipSuccess) return nullptr;
+    if (hipMemsetAsync(p, 0, grown, ctx->stream) != hipSuccess) {
+        (void)hipFree(p);
+        return nullptr;
+    }
+    if (ctx->chain_slots) ctx->retired.push_back(ctx->chain_slots);
+    ctx->chain_slots = static_cast<std::uint64_t*>(p);
+    ctx->chain_slots_bytes = grown;
+    ++ctx->generation;
+    return ctx->chain_slots;
 }
 
 int ensure_split_buffers(air_hip_context* ctx, std::uint64_t partial_bytes, std::uint32_t counters) {
@@ -670,6 +718,7 @@ int air_hip_context_destroy(air_hip_context* ctx) {
         if (ctx->argmax_partials) (void)hipFree(ctx->argmax_partials);
         if (ctx->epilogue_rows) (void)hipFree(ctx->epilogue_rows);
         if (ctx->gemv_pairs) (void)hipFree(ctx->gemv_pairs);
+        if (ctx->chain_slots) (void)hipFree(ctx->chain_slots);
         for (void* p : ctx->retired) (void)hipFree(p);
     }
     delete ctx;
@@ -773,6 +822,13 @@ int air_hip_context_set_tuning(air_hip_context* ctx, uint32_t rows_per_wave, uin
     ctx->tuning.rows_per_wave = rows_per_wave;
     ctx->tuning.waves_per_group = waves_per_group;
     ctx->tuning.k_splits = k_splits;
+    return AIR_HIP_OK;
+}
+
+int air_hip_context_set_split_chain(air_hip_context* ctx, uint32_t mode) {
+    if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
+    if (mode > 2u) return fail(AIR_HIP_INVALID_ARGUMENT, "mode must be 0, 1 or 2");
+    ctx->chain_mode = mode;
     return AIR_HIP_OK;
 }
 
@@ -1107,8 +1163,9 @@ int linear_loaded(air_hip_context* ctx, const air_hip_matrix* m, float* y, const
             if (rc != AIR_HIP_OK) return rc;
         }
         const SplitEpilogue* epi = reduction_epilogue(ctx, m, shape, bias, rows, epilogue, applied);
+        std::uint64_t* chain = epi ? nullptr : chain_for(ctx, shape.splits, rows, m->planes.n);
         const hipError_t err = launch_skinny_linear(m->planes, ws, bias, y, rows, shape,
-                                                    static_cast<float*>(ctx->split_partials), ctx->stream, epi);
+                                                    static_cast<float*>(ctx->split_partials), ctx->stream, epi, chain);
         if (err != hipSuccess) return hip_fail(err, "skinny_kernel");
         ctx->decode_linear_calls.fetch_add(1, std::memory_order_relaxed);
         ctx->decode_rows.fetch_add(rows, std::memory_order_relaxed);
@@ -1197,6 +1254,13 @@ int linear_rows(air_hip_context* ctx, const air_hip_matrix* m, const float* x, f
     return AIR_HIP_OK;
 }
 
+// How a plain linear's K split of `splits` workgroups is summed.
+const char* split_tail(const air_hip_context* ctx, std::uint32_t splits, std::uint32_t m, std::uint64_t n) {
+    if (splits < 2u) return "";
+    const bool chain = ctx->chain_mode == 2u || (ctx->chain_mode == 0u && chain_auto(splits, m, n));
+    return chain ? " + in-kernel chain" : " + split reduction";
+}
+
 // Text description of the launches of a linear (air_hip_linear_plan).
 std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m, std::uint32_t rows, int tactic) {
     const char* fmt = m->planes.type == kQ8_0 ? (m->type == kQ5_0 ? "q8_0 from q5_0" : "q8_0")
@@ -1276,7 +1340,7 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
         std::snprintf(buf, sizeof buf, "%s%s<%s%s> mt=%u tile_n=%u groups=%u splits=%u%s%s",
                       loaded ? "split_rows_kernel + " : "", lds ? "skinny_lds_kernel" : "skinny_kernel", fmt,
                       loaded ? "" : ", f32 input", k.mt, k.tile_n, k.groups, k.splits, stages,
-                      k.splits > 1u ? " + split reduction" : "");
+                      split_tail(ctx, k.splits, rows, m->planes.n));
         break;
     }
     case Route::decode_linear:
@@ -1286,7 +1350,7 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
         const WsplitShape w = plan_wsplit(m->planes, rows, ctx->wsplit_tuning);
         std::snprintf(buf, sizeof buf, "%swsplit_kernel<%s%s> mt=%u tile_n=%u waves=%u depth=%u groups=%u splits=%u%s",
                       w.split_x ? "split_rows_kernel + " : "", fmt, w.split_x ? "" : ", f32 input", w.mt, w.tile_n,
-                      w.waves, w.depth, w.groups, w.splits, w.splits > 1u ? " + split reduction" : "");
+                      w.waves, w.depth, w.groups, w.splits, split_tail(ctx, w.splits, rows, m->planes.n));
         break;
     }
     }

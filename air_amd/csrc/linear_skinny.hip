@@ -54,7 +54,26 @@ struct SkinnyArgs {
     std::uint32_t steps;
     std::uint32_t steps_per_split;
     std::uint32_t partial;
+    // K split combined in the kernel (chain_combine): slots [splits-1][m][n],
+    // y and the bias the last arrival adds; null: partials for a reduction.
+    std::uint64_t* chain;
+    float* y;
+    const float* chain_bias;
+    std::uint32_t splits;
 };
+
+// Stores element (m, n) of a workgroup of split `split`: y (not split), the
+// partial for the reduction launch, or the partial into the in-kernel chain.
+__device__ __forceinline__ void skinny_store(const SkinnyArgs& a, float* out, std::uint32_t split, std::uint32_t m,
+                                             std::uint64_t n, float v) {
+    const std::uint64_t e = static_cast<std::uint64_t>(m) * a.n + n;
+    if (a.chain) {
+        if (!chain_combine(a.chain, static_cast<std::uint64_t>(a.m) * a.n, e, split, a.splits, v)) return;
+        a.y[e] = a.chain_bias ? v + a.chain_bias[n] : v;
+        return;
+    }
+    out[e] = v;
+}
 
 template <int FMT, int MT, int TN, bool XF>
 __global__ __launch_bounds__(kThreads, 2) void skinny_kernel(SkinnyArgs a) {
@@ -247,7 +266,7 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_kernel(SkinnyArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const std::uint32_t m = static_cast<std::uint32_t>(t) * 16u + 4u * (lane >> 4) + static_cast<std::uint32_t>(i);
-                if (m < a.m) out[static_cast<std::uint64_t>(m) * a.n + n] = acc[j][t][i] * inv[t][i] + bn;
+                if (m < a.m) skinny_store(a, out, split, m, n, acc[j][t][i] * inv[t][i] + bn);
             }
         }
     }
@@ -497,7 +516,7 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_lds_kernel(SkinnyArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const std::uint32_t m = static_cast<std::uint32_t>(t) * 16u + 4u * (lane >> 4) + static_cast<std::uint32_t>(i);
-                if (m < a.m) out[static_cast<std::uint64_t>(m) * a.n + n] = acc[j][t][i] * inv[t][i] + bn;
+                if (m < a.m) skinny_store(a, out, split, m, n, acc[j][t][i] * inv[t][i] + bn);
             }
         }
     }
@@ -732,7 +751,7 @@ std::uint64_t skinny_partials_bytes(const SkinnyShape& shape, std::uint32_t m, s
 
 hipError_t launch_skinny_linear(const TilePlanes& p, const SplitWorkspace& ws, const float* bias, float* y,
                                 std::uint32_t m, const SkinnyShape& shape, float* partials, hipStream_t stream,
-                                const SplitEpilogue* epilogue) {
+                                const SplitEpilogue* epilogue, std::uint64_t* chain) {
     if (m == 0u || m > 64u || shape.mt != ceil_div(m, 16u)) return hipErrorInvalidValue;
     SkinnyArgs a{};
     a.codes = p.codes;
@@ -748,20 +767,27 @@ hipError_t launch_skinny_linear(const TilePlanes& p, const SplitWorkspace& ws, c
     a.steps = shape.steps;
     a.steps_per_split = shape.steps_per_split;
     const bool split = shape.splits > 1u;
+    const bool chained = split && chain && !epilogue;
     a.partial = split ? 1u : 0u;
     a.bias = split ? nullptr : bias;
     a.out = split ? partials : y;
+    if (chained) {
+        a.chain = chain;
+        a.y = y;
+        a.chain_bias = bias;
+        a.splits = shape.splits;
+    }
     const std::uint32_t blocks = shape.groups * shape.splits;
     const hipError_t err = shape.lds_stages >= 2u ? launch_lds(p.type, a, shape, blocks, stream)
                                                   : launch_any<false>(p, a, shape, blocks, stream);
-    if (err != hipSuccess || !split) return err;
+    if (err != hipSuccess || !split || chained) return err;
     if (epilogue) return launch_split_epilogue(partials, shape.splits, m, p.n, bias, *epilogue, stream);
     return launch_split_reduce(partials, shape.splits, m, p.n, bias, y, stream);
 }
 
 hipError_t launch_skinny_linear_x(const TilePlanes& p, const float* x, const float* bias, float* y, std::uint32_t m,
                                   const SkinnyShape& shape, float* partials, hipStream_t stream,
-                                  const SplitEpilogue* epilogue) {
+                                  const SplitEpilogue* epilogue, std::uint64_t* chain) {
     if (m == 0u || m > 64u || shape.mt != ceil_div(m, 16u) || p.k % 32u != 0u) return hipErrorInvalidValue;
     SkinnyArgs a{};
     a.x = x;
@@ -776,12 +802,19 @@ hipError_t launch_skinny_linear_x(const TilePlanes& p, const float* x, const flo
     a.steps = shape.steps;
     a.steps_per_split = shape.steps_per_split;
     const bool split = shape.splits > 1u;
+    const bool chained = split && chain && !epilogue;
     a.partial = split ? 1u : 0u;
     a.bias = split ? nullptr : bias;
     a.out = split ? partials : y;
+    if (chained) {
+        a.chain = chain;
+        a.y = y;
+        a.chain_bias = bias;
+        a.splits = shape.splits;
+    }
     const std::uint32_t blocks = shape.groups * shape.splits;
     const hipError_t err = launch_any<true>(p, a, shape, blocks, stream);
-    if (err != hipSuccess || !split) return err;
+    if (err != hipSuccess || !split || chained) return err;
     if (epilogue) return launch_split_epilogue(partials, shape.splits, m, p.n, bias, *epilogue, stream);
     return launch_split_reduce(partials, shape.splits, m, p.n, bias, y, stream);
 }

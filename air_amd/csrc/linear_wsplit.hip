@@ -54,6 +54,12 @@ struct WsArgs {
     std::uint32_t steps;
     std::uint32_t steps_per_split;
     std::uint32_t partial;
+    // K split combined in the kernel (chain_combine): slots [splits-1][m][n],
+    // y and the bias the last arrival adds; null: partials for a reduction.
+    std::uint64_t* chain;
+    float* y;
+    const float* chain_bias;
+    std::uint32_t splits;
 };
 
 // The activations of one 64-k step for one wave: XF holds the lane's f32
@@ -280,7 +286,16 @@ __global__ __launch_bounds__(512) void wsplit_kernel(WsArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const std::uint32_t m = t * 16u + drow + static_cast<std::uint32_t>(i);
-            if (m < a.m) out[static_cast<std::uint64_t>(m) * a.n + n] = sum[i] * invt[i] + bn;
+            if (m >= a.m) continue;
+            const std::uint64_t e = static_cast<std::uint64_t>(m) * a.n + n;
+            float v = sum[i] * invt[i] + bn;
+            if (a.chain) {
+                if (chain_combine(a.chain, static_cast<std::uint64_t>(a.m) * a.n, e, split, a.splits, v)) {
+                    a.y[e] = a.chain_bias ? v + a.chain_bias[n] : v;
+                }
+            } else {
+                out[e] = v;
+            }
         }
     }
 }
@@ -402,7 +417,7 @@ std::uint64_t wsplit_partials_bytes(const WsplitShape& s, std::uint32_t m, std::
 
 hipError_t launch_wsplit_linear(const TilePlanes& p, const float* x, const SplitWorkspace* ws, const float* bias,
                                 float* y, std::uint32_t m, const WsplitShape& s, float* partials, hipStream_t stream,
-                                const SplitEpilogue* epilogue) {
+                                const SplitEpilogue* epilogue, std::uint64_t* chain) {
     if (m == 0u || m > 64u || s.mt != ceil_div(m, 16u) || s.waves == 0u || s.waves > 8u) return hipErrorInvalidValue;
     if (!ws && (x == nullptr || p.k % 32u != 0u)) return hipErrorInvalidValue;
     WsArgs a{};
@@ -423,11 +438,18 @@ hipError_t launch_wsplit_linear(const TilePlanes& p, const float* x, const Split
     a.steps = s.steps;
     a.steps_per_split = s.steps_per_split;
     const bool split = s.splits > 1u;
+    const bool chained = split && chain && !epilogue;
     a.partial = split ? 1u : 0u;
     a.bias = split ? nullptr : bias;
     a.out = split ? partials : y;
+    if (chained) {
+        a.chain = chain;
+        a.y = y;
+        a.chain_bias = bias;
+        a.splits = s.splits;
+    }
     const hipError_t err = ws ? launch_wsplit_any<false>(p.type, a, s, stream) : launch_wsplit_any<true>(p.type, a, s, stream);
-    if (err != hipSuccess || !split) return err;
+    if (err != hipSuccess || !split || chained) return err;
     if (epilogue) return launch_split_epilogue(partials, s.splits, m, p.n, bias, *epilogue, stream);
     return launch_split_reduce(partials, s.splits, m, p.n, bias, y, stream);
 }

@@ -168,6 +168,19 @@ int air_hip_context_set_tuning(air_hip_context* ctx, uint32_t rows_per_wave, uin
  * (src/cuda/cuda_backend.cu:585-606). */
 int air_hip_context_set_gemv_shape(air_hip_context* ctx, uint32_t pair_mode, uint32_t units_per_chunk,
                                    uint32_t depth);
+/* How the skinny and wave-split decode kernels (2..64 rows) sum a K split
+ * over workgroups when no epilogue rides on the sum (autotuning): mode 0 =
+ * automatic (in the kernel for small outputs: a 2-way split up to 256k
+ * outputs, longer splits up to 56k outputs per added split; otherwise the
+ * reduction launch), 1 = always the reduction launch, 2 = always in the
+ * kernel.  In the kernel,
+ * the workgroups of an output meet through context-owned 64-bit slots (a
+ * chain in split order, so the bits equal the reduction launch's); the
+ * slots grow on demand outside graph capture, and a call that would need
+ * them to grow during capture takes the reduction launch.  Replaces the
+ * second pass of the reference's batch-reuse matmul
+ * (src/cuda/cuda_backend.cu:529-583) for these widths. */
+int air_hip_context_set_split_chain(air_hip_context* ctx, uint32_t mode);
 /* Chooses the decode kernel for 2..64 rows (autotuning): path 0 = automatic
  * (the skinny kernel: activations split once into the workspace and staged
  * through LDS, every weight read once, K split over workgroups when the

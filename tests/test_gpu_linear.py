@@ -6,6 +6,8 @@ matvec (tensor_reader.cpp:369-394) on the decode tactic.
 """
 from __future__ import annotations
 
+import re
+
 import numpy as np
 import pytest
 
@@ -435,6 +437,137 @@ def test_graph_replay_after_workspace_growth(torch_cuda):
     finally:
         torch.cuda.synchronize()
         graph = None                              # before the context frees its kept buffers
+        mat.release()
+        ctx.close()
+
+
+# (format, K, N, M, route override): the wave-split kernel (f32 rows and the
+# row-scaled split, 2..8-way K splits), the skinny register and LDS kernels
+# (2, 3 and 5-way splits), on 7B-like and ragged shapes.
+CHAIN_CASES = [
+    (capi.TYPE_Q8_0, 3584, 4608, 8, None),
+    (capi.TYPE_Q8_0, 18944, 3584, 8, None),
+    (capi.TYPE_Q8_0, 3584, 4608, 32, None),
+    (capi.TYPE_Q8_0, 18944, 3584, 32, None),
+    (capi.TYPE_Q8_0, 3584, 1000, 33, ("wsplit", 1, 4, 2, 3, 1)),
+    (capi.TYPE_Q4_0, 2048, 777, 5, ("wsplit", 2, 4, 2, 4, 2)),
+    (capi.TYPE_Q4_K, 2304, 512, 20, ("wsplit", 1, 8, 2, 2, 1)),
+    (capi.TYPE_Q8_0, 3584, 1000, 40, ("skinny", 1, 3, 2)),
+    (capi.TYPE_Q4_0, 1152, 333, 17, ("skinny", 2, 5, 1)),
+    (capi.TYPE_Q4_K, 3584, 512, 64, ("skinny", 1, 2, 2)),
+]
+
+
+def _route(ctx, route):
+    if route is None:
+        return
+    if route[0] == "wsplit":
+        _, tn, waves, depth, splits, sx = route
+        ctx.set_wsplit(1, tn, waves, depth, splits, sx)
+    else:
+        _, tn, splits, stages = route
+        ctx.set_wsplit(2)
+        ctx.set_decode_path(2, tn, splits)
+        ctx.set_decode_pipeline(stages)
+
+
+@pytest.mark.parametrize("type_id,k,n,m,route", CHAIN_CASES)
+def test_split_chain_matches_reduction(torch_cuda, hip_ctx, type_id, k, n, m, route):
+    """A K split over workgroups summed inside the kernel (each output's
+    partials meet through 64-bit exchange slots in split order) gives the
+    reduction launch's bits, with and without bias, on every repeat and after
+    a launch on another shape (the slots return to zero); the oracle's result
+    to 1e-4."""
+    torch = torch_cuda
+    canon = helpers.weights(type_id, k, n, seed=k + 5 * n + m)
+    mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    other_canon = helpers.weights(capi.TYPE_Q8_0, 1024, 96, seed=4)
+    other = capi.Matrix(hip_ctx, capi.TYPE_Q8_0, 1024, 96, other_canon, other_canon.nbytes, on_device=False)
+    try:
+        _route(hip_ctx, route)
+        x = helpers.activations(m, k, seed=m + k)
+        x[:, ::61] *= 40.0
+        xd = _dev(torch, x)
+        xo = _dev(torch, helpers.activations(m, 1024, seed=9))
+        yo = torch.empty((m, 96), dtype=torch.float32, device="cuda:0")
+        bias = helpers.activations(1, n, seed=n)[0] * 0.1
+        bias_d = _dev(torch, bias)
+        hip_ctx.set_split_chain(2)
+        plan = mat.plan(m)
+        print(f"chain {capi.TYPE_NAMES[type_id]} {n}x{k} M={m}: {plan}", flush=True)
+        assert int(re.search(r"splits=(\d+)", plan).group(1)) > 1 and "in-kernel chain" in plan, plan
+        for b, bd in ((None, None), (bias, bias_d)):
+            hip_ctx.set_split_chain(1)
+            ref = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+            mat.linear(xd, ref, m, bias=bd)
+            torch.cuda.synchronize()
+            want = ref.cpu().numpy()
+            assert helpers.rel_l2(want, oracle.linear(type_id, canon, k, n, x, bias=b)) <= DECODE_TOL
+            hip_ctx.set_split_chain(2)
+            for _ in range(3):
+                y = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+                mat.linear(xd, y, m, bias=bd)
+                other.linear(xo, yo, m)
+                torch.cuda.synchronize()
+                assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32)), (b is None)
+    finally:
+        hip_ctx.set_split_chain(0)
+        hip_ctx.set_wsplit(0)
+        hip_ctx.set_decode_path(0)
+        hip_ctx.set_decode_pipeline(0)
+        other.release()
+        mat.release()
+
+
+def test_split_chain_under_graph_capture(torch_cuda):
+    """A captured linear whose chain slots would have to grow during capture
+    takes the reduction launch instead (same bits); once the slots exist, a
+    captured chain replays correctly, the slots returning to zero between
+    replays.  A context of its own, so no slots exist at first."""
+    torch = torch_cuda
+    dev = torch.device("cuda:0")
+    main = torch.cuda.current_stream(dev)
+    type_id, k, n, m = capi.TYPE_Q8_0, 3584, 4608, 8
+    canon = helpers.weights(type_id, k, n, seed=91)
+    x = helpers.activations(m, k, seed=92)
+    ctx = capi.Context(0, main.cuda_stream)
+    mat = capi.Matrix(ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    graphs = []
+    try:
+        assert "in-kernel chain" in mat.plan(m), mat.plan(m)
+        xd = _dev(torch, x)
+        ctx.set_split_chain(1)
+        ref = torch.empty((m, n), dtype=torch.float32, device=dev)
+        mat.linear(xd, ref, m)
+        torch.cuda.synchronize()
+        want = ref.cpu().numpy()
+        ctx.set_split_chain(0)
+        outs = []
+        for _ in range(2):      # first capture: no slots yet; second: slots grown by the eager call between
+            y = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+            capture = torch.cuda.Stream(dev)
+            ctx.set_stream(capture.cuda_stream)
+            graph = torch.cuda.CUDAGraph()
+            try:
+                with torch.cuda.graph(graph, stream=capture):
+                    mat.linear(xd, y, m)
+            finally:
+                ctx.set_stream(main.cuda_stream)
+            graphs.append(graph)
+            outs.append(y)
+            eager = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+            mat.linear(xd, eager, m)   # grows the slots outside capture
+            torch.cuda.synchronize()
+            assert np.array_equal(eager.cpu().numpy().view(np.uint32), want.view(np.uint32))
+        for _ in range(3):
+            for graph, y in zip(graphs, outs):
+                y.fill_(float("nan"))
+                graph.replay()
+                torch.cuda.synchronize()
+                assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    finally:
+        torch.cuda.synchronize()
+        graphs = None
         mat.release()
         ctx.close()
 
