@@ -650,6 +650,8 @@ def main() -> int:
     ap.add_argument("--e2e-only", action="store_true", help="run only the end-to-end leg and print its JSON")
     ap.add_argument("--dense-only", action="store_true",
                     help="run only the dense-route leg (F16 / Q6_K matrices at 7B shapes) and print its JSON")
+    ap.add_argument("--small-only", action="store_true",
+                    help="run only the configs[0] / configs[1] legs (0.5B shapes) and print their JSON")
     ap.add_argument("--e2e-eager", action="store_true",
                     help="decode steps launch kernel by kernel instead of replaying graphs (for kernel traces)")
     ap.add_argument("--trace-summary", default=None, metavar="CSV",
@@ -695,6 +697,9 @@ def main() -> int:
     if args.dense_only:
         print(json.dumps({"dense": measure_dense(torch, capi, dev, stream, ctx, args.steps, args.warmup,
                                                  bool(args.graph))}), flush=True)
+        return 0
+    if args.small_only:
+        print(json.dumps(measure_small_configs(torch, capi, quant, dev, stream, args.steps, args.warmup)), flush=True)
         return 0
 
     t_build = time.perf_counter()
