@@ -642,9 +642,11 @@ GemvShape plan_decode_gemv(const TilePlanes& p, const DecodeTuning& tuning) {
     }
     // A grid just past one workgroup per CU (q|k|v: 288 row tiles on 256
     // CUs) ends in a round of few workgroups: split each tile's units over a
-    // pair of workgroups with half the waves each.
+    // pair of workgroups with half the waves each.  Measured (Q8_0, 288-304
+    // row tiles): K = 3584 (14 units) 7.00 -> 6.71 us, K = 2048 (8) 5.37 ->
+    // 5.29; K = 1536 (6) even; K = 896 (4) 4.17 -> 4.37, two waves a side.
     const bool pair_fits = g.rows_per_wave == 1u && p.n <= kGemvPairSlots && units >= 2u;
-    bool pair = pair_fits && groups > 256u && groups <= 320u;
+    bool pair = pair_fits && groups > 256u && groups <= 320u && units >= 8u;
     if (tuning.pair_split == 1u) pair = false;
     if (tuning.pair_split == 2u) pair = pair_fits;
     if (pair && tuning.waves_per_group == 0u) {
