@@ -738,6 +738,12 @@ SkinnyShape plan_skinny(const TilePlanes& p, std::uint32_t m, std::uint32_t tile
                partial_trip * splits * 2u <= 2u * weight_bytes) {
             splits *= 2u;
         }
+        // Q4_K on wide grids (gate|up, 592 groups of one tile) at M <= 32
+        // takes two splits past that limit: 45.1 -> 37.6 us at M = 16, 54.8
+        // -> 50.6 at M = 32 (three or four splits slower; M = 64 even).
+        if (p.type == kQ4_K && s.mt <= 2u && p.nt >= 2000u && p.nt <= 4096u && s.lds_stages >= 2u && splits < 2u) {
+            splits = 2u;
+        }
     }
     splits = splits < 1u ? 1u : (splits > s.steps ? s.steps : splits);
     s.steps_per_split = static_cast<std::uint32_t>(ceil_div(s.steps, splits));

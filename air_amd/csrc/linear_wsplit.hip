@@ -356,11 +356,13 @@ bool wsplit_preferred(const TilePlanes& p, std::uint32_t m) {
     //    activations among four waves (gate|up 43.8 against 48.2);
     //  * three or four: only o-shaped matrices (<= 256 row tiles, K <= 4096)
     //    outside Q4_K (o 20.1 -> 18.7 us at M = 64).
-    // The lm_head (thousands of row tiles) keeps its register kernel.
+    // The lm_head (thousands of row tiles) keeps its register kernel.  Q4_K
+    // gate|up (2368 row tiles) at M <= 16 is faster on the LDS pipeline with
+    // a 2-way K split (36.1-37.6 us against 41.0 at M = 4..16).
     if (m < 2u || m > 64u || p.nt > 4096u) return false;
     const std::uint32_t mt = static_cast<std::uint32_t>(ceil_div(m, 16u));
     const bool short_k = p.k <= 4096u;
-    if (mt == 1u) return !(p.type == kQ4_K && p.nt > 256u && p.nt <= 512u && short_k);
+    if (mt == 1u) return !(p.type == kQ4_K && ((p.nt > 256u && p.nt <= 512u && short_k) || p.nt >= 2000u));
     if (mt == 2u) return p.nt <= 256u;
     return p.type != kQ4_K && p.nt <= 256u && short_k;
 }
