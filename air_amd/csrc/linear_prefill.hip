@@ -685,13 +685,15 @@ PrefillShape plan_prefill(const TilePlanes& p, std::uint32_t m, const PrefillTun
     }
     // The LDS pipeline runs the Q8_0 8x4 and 4x2 tiles only.  Automatic: two
     // stages for the 8x4 tile (measured at M = 512: gate|up 716 vs 700
-    // TFLOP/s, down 690 vs 637; the 4x2 remainder 48 vs 55 us), registers
-    // for the 4x2 tile on its own (q|k|v 400 vs 367, o 369 vs 385).
+    // TFLOP/s, down 690 vs 637; the 4x2 remainder 48 vs 55 us); the 4x2 tile
+    // on its own takes registers above 256 row tiles (q|k|v, 288: 41.4 us
+    // against 43.5 on LDS) and the LDS pipeline up to them (o, 224: 34.1
+    // against 35.9).
     const bool lds_tile = (s.tile_m == 8u && s.tile_n == 4u) || (s.tile_m == 4u && s.tile_n == 2u);
     if (p.type == kQ8_0 && lds_tile) {
         if (tuning.lds_stages >= 2u && tuning.lds_stages <= 4u) {
             s.lds_stages = tuning.lds_stages;
-        } else if (tuning.lds_stages == 0u && s.tile_m == 8u) {
+        } else if (tuning.lds_stages == 0u && (s.tile_m == 8u || p.nt <= 256u)) {
             s.lds_stages = 2u;
         }
     }
