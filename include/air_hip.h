@@ -322,10 +322,14 @@ int air_hip_linear_plan(const air_hip_context* ctx, const air_hip_matrix* matrix
  * so code under HIP graph capture, tight serving loops and harnesses that
  * forbid allocation can call it.  Same kernels and launch shapes as
  * air_hip_linear through this context (its tuning overrides included), so
- * the outputs are bit-identical.  Its split activations and K-split partials
- * live in a 16 MiB device array per GPU, held from library load until the
- * process ends (every Qwen2-7B projection and lm_head at m <= 64 needs at
- * most 12.5 MiB); a linear needing more, m > 64, the PREFILL tactic, and the
+ * the outputs are bit-identical; a K split that air_hip_linear sums inside
+ * the kernel (air_hip_context_set_split_chain) takes the reduction launch
+ * here, which the in-kernel sum reproduces bit for bit.  Its split
+ * activations and K-split partials live in a 16 MiB device array per GPU,
+ * and the one-row GEMV's pair-split row slots in a second one of 8192
+ * words, both held from library load until the process ends (every
+ * Qwen2-7B projection and lm_head at m <= 64 needs at most 12.5 MiB); a
+ * linear needing more, m > 64, the PREFILL tactic, and the
  * fused kernel's cross-workgroup K split (a tuning override) return
  * AIR_HIP_UNSUPPORTED.  The array keeps the last call's contents and is
  * shared by every call on that GPU: calls that overlap on one GPU (other
