@@ -29,7 +29,8 @@ pytestmark = pytest.mark.gpu
 # from f32 rows (down at M = 8 with a K split, q|k|v at M = 16 and 3, o at M
 # = 4, Q4_0 gate|up at M = 2) and over the row-scaled split (gate|up at M =
 # 16, Q4_K o at M = 17), Q4_K o at M = 64 on the LDS pipeline, and the M = 1
-# GEMV with its workgroup pairs (o; down with bias after down at M = 2).
+# GEMV (o; down with bias after down at M = 2) and its pair split (q|k|v at
+# M = 1 after M = 2, its row slots in the second static array).
 CASES = [
     (capi.TYPE_Q8_0, 3584, 18944, False, (64, 8)),
     (capi.TYPE_Q8_0, 37888, 3584, False, (32, 16)),
@@ -38,6 +39,7 @@ CASES = [
     (capi.TYPE_Q4_K, 3584, 3584, False, (64, 17)),
     (capi.TYPE_Q4_0, 37888, 3584, False, (64, 2)),
     (capi.TYPE_Q8_0, 3584, 18944, True, (2, 1)),
+    (capi.TYPE_Q8_0, 4608, 3584, True, (2, 1)),
 ]
 
 
