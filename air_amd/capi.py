@@ -127,6 +127,7 @@ SIGNATURES = {
     "air_hip_context_set_tuning": (_I, [_P, _U32, _U32, _U32]),
     "air_hip_context_set_gemv_shape": (_I, [_P, _U32, _U32, _U32]),
     "air_hip_context_set_split_chain": (_I, [_P, _U32]),
+    "air_hip_context_set_skinny_waves": (_I, [_P, _U32]),
     "air_hip_context_set_prefill_tuning": (_I, [_P, _U32, _U32, _U32, _U32]),
     "air_hip_context_set_decode_path": (_I, [_P, _U32, _U32, _U32]),
     "air_hip_context_set_wsplit": (_I, [_P, _U32, _U32, _U32, _U32, _U32, _U32]),
@@ -245,6 +246,10 @@ class Context:
 
     def set_tuning(self, rows_per_wave: int = 0, waves_per_group: int = 0, k_splits: int = 0) -> None:
         check(lib().air_hip_context_set_tuning(self.handle, rows_per_wave, waves_per_group, k_splits))
+
+    def set_skinny_waves(self, waves: int = 0) -> None:
+        """Waves per workgroup of the LDS skinny kernel: 0 / 4 automatic, 8."""
+        check(lib().air_hip_context_set_skinny_waves(self.handle, waves))
 
     def set_split_chain(self, mode: int = 0) -> None:
         """K splits of the 2..64-row kernels: 0 automatic, 1 reduction launch,

@@ -240,11 +240,14 @@ struct SkinnyShape {
     std::uint32_t steps_per_split{0};
     std::uint32_t splits{1};
     std::uint32_t lds_stages{0};  // Q8_0 from split activations: stages of the LDS pipeline (0 = registers)
+    std::uint32_t waves{4};       // waves per workgroup: 4, or 8 on the LDS pipeline
 };
 // lds_stages: 0 automatic, 1 the register pipeline, 2..4 the LDS ring
 // (Q8_0 from split activations; other formats and f32 inputs ignore it).
+// waves: 0 or 4, or 8 (the LDS pipeline with two stages and two or four
+// activation tiles; otherwise 4).
 SkinnyShape plan_skinny(const TilePlanes& planes, std::uint32_t m, std::uint32_t tile_n, std::uint32_t k_splits,
-                        std::uint32_t lds_stages = 0);
+                        std::uint32_t lds_stages = 0, std::uint32_t waves = 0);
 std::uint64_t skinny_partials_bytes(const SkinnyShape& shape, std::uint32_t m, std::uint64_t n);
 // With `epilogue` (only when shape.splits > 1 and split_epilogue_fits), the
 // split reduction applies it and y is not written.  Without one, a non-null

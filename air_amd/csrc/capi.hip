@@ -83,6 +83,7 @@ struct air_hip_context {
     std::uint32_t skinny_tile_n{0};
     std::uint32_t skinny_splits{0};
     std::uint32_t skinny_lds_stages{0};   // 0 automatic, 1 registers, 2..4 LDS ring stages
+    std::uint32_t skinny_waves{0};        // 0 automatic, 4, or 8 waves per workgroup on the LDS pipeline
     // Decode widths 2..64 on the wave-split kernel: 0 = automatic, 1 = always,
     // 2 = never; and its launch-shape overrides.
     std::uint32_t wsplit_mode{0};
@@ -357,7 +358,8 @@ enum class Route { prefill, gemv, fused, skinny_x, skinny_loaded, decode_linear,
 // faster), and loses on wide ones (gate|up, lm_head: up to 2x slower) and at
 // M = 64.  Q4_K with four activation tiles would also spill in it.
 Route skinny_route(const air_hip_context* ctx, const air_hip_matrix* m, std::uint32_t rows) {
-    const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages);
+    const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages,
+                                          ctx->skinny_waves);
     // From 17 rows the split activations feed the LDS pipeline, which beats
     // the f32-input kernel on the narrow 7B matrices too, split launch
     // included (Q8_0, M = 32: q|k|v 18.4 -> 16.2 us, o 16.3 -> 14.7, down
@@ -401,7 +403,8 @@ Route route_linear(const air_hip_context* ctx, const air_hip_matrix* m, std::uin
 // (two with a K split), no activation workspace.
 int run_skinny_x(air_hip_context* ctx, const air_hip_matrix* m, const float* x, float* y, const float* bias,
                  std::uint32_t rows, const SplitEpilogue* epilogue, bool* applied, const void* ready) {
-    const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages);
+    const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages,
+                                          ctx->skinny_waves);
     if (skinny_route(ctx, m, rows) == Route::skinny_loaded) {
         int rc = load_activations_for(ctx, x, m->planes.k, rows, ready);
         if (rc != AIR_HIP_OK) return rc;
@@ -825,6 +828,13 @@ int air_hip_context_set_tuning(air_hip_context* ctx, uint32_t rows_per_wave, uin
     return AIR_HIP_OK;
 }
 
+int air_hip_context_set_skinny_waves(air_hip_context* ctx, uint32_t waves) {
+    if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
+    if (waves != 0u && waves != 4u && waves != 8u) return fail(AIR_HIP_INVALID_ARGUMENT, "waves must be 0, 4 or 8");
+    ctx->skinny_waves = waves;
+    return AIR_HIP_OK;
+}
+
 int air_hip_context_set_split_chain(air_hip_context* ctx, uint32_t mode) {
     if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
     if (mode > 2u) return fail(AIR_HIP_INVALID_ARGUMENT, "mode must be 0, 1 or 2");
@@ -1156,7 +1166,8 @@ int linear_loaded(air_hip_context* ctx, const air_hip_matrix* m, float* y, const
         return fail(AIR_HIP_INVALID_STATE, "activations were loaded for another decode path; load them again");
     }
     if (skinny) {
-        const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages);
+        const SkinnyShape shape = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages,
+                                          ctx->skinny_waves);
         const std::uint64_t partial_bytes = skinny_partials_bytes(shape, rows, m->planes.n);
         if (partial_bytes > 0u) {
             const int rc = ensure_split_buffers(ctx, partial_bytes, 0u);
@@ -1333,10 +1344,11 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
     case Route::skinny_x:
     case Route::skinny_loaded: {
         const bool loaded = route_linear(ctx, m, rows, tactic) == Route::skinny_loaded;
-        const SkinnyShape k = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages);
+        const SkinnyShape k = plan_skinny(m->planes, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages,
+                                          ctx->skinny_waves);
         const bool lds = loaded && k.lds_stages >= 2u;
         char stages[32] = "";
-        if (lds) std::snprintf(stages, sizeof stages, " lds_stages=%u", k.lds_stages);
+        if (lds) std::snprintf(stages, sizeof stages, " lds_stages=%u%s", k.lds_stages, k.waves == 8u ? " waves=8" : "");
         std::snprintf(buf, sizeof buf, "%s%s<%s%s> mt=%u tile_n=%u groups=%u splits=%u%s%s",
                       loaded ? "split_rows_kernel + " : "", lds ? "skinny_lds_kernel" : "skinny_kernel", fmt,
                       loaded ? "" : ", f32 input", k.mt, k.tile_n, k.groups, k.splits, stages,
@@ -1408,7 +1420,8 @@ int air_hip_linear_noalloc(air_hip_context* ctx, const air_hip_matrix* m, const 
     SkinnyShape shape{};
     WsplitShape wshape{};
     if (route == Route::skinny_x || route == Route::skinny_loaded) {
-        shape = plan_skinny(p, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages);
+        shape = plan_skinny(p, rows, ctx->skinny_tile_n, ctx->skinny_splits, ctx->skinny_lds_stages,
+                                          ctx->skinny_waves);
         partial_bytes = skinny_partials_bytes(shape, rows, p.n);
     }
     if (route == Route::wsplit) {

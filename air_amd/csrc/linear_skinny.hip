@@ -311,24 +311,30 @@ constexpr unsigned lds_code_bytes() {
     return FMT == kQ8_0 ? 1024u : 512u;   // per tile and step
 }
 
-template <int FMT, int MT, int TN>
+template <int FMT, int MT, int TN, int W = 4>
 constexpr unsigned skinny_stage_bytes() {
-    return 4u * MT * 1024u + 4u * TN * (lds_code_bytes<FMT>() + 256u) + (FMT == kQ4_K ? 1024u : 0u);
+    return 4u * MT * 1024u + W * TN * (lds_code_bytes<FMT>() + 256u) + (FMT == kQ4_K ? W * 256u : 0u);
 }
 
-template <int FMT, int MT, int TN, int NS>
-__global__ __launch_bounds__(kThreads, 2) void skinny_lds_kernel(SkinnyArgs a) {
-    constexpr unsigned kStage = skinny_stage_bytes<FMT, MT, TN>();
+// W waves per workgroup (4, or 8 with two or four activation tiles): the
+// workgroup covers W * TN weight tiles, so eight waves read each step's
+// activations into LDS once for twice the weight rows.
+template <int FMT, int MT, int TN, int NS, int W = 4>
+__global__ __launch_bounds__(64 * W, W == 4 ? 2 : 1) void skinny_lds_kernel(SkinnyArgs a) {
+    constexpr unsigned kStage = skinny_stage_bytes<FMT, MT, TN, W>();
     constexpr unsigned kCodeBytes = lds_code_bytes<FMT>();
     constexpr unsigned kCodes = 4u * MT * 1024u;                  // offset of the weight codes in a stage
-    constexpr unsigned kScales = kCodes + 4u * TN * kCodeBytes;   // offset of the weight scales
-    constexpr unsigned kSumsAt = kScales + 4u * TN * 256u;        // offset of the block sums (Q4_K)
+    constexpr unsigned kScales = kCodes + W * TN * kCodeBytes;    // offset of the weight scales
+    constexpr unsigned kSumsAt = kScales + W * TN * 256u;         // offset of the block sums (Q4_K)
     constexpr bool kSums = FMT == kQ4_K;
     constexpr unsigned kMp = 16u * MT;
-    // Load instructions per wave per stage.
-    constexpr unsigned kLoads = MT + TN * (FMT == kQ8_0 ? 2u : 3u) + (kSums ? 1u : 0u);
+    constexpr unsigned kActLoads = 4u * MT / W;                   // activation fragments per wave per step
+    // Load instructions per wave per stage (the same for every wave).
+    constexpr unsigned kLoads = kActLoads + TN * (FMT == kQ8_0 ? 2u : 3u) + (kSums ? 1u : 0u);
+    static_assert(W == 4 || W == 8, "four or eight waves");
+    static_assert((4u * MT) % W == 0u, "activation fragments split evenly over the waves");
     static_assert(NS >= 2 && NS <= 4, "two to four stages");
-    static_assert(2u * kMp <= 4u * 64u, "one block-sum load per wave covers a step");
+    static_assert(2u * kMp <= W * 64u, "one block-sum load per wave covers a step");
     // One LDS object per stage, addressed with compile-time stage numbers:
     // the compiler's wait-count pass then sees that a stage's direct loads
     // and another stage's reads touch different objects.
@@ -344,7 +350,7 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_lds_kernel(SkinnyArgs a) {
     const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const std::uint32_t group = blockIdx.x % a.groups;
     const std::uint32_t split = blockIdx.x / a.groups;
-    const std::uint32_t rt0 = (group * 4u + wave) * TN;
+    const std::uint32_t rt0 = (group * W + wave) * TN;
     const std::uint32_t s_begin = split * a.steps_per_split;
     const std::uint32_t s_end = min(a.steps, s_begin + a.steps_per_split);
 
@@ -373,8 +379,8 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_lds_kernel(SkinnyArgs a) {
         unsigned char* base = stage(st);
         // Fragment f of the step: block f / (2 MT), tile (f / 2) % MT, part f % 2.
 #pragma unroll
-        for (unsigned j = 0; j < static_cast<unsigned>(MT); ++j) {
-            const unsigned f = wave + 4u * j;
+        for (unsigned j = 0; j < kActLoads; ++j) {
+            const unsigned f = wave + W * j;
             lds_load16(xs + (static_cast<std::uint64_t>(s) * (4u * MT) + f) * 64u + lane, base + f * 1024u);
         }
 #pragma unroll
@@ -618,6 +624,7 @@ hipError_t launch_mt(const SkinnyArgs& a, std::uint32_t tn, std::uint32_t blocks
 
 template <int FMT, bool XF>
 hipError_t launch_fmt(const SkinnyArgs& a, const SkinnyShape& shape, std::uint32_t blocks, hipStream_t stream) {
+    if (shape.waves != 4u) return hipErrorInvalidConfiguration;   // eight waves: the LDS pipeline only
     switch (shape.mt) {
     case 1: return launch_mt<FMT, 1, XF>(a, shape.tile_n, blocks, stream);
     case 2: return launch_mt<FMT, 2, XF>(a, shape.tile_n, blocks, stream);
@@ -629,6 +636,17 @@ hipError_t launch_fmt(const SkinnyArgs& a, const SkinnyShape& shape, std::uint32
 template <int FMT, int MT>
 hipError_t launch_lds_mt(const SkinnyArgs& a, const SkinnyShape& shape, std::uint32_t blocks, hipStream_t stream) {
     const bool two = shape.tile_n == 2u;
+    if (shape.waves == 8u) {
+        // Eight waves: two or four activation tiles, two stages.
+        if constexpr (MT == 2 || MT == 4) {
+            if (shape.lds_stages != 2u) return hipErrorInvalidConfiguration;
+            if (two) hipLaunchKernelGGL((skinny_lds_kernel<FMT, MT, 2, 2, 8>), dim3(blocks), dim3(512), 0, stream, a);
+            else hipLaunchKernelGGL((skinny_lds_kernel<FMT, MT, 1, 2, 8>), dim3(blocks), dim3(512), 0, stream, a);
+            return hipGetLastError();
+        }
+        return hipErrorInvalidConfiguration;
+    }
+    if (shape.waves != 4u) return hipErrorInvalidConfiguration;
     switch (shape.lds_stages) {
     case 2:
         if (two) hipLaunchKernelGGL((skinny_lds_kernel<FMT, MT, 2, 2>), dim3(blocks), dim3(kThreads), 0, stream, a);
@@ -689,7 +707,7 @@ hipError_t launch_split_activations_rows(const float* x, std::uint32_t m, std::u
 }
 
 SkinnyShape plan_skinny(const TilePlanes& p, std::uint32_t m, std::uint32_t tile_n, std::uint32_t k_splits,
-                        std::uint32_t lds_stages) {
+                        std::uint32_t lds_stages, std::uint32_t waves) {
     SkinnyShape s;
     s.mt = static_cast<std::uint32_t>(ceil_div(m, 16u));
     // The LDS pipeline (split activations): two stages measured best (three
@@ -721,7 +739,16 @@ SkinnyShape plan_skinny(const TilePlanes& p, std::uint32_t m, std::uint32_t tile
     const bool tn2_auto = s.mt <= 2u && p.nt >= 2000u && (p.type == kQ8_0 || s.lds_stages == 0u);
     const std::uint32_t want = tile_n != 0u ? tile_n : (tn2_auto ? 2u : 1u);
     s.tile_n = (want == 2u && s.mt <= tn2_max_mt) ? 2u : 1u;
-    s.groups = static_cast<std::uint32_t>(ceil_div(p.nt, 4u * s.tile_n));
+    // Eight waves per workgroup: the LDS pipeline with two stages and two or
+    // four activation tiles.  Automatic for Q8_0 gate|up-sized matrices at
+    // 17..32 rows, with one weight tile per wave (45.5 -> 44.0 us at M = 32);
+    // measured even or slower on every other 7B matrix, width and format.
+    const bool eight_auto = waves == 0u && p.type == kQ8_0 && s.mt == 2u && p.nt >= 2000u && p.nt <= 4096u &&
+                            tile_n == 0u;
+    const bool eight = (waves == 8u || eight_auto) && s.lds_stages == 2u && (s.mt == 2u || s.mt == 4u);
+    s.waves = eight ? 8u : 4u;
+    if (eight_auto && eight) s.tile_n = 1u;
+    s.groups = static_cast<std::uint32_t>(ceil_div(p.nt, s.waves * s.tile_n));
     s.steps = static_cast<std::uint32_t>(p.kp / kStepK);
     std::uint32_t splits = k_splits;
     if (splits == 0u) {

@@ -181,6 +181,12 @@ int air_hip_context_set_gemv_shape(air_hip_context* ctx, uint32_t pair_mode, uin
  * second pass of the reference's batch-reuse matmul
  * (src/cuda/cuda_backend.cu:529-583) for these widths. */
 int air_hip_context_set_split_chain(air_hip_context* ctx, uint32_t mode);
+/* Waves per workgroup of the LDS-pipelined skinny kernel (autotuning): 0 =
+ * automatic (eight for Q8_0 gate|up-sized matrices at 17..32 rows, else
+ * four), 4, or 8 = eight waves over twice the weight rows sharing each
+ * step's activations (two stages, 17..32 or 49..64 rows; other widths keep
+ * four).  Same arithmetic and bits as four waves. */
+int air_hip_context_set_skinny_waves(air_hip_context* ctx, uint32_t waves);
 /* Chooses the decode kernel for 2..64 rows (autotuning): path 0 = automatic
  * (the skinny kernel: activations split once into the workspace and staged
  * through LDS, every weight read once, K split over workgroups when the

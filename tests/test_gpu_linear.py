@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import oracle
-from air_amd import capi
+from air_amd import capi, quant
 from tests import helpers
 
 pytestmark = pytest.mark.gpu
@@ -516,6 +516,72 @@ def test_split_chain_matches_reduction(torch_cuda, hip_ctx, type_id, k, n, m, ro
         hip_ctx.set_decode_path(0)
         hip_ctx.set_decode_pipeline(0)
         other.release()
+        mat.release()
+
+
+@pytest.mark.parametrize("type_id,k,n,m", [(capi.TYPE_Q8_0, 3584, 1000, 20), (capi.TYPE_Q8_0, 3584, 1000, 64),
+                                           (capi.TYPE_Q4_0, 2048, 777, 32), (capi.TYPE_Q4_K, 2304, 520, 64),
+                                           (capi.TYPE_Q8_0, 1024, 600, 45)])
+def test_skinny_eight_waves_bit_identical(torch_cuda, hip_ctx, type_id, k, n, m):
+    """The LDS skinny kernel with eight waves per workgroup (twice the weight
+    rows sharing each step's activations) gives the four-wave kernel's bits
+    at every split count, and the oracle's result; widths of one or three
+    activation tiles keep four waves."""
+    torch = torch_cuda
+    canon = helpers.weights(type_id, k, n, seed=k + n + m)
+    mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    try:
+        x = helpers.activations(m, k, seed=m + 3)
+        xd = _dev(torch, x)
+        want = oracle.linear(type_id, canon, k, n, x)
+        hip_ctx.set_wsplit(2)
+        for splits in (1, 2, 4):
+            hip_ctx.set_decode_path(2, 1, splits)
+            outs = []
+            for waves in (4, 8):
+                hip_ctx.set_skinny_waves(waves)
+                plan = mat.plan(m)
+                assert ("waves=8" in plan) == (waves == 8 and -(-m // 16) in (2, 4)), plan
+                y = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+                mat.linear(xd, y, m)
+                torch.cuda.synchronize()
+                outs.append(y.cpu().numpy())
+            assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), splits
+            assert helpers.rel_l2(outs[1], want) <= DECODE_TOL, splits
+    finally:
+        hip_ctx.set_skinny_waves(0)
+        hip_ctx.set_decode_path(0)
+        hip_ctx.set_wsplit(0)
+        mat.release()
+
+
+def test_skinny_eight_waves_automatic(torch_cuda, hip_ctx):
+    """Q8_0 gate|up-sized matrices at 17..32 rows take eight waves by
+    themselves (one weight tile per wave, two K splits), with the bits of the
+    four-wave kernel at the same tile and split counts."""
+    torch = torch_cuda
+    k, n, m = 3584, 37888, 32
+    canon = quant.synthetic_weights_device(capi.TYPE_Q8_0, k, n, 9, torch.device("cuda:0"))
+    mat = capi.Matrix(hip_ctx, capi.TYPE_Q8_0, k, n, canon, canon.numel(), on_device=True)
+    del canon
+    try:
+        plan = mat.plan(m)
+        assert "waves=8" in plan and "tile_n=1" in plan and "splits=2" in plan, plan
+        assert "waves=8" not in mat.plan(40)
+        xd = _dev(torch, helpers.activations(m, k, seed=8))
+        outs = []
+        for waves, tile_n, splits in ((0, 0, 0), (4, 1, 2)):
+            hip_ctx.set_skinny_waves(waves)
+            hip_ctx.set_decode_path(0, tile_n, splits)
+            y = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+            mat.linear(xd, y, m)
+            torch.cuda.synchronize()
+            outs.append(y.cpu().numpy())
+        assert np.isfinite(outs[0]).all()
+        assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    finally:
+        hip_ctx.set_skinny_waves(0)
+        hip_ctx.set_decode_path(0)
         mat.release()
 
 
