@@ -1,7 +1,7 @@
 // attention.hip -- tiled online-softmax attention over the paged fp32 KV pool.
 //
 // The online_softmax tactic of AttentionPolicy (the reference's
-// attention_batch_paged_online_kernel, src/cuda/cuda_backend.cu:1089-1154,
+// attention_batch_paged_online_kernel, src/cuda/cuda_backend.cu:1093-1154,
 // keeps one (query token, head) pair per block and walks the keys one at a
 // time).  Here a workgroup owns a tile of up to 16 query vectors that share a
 // sequence and a KV head -- 16 consecutive prompt rows of one q head in a

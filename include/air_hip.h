@@ -120,9 +120,13 @@ typedef struct air_hip_stats {
 
 /* ---- library ---------------------------------------------------------- */
 
+/* Version of this C ABI (no counterpart in the reference). */
 int air_hip_abi_version(void);
+/* Name of an AIR_HIP_* status: the values mirror air::ErrorCode
+ * (include/air/status.hpp:8-17), whose names they return. */
 const char* air_hip_status_string(int status);
-/* Message of the calling thread's most recent failure ("" if none). */
+/* Message of the calling thread's most recent failure ("" if none): the
+ * message a failing air::Status carries (include/air/status.hpp:19-40). */
 const char* air_hip_last_error(void);
 
 /* Number of visible HIP devices.  cuda_devices() (cuda_backend.cu:2447-2471). */
@@ -140,7 +144,12 @@ int air_hip_mem_info(int device, uint64_t* free_bytes, uint64_t* total_bytes);
  * ordered on its stream, so one context must not be used from two threads
  * at once. */
 int air_hip_context_create(int device, void* stream, air_hip_context** out);
+/* Frees the context's buffers after its stream drains (the executor's
+ * teardown of the same workspace). */
 int air_hip_context_destroy(air_hip_context* ctx);
+/* Rebinds the context to another stream, as cublasSetStream rebinds the
+ * reference's handle (cuda_backend.cu:1780); work already queued stays on
+ * the old one. */
 int air_hip_context_set_stream(air_hip_context* ctx, void* stream);
 /* Grows the workspaces so linears with input width <= max_k and up to max_m
  * rows never allocate on the hot path (workspace sizing,
@@ -148,13 +157,16 @@ int air_hip_context_set_stream(air_hip_context* ctx, void* stream);
  * which depend on the output width, are sized by the first call that needs
  * them.  Without it the first call that needs more space allocates. */
 int air_hip_context_reserve(air_hip_context* ctx, uint64_t max_k, uint32_t max_m);
+/* Counters and buffer sizes of the context (air_hip_stats above; no
+ * counterpart in the reference). */
 int air_hip_context_stats(const air_hip_context* ctx, air_hip_stats* out);
 /* Overrides the decode linear's launch shape for this context (autotuning):
  * rows_per_wave = 16-row tiles per wavefront (1, 2 or 4), waves_per_group =
  * wavefronts splitting K inside one workgroup (1..16), k_splits =
  * workgroups splitting K (1..64, single-launch path only).  0 keeps the
  * automatic choice; wave counts beyond what a compiled variant supports are
- * clamped to its maximum. */
+ * clamped to its maximum.  Tunes the replacement of specialized_matvec_kernel
+ * (src/cuda/cuda_backend.cu:585-606). */
 int air_hip_context_set_tuning(air_hip_context* ctx, uint32_t rows_per_wave, uint32_t waves_per_group,
                                uint32_t k_splits);
 /* One-row decode GEMV launch shape (autotuning; 0 keeps the automatic
@@ -185,7 +197,8 @@ int air_hip_context_set_split_chain(air_hip_context* ctx, uint32_t mode);
  * automatic (eight for Q8_0 gate|up-sized matrices at 17..32 rows, else
  * four), 4, or 8 = eight waves over twice the weight rows sharing each
  * step's activations (two stages, 17..32 or 49..64 rows; other widths keep
- * four).  Same arithmetic and bits as four waves. */
+ * four).  Same arithmetic and bits as four waves.  Tunes the replacement of
+ * the reference's batch-reuse matmul (src/cuda/cuda_backend.cu:529-583). */
 int air_hip_context_set_skinny_waves(air_hip_context* ctx, uint32_t waves);
 /* Chooses the decode kernel for 2..64 rows (autotuning): path 0 = automatic
  * (the skinny kernel: activations split once into the workspace and staged
@@ -274,7 +287,11 @@ uint64_t air_hip_canonical_bytes(int type, uint64_t k, uint64_t n);
 int air_hip_matrix_prepare(air_hip_context* ctx, int type, uint64_t k, uint64_t n,
                            const void* canonical, uint64_t canonical_bytes,
                            int bytes_on_device, air_hip_matrix** out);
+/* Frees the resident matrix (the prepared weights' device buffer of
+ * cuda_backend.cu:1797-1801). */
 int air_hip_matrix_release(air_hip_matrix* matrix);
+/* Type, shape and sizes of a resident matrix (no counterpart in the
+ * reference, which keeps its GGUF tensor info on the host). */
 int air_hip_matrix_describe(const air_hip_matrix* matrix, air_hip_matrix_desc* out);
 
 /* Decodes the resident matrix to f32 out[n][k] (device pointer), bit-exact
@@ -291,13 +308,15 @@ int air_hip_dequantize_canonical(air_hip_context* ctx, int type, const void* can
 
 /* Stage 1: loads activations x [m][k] (device f32, row-major) into the
  * context workspace as the engine's split f16 hi/lo operand tiles with a
- * per-row power-of-two scale.  One load serves every following
+ * per-row power-of-two scale -- the staging that the reference's
+ * batch-reuse matmul does per launch (src/cuda/cuda_backend.cu:529-583).  One load serves every following
  * air_hip_linear_loaded call with the same input width k (q/k/v and
  * gate/up share their input).  Asynchronous on the context's stream. */
 int air_hip_activations_load(air_hip_context* ctx, const float* x, uint64_t k, uint32_t m);
 
 /* Stage 2: y[m][n] = sum_k w[n][k] * x[m][k] (+ bias[n]) over the activations
- * last loaded into ctx; the matrix input width must equal the loaded k.
+ * last loaded into ctx (specialized_matmul_batch_reuse_kernel's product,
+ * cuda_backend.cu:529-583); the matrix input width must equal the loaded k.
  * Decode tactic only (PREFILL returns unsupported: it loads its own f16
  * operand inside air_hip_linear).  Asynchronous on the context's stream. */
 int air_hip_linear_loaded(air_hip_context* ctx, const air_hip_matrix* matrix,
@@ -476,7 +495,8 @@ typedef struct air_hip_kv_layout {
 } air_hip_kv_layout;
 
 /* Writes each row's k and v (the q|k|v row after RoPE) into the slot of
- * positions[r] of its sequence: page_tables is int32 [m][max_pages]. */
+ * positions[r] of its sequence: page_tables is int32 [m][max_pages].
+ * append_kv_batch_kernel (src/cuda/cuda_backend.cu:1156-1173). */
 int air_hip_kv_append(air_hip_context* ctx, const air_hip_kv_layout* kv, const float* qkv, uint64_t row_stride,
                       uint64_t q_width, uint32_t m, const int32_t* positions, const int32_t* page_tables,
                       uint32_t layer);
@@ -517,7 +537,7 @@ int air_hip_attention(air_hip_context* ctx, const air_hip_kv_layout* kv, const f
 
 /* The online_softmax attention tactic (AttentionExecutionKind::online_softmax,
  * include/air/execution.hpp:47-50; the reference's
- * attention_batch_paged_online_kernel, cuda_backend.cu:1089-1154): the same
+ * attention_batch_paged_online_kernel, cuda_backend.cu:1093-1154): the same
  * output as air_hip_attention, computed in f32 with a running maximum over
  * key chunks staged through LDS, ~1e-6 relative from the double softmax.
  * Work is cut into tiles of up to 16 query vectors that share a sequence and
@@ -529,7 +549,8 @@ typedef struct air_hip_attention_tile {
     uint32_t heads;  /* q heads of one KV head; rows * heads <= 16 */
 } air_hip_attention_tile;
 
-/* Host helper: the tiles of a step whose rows form `runs` consecutive runs,
+/* Host helper (no counterpart in the reference, whose online kernel takes
+ * one (token, head) per block): the tiles of a step whose rows form `runs` consecutive runs,
  * run i holding run_rows[i] rows of one sequence at consecutive positions.
  * A one-row run (decode) gives a tile per KV head of its grouped q heads; a
  * longer run (prefill) tiles of 16 rows per q head, its last rows (the
@@ -540,7 +561,8 @@ int air_hip_attention_make_tiles(const uint32_t* run_rows, uint32_t runs, uint32
 
 /* Attention through tiles made by air_hip_attention_make_tiles for these m
  * rows (device array, uploaded by the caller; the kernel skips a tile that
- * names rows or heads outside the call).  head_dim 64 or 128; q|k|v rows,
+ * names rows or heads outside the call): the online_softmax tactic, in place
+ * of attention_batch_paged_online_kernel (src/cuda/cuda_backend.cu:1093-1154).  head_dim 64 or 128; q|k|v rows,
  * out and the pool 16-byte aligned.  Tiles with long key ranges are split
  * over workgroups and merged in a second pass (context scratch). */
 int air_hip_attention_online(air_hip_context* ctx, const air_hip_kv_layout* kv, const float* qkv, uint64_t row_stride,
