@@ -26,12 +26,18 @@ extern "C" {
 typedef struct air_host_model air_host_model;
 typedef struct air_host_engine air_host_engine;
 
+/* Version of this C ABI (no counterpart in the reference). */
 int air_host_abi_version(void);
+/* The calling thread's last failure message: the message of a failing
+ * air::Status (include/air/status.hpp:19-40). */
 const char* air_host_last_error(void);
 
 /* Random-init Qwen2 model (weights N(0, sigma) quantized to weight_format,
  * norms 1, RoPE theta 1e6, RMSNorm eps 1e-6), generated on the host; the
- * same bytes for the same spec on every machine. */
+ * same bytes for the same spec on every machine.  The in-memory form of the
+ * synthetic GGUF models the reference's tests write (tests/core_tests.cpp:80,
+ * tests/make_quantized_qwen2_gguf.py), as a ModelDefinition
+ * (include/air/model.hpp:57). */
 typedef struct air_host_qwen2_spec {
     uint32_t layers;
     uint32_t embedding;
@@ -50,8 +56,10 @@ typedef struct air_host_qwen2_spec {
 } air_host_qwen2_spec;
 
 int air_host_synthetic_qwen2(const air_host_qwen2_spec* spec, air_host_model** out);
-/* Model bytes and tensor count, for callers that size host memory. */
+/* Model bytes and tensor count, for callers that size host memory
+ * (ModelDefinition's storage and tensors(), include/air/model.hpp:57-72). */
 int air_host_model_describe(const air_host_model* model, uint64_t* storage_bytes, uint64_t* tensors);
+/* Frees the model (the ModelDefinition and its mapped storage). */
 int air_host_model_release(air_host_model* model);
 
 /* A GGUF v3 file (memory-mapped, read-only), loaded with the rules of AIR's
@@ -62,7 +70,9 @@ int air_host_model_release(air_host_model* model);
 int air_host_load_gguf(const char* path, air_host_model** out);
 /* Writes the model as a GGUF v3 file: Qwen2 metadata from its config, a
  * placeholder vocabulary of vocab tokens, eos_token_id when eos >= 0, and
- * every tensor at 32-byte aligned offsets. */
+ * every tensor at 32-byte aligned offsets -- the layout GgufFormat::load
+ * reads (src/formats/gguf/gguf_format.cpp:283), as the reference's test
+ * writers produce it (tests/core_tests.cpp:80-120). */
 int air_host_write_gguf(const air_host_model* model, const char* path, int32_t eos);
 
 typedef struct air_host_model_config {
@@ -80,6 +90,7 @@ typedef struct air_host_model_config {
     int32_t eos;                /* -1 when the file names none (or for synthetic models) */
     uint32_t tensors;
 } air_host_model_config;
+/* ModelDefinition::config() (include/air/model.hpp:17-55, 67). */
 int air_host_model_get_config(const air_host_model* model, air_host_model_config* out);
 
 /* Tensor `index` of the model's table (file order for GGUF). */
@@ -91,6 +102,7 @@ typedef struct air_host_tensor_info {
     uint64_t offset;            /* byte offset in the model's storage (the file) */
     uint64_t size;              /* bytes */
 } air_host_tensor_info;
+/* Entry `index` of ModelDefinition::tensors() (include/air/model.hpp:70). */
 int air_host_model_tensor(const air_host_model* model, uint32_t index, air_host_tensor_info* out);
 
 typedef struct air_host_engine_config {
@@ -110,8 +122,12 @@ typedef struct air_host_engine_config {
 } air_host_engine_config;
 
 /* Prepares the model on `device` (weights resident, repacked) and creates
- * the token service.  The engine keeps the model alive. */
+ * the token service.  The engine keeps the model alive.  A PreparedModel
+ * (src/runtime/backend.hpp:97-145) under the token-id slice of
+ * InferenceService (src/runtime/serving.cpp:203, 2034-2050). */
 int air_host_engine_create(const air_host_model* model, const air_host_engine_config* config, air_host_engine** out);
+/* Drains and frees the engine (InferenceService::shutdown,
+ * src/runtime/serving.cpp:2037). */
 int air_host_engine_release(air_host_engine* engine);
 
 typedef struct air_host_capacity {
@@ -128,7 +144,7 @@ typedef struct air_host_capacity {
 int air_host_engine_capacity(const air_host_engine* engine, air_host_capacity* out);
 /* The device bytes admission reserves for a request of `tokens` prompt plus
  * generated tokens (PreparedModel::estimate_sequence_device_bytes with the
- * engine's plan). */
+ * engine's plan, src/runtime/backend.hpp:134). */
 int air_host_engine_sequence_bytes(const air_host_engine* engine, uint64_t tokens, uint64_t* out);
 
 typedef struct air_host_cohort_stats {
@@ -146,7 +162,8 @@ typedef struct air_host_cohort_stats {
     double mean_ttft_ms;
 } air_host_cohort_stats;
 
-/* Runs `requests` greedy requests to completion.  Prompts are concatenated
+/* Runs `requests` greedy requests to completion, as InferenceService runs
+ * token requests (src/runtime/serving.cpp:2401-2481).  Prompts are concatenated
  * in prompt_tokens with prompt_lengths[i] tokens each; out_tokens holds
  * requests x max_new_tokens ids (row i = request i), out_counts[i] the
  * number generated (fewer when stop_token >= 0 was produced).  stats may be
