@@ -384,7 +384,8 @@ WsplitShape plan_wsplit(const TilePlanes& p, std::uint32_t m, const WsplitTuning
     //  * the activations split in each wave for one activation tile, except
     //    for wide matrices at M > 8 and wide Q4_K ones (whose many
     //    workgroups would repeat the split, block sums included); split once
-    //    into the workspace for two or more tiles;
+    //    into the workspace for two or more tiles, but for Q8_0 down and
+    //    o at two tiles (below);
     //  * a K split over workgroups only while the grid holds fewer than 256
     //    workgroups, keeping at least 16 steps per split.
     std::uint32_t tn = tuning.tile_n;
@@ -407,8 +408,16 @@ WsplitShape plan_wsplit(const TilePlanes& p, std::uint32_t m, const WsplitTuning
     if (tuning.split_x != 0u) {
         s.split_x = tuning.split_x == 1u ? 1u : 0u;
     } else {
+        // Two Q8_0 activation tiles are also split in each wave for long K
+        // (down) and up to 24 rows otherwise (o).  Measured per linear in
+        // graph replay, the split launch included: down (K = 18944) 31.9 /
+        // 33.3 / 35.3 us at M = 17 / 24 / 32 against 37.7 / 37.9 / 37.8 with
+        // split_rows_kernel first, o (K = 3584) 13.3 / 14.0 / 15.0 against
+        // 14.5 / 14.5 / 14.8.  Q4_0 is even or slower, Q4_K's in-wave block
+        // sums far slower (down 87-90 us against 39).
         const bool wide = p.nt >= 2048u;
-        s.split_x = (s.mt >= 2u || (wide && (m > 8u || p.type == kQ4_K))) ? 1u : 0u;
+        const bool wave_split2 = s.mt == 2u && p.type == kQ8_0 && (!short_k || m <= 24u);
+        s.split_x = ((s.mt >= 2u && !wave_split2) || (wide && (m > 8u || p.type == kQ4_K))) ? 1u : 0u;
     }
     return s;
 }
