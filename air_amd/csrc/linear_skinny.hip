@@ -717,12 +717,14 @@ SkinnyShape plan_skinny(const TilePlanes& p, std::uint32_t m, std::uint32_t tile
     // 105 -> 75 at M = 64; down 55 -> 37 at M = 32; lm_head M = 32 157 us
     // against 208); Q4_0 from 17 rows (M = 64: q|k|v 31 -> 21 us, gate|up
     // 66 -> 57, down 51 -> 44), except its lm_head at M <= 32 (132 us on
-    // registers with two tiles, 157 on LDS); at M <= 16 its gate|up is
-    // faster on registers (29 vs 33 us).
+    // registers with two tiles, 157 on LDS) and its gate|up below 33 rows
+    // (registers with two tiles: 42.4 / 44.8 us at M = 17 / 32 against 46.0 /
+    // 46.5 on LDS; at M <= 16 29 vs 33 us).
     if (lds_stages == 0u) {
         const bool narrow_or_tall = p.nt <= 4096u || s.mt >= 3u;
+        const bool q4_0_gate_up = p.nt >= 2000u && p.nt <= 4096u && s.mt <= 2u;
         const bool lds = p.type == kQ8_0   ? narrow_or_tall
-                         : p.type == kQ4_0 ? s.mt >= 2u && narrow_or_tall
+                         : p.type == kQ4_0 ? s.mt >= 2u && narrow_or_tall && !q4_0_gate_up
                                            : true;
         lds_stages = lds ? 2u : 1u;
     }
@@ -734,17 +736,22 @@ SkinnyShape plan_skinny(const TilePlanes& p, std::uint32_t m, std::uint32_t tile
     // for matrices of 2000..4096 row tiles (gate|up) at M <= 32, and not for
     // the 4-bit formats on the LDS pipeline (Q4_K gate|up M = 32: 52 vs 48 us).
     // lm_head-sized matrices (9504 row tiles) also take two at M <= 32 on the
-    // register pipeline (M = 32: 155 -> 132 us).
+    // register pipeline (M = 32: 155 -> 132 us), and so does the Q4_K one on
+    // the LDS pipeline (M = 17 / 32: 154.8 -> 145.5 / 165.6 -> 154.4 us).
     const std::uint32_t tn2_max_mt = 2u;
-    const bool tn2_auto = s.mt <= 2u && p.nt >= 2000u && (p.type == kQ8_0 || s.lds_stages == 0u);
+    const bool tn2_auto = s.mt <= 2u && p.nt >= 2000u &&
+                          (p.type == kQ8_0 || s.lds_stages == 0u || (p.type == kQ4_K && p.nt > 4096u));
     const std::uint32_t want = tile_n != 0u ? tile_n : (tn2_auto ? 2u : 1u);
     s.tile_n = (want == 2u && s.mt <= tn2_max_mt) ? 2u : 1u;
     // Eight waves per workgroup: the LDS pipeline with two stages and two or
     // four activation tiles.  Automatic for Q8_0 gate|up-sized matrices at
-    // 17..32 rows, with one weight tile per wave (45.5 -> 44.0 us at M = 32);
-    // measured even or slower on every other 7B matrix, width and format.
-    const bool eight_auto = waves == 0u && p.type == kQ8_0 && s.mt == 2u && p.nt >= 2000u && p.nt <= 4096u &&
-                            tile_n == 0u;
+    // 17..32 rows, with one weight tile per wave (45.5 -> 44.0 us at M = 32),
+    // and for lm_head-sized Q8_0 and Q4_0 matrices at 49..64 rows (229 -> 199
+    // us and 216 -> 192); measured even or slower on every other 7B matrix,
+    // width and format (Q4_K lm_head at 64 rows 251 -> 298).
+    const bool eight_auto = waves == 0u && tile_n == 0u &&
+                            ((p.type == kQ8_0 && s.mt == 2u && p.nt >= 2000u && p.nt <= 4096u) ||
+                             ((p.type == kQ8_0 || p.type == kQ4_0) && s.mt == 4u && p.nt > 4096u));
     const bool eight = (waves == 8u || eight_auto) && s.lds_stages == 2u && (s.mt == 2u || s.mt == 4u);
     s.waves = eight ? 8u : 4u;
     if (eight_auto && eight) s.tile_n = 1u;

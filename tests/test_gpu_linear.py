@@ -585,6 +585,53 @@ def test_skinny_eight_waves_automatic(torch_cuda, hip_ctx):
         mat.release()
 
 
+def test_skinny_wide_matrix_plans(torch_cuda, hip_ctx):
+    """The automatic plans of wide (lm_head-sized) and gate|up-sized matrices
+    between 17 and 64 rows: Q8_0 past 4096 row tiles at 49..64 rows takes
+    eight waves (the four-wave kernel's bits), Q4_K past 4096 row tiles at
+    17..32 rows two weight tiles per wave on the LDS pipeline, and Q4_0
+    gate|up-sized matrices at 17..32 rows the register kernel with two
+    tiles -- each within the decode tolerance of the oracle."""
+    torch = torch_cuda
+    big = capi.Matrix(hip_ctx, capi.TYPE_Q8_0, 1024, 65600,
+                      *(lambda c: (c, c.nbytes))(helpers.weights(capi.TYPE_Q8_0, 1024, 65600, seed=71)),
+                      on_device=False)
+    try:
+        m = 64
+        plan = big.plan(m)
+        assert "skinny_lds_kernel<q8_0>" in plan and "waves=8" in plan and "tile_n=1" in plan, plan
+        splits = int(re.search(r"splits=(\d+)", plan).group(1))
+        xd = _dev(torch, helpers.activations(m, 1024, seed=72))
+        outs = []
+        for waves, tile_n, k_splits in ((0, 0, 0), (4, 1, splits)):
+            hip_ctx.set_skinny_waves(waves)
+            hip_ctx.set_decode_path(0, tile_n, k_splits)
+            y = torch.full((m, 65600), float("nan"), dtype=torch.float32, device="cuda:0")
+            big.linear(xd, y, m)
+            torch.cuda.synchronize()
+            outs.append(y.cpu().numpy())
+        assert np.isfinite(outs[0]).all()
+        assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    finally:
+        hip_ctx.set_skinny_waves(0)
+        hip_ctx.set_decode_path(0)
+        big.release()
+    for type_id, k, n, m, kernel in ((capi.TYPE_Q4_K, 1024, 65600, 20, "skinny_lds_kernel<q4_k>"),
+                                     (capi.TYPE_Q4_0, 512, 32016, 24, "skinny_kernel<q4_0>")):
+        canon = helpers.weights(type_id, k, n, seed=n + m)
+        mat = capi.Matrix(hip_ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+        try:
+            plan = mat.plan(m)
+            assert kernel in plan and "tile_n=2" in plan, plan
+            x = helpers.activations(m, k, seed=m + 5)
+            y = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+            mat.linear(_dev(torch, x), y, m)
+            torch.cuda.synchronize()
+            assert helpers.rel_l2(y.cpu().numpy(), oracle.linear(type_id, canon, k, n, x)) <= DECODE_TOL, plan
+        finally:
+            mat.release()
+
+
 def test_split_chain_under_graph_capture(torch_cuda):
     """A captured linear whose chain slots would have to grow during capture
     takes the reduction launch instead (same bits); once the slots exist, a
