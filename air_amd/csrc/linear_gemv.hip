@@ -621,6 +621,7 @@ GemvShape plan_decode_gemv(const TilePlanes& p, const DecodeTuning& tuning) {
     // Units in flight per wave: one for wide grids and when no wave owns
     // more than one unit, else two; the buffer count bounds the waves.
     const auto depth_for = [&](std::uint64_t waves) -> std::uint32_t {
+        if (tuning.depth == 1u || tuning.depth == 2u) return tuning.depth;   // a forced depth bounds the waves
         return (wide || ceil_div(units, waves) <= 1u) ? 1u : 2u;
     };
     const std::uint64_t wanted = w;
@@ -631,13 +632,29 @@ GemvShape plan_decode_gemv(const TilePlanes& p, const DecodeTuning& tuning) {
         if (w > cap) w = cap;
         depth = depth_for(w);
     }
-    // Long K on a narrow grid (down: 224 row tiles, 37 chunks each) wants
-    // more than eight waves per row tile: sixteen single-buffered waves (twice
-    // the waves resident on the same CUs) beat eight double-buffered ones by
-    // 6 % in Q8_0 and 4-8 % in the 4-bit formats on back-to-back launches,
-    // 0.5 % on the whole Q8_0 step (where down follows gate|up).
+    // Long K on a narrow grid (down: 224 row tiles, 37 chunks each) runs
+    // single-buffered waves.  A workgroup ends with its wave of most chunks,
+    // so the count is chosen for balance (warmed graph replay of 12 distinct
+    // copies of down, us per launch):
+    //  * Q8_0: eight waves (5 or 4 chunks each) 14.75-14.86, thirteen 15.03,
+    //    sixteen 15.31-15.67 (eight double-buffered 15.50); the M = 1 step
+    //    1.536 -> 1.520 ms;
+    //  * the 4-bit formats: from twelve to sixteen waves, the count whose
+    //    chunks spread most evenly -- thirteen for 37 chunks (2.85 of at most
+    //    3 each): Q4_0 11.68-11.87 against sixteen's 12.09-12.22 and eight's
+    //    12.78-12.83, Q4_K 12.42-12.61 against 12.68-12.76.
     if (tuning.waves_per_group == 0u && !wide && g.units_per_chunk == 1u && g.rows_per_wave == 1u && wanted > 8u) {
         w = wanted > 16u ? 16u : wanted;
+        if (p.type == kQ8_0) {
+            w = 8u;
+        } else if (w == 16u && units > 16u) {
+            std::uint64_t best = 16u;
+            for (std::uint64_t c = 16u; c >= 12u; --c) {
+                // balance = units / (c * ceil(units / c)); compare cross-multiplied
+                if (c * ceil_div(units, c) < best * ceil_div(units, best)) best = c;
+            }
+            w = best;
+        }
         depth = 1u;
     }
     // A grid just past one workgroup per CU (q|k|v: 288 row tiles on 256
