@@ -184,7 +184,9 @@ struct PrefillTuning {
     std::uint32_t prefetch{0}; // weight prefetch distance in steps: 1 or 2 (8x4 tile only)
     // Operand staging: 0 automatic, 1 registers (prefill_gemm_kernel), 2..4
     // an LDS ring of that many 64-k steps (prefill_lds_kernel; Q8_0, 8x4 and
-    // 4x2 tiles).
+    // 4x2 tiles); 0x12 / 0x13 activations alone through an LDS ring of 2 / 3
+    // stages with the weights in registers (prefill_hyb_kernel; any format,
+    // 8x4, 8x2 and 4x2 tiles).
     std::uint32_t lds_stages{0};
     std::uint32_t cus{256};        // compute units of the device (round sizes)
 };
@@ -193,6 +195,7 @@ struct PrefillShape {
     std::uint32_t tile_n{4};
     std::uint32_t prefetch{1};
     std::uint32_t lds_stages{0};   // 0: registers; 2..4: LDS ring stages
+    std::uint32_t hybrid{0};       // 2, 3: activation-only LDS ring (prefill_hyb_kernel)
     // Rows past the first `groups` weight groups (a grid that would end in a
     // mostly empty round of workgroups) run as a second launch on the 4x2
     // tile: rem_groups groups of 128 rows from row tile 4 * tile_n * groups.

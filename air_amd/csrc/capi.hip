@@ -795,7 +795,8 @@ int air_hip_context_set_decode_pipeline(air_hip_context* ctx, uint32_t lds_stage
 
 int air_hip_context_set_prefill_pipeline(air_hip_context* ctx, uint32_t lds_stages) {
     if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
-    if (lds_stages > 4u) return fail(AIR_HIP_INVALID_ARGUMENT, "lds_stages must be 0 .. 4");
+    if (lds_stages > 4u && lds_stages != 0x12u && lds_stages != 0x13u)
+        return fail(AIR_HIP_INVALID_ARGUMENT, "lds_stages must be 0 .. 4, 0x12 or 0x13");
     ctx->prefill_tuning.lds_stages = lds_stages;
     return AIR_HIP_OK;
 }
@@ -1282,8 +1283,9 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
         const char* t = m->type == kF32 ? "f32" : m->type == kF16 ? "f16" : m->type == kBF16 ? "bf16" : "q6_k";
         if (dense_prefill(ctx, m, rows, tactic)) {
             const PrefillShape s = plan_prefill(m->gemm, rows, ctx->prefill_tuning);
-            std::snprintf(buf, sizeof buf, "prefill_gemm_kernel<%s> tile_m=%u tile_n=%u prefetch=%u m_tiles=%u "
-                          "groups=%u splits=%u (dense %s %s)", t, s.tile_m, s.tile_n, s.prefetch, s.m_tiles, s.groups,
+            std::snprintf(buf, sizeof buf, "%s<%s> tile_m=%u tile_n=%u prefetch=%u m_tiles=%u "
+                          "groups=%u splits=%u (dense %s %s)", s.hybrid ? "prefill_hyb_kernel" : "prefill_gemm_kernel",
+                          t, s.tile_m, s.tile_n, s.prefetch, s.m_tiles, s.groups,
                           s.splits, t, m->type == kQ6_K ? "super-block rows" : "rows");
             if (s.rem_groups) {
                 const std::size_t used = std::strlen(buf);
@@ -1313,7 +1315,10 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
     }
     case Route::prefill: {
         const PrefillShape s = plan_prefill(m->planes, rows, ctx->prefill_tuning);
-        if (s.lds_stages) {
+        if (s.hybrid) {
+            std::snprintf(buf, sizeof buf, "prefill_hyb_kernel<%s> tile_m=%u tile_n=%u stages=%u m_tiles=%u groups=%u "
+                          "splits=%u", fmt, s.tile_m, s.tile_n, s.hybrid, s.m_tiles, s.groups, s.splits);
+        } else if (s.lds_stages) {
             std::snprintf(buf, sizeof buf, "prefill_lds_kernel<%s> tile_m=%u tile_n=%u stages=%u m_tiles=%u groups=%u "
                           "splits=%u", fmt, s.tile_m, s.tile_n, s.lds_stages, s.m_tiles, s.groups, s.splits);
         } else {

@@ -511,6 +511,130 @@ __global__ __launch_bounds__(kThreads, ((NS * lds_stage_bytes<TM, TN>()) <= 80u 
     store_tile<TM, TN>(a, acc, g.m0, g.rt0, g.split, lane);
 }
 
+// ---- 2c. GEMM: activations through an LDS ring, weights in registers ----
+//
+// prefill_lds_kernel's activation pipeline (direct global -> LDS loads of
+// lane-ordered fragments, a ring of NS stages) with every wave's weight
+// records loaded straight into registers one step ahead, as
+// prefill_gemm_kernel loads them.  A wave's weights are read by that wave
+// alone, so passing them through LDS only adds LDS traffic (their write and
+// read back) beside the activation fragments that all four waves read; here
+// a stage holds activations only (2 * TM KiB), and any storage format runs.
+//
+// Per step q a wave issues, in this order, the weights of step q + 1 (into
+// the register set not being computed) and then the activation fragments of
+// step q + NS - 1.  At the top of step q the fragments of step q must have
+// landed: with two stages everything issued is waited for; with three, the
+// last kA loads (the fragments of step q + 1) may stay in flight -- the
+// weights of step q were issued before them, so they have landed too.
+template <int FMT, int TM, int TN, int NS>
+__global__ __launch_bounds__(kThreads, 2) void prefill_hyb_kernel(GemmArgs a) {
+    constexpr unsigned kStage = 2u * TM * 1024u;
+    constexpr unsigned kA = 2u * TM / 4u;   // activation fragment loads per wave per stage
+    static_assert((2u * TM) % 4u == 0u, "activation fragments split over the four waves");
+    static_assert(NS == 2 || NS == 3, "two or three stages");
+    __shared__ __attribute__((aligned(1024))) unsigned char stage0[kStage];
+    __shared__ __attribute__((aligned(1024))) unsigned char stage1[kStage];
+    __shared__ __attribute__((aligned(1024))) unsigned char stage2[NS > 2 ? kStage : 16];
+    const auto stage = [&](unsigned st) __attribute__((always_inline)) -> unsigned char* {
+        return st == 0u ? stage0 : st == 1u ? stage1 : stage2;
+    };
+
+    const std::uint32_t lane = threadIdx.x & 63u;
+    const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    GemmTile g;
+    if (!gemm_tile<TM, TN>(a, wave, g)) return;
+
+    float4v acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int t = 0; t < TN; ++t) acc[i][t] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const _Float16* xsrc[kA];
+#pragma unroll
+    for (unsigned j = 0; j < kA; ++j) {
+        const unsigned f = wave + 4u * j, i = f >> 1, b = f & 1u;
+        xsrc[j] = a.xh + static_cast<std::uint64_t>(g.m0 + i * 16u + (lane & 15u)) * a.ldx + 32u * b + 8u * (lane >> 4);
+    }
+    const auto issue_x = [&](std::uint32_t s, std::uint32_t st) __attribute__((always_inline)) {
+        unsigned char* base = stage(st);
+#pragma unroll
+        for (unsigned j = 0; j < kA; ++j) {
+            load_lds16(xsrc[j] + static_cast<std::uint64_t>(s) * kStepK, base + (wave + 4u * j) * 1024u);
+        }
+    };
+    const auto load_w = [&](StepCodes<FMT>(&dst)[TN], std::uint32_t s) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+            const std::uint32_t rt = g.rt0 + static_cast<std::uint32_t>(t);
+            if constexpr (dense_storage(FMT)) {
+                load_dense_step<FMT>(a.codes, a.n, a.kt, rt, s, lane, dst[t]);
+            } else {
+                load_step<FMT>(a.codes, a.scales, rt, a.kt, s, lane, rt < a.nt, dst[t]);
+            }
+        }
+    };
+    const auto compute = [&](std::uint32_t s, std::uint32_t st, const StepCodes<FMT>(&w_in)[TN])
+        __attribute__((always_inline)) {
+        const unsigned char* base = stage(st);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            half8v xf[TM];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                xf[i] = *reinterpret_cast<const half8v*>(base + (static_cast<unsigned>(i) * 2u + b) * 1024u + lane * 16u);
+            }
+            half8v w[TN];
+#pragma unroll
+            for (int t = 0; t < TN; ++t) w[t] = dequant_block<FMT>(w_in[t], s, b, a.w_scale);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int t = 0; t < TN; ++t) acc[i][t] = mfma16x16x32(w[t], xf[i], acc[i][t]);
+        }
+    };
+
+    const std::uint32_t steps = g.s_end - g.s_begin;
+    StepCodes<FMT> wa[TN], wb[TN];
+    if (steps > 0u) load_w(wa, g.s_begin);
+#pragma unroll
+    for (unsigned q = 0; q + 1u < NS; ++q) {
+        if (q < steps) issue_x(g.s_begin + q, q);
+    }
+    // Step q computes stage q mod NS (ST, a constant) with weight set `cur`
+    // and loads the next step's weights into `nxt`.
+    const auto step = [&](std::uint32_t q, auto st_tag, StepCodes<FMT>(&cur)[TN], StepCodes<FMT>(&nxt)[TN])
+        __attribute__((always_inline)) {
+        constexpr unsigned ST = decltype(st_tag)::value;
+        if (NS == 3 && q + 1u < steps) {
+            wait_vmcnt<kA>();
+        } else {
+            wait_vmcnt<0u>();
+        }
+        // Every wave's reads of the stage about to be refilled are complete
+        // before the barrier (lgkmcnt(0)), after which it takes new loads.
+        __builtin_amdgcn_s_waitcnt(0xc07fu);
+        __builtin_amdgcn_s_barrier();
+        if (q + 1u < steps) load_w(nxt, g.s_begin + q + 1u);
+        if (q + NS - 1u < steps) issue_x(g.s_begin + q + NS - 1u, (ST + NS - 1u) % NS);
+        compute(g.s_begin + q, ST, cur);
+    };
+    // The ring position and the weight set both alternate; a period of
+    // 2 * NS steps keeps both compile-time.
+    for (std::uint32_t q = 0; q < steps; q += 2u * NS) {
+        step(q, std::integral_constant<unsigned, 0>{}, wa, wb);
+        if (q + 1u < steps) step(q + 1u, std::integral_constant<unsigned, 1 % NS>{}, wb, wa);
+        if (q + 2u < steps) step(q + 2u, std::integral_constant<unsigned, 2 % NS>{}, wa, wb);
+        if (q + 3u < steps) step(q + 3u, std::integral_constant<unsigned, 3 % NS>{}, wb, wa);
+        if constexpr (NS == 3) {
+            if (q + 4u < steps) step(q + 4u, std::integral_constant<unsigned, 4 % NS>{}, wa, wb);
+            if (q + 5u < steps) step(q + 5u, std::integral_constant<unsigned, 5 % NS>{}, wb, wa);
+        }
+    }
+    store_tile<TM, TN>(a, acc, g.m0, g.rt0, g.split, lane);
+}
+
 // ---- 3. split reduction ------------------------------------------------
 
 __global__ __launch_bounds__(kThreads) void prefill_reduce_kernel(const float* __restrict__ partials,
@@ -597,10 +721,23 @@ hipError_t launch_lds(const GemmArgs& args, std::uint32_t stages, std::uint32_t 
     return hipGetLastError();
 }
 
+template <int FMT, int TM, int TN>
+hipError_t launch_hyb(const GemmArgs& args, std::uint32_t stages, std::uint32_t blocks, hipStream_t stream) {
+    const dim3 grid(blocks), block(kThreads);
+    if (stages == 2u) hipLaunchKernelGGL((prefill_hyb_kernel<FMT, TM, TN, 2>), grid, block, 0, stream, args);
+    else hipLaunchKernelGGL((prefill_hyb_kernel<FMT, TM, TN, 3>), grid, block, 0, stream, args);
+    return hipGetLastError();
+}
+
 template <int FMT>
 hipError_t launch_gemm_fmt(const GemmArgs& args, const PrefillShape& shape, std::uint32_t blocks, hipStream_t stream) {
     const dim3 grid(blocks), block(kThreads);
     const std::uint32_t tm = shape.tile_m, tn = shape.tile_n, pf = shape.prefetch;
+    if (shape.hybrid >= 2u) {
+        if (tm == 8 && tn == 4) return launch_hyb<FMT, 8, 4>(args, shape.hybrid, blocks, stream);
+        if (tm == 8 && tn == 2) return launch_hyb<FMT, 8, 2>(args, shape.hybrid, blocks, stream);
+        if (tm == 4 && tn == 2) return launch_hyb<FMT, 4, 2>(args, shape.hybrid, blocks, stream);
+    }
     if constexpr (FMT == kQ8_0) {
         if (shape.lds_stages >= 2u) {
             return (tm == 8 && tn == 4) ? launch_lds<8, 4>(args, shape.lds_stages, blocks, stream)
@@ -634,9 +771,14 @@ PrefillShape plan_prefill(const TilePlanes& p, std::uint32_t m, const PrefillTun
     //    register tile keeps more waves resident for the same loads;
     //  * narrow grids (q|k|v, o): 4x2 with a 2-way K split (381 / 376 / 316
     //    on q|k|v; 4x4 335 / 328 / 263).
+    //  * Q4_K on the hybrid kernel (activations through LDS, weights in
+    //    registers; measured at M = 512: gate|up 8x4 234 -> 190 us, down
+    //    126 -> 117, o 4x2 45 -> 42, q|k|v 54 -> 52), the 8x4 tile for wide
+    //    grids too.  Q8_0 and Q4_0 measured even on it (within 3 %).
     const bool long_k = p.k >= 8192u;
     const bool wide = p.nt >= 1024u;
-    if (long_k || (wide && p.type == kQ8_0)) {
+    const bool hyb_auto = p.type == kQ4_K;
+    if (long_k || (wide && (p.type == kQ8_0 || hyb_auto))) {
         s.tile_m = 8u;
         s.tile_n = 4u;
         s.prefetch = 1u;
@@ -677,7 +819,7 @@ PrefillShape plan_prefill(const TilePlanes& p, std::uint32_t m, const PrefillTun
         const std::uint64_t grid = static_cast<std::uint64_t>(s.m_tiles) * s.groups;
         if (grid > slots && grid % slots != 0u && (grid % slots) * 2u < slots && slots % s.m_tiles == 0u) {
             const std::uint32_t main_groups = static_cast<std::uint32_t>(grid / slots * slots / s.m_tiles);
-            const std::uint64_t rest_tiles = p.nt - static_cast<std::uint64_t>(main_groups) * 16u;
+            const std::uint64_t rest_tiles = p.nt - static_cast<std::uint64_t>(main_groups) * 4u * s.tile_n;
             s.groups = main_groups;
             s.rem_groups = static_cast<std::uint32_t>(ceil_div(rest_tiles, 8u));
             s.rem_m_tiles = static_cast<std::uint32_t>(ceil_div(m, 64u));
@@ -690,7 +832,12 @@ PrefillShape plan_prefill(const TilePlanes& p, std::uint32_t m, const PrefillTun
     // against 43.5 on LDS) and the LDS pipeline up to them (o, 224: 34.1
     // against 35.9).
     const bool lds_tile = (s.tile_m == 8u && s.tile_n == 4u) || (s.tile_m == 4u && s.tile_n == 2u);
-    if (p.type == kQ8_0 && lds_tile) {
+    const bool hyb_tile = lds_tile || (s.tile_m == 8u && s.tile_n == 2u);
+    if ((tuning.lds_stages == 0x12u || tuning.lds_stages == 0x13u) && hyb_tile) {
+        s.hybrid = tuning.lds_stages - 0x10u;
+    } else if (tuning.lds_stages == 0u && hyb_auto && hyb_tile) {
+        s.hybrid = 2u;
+    } else if (p.type == kQ8_0 && lds_tile) {
         if (tuning.lds_stages >= 2u && tuning.lds_stages <= 4u) {
             s.lds_stages = tuning.lds_stages;
         } else if (tuning.lds_stages == 0u && (s.tile_m == 8u || p.nt <= 256u)) {

@@ -254,7 +254,10 @@ int air_hip_stream_read(air_hip_context* ctx, const void* data, uint64_t bytes, 
  * automatic, 1 = through registers (prefill_gemm_kernel), 2..4 = an LDS ring
  * of that many 64-k steps filled by direct global -> LDS loads
  * (prefill_lds_kernel; Q8_0 with the 8x4 or 4x2 tile, others keep the
- * register path).  No counterpart in the reference. */
+ * register path); 0x12 / 0x13 = the activation fragments alone through a
+ * ring of 2 / 3 steps with every wave's weight records loaded straight into
+ * registers (prefill_hyb_kernel; any storage format, 8x4, 8x2 and 4x2
+ * tiles; the automatic choice for Q4_K).  No counterpart in the reference. */
 int air_hip_context_set_prefill_pipeline(air_hip_context* ctx, uint32_t lds_stages);
 /* Overrides the prefill GEMM's launch shape for this context: tile_m =
  * 16-row activation tiles per wavefront (4 or 8), tile_n = 16-row weight

@@ -205,6 +205,53 @@ def test_prefill_real_shapes_m512(torch_cuda, hip_ctx, _oracle_threads, type_id,
         mat.release()
 
 
+HYB_TYPES = [capi.TYPE_Q8_0, capi.TYPE_Q4_0, capi.TYPE_Q4_K, capi.TYPE_F16, capi.TYPE_BF16, capi.TYPE_Q6_K]
+
+
+@pytest.mark.parametrize("type_id", HYB_TYPES, ids=lambda t: capi.TYPE_NAMES[t])
+@pytest.mark.parametrize("stages", [2, 3])
+@pytest.mark.parametrize("k,n,m,tile", [(3584, 4608, 512, (4, 2, 2)), (4096, 700, 257, (8, 4, 8)),
+                                         (768, 1000, 65, (8, 2, 1)), (1280, 37, 130, (8, 4, 3)),
+                                         (512, 300, 100, (4, 2, 1))])
+def test_prefill_hybrid_matches_register_path(torch_cuda, type_id, stages, k, n, m, tile):
+    """The hybrid GEMM (activation fragments through an LDS ring, weight
+    records straight into registers) runs the register kernel's arithmetic
+    in the same order, so on the same tile and K split its outputs are
+    bit-identical in every storage format; both are held to the oracle
+    (ragged N, M not a whole activation tile, splits with a short last
+    split, the 8x4 launch with its 4x2 remainder)."""
+    from tests.test_gpu_dense import _weights as dense_weights
+    torch = torch_cuda
+    stream = torch.cuda.current_stream(torch.device("cuda:0")).cuda_stream
+    ctx = capi.Context(0, stream)
+    seed = k + 7 * n + type_id
+    canon = (dense_weights(type_id, k, n, seed) if type_id in (capi.TYPE_F16, capi.TYPE_BF16, capi.TYPE_Q6_K)
+             else helpers.weights(type_id, k, n, seed=seed))
+    mat = capi.Matrix(ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    x = helpers.activations(m, k, seed=k + m + 1)
+    bias = np.random.default_rng(n + 1).standard_normal(n).astype(np.float32) * 0.02
+    try:
+        tm, tn, splits = tile
+        ctx.set_prefill_tuning(tm, tn, splits, 2)
+        ctx.set_prefill_pipeline(1)
+        ref = _run(torch, mat, x, n, m, bias)
+        ctx.set_prefill_pipeline(0x10 + stages)
+        plan = mat.plan(m, tactic=capi.LINEAR_PREFILL)
+        assert plan.startswith("prefill_hyb_kernel"), plan
+        got = _run(torch, mat, x, n, m, bias)
+        again = _run(torch, mat, x, n, m, bias)
+        print(f"hybrid {capi.TYPE_NAMES[type_id]} {stages} stages {n}x{k} M={m}: {plan}", flush=True)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+        assert np.array_equal(again.view(np.uint32), got.view(np.uint32))
+        rows = np.unique(np.concatenate([np.arange(min(n, 16)), np.arange(max(0, n - 16), n),
+                                         np.random.default_rng(k).choice(n, size=min(n, 128), replace=False)]))
+        want = oracle.linear_row_list(type_id, canon, k, n, x, rows.astype(np.uint64), bias=bias)
+        assert helpers.rel_l2(got[:, rows], want) <= PREFILL_EXPECT
+    finally:
+        mat.release()
+        ctx.close()
+
+
 @pytest.mark.parametrize("stages", [2, 3, 4])
 @pytest.mark.parametrize("k,n,m,tile", [(3584, 4608, 512, (4, 2, 2)), (18944, 3584, 512, (8, 4, 8)),
                                          (896, 4864, 65, (8, 4, 1)), (512, 3584, 257, (4, 2, 1)),
