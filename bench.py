@@ -449,9 +449,10 @@ def format_step_bytes(type_id: int, m: int, layers: int) -> int:
     return total + VOCAB * (HIDDEN // be) * bb + 4 * m * HIDDEN + 4 * m * VOCAB
 
 
-def measure_formats(torch, capi, quant, dev, stream, types, ms, layers, steps, warmup) -> dict:
+def measure_formats(torch, capi, quant, dev, stream, types, ms, layers, steps, warmup, prefill_m=0) -> dict:
     """the same 7B linear set in Q4_0 / Q4_K at each M, one step
-    replayed as a HIP graph, GB/s on the format's algorithmic bytes."""
+    replayed as a HIP graph, GB/s on the format's algorithmic bytes; with
+    prefill_m, also one prefill pass of the layers' linears at that M."""
     out = {}
     ctx = capi.Context(0, stream.cuda_stream)
     for type_id in types:
@@ -510,6 +511,8 @@ def measure_formats(torch, capi, quant, dev, stream, types, ms, layers, steps, w
             res[str(m)] = {"ms_per_step": round(ms_step, 4), "gbps": round(algo / (ms_step * 1e-3) / 1e9, 1),
                            "tok_s": round(m / (ms_step * 1e-3), 1)}
             del graph
+        if prefill_m > 0:
+            res["prefill"] = measure_prefill(torch, ctx, capi, mats, prefill_m, max(3, steps // 5), dev, stream)
         out[capi.TYPE_NAMES[type_id]] = res
         for layer in mats:
             for mat in layer.values():
@@ -868,7 +871,7 @@ def main() -> int:
         torch.cuda.empty_cache()
         formats = measure_formats(torch, capi, quant, dev, stream, [int(v) for v in args.formats.split(",")],
                                   [int(v) for v in args.formats_m.split(",")], args.layers, max(5, args.steps // 3),
-                                  args.warmup)
+                                  args.warmup, prefill_m=args.prefill_m)
 
     small = None
     if args.small:

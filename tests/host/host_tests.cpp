@@ -1056,6 +1056,14 @@ void gpu_long_sequences_vs_oracle(std::uint32_t format,
     auto& p = *prepared.value();
     const auto plan = hip_plan(air::QuantizedLinearExecutionKind::hip_decode, 4U);
     const std::uint64_t vocab = spec.config.vocabulary_size;
+    {
+        // Capacity is answered in the prepared page size, so a plan with
+        // another page size is refused, before and after the pool exists.
+        const auto other = p.create_sequence(hip_plan(air::QuantizedLinearExecutionKind::hip_decode, 8U));
+        check(!other && other.status().code() == air::ErrorCode::invalid_argument &&
+                  p.kv_pool_allocated_bytes() == 0U,
+              tag + ": a plan with another KV page size is refused");
+    }
 
     std::uint64_t lcg = 0x9E3779B97F4A7C15ULL + format;
     const auto next = [&]() {
