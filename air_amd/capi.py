@@ -133,6 +133,7 @@ SIGNATURES = {
     "air_hip_context_set_wsplit": (_I, [_P, _U32, _U32, _U32, _U32, _U32, _U32]),
     "air_hip_context_set_dense_path": (_I, [_P, _U32, _U32, _U32, _U32]),
     "air_hip_context_set_prefill_pipeline": (_I, [_P, _U32]),
+    "air_hip_context_set_prefill_remainder_splits": (_I, [_P, _U32]),
     "air_hip_context_set_decode_pipeline": (_I, [_P, _U32]),
     "air_hip_matrix_rows": (_I, [_P, _P, _P, _U32, _P]),
     "air_hip_rms_norm": (_I, [_P, _P, _P, _P, _U32, _U64, ctypes.c_double]),
@@ -283,6 +284,10 @@ class Context:
     def set_prefill_pipeline(self, lds_stages: int = 0) -> None:
         """Prefill operand staging: 0 automatic, 1 registers, 2..4 LDS ring stages."""
         check(lib().air_hip_context_set_prefill_pipeline(self.handle, lds_stages))
+
+    def set_prefill_remainder_splits(self, splits: int = 0) -> None:
+        """K split of the prefill remainder launch (0 automatic, 1 unsplit)."""
+        check(lib().air_hip_context_set_prefill_remainder_splits(self.handle, splits))
 
     def set_prefill_tuning(self, tile_m: int = 0, tile_n: int = 0, k_splits: int = 0, prefetch: int = 0) -> None:
         check(lib().air_hip_context_set_prefill_tuning(self.handle, tile_m, tile_n, k_splits, prefetch))

@@ -189,6 +189,7 @@ struct PrefillTuning {
     // 8x4, 8x2 and 4x2 tiles).
     std::uint32_t lds_stages{0};
     std::uint32_t cus{256};        // compute units of the device (round sizes)
+    std::uint32_t rem_splits{0};   // remainder launch K split: 0 automatic, 1 none, n splits
 };
 struct PrefillShape {
     std::uint32_t tile_m{8};
@@ -201,6 +202,10 @@ struct PrefillShape {
     // tile: rem_groups groups of 128 rows from row tile 4 * tile_n * groups.
     std::uint32_t rem_groups{0};
     std::uint32_t rem_m_tiles{0};
+    // The remainder launch's K split (partials of its columns only, summed
+    // in split order by a column reduction).
+    std::uint32_t rem_splits{1};
+    std::uint32_t rem_steps_per_split{0};
     std::uint32_t m_tiles{0};
     std::uint32_t groups{0};
     std::uint32_t steps{0};

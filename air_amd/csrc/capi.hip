@@ -815,6 +815,13 @@ int air_hip_context_set_prefill_tuning(air_hip_context* ctx, uint32_t tile_m, ui
     return AIR_HIP_OK;
 }
 
+int air_hip_context_set_prefill_remainder_splits(air_hip_context* ctx, uint32_t splits) {
+    if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
+    if (splits > 64u) return fail(AIR_HIP_INVALID_ARGUMENT, "splits must be at most 64");
+    ctx->prefill_tuning.rem_splits = splits;
+    return AIR_HIP_OK;
+}
+
 int air_hip_context_set_tuning(air_hip_context* ctx, uint32_t rows_per_wave, uint32_t waves_per_group,
                                uint32_t k_splits) {
     if (!ctx) return fail(AIR_HIP_INVALID_ARGUMENT, "context must not be null");
@@ -1289,8 +1296,8 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
                           s.splits, t, m->type == kQ6_K ? "super-block rows" : "rows");
             if (s.rem_groups) {
                 const std::size_t used = std::strlen(buf);
-                std::snprintf(buf + used, sizeof buf - used, " + remainder tile_m=4 tile_n=2 m_tiles=%u groups=%u",
-                              s.rem_m_tiles, s.rem_groups);
+                std::snprintf(buf + used, sizeof buf - used, " + remainder tile_m=4 tile_n=2 m_tiles=%u groups=%u splits=%u",
+                              s.rem_m_tiles, s.rem_groups, s.rem_splits);
             }
             break;
         }
@@ -1327,8 +1334,8 @@ std::string describe_linear(const air_hip_context* ctx, const air_hip_matrix* m,
         }
         if (s.rem_groups) {
             const std::size_t used = std::strlen(buf);
-            std::snprintf(buf + used, sizeof buf - used, " + remainder tile_m=4 tile_n=2 m_tiles=%u groups=%u",
-                          s.rem_m_tiles, s.rem_groups);
+            std::snprintf(buf + used, sizeof buf - used, " + remainder tile_m=4 tile_n=2 m_tiles=%u groups=%u splits=%u",
+                          s.rem_m_tiles, s.rem_groups, s.rem_splits);
         }
         break;
     }

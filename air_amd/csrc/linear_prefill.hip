@@ -28,6 +28,7 @@
 #include "air_hip_kernels.hpp"
 #include "air_hip_steps.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <type_traits>
 #include <cstring>
@@ -168,7 +169,9 @@ struct GemmArgs {
     const float* row_inv;        // [Mp]
     float w_scale, w_unscale;
     const float* bias;           // [n] or null (ignored when splits > 1)
-    float* out;                  // y [m][n], or partials [splits][m][n]
+    float* out;                  // y [m][ldo], or partials [splits][m][ldo]
+    std::uint64_t ldo;           // row stride of out (n, or the partials' column count)
+    std::uint64_t col0;          // first column that out holds
     std::uint32_t m;
     std::uint32_t m_tiles;       // ceil(m / BM)
     std::uint32_t groups;        // ceil(nt / (4 * TN))
@@ -184,14 +187,14 @@ struct GemmArgs {
 template <int TM, int TN>
 __device__ __forceinline__ void store_tile(const GemmArgs& a, const float4v (&acc)[TM][TN], std::uint32_t m0,
                                            std::uint32_t rt0, std::uint32_t split, std::uint32_t lane) {
-    float* out = a.out + (a.partial ? static_cast<std::uint64_t>(split) * a.m * a.n : 0u);
-    const bool vec = (a.n & 3u) == 0u;
+    float* out = a.out + (a.partial ? static_cast<std::uint64_t>(split) * a.m * a.ldo : 0u);
+    const bool vec = (a.n & 3u) == 0u && (a.ldo & 3u) == 0u && (a.col0 & 3u) == 0u;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         const std::uint32_t m = m0 + static_cast<std::uint32_t>(i) * 16u + (lane & 15u);
         if (m >= a.m) continue;
         const float scale = a.row_inv[m] * a.w_unscale;
-        float* yrow = out + static_cast<std::uint64_t>(m) * a.n;
+        float* yrow = out + static_cast<std::uint64_t>(m) * a.ldo;
 #pragma unroll
         for (int t = 0; t < TN; ++t) {
             const std::uint64_t n0 = static_cast<std::uint64_t>(rt0 + static_cast<std::uint32_t>(t)) * 16u + 4u * (lane >> 4);
@@ -202,11 +205,12 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const float4v (&ac
                 v[r] = acc[i][t][r] * scale;
                 if (a.bias && n0 + r < a.n) v[r] += a.bias[n0 + r];
             }
+            float* dst = yrow + (n0 - a.col0);   // n0 >= col0: the launch covers columns from col0 on
             if (vec && n0 + 4u <= a.n) {
-                *reinterpret_cast<float4*>(yrow + n0) = make_float4(v[0], v[1], v[2], v[3]);
+                *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
             } else {
                 for (int r = 0; r < 4; ++r)
-                    if (n0 + r < a.n) yrow[n0 + r] = v[r];
+                    if (n0 + r < a.n) dst[r] = v[r];
             }
         }
     }
@@ -665,6 +669,42 @@ __global__ __launch_bounds__(kThreads) void split_reduce4_kernel(const float4v* 
     }
 }
 
+// Partials [splits][m][ncols] of columns col0 .. col0 + ncols - 1 summed in
+// split order into y [m][ldy] (+ bias): the remainder launch's K split.
+// Four columns at a time (ncols, col0 and ldy multiples of 4).
+__global__ __launch_bounds__(kThreads) void split_reduce_cols4_kernel(const float4v* __restrict__ partials,
+                                                                      std::uint32_t splits, std::uint32_t m,
+                                                                      std::uint32_t ncols4, std::uint64_t ldy4,
+                                                                      std::uint64_t col0_4,
+                                                                      const float4v* __restrict__ bias,
+                                                                      float4v* __restrict__ y) {
+    const std::uint32_t total4 = m * ncols4;
+    for (std::uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < total4; i += gridDim.x * kThreads) {
+        const std::uint32_t row = i / ncols4, c = i - row * ncols4;
+        float4v v = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (std::uint32_t s = 0; s < splits; ++s) v += partials[static_cast<std::uint64_t>(s) * total4 + i];
+        if (bias) v += bias[col0_4 + c];
+        y[static_cast<std::uint64_t>(row) * ldy4 + col0_4 + c] = v;
+    }
+}
+
+// The same sum one column at a time (any alignment, 64-bit indices).
+__global__ __launch_bounds__(kThreads) void split_reduce_cols_kernel(const float* __restrict__ partials,
+                                                                     std::uint32_t splits, std::uint32_t m,
+                                                                     std::uint64_t ncols, std::uint64_t ldy,
+                                                                     std::uint64_t col0, const float* __restrict__ bias,
+                                                                     float* __restrict__ y) {
+    const std::uint64_t total = static_cast<std::uint64_t>(m) * ncols;
+    for (std::uint64_t i = blockIdx.x * static_cast<std::uint64_t>(kThreads) + threadIdx.x; i < total;
+         i += static_cast<std::uint64_t>(gridDim.x) * kThreads) {
+        const std::uint64_t row = i / ncols, c = i - row * ncols;
+        float v = 0.0f;
+        for (std::uint32_t s = 0; s < splits; ++s) v += partials[s * total + i];
+        if (bias) v += bias[col0 + c];
+        y[row * ldy + col0 + c] = v;
+    }
+}
+
 // ---- weight exponent ---------------------------------------------------
 
 // Largest |dequantized weight| bound over all blocks, as float bits (>= 0).
@@ -823,6 +863,21 @@ PrefillShape plan_prefill(const TilePlanes& p, std::uint32_t m, const PrefillTun
             s.groups = main_groups;
             s.rem_groups = static_cast<std::uint32_t>(ceil_div(rest_tiles, 8u));
             s.rem_m_tiles = static_cast<std::uint32_t>(ceil_div(m, 64u));
+            // The 4x2 remainder splits K until its grid reaches about two
+            // workgroups per CU, at least 8 steps per split, the partials'
+            // columns whole float4 runs.  Measured on gate|up at M = 512
+            // (320 workgroups unsplit; warmed, same process): Q8_0 170.8 us
+            // unsplit, 164.8 at 2 splits, 166.6 at 3, 173.5 at 4; Q4_K
+            // 192.8 / 183.8 / 186.5 / 193.0.
+            const std::uint64_t rem_blocks = static_cast<std::uint64_t>(s.rem_groups) * s.rem_m_tiles;
+            const std::uint64_t rem_cols = p.n - static_cast<std::uint64_t>(main_groups) * 4u * s.tile_n * 16u;
+            std::uint64_t rs = ceil_div(2ull * (tuning.cus ? tuning.cus : 256u), rem_blocks);
+            rs = std::min<std::uint64_t>(rs, s.steps / 8u);
+            if (tuning.rem_splits) rs = std::min<std::uint64_t>(tuning.rem_splits, s.steps);
+            if (rs > 1u && rem_cols % 4u == 0u) {
+                s.rem_steps_per_split = static_cast<std::uint32_t>(ceil_div(s.steps, rs));
+                s.rem_splits = static_cast<std::uint32_t>(ceil_div(s.steps, s.rem_steps_per_split));
+            }
         }
     }
     // The LDS pipeline runs the Q8_0 8x4 and 4x2 tiles only.  Automatic: two
@@ -857,6 +912,10 @@ std::uint64_t prefill_workspace_bytes(std::uint64_t k, std::uint32_t m, const Pr
     const std::uint64_t mp = prefill_rows_padded(m);
     std::uint64_t bytes = ceil_div(mp * prefill_ldx(k) * 2u, 256u) * 256u + ceil_div(mp * 4u, 256u) * 256u;
     if (shape.splits > 1u) bytes += static_cast<std::uint64_t>(shape.splits) * m * n * 4u;
+    if (shape.rem_groups && shape.rem_splits > 1u) {
+        const std::uint64_t col0 = static_cast<std::uint64_t>(shape.groups) * 4u * shape.tile_n * 16u;
+        bytes += static_cast<std::uint64_t>(shape.rem_splits) * m * (n - col0) * 4u;
+    }
     return bytes;
 }
 
@@ -900,6 +959,8 @@ hipError_t launch_prefill_linear(const TilePlanes& p, const float* x, const floa
     a.partial = split ? 1u : 0u;
     a.bias = split ? nullptr : bias;
     a.out = split ? partials : y;
+    a.ldo = p.n;
+    a.col0 = 0u;
     a.blocks = shape.m_tiles * shape.groups * shape.splits;
     a.rt_base = 0u;
     const auto launch = [&](const GemmArgs& args, const PrefillShape& sh) {
@@ -927,8 +988,36 @@ hipError_t launch_prefill_linear(const TilePlanes& p, const float* x, const floa
         r.rt_base = shape.groups * 4u * shape.tile_n;
         r.m_tiles = rem.m_tiles;
         r.groups = rem.groups;
-        r.blocks = rem.m_tiles * rem.groups;
+        const bool rem_split = shape.rem_splits > 1u;
+        const std::uint64_t col0 = static_cast<std::uint64_t>(r.rt_base) * 16u;
+        if (rem_split) {
+            r.steps_per_split = shape.rem_steps_per_split;
+            r.partial = 1u;
+            r.bias = nullptr;
+            r.out = partials;
+            r.ldo = p.n - col0;
+            r.col0 = col0;
+        }
+        r.blocks = rem.m_tiles * rem.groups * shape.rem_splits;
         err = launch(r, rem);
+        if (err == hipSuccess && rem_split) {
+            const std::uint64_t ncols = p.n - col0;
+            const std::uint64_t total4 = static_cast<std::uint64_t>(m) * ncols / 4u;
+            const auto aligned = [](const void* q) { return reinterpret_cast<std::uintptr_t>(q) % 16u == 0u; };
+            if (ncols % 4u == 0u && p.n % 4u == 0u && total4 < (1ull << 32) && aligned(partials) && aligned(y) &&
+                (!bias || aligned(bias))) {
+                const std::uint64_t grid = ceil_div(total4, kThreads);
+                hipLaunchKernelGGL(split_reduce_cols4_kernel, dim3(static_cast<unsigned>(grid < 1024u ? grid : 1024u)),
+                                   dim3(kThreads), 0, stream, reinterpret_cast<const float4v*>(partials),
+                                   shape.rem_splits, m, static_cast<std::uint32_t>(ncols / 4u), p.n / 4u, col0 / 4u,
+                                   reinterpret_cast<const float4v*>(bias), reinterpret_cast<float4v*>(y));
+            } else {
+                const std::uint64_t grid = ceil_div(static_cast<std::uint64_t>(m) * ncols, kThreads);
+                hipLaunchKernelGGL(split_reduce_cols_kernel, dim3(static_cast<unsigned>(grid < 4096u ? grid : 4096u)),
+                                   dim3(kThreads), 0, stream, partials, shape.rem_splits, m, ncols, p.n, col0, bias, y);
+            }
+            err = hipGetLastError();
+        }
     }
     if (err != hipSuccess || !split) return err;
     if (epilogue) return launch_split_epilogue(partials, shape.splits, m, p.n, bias, *epilogue, stream);

@@ -268,6 +268,12 @@ int air_hip_context_set_prefill_pipeline(air_hip_context* ctx, uint32_t lds_stag
  * fixed shapes); it exists for autotuning sweeps. */
 int air_hip_context_set_prefill_tuning(air_hip_context* ctx, uint32_t tile_m, uint32_t tile_n,
                                        uint32_t k_splits, uint32_t prefetch);
+/* Overrides the K split of the prefill GEMM's remainder launch (the rows past
+ * the 8x4 tile's whole rounds, run on the 4x2 tile): 1 = unsplit, 2..64 that
+ * many splits (a column reduction sums them in split order), 0 = automatic
+ * (enough splits to fill a round, at least 8 steps each).  No counterpart in
+ * the reference; it exists for autotuning sweeps. */
+int air_hip_context_set_prefill_remainder_splits(air_hip_context* ctx, uint32_t splits);
 
 /* ---- matrices ----------------------------------------------------------- */
 

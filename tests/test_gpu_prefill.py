@@ -326,6 +326,56 @@ def test_prefill_remainder_launch_is_bit_identical(torch_cuda):
         ctx.close()
 
 
+@pytest.mark.parametrize("type_id", [capi.TYPE_Q8_0, capi.TYPE_Q4_K], ids=lambda t: capi.TYPE_NAMES[t])
+def test_prefill_split_remainder(torch_cuda, type_id):
+    """With a long K the 4x2 remainder launch splits K towards two
+    workgroups per CU (here 72 workgroups x 7 splits of 8 steps, the most
+    that keep 8 steps per split) and a column reduction sums
+    its partials in split order into the remainder's columns only.  The
+    8x4 launch's columns stay bit-identical to an unsplit 4x2 launch; the
+    remainder's columns differ only in f32 summation order; both are held to
+    the oracle, the boundary row tiles and the ragged last tile included."""
+    torch = torch_cuda
+    stream = torch.cuda.current_stream(torch.device("cuda:0")).cuda_stream
+    ctx = capi.Context(0, stream)
+    k, n, m = 3584, 33800, 512
+    canon = helpers.weights(type_id, k, n, seed=33801 + type_id)
+    mat = capi.Matrix(ctx, type_id, k, n, canon, canon.nbytes, on_device=False)
+    x = helpers.activations(m, k, seed=19)
+    bias = np.random.default_rng(6).standard_normal(n).astype(np.float32) * 0.02
+    try:
+        ctx.set_prefill_tuning(8, 4, 1, 1)
+        plan = mat.plan(m, tactic=capi.LINEAR_PREFILL)
+        print(f"split remainder {capi.TYPE_NAMES[type_id]} {n}x{k} M={m}: {plan}", flush=True)
+        assert "remainder" in plan and plan.endswith("groups=9 splits=7"), plan
+        got = _run(torch, mat, x, n, m, bias)
+        again = _run(torch, mat, x, n, m, bias)
+        assert np.array_equal(again.view(np.uint32), got.view(np.uint32))
+        ctx.set_prefill_tuning(4, 2, 1, 2)
+        ctx.set_prefill_pipeline(1)
+        ref = _run(torch, mat, x, n, m, bias)
+        assert np.array_equal(got[:, :32768].view(np.uint32), ref[:, :32768].view(np.uint32))
+        assert helpers.rel_l2(got[:, 32768:], ref[:, 32768:]) <= 1e-6
+        # An unsplit remainder (the override) is the 4x2 launch bit for bit.
+        ctx.set_prefill_pipeline(0)
+        ctx.set_prefill_tuning(8, 4, 1, 1)
+        ctx.set_prefill_remainder_splits(1)
+        assert mat.plan(m, tactic=capi.LINEAR_PREFILL).endswith("groups=9 splits=1")
+        unsplit = _run(torch, mat, x, n, m, bias)
+        assert np.array_equal(unsplit.view(np.uint32), ref.view(np.uint32))
+        with pytest.raises(capi.HipError) as e:
+            ctx.set_prefill_remainder_splits(65)
+        assert e.value.status_name == "invalid_argument"
+        rows = np.unique(np.concatenate([np.arange(32768 - 16, 32768 + 16), np.arange(n - 24, n),
+                                         np.random.default_rng(2).choice(np.arange(32768, n), size=128,
+                                                                         replace=False)]))
+        want = oracle.linear_row_list(type_id, canon, k, n, x, rows.astype(np.uint64), bias=bias)
+        assert helpers.rel_l2(got[:, rows], want) <= PREFILL_EXPECT
+    finally:
+        mat.release()
+        ctx.close()
+
+
 @pytest.mark.parametrize("k,f,m", [(3584, 18944, 512), (96, 600, 70), (992, 200, 65)])
 def test_prefill_operand_from_norm_and_swiglu(torch_cuda, hip_ctx, k, f, m):
     """air_hip_rms_norm_prefill and air_hip_silu_mul_prefill leave the next
