@@ -85,6 +85,86 @@ __global__ __launch_bounds__(kThreads) void prefill_activations_kernel(const flo
     if (threadIdx.x == 0) row_inv[row] = inv;
 }
 
+// The same conversion reading the row once: thread t holds the runs of 8
+// floats at (t + 256 j) * 8 for j < C in registers, so the row's max and
+// its conversion take one pass over memory instead of two (same scale, same
+// per-element arithmetic: bit-identical).  Rows with ldx <= 2048 * C.
+template <int C>
+__global__ __launch_bounds__(kThreads) void prefill_activations_reg_kernel(const float* __restrict__ x,
+                                                                           std::uint32_t m, std::uint64_t k,
+                                                                           std::uint64_t ldx,
+                                                                           _Float16* __restrict__ xh,
+                                                                           float* __restrict__ row_inv) {
+    __shared__ float red[kThreads / 64];
+    const std::uint32_t row = blockIdx.x;
+    _Float16* out = xh + static_cast<std::uint64_t>(row) * ldx;
+    if (row >= m) {
+        for (std::uint64_t c = threadIdx.x * 8u; c < ldx; c += kThreads * 8u) {
+            *reinterpret_cast<uint4*>(out + c) = make_uint4(0u, 0u, 0u, 0u);
+        }
+        if (threadIdx.x == 0) row_inv[row] = 1.0f;
+        return;
+    }
+    const float* in = x + static_cast<std::uint64_t>(row) * k;
+    float4 v[C][2];
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+        const std::uint64_t c = (threadIdx.x + kThreads * static_cast<std::uint64_t>(j)) * 8u;
+        if (c < k) {  // k is a multiple of 32, so a run of 8 is all in or all out
+            v[j][0] = *reinterpret_cast<const float4*>(in + c);
+            v[j][1] = *reinterpret_cast<const float4*>(in + c + 4);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j][h].x), fabsf(v[j][h].y)),
+                                         fmaxf(fabsf(v[j][h].z), fabsf(v[j][h].w))));
+            }
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float s, inv;
+    block_scale(amax, s, inv);
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+        const std::uint64_t c = (threadIdx.x + kThreads * static_cast<std::uint64_t>(j)) * 8u;
+        if (c >= ldx) continue;
+        half8v h;
+        if (c < k) {
+            const float4 a = v[j][0], b = v[j][1];
+            h[0] = static_cast<_Float16>(a.x * s); h[1] = static_cast<_Float16>(a.y * s);
+            h[2] = static_cast<_Float16>(a.z * s); h[3] = static_cast<_Float16>(a.w * s);
+            h[4] = static_cast<_Float16>(b.x * s); h[5] = static_cast<_Float16>(b.y * s);
+            h[6] = static_cast<_Float16>(b.z * s); h[7] = static_cast<_Float16>(b.w * s);
+        } else {
+            for (int e = 0; e < 8; ++e) h[e] = static_cast<_Float16>(0.0f);
+        }
+        *reinterpret_cast<half8v*>(out + c) = h;
+    }
+    if (threadIdx.x == 0) row_inv[row] = inv;
+}
+
+// One launch converting rows [0, mp) of x (rows >= m zero-filled).
+hipError_t launch_prefill_activations(const float* x, std::uint32_t m, std::uint64_t k, std::uint64_t ldx,
+                                      std::uint64_t mp, _Float16* xh, float* row_inv, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(mp)), block(kThreads);
+    const std::uint64_t chunks = ceil_div(ldx, 8u * kThreads);
+    if (chunks <= 2u) {
+        hipLaunchKernelGGL(prefill_activations_reg_kernel<2>, grid, block, 0, stream, x, m, k, ldx, xh, row_inv);
+    } else if (chunks <= 4u) {
+        hipLaunchKernelGGL(prefill_activations_reg_kernel<4>, grid, block, 0, stream, x, m, k, ldx, xh, row_inv);
+    } else if (chunks <= 8u) {
+        hipLaunchKernelGGL(prefill_activations_reg_kernel<8>, grid, block, 0, stream, x, m, k, ldx, xh, row_inv);
+    } else if (chunks <= 12u) {
+        hipLaunchKernelGGL(prefill_activations_reg_kernel<12>, grid, block, 0, stream, x, m, k, ldx, xh, row_inv);
+    } else {
+        hipLaunchKernelGGL(prefill_activations_kernel, grid, block, 0, stream, x, m, k, ldx, xh, row_inv);
+    }
+    return hipGetLastError();
+}
+
 // ---- weight fragments -----------------------------------------------------
 
 __device__ __forceinline__ _Float16 scaled_half(std::uint32_t bits, float w_scale) {
@@ -932,11 +1012,7 @@ hipError_t launch_prefill_linear(const TilePlanes& p, const float* x, const floa
     auto* partials = reinterpret_cast<float*>(base);
 
     // `converted`: the operand of these rows is already in the workspace.
-    if (!converted) {
-        hipLaunchKernelGGL(prefill_activations_kernel, dim3(static_cast<unsigned>(mp)), dim3(kThreads), 0, stream, x,
-                           m, p.k, ldx, xh, row_inv);
-    }
-    hipError_t err = hipGetLastError();
+    hipError_t err = converted ? hipSuccess : launch_prefill_activations(x, m, p.k, ldx, mp, xh, row_inv, stream);
     if (err != hipSuccess) return err;
 
     GemmArgs a{};
